@@ -1,0 +1,288 @@
+"""Functional wrappers over the gfx950 kernels (one Python call -> one or two launches).
+
+These are the building blocks of the drop-in APIs (``cortex.kernels.*``,
+``cortex.quantization``) and of the model forward (``cortex.models``).  Every
+function takes GPU tensors, allocates its outputs with torch's caching allocator
+(unless ``out=`` is given), launches on torch's current stream and never
+synchronises the host.
+"""
+
+from __future__ import annotations
+
+import math
+
+import torch
+
+from cortex import _native as nat
+
+NORM = {None: 0, "none": 0, "layer": 1, "rms": 2}
+ACT = {None: 0, "none": 0, "gelu": 1}
+
+
+def _row_major_2d(x: torch.Tensor) -> torch.Tensor:
+    if x.dim() != 2:
+        raise ValueError(f"expected a 2-D tensor, got shape {tuple(x.shape)}")
+    if x.stride(1) != 1 or (x.size(0) > 1 and x.stride(0) < x.size(1)):
+        x = x.contiguous()
+    return x
+
+
+# --------------------------------------------------------------------------- pack
+
+
+def pack_plan(batch_indices: torch.Tensor, batch_size: int, err: torch.Tensor | None = None):
+    """Stable CSR plan of ragged events: ``(offsets (B+1), order (E), rank (E))``.
+
+    offsets/order/rank are int64 device tensors; see ``cortex_pack_plan``.
+    """
+    dev = nat.require_gpu(batch_indices, what="pack_plan")
+    if batch_indices.dtype != torch.int64 or batch_indices.dim() != 1:
+        raise ValueError("batch_indices must be a 1-D int64 tensor")
+    E = batch_indices.shape[0]
+    B = int(batch_size)
+    offsets = torch.empty(B + 1, dtype=torch.int64, device=dev)
+    order = torch.empty(E, dtype=torch.int64, device=dev)
+    rank = torch.empty(E, dtype=torch.int64, device=dev)
+    ws_bytes = nat.load().cortex_pack_workspace_bytes(E, B)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+    nat.call("cortex_pack_plan", nat.ptr(batch_indices), batch_indices.stride(0) if E else 1, E, B,
+             nat.ptr(offsets), nat.ptr(order), None, nat.ptr(rank), nat.ptr(ws), ws_bytes, nat.ptr(err),
+             nat.stream_of(dev))
+    return offsets, order, rank
+
+
+def tokenize(neuron_emb, time_emb, value_emb, neuron_ids, time_bins, values, *, order=None, offsets=None,
+             csr_offsets=None, batch_size: int = 0, max_events: int = 0, out=None, mask=None, err=None):
+    """Fused gather-add ``(N[nid] + T[tb]) + V[val]`` into CSR rows (``offsets`` None) or
+    the padded ``(B, max_events, D)`` layout with its mask (``offsets`` given).
+
+    In CSR mode pass the plan's offsets as ``csr_offsets``: rows past
+    ``offsets[B]`` (events dropped for an invalid batch index) are then zeroed.
+    """
+    dev = nat.require_gpu(neuron_emb, time_emb, value_emb, neuron_ids, time_bins, values, what="tokenize")
+    D = neuron_emb.shape[1]
+    E = neuron_ids.shape[0]
+    padded = offsets is not None
+    if out is None:
+        shape = (batch_size, max_events, D) if padded else (E, D)
+        out = torch.empty(shape, dtype=neuron_emb.dtype, device=dev)
+    if padded and mask is None:
+        mask = torch.empty((batch_size, max_events), dtype=torch.bool, device=dev)
+    ld_out = out.stride(-2) if out.dim() >= 2 and out.shape[-2] > 1 else D
+    st = [t.stride(0) if t.numel() else 1 for t in (neuron_ids, time_bins, values)]
+    nat.call("cortex_tokenize", nat.code(neuron_emb.dtype), D,
+             nat.ptr(neuron_emb), neuron_emb.shape[0], neuron_emb.stride(0),
+             nat.ptr(time_emb), time_emb.shape[0], time_emb.stride(0),
+             nat.ptr(value_emb), value_emb.shape[0], value_emb.stride(0),
+             nat.ptr(neuron_ids), st[0], nat.ptr(time_bins), st[1], nat.ptr(values), st[2], E,
+             nat.ptr(order), _end_ptr(csr_offsets), nat.ptr(offsets), batch_size, max_events, nat.ptr(out),
+             ld_out, nat.ptr(mask) if padded else None, nat.ptr(err), nat.stream_of(dev))
+    return (out, mask) if padded else out
+
+
+def _end_ptr(offsets) -> int | None:
+    """Device address of offsets[B] (the number of valid CSR rows)."""
+    if offsets is None:
+        return None
+    return offsets.data_ptr() + (offsets.numel() - 1) * offsets.element_size()
+
+
+def pack_rows(src, order, offsets, batch_size: int, max_events: int):
+    """Padded ``(B, max_events, D)`` copy of CSR-ordered rows plus the bool mask."""
+    dev = nat.require_gpu(src, order, offsets, what="pack_rows")
+    src = _row_major_2d(src)
+    E, D = src.shape
+    out = torch.empty((batch_size, max_events, D), dtype=src.dtype, device=dev)
+    mask = torch.empty((batch_size, max_events), dtype=torch.bool, device=dev)
+    nat.call("cortex_pack_rows", nat.code(src.dtype), D, nat.ptr(src), src.stride(0) if E > 1 else D, E,
+             nat.ptr(order), None, nat.ptr(offsets), batch_size, max_events, nat.ptr(out), D, nat.ptr(mask),
+             nat.stream_of(dev))
+    return out, mask
+
+
+# --------------------------------------------------------------------------- quantise
+
+
+def quantize_int8(weight: torch.Tensor, scale: torch.Tensor | None = None):
+    """INT8 per-row quantisation of a 2-D fp32 weight: ``(q int8 (N,K), scale fp32 (N,))``."""
+    dev = nat.require_gpu(weight, scale, what="quantize_int8")
+    w = _row_major_2d(weight.detach().float())
+    N, K = w.shape
+    q = torch.empty((N, K), dtype=torch.int8, device=dev)
+    s_out = None
+    if scale is None:
+        s_out = torch.empty(N, dtype=torch.float32, device=dev)
+    else:
+        scale = scale.detach().to(device=dev, dtype=torch.float32).contiguous()
+    nat.call("cortex_quantize_int8", nat.ptr(w), N, K, w.stride(0) if N > 1 else K, nat.ptr(scale),
+             nat.ptr(s_out), nat.ptr(q), K, nat.stream_of(dev))
+    return q, (s_out if scale is None else scale)
+
+
+# --------------------------------------------------------------------------- norms
+
+
+def row_stats(x: torch.Tensor, norm: str, eps: float, out=None) -> torch.Tensor:
+    """(M, 2) fp32 per-row statistics: LayerNorm (mean, rstd) or RMSNorm (0, rms)."""
+    dev = nat.require_gpu(x, what="row_stats")
+    x = _row_major_2d(x)
+    M, K = x.shape
+    if out is None:
+        out = torch.empty((M, 2), dtype=torch.float32, device=dev)
+    nat.call("cortex_row_stats", M, K, nat.code(x.dtype), nat.ptr(x), x.stride(0) if M > 1 else K, NORM[norm],
+             float(eps), nat.ptr(out), nat.stream_of(dev))
+    return out
+
+
+def layer_norm(x: torch.Tensor, weight, bias, eps: float, out_dtype=None, out=None) -> torch.Tensor:
+    """LayerNorm over the last dim, written out (any leading shape)."""
+    dev = nat.require_gpu(x, weight, bias, what="layer_norm")
+    K = x.shape[-1]
+    x2 = _row_major_2d(x.reshape(-1, K))
+    M = x2.shape[0]
+    out_dtype = out_dtype or x.dtype
+    if out is None:
+        out = torch.empty(x.shape, dtype=out_dtype, device=dev)
+    gdt = nat.code(weight.dtype) if weight is not None else nat.F32
+    nat.call("cortex_layer_norm", M, K, nat.code(x2.dtype), nat.ptr(x2), x2.stride(0) if M > 1 else K,
+             nat.ptr(weight), nat.ptr(bias), gdt, float(eps), nat.code(out.dtype), nat.ptr(out), K,
+             nat.stream_of(dev))
+    return out
+
+
+# --------------------------------------------------------------------------- linear
+
+
+def norm_linear(x: torch.Tensor, *, weight: torch.Tensor | None = None, weight_int8: torch.Tensor | None = None,
+                weight_scale: torch.Tensor | None = None, w_layout: str = "nk", norm: str | None = None,
+                gamma=None, beta=None, eps: float = 1e-5, stats=None, bias=None, act: str | None = None,
+                residual: torch.Tensor | None = None, res_rows: int = 0, out_dtype=None,
+                compute_dtype=torch.bfloat16, out: torch.Tensor | None = None) -> torch.Tensor:
+    """``act(norm(x) @ W^T * scale + bias) + residual`` over the last dim of ``x``.
+
+    ``weight`` is a float (N, K) (``w_layout='nk'``, nn.Linear) or (K, N)
+    (``'kn'``, rms_norm_linear) matrix; ``weight_int8``/``weight_scale`` is the
+    QuantizedLinear form.  ``compute_dtype`` is the MFMA input dtype (bf16 or fp32).
+    """
+    w = weight if weight is not None else weight_int8
+    dev = nat.require_gpu(x, w, weight_scale, gamma, beta, bias, residual, out, what="norm_linear")
+    K = x.shape[-1]
+    lead = x.shape[:-1]
+    x2 = _row_major_2d(x.reshape(-1, K))
+    M = x2.shape[0]
+    if weight_int8 is not None:
+        if weight_int8.dtype != torch.int8 or weight_scale is None:
+            raise ValueError("weight_int8 must be int8 and come with weight_scale")
+        w2 = _row_major_2d(weight_int8)
+        N, Kw = w2.shape
+        layout = 0
+        ws = weight_scale.contiguous()
+    else:
+        w2 = _row_major_2d(weight.detach())
+        layout = 0 if w_layout == "nk" else 1
+        N, Kw = (w2.shape if layout == 0 else (w2.shape[1], w2.shape[0]))
+        ws = None
+    if Kw != K:
+        raise ValueError(f"inner dims differ: x has K={K}, weight has K={Kw}")
+    if compute_dtype not in (torch.bfloat16, torch.float32):
+        raise ValueError(f"compute dtype {compute_dtype} not supported (bfloat16 or float32)")
+    if x2.dtype == torch.bfloat16 and compute_dtype != torch.bfloat16:
+        raise ValueError("bf16 activations need bf16 compute")
+    out_dtype = out_dtype or x.dtype
+    if out is None:
+        out = torch.empty((*lead, N), dtype=out_dtype, device=dev)
+    out2 = out.reshape(-1, N)
+    if out2.data_ptr() != out.data_ptr() or (M > 1 and out2.stride(0) < N) or out2.stride(-1) != 1:
+        raise ValueError("out must be row-major contiguous over its last dim")
+    nrm = NORM[norm]
+    if nrm and stats is None:
+        stats = row_stats(x2, "layer" if nrm == 1 else "rms", eps)
+    res2 = None
+    if residual is not None:
+        res2 = residual.reshape(-1, N) if residual.dim() != 2 else residual
+        res2 = _row_major_2d(res2)
+    ld_w = w2.stride(0) if w2.shape[0] > 1 else w2.shape[1]
+    gdt = nat.code(gamma.dtype) if gamma is not None else nat.F32
+    nat.call("cortex_norm_linear", M, N, K, nat.code(x2.dtype), nat.ptr(x2), x2.stride(0) if M > 1 else K, nrm,
+             nat.ptr(stats), nat.ptr(gamma), nat.ptr(beta), gdt, nat.code(compute_dtype),
+             nat.code(w2.dtype), layout, nat.ptr(w2), ld_w, nat.ptr(ws),
+             nat.code(bias.dtype) if bias is not None else nat.F32, nat.ptr(bias), ACT[act],
+             nat.code(res2.dtype) if res2 is not None else nat.F32, nat.ptr(res2),
+             (res2.stride(0) if res2.shape[0] > 1 else N) if res2 is not None else 0, int(res_rows),
+             nat.code(out2.dtype), nat.ptr(out2), out2.stride(0) if M > 1 else N, nat.stream_of(dev))
+    return out
+
+
+# --------------------------------------------------------------------------- attention
+
+
+def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, scale: float | None = None,
+              kv_offsets: torch.Tensor | None = None, kv_lengths: torch.Tensor | None = None,
+              key_mask: torch.Tensor | None = None, block_mask: torch.Tensor | None = None,
+              block_l: int = 64, block_e: int = 64, out: torch.Tensor | None = None,
+              batch: int | None = None) -> torch.Tensor:
+    """``softmax(scale q k^T | allowed) v`` for (B, H, L, Dh) views (any strides, Dh contiguous).
+
+    ``q`` may have batch stride 0 (batch-invariant queries, ``expand``-ed).  With
+    ``kv_offsets`` (B+1) ``k``/``v`` are (1, H, E_total, Dh) CSR views and sample b
+    uses rows [kv_offsets[b], kv_offsets[b+1]).
+    """
+    tensors = [q, k, v, kv_offsets, kv_lengths, key_mask, block_mask, out]
+    dev = nat.require_gpu(*tensors, what="attention")
+    if q.dtype != k.dtype or q.dtype != v.dtype:
+        raise ValueError("q, k, v must share a dtype")
+    if q.dtype not in (torch.bfloat16, torch.float32):
+        raise ValueError(f"attention dtype {q.dtype} not supported (bfloat16 or float32)")
+    for t in (q, k, v):
+        if t.stride(-1) != 1:
+            raise ValueError("attention inputs need a contiguous last (head) dim")
+    B = q.shape[0] if batch is None else batch
+    H, Lq, Dh = q.shape[1], q.shape[2], q.shape[3]
+    Lk = k.shape[2]
+    if out is None:
+        out = torch.empty((B, H, Lq, Dh), dtype=q.dtype, device=dev)
+    s = float(scale) if scale is not None else Dh ** -0.5
+    km_sb = 0
+    if key_mask is not None:
+        key_mask = key_mask.to(torch.uint8) if key_mask.dtype == torch.bool else key_mask
+        key_mask = key_mask.contiguous()
+        km_sb = key_mask.stride(0) if key_mask.dim() == 2 else 0
+    bm_sb = n_qt = n_kt = 0
+    if block_mask is not None:
+        block_mask = block_mask.to(device=dev, dtype=torch.uint8).contiguous()
+        n_qt, n_kt = block_mask.shape[-2], block_mask.shape[-1]
+        bm_sb = block_mask.stride(0) if block_mask.dim() == 3 else 0
+    qsb = q.stride(0) if q.shape[0] > 1 else 0
+    nat.call("cortex_attention", nat.code(q.dtype), B, H, Lq, Lk, Dh,
+             nat.ptr(q), qsb, q.stride(1), q.stride(2),
+             nat.ptr(k), k.stride(0), k.stride(1), k.stride(2),
+             nat.ptr(v), v.stride(0), v.stride(1), v.stride(2),
+             nat.ptr(kv_offsets), nat.ptr(kv_lengths), nat.ptr(key_mask), km_sb,
+             nat.ptr(block_mask), bm_sb, n_qt, n_kt, int(block_l), int(block_e), s,
+             nat.ptr(out), out.stride(0), out.stride(1), out.stride(2), nat.stream_of(dev))
+    return out
+
+
+def heads_view(x2d: torch.Tensor, batch: int, length: int, heads: int, col0: int = 0, width: int | None = None):
+    """(B*L, C) row-major buffer -> (B, H, L, Dh) view of columns [col0, col0+width)."""
+    C = x2d.shape[-1]
+    width = width if width is not None else C - col0
+    dh = width // heads
+    return x2d.as_strided((batch, heads, length, dh), (length * x2d.stride(0), dh, x2d.stride(0), 1),
+                          x2d.storage_offset() + col0)
+
+
+def merge_heads_out(batch: int, length: int, heads: int, dh: int, dtype, device):
+    """Allocate a (B*L, H*Dh) buffer and its (B, H, L, Dh) view for attention output."""
+    buf = torch.empty((batch * length, heads * dh), dtype=dtype, device=device)
+    return buf, heads_view(buf, batch, length, heads)
+
+
+def ceil_div(a: int, b: int) -> int:
+    return -(-a // b)
+
+
+__all__ = [
+    "pack_plan", "tokenize", "pack_rows", "quantize_int8", "row_stats", "layer_norm", "norm_linear",
+    "attention", "heads_view", "merge_heads_out", "ceil_div", "math",
+]

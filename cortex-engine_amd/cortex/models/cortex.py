@@ -1,0 +1,142 @@
+"""Top-level Cortex model (reference cortex/models/cortex.py:15-165).
+
+``CortexModel.forward`` on a ROCm device runs the whole Cortex-S inference path on
+the gfx950 kernels without padding the events:
+
+1. device-side stable pack plan of ``batch_indices`` -> CSR offsets + row order
+   (no host read-back when ``batch_size`` is given);
+2. fused tokenizer writing the tokens directly in CSR order;
+3. ``norm_kv`` + ``kv_proj`` on the E_total real event rows only;
+4. cross-attention of the batch-invariant latent queries (projected once, not
+   once per sample) against each sample's CSR key/value rows -- padded tiles do
+   not exist, so they are never visited;
+5. ``out_proj`` with the learned latents as a broadcast residual, 7 fused
+   self-attention blocks, ``final_norm``;
+6. behaviour head: ``norm`` + ``kv_proj`` fused, the 2 batch-invariant queries
+   projected once, attention, ``out_proj`` to (B, behavior_dim).
+
+Results equal the reference forward (padded SDPA with a key-padding mask) up to
+floating-point rounding; with ``config.dtype='float32'`` every operand is fp32.
+"""
+
+from __future__ import annotations
+
+import torch
+from torch import nn
+
+from cortex.kernels import ops
+from cortex.kernels.pack import pack_events as _device_pack_events
+from cortex.models._layers import apply_linear
+from cortex.models.config import CortexConfig
+from cortex.models.perceiver import PerceiverEncoder
+from cortex.models.tokenizer import SpikeTokenizer
+
+
+class BehaviorDecoder(nn.Module):
+    """Learned behaviour queries cross-attending to the latents (reference :15-53)."""
+
+    def __init__(self, config: CortexConfig) -> None:
+        super().__init__()
+        self.config = config
+        self.query = nn.Parameter(torch.randn(config.behavior_dim, config.latent_dim) * 0.02)
+        self.q_proj = nn.Linear(config.latent_dim, config.latent_dim, bias=False)
+        self.kv_proj = nn.Linear(config.latent_dim, 2 * config.latent_dim, bias=False)
+        self.out_proj = nn.Linear(config.latent_dim, 1, bias=False)
+        self.norm = nn.LayerNorm(config.latent_dim)
+        self.num_heads = config.num_heads
+        self.head_dim = config.head_dim
+
+    def forward_rows(self, lat: torch.Tensor, batch: int) -> torch.Tensor:
+        """(B*L, D) latents (after final_norm) -> (B, behavior_dim) fp32."""
+        compute = self.config.compute_dtype
+        L = self.config.num_latents
+        D = lat.shape[1]
+        H = self.num_heads
+        Q = self.query.shape[0]
+        kv = apply_linear(self.kv_proj, lat, norm=self.norm, out_dtype=compute, compute=compute)
+        q = apply_linear(self.q_proj, self.query, out_dtype=compute, compute=compute)  # (Q, D), batch-invariant
+        o_buf, o = ops.merge_heads_out(batch, Q, H, D // H, compute, lat.device)
+        ops.attention(ops.heads_view(q, 1, Q, H), ops.heads_view(kv, batch, L, H, 0, D),
+                      ops.heads_view(kv, batch, L, H, D, D), out=o, batch=batch)
+        out = apply_linear(self.out_proj, o_buf, out_dtype=torch.float32, compute=compute)
+        return out.reshape(batch, Q)
+
+    def forward(self, latents: torch.Tensor) -> torch.Tensor:
+        """latents (B, L, D) -> behaviour (B, behavior_dim)."""
+        B, L, D = latents.shape
+        return self.forward_rows(latents.reshape(B * L, D).contiguous(), B).to(latents.dtype)
+
+
+class MaskedSpikeHead(nn.Module):
+    """Self-supervised pretraining head (reference :56-69); not part of inference."""
+
+    def __init__(self, config: CortexConfig) -> None:
+        super().__init__()
+        self.proj = nn.Linear(config.latent_dim, config.spike_value_buckets)
+
+    def forward(self, latents: torch.Tensor) -> torch.Tensor:
+        raise NotImplementedError("the masked spike head is a training head; the HIP path covers inference")
+
+
+class CortexModel(nn.Module):
+    """Perceiver-style neural decoder (reference :72-122)."""
+
+    def __init__(self, config: CortexConfig) -> None:
+        super().__init__()
+        self.config = config
+        self.tokenizer = SpikeTokenizer(config)
+        self.encoder = PerceiverEncoder(config)
+        self.behavior_head = BehaviorDecoder(config)
+        self.masked_spike_head = MaskedSpikeHead(config) if config.use_masked_spike_head else None
+
+    def forward(self, neuron_ids: torch.Tensor, time_bins: torch.Tensor, values: torch.Tensor,
+                batch_indices: torch.Tensor, return_aux: bool = False, *, batch_size: int | None = None,
+                err_flag: torch.Tensor | None = None) -> dict[str, torch.Tensor]:
+        """Spike events -> ``{"behavior": (B, behavior_dim)}``.
+
+        ``batch_size`` (keyword-only) avoids reading ``max(batch_indices)+1`` back to the
+        host; ``err_flag`` (int32 device tensor) collects index-range violations
+        without a synchronisation.
+        """
+        if return_aux:
+            raise NotImplementedError("return_aux (masked spike head) is a training output; not on the HIP path")
+        if not (neuron_ids.shape == time_bins.shape == values.shape == batch_indices.shape):
+            raise ValueError(
+                f"shape mismatch: neuron_ids={neuron_ids.shape}, time_bins={time_bins.shape}, "
+                f"values={values.shape}, batch_indices={batch_indices.shape}"
+            )
+        E = neuron_ids.shape[0]
+        if batch_size is None:
+            batch_size = int(batch_indices.max().item()) + 1 if E > 0 else 1
+        return {"behavior": self._forward_csr(neuron_ids, time_bins, values, batch_indices, int(batch_size),
+                                              err_flag)}
+
+    def _forward_csr(self, neuron_ids, time_bins, values, batch_indices, B: int, err_flag=None) -> torch.Tensor:
+        cfg = self.config
+        compute = cfg.compute_dtype
+        tok = self.tokenizer
+        enc = self.encoder
+        xa = enc.cross_attn
+        D, L, H = cfg.latent_dim, cfg.num_latents, xa.num_heads
+        offsets, order, _ = ops.pack_plan(batch_indices, B, err=err_flag)
+        tokens = ops.tokenize(tok.neuron_emb.weight, tok.time_emb.weight, tok.value_emb.weight, neuron_ids,
+                              time_bins, values, order=order, csr_offsets=offsets, err=err_flag)  # CSR rows
+        E = tokens.shape[0]
+        kv = apply_linear(xa.kv_proj, tokens, norm=xa.norm_kv, out_dtype=compute, compute=compute)  # (E, 2D)
+        q = xa.project_queries(enc.latents, compute)  # (L, D), shared by every sample
+        o_buf, o = ops.merge_heads_out(B, L, H, D // H, compute, tokens.device)
+        ops.attention(ops.heads_view(q, 1, L, H), ops.heads_view(kv, 1, E, H, 0, D),
+                      ops.heads_view(kv, 1, E, H, D, D), kv_offsets=offsets, out=o, batch=B)
+        x = apply_linear(xa.out_proj, o_buf, residual=enc.latents, res_rows=L, out_dtype=torch.float32,
+                         compute=compute)  # (B*L, D) fp32 residual stream
+        lat = enc.encode_rows(x, B)
+        return self.behavior_head.forward_rows(lat, B)
+
+
+def _pack_events(flat_tokens: torch.Tensor, batch_indices: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """Pack flat (E, D) tokens into (B, E_max, D) with a (B, E_max) bool mask.
+
+    Same contract as reference cortex/models/cortex.py:125-165 (B and E_max read
+    back from the device); runs the device-side stable pack.
+    """
+    return _device_pack_events(flat_tokens, batch_indices)

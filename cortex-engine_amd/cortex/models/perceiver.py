@@ -1,0 +1,122 @@
+"""Perceiver encoder modules (reference cortex/models/perceiver.py:35-158).
+
+Parameters, names and construction order follow the reference so that seeded
+initialisation and state_dicts are identical.  On a ROCm device each block runs as
+fused HIP kernels: LayerNorm folded into the following linear's A-tile staging,
+INT8/float weights on MFMA with dequant / GELU / residual in the epilogue, and the
+attention kernel reading heads straight out of the projection buffers (no
+rearrange copies).  The residual stream stays fp32; linear operands use the
+config's compute dtype.
+"""
+
+from __future__ import annotations
+
+import torch
+from torch import nn
+
+from cortex.kernels import ops
+from cortex.models._layers import apply_linear
+from cortex.models.config import CortexConfig
+
+
+class CrossAttentionBlock(nn.Module):
+    """Cross-attention from input tokens into the latent array (reference :35-82)."""
+
+    def __init__(self, config: CortexConfig) -> None:
+        super().__init__()
+        self.config = config
+        self.num_heads = config.cross_attn_heads
+        self.head_dim = config.latent_dim // config.cross_attn_heads
+        if self.head_dim * self.num_heads != config.latent_dim:
+            raise ValueError("latent_dim must be divisible by cross_attn_heads")
+        self.q_proj = nn.Linear(config.latent_dim, config.latent_dim, bias=False)
+        self.kv_proj = nn.Linear(config.hidden_dim, 2 * config.latent_dim, bias=False)
+        self.out_proj = nn.Linear(config.latent_dim, config.latent_dim, bias=False)
+        self.norm_q = nn.LayerNorm(config.latent_dim)
+        self.norm_kv = nn.LayerNorm(config.hidden_dim)
+
+    def project_queries(self, latents: torch.Tensor, compute: torch.dtype) -> torch.Tensor:
+        """``q_proj(norm_q(latents))`` for (L, D) batch-invariant latents -> (L, D)."""
+        return apply_linear(self.q_proj, latents, norm=self.norm_q, out_dtype=compute, compute=compute)
+
+    def forward(self, latents: torch.Tensor, tokens: torch.Tensor,
+                token_mask: torch.Tensor | None = None) -> torch.Tensor:
+        """latents (B, L, D), tokens (B, E, D), token_mask (B, E) bool -> (B, L, D)."""
+        compute = self.config.compute_dtype
+        B, L, D = latents.shape
+        E = tokens.shape[1]
+        H = self.num_heads
+        q = apply_linear(self.q_proj, latents, norm=self.norm_q, out_dtype=compute, compute=compute)
+        kv = apply_linear(self.kv_proj, tokens, norm=self.norm_kv, out_dtype=compute, compute=compute)
+        q2, kv2 = q.reshape(B * L, D), kv.reshape(B * E, 2 * D)
+        o_buf, o = ops.merge_heads_out(B, L, H, D // H, compute, latents.device)
+        ops.attention(ops.heads_view(q2, B, L, H), ops.heads_view(kv2, B, E, H, 0, D),
+                      ops.heads_view(kv2, B, E, H, D, D), key_mask=token_mask, out=o)
+        return apply_linear(self.out_proj, o_buf, residual=latents.reshape(B * L, D).contiguous(),
+                            out_dtype=latents.dtype, compute=compute).reshape(B, L, D)
+
+
+class SelfAttentionBlock(nn.Module):
+    """Pre-norm self-attention + GELU MLP over the latents (reference :85-126)."""
+
+    def __init__(self, config: CortexConfig) -> None:
+        super().__init__()
+        self.config = config
+        self.num_heads = config.num_heads
+        self.head_dim = config.head_dim
+        self.qkv_proj = nn.Linear(config.latent_dim, 3 * config.latent_dim, bias=False)
+        self.out_proj = nn.Linear(config.latent_dim, config.latent_dim, bias=False)
+        self.norm_attn = nn.LayerNorm(config.latent_dim)
+        self.norm_mlp = nn.LayerNorm(config.latent_dim)
+        mlp_hidden = int(config.latent_dim * config.mlp_ratio)
+        self.mlp = nn.Sequential(
+            nn.Linear(config.latent_dim, mlp_hidden, bias=False),
+            nn.GELU(),
+            nn.Linear(mlp_hidden, config.latent_dim, bias=False),
+        )
+
+    def forward_rows(self, x: torch.Tensor, batch: int, length: int) -> torch.Tensor:
+        """Block on a (B*L, D) fp32 residual buffer; returns the new residual buffer."""
+        compute = self.config.compute_dtype
+        D = x.shape[1]
+        H = self.num_heads
+        qkv = apply_linear(self.qkv_proj, x, norm=self.norm_attn, out_dtype=compute, compute=compute)
+        o_buf, o = ops.merge_heads_out(batch, length, H, D // H, compute, x.device)
+        ops.attention(ops.heads_view(qkv, batch, length, H, 0, D), ops.heads_view(qkv, batch, length, H, D, D),
+                      ops.heads_view(qkv, batch, length, H, 2 * D, D), out=o)
+        x = apply_linear(self.out_proj, o_buf, residual=x, out_dtype=x.dtype, compute=compute)
+        h = apply_linear(self.mlp[0], x, norm=self.norm_mlp, act="gelu", out_dtype=compute, compute=compute)
+        return apply_linear(self.mlp[2], h, residual=x, out_dtype=x.dtype, compute=compute)
+
+    def forward(self, latents: torch.Tensor) -> torch.Tensor:
+        """(B, L, D) -> (B, L, D)."""
+        B, L, D = latents.shape
+        x = latents.reshape(B * L, D).contiguous()
+        return self.forward_rows(x, B, L).reshape(B, L, D)
+
+
+class PerceiverEncoder(nn.Module):
+    """Cross-attention into learned latents, then N self-attention blocks (reference :129-158)."""
+
+    def __init__(self, config: CortexConfig) -> None:
+        super().__init__()
+        self.config = config
+        self.latents = nn.Parameter(torch.randn(config.num_latents, config.latent_dim) * 0.02)
+        self.cross_attn = CrossAttentionBlock(config)
+        self.self_attn_blocks = nn.ModuleList([SelfAttentionBlock(config) for _ in range(config.num_layers)])
+        self.final_norm = nn.LayerNorm(config.latent_dim)
+
+    def encode_rows(self, x: torch.Tensor, batch: int) -> torch.Tensor:
+        """Self-attention stack + final norm on the (B*L, D) residual after cross-attention."""
+        L = self.config.num_latents
+        for block in self.self_attn_blocks:
+            x = block.forward_rows(x, batch, L)
+        return ops.layer_norm(x, self.final_norm.weight, self.final_norm.bias, self.final_norm.eps)
+
+    def forward(self, tokens: torch.Tensor, token_mask: torch.Tensor | None = None) -> torch.Tensor:
+        """tokens (B, E, D), token_mask (B, E) bool -> latents (B, L, D)."""
+        B = tokens.shape[0]
+        L, D = self.latents.shape
+        lat = self.latents.unsqueeze(0).expand(B, -1, -1)
+        x = self.cross_attn(lat, tokens, token_mask)
+        return self.encode_rows(x.reshape(B * L, D), B).reshape(B, L, D)

@@ -1,0 +1,116 @@
+// Shared device/host helpers for the Cortex gfx950 kernels.
+//
+// Conventions used by every kernel in this library:
+//  * one 64-lane wavefront is the unit of cooperation (CDNA4);
+//  * MFMA fragments are 8 consecutive K-elements per lane: lane l owns row/column
+//    (l % 16) and the K slice [8*(l/16), 8*(l/16)+8) of a 16 x 32 operand block;
+//    bf16 feeds one v_mfma_f32_16x16x32_bf16, fp32 feeds eight
+//    v_mfma_f32_16x16x4_f32 (slot j of every lane forms the j-th 16x16x4 step,
+//    i.e. the K order is permuted identically on both operands);
+//  * the 16x16 fp32 accumulator holds element (4*(l/16)+i, l%16) in register i.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <cmath>
+
+namespace cortex {
+
+typedef __bf16 bf16;
+typedef _Float16 f16;
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x8 __attribute__((ext_vector_type(8)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x2 __attribute__((ext_vector_type(2)));
+
+// dtype codes shared with include/cortex_hip.h
+enum DType : int { DT_F32 = 0, DT_BF16 = 1, DT_F16 = 2, DT_I8 = 3, DT_I32 = 4, DT_I64 = 5, DT_U8 = 6 };
+
+__device__ __forceinline__ float to_f32(float x) { return x; }
+__device__ __forceinline__ float to_f32(bf16 x) { return (float)x; }
+__device__ __forceinline__ float to_f32(int8_t x) { return (float)(int)x; }
+__device__ __forceinline__ float to_f32(f16 x) { return (float)x; }
+
+template <class T>
+__device__ __forceinline__ T from_f32(float x);
+template <>
+__device__ __forceinline__ float from_f32<float>(float x) { return x; }
+template <>
+__device__ __forceinline__ bf16 from_f32<bf16>(float x) { return (bf16)x; }  // RNE
+template <>
+__device__ __forceinline__ f16 from_f32<f16>(float x) { return (f16)x; }  // RNE
+
+// Fragment of 8 K-consecutive operand values for one lane.
+template <class T>
+struct Frag;
+template <>
+struct Frag<bf16> {
+  bf16x8 v;
+};
+template <>
+struct Frag<float> {
+  f32x8 v;
+};
+
+// acc(16x16, fp32) += A(16 x 32) * B(32 x 16) with both operands as fragments.
+__device__ __forceinline__ void mfma_16x16x32(f32x4& acc, const Frag<bf16>& a, const Frag<bf16>& b) {
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.v, b.v, acc, 0, 0, 0);
+}
+__device__ __forceinline__ void mfma_16x16x32(f32x4& acc, const Frag<float>& a, const Frag<float>& b) {
+#pragma unroll
+  for (int j = 0; j < 8; ++j) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.v[j], b.v[j], acc, 0, 0, 0);
+}
+
+// Cross-lane reductions inside one wavefront.
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+  return v;
+}
+
+__host__ __device__ __forceinline__ int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// erf-form GELU, as torch.nn.GELU() with approximate='none': 0.5 x (1 + erf(x / sqrt 2)).
+__device__ __forceinline__ float gelu_erf(float x) { return 0.5f * x * (1.0f + erff(x * 0.70710678118654752440f)); }
+
+}  // namespace cortex
+
+// ----------------------------------------------------------------------------
+// Host-side error plumbing for the C ABI: every entry point returns 0 or a
+// negative status and records a message retrievable by cortex_last_error().
+// ----------------------------------------------------------------------------
+namespace cortex {
+enum Status : int {
+  OK = 0,
+  E_INVALID = -1,      // bad shape / dtype / stride / pointer
+  E_UNSUPPORTED = -2,  // valid request this build does not implement
+  E_LAUNCH = -3,       // HIP launch or runtime error
+  E_WORKSPACE = -4,    // workspace too small
+};
+void set_error(const char* fmt, ...);
+}  // namespace cortex
+
+#define CORTEX_CHECK_ARG(cond, ...)          \
+  do {                                       \
+    if (!(cond)) {                           \
+      ::cortex::set_error(__VA_ARGS__);      \
+      return ::cortex::E_INVALID;            \
+    }                                        \
+  } while (0)
+
+#define CORTEX_CHECK_LAUNCH(what)                                                   \
+  do {                                                                              \
+    hipError_t _e = hipGetLastError();                                              \
+    if (_e != hipSuccess) {                                                         \
+      ::cortex::set_error("%s: launch failed: %s", what, hipGetErrorString(_e));    \
+      return ::cortex::E_LAUNCH;                                                    \
+    }                                                                               \
+  } while (0)

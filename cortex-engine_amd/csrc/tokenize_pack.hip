@@ -1,0 +1,423 @@
+// Spike tokenizer and ragged-event pack for gfx950.
+//
+//   * pack plan: a device-side stable counting sort of the events by batch index
+//     (three short launches, no host synchronisation): per-chunk histograms,
+//     one scan over (chunk, sample), then in-order ranking inside each chunk.
+//     It yields CSR offsets (B+1), the CSR row of every event and the source
+//     event of every CSR row -- exactly the stable argsort + exclusive cumsum of
+//     the reference pack (cortex/models/cortex.py:140-160).
+//   * row writer: one wavefront per output row, 16-byte coalesced stores, that
+//     either gathers the three embedding rows and adds them
+//     ((N[nid] + T[tb]) + V[val], reference cortex/kernels/tokenizer.py:81) or
+//     copies an existing token row.  Output rows are CSR order (E rows) or the
+//     padded (B, E_max) layout with its bool mask (cortex.py:146-147,163-164).
+#include <hip/hip_runtime.h>
+
+#include "common.h"
+
+namespace cortex {
+
+// Error-flag bits (device int32, OR-ed).
+constexpr int ERR_TOKEN_INDEX = 1;  // neuron/time/value index outside its table
+constexpr int ERR_BATCH_INDEX = 2;  // batch index outside [0, B)
+
+constexpr int PACK_MAX_B = 8192;   // LDS histogram bins per chunk
+constexpr int PACK_MAX_CHUNKS = 1024;
+
+__host__ __device__ inline int64_t pack_chunk_size(int64_t E) {
+  int64_t c = 1024;
+  int64_t need = cdiv(E, PACK_MAX_CHUNKS);
+  if (need > c) c = cdiv(need, 64) * 64;
+  return c;
+}
+
+// Small fill (kept as a kernel so that callers may capture it in a graph).
+__global__ void fill_i64_kernel(int64_t* p, int64_t n, int64_t v) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = v;
+}
+
+// 1) per-chunk histogram of batch indices.
+__global__ __launch_bounds__(256) void pack_count_kernel(const int64_t* __restrict__ bidx, int64_t s_bidx, int64_t E,
+                                                          int B, int64_t C, int* __restrict__ counts,
+                                                          int* __restrict__ err) {
+  __shared__ int hist[PACK_MAX_B];
+  const int chunk = blockIdx.x;
+  for (int b = threadIdx.x; b < B; b += blockDim.x) hist[b] = 0;
+  __syncthreads();
+  const int64_t beg = (int64_t)chunk * C;
+  const int64_t end = min(E, beg + C);
+  bool bad = false;
+  for (int64_t i = beg + threadIdx.x; i < end; i += blockDim.x) {
+    int64_t b = bidx[i * s_bidx];
+    if (b < 0 || b >= B) {
+      bad = true;
+    } else {
+      atomicAdd(&hist[b], 1);
+    }
+  }
+  if (bad && err) atomicOr(err, ERR_BATCH_INDEX);
+  __syncthreads();
+  for (int b = threadIdx.x; b < B; b += blockDim.x) counts[(int64_t)chunk * B + b] = hist[b];
+}
+
+// 2) exclusive scan over chunks per sample (in place), then over samples.
+__global__ __launch_bounds__(1024) void pack_scan_kernel(int* __restrict__ counts, int nchunks, int B,
+                                                          int64_t* __restrict__ offsets) {
+  __shared__ int64_t part[1024];
+  __shared__ int totals[PACK_MAX_B];
+  const int tid = threadIdx.x;
+  for (int b = tid; b < B; b += blockDim.x) {
+    int run = 0;
+    for (int c = 0; c < nchunks; ++c) {
+      int t = counts[(int64_t)c * B + b];
+      counts[(int64_t)c * B + b] = run;
+      run += t;
+    }
+    totals[b] = run;
+  }
+  __syncthreads();
+  // each thread owns a contiguous span of samples
+  const int per = (B + blockDim.x - 1) / blockDim.x;
+  const int b0 = tid * per;
+  int64_t local = 0;
+  for (int b = b0; b < min(B, b0 + per); ++b) local += totals[b];
+  part[tid] = local;
+  __syncthreads();
+  // Hillis-Steele inclusive scan of the 1024 partials
+  for (int off = 1; off < (int)blockDim.x; off <<= 1) {
+    int64_t v = (tid >= off) ? part[tid - off] : 0;
+    __syncthreads();
+    part[tid] += v;
+    __syncthreads();
+  }
+  int64_t run = part[tid] - local;  // exclusive prefix of this span
+  for (int b = b0; b < min(B, b0 + per); ++b) {
+    offsets[b] = run;
+    run += totals[b];
+  }
+  if (tid == blockDim.x - 1) offsets[B] = part[tid];
+}
+
+// 3) in-order ranking inside each chunk: one wavefront walks its chunk 64 events
+//    at a time; lanes holding the same sample are ranked by lane order.
+__global__ __launch_bounds__(64) void pack_rank_kernel(const int64_t* __restrict__ bidx, int64_t s_bidx, int64_t E,
+                                                        int B, int64_t C, const int* __restrict__ chunk_base,
+                                                        const int64_t* __restrict__ offsets,
+                                                        int64_t* __restrict__ order, int64_t* __restrict__ dst_rows,
+                                                        int64_t* __restrict__ rank) {
+  __shared__ int64_t next[PACK_MAX_B];
+  const int chunk = blockIdx.x;
+  const int lane = threadIdx.x;
+  for (int b = lane; b < B; b += 64) next[b] = offsets[b] + chunk_base[(int64_t)chunk * B + b];
+  __syncthreads();
+  const int64_t beg = (int64_t)chunk * C;
+  const int64_t end = min(E, beg + C);
+  const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  for (int64_t base = beg; base < end; base += 64) {
+    const int64_t i = base + lane;
+    int64_t b = -1;
+    if (i < end) {
+      b = bidx[i * s_bidx];
+      if (b >= B) b = -1;  // counted as an error by pack_count_kernel
+    }
+    uint64_t active = __ballot(b >= 0);
+    while (active) {
+      const int leader = __ffsll((unsigned long long)active) - 1;
+      const int64_t lb = __shfl(b, leader, 64);
+      const uint64_t same = __ballot(b == lb) & active;
+      const int64_t row0 = next[lb];
+      if (b == lb) {
+        const int64_t row = row0 + __popcll(same & lt_mask);
+        order[row] = i;
+        if (dst_rows) dst_rows[i] = row;
+        if (rank) rank[i] = row - offsets[lb];
+      }
+      __syncthreads();  // single wavefront: orders the LDS read above before the update below
+      if (lane == leader) next[lb] = row0 + __popcll(same);
+      __syncthreads();
+      active &= ~same;
+    }
+  }
+}
+
+// Row writer -------------------------------------------------------------------
+
+template <class T>
+__device__ __forceinline__ T add_rn(T a, T b) {
+  return from_f32<T>(to_f32(a) + to_f32(b));
+}
+template <>
+__device__ __forceinline__ float add_rn<float>(float a, float b) {
+  return a + b;
+}
+
+// 16-byte vector of T
+template <class T>
+struct Vec16 {
+  static constexpr int N = 16 / sizeof(T);
+  T v[N];
+};
+
+struct RowArgs {
+  // sources
+  const void* tab[3];      // neuron, time, value tables (table mode)
+  int64_t tab_rows[3];
+  int64_t tab_ld[3];
+  const int64_t* ids[3];   // per-event indices (table mode)
+  int64_t ids_stride[3];
+  const void* src;         // (E, D) token rows (copy mode)
+  int64_t src_ld;
+  // mapping
+  int64_t E;               // number of events
+  int64_t D;
+  const int64_t* order;    // CSR row -> source event (nullable: identity)
+  const int64_t* offsets;  // padded mode: (B+1) CSR offsets
+  const int64_t* csr_end;  // CSR mode (nullable): number of valid CSR rows (offsets[B])
+  int64_t B, E_max;        // padded mode
+  // output
+  void* out;
+  int64_t out_ld;
+  uint8_t* mask;           // padded mode (B, E_max), nullable
+  int* err;
+};
+
+// MODE_TABLE: gather-add from three tables; MODE_COPY: copy src rows.
+enum { MODE_TABLE = 0, MODE_COPY = 1 };
+
+template <class T, int MODE, bool PADDED, bool VEC>
+__global__ __launch_bounds__(256) void row_writer_kernel(RowArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int64_t rows = PADDED ? a.B * a.E_max : a.E;
+  const int64_t r = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  if (r >= rows) return;
+  int64_t e;
+  if (PADDED) {
+    const int64_t b = r / a.E_max, j = r - b * a.E_max;
+    const int64_t o0 = a.offsets[b], cnt = a.offsets[b + 1] - o0;
+    e = (j < cnt) ? (a.order ? a.order[o0 + j] : o0 + j) : -1;
+    if (a.mask && lane == 0) a.mask[r] = (j < cnt) ? 1 : 0;
+  } else {
+    // rows past offsets[B] exist only when some batch indices were invalid: zero them
+    e = (a.csr_end && r >= *a.csr_end) ? -1 : (a.order ? a.order[r] : r);
+  }
+  if (e >= a.E) e = -1;  // defensive: never follow a corrupt order entry
+  T* out = reinterpret_cast<T*>(a.out) + r * a.out_ld;
+  const T* s0 = nullptr;
+  const T* s1 = nullptr;
+  const T* s2 = nullptr;
+  if (e >= 0) {
+    if (MODE == MODE_TABLE) {
+      const int64_t i0 = a.ids[0][e * a.ids_stride[0]];
+      const int64_t i1 = a.ids[1][e * a.ids_stride[1]];
+      const int64_t i2 = a.ids[2][e * a.ids_stride[2]];
+      if (i0 < 0 || i0 >= a.tab_rows[0] || i1 < 0 || i1 >= a.tab_rows[1] || i2 < 0 || i2 >= a.tab_rows[2]) {
+        if (lane == 0 && a.err) atomicOr(a.err, ERR_TOKEN_INDEX);
+        e = -1;  // never read out of bounds: the row is written as zeros
+      } else {
+        s0 = reinterpret_cast<const T*>(a.tab[0]) + i0 * a.tab_ld[0];
+        s1 = reinterpret_cast<const T*>(a.tab[1]) + i1 * a.tab_ld[1];
+        s2 = reinterpret_cast<const T*>(a.tab[2]) + i2 * a.tab_ld[2];
+      }
+    } else {
+      s0 = reinterpret_cast<const T*>(a.src) + e * a.src_ld;
+    }
+  }
+  if (VEC) {
+    using V = Vec16<T>;
+    constexpr int NV = V::N;
+    for (int64_t d = (int64_t)lane * NV; d < a.D; d += 64 * NV) {
+      V o;
+      if (e < 0) {
+#pragma unroll
+        for (int q = 0; q < NV; ++q) o.v[q] = from_f32<T>(0.0f);
+      } else if (MODE == MODE_TABLE) {
+        const V x = *reinterpret_cast<const V*>(s0 + d);
+        const V y = *reinterpret_cast<const V*>(s1 + d);
+        const V z = *reinterpret_cast<const V*>(s2 + d);
+#pragma unroll
+        for (int q = 0; q < NV; ++q) o.v[q] = add_rn<T>(add_rn<T>(x.v[q], y.v[q]), z.v[q]);
+      } else {
+        o = *reinterpret_cast<const V*>(s0 + d);
+      }
+      *reinterpret_cast<V*>(out + d) = o;
+    }
+  } else {
+    for (int64_t d = lane; d < a.D; d += 64) {
+      T o;
+      if (e < 0) {
+        o = from_f32<T>(0.0f);
+      } else if (MODE == MODE_TABLE) {
+        o = add_rn<T>(add_rn<T>(s0[d], s1[d]), s2[d]);
+      } else {
+        o = s0[d];
+      }
+      out[d] = o;
+    }
+  }
+}
+
+}  // namespace cortex
+
+using namespace cortex;
+
+template <class T, int MODE>
+static int launch_rows(const RowArgs& a, bool padded, hipStream_t stream) {
+  const int64_t rows = padded ? a.B * a.E_max : a.E;
+  if (rows == 0) return OK;
+  const int waves_per_block = 4;
+  if (cdiv(rows, waves_per_block) > 0x7fffffffLL) {
+    set_error("cortex row writer: %lld rows exceed the grid limit", (long long)rows);
+    return E_INVALID;
+  }
+  const dim3 grid((unsigned)cdiv(rows, waves_per_block));
+  constexpr int NV = 16 / sizeof(T);
+  bool vec = (a.D % NV == 0) && ((uintptr_t)a.out % 16 == 0) && ((a.out_ld * (int64_t)sizeof(T)) % 16 == 0);
+  if (MODE == MODE_TABLE) {
+    for (int t = 0; t < 3; ++t)
+      vec = vec && ((uintptr_t)a.tab[t] % 16 == 0) && ((a.tab_ld[t] * (int64_t)sizeof(T)) % 16 == 0);
+  } else {
+    vec = vec && ((uintptr_t)a.src % 16 == 0) && ((a.src_ld * (int64_t)sizeof(T)) % 16 == 0);
+  }
+  if (padded) {
+    if (vec)
+      hipLaunchKernelGGL((row_writer_kernel<T, MODE, true, true>), grid, dim3(256), 0, stream, a);
+    else
+      hipLaunchKernelGGL((row_writer_kernel<T, MODE, true, false>), grid, dim3(256), 0, stream, a);
+  } else {
+    if (vec)
+      hipLaunchKernelGGL((row_writer_kernel<T, MODE, false, true>), grid, dim3(256), 0, stream, a);
+    else
+      hipLaunchKernelGGL((row_writer_kernel<T, MODE, false, false>), grid, dim3(256), 0, stream, a);
+  }
+  CORTEX_CHECK_LAUNCH("cortex row writer");
+  return OK;
+}
+
+template <int MODE>
+static int dispatch_rows(int dtype, const RowArgs& a, bool padded, hipStream_t stream) {
+  switch (dtype) {
+    case DT_F32:
+      return launch_rows<float, MODE>(a, padded, stream);
+    case DT_BF16:
+      return launch_rows<bf16, MODE>(a, padded, stream);
+    case DT_F16:
+      return launch_rows<f16, MODE>(a, padded, stream);
+    default:
+      set_error("unsupported token dtype %d (expected f32, bf16 or f16)", dtype);
+      return E_UNSUPPORTED;
+  }
+}
+
+extern "C" {
+
+int64_t cortex_pack_workspace_bytes(int64_t E, int64_t B) {
+  if (E <= 0 || B <= 0) return 0;
+  const int64_t C = pack_chunk_size(E);
+  const int64_t nchunks = cdiv(E, C);
+  return nchunks * B * (int64_t)sizeof(int);
+}
+
+int cortex_pack_plan(const int64_t* batch_indices, int64_t s_bidx, int64_t E, int64_t B, int64_t* offsets,
+                     int64_t* order, int64_t* dst_rows, int64_t* rank, void* workspace, int64_t workspace_bytes,
+                     int32_t* err_flag, hipStream_t stream) {
+  CORTEX_CHECK_ARG(E >= 0 && B >= 1, "cortex_pack_plan: need E >= 0 and B >= 1 (got E=%lld B=%lld)",
+                   (long long)E, (long long)B);
+  CORTEX_CHECK_ARG(B <= PACK_MAX_B, "cortex_pack_plan: B=%lld exceeds the supported maximum %d", (long long)B,
+                   PACK_MAX_B);
+  CORTEX_CHECK_ARG(offsets != nullptr, "cortex_pack_plan: offsets must not be null");
+  if (E == 0) {
+    hipLaunchKernelGGL(fill_i64_kernel, dim3((unsigned)cdiv(B + 1, 256)), dim3(256), 0, stream, offsets, B + 1,
+                       (int64_t)0);
+    CORTEX_CHECK_LAUNCH("cortex_pack_plan(E=0)");
+    return OK;
+  }
+  CORTEX_CHECK_ARG(batch_indices && order, "cortex_pack_plan: batch_indices and order must not be null");
+  const int64_t need = cortex_pack_workspace_bytes(E, B);
+  if (workspace_bytes < need || (need > 0 && workspace == nullptr)) {
+    set_error("cortex_pack_plan: workspace of %lld bytes is smaller than the required %lld",
+              (long long)workspace_bytes, (long long)need);
+    return E_WORKSPACE;
+  }
+  const int64_t C = pack_chunk_size(E);
+  const int nchunks = (int)cdiv(E, C);
+  int* counts = reinterpret_cast<int*>(workspace);
+  hipLaunchKernelGGL(pack_count_kernel, dim3(nchunks), dim3(256), 0, stream, batch_indices, s_bidx, E, (int)B, C,
+                     counts, err_flag);
+  CORTEX_CHECK_LAUNCH("pack_count_kernel");
+  hipLaunchKernelGGL(pack_scan_kernel, dim3(1), dim3(1024), 0, stream, counts, nchunks, (int)B, offsets);
+  CORTEX_CHECK_LAUNCH("pack_scan_kernel");
+  hipLaunchKernelGGL(pack_rank_kernel, dim3(nchunks), dim3(64), 0, stream, batch_indices, s_bidx, E, (int)B, C,
+                     counts, offsets, order, dst_rows, rank);
+  CORTEX_CHECK_LAUNCH("pack_rank_kernel");
+  return OK;
+}
+
+int cortex_tokenize(int dtype, int64_t D, const void* neuron_emb, int64_t n_neuron, int64_t ld_neuron,
+                    const void* time_emb, int64_t n_time, int64_t ld_time, const void* value_emb, int64_t n_value,
+                    int64_t ld_value, const int64_t* neuron_ids, int64_t s_nid, const int64_t* time_bins,
+                    int64_t s_tb, const int64_t* values, int64_t s_val, int64_t E, const int64_t* order,
+                    const int64_t* csr_end, const int64_t* offsets, int64_t B, int64_t E_max, void* out,
+                    int64_t ld_out, uint8_t* mask, int32_t* err_flag, hipStream_t stream) {
+  CORTEX_CHECK_ARG(D > 0 && E >= 0, "cortex_tokenize: need D > 0 and E >= 0");
+  CORTEX_CHECK_ARG(neuron_emb && time_emb && value_emb, "cortex_tokenize: null embedding table");
+  CORTEX_CHECK_ARG(E == 0 || (neuron_ids && time_bins && values), "cortex_tokenize: null index array");
+  CORTEX_CHECK_ARG(out != nullptr || (offsets ? B * E_max == 0 : E == 0), "cortex_tokenize: null output");
+  CORTEX_CHECK_ARG(ld_out >= D && ld_neuron >= D && ld_time >= D && ld_value >= D,
+                   "cortex_tokenize: row strides must be >= D");
+  RowArgs a = {};
+  a.tab[0] = neuron_emb;
+  a.tab[1] = time_emb;
+  a.tab[2] = value_emb;
+  a.tab_rows[0] = n_neuron;
+  a.tab_rows[1] = n_time;
+  a.tab_rows[2] = n_value;
+  a.tab_ld[0] = ld_neuron;
+  a.tab_ld[1] = ld_time;
+  a.tab_ld[2] = ld_value;
+  a.ids[0] = neuron_ids;
+  a.ids[1] = time_bins;
+  a.ids[2] = values;
+  a.ids_stride[0] = s_nid;
+  a.ids_stride[1] = s_tb;
+  a.ids_stride[2] = s_val;
+  a.E = E;
+  a.D = D;
+  a.order = order;
+  a.csr_end = csr_end;
+  a.offsets = offsets;
+  a.B = B;
+  a.E_max = E_max;
+  a.out = out;
+  a.out_ld = ld_out;
+  a.mask = mask;
+  a.err = err_flag;
+  const bool padded = offsets != nullptr;
+  if (padded) CORTEX_CHECK_ARG(B >= 1 && E_max >= 0, "cortex_tokenize: padded output needs B >= 1, E_max >= 0");
+  return dispatch_rows<MODE_TABLE>(dtype, a, padded, stream);
+}
+
+int cortex_pack_rows(int dtype, int64_t D, const void* src, int64_t ld_src, int64_t E, const int64_t* order,
+                     const int64_t* csr_end, const int64_t* offsets, int64_t B, int64_t E_max, void* out,
+                     int64_t ld_out, uint8_t* mask, hipStream_t stream) {
+  CORTEX_CHECK_ARG(D > 0 && E >= 0, "cortex_pack_rows: need D > 0 and E >= 0");
+  CORTEX_CHECK_ARG(E == 0 || src, "cortex_pack_rows: null source rows");
+  CORTEX_CHECK_ARG(ld_out >= D && ld_src >= D, "cortex_pack_rows: row strides must be >= D");
+  RowArgs a = {};
+  a.src = src;
+  a.src_ld = ld_src;
+  a.E = E;
+  a.D = D;
+  a.order = order;
+  a.csr_end = csr_end;
+  a.offsets = offsets;
+  a.B = B;
+  a.E_max = E_max;
+  a.out = out;
+  a.out_ld = ld_out;
+  a.mask = mask;
+  const bool padded = offsets != nullptr;
+  return dispatch_rows<MODE_COPY>(dtype, a, padded, stream);
+}
+
+}  // extern "C"

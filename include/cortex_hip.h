@@ -1,0 +1,151 @@
+/*
+ * cortex_hip.h -- C ABI of libcortex_hip.so, the gfx950 (MI355X) kernels of the
+ * Cortex-S inference forward.
+ *
+ * Conventions
+ *   - Every entry point returns 0 on success or a negative status
+ *     (-1 invalid argument, -2 unsupported combination, -3 launch error,
+ *     -4 workspace too small); cortex_last_error() describes the last failure on
+ *     the calling thread.  Nothing throws across the ABI.
+ *   - All pointers are device pointers owned by the caller; the library keeps no
+ *     pointer after returning.  Work is enqueued on `stream` (the caller's current
+ *     stream) and the library never synchronises the host.
+ *   - Shapes and strides are int64 element counts.  dtype codes:
+ *     0 f32, 1 bf16, 2 f16, 3 int8, 4 int32, 5 int64, 6 uint8.
+ *   - Index-range violations never read or write out of bounds: the offending row
+ *     is written as zeros and a bit is OR-ed into the caller's device `err_flag`
+ *     (1: token index outside its table, 2: batch index outside [0, B)).
+ *
+ * Reference interfaces (upstream repository, file:line) are cited per entry point.
+ */
+#ifndef CORTEX_HIP_H_
+#define CORTEX_HIP_H_
+
+#include <stdint.h>
+
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Library version (1) and the last error message of the calling thread. */
+int cortex_version(void);
+const char* cortex_last_error(void);
+
+/* ---- a2: stable pack of ragged events ------------------------------------
+ * Replaces the bincount / stable argsort / exclusive cumsum of
+ * _pack_events (cortex/models/cortex.py:140-160), without its two host syncs
+ * (cortex.py:140,142): B is supplied by the caller.
+ *   offsets  (B+1)  CSR offsets: sample b owns rows [offsets[b], offsets[b+1])
+ *   order    (E)    source event of every CSR row (stable in event order)
+ *   dst_rows (E)    CSR row of every event (nullable)
+ *   rank     (E)    position of every event inside its sample (nullable)
+ * workspace: at least cortex_pack_workspace_bytes(E, B) bytes of device memory. */
+int64_t cortex_pack_workspace_bytes(int64_t E, int64_t B);
+int cortex_pack_plan(const int64_t* batch_indices, int64_t s_bidx, int64_t E, int64_t B, int64_t* offsets,
+                     int64_t* order, int64_t* dst_rows, int64_t* rank, void* workspace, int64_t workspace_bytes,
+                     int32_t* err_flag, hipStream_t stream);
+
+/* ---- a1 (+a2): fused spike tokenizer --------------------------------------
+ * Replaces fused_tokenizer (cortex/kernels/tokenizer.py:177-249) and the eager
+ * embedding sum of SpikeTokenizer.forward (cortex/models/tokenizer.py:90-93):
+ *   out[r, :] = (neuron_emb[nid[e]] + time_emb[tb[e]]) + value_emb[val[e]]
+ * evaluated left to right in the table dtype (f32 / bf16 / f16), where e is
+ *   - r                        (order == NULL, offsets == NULL),
+ *   - order[r]                 (CSR pack: order from cortex_pack_plan; rows
+ *                              r >= *csr_end, if csr_end != NULL, are zero -- pass
+ *                              &offsets[B] so that events dropped for an invalid
+ *                              batch index never leave an unwritten order entry), or
+ *   - order[offsets[b] + j]    for padded row r = b*E_max + j when offsets != NULL;
+ *     rows j >= count_b are zero and mask[r] = (j < count_b), as the padded
+ *     output of _pack_events (cortex/models/cortex.py:146-147,163-164). */
+int cortex_tokenize(int dtype, int64_t D, const void* neuron_emb, int64_t n_neuron, int64_t ld_neuron,
+                    const void* time_emb, int64_t n_time, int64_t ld_time, const void* value_emb, int64_t n_value,
+                    int64_t ld_value, const int64_t* neuron_ids, int64_t s_nid, const int64_t* time_bins,
+                    int64_t s_tb, const int64_t* values, int64_t s_val, int64_t E, const int64_t* order,
+                    const int64_t* csr_end, const int64_t* offsets, int64_t B, int64_t E_max, void* out,
+                    int64_t ld_out, uint8_t* mask, int32_t* err_flag, hipStream_t stream);
+
+/* ---- a2: pack existing token rows ------------------------------------------
+ * Replaces the gather/scatter of _pack_events (cortex/models/cortex.py:150-164)
+ * for already-tokenized (E, D) rows; same row mapping as cortex_tokenize. */
+int cortex_pack_rows(int dtype, int64_t D, const void* src, int64_t ld_src, int64_t E, const int64_t* order,
+                     const int64_t* csr_end, const int64_t* offsets, int64_t B, int64_t E_max, void* out,
+                     int64_t ld_out, uint8_t* mask, hipStream_t stream);
+
+/* ---- a7: INT8 per-channel weight quantisation ------------------------------
+ * Replaces the weight scale of derive_scales (cortex/quantization/calibrate.py:154)
+ * and the quantise step of QuantizedLinear.from_linear (calibrate.py:216-220):
+ *   scale[n] = max(max_k |w[n,k]|, 1e-8) / 127   (written to scale_out)
+ *   q[n,k]   = clamp(rint(w[n,k] / scale[n]), -127, 127)
+ * When scale_in is not NULL it is used instead of the computed scale; when q is
+ * NULL only the scales are computed (derive_scales). */
+int cortex_quantize_int8(const float* w, int64_t N, int64_t K, int64_t ld_w, const float* scale_in,
+                         float* scale_out, int8_t* q, int64_t ld_q, hipStream_t stream);
+
+/* ---- a5/a6: per-row norm statistics ----------------------------------------
+ * norm 1 (LayerNorm, cortex/models/perceiver.py:51-52): stats[2m] = mean,
+ * stats[2m+1] = 1/sqrt(var + eps); norm 2 (RMSNorm,
+ * cortex/kernels/fused_rmsnorm.py:102): stats[2m] = 0, stats[2m+1] = sqrt(mean(x^2) + eps). */
+int cortex_row_stats(int64_t M, int64_t K, int x_dtype, const void* x, int64_t ld_x, int norm, float eps,
+                     float* stats, hipStream_t stream);
+
+/* ---- a8: LayerNorm written out ---------------------------------------------
+ * Replaces nn.LayerNorm where its output is consumed by something other than a
+ * linear, e.g. the encoder's final_norm feeding the behaviour head's own norm
+ * (cortex/models/perceiver.py:158, cortex/models/cortex.py:37):
+ *   out[m,k] = (x[m,k] - mean_m) * rstd_m * gamma[k] + beta[k]  (gamma/beta nullable). */
+int cortex_layer_norm(int64_t M, int64_t K, int x_dtype, const void* x, int64_t ld_x, const void* gamma,
+                      const void* beta, int gamma_dtype, float eps, int out_dtype, void* out, int64_t ld_out,
+                      hipStream_t stream);
+
+/* ---- a5/a6/a7: fused norm + linear -----------------------------------------
+ * Replaces rms_norm_linear (cortex/kernels/fused_rmsnorm.py:239-301),
+ * QuantizedLinear.forward (cortex/quantization/calibrate.py:225-228) and the
+ * LayerNorm -> Linear (-> GELU) (+ residual) chains of SelfAttentionBlock /
+ * CrossAttentionBlock / BehaviorDecoder (cortex/models/perceiver.py:67-68,113-125;
+ * cortex/models/cortex.py:37-53):
+ *   a[m,k]   = x[m,k]                                  (norm 0)
+ *            = (x[m,k]-mean_m)*rstd_m*gamma[k]+beta[k]   (norm 1, stats from cortex_row_stats)
+ *            = (x[m,k]/rms_m)*gamma[k]                    (norm 2)
+ *   a is rounded to the compute dtype (1 bf16 / 0 f32);
+ *   acc[m,n] = sum_k a[m,k] * W[n,k]   (fp32 accumulation on MFMA)
+ *   y[m,n]   = act(acc*w_scale[n] + bias[n]) + residual[(m % res_rows), n]
+ * W: int8 (N,K) (w_layout 0) with w_scale, or bf16/f32 in (N,K) (layout 0) or
+ * (K,N) (layout 1, the rms_norm_linear weight).  act: 0 none, 1 erf-GELU.
+ * res_rows 0 means M (ordinary residual); a smaller value broadcasts a
+ * batch-invariant residual such as the learned latents. */
+int cortex_norm_linear(int64_t M, int64_t N, int64_t K, int x_dtype, const void* x, int64_t ld_x, int norm,
+                       const float* stats, const void* gamma, const void* beta, int gamma_dtype, int compute,
+                       int w_dtype, int w_layout, const void* w, int64_t ld_w, const float* w_scale,
+                       int bias_dtype, const void* bias, int act, int res_dtype, const void* residual,
+                       int64_t ld_res, int64_t res_rows, int out_dtype, void* out, int64_t ld_out,
+                       hipStream_t stream);
+
+/* ---- a3/a4/a5/a8: attention ------------------------------------------------
+ * Replaces sparse_cross_attention (cortex/kernels/sparse_xattn.py:340-434) and
+ * the scaled_dot_product_attention calls of CrossAttentionBlock
+ * (cortex/models/perceiver.py:75-80), SelfAttentionBlock (perceiver.py:121) and
+ * BehaviorDecoder (cortex/models/cortex.py:49):
+ *   out[b,h,i,:] = softmax_j(scale * q[b,h,i,:].k[b,h,j,:] | allowed) v[b,h,j,:]
+ * Element (b,h,i,j) = base + b*s_b + h*s_h + i*s_l + d (q batch stride may be 0).
+ * With kv_offsets (B+1), sample b's keys are CSR rows [kv_offsets[b], kv_offsets[b+1])
+ * (row r at base + r*s_l + h*s_h); otherwise Lk keys per sample.
+ * Key j is allowed iff j < length (kv_lengths[b] when given), key_mask[b*km_sb + j]
+ * != 0 (when given) and block_mask[b*bm_sb + (i/block_l)*n_kt + j/block_e] != 0
+ * (when given; bm_sb 0 shares one tile mask across the batch).  Rows with no
+ * allowed key are written as 0.  dtype: 1 bf16 or 0 f32; Dh <= 128. */
+int cortex_attention(int dtype, int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64_t Dh, const void* q,
+                     int64_t q_sb, int64_t q_sh, int64_t q_sl, const void* k, int64_t k_sb, int64_t k_sh,
+                     int64_t k_sl, const void* v, int64_t v_sb, int64_t v_sh, int64_t v_sl,
+                     const int64_t* kv_offsets, const int64_t* kv_lengths, const uint8_t* key_mask, int64_t km_sb,
+                     const uint8_t* block_mask, int64_t bm_sb, int64_t n_qt, int64_t n_kt, int64_t block_l,
+                     int64_t block_e, float scale, void* out, int64_t o_sb, int64_t o_sh, int64_t o_sl,
+                     hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CORTEX_HIP_H_ */

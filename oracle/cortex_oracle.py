@@ -1,0 +1,434 @@
+"""CPU oracle for the Cortex-S inference forward.
+
+TEST INFRASTRUCTURE ONLY.  Only ``tests/``, ``__graft_entry__.smoke()`` and the
+``cpu_baseline`` leg of ``bench.py`` may import this module, and only as the
+checker or the timed CPU baseline -- never as the thing measured or shipped.  The
+product package (``cortex-engine_amd/cortex``) never imports it.
+
+It restates the reference algorithm from the reference sources (cited per
+function as file:line under the upstream repository root):
+
+* integer / byte work (event packing, INT8 weight quantisation, the tokenizer
+  gather-add, the temporal tile mask) in numpy with explicit fp32 arithmetic;
+* floating-point layers (LayerNorm, GELU, SDPA, Linear) with the same PyTorch CPU
+  library routines the reference calls, in fp32.
+
+How each function is pinned (checked by tests/test_oracle.py):
+
+==========================  ==================================================
+function                    pinned by
+==========================  ==================================================
+tokenize                    pure-Python brute force on tiny inputs; reference
+                            known answers (single event, identical indices);
+                            model goldens
+pack_events                 pure-Python stable bucket on tiny inputs; invariants
+                            (row multiset, stability, mask count); model goldens
+                            with shuffled batch indices
+quantize_int8               error bound |w - q*s| <= s/2, constructed half-way
+                            ties (round-half-even), all-zero row, +-127 at the
+                            row max; int8 checksums from the reference's own
+                            convert_model on the seeded CORTEX_XS / CORTEX_S
+attention / masked SDPA     float64 brute-force softmax; all-true tile mask
+                            equals SDPA (reference test); l=0 rows
+temporal_block_mask         reference known answers (full window -> all True,
+                            window 0 with events at t=0 -> some False); brute
+                            force per-element definition (superset property)
+rms_norm_linear             torch.nn.functional.rms_norm + matmul (library
+                            routine); gamma=1 and large-x known answers
+forward / forward_int8      behavior goldens written by importing the reference
+                            (seeded CORTEX_XS and CORTEX_S, fp32 and INT8)
+==========================  ==================================================
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+
+import numpy as np
+import torch
+import torch.nn.functional as F
+
+# --------------------------------------------------------------------------- #
+# a1 tokenizer                                                                 #
+# --------------------------------------------------------------------------- #
+
+
+def tokenize(neuron_emb, time_emb, value_emb, neuron_ids, time_bins, values) -> np.ndarray:
+    """``(N[nid] + T[tb]) + V[val]`` evaluated left to right in the table dtype.
+
+    Follows reference cortex/kernels/tokenizer.py:68-81 (``fused_tokenizer_reference``)
+    and cortex/models/tokenizer.py:90-93 (eager ``emb(n) + emb(t) + emb(v)``).
+    Out-of-range indices raise ``IndexError`` like the reference's eager gather.
+    """
+    n = np.asarray(neuron_emb)
+    t = np.asarray(time_emb)
+    v = np.asarray(value_emb)
+    nid = np.asarray(neuron_ids, dtype=np.int64)
+    tb = np.asarray(time_bins, dtype=np.int64)
+    val = np.asarray(values, dtype=np.int64)
+    if not (nid.shape == tb.shape == val.shape):
+        raise ValueError("index arrays must have identical shapes")
+    for idx, tab in ((nid, n), (tb, t), (val, v)):
+        if idx.size and (idx.min() < 0 or idx.max() >= tab.shape[0]):
+            raise IndexError("index out of range")
+    acc = n[nid] + t[tb]  # first add in the table dtype
+    return acc + v[val]
+
+
+# --------------------------------------------------------------------------- #
+# a2 pack                                                                      #
+# --------------------------------------------------------------------------- #
+
+
+@dataclass
+class Packed:
+    padded: np.ndarray  # (B, E_max, D), zeros where mask is False
+    mask: np.ndarray  # (B, E_max) bool
+    csr: np.ndarray  # (E, D) rows in stable batch order
+    offsets: np.ndarray  # (B+1,) int64
+    order: np.ndarray  # (E,) source event index of each CSR row
+    rank: np.ndarray  # (E,) position of each source event inside its sample
+
+
+def pack_events(flat_tokens, batch_indices, batch_size: int | None = None) -> Packed:
+    """Stable bucket of flat tokens by batch index.
+
+    Follows reference cortex/models/cortex.py:125-165 (``_pack_events``):
+    ``B = max(bidx)+1`` (1 when empty), ``counts = bincount``, stable argsort,
+    ``pos = i - exclusive_cumsum(counts)[b]``, scatter into zeros + bool mask.  The
+    CSR view (``sorted_tokens`` and the cumulative counts, :149-160) is returned too.
+    ``batch_size`` may force a larger B (trailing empty samples), as a serving
+    caller that knows its batch would.
+    """
+    x = np.asarray(flat_tokens)
+    b = np.asarray(batch_indices, dtype=np.int64)
+    E = b.shape[0]
+    if E and b.min() < 0:
+        raise IndexError("negative batch index")
+    B = int(b.max()) + 1 if E > 0 else 1
+    if batch_size is not None:
+        if batch_size < B:
+            raise ValueError("batch_size smaller than max(batch_indices)+1")
+        B = batch_size
+    counts = np.bincount(b, minlength=B).astype(np.int64)
+    e_max = int(counts.max()) if counts.size else 0
+    order = np.argsort(b, kind="stable")
+    sorted_b = b[order]
+    offsets = np.zeros(B + 1, dtype=np.int64)
+    offsets[1:] = np.cumsum(counts)
+    pos = np.arange(E, dtype=np.int64) - offsets[sorted_b]
+    D = x.shape[-1]
+    padded = np.zeros((B, e_max, D), dtype=x.dtype)
+    mask = np.zeros((B, e_max), dtype=bool)
+    csr = x[order]
+    padded[sorted_b, pos] = csr
+    mask[sorted_b, pos] = True
+    rank = np.empty(E, dtype=np.int64)
+    rank[order] = pos
+    return Packed(padded, mask, csr, offsets, order, rank)
+
+
+# --------------------------------------------------------------------------- #
+# a7 INT8 per-channel weight quantisation                                      #
+# --------------------------------------------------------------------------- #
+
+
+def weight_scale(w) -> np.ndarray:
+    """``max(max_k |W[n,k]|, 1e-8) / 127`` in fp32.
+
+    Follows reference cortex/quantization/calibrate.py:154 (``derive_scales``):
+    ``w.abs().amax(dim=1).clamp(min=1e-8) / 127.0`` on the fp32 weight.
+    """
+    w32 = np.asarray(w, dtype=np.float32)
+    amax = np.abs(w32).max(axis=1) if w32.shape[1] else np.zeros(w32.shape[0], np.float32)
+    amax = np.maximum(amax, np.float32(1e-8)).astype(np.float32)
+    return (amax / np.float32(127.0)).astype(np.float32)
+
+
+def quantize_int8(w, scale=None) -> tuple[np.ndarray, np.ndarray]:
+    """``q = clamp(round_half_even(W / scale[:,None]), -127, 127)`` as int8.
+
+    Follows reference cortex/quantization/calibrate.py:216-220
+    (``QuantizedLinear.from_linear``): IEEE fp32 division by the per-row scale,
+    ``Tensor.round`` (half to even), clamp, cast.
+    """
+    w32 = np.asarray(w, dtype=np.float32)
+    s = weight_scale(w32) if scale is None else np.asarray(scale, dtype=np.float32)
+    scaled = (w32 / s[:, None]).astype(np.float32)
+    q = np.clip(np.rint(scaled), -127, 127).astype(np.int8)
+    return q, s
+
+
+def dequantize(q, scale) -> np.ndarray:
+    """``q.float() * scale[:, None]`` (reference calibrate.py:227)."""
+    return (np.asarray(q).astype(np.float32) * np.asarray(scale, np.float32)[:, None]).astype(
+        np.float32
+    )
+
+
+# --------------------------------------------------------------------------- #
+# a4 attention                                                                 #
+# --------------------------------------------------------------------------- #
+
+
+def attention_bruteforce_f64(q, k, v, allowed=None, scale=None, empty_rows="zero"):
+    """float64 softmax(q k^T * scale + mask) v, row by row.
+
+    ``allowed`` broadcasts to (B, H, Lq, Lk) bool.  Rows with no allowed key give 0
+    (``empty_rows="zero"``, the l=0 guard of reference sparse_xattn.py:325-328) or
+    NaN (``"nan"``, what softmax over all -inf gives in
+    sparse_cross_attention_reference, sparse_xattn.py:143-146).
+    """
+    q = np.asarray(q, dtype=np.float64)
+    k = np.asarray(k, dtype=np.float64)
+    v = np.asarray(v, dtype=np.float64)
+    s = q.shape[-1] ** -0.5 if scale is None else scale
+    scores = np.einsum("bhld,bhed->bhle", q, k) * s
+    if allowed is not None:
+        allowed = np.broadcast_to(np.asarray(allowed, dtype=bool), scores.shape)
+        scores = np.where(allowed, scores, -np.inf)
+    m = scores.max(axis=-1, keepdims=True)
+    empty = ~np.isfinite(m)
+    m = np.where(empty, 0.0, m)
+    p = np.exp(scores - m)
+    denom = p.sum(axis=-1, keepdims=True)
+    with np.errstate(invalid="ignore", divide="ignore"):
+        out = np.einsum("bhle,bhed->bhld", p / denom, v)
+    fill = 0.0 if empty_rows == "zero" else np.nan
+    return np.where(empty, fill, out)
+
+
+def expand_block_mask(block_mask, L: int, E: int, BLOCK_L: int, BLOCK_E: int) -> np.ndarray:
+    """Tile mask (n_q, n_k) or (B, n_q, n_k) -> element mask (..., L, E).
+
+    Follows reference sparse_xattn.py:116-131 (tile (qi,kj) covers rows
+    [qi*BLOCK_L, ...) and columns [kj*BLOCK_E, ...)).
+    """
+    bm = np.asarray(block_mask, dtype=bool)
+    li = np.arange(L) // BLOCK_L
+    ei = np.arange(E) // BLOCK_E
+    return bm[..., li[:, None], ei[None, :]]
+
+
+def sparse_cross_attention(q, k, v, block_mask=None, BLOCK_L=64, BLOCK_E=64, scale=None,
+                           kv_lengths=None, empty_rows="zero"):
+    """Masked attention as the sparse kernel defines it.
+
+    Element (l, e) of sample b is attended iff ``e < kv_lengths[b]`` (when given)
+    and the tile mask holds for ``(l // BLOCK_L, e // BLOCK_E)`` (when given).
+    Follows reference sparse_xattn.py:96-146 and, for per-sample lengths, the
+    key-padding mask of perceiver.py:75-80.
+    """
+    q = np.asarray(q)
+    B, H, L, _ = q.shape
+    E = np.asarray(k).shape[2]
+    allowed = np.ones((B, 1, L, E), dtype=bool)
+    if block_mask is not None:
+        em = expand_block_mask(block_mask, L, E, BLOCK_L, BLOCK_E)
+        if em.ndim == 2:
+            em = em[None]
+        allowed &= em[:, None]
+    if kv_lengths is not None:
+        lens = np.asarray(kv_lengths)
+        allowed &= (np.arange(E)[None, :] < lens[:, None])[:, None, None, :]
+    return attention_bruteforce_f64(q, k, v, allowed, scale, empty_rows)
+
+
+def temporal_block_mask(event_times, n_latents: int, max_time_bins: int, window_bins: int = 30,
+                        BLOCK_L: int = 64, BLOCK_E: int = 64) -> np.ndarray:
+    """Conservative tile mask from latent time centres.
+
+    Follows reference sparse_xattn.py:152-200: latent i has centre
+    ``float32(i) / L * T`` (fp32, left to right), a latent tile spans
+    ``[int(min centre) - w, int(max centre) + w]`` (``int`` truncates), an event
+    tile spans [min t, max t] of its events; the tile pair is kept iff the
+    intervals overlap.
+    """
+    t = np.asarray(event_times, dtype=np.int64)
+    E = t.shape[0]
+    n_q = math.ceil(n_latents / BLOCK_L)
+    n_k = math.ceil(E / BLOCK_E)
+    out = np.zeros((n_q, n_k), dtype=bool)
+    tmin = [int(t[j * BLOCK_E:(j + 1) * BLOCK_E].min()) for j in range(n_k)]
+    tmax = [int(t[j * BLOCK_E:(j + 1) * BLOCK_E].max()) for j in range(n_k)]
+    for qi in range(n_q):
+        idx = np.arange(qi * BLOCK_L, min((qi + 1) * BLOCK_L, n_latents), dtype=np.float32)
+        centres = (idx / np.float32(n_latents)).astype(np.float32) * np.float32(max_time_bins)
+        lo = int(centres.min()) - window_bins
+        hi = int(centres.max()) + window_bins
+        for kj in range(n_k):
+            out[qi, kj] = (tmin[kj] <= hi) and (tmax[kj] >= lo)
+    return out
+
+
+# --------------------------------------------------------------------------- #
+# a6 RMSNorm + linear                                                          #
+# --------------------------------------------------------------------------- #
+
+
+def rms_norm_linear(x: torch.Tensor, gamma: torch.Tensor, w: torch.Tensor, bias=None,
+                    eps: float = 1e-6) -> torch.Tensor:
+    """``((x_f32 / sqrt(mean(x^2)+eps)) * gamma).to(x.dtype) @ w (+ bias)``.
+
+    Follows reference cortex/kernels/fused_rmsnorm.py:86-108; ``w`` is (K, N).
+    The matmul runs in fp32 on the CPU (the product compares bf16 kernels against
+    this with a stated tolerance).
+    """
+    xf = x.float()
+    rms = torch.sqrt(xf.pow(2).mean(dim=-1, keepdim=True) + eps)
+    xn = ((xf / rms) * gamma.float()).to(x.dtype)
+    out = xn.float() @ w.float()
+    if bias is not None:
+        out = out + bias.float()
+    return out
+
+
+# --------------------------------------------------------------------------- #
+# a3/a5/a8/a9 full forward                                                     #
+# --------------------------------------------------------------------------- #
+
+
+@dataclass
+class ModelShape:
+    hidden_dim: int
+    num_layers: int
+    num_heads: int
+    num_latents: int
+    latent_dim: int
+    cross_attn_heads: int
+    behavior_dim: int = 2
+    spike_value_buckets: int = 8
+
+
+CORTEX_XS_SHAPE = ModelShape(256, 5, 4, 128, 256, 4)
+CORTEX_S_SHAPE = ModelShape(512, 7, 8, 256, 512, 8)
+
+
+def _linear(sd: dict, name: str, x: torch.Tensor) -> torch.Tensor:
+    """``nn.Linear`` (no bias) or the reference's QuantizedLinear dequant forward
+    (calibrate.py:225-228: ``F.linear(x, (q.float()*scale[:,None]).to(x.dtype))``)."""
+    if f"{name}.weight_int8" in sd:
+        q = sd[f"{name}.weight_int8"]
+        s = sd[f"{name}.weight_scale"]
+        w = (q.float() * s[:, None]).to(x.dtype)
+    else:
+        w = sd[f"{name}.weight"]
+    b = sd.get(f"{name}.bias")
+    return F.linear(x, w, b)
+
+
+def _ln(sd: dict, name: str, x: torch.Tensor) -> torch.Tensor:
+    """``nn.LayerNorm`` with affine weight and bias, eps 1e-5 (perceiver.py:51-52)."""
+    w = sd[f"{name}.weight"]
+    return F.layer_norm(x, (w.shape[0],), w, sd[f"{name}.bias"], 1e-5)
+
+
+def _heads(x: torch.Tensor, h: int) -> torch.Tensor:
+    """``rearrange('b l (h d) -> b h l d')``."""
+    b, l, d = x.shape
+    return x.reshape(b, l, h, d // h).permute(0, 2, 1, 3)
+
+
+def _merge(x: torch.Tensor) -> torch.Tensor:
+    """``rearrange('b h l d -> b l (h d)')``."""
+    b, h, l, d = x.shape
+    return x.permute(0, 2, 1, 3).reshape(b, l, h * d)
+
+
+def encode(sd: dict, shape: ModelShape, tokens: torch.Tensor, mask: torch.Tensor) -> torch.Tensor:
+    """PerceiverEncoder.forward (reference perceiver.py:145-158) with the
+    cross-attention block (:54-82) and self-attention blocks (:107-126)."""
+    B = tokens.shape[0]
+    lat = sd["encoder.latents"].unsqueeze(0).expand(B, -1, -1)
+    p = "encoder.cross_attn"
+    q = _linear(sd, f"{p}.q_proj", _ln(sd, f"{p}.norm_q", lat))
+    kv = _linear(sd, f"{p}.kv_proj", _ln(sd, f"{p}.norm_kv", tokens))
+    k, v = kv.chunk(2, dim=-1)
+    h = shape.cross_attn_heads
+    o = F.scaled_dot_product_attention(_heads(q, h), _heads(k, h), _heads(v, h),
+                                       attn_mask=mask[:, None, None, :])
+    x = lat + _linear(sd, f"{p}.out_proj", _merge(o))
+    for i in range(shape.num_layers):
+        p = f"encoder.self_attn_blocks.{i}"
+        qkv = _linear(sd, f"{p}.qkv_proj", _ln(sd, f"{p}.norm_attn", x))
+        q, k, v = qkv.chunk(3, dim=-1)
+        h = shape.num_heads
+        o = F.scaled_dot_product_attention(_heads(q, h), _heads(k, h), _heads(v, h))
+        x = x + _linear(sd, f"{p}.out_proj", _merge(o))
+        hmid = F.gelu(_linear(sd, f"{p}.mlp.0", _ln(sd, f"{p}.norm_mlp", x)))
+        x = x + _linear(sd, f"{p}.mlp.2", hmid)
+    return _ln(sd, "encoder.final_norm", x)
+
+
+def behavior_head(sd: dict, shape: ModelShape, latents: torch.Tensor) -> torch.Tensor:
+    """BehaviorDecoder.forward (reference cortex/models/cortex.py:29-53)."""
+    p = "behavior_head"
+    lat = _ln(sd, f"{p}.norm", latents)
+    B = lat.shape[0]
+    query = sd[f"{p}.query"].unsqueeze(0).expand(B, -1, -1)
+    q = _linear(sd, f"{p}.q_proj", query)
+    kv = _linear(sd, f"{p}.kv_proj", lat)
+    k, v = kv.chunk(2, dim=-1)
+    h = shape.num_heads
+    o = F.scaled_dot_product_attention(_heads(q, h), _heads(k, h), _heads(v, h))
+    return _linear(sd, f"{p}.out_proj", _merge(o)).squeeze(-1)
+
+
+def forward(sd: dict, shape: ModelShape, neuron_ids, time_bins, values, batch_indices,
+            batch_size: int | None = None) -> torch.Tensor:
+    """CortexModel.forward (reference cortex/models/cortex.py:90-122) in fp32 on the CPU.
+
+    ``sd`` is a CPU state_dict of a float model or of a model after the reference's
+    ``convert_model`` (int8 ``weight_int8`` + fp32 ``weight_scale`` buffers).
+    Returns ``behavior`` (B, behavior_dim).
+    """
+    sd = {k: v.detach().cpu() for k, v in sd.items()}
+    nid = np.asarray(neuron_ids, dtype=np.int64)
+    tb = np.asarray(time_bins, dtype=np.int64)
+    val = np.asarray(values, dtype=np.int64)
+    tok = tokenize(sd["tokenizer.neuron_emb.weight"].numpy(), sd["tokenizer.time_emb.weight"].numpy(),
+                   sd["tokenizer.value_emb.weight"].numpy(), nid, tb, val)
+    packed = pack_events(tok, batch_indices, batch_size)
+    tokens = torch.from_numpy(packed.padded)
+    mask = torch.from_numpy(packed.mask)
+    with torch.no_grad():
+        lat = encode(sd, shape, tokens, mask)
+        return behavior_head(sd, shape, lat)
+
+
+def quantize_state_dict(sd: dict, skip_prefixes=("masked_spike_head.",)) -> dict:
+    """Replace every 2-D ``*.weight`` of a Linear by ``weight_int8`` + ``weight_scale``.
+
+    Mirrors what reference convert_model does on CortexModel (calibrate.py:240-279):
+    every nn.Linear that saw calibration data -- all of them except
+    ``masked_spike_head.proj`` (results.md:18) -- is converted.  Embeddings,
+    LayerNorms and the latent/query parameters stay float.
+    """
+    out = {}
+    for k, v in sd.items():
+        mod = k.rsplit(".", 1)[0]
+        is_linear = (k.endswith(".weight") and v.dim() == 2 and "emb" not in k
+                     and not k.startswith(skip_prefixes))
+        if is_linear:
+            q, s = quantize_int8(v.detach().cpu().float().numpy())
+            out[f"{mod}.weight_int8"] = torch.from_numpy(q)
+            out[f"{mod}.weight_scale"] = torch.from_numpy(s)
+        else:
+            out[k] = v
+    return out
+
+
+def flops_per_sample(shape: ModelShape, events: int, behavior_queries: int = 2) -> float:
+    """Algorithmic FLOPs of one sample's forward (multiply-add = 2 FLOPs).
+
+    Cross block: q proj (batch-invariant, counted once per sample as written by
+    the reference), kv proj over the sample's events, attention, out proj; seven
+    self blocks (qkv 3LD^2, out LD^2, mlp 8LD^2 -> 24LD^2 FLOPs, attention 4L^2D);
+    behaviour head (kv proj 4LD^2, q 2QD^2, attention 4QLD, out 2QD).
+    """
+    L, D, E, Q = shape.num_latents, shape.latent_dim, events, behavior_queries
+    cross = 2 * L * D * D + 4 * E * D * D + 4 * L * E * D + 2 * L * D * D
+    selfb = shape.num_layers * (24 * L * D * D + 4 * L * L * D)
+    head = 4 * L * D * D + 2 * Q * D * D + 4 * Q * L * D + 2 * Q * D
+    return float(cross + selfb + head)

@@ -1,0 +1,86 @@
+"""The C-ABI library loads and exports exactly what include/cortex_hip.h declares (CPU only).
+
+No kernel is launched: only symbol checks and argument-validation paths that
+return before touching the HIP runtime.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "cortex_hip.h"
+
+
+def _declared() -> dict[str, int]:
+    """name -> number of parameters, parsed from the header."""
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    out = {}
+    for m in re.finditer(r"\b(?:int|int64_t|const char\*)\s+(cortex_\w+)\s*\(([^)]*)\)\s*;", text):
+        params = [p for p in m.group(2).split(",") if p.strip() and p.strip() != "void"]
+        out[m.group(1)] = len(params)
+    return out
+
+
+def test_header_declares_entry_points():
+    names = _declared()
+    for must in ("cortex_pack_plan", "cortex_tokenize", "cortex_quantize_int8", "cortex_norm_linear",
+                 "cortex_attention", "cortex_row_stats", "cortex_layer_norm", "cortex_last_error"):
+        assert must in names
+
+
+def test_library_exports_every_declared_symbol():
+    from cortex import _native as nat
+
+    lib = nat.load()
+    for name in _declared():
+        assert hasattr(lib, name), name
+
+
+def test_binding_signatures_match_header():
+    from cortex import _native as nat
+
+    decl = _declared()
+    assert set(decl) == set(nat.EXPORTED)
+    for name, (_, args) in nat._SIGNATURES.items():
+        assert len(args) == decl[name], (name, len(args), decl[name])
+
+
+def test_invalid_arguments_return_status_and_message():
+    from cortex import _native as nat
+
+    lib = nat.load()
+    assert lib.cortex_version() == 1
+    rc = lib.cortex_quantize_int8(None, -1, 4, 4, None, None, None, 4, None)
+    assert rc == -1 and b"negative shape" in lib.cortex_last_error()
+    rc = lib.cortex_attention(1, 1, 1, 1, 1, 0, *([None, 0, 0, 0] * 3), None, None, None, 0, None, 0, 0, 0, 0, 0,
+                              ctypes.c_float(1.0), None, 0, 0, 0, None)
+    assert rc == -1 and b"head dim" in lib.cortex_last_error()
+    rc = lib.cortex_norm_linear(4, 4, 4, 0, None, 4, 0, None, None, None, 0, 1, 3, 0, None, 4, None, 0, None, 0, 0,
+                                None, 0, 0, 0, None, 4, None)
+    assert rc == -1
+    assert lib.cortex_pack_workspace_bytes(0, 4) == 0
+    assert lib.cortex_pack_workspace_bytes(5000, 32) == 5 * 32 * 4
+    rc = lib.cortex_pack_plan(None, 1, 10, 100000, None, None, None, None, None, 0, None, None)
+    assert rc == -1 and b"exceeds" in lib.cortex_last_error()
+
+
+def test_missing_library_fails_loudly(monkeypatch, tmp_path):
+    import importlib
+
+    from cortex import _native as nat
+
+    monkeypatch.setenv("CORTEX_HIP_LIB", str(tmp_path / "nope.so"))
+    fresh = importlib.reload(nat)
+    try:
+        with pytest.raises(fresh.NativeLibraryError):
+            fresh.load()
+        assert not fresh.available()
+    finally:
+        monkeypatch.delenv("CORTEX_HIP_LIB")
+        importlib.reload(nat)

@@ -1,0 +1,136 @@
+"""Full Cortex forward on the GPU vs the reference goldens and the oracle (a3, a5, a8, a9)."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import cortex_oracle as O
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+INPUT_KEYS = ("neuron_ids", "time_bins", "values", "batch_indices")
+
+
+def _cfg(name: str, dtype: str):
+    from cortex.models.config import CORTEX_S, CORTEX_XS, CortexConfig
+
+    base = {"xs": CORTEX_XS, "s": CORTEX_S}[name]
+    return CortexConfig(**{**base.model_dump(), "dtype": dtype})
+
+
+def _model(name: str, dtype: str, seed: int = 0):
+    from cortex.models import CortexModel
+
+    torch.manual_seed(seed)
+    return CortexModel(_cfg(name, dtype)).to(DEV).eval()
+
+
+def _inputs(arr, prefix):
+    return [torch.from_numpy(arr[prefix + k]).to(DEV) for k in INPUT_KEYS]
+
+
+def _int8(model, inputs):
+    from cortex.quantization.calibrate import (attach_calibration_hooks, convert_model, derive_scales,
+                                               remove_calibration_hooks)
+
+    hooks = attach_calibration_hooks(model)
+    with torch.no_grad():
+        model(*inputs)
+    remove_calibration_hooks(hooks)
+    assert all(h.stats.n_batches == 1 for n, h in hooks.items() if not n.startswith("masked_spike_head"))
+    return convert_model(model, derive_scales(model, hooks), inplace=True)
+
+
+@pytest.mark.parametrize("name", ["xs", "s"])
+@pytest.mark.parametrize("inputs", ["sorted", "shuffled"])
+def test_fp32_forward_matches_reference_golden(golden, name, inputs):
+    """float32 compute: <= 1e-5 relative (to the largest |output|) vs the reference forward."""
+    _, arr = golden
+    model = _model(name, "float32")
+    with torch.no_grad():
+        beh = model(*_inputs(arr, f"{name}_{inputs}_"))["behavior"].cpu().numpy()
+    ref = arr[f"{name}_{inputs}_behavior_fp32"]
+    assert beh.shape == ref.shape
+    assert np.abs(beh - ref).max() <= 1e-5 * np.abs(ref).max()
+
+
+@pytest.mark.parametrize("name", ["xs", "s"])
+@pytest.mark.parametrize("dtype,tol", [("float32", "rel1e-5"), ("bfloat16", 2e-2)])
+def test_int8_forward_matches_reference_golden(golden, name, dtype, tol):
+    """INT8 weights (quantised on the GPU): fp32 compute <= 1e-5 relative; bf16 compute <= 2e-2 max-abs."""
+    _, arr = golden
+    model = _int8(_model(name, dtype), _inputs(arr, f"{name}_sorted_"))
+    for inputs in ("sorted", "shuffled"):
+        with torch.no_grad():
+            beh = model(*_inputs(arr, f"{name}_{inputs}_"))["behavior"].cpu().numpy()
+        ref = arr[f"{name}_{inputs}_behavior_int8"]
+        if tol == "rel1e-5":
+            assert np.abs(beh - ref).max() <= 1e-5 * np.abs(ref).max(), np.abs(beh - ref).max()
+        else:
+            assert np.abs(beh - ref).max() <= tol, np.abs(beh - ref).max()
+
+
+def _config3_inputs(B=32, per=512, seed=0):
+    rng = np.random.default_rng(seed)
+    E = B * per
+    nid = rng.integers(0, 137, E)
+    tb = rng.integers(0, 600, E)
+    val = np.clip(rng.poisson(1.0, E) + 1, 0, 7)
+    bidx = np.repeat(np.arange(B), per)
+    return nid, tb, val, bidx
+
+
+def test_config3_int8_bf16_forward_vs_oracle():
+    """Config 3 shape (B=32 x 512 events, CORTEX_S, INT8): decoded velocity within 2e-2 max-abs."""
+    arrs = _config3_inputs()
+    inputs = [torch.from_numpy(a).to(DEV) for a in arrs]
+    model = _int8(_model("s", "bfloat16"), [t[:2048] for t in inputs])
+    with torch.no_grad():
+        beh = model(*inputs, batch_size=32)["behavior"].cpu().numpy()
+    sd = {k: v.detach().cpu() for k, v in model.state_dict().items()}
+    torch.set_num_threads(max(1, torch.get_num_threads()))
+    ref = O.forward(sd, O.CORTEX_S_SHAPE, *arrs).numpy()
+    assert beh.shape == (32, 2)
+    assert np.abs(beh - ref).max() <= 2e-2, np.abs(beh - ref).max()
+
+
+def test_module_path_equals_fused_csr_path_fp32():
+    """tokenizer -> _pack_events -> encoder -> behavior_head (padded modules) == fused CSR forward."""
+    from cortex.models.cortex import _pack_events
+
+    arrs = _config3_inputs(B=3, per=100, seed=3)
+    nid, tb, val, bidx = (torch.from_numpy(a).to(DEV) for a in arrs)
+    bidx = bidx[torch.randperm(bidx.shape[0], device=DEV)]
+    model = _model("xs", "float32")
+    with torch.no_grad():
+        fused = model(nid, tb, val, bidx)["behavior"]
+        tokens, mask = _pack_events(model.tokenizer(nid, tb, val), bidx)
+        lat = model.encoder(tokens, mask)
+        modular = model.behavior_head(lat)
+    torch.testing.assert_close(modular, fused, rtol=1e-5, atol=1e-6)
+
+
+def test_captured_graph_replays_match_eager():
+    from cortex.runtime import CapturedForward
+
+    model = _int8(_model("s", "bfloat16"), [torch.from_numpy(a).to(DEV) for a in _config3_inputs(2, 64)])
+    cap = CapturedForward(model, batch_size=4, n_events=4 * 300)
+    for seed in range(3):
+        inputs = [torch.from_numpy(a).to(DEV) for a in _config3_inputs(4, 300, seed=10 + seed)]
+        got = cap(*inputs).clone()
+        with torch.no_grad():
+            want = model(*inputs, batch_size=4)["behavior"]
+        torch.cuda.synchronize()
+        torch.testing.assert_close(got, want, rtol=0, atol=0)
+
+
+def test_invalid_token_index_sets_error_flag():
+    model = _model("xs", "bfloat16")
+    nid, tb, val, bidx = (torch.from_numpy(a).to(DEV) for a in _config3_inputs(2, 50))
+    nid[7] = 10_000
+    err = torch.zeros(1, dtype=torch.int32, device=DEV)
+    with torch.no_grad():
+        out = model(nid, tb, val, bidx, batch_size=2, err_flag=err)["behavior"]
+    assert torch.isfinite(out).all() and int(err.item()) & 1

@@ -1,0 +1,133 @@
+"""Fused norm + linear on the GPU vs the oracle (a5, a6, a7)."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import cortex_oracle as O
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _rel_err(out: torch.Tensor, ref: torch.Tensor) -> float:
+    return float((out.double() - ref.double()).abs().max() / ref.double().abs().max().clamp_min(1e-30))
+
+
+@pytest.mark.parametrize("M,K,N", [(16, 64, 128), (64, 128, 256), (256, 512, 512), (8192, 512, 1536),
+                                   (8192, 512, 2048), (33, 70, 97), (1, 512, 2048)])
+def test_rms_norm_linear_fp32(M, K, N):
+    """fp32: <= 1e-5 relative to the oracle (fp32 MFMA, fp32 accumulation)."""
+    from cortex.kernels.fused_rmsnorm import rms_norm_linear
+
+    torch.manual_seed(17)
+    x, w = torch.randn(M, K), torch.randn(K, N)
+    g = torch.ones(K) + 0.02 * torch.randn(K)
+    out = rms_norm_linear(x.to(DEV), g.to(DEV), w.to(DEV))
+    ref = O.rms_norm_linear(x.double(), g.double(), w.double()).float()
+    assert out.shape == (M, N) and out.dtype == torch.float32
+    assert _rel_err(out.cpu(), ref) <= 1e-5
+    torch.testing.assert_close(out.cpu(), ref, rtol=1e-4, atol=1e-4)
+
+
+@pytest.mark.parametrize("M,K,N", [(8192, 512, 1536), (8192, 512, 2048), (8192, 512, 512), (33, 70, 97)])
+def test_rms_norm_linear_bf16(M, K, N):
+    from cortex.kernels.fused_rmsnorm import rms_norm_linear
+
+    torch.manual_seed(17)
+    x = torch.randn(M, K).bfloat16()
+    w = torch.randn(K, N).bfloat16()
+    g = (torch.ones(K) + 0.02 * torch.randn(K)).bfloat16()
+    out = rms_norm_linear(x.to(DEV), g.to(DEV), w.to(DEV))
+    ref = O.rms_norm_linear(x, g, w)  # x_norm rounded to bf16 as in the reference, fp32 matmul
+    assert out.dtype == torch.bfloat16
+    torch.testing.assert_close(out.float().cpu(), ref, rtol=1e-2, atol=2e-2 * float(ref.abs().max()) / 8)
+
+
+def test_rms_norm_linear_bias_and_3d():
+    from cortex.kernels.fused_rmsnorm import rms_norm_linear
+
+    torch.manual_seed(3)
+    x, g, w, b = torch.randn(2, 256, 512), torch.ones(512), torch.randn(512, 1536), torch.randn(1536)
+    out = rms_norm_linear(x.to(DEV), g.to(DEV), w.to(DEV), b.to(DEV))
+    assert out.shape == (2, 256, 1536)
+    ref = O.rms_norm_linear(x.reshape(-1, 512).double(), g.double(), w.double(), b.double()).float()
+    assert _rel_err(out.reshape(-1, 1536).cpu(), ref) <= 1e-5
+
+
+def _config2(N, seed=0):
+    rng = np.random.default_rng(seed)
+    x = torch.from_numpy(rng.normal(0, 1, (8192, 512)).astype(np.float32)).bfloat16()
+    g = torch.from_numpy(rng.normal(1, 0.02, 512).astype(np.float32))
+    w = rng.normal(0, 0.02, (N, 512)).astype(np.float32)
+    q, s = O.quantize_int8(w)
+    return x, g, torch.from_numpy(q), torch.from_numpy(s)
+
+
+@pytest.mark.parametrize("N", [1536, 2048, 512])
+def test_rms_int8_linear_config2(N):
+    """Config 2: RMSNorm(eps 1e-6) + INT8 per-channel linear, bf16 in/out."""
+    from cortex.kernels.fused_rmsnorm import norm_linear_int8
+
+    x, g, q, s = _config2(N)
+    out = norm_linear_int8(x.to(DEV), q.to(DEV), s.to(DEV), norm="rms", gamma=g.to(DEV), eps=1e-6)
+    wdq = torch.from_numpy(O.dequantize(q.numpy(), s.numpy()))
+    ref = O.rms_norm_linear(x, g, wdq.T.contiguous())  # bf16 x_norm, fp32 contraction
+    assert out.dtype == torch.bfloat16
+    err = (out.float().cpu() - ref).abs()
+    # one bf16 rounding of the output plus accumulation-order noise
+    assert float((err / ref.abs().clamp_min(1e-3)).median()) < 4e-3
+    assert float(err.max()) <= 2e-2 * float(ref.abs().max())
+
+
+def test_layernorm_gelu_residual_epilogues_fp32():
+    """LayerNorm prologue + GELU epilogue and residual epilogue, fp32 compute vs torch CPU."""
+    from cortex.kernels import ops
+
+    torch.manual_seed(5)
+    x = torch.randn(300, 512) * 3 + 1
+    ln_w, ln_b = 1 + 0.1 * torch.randn(512), 0.1 * torch.randn(512)
+    w = torch.randn(2048, 512) * 0.02
+    q, s = O.quantize_int8(w.numpy())
+    qd, sd = torch.from_numpy(q), torch.from_numpy(s)
+    h = ops.norm_linear(x.to(DEV), weight_int8=qd.to(DEV), weight_scale=sd.to(DEV), norm="layer",
+                        gamma=ln_w.to(DEV), beta=ln_b.to(DEV), eps=1e-5, act="gelu", out_dtype=torch.float32,
+                        compute_dtype=torch.float32)
+    wdq = torch.from_numpy(O.dequantize(q, s))
+    ref_h = F.gelu(F.linear(F.layer_norm(x, (512,), ln_w, ln_b, 1e-5), wdq))
+    assert _rel_err(h.cpu(), ref_h) <= 1e-5
+    w2 = torch.randn(512, 2048) * 0.02
+    res = torch.randn(300, 512)
+    y = ops.norm_linear(h, weight=w2.to(DEV), residual=res.to(DEV), out_dtype=torch.float32,
+                        compute_dtype=torch.float32)
+    ref_y = res + F.linear(ref_h, w2)
+    assert _rel_err(y.cpu(), ref_y) <= 1e-5
+
+
+def test_broadcast_residual_rows():
+    """res_rows broadcasts a batch-invariant residual (the learned latents) over the batch."""
+    from cortex.kernels import ops
+
+    torch.manual_seed(9)
+    a = torch.randn(4 * 256, 512).bfloat16()
+    w = torch.randn(512, 512) * 0.02
+    lat = torch.randn(256, 512)
+    y = ops.norm_linear(a.to(DEV), weight=w.to(DEV), residual=lat.to(DEV), res_rows=256,
+                        out_dtype=torch.float32, compute_dtype=torch.bfloat16)
+    ref = lat.repeat(4, 1) + a.float() @ w.bfloat16().float().T
+    torch.testing.assert_close(y.cpu(), ref, rtol=1e-4, atol=1e-4)
+
+
+def test_layer_norm_kernel_and_row_stats():
+    from cortex.kernels import ops
+
+    torch.manual_seed(2)
+    x = torch.randn(777, 512) * 2 + 0.5
+    w, b = torch.randn(512), torch.randn(512)
+    y = ops.layer_norm(x.to(DEV), w.to(DEV), b.to(DEV), 1e-5)
+    torch.testing.assert_close(y.cpu(), F.layer_norm(x, (512,), w, b, 1e-5), rtol=1e-5, atol=2e-5)
+    st = ops.row_stats(x.to(DEV), "rms", 1e-6).cpu()
+    torch.testing.assert_close(st[:, 1], torch.sqrt(x.pow(2).mean(-1) + 1e-6), rtol=1e-6, atol=1e-6)

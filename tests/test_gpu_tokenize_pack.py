@@ -1,0 +1,166 @@
+"""Tokenizer + pack on the GPU vs the oracle: bit-exact (a1, a2)."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import cortex_oracle as O
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _tables(N, T, V, D, dtype, seed=42):
+    g = torch.Generator().manual_seed(seed)
+    return tuple(torch.randn(s, D, generator=g).to(dtype) for s in (N, T, V))
+
+
+def _ids(E, N, T, V, seed=99):
+    g = torch.Generator().manual_seed(seed)
+    return tuple(torch.randint(0, s, (E,), generator=g, dtype=torch.int64) for s in (N, T, V))
+
+
+def _ref_torch(n, t, v, nid, tb, val):
+    """Left-to-right add in the table dtype on the CPU (bf16 adds round to nearest even)."""
+    return (n[nid] + t[tb]) + v[val]
+
+
+@pytest.mark.parametrize("E,D,N,T,V", [(1, 64, 32, 64, 8), (127, 64, 32, 64, 8), (128, 64, 256, 512, 8),
+                                       (1024, 128, 256, 512, 8), (4096, 256, 512, 1024, 8),
+                                       (16384, 512, 512, 1024, 16), (33, 70, 5, 7, 3)])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_fused_tokenizer_bitexact(E, D, N, T, V, dtype):
+    from cortex.kernels.tokenizer import fused_tokenizer
+
+    n, t, v = _tables(N, T, V, D, dtype)
+    nid, tb, val = _ids(E, N, T, V)
+    out = fused_tokenizer(n.to(DEV), t.to(DEV), v.to(DEV), nid.to(DEV), tb.to(DEV), val.to(DEV))
+    assert out.shape == (E, D) and out.dtype == dtype
+    if dtype == torch.float32:
+        want = O.tokenize(n.numpy(), t.numpy(), v.numpy(), nid.numpy(), tb.numpy(), val.numpy())
+        np.testing.assert_array_equal(out.cpu().numpy(), want)
+    else:
+        assert torch.equal(out.cpu(), _ref_torch(n, t, v, nid, tb, val))
+
+
+def test_fused_tokenizer_edge_cases():
+    from cortex.kernels.tokenizer import fused_tokenizer
+
+    n, t, v = (x.to(DEV) for x in _tables(32, 64, 8, 128, torch.float32))
+    empty = torch.zeros(0, dtype=torch.int64, device=DEV)
+    assert fused_tokenizer(n, t, v, empty, empty, empty).shape == (0, 128)
+    big = torch.randint(0, 32, (128,), device=DEV)
+    nid = big[::2]  # strided view
+    tb = torch.randint(0, 64, (64,), device=DEV)
+    val = torch.randint(0, 8, (64,), device=DEV)
+    out = fused_tokenizer(n, t, v, nid, tb, val)
+    want = O.tokenize(n.cpu().numpy(), t.cpu().numpy(), v.cpu().numpy(), nid.cpu().numpy(), tb.cpu().numpy(),
+                      val.cpu().numpy())
+    np.testing.assert_array_equal(out.cpu().numpy(), want)
+    with pytest.raises(ValueError):
+        fused_tokenizer(n.t(), t, v, nid, tb, val)
+    with pytest.raises(ValueError):
+        fused_tokenizer(n, t, v, nid, tb[:-1], val)
+    # out-of-range index: zero row, no out-of-bounds access, IndexError when checked
+    bad = nid.clone()
+    bad[5] = 32
+    out = fused_tokenizer(n, t, v, bad, tb, val)
+    assert (out[5] == 0).all()
+    with pytest.raises(IndexError):
+        fused_tokenizer(n, t, v, bad, tb, val, check_indices=True)
+
+
+def _config0_inputs(seed=0, shuffle=False, B=32):
+    rng = np.random.default_rng(seed)
+    counts = rng.integers(128, 513, B)
+    E = int(counts.sum())
+    nid = rng.integers(0, 137, E)
+    tb = rng.integers(0, 600, E)
+    val = np.clip(rng.poisson(1.0, E) + 1, 0, 7)
+    bidx = np.repeat(np.arange(B), counts)
+    if shuffle:
+        p = rng.permutation(E)
+        nid, tb, val, bidx = nid[p], tb[p], val[p], bidx[p]
+    tabs = [rng.normal(0, 0.02, (s, 512)).astype(np.float32) for s in (137, 600, 8)]
+    return tabs, nid, tb, val, bidx
+
+
+@pytest.mark.parametrize("shuffle", [False, True])
+def test_tokenize_and_pack_config0_bitexact(shuffle):
+    """Config 0: B=32, E_b ~ U[128,512], tables 137/600/8 x 512 fp32 -> CSR and padded, bit-exact."""
+    from cortex.kernels.tokenizer import tokenize_and_pack
+
+    tabs, nid, tb, val, bidx = _config0_inputs(shuffle=shuffle)
+    want_tok = O.tokenize(*tabs, nid, tb, val)
+    want = O.pack_events(want_tok, bidx)
+    args = [torch.from_numpy(a).to(DEV) for a in (*tabs, nid, tb, val, bidx)]
+    tok, off = tokenize_and_pack(*args, batch_size=32, layout="csr")
+    np.testing.assert_array_equal(off.cpu().numpy(), want.offsets)
+    np.testing.assert_array_equal(tok.cpu().numpy(), want.csr)
+    pad, mask = tokenize_and_pack(*args, layout="padded")
+    np.testing.assert_array_equal(pad.cpu().numpy(), want.padded)
+    np.testing.assert_array_equal(mask.cpu().numpy(), want.mask)
+
+
+@pytest.mark.parametrize("seed", range(4))
+def test_pack_plan_stable_rank_random(seed):
+    """Unsorted batch indices with many collisions, empty samples, E not a multiple of 64."""
+    from cortex.kernels.pack import pack_plan
+
+    rng = np.random.default_rng(seed)
+    E = int(rng.integers(1, 5000))
+    B = int(rng.integers(1, 300))
+    bidx = rng.integers(0, B, E)
+    p = O.pack_events(np.zeros((E, 1), np.float32), bidx, batch_size=B)
+    off, order, rank = pack_plan(torch.from_numpy(bidx).to(DEV), B)
+    np.testing.assert_array_equal(off.cpu().numpy(), p.offsets)
+    np.testing.assert_array_equal(order.cpu().numpy(), p.order)
+    np.testing.assert_array_equal(rank.cpu().numpy(), p.rank)
+
+
+def test_pack_plan_large_multi_chunk():
+    """E spans several 1024-event chunks (and a chunk size above 1024)."""
+    from cortex.kernels.pack import pack_plan
+
+    rng = np.random.default_rng(7)
+    for E, B in ((131072, 256), (1_200_000, 64)):
+        bidx = np.sort(rng.integers(0, B, E)) if E > 200000 else rng.integers(0, B, E)
+        p = O.pack_events(np.zeros((E, 1), np.float32), bidx, batch_size=B)
+        off, order, rank = pack_plan(torch.from_numpy(bidx).to(DEV), B)
+        np.testing.assert_array_equal(off.cpu().numpy(), p.offsets)
+        np.testing.assert_array_equal(order.cpu().numpy(), p.order)
+
+
+def test_pack_events_drop_in_matches_oracle():
+    from cortex.models.cortex import _pack_events
+
+    rng = np.random.default_rng(11)
+    E = 700
+    bidx = rng.integers(0, 9, E)
+    x = rng.normal(size=(E, 96)).astype(np.float32)
+    want = O.pack_events(x, bidx)
+    out, mask = _pack_events(torch.from_numpy(x).to(DEV), torch.from_numpy(bidx).to(DEV))
+    np.testing.assert_array_equal(out.cpu().numpy(), want.padded)
+    np.testing.assert_array_equal(mask.cpu().numpy(), want.mask)
+    e_out, e_mask = _pack_events(torch.zeros(0, 96, device=DEV), torch.zeros(0, dtype=torch.int64, device=DEV))
+    assert e_out.shape == (1, 0, 96) and e_mask.shape == (1, 0)
+
+
+def test_invalid_batch_index_sets_flag_and_stays_in_bounds():
+    from cortex.kernels import ops
+
+    tabs, nid, tb, val, bidx = _config0_inputs(B=4)
+    bidx = bidx.copy()
+    bidx[3] = 4  # == B: invalid
+    bidx[10] = -1
+    err = torch.zeros(1, dtype=torch.int32, device=DEV)
+    t = [torch.from_numpy(a).to(DEV) for a in (*tabs, nid, tb, val, bidx)]
+    off, order, _ = ops.pack_plan(t[6], 4, err=err)
+    tok = ops.tokenize(*t[:6], order=order, csr_offsets=off, err=err)
+    torch.cuda.synchronize()
+    assert int(err.item()) & 2
+    valid = (bidx >= 0) & (bidx < 4)
+    assert int(off[-1].item()) == int(valid.sum())
+    assert (tok[int(valid.sum()):] == 0).all()

@@ -1,0 +1,127 @@
+"""Host-side logic of the package (CPU only): config, calibration bookkeeping,
+save/load, temporal tile mask, and the refusal to run kernels on CPU tensors."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+from torch import nn
+
+from oracle import cortex_oracle as O
+
+
+def test_config_validation_and_compute_dtype():
+    from cortex.models.config import CORTEX_M, CORTEX_S, CORTEX_XS, CortexConfig
+
+    with pytest.raises(ValueError, match="must equal hidden_dim"):
+        CortexConfig(hidden_dim=128, num_layers=2, num_heads=2, head_dim=32, num_latents=32, latent_dim=128,
+                     cross_attn_heads=2, max_neurons=256, max_time_bins=512, behavior_dim=2)
+    assert CORTEX_S.compute_dtype == torch.bfloat16
+    assert CortexConfig(**{**CORTEX_XS.model_dump(), "dtype": "float32"}).compute_dtype == torch.float32
+    with pytest.raises(NotImplementedError):
+        _ = CortexConfig(**{**CORTEX_XS.model_dump(), "dtype": "float16"}).compute_dtype
+    assert (CORTEX_M.hidden_dim, CORTEX_M.num_layers, CORTEX_M.num_latents) == (768, 11, 384)
+
+
+def test_activation_stats_percentile():
+    from cortex.quantization.calibrate import ActivationStats
+
+    s = ActivationStats()
+    assert s.percentile_99 == 1.0
+    s.update(torch.tensor([1.0, -2.0, 3.0]))
+    assert s.n_batches == 1 and s.percentile_99 == pytest.approx(3.0)
+    s = ActivationStats()
+    for _ in range(99):
+        s.update(torch.ones(10))
+    s.update(torch.full((10,), 100.0))
+    assert s.n_batches == 100 and s.percentile_99 < 50.0
+    s = ActivationStats()
+    s.update(torch.tensor([-5.0, 1.0]))
+    assert s.percentile_99 == pytest.approx(5.0)
+
+
+def test_hooks_attach_count_and_remove():
+    from cortex.quantization.calibrate import attach_calibration_hooks, remove_calibration_hooks
+
+    model = nn.Sequential(nn.Linear(16, 32), nn.ReLU(), nn.Linear(32, 8))
+    hooks = attach_calibration_hooks(model)
+    assert len(hooks) == 2
+    with torch.no_grad():
+        for _ in range(5):
+            model(torch.randn(4, 16))
+    remove_calibration_hooks(hooks)
+    with torch.no_grad():
+        model(torch.randn(4, 16))
+    assert all(h.stats.n_batches == 5 for h in hooks.values())
+
+
+def test_quantized_linear_buffers_save_load_roundtrip(tmp_path):
+    from cortex.quantization.calibrate import (QuantizedLinear, calibration_summary, count_quantized_linears,
+                                               load_quantized, model_weight_bytes, save_quantized)
+
+    q, s = O.quantize_int8(np.random.default_rng(0).normal(0, 0.02, (8, 16)).astype(np.float32))
+    m = nn.Sequential(QuantizedLinear(torch.from_numpy(q), torch.from_numpy(s), None), nn.Linear(8, 4))
+    assert count_quantized_linears(m) == (1, 2)
+    assert model_weight_bytes(m) == 8 * 16 + 8 * 4 + (4 * 8 + 4) * 4
+    assert "INT8" in m[0].extra_repr()
+    assert set(m[0].state_dict()) == {"weight_int8", "weight_scale"}
+    save_quantized(m, tmp_path / "q.pt", meta={"note": "x"})
+    m2 = nn.Sequential(QuantizedLinear(torch.zeros(8, 16, dtype=torch.int8), torch.zeros(8), None),
+                       nn.Linear(8, 4))
+    load_quantized(tmp_path / "q.pt", m2)
+    assert torch.equal(m2[0].weight_int8, m[0].weight_int8) and torch.equal(m2[0].weight_scale, m[0].weight_scale)
+    assert calibration_summary({}, {}) == []
+
+
+def test_temporal_block_mask_matches_oracle():
+    from cortex.kernels.sparse_xattn import build_temporal_block_mask
+
+    rng = np.random.default_rng(8)
+    for _ in range(8):
+        E, L = int(rng.integers(1, 700)), int(rng.integers(1, 300))
+        t = np.sort(rng.integers(0, 600, E))
+        w = int(rng.integers(0, 60))
+        got = build_temporal_block_mask(torch.from_numpy(t), L, 600, w, 32, 64)
+        np.testing.assert_array_equal(got.numpy(), O.temporal_block_mask(t, L, 600, w, 32, 64))
+    assert build_temporal_block_mask(torch.arange(64) % 120, 32, 120, window_bins=120, BLOCK_L=32,
+                                     BLOCK_E=32).all()
+
+
+def test_reference_formulations_are_exported():
+    """The *_reference functions of the reference API stay importable (torch formulations)."""
+    from cortex.kernels.fused_rmsnorm import rms_norm_linear_reference
+    from cortex.kernels.sparse_xattn import sparse_cross_attention_reference
+    from cortex.kernels.tokenizer import fused_tokenizer_reference
+
+    torch.manual_seed(0)
+    x, g, w = torch.randn(4, 8), torch.ones(8), torch.randn(8, 3)
+    torch.testing.assert_close(rms_norm_linear_reference(x, g, w), O.rms_norm_linear(x, g, w))
+    n = torch.randn(5, 4)
+    i = torch.tensor([1, 2])
+    assert torch.equal(fused_tokenizer_reference(n, n, n, i, i, i), (n[i] + n[i]) + n[i])
+    q = torch.randn(1, 1, 8, 4)
+    assert sparse_cross_attention_reference(q, q, q).shape == q.shape
+
+
+def test_kernels_refuse_cpu_tensors():
+    from cortex.kernels.fused_rmsnorm import rms_norm_linear
+    from cortex.kernels.sparse_xattn import sparse_cross_attention
+    from cortex.kernels.tokenizer import fused_tokenizer
+    from cortex.models import CortexModel
+    from cortex.models.config import CORTEX_XS
+
+    n = torch.randn(4, 8)
+    i = torch.zeros(3, dtype=torch.int64)
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        fused_tokenizer(n, n, n, i, i, i)
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        rms_norm_linear(torch.randn(2, 8), torch.ones(8), torch.randn(8, 4))
+    q = torch.randn(1, 1, 4, 8)
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        sparse_cross_attention(q, q, q)
+    model = CortexModel(CORTEX_XS)
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        model(i, i, i, i)
+    with pytest.raises(ValueError, match="shape mismatch"):
+        model.tokenizer(i, i[:-1], i)
