@@ -55,6 +55,9 @@ _SIGNATURES = {
     "cortex_quantize_int8": (_int, [_ptr, _i64, _i64, _i64, _ptr, _ptr, _ptr, _i64, _ptr]),
     "cortex_row_stats": (_int, [_i64, _i64, _int, _ptr, _i64, _int, _f32, _ptr, _ptr]),
     "cortex_layer_norm": (_int, [_i64, _i64, _int, _ptr, _i64, _ptr, _ptr, _int, _f32, _int, _ptr, _i64, _ptr]),
+    "cortex_ln_rows": (
+        _int, [_i64, _i64, _ptr, _i64, _ptr, _ptr, _f32, _ptr, _ptr, _f32, _ptr, _i64, _ptr, _i64, _ptr]),
+    "cortex_convert": (_int, [_int, _ptr, _int, _ptr, _i64, _ptr]),
     "cortex_norm_linear": (
         _int,
         [_i64, _i64, _i64, _int, _ptr, _i64, _int, _ptr, _ptr, _ptr, _int, _int, _int, _int, _ptr, _i64, _ptr,

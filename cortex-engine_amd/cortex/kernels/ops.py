@@ -150,6 +150,34 @@ def layer_norm(x: torch.Tensor, weight, bias, eps: float, out_dtype=None, out=No
     return out
 
 
+def ln_rows(x: torch.Tensor, ln1, ln2=None, out_bf16: bool = True, out_f32: bool = False):
+    """LayerNorm over rows of fp32 ``x`` (K in {256, 512, 768, 1024}); ``ln1``/``ln2``
+    are ``(weight, bias, eps)`` triples (``ln2`` applied after ``ln1`` when given).
+    Returns the bf16 and/or fp32 result(s)."""
+    dev = nat.require_gpu(x, what="ln_rows")
+    x2 = _row_major_2d(x.reshape(-1, x.shape[-1]))
+    M, K = x2.shape
+    ob = torch.empty((M, K), dtype=torch.bfloat16, device=dev) if out_bf16 else None
+    of = torch.empty((M, K), dtype=torch.float32, device=dev) if out_f32 else None
+    g1, b1, e1 = ln1
+    g2, b2, e2 = ln2 if ln2 is not None else (None, None, 0.0)
+    nat.call("cortex_ln_rows", M, K, nat.ptr(x2), x2.stride(0) if M > 1 else K, nat.ptr(g1), nat.ptr(b1),
+             float(e1), nat.ptr(g2), nat.ptr(b2), float(e2), nat.ptr(ob), K, nat.ptr(of), K, nat.stream_of(dev))
+    if out_bf16 and out_f32:
+        return ob, of
+    return ob if out_bf16 else of
+
+
+def convert(t: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
+    """Elementwise dtype conversion on the GPU (int8/f32/bf16/f16 -> f32/bf16)."""
+    dev = nat.require_gpu(t, what="convert")
+    src = t.detach().contiguous()
+    out = torch.empty(src.shape, dtype=dtype, device=dev)
+    nat.call("cortex_convert", nat.code(src.dtype), nat.ptr(src), nat.code(dtype), nat.ptr(out), src.numel(),
+             nat.stream_of(dev))
+    return out
+
+
 # --------------------------------------------------------------------------- linear
 
 
@@ -181,7 +209,7 @@ def norm_linear(x: torch.Tensor, *, weight: torch.Tensor | None = None, weight_i
         w2 = _row_major_2d(weight.detach())
         layout = 0 if w_layout == "nk" else 1
         N, Kw = (w2.shape if layout == 0 else (w2.shape[1], w2.shape[0]))
-        ws = None
+        ws = weight_scale.contiguous() if weight_scale is not None else None
     if Kw != K:
         raise ValueError(f"inner dims differ: x has K={K}, weight has K={Kw}")
     if compute_dtype not in (torch.bfloat16, torch.float32):
@@ -227,8 +255,8 @@ def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, scale: float
     ``kv_offsets`` (B+1) ``k``/``v`` are (1, H, E_total, Dh) CSR views and sample b
     uses rows [kv_offsets[b], kv_offsets[b+1]).
     """
-    tensors = [q, k, v, kv_offsets, kv_lengths, key_mask, block_mask, out]
-    dev = nat.require_gpu(*tensors, what="attention")
+    # the tile mask is a small host-side structure (the reference builds it on the CPU)
+    dev = nat.require_gpu(q, k, v, kv_offsets, kv_lengths, key_mask, out, what="attention")
     if q.dtype != k.dtype or q.dtype != v.dtype:
         raise ValueError("q, k, v must share a dtype")
     if q.dtype not in (torch.bfloat16, torch.float32):

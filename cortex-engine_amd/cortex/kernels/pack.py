@@ -36,7 +36,7 @@ def pack_events(flat_tokens: torch.Tensor, batch_indices: torch.Tensor, *, batch
     offsets, order, _ = ops.pack_plan(batch_indices, batch_size)
     if max_events is None:
         max_events = int((offsets[1:] - offsets[:-1]).max().item()) if E > 0 else 0
-    return ops.pack_rows(flat_tokens.reshape(E, -1), order, offsets, batch_size, max_events)
+    return ops.pack_rows(flat_tokens.reshape(E, flat_tokens.shape[-1]), order, offsets, batch_size, max_events)
 
 
 def pack_csr(flat_tokens: torch.Tensor, batch_indices: torch.Tensor, batch_size: int):
@@ -45,9 +45,9 @@ def pack_csr(flat_tokens: torch.Tensor, batch_indices: torch.Tensor, batch_size:
     offsets, order, _ = ops.pack_plan(batch_indices, batch_size)
     E = batch_indices.shape[0]
     dev = flat_tokens.device
-    out = torch.empty_like(flat_tokens.reshape(E, -1))
+    out = torch.empty_like(flat_tokens.reshape(E, flat_tokens.shape[-1]))
     if E:
-        src = ops._row_major_2d(flat_tokens.reshape(E, -1))
+        src = ops._row_major_2d(flat_tokens.reshape(E, flat_tokens.shape[-1]))
         nat.call("cortex_pack_rows", nat.code(src.dtype), src.shape[1], nat.ptr(src),
                  src.stride(0) if E > 1 else src.shape[1], E, nat.ptr(order), ops._end_ptr(offsets), None, 0, 0,
                  nat.ptr(out), out.shape[1], None, nat.stream_of(dev))

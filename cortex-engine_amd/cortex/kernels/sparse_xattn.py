@@ -82,7 +82,7 @@ def sparse_cross_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, bl
     ``(n_q, n_k)`` (shared by every (b, h), as in the reference) or ``(B, n_q, n_k)``;
     ``None`` is dense attention (also on the HIP kernel).
     """
-    nat.require_gpu(q, k, v, kv_lengths, key_padding_mask, what="sparse_cross_attention")
+    nat.require_gpu(q, k, v, what="sparse_cross_attention")
     B, H, L, Dh = q.shape
     E = k.shape[2]
     if block_mask is not None:
@@ -95,5 +95,7 @@ def sparse_cross_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, bl
                 f"block_mask shape {block_mask.shape} != expected ({B}, {n_q}, {n_k})")
     if kv_lengths is not None:
         kv_lengths = kv_lengths.to(device=q.device, dtype=torch.int64).contiguous()
+    if key_padding_mask is not None:
+        key_padding_mask = key_padding_mask.to(device=q.device)
     return ops.attention(q, k, v, scale=scale, kv_lengths=kv_lengths, key_mask=key_padding_mask,
                          block_mask=block_mask, block_l=BLOCK_L, block_e=BLOCK_E)

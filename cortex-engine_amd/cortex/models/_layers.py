@@ -1,25 +1,81 @@
-"""Module-level glue between nn.Linear / QuantizedLinear / nn.LayerNorm and the
-fused HIP ops (norm prologue, dequant + bias + GELU + residual epilogue)."""
+"""Module-level glue between nn.Linear / QuantizedLinear / nn.LayerNorm and the HIP ops.
+
+bf16 compute (the default):
+  * ``norm -> linear`` runs as one LayerNorm row kernel writing bf16 rows
+    (``cortex_ln_rows``) followed by the pipelined MFMA GEMM on bf16 operands;
+  * the GEMM reads the weight's bf16 execution image, built once per weight tensor
+    on the device and cached on the module (rebuilt when the weight's storage or
+    version changes).  For a QuantizedLinear the image holds the int8 values
+    themselves -- every int8 value is exactly a bf16 value -- and the per-channel
+    scale is applied to the fp32 accumulator in the epilogue, so results are
+    identical to widening the int8 weight inside the kernel (set
+    ``CORTEX_INT8_WEIGHTS=widen`` to stream the int8 weight instead).  For a float
+    nn.Linear the image is the weight rounded to bf16, as ``F.linear`` on bf16
+    inputs would use it.
+fp32 compute: int8 or fp32 weights, fp32 operands, fused norm prologue.
+"""
 
 from __future__ import annotations
+
+import os
 
 import torch
 from torch import nn
 
 from cortex.kernels import ops
 
+INT8_WEIGHTS = os.environ.get("CORTEX_INT8_WEIGHTS", "image")
+_LN_ROWS_K = (256, 512, 768, 1024)
+
 
 def linear_weights(lin: nn.Module) -> dict:
-    """Weight arguments of ``ops.norm_linear`` for an nn.Linear or a QuantizedLinear."""
+    """Weight arguments of ``ops.norm_linear`` in their stored form."""
     if hasattr(lin, "weight_int8"):
         return {"weight_int8": lin.weight_int8, "weight_scale": lin.weight_scale, "bias": lin.bias}
     return {"weight": lin.weight, "bias": lin.bias}
 
 
+def exec_weights(lin: nn.Module, compute: torch.dtype) -> dict:
+    """Weight arguments for the GEMM at ``compute`` precision (bf16 image when bf16)."""
+    quant = hasattr(lin, "weight_int8")
+    if compute != torch.bfloat16 or (quant and INT8_WEIGHTS == "widen"):
+        return linear_weights(lin)
+    src = lin.weight_int8 if quant else lin.weight
+    key = (src.data_ptr(), src._version, tuple(src.shape), src.device)
+    cached = lin.__dict__.get("_cortex_exec")
+    if cached is None or cached[0] != key:
+        cached = (key, ops.convert(src, torch.bfloat16))
+        lin.__dict__["_cortex_exec"] = cached
+    return {"weight": cached[1], "weight_scale": lin.weight_scale if quant else None, "bias": lin.bias}
+
+
+def _ln_params(norm: nn.LayerNorm):
+    return (norm.weight, norm.bias, norm.eps)
+
+
+def ln_rows_ok(x: torch.Tensor, *norms: nn.LayerNorm) -> bool:
+    """Whether the register-resident LayerNorm row kernel covers this input."""
+    if x.dtype != torch.float32 or x.shape[-1] not in _LN_ROWS_K:
+        return False
+    for n in norms:
+        for p in (n.weight, n.bias):
+            if p is None or p.dtype != torch.float32 or p.data_ptr() % 16:
+                return False
+    return True
+
+
+def normalize_bf16(x: torch.Tensor, norm: nn.LayerNorm, norm2: nn.LayerNorm | None = None) -> torch.Tensor:
+    """``norm2(norm(x))`` (or ``norm(x)``) as bf16 rows (one launch)."""
+    x2 = x.reshape(-1, x.shape[-1])
+    if x2.data_ptr() % 16 or (x2.shape[0] > 1 and x2.stride(0) % 4) or x2.stride(-1) != 1:
+        x2 = x2.contiguous()
+    return ops.ln_rows(x2, _ln_params(norm), _ln_params(norm2) if norm2 is not None else None)
+
+
 def apply_linear(lin: nn.Module, x: torch.Tensor, *, norm: nn.LayerNorm | None = None, stats=None,
                  act: str | None = None, residual: torch.Tensor | None = None, res_rows: int = 0,
                  out_dtype: torch.dtype, compute: torch.dtype, out: torch.Tensor | None = None) -> torch.Tensor:
-    """``act(lin(norm(x))) + residual`` as one fused kernel.
+    """``act(lin(norm(x))) + residual`` on the HIP kernels.
 
     When the linear carries forward pre-hooks (calibration), its input is
     materialised first and handed to the hooks exactly as ``nn.Module.__call__``
@@ -31,8 +87,14 @@ def apply_linear(lin: nn.Module, x: torch.Tensor, *, norm: nn.LayerNorm | None =
             hook(lin, (xin,))
         return ops.norm_linear(xin, **linear_weights(lin), act=act, residual=residual, res_rows=res_rows,
                                out_dtype=out_dtype, compute_dtype=compute, out=out)
+    w = exec_weights(lin, compute)
+    if norm is not None and compute == torch.bfloat16 and stats is None and ln_rows_ok(x, norm):
+        lead = x.shape[:-1]
+        xn = normalize_bf16(x, norm).reshape(*lead, x.shape[-1])
+        return ops.norm_linear(xn, **w, act=act, residual=residual, res_rows=res_rows, out_dtype=out_dtype,
+                               compute_dtype=compute, out=out)
     kw = {}
     if norm is not None:
         kw = {"norm": "layer", "gamma": norm.weight, "beta": norm.bias, "eps": norm.eps, "stats": stats}
-    return ops.norm_linear(x, **linear_weights(lin), **kw, act=act, residual=residual, res_rows=res_rows,
-                           out_dtype=out_dtype, compute_dtype=compute, out=out)
+    return ops.norm_linear(x, **w, **kw, act=act, residual=residual, res_rows=res_rows, out_dtype=out_dtype,
+                           compute_dtype=compute, out=out)

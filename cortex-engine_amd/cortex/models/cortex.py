@@ -26,7 +26,7 @@ from torch import nn
 
 from cortex.kernels import ops
 from cortex.kernels.pack import pack_events as _device_pack_events
-from cortex.models._layers import apply_linear
+from cortex.models._layers import apply_linear, exec_weights, ln_rows_ok, normalize_bf16
 from cortex.models.config import CortexConfig
 from cortex.models.perceiver import PerceiverEncoder
 from cortex.models.tokenizer import SpikeTokenizer
@@ -46,14 +46,25 @@ class BehaviorDecoder(nn.Module):
         self.num_heads = config.num_heads
         self.head_dim = config.head_dim
 
-    def forward_rows(self, lat: torch.Tensor, batch: int) -> torch.Tensor:
-        """(B*L, D) latents (after final_norm) -> (B, behavior_dim) fp32."""
+    def forward_rows(self, lat: torch.Tensor, batch: int, pre_norm: nn.LayerNorm | None = None) -> torch.Tensor:
+        """(B*L, D) latents -> (B, behavior_dim) fp32.
+
+        ``pre_norm`` (the encoder's final norm) is applied to ``lat`` first; with bf16
+        compute both LayerNorms run in one row kernel that writes the kv_proj operand.
+        """
         compute = self.config.compute_dtype
         L = self.config.num_latents
         D = lat.shape[1]
         H = self.num_heads
         Q = self.query.shape[0]
-        kv = apply_linear(self.kv_proj, lat, norm=self.norm, out_dtype=compute, compute=compute)
+        if (pre_norm is not None and compute == torch.bfloat16 and not self.kv_proj._forward_pre_hooks
+                and ln_rows_ok(lat, pre_norm, self.norm)):
+            kv = ops.norm_linear(normalize_bf16(lat, pre_norm, self.norm), **exec_weights(self.kv_proj, compute),
+                                 out_dtype=compute, compute_dtype=compute)
+        else:
+            if pre_norm is not None:
+                lat = ops.layer_norm(lat, pre_norm.weight, pre_norm.bias, pre_norm.eps)
+            kv = apply_linear(self.kv_proj, lat, norm=self.norm, out_dtype=compute, compute=compute)
         q = apply_linear(self.q_proj, self.query, out_dtype=compute, compute=compute)  # (Q, D), batch-invariant
         o_buf, o = ops.merge_heads_out(batch, Q, H, D // H, compute, lat.device)
         ops.attention(ops.heads_view(q, 1, Q, H), ops.heads_view(kv, batch, L, H, 0, D),
@@ -129,8 +140,8 @@ class CortexModel(nn.Module):
                       ops.heads_view(kv, 1, E, H, D, D), kv_offsets=offsets, out=o, batch=B)
         x = apply_linear(xa.out_proj, o_buf, residual=enc.latents, res_rows=L, out_dtype=torch.float32,
                          compute=compute)  # (B*L, D) fp32 residual stream
-        lat = enc.encode_rows(x, B)
-        return self.behavior_head.forward_rows(lat, B)
+        x = enc.encode_rows(x, B, final_norm=False)
+        return self.behavior_head.forward_rows(x, B, pre_norm=enc.final_norm)
 
 
 def _pack_events(flat_tokens: torch.Tensor, batch_indices: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:

@@ -106,11 +106,13 @@ class PerceiverEncoder(nn.Module):
         self.self_attn_blocks = nn.ModuleList([SelfAttentionBlock(config) for _ in range(config.num_layers)])
         self.final_norm = nn.LayerNorm(config.latent_dim)
 
-    def encode_rows(self, x: torch.Tensor, batch: int) -> torch.Tensor:
-        """Self-attention stack + final norm on the (B*L, D) residual after cross-attention."""
+    def encode_rows(self, x: torch.Tensor, batch: int, final_norm: bool = True) -> torch.Tensor:
+        """Self-attention stack (+ final norm) on the (B*L, D) residual after cross-attention."""
         L = self.config.num_latents
         for block in self.self_attn_blocks:
             x = block.forward_rows(x, batch, L)
+        if not final_norm:
+            return x
         return ops.layer_norm(x, self.final_norm.weight, self.final_norm.bias, self.final_norm.eps)
 
     def forward(self, tokens: torch.Tensor, token_mask: torch.Tensor | None = None) -> torch.Tensor:

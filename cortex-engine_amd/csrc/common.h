@@ -81,6 +81,24 @@ __host__ __device__ __forceinline__ int64_t cdiv(int64_t a, int64_t b) { return 
 // erf-form GELU, as torch.nn.GELU() with approximate='none': 0.5 x (1 + erf(x / sqrt 2)).
 __device__ __forceinline__ float gelu_erf(float x) { return 0.5f * x * (1.0f + erff(x * 0.70710678118654752440f)); }
 
+// Same GELU with erf from Abramowitz & Stegun, Handbook of Mathematical Functions,
+// eq. 7.1.26: erf(z) = 1 - (a1 t + a2 t^2 + a3 t^3 + a4 t^4 + a5 t^5) exp(-z^2),
+// t = 1 / (1 + p z), z >= 0, |error| <= 1.5e-7.  Used where the result is rounded
+// to bf16 (relative step 2^-8), so the approximation is far below the output
+// resolution; about a dozen VALU operations instead of the library's erff.
+__device__ __forceinline__ float gelu_erf_bf16out(float x) {
+  const float z = fabsf(x) * 0.70710678118654752440f;
+  const float t = __builtin_amdgcn_rcpf(1.0f + 0.3275911f * z);
+  float poly = 1.061405429f;
+  poly = poly * t - 1.453152027f;
+  poly = poly * t + 1.421413741f;
+  poly = poly * t - 0.284496736f;
+  poly = poly * t + 0.254829592f;
+  poly *= t;
+  const float e = 1.0f - poly * __expf(-z * z);
+  return 0.5f * x * (1.0f + copysignf(e, x));
+}
+
 }  // namespace cortex
 
 // ----------------------------------------------------------------------------

@@ -1,0 +1,44 @@
+// Arguments shared by the general and the fast-path GEMM kernels.
+#pragma once
+
+#include "common.h"
+
+namespace cortex {
+
+enum NormMode : int { NORM_NONE = 0, NORM_LAYER = 1, NORM_RMS = 2 };
+enum ActMode : int { ACT_NONE = 0, ACT_GELU = 1 };
+
+struct GemmArgs {
+  int64_t M, N, K;
+  const void* x;
+  int64_t ld_x;
+  int norm;
+  const float2* stats;
+  const void* gamma;
+  const void* beta;
+  int gamma_dtype;
+  const void* w;
+  int64_t ld_w;
+  const float* w_scale;
+  const void* bias;
+  int bias_dtype;
+  int act;
+  const void* res;
+  int res_dtype;
+  int64_t ld_res;
+  int64_t res_rows;
+  void* out;
+  int out_dtype;
+  int64_t ld_out;
+  int vec;  // 1: 16-byte aligned rows, vector loads allowed
+};
+
+// Fast path for aligned bf16-compute GEMMs (gemm_fast.hip).  Returns 1 when it
+// launched the kernel, 0 when the request is outside its specialisations (the
+// caller then uses the general kernel), or a negative status on a launch error.
+int try_gemm_fast(const GemmArgs& g, int x_dtype, int w_dtype, int w_layout, int compute, hipStream_t stream);
+
+// Pipelined bf16 x int8 path (gemm_pipe.hip), same return convention.
+int try_gemm_pipe(const GemmArgs& g, int x_dtype, int w_dtype, int w_layout, int compute, hipStream_t stream);
+
+}  // namespace cortex

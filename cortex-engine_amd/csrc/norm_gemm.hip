@@ -19,11 +19,9 @@
 #include <hip/hip_runtime.h>
 
 #include "common.h"
+#include "gemm.h"
 
 namespace cortex {
-
-enum NormMode : int { NORM_NONE = 0, NORM_LAYER = 1, NORM_RMS = 2 };
-enum ActMode : int { ACT_NONE = 0, ACT_GELU = 1 };
 
 __device__ __forceinline__ float load_f32(const void* p, int dtype, int64_t i) {
   if (dtype == DT_BF16) return (float)reinterpret_cast<const bf16*>(p)[i];
@@ -102,30 +100,7 @@ __global__ __launch_bounds__(256) void layer_norm_kernel(const TX* __restrict__ 
 // --------------------------------------------------------------------------
 // GEMM
 // --------------------------------------------------------------------------
-struct GemmArgs {
-  int64_t M, N, K;
-  const void* x;
-  int64_t ld_x;
-  int norm;
-  const float2* stats;
-  const void* gamma;
-  const void* beta;
-  int gamma_dtype;
-  const void* w;
-  int64_t ld_w;
-  const float* w_scale;
-  const void* bias;
-  int bias_dtype;
-  int act;
-  const void* res;
-  int res_dtype;
-  int64_t ld_res;
-  int64_t res_rows;
-  void* out;
-  int out_dtype;
-  int64_t ld_out;
-  int vec;  // 1: 16-byte aligned rows, vector loads allowed
-};
+
 
 template <class TC>
 struct TileCfg;
@@ -483,6 +458,9 @@ int cortex_norm_linear(int64_t M, int64_t N, int64_t K, int x_dtype, const void*
   const bool vec = ((uintptr_t)x % 16 == 0) && ((ld_x * xs) % 16 == 0) && ((uintptr_t)w % 16 == 0) &&
                    ((ld_w * ws) % 16 == 0) && (ws != 1 || ((uintptr_t)w % 8 == 0 && (ld_w % 8) == 0));
   g.vec = vec ? 1 : 0;
+  int fast = try_gemm_pipe(g, x_dtype, w_dtype, w_layout, compute, stream);
+  if (fast == 0) fast = try_gemm_fast(g, x_dtype, w_dtype, w_layout, compute, stream);
+  if (fast != 0) return fast > 0 ? OK : fast;
   if (compute == DT_BF16) {
     // fp32 weights are rounded to bf16 (RNE) while staged, i.e. W.to(bfloat16)
     if (x_dtype == DT_BF16) {

@@ -100,6 +100,22 @@ int cortex_layer_norm(int64_t M, int64_t K, int x_dtype, const void* x, int64_t 
                       const void* beta, int gamma_dtype, float eps, int out_dtype, void* out, int64_t ld_out,
                       hipStream_t stream);
 
+/* ---- a5/a8: LayerNorm rows to bf16 ----------------------------------------
+ * Replaces nn.LayerNorm feeding a bf16 linear (cortex/models/perceiver.py:67-68,
+ * 113,125,158; cortex/models/cortex.py:37), K in {256, 512, 768, 1024}:
+ *   y = LN1(x) (gamma1/beta1/eps1), then y = LN2(y) when gamma2 or beta2 is given;
+ *   written to out_bf16 (bf16) and/or out_f32.  fp32 x, gamma, beta (16-byte aligned). */
+int cortex_ln_rows(int64_t M, int64_t K, const float* x, int64_t ld_x, const float* gamma1, const float* beta1,
+                   float eps1, const float* gamma2, const float* beta2, float eps2, void* out_bf16, int64_t ld_bf16,
+                   float* out_f32, int64_t ld_f32, hipStream_t stream);
+
+/* ---- a7: dtype conversion ---------------------------------------------------
+ * out[i] = (out dtype) in[i]; int8 / f32 / bf16 / f16 in, f32 / bf16 out (bf16 by
+ * round-to-nearest-even).  Builds the bf16 execution image of INT8 weights, which is
+ * exact: every int8 value is a bf16 value (no reference counterpart; used by the
+ * linear layers of cortex/quantization/calibrate.py:170-235). */
+int cortex_convert(int in_dtype, const void* in, int out_dtype, void* out, int64_t n, hipStream_t stream);
+
 /* ---- a5/a6/a7: fused norm + linear -----------------------------------------
  * Replaces rms_norm_linear (cortex/kernels/fused_rmsnorm.py:239-301),
  * QuantizedLinear.forward (cortex/quantization/calibrate.py:225-228) and the
@@ -113,7 +129,8 @@ int cortex_layer_norm(int64_t M, int64_t K, int x_dtype, const void* x, int64_t 
  *   acc[m,n] = sum_k a[m,k] * W[n,k]   (fp32 accumulation on MFMA)
  *   y[m,n]   = act(acc*w_scale[n] + bias[n]) + residual[(m % res_rows), n]
  * W: int8 (N,K) (w_layout 0) with w_scale, or bf16/f32 in (N,K) (layout 0) or
- * (K,N) (layout 1, the rms_norm_linear weight).  act: 0 none, 1 erf-GELU.
+ * (K,N) (layout 1, the rms_norm_linear weight); a bf16 W may carry w_scale too
+ * (the exact bf16 image of an int8 weight).  act: 0 none, 1 erf-GELU.
  * res_rows 0 means M (ordinary residual); a smaller value broadcasts a
  * batch-invariant residual such as the learned latents. */
 int cortex_norm_linear(int64_t M, int64_t N, int64_t K, int x_dtype, const void* x, int64_t ld_x, int norm,

@@ -1,0 +1,173 @@
+"""LayerNorm row kernel, dtype conversion and the pipelined bf16-operand GEMM on the GPU.
+
+The LayerNorm rows (a5's norm half) are checked against torch's CPU LayerNorm in
+fp32 (fp32 output <= 2e-5 absolute at unit scale; bf16 output within one bf16
+rounding of the fp32 result).  The pipelined GEMM (a6/a7: bf16 rows x int8 or
+bf16 weight rows, per-channel scale, bias, GELU, fp32 residual) is checked
+against a float64 contraction of the same bf16/int8 operands, and the int8-widen
+and bf16-image weight forms are checked to agree with each other.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import cortex_oracle as O
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _bf16_ulp(x: torch.Tensor) -> torch.Tensor:
+    """Spacing of bf16 values at |x| (2^(e-7) for |x| in [2^e, 2^(e+1)))."""
+    e = torch.floor(torch.log2(x.abs().clamp_min(1e-30)))
+    return torch.pow(2.0, e - 7)
+
+
+@pytest.mark.parametrize("K", [256, 512, 768, 1024])
+@pytest.mark.parametrize("M", [1, 7, 8192])
+def test_ln_rows_single(M, K):
+    from cortex.kernels import ops
+
+    torch.manual_seed(K + M)
+    x = torch.randn(M, K) * 2.5 + 0.7
+    w, b = 1 + 0.2 * torch.randn(K), 0.2 * torch.randn(K)
+    ob, of = ops.ln_rows(x.to(DEV), (w.to(DEV), b.to(DEV), 1e-5), out_bf16=True, out_f32=True)
+    ref = F.layer_norm(x, (K,), w, b, 1e-5)
+    torch.testing.assert_close(of.cpu(), ref, rtol=0, atol=2e-5 * float(ref.abs().max()))
+    # bf16 output is the fp32 value rounded once: within one bf16 spacing of the exact result
+    err = (ob.float().cpu() - ref).abs()
+    assert bool((err <= _bf16_ulp(ref) + 2e-5 * float(ref.abs().max())).all())
+
+
+@pytest.mark.parametrize("K", [256, 512])
+def test_ln_rows_double(K):
+    """final_norm followed by the behaviour head's norm in one pass."""
+    from cortex.kernels import ops
+
+    torch.manual_seed(11)
+    M = 8192
+    x = torch.randn(M, K) * 4 - 1
+    w1, b1 = 1 + 0.3 * torch.randn(K), 0.3 * torch.randn(K)
+    w2, b2 = 1 + 0.3 * torch.randn(K), 0.3 * torch.randn(K)
+    of = ops.ln_rows(x.to(DEV), (w1.to(DEV), b1.to(DEV), 1e-5), (w2.to(DEV), b2.to(DEV), 1e-6),
+                     out_bf16=False, out_f32=True)
+    ref = F.layer_norm(F.layer_norm(x, (K,), w1, b1, 1e-5), (K,), w2, b2, 1e-6)
+    torch.testing.assert_close(of.cpu(), ref, rtol=0, atol=3e-5 * float(ref.abs().max()))
+
+
+def test_ln_rows_strided_rows():
+    """Rows with a leading stride larger than K (a column slice of a wider buffer)."""
+    from cortex.kernels import ops
+
+    torch.manual_seed(4)
+    big = torch.randn(300, 1024)
+    x = big[:, :512]
+    w, b = torch.randn(512), torch.randn(512)
+    of = ops.ln_rows(x.to(DEV), (w.to(DEV), b.to(DEV), 1e-5), out_bf16=False, out_f32=True)
+    torch.testing.assert_close(of.cpu(), F.layer_norm(x, (512,), w, b, 1e-5), rtol=0, atol=1e-4)
+
+
+@pytest.mark.parametrize("src", [torch.int8, torch.float32, torch.bfloat16])
+def test_convert_exact(src):
+    from cortex.kernels import ops
+
+    torch.manual_seed(1)
+    if src == torch.int8:
+        t = torch.randint(-127, 128, (2048, 512), dtype=torch.int8)
+    else:
+        t = (torch.randn(1001, 37) * 100).to(src)
+    for dst in (torch.bfloat16, torch.float32):
+        out = ops.convert(t.to(DEV), dst).cpu()
+        assert out.dtype == dst
+        assert torch.equal(out, t.to(dst)), (src, dst)  # RNE to bf16, exact widening
+
+
+def _operands(M, N, K, seed):
+    g = torch.Generator().manual_seed(seed)
+    a = torch.randn(M, K, generator=g).bfloat16()
+    w = torch.randn(N, K, generator=g) * 0.05
+    q, s = O.quantize_int8(w.numpy())
+    return a, torch.from_numpy(q), torch.from_numpy(s)
+
+
+def _ref(a, q, s, bias=None, act=None, res=None, res_rows=0):
+    y = a.double() @ q.double().T * s.double()
+    if bias is not None:
+        y = y + bias.double()
+    if act == "gelu":
+        y = F.gelu(y)
+    if res is not None:
+        r = res.double()
+        if res_rows:
+            r = r.repeat(a.shape[0] // res_rows, 1)
+        y = y + r
+    return y
+
+
+@pytest.mark.parametrize("M,N,K", [(8192, 1536, 512), (8192, 2048, 512), (8192, 512, 2048), (8192, 512, 512),
+                                   (16384, 1024, 512), (300, 512, 512), (1, 1024, 512), (130, 200, 64)])
+def test_pipe_gemm_int8_and_image(M, N, K):
+    """int8 weights widened in the kernel and their bf16 image agree, and both match fp64."""
+    from cortex.kernels import ops
+
+    a, q, s = _operands(M, N, K, seed=M + N + K)
+    ad, qd, sd = a.to(DEV), q.to(DEV), s.to(DEV)
+    y8 = ops.norm_linear(ad, weight_int8=qd, weight_scale=sd, out_dtype=torch.float32)
+    img = ops.convert(qd, torch.bfloat16)
+    yi = ops.norm_linear(ad, weight=img, weight_scale=sd, out_dtype=torch.float32)
+    ref = _ref(a, q, s)
+    scale = float(ref.abs().max())
+    assert float((y8.cpu().double() - ref).abs().max()) <= 1e-5 * scale
+    assert float((yi.cpu().double() - ref).abs().max()) <= 1e-5 * scale
+    torch.testing.assert_close(yi, y8, rtol=0, atol=2e-6 * scale)
+
+
+@pytest.mark.parametrize("wform", ["int8", "image"])
+def test_pipe_gemm_gelu_bf16_out(wform):
+    """MLP-up shape: GELU epilogue, bf16 output within bf16 rounding of the fp64 result."""
+    from cortex.kernels import ops
+
+    M, N, K = 8192, 2048, 512
+    a, q, s = _operands(M, N, K, seed=5)
+    ad, qd, sd = a.to(DEV), q.to(DEV), s.to(DEV)
+    w = {"weight_int8": qd} if wform == "int8" else {"weight": ops.convert(qd, torch.bfloat16)}
+    y = ops.norm_linear(ad, **w, weight_scale=sd, act="gelu", out_dtype=torch.bfloat16).cpu().double()
+    ref = _ref(a, q, s, act="gelu")
+    err = (y - ref).abs()
+    assert bool((err <= _bf16_ulp(ref) + 1e-5 * float(ref.abs().max())).all())
+
+
+def test_pipe_gemm_bias_and_broadcast_residual():
+    """Bias epilogue, and the latents residual broadcast every 256 rows into fp32 output."""
+    from cortex.kernels import ops
+
+    M, N, K, L = 32 * 256, 512, 512, 256
+    a, q, s = _operands(M, N, K, seed=8)
+    bias = torch.randn(N)
+    lat = torch.randn(L, N)
+    ad, qd, sd = a.to(DEV), q.to(DEV), s.to(DEV)
+    img = ops.convert(qd, torch.bfloat16)
+    y = ops.norm_linear(ad, weight=img, weight_scale=sd, bias=bias.to(DEV), out_dtype=torch.float32).cpu()
+    ref = _ref(a, q, s, bias=bias)
+    assert float((y.double() - ref).abs().max()) <= 1e-5 * float(ref.abs().max())
+    y2 = ops.norm_linear(ad, weight=img, weight_scale=sd, residual=lat.to(DEV), res_rows=L,
+                         out_dtype=torch.float32).cpu()
+    ref2 = _ref(a, q, s, res=lat, res_rows=L)
+    assert float((y2.double() - ref2).abs().max()) <= 1e-5 * float(ref2.abs().max())
+
+
+def test_pipe_gemm_float_weight_image():
+    """A float nn.Linear weight rounded to bf16 (no scale), residual into fp32 output."""
+    from cortex.kernels import ops
+
+    M, N, K = 4096, 512, 2048
+    g = torch.Generator().manual_seed(3)
+    a = torch.randn(M, K, generator=g).bfloat16()
+    w = (torch.randn(N, K, generator=g) * 0.02).bfloat16()
+    res = torch.randn(M, N, generator=g)
+    y = ops.norm_linear(a.to(DEV), weight=w.to(DEV), residual=res.to(DEV), out_dtype=torch.float32).cpu()
+    ref = res.double() + a.double() @ w.double().T
+    assert float((y.double() - ref).abs().max()) <= 1e-5 * float(ref.abs().max())
