@@ -26,7 +26,7 @@ from torch import nn
 
 from cortex.kernels import ops
 from cortex.kernels.pack import pack_events as _device_pack_events
-from cortex.models._layers import apply_linear, exec_weights, ln_rows_ok, normalize_bf16
+from cortex.models._layers import apply_linear, batch_invariant, exec_weights, ln_rows_ok, normalize_bf16
 from cortex.models.config import CortexConfig
 from cortex.models.perceiver import PerceiverEncoder
 from cortex.models.tokenizer import SpikeTokenizer
@@ -65,7 +65,8 @@ class BehaviorDecoder(nn.Module):
             if pre_norm is not None:
                 lat = ops.layer_norm(lat, pre_norm.weight, pre_norm.bias, pre_norm.eps)
             kv = apply_linear(self.kv_proj, lat, norm=self.norm, out_dtype=compute, compute=compute)
-        q = apply_linear(self.q_proj, self.query, out_dtype=compute, compute=compute)  # (Q, D), batch-invariant
+        q = batch_invariant(self, f"q_{compute}", [self.query], [self.q_proj],  # (Q, D), batch-invariant
+                            lambda: apply_linear(self.q_proj, self.query, out_dtype=compute, compute=compute))
         o_buf, o = ops.merge_heads_out(batch, Q, H, D // H, compute, lat.device)
         ops.attention(ops.heads_view(q, 1, Q, H), ops.heads_view(kv, batch, L, H, 0, D),
                       ops.heads_view(kv, batch, L, H, D, D), out=o, batch=batch)

@@ -15,7 +15,7 @@ import torch
 from torch import nn
 
 from cortex.kernels import ops
-from cortex.models._layers import apply_linear
+from cortex.models._layers import apply_linear, batch_invariant
 from cortex.models.config import CortexConfig
 
 
@@ -36,8 +36,12 @@ class CrossAttentionBlock(nn.Module):
         self.norm_kv = nn.LayerNorm(config.hidden_dim)
 
     def project_queries(self, latents: torch.Tensor, compute: torch.dtype) -> torch.Tensor:
-        """``q_proj(norm_q(latents))`` for (L, D) batch-invariant latents -> (L, D)."""
-        return apply_linear(self.q_proj, latents, norm=self.norm_q, out_dtype=compute, compute=compute)
+        """``q_proj(norm_q(latents))`` for (L, D) batch-invariant latents -> (L, D).
+
+        Depends on parameters only, so it is computed once per parameter state."""
+        return batch_invariant(
+            self, f"q_{compute}", [latents], [self.q_proj, self.norm_q],
+            lambda: apply_linear(self.q_proj, latents, norm=self.norm_q, out_dtype=compute, compute=compute))
 
     def forward(self, latents: torch.Tensor, tokens: torch.Tensor,
                 token_mask: torch.Tensor | None = None) -> torch.Tensor:

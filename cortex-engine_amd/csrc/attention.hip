@@ -22,29 +22,11 @@
 // Dao 2023).
 #include <hip/hip_runtime.h>
 
+#include "attention.h"
 #include "common.h"
 
 namespace cortex {
 
-struct AttnArgs {
-  int64_t B, H, Lq, Lk, Dh;
-  const void* q;
-  int64_t q_sb, q_sh, q_sl;
-  const void* k;
-  int64_t k_sb, k_sh, k_sl;
-  const void* v;
-  int64_t v_sb, v_sh, v_sl;
-  const int64_t* kv_off;  // (B+1) CSR row offsets (row index scaled by k_sl / v_sl)
-  const int64_t* kv_len;  // (B,) valid keys per sample
-  const uint8_t* key_mask;
-  int64_t km_sb;
-  const uint8_t* block_mask;
-  int64_t bm_sb, n_qt, n_kt, block_l, block_e;
-  float scale_log2;
-  void* out;
-  int64_t o_sb, o_sh, o_sl;
-  int vec;
-};
 
 constexpr int ATT_KT = 64;       // keys per tile
 constexpr int ATT_QW = 16;       // queries per wavefront
@@ -353,6 +335,8 @@ extern "C" int cortex_attention(int dtype, int64_t B, int64_t H, int64_t Lq, int
   for (const void* p : {q, k, v}) vec = vec && ((uintptr_t)p % 16 == 0);
   for (int64_t s : {q_sb, q_sh, q_sl, k_sb, k_sh, k_sl, v_sb, v_sh, v_sl}) vec = vec && ((s * es) % 16 == 0);
   a.vec = vec ? 1 : 0;
+  const int fast = try_attention_fast(a, dtype, stream);
+  if (fast != 0) return fast > 0 ? OK : fast;
   if (dtype == DT_BF16) return launch_attn<bf16>(a, stream);
   if (dtype == DT_F32) return launch_attn<float>(a, stream);
   set_error("cortex_attention: unsupported dtype %d (bf16 or f32)", dtype);

@@ -356,6 +356,71 @@ static int elem_size(int dt) {
   return 0;
 }
 
+// --------------------------------------------------------------------------
+// Narrow outputs (N <= 8, e.g. the behaviour head's 512 -> 1 projection): one
+// wavefront per row, lanes striding over K, fp32 accumulation.  Operands are
+// rounded to bf16 first under bf16 compute, as the MFMA kernels stage them.
+// --------------------------------------------------------------------------
+constexpr int ROWDOT_MAX_N = 8;
+
+template <class TX, class TW>
+__global__ __launch_bounds__(256) void rowdot_kernel(GemmArgs g, int bf16c) {
+  const int lane = threadIdx.x & 63;
+  const int64_t m = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (m >= g.M) return;
+  const TX* xr = reinterpret_cast<const TX*>(g.x) + m * g.ld_x;
+  const TW* w = reinterpret_cast<const TW*>(g.w);
+  float acc[ROWDOT_MAX_N];
+#pragma unroll
+  for (int n = 0; n < ROWDOT_MAX_N; ++n) acc[n] = 0.0f;
+  for (int64_t k = lane; k < g.K; k += 64) {
+    float xv = to_f32(xr[k]);
+    if (bf16c) xv = (float)(bf16)xv;
+#pragma unroll
+    for (int n = 0; n < ROWDOT_MAX_N; ++n) {
+      if (n < g.N) {
+        float wv = to_f32(w[n * g.ld_w + k]);
+        if (bf16c) wv = (float)(bf16)wv;
+        acc[n] = fmaf(xv, wv, acc[n]);
+      }
+    }
+  }
+  const int64_t rr = g.res_rows > 0 ? m % g.res_rows : m;
+#pragma unroll
+  for (int n = 0; n < ROWDOT_MAX_N; ++n) {
+    if (n >= g.N) break;
+    float v = wave_sum(acc[n]);
+    if (lane != 0) continue;
+    if (g.w_scale) v *= g.w_scale[n];
+    if (g.bias) v += load_f32(g.bias, g.bias_dtype, n);
+    if (g.act == ACT_GELU) v = gelu_erf(v);
+    if (g.res) v += load_f32(g.res, g.res_dtype, rr * g.ld_res + n);
+    store_f32(g.out, g.out_dtype, m * g.ld_out + n, v);
+  }
+}
+
+template <class TX, class TW>
+static int launch_rowdot(const GemmArgs& g, int bf16c, hipStream_t stream) {
+  hipLaunchKernelGGL((rowdot_kernel<TX, TW>), dim3((unsigned)cdiv(g.M, 4)), dim3(256), 0, stream, g, bf16c);
+  CORTEX_CHECK_LAUNCH("rowdot_kernel");
+  return OK;
+}
+
+static int try_rowdot(const GemmArgs& g, int x_dtype, int w_dtype, int w_layout, int compute, hipStream_t stream) {
+  if (g.N > ROWDOT_MAX_N || g.norm != NORM_NONE || w_layout != 0 || cdiv(g.M, 4) > 0x7fffffffLL) return 0;
+  const int bf16c = compute == DT_BF16 ? 1 : 0;
+  if (!bf16c && (x_dtype == DT_BF16 || w_dtype == DT_BF16)) return 0;
+  int r = 1;
+  if (x_dtype == DT_BF16 && w_dtype == DT_BF16) r = launch_rowdot<bf16, bf16>(g, bf16c, stream);
+  else if (x_dtype == DT_BF16 && w_dtype == DT_I8) r = launch_rowdot<bf16, int8_t>(g, bf16c, stream);
+  else if (x_dtype == DT_BF16 && w_dtype == DT_F32) r = launch_rowdot<bf16, float>(g, bf16c, stream);
+  else if (x_dtype == DT_F32 && w_dtype == DT_BF16) r = launch_rowdot<float, bf16>(g, bf16c, stream);
+  else if (x_dtype == DT_F32 && w_dtype == DT_I8) r = launch_rowdot<float, int8_t>(g, bf16c, stream);
+  else if (x_dtype == DT_F32 && w_dtype == DT_F32) r = launch_rowdot<float, float>(g, bf16c, stream);
+  else return 0;
+  return r == OK ? 1 : r;
+}
+
 extern "C" {
 
 int cortex_row_stats(int64_t M, int64_t K, int x_dtype, const void* x, int64_t ld_x, int norm, float eps,
@@ -458,7 +523,8 @@ int cortex_norm_linear(int64_t M, int64_t N, int64_t K, int x_dtype, const void*
   const bool vec = ((uintptr_t)x % 16 == 0) && ((ld_x * xs) % 16 == 0) && ((uintptr_t)w % 16 == 0) &&
                    ((ld_w * ws) % 16 == 0) && (ws != 1 || ((uintptr_t)w % 8 == 0 && (ld_w % 8) == 0));
   g.vec = vec ? 1 : 0;
-  int fast = try_gemm_pipe(g, x_dtype, w_dtype, w_layout, compute, stream);
+  int fast = try_rowdot(g, x_dtype, w_dtype, w_layout, compute, stream);
+  if (fast == 0) fast = try_gemm_pipe(g, x_dtype, w_dtype, w_layout, compute, stream);
   if (fast == 0) fast = try_gemm_fast(g, x_dtype, w_dtype, w_layout, compute, stream);
   if (fast != 0) return fast > 0 ? OK : fast;
   if (compute == DT_BF16) {

@@ -134,3 +134,22 @@ def test_invalid_token_index_sets_error_flag():
     with torch.no_grad():
         out = model(nid, tb, val, bidx, batch_size=2, err_flag=err)["behavior"]
     assert torch.isfinite(out).all() and int(err.item()) & 1
+
+
+def test_batch_invariant_queries_follow_parameter_updates():
+    """The cached latent/behaviour query projections are rebuilt when a parameter changes in place."""
+    model = _int8(_model("xs", "bfloat16"), [torch.from_numpy(a).to(DEV) for a in _config3_inputs(2, 64)])
+    inputs = [torch.from_numpy(a).to(DEV) for a in _config3_inputs(3, 80, seed=21)]
+    with torch.no_grad():
+        a = model(*inputs, batch_size=3)["behavior"].clone()
+        b = model(*inputs, batch_size=3)["behavior"].clone()
+        torch.testing.assert_close(a, b, rtol=0, atol=0)
+        model.encoder.latents.mul_(1.5)
+        model.behavior_head.query.add_(0.05)
+        c = model(*inputs, batch_size=3)["behavior"].clone()
+        model.encoder.__dict__.pop("_cortex_invariant", None)
+        model.encoder.cross_attn.__dict__.pop("_cortex_invariant", None)
+        model.behavior_head.__dict__.pop("_cortex_invariant", None)
+        d = model(*inputs, batch_size=3)["behavior"].clone()
+    assert not torch.equal(a, c)
+    torch.testing.assert_close(c, d, rtol=0, atol=0)

@@ -171,3 +171,35 @@ def test_pipe_gemm_float_weight_image():
     y = ops.norm_linear(a.to(DEV), weight=w.to(DEV), residual=res.to(DEV), out_dtype=torch.float32).cpu()
     ref = res.double() + a.double() @ w.double().T
     assert float((y.double() - ref).abs().max()) <= 1e-5 * float(ref.abs().max())
+
+
+@pytest.mark.parametrize("N", [1, 2, 8])
+@pytest.mark.parametrize("form", ["bf16x_bf16w", "bf16x_int8w", "f32x_f32w_fp32", "f32x_f32w_bf16"])
+def test_narrow_output_rows(N, form):
+    """N <= 8 outputs (the behaviour head's 512 -> 1 projection) on the row-dot kernel."""
+    from cortex.kernels import ops
+
+    g = torch.Generator().manual_seed(N)
+    M, K = 64, 512
+    x = torch.randn(M, K, generator=g)
+    w = torch.randn(N, K, generator=g) * 0.05
+    res = torch.randn(M, N, generator=g)
+    if form == "bf16x_bf16w":
+        xb, wb = x.bfloat16(), w.bfloat16()
+        y = ops.norm_linear(xb.to(DEV), weight=wb.to(DEV), residual=res.to(DEV), out_dtype=torch.float32)
+        ref = xb.double() @ wb.double().T + res.double()
+    elif form == "bf16x_int8w":
+        xb = x.bfloat16()
+        q, s = O.quantize_int8(w.numpy())
+        q, s = torch.from_numpy(q), torch.from_numpy(s)
+        y = ops.norm_linear(xb.to(DEV), weight_int8=q.to(DEV), weight_scale=s.to(DEV), out_dtype=torch.float32)
+        ref = xb.double() @ q.double().T * s.double()
+    elif form == "f32x_f32w_fp32":
+        y = ops.norm_linear(x.to(DEV), weight=w.to(DEV), act="gelu", out_dtype=torch.float32,
+                            compute_dtype=torch.float32)
+        ref = torch.nn.functional.gelu(x.double() @ w.double().T)
+    else:  # fp32 operands under bf16 compute: both rounded to bf16 first
+        y = ops.norm_linear(x.to(DEV), weight=w.to(DEV), out_dtype=torch.float32, compute_dtype=torch.bfloat16)
+        ref = x.bfloat16().double() @ w.bfloat16().double().T
+    assert y.shape == (M, N)
+    assert float((y.cpu().double() - ref).abs().max()) <= 1e-5 * float(ref.abs().max())
