@@ -38,6 +38,9 @@ struct GemmArgs {
 // caller then uses the general kernel), or a negative status on a launch error.
 int try_gemm_fast(const GemmArgs& g, int x_dtype, int w_dtype, int w_layout, int compute, hipStream_t stream);
 
+// bf16 x bf16 path with a register epilogue (gemm_bf16.hip), same return convention.
+int try_gemm_bf16(const GemmArgs& g, int x_dtype, int w_dtype, int w_layout, int compute, hipStream_t stream);
+
 // Pipelined bf16 x int8 path (gemm_pipe.hip), same return convention.
 int try_gemm_pipe(const GemmArgs& g, int x_dtype, int w_dtype, int w_layout, int compute, hipStream_t stream);
 

@@ -1,0 +1,371 @@
+// bf16 x bf16 GEMM for gfx950 with direct-to-LDS operand streaming and a
+// register epilogue:
+//
+//   C[m, n] = epi( sum_k A[m, k] * W[n, k] ),  A (M, K) bf16 rows, W (N, K) bf16 rows
+//   epi: * w_scale[n] (+ bias[n]) (-> erf-GELU) -> bf16 | fp32, or (+ fp32 residual) -> fp32
+//
+// W is the bf16 execution image of a QuantizedLinear's int8 weight (exact) with the
+// per-channel scale applied in the epilogue, or a float weight rounded to bf16.
+//
+// Operands travel global -> LDS with global_load_lds_dwordx4 (1 KiB per wavefront
+// instruction, no VGPRs held while in flight) through a STAGES-deep ring; a step
+// waits only for its own transfers (vmcnt) plus a raw s_barrier.
+//
+// LDS rows hold 64 bf16 of K (128 bytes); the 16-byte chunk c of row r is stored at
+// c ^ sw(r), with sw chosen so that the 16 rows read by one MFMA fragment cover all
+// 16 four-bank groups.
+//
+// The MFMA computes C^T tiles (A operand = W rows, B operand = A rows) with the W
+// rows of two adjacent tiles interleaved, so a lane ends up with 8 CONSECUTIVE
+// output columns of one row: the epilogue reads scale, bias and residual as float4
+// pairs and writes 16- or 32-byte vectors straight from the accumulators, without
+// an LDS round trip or a workgroup barrier.
+#include <hip/hip_runtime.h>
+
+#include "common.h"
+#include "gemm.h"
+
+namespace cortex {
+
+namespace {
+
+template <int n>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(n >= 0 && n < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((n & 15) | 0x70 | 0xF00 | ((n >> 4) << 14));
+}
+
+template <int BM_, int BN_, int STAGES_, int WM_, int WN_>
+struct BTile {
+  static constexpr int BM = BM_, BN = BN_, BK = 64, STAGES = STAGES_, WM = WM_, WN = WN_;
+  static constexpr int WAVES = WM * WN, THREADS = 64 * WAVES;
+  static constexpr int TM = BM / WM / 16, TN = BN / WN / 16;  // 16x16 tiles per wavefront
+  static constexpr int A_STAGE = BM * 128, W_STAGE = BN * 128;  // bytes (rows of 64 bf16)
+  static constexpr int A_BLOCKS = A_STAGE / 1024 / WAVES, W_BLOCKS = W_STAGE / 1024 / WAVES;
+  static constexpr int PER = A_BLOCKS + W_BLOCKS;              // transfers per wavefront per step
+  static constexpr int LDS = STAGES * (A_STAGE + W_STAGE);
+  static_assert(A_STAGE % (1024 * WAVES) == 0 && W_STAGE % (1024 * WAVES) == 0, "transfer split");
+  static_assert(TM >= 1 && TN >= 2 && TN % 2 == 0 && STAGES >= 2, "shape");
+  static_assert(PER * (STAGES - 1) < 64, "vmcnt range");
+};
+
+// 16-byte chunk swizzles of the 128-byte LDS rows.  A fragments read 16 consecutive
+// rows; W fragments read rows 8q + 4jj + i (q, i in 0..3) -- see the column order
+// below.  Each swizzle puts its fragment's 16 rows into the 16 distinct (row parity,
+// chunk) four-bank groups.
+__device__ __forceinline__ int swz_a(int r) { return (r >> 1) & 7; }
+__device__ __forceinline__ int swz_w(int r) { return ((r >> 1) & 1) | ((r >> 2) & 6); }
+
+// Column order.  W fragment row rho (0..15) of tile 2p + jj of a wavefront holds
+// output column 32 p + 8 (rho / 4) + 4 jj + rho % 4, so that the accumulators of
+// tiles 2p and 2p+1 give lane group g4 the 8 consecutive columns 32 p + 8 g4 .. +7.
+__device__ __forceinline__ int wrow_of(int p, int jj, int rho) { return 32 * p + 8 * (rho >> 2) + 4 * jj + (rho & 3); }
+
+template <class TL, int ACT, bool RES, class TOUT>
+__global__ __launch_bounds__(TL::THREADS) void gemm_bf16_kernel(GemmArgs g) {
+  constexpr int BM = TL::BM, BN = TL::BN, TM = TL::TM, TN = TL::TN, S = TL::STAGES;
+  constexpr int AB = TL::A_BLOCKS, WB = TL::W_BLOCKS, PER = TL::PER;
+  // bf16 output: interleaved W rows, 8 consecutive columns (16 bytes) per lane;
+  // fp32 output: natural order, 4 consecutive columns (16 bytes) per lane and tile.
+  constexpr bool IL = sizeof(TOUT) == 2;
+  __shared__ __attribute__((aligned(1024))) unsigned char smem[TL::LDS];
+
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int wm = wid / TL::WN, wn = wid % TL::WN;
+  const int nbx = gridDim.x, total = gridDim.x * gridDim.y;
+  int id = blockIdx.x + nbx * blockIdx.y;
+  if ((total & 7) == 0) id = (id & 7) * (total >> 3) + (id >> 3);  // contiguous tiles per XCD
+  const int m0 = (id / nbx) * BM, n0 = (id % nbx) * BN;
+  const int M = (int)g.M, N = (int)g.N, K = (int)g.K;
+  const bf16* __restrict__ A = reinterpret_cast<const bf16*>(g.x);
+  const bf16* __restrict__ W = reinterpret_cast<const bf16*>(g.w);
+
+  // Global source of each of this lane's transfers (K offset added per step).  Lane i
+  // of a transfer writes LDS bytes [16 i, 16 i + 16) of its 1 KiB block: row i / 8,
+  // stored chunk i % 8, which holds logical chunk (i % 8) ^ swizzle(row).
+  const bf16* a_src[AB];
+#pragma unroll
+  for (int i = 0; i < AB; ++i) {
+    const int r = (wid * AB + i) * 8 + (lane >> 3);
+    a_src[i] = A + (int64_t)min(m0 + r, M - 1) * g.ld_x + ((lane & 7) ^ swz_a(r)) * 8;
+  }
+  const bf16* w_src[WB];
+#pragma unroll
+  for (int i = 0; i < WB; ++i) {
+    const int r = (wid * WB + i) * 8 + (lane >> 3);
+    w_src[i] = W + (int64_t)min(n0 + r, N - 1) * g.ld_w + ((lane & 7) ^ (IL ? swz_w(r) : swz_a(r))) * 8;
+  }
+  auto a_stage = [&](int s) { return smem + s * TL::A_STAGE; };
+  auto w_stage = [&](int s) { return smem + S * TL::A_STAGE + s * TL::W_STAGE; };
+  auto issue = [&](int kt) {
+    const int s = kt % S, k0 = kt * TL::BK;
+#pragma unroll
+    for (int i = 0; i < AB; ++i)
+      __builtin_amdgcn_global_load_lds(static_cast<const void*>(a_src[i] + k0),
+                                       static_cast<void*>(a_stage(s) + (wid * AB + i) * 1024), 16, 0, 0);
+#pragma unroll
+    for (int i = 0; i < WB; ++i)
+      __builtin_amdgcn_global_load_lds(static_cast<const void*>(w_src[i] + k0),
+                                       static_cast<void*>(w_stage(s) + (wid * WB + i) * 1024), 16, 0, 0);
+  };
+
+  f32x4 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) acc[i][j] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+
+  const int fr = lane & 15, g4 = lane >> 4;
+  const int wrow = wm * (BM / TL::WM), wcol = wn * (BN / TL::WN);
+  // fragment-read byte offsets inside a stage (row base) and the row swizzles
+  int a_off[TM], w_off[TN], a_sw[TM], w_sw[TN];
+#pragma unroll
+  for (int t = 0; t < TM; ++t) {
+    const int r = wrow + t * 16 + fr;
+    a_off[t] = r * 128;
+    a_sw[t] = swz_a(r);
+  }
+#pragma unroll
+  for (int t = 0; t < TN; ++t) {
+    const int r = wcol + (IL ? wrow_of(t >> 1, t & 1, fr) : t * 16 + fr);
+    w_off[t] = r * 128;
+    w_sw[t] = IL ? swz_w(r) : swz_a(r);
+  }
+  auto read_frags = [&](int stage, int ks, bf16x8 (&af)[TM], bf16x8 (&wf)[TN]) {
+    const unsigned char* as = a_stage(stage);
+    const unsigned char* ws = w_stage(stage);
+#pragma unroll
+    for (int t = 0; t < TM; ++t)
+      af[t] = *reinterpret_cast<const bf16x8*>(as + a_off[t] + (((ks * 4 + g4) ^ a_sw[t]) << 4));
+#pragma unroll
+    for (int t = 0; t < TN; ++t)
+      wf[t] = *reinterpret_cast<const bf16x8*>(ws + w_off[t] + (((ks * 4 + g4) ^ w_sw[t]) << 4));
+  };
+  auto mma = [&](const bf16x8 (&af)[TM], const bf16x8 (&wf)[TN]) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf[j], af[i], acc[i][j], 0, 0, 0);
+  };
+  const int nk = K / TL::BK;
+
+  // The residual tile is fetched into registers before the main loop, so its latency
+  // hides behind the MFMAs instead of stalling the epilogue.
+  const float* res = reinterpret_cast<const float*>(g.res);
+  const int res_rows = g.res_rows > 0 ? (int)g.res_rows : M;
+  float4 rv[RES ? TM : 1][RES ? TN : 1];
+  if constexpr (RES && !IL) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      const int m = min(m0 + wrow + i * 16 + fr, M - 1);
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const int n = min(n0 + wcol + 16 * j + 4 * g4, N - 4);
+        rv[i][j] = *reinterpret_cast<const float4*>(res + (int64_t)(m % res_rows) * g.ld_res + n);
+      }
+    }
+  }
+
+  // Every stage of the ring is in flight at once; a stage is refilled as soon as all
+  // wavefronts hold its last fragments in registers.  Fragments are double-buffered
+  // in registers, so the LDS reads of the next K sub-step overlap the MFMAs.
+#pragma unroll
+  for (int p = 0; p < S; ++p)
+    if (p < nk) issue(p);
+  // wait until this wave's transfers of step j landed, steps up to `last` being issued
+  auto wait_step = [&](int j, int last) {
+    const int ahead = min(nk - 1, last) - j;  // steps issued after j
+    if constexpr (S >= 3) {
+      if (ahead >= 2)
+        wait_vm<2 * PER>();
+      else if (ahead == 1)
+        wait_vm<PER>();
+      else
+        wait_vm<0>();
+    } else {
+      if (ahead >= 1)
+        wait_vm<PER>();
+      else
+        wait_vm<0>();
+    }
+  };
+  bf16x8 af0[TM], wf0[TN], af1[TM], wf1[TN];
+  wait_step(0, S - 1);
+  __builtin_amdgcn_s_barrier();
+  read_frags(0, 0, af0, wf0);
+  for (int kt = 0; kt < nk; ++kt) {
+    const int st = kt % S;
+    read_frags(st, 1, af1, wf1);
+    mma(af0, wf0);
+    if (kt + 1 < nk) {
+      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's reads of stage st are in registers
+      wait_step(kt + 1, kt + S - 1);
+      __builtin_amdgcn_s_barrier();        // all waves done with stage st; step kt+1 visible
+      if (kt + S < nk) issue(kt + S);      // refill stage st
+      read_frags((kt + 1) % S, 0, af0, wf0);
+    }
+    mma(af1, wf1);
+  }
+
+  // ---- epilogue from registers.  Row m0 + wrow + 16 i + fr; columns
+  //   IL:  tiles 2p, 2p+1 -> n0 + wcol + 32 p + 8 g4 .. +7
+  //   !IL: tile j         -> n0 + wcol + 16 j + 4 g4 .. +3
+  const float* bias = reinterpret_cast<const float*>(g.bias);
+  TOUT* out = reinterpret_cast<TOUT*>(g.out);
+  constexpr int NV = IL ? 8 : 4;           // consecutive columns per lane and group
+  constexpr int NG = IL ? TN / 2 : TN;     // column groups per lane
+#pragma unroll
+  for (int p = 0; p < NG; ++p) {
+    const int n = n0 + wcol + (IL ? 32 * p + 8 * g4 : 16 * p + 4 * g4);
+    if (n >= N) continue;  // N % 8 == 0: a lane's columns are all in or all out
+    float sc[NV], bi[NV];
+#pragma unroll
+    for (int e = 0; e < NV; ++e) {
+      sc[e] = 1.0f;
+      bi[e] = 0.0f;
+    }
+#pragma unroll
+    for (int h = 0; h < NV / 4; ++h) {
+      if (g.w_scale) {
+        const float4 s4 = *reinterpret_cast<const float4*>(g.w_scale + n + 4 * h);
+        sc[4 * h] = s4.x; sc[4 * h + 1] = s4.y; sc[4 * h + 2] = s4.z; sc[4 * h + 3] = s4.w;
+      }
+      if (bias) {
+        const float4 b4 = *reinterpret_cast<const float4*>(bias + n + 4 * h);
+        bi[4 * h] = b4.x; bi[4 * h + 1] = b4.y; bi[4 * h + 2] = b4.z; bi[4 * h + 3] = b4.w;
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      const int m = m0 + wrow + i * 16 + fr;
+      if (m >= M) continue;
+      float v[NV];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        if constexpr (IL) {
+          v[r] = acc[i][2 * p][r] * sc[r] + bi[r];
+          v[4 + r] = acc[i][2 * p + 1][r] * sc[4 + r] + bi[4 + r];
+        } else {
+          v[r] = acc[i][p][r] * sc[r] + bi[r];
+        }
+      }
+      if (ACT == ACT_GELU) {
+#pragma unroll
+        for (int e = 0; e < NV; ++e) v[e] = sizeof(TOUT) == 2 ? gelu_erf_bf16out(v[e]) : gelu_erf(v[e]);
+      }
+      if constexpr (RES && !IL) {
+        const float4 x = rv[i][p];
+        v[0] += x.x; v[1] += x.y; v[2] += x.z; v[3] += x.w;
+      }
+      TOUT* op = out + (int64_t)m * g.ld_out + n;
+      if constexpr (sizeof(TOUT) == 2) {
+        bf16x8 o;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[e] = (bf16)v[e];
+        *reinterpret_cast<bf16x8*>(op) = o;
+      } else {
+#pragma unroll
+        for (int h = 0; h < NV / 4; ++h)
+          reinterpret_cast<float4*>(op)[h] = make_float4(v[4 * h], v[4 * h + 1], v[4 * h + 2], v[4 * h + 3]);
+      }
+    }
+  }
+}
+
+template <class TL, int ACT, bool RES, class TOUT>
+int launch(const GemmArgs& g, hipStream_t stream) {
+  const int64_t gy = cdiv(g.M, TL::BM), gx = cdiv(g.N, TL::BN);
+  if (gy > 65535 || gx * gy > 0x7fffffffLL) return 0;
+  hipLaunchKernelGGL((gemm_bf16_kernel<TL, ACT, RES, TOUT>), dim3((unsigned)gx, (unsigned)gy), dim3(TL::THREADS), 0,
+                     stream, g);
+  CORTEX_CHECK_LAUNCH("gemm_bf16_kernel");
+  return 1;
+}
+
+using B128x128s2 = BTile<128, 128, 2, 2, 2>;
+using B128x128s3 = BTile<128, 128, 3, 2, 2>;
+using B256x128s2 = BTile<256, 128, 2, 4, 2>;
+using B128x256s2 = BTile<128, 256, 2, 2, 4>;
+using B256x256s2 = BTile<256, 256, 2, 4, 2>;
+using B64x128s2 = BTile<64, 128, 2, 1, 2>;
+
+int bf16_tile() {
+  static int v = [] {
+    const char* s = getenv("CORTEX_BF16_TILE");
+    return s ? atoi(s) : -1;
+  }();
+  return v;
+}
+
+template <int ACT, bool RES, class TOUT>
+int dispatch(const GemmArgs& g, hipStream_t stream) {
+  int t = bf16_tile();
+  if (t < 0) {
+    // 256x256 tiles halve the operand traffic per MFMA; take them while they still
+    // give at least three quarters of a workgroup per CU
+    const int64_t big = cdiv(g.M, 256) * cdiv(g.N, 256);
+    t = big >= 192 ? 4 : 0;
+  }
+  switch (t) {
+    case 1:
+      return launch<B128x128s3, ACT, RES, TOUT>(g, stream);
+    case 2:
+      return launch<B256x128s2, ACT, RES, TOUT>(g, stream);
+    case 3:
+      return launch<B128x256s2, ACT, RES, TOUT>(g, stream);
+    case 4:
+      return launch<B256x256s2, ACT, RES, TOUT>(g, stream);
+    case 5:
+      return launch<B64x128s2, ACT, RES, TOUT>(g, stream);
+    default:
+      return launch<B128x128s2, ACT, RES, TOUT>(g, stream);
+  }
+}
+
+int dispatch_res(const GemmArgs& g, int t, hipStream_t stream) {
+  switch (t) {
+    case 1:
+      return launch<B128x128s3, ACT_NONE, true, float>(g, stream);
+    case 2:
+      return launch<B256x128s2, ACT_NONE, true, float>(g, stream);
+    case 3:
+      return launch<B128x256s2, ACT_NONE, true, float>(g, stream);
+    case 5:
+      return launch<B64x128s2, ACT_NONE, true, float>(g, stream);
+    default:
+      return launch<B128x128s2, ACT_NONE, true, float>(g, stream);
+  }
+}
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+}  // namespace
+
+int try_gemm_bf16(const GemmArgs& g, int x_dtype, int w_dtype, int w_layout, int compute, hipStream_t stream) {
+  if (compute != DT_BF16 || w_layout != 0 || x_dtype != DT_BF16 || w_dtype != DT_BF16) return 0;
+  if (g.norm != NORM_NONE || g.K % 64 != 0 || g.N % 8 != 0 || g.M <= 0 || g.N <= 0) return 0;
+  if (g.M > 0x7fffffff || g.N > 0x7fffffff || g.K > 0x7fffffff) return 0;
+  if (!aligned16(g.x) || (g.ld_x * 2) % 16 || !aligned16(g.w) || (g.ld_w * 2) % 16) return 0;
+  if (g.w_scale && !aligned16(g.w_scale)) return 0;
+  if (g.bias && (g.bias_dtype != DT_F32 || !aligned16(g.bias))) return 0;
+  const bool res = g.res != nullptr;
+  if (res && (g.res_dtype != DT_F32 || g.out_dtype != DT_F32 || !aligned16(g.res) || g.ld_res % 8)) return 0;
+  const bool out_bf16 = g.out_dtype == DT_BF16;
+  if (!out_bf16 && g.out_dtype != DT_F32) return 0;
+  if (!aligned16(g.out) || g.ld_out % 8) return 0;
+  // Residual (fp32 in/out) GEMMs are memory bound and go to the pipelined kernel
+  // (LDS-staged epilogue, fully coalesced residual reads and stores) unless a tile of
+  // this kernel is asked for.
+  if (res) {
+    const char* e = getenv("CORTEX_RES_TILE");
+    const int t = e ? atoi(e) : -1;
+    if (t < 0 || t >= 10 || g.act) return 0;
+    return dispatch_res(g, t, stream);
+  }
+  if (out_bf16)
+    return g.act ? dispatch<ACT_GELU, false, bf16>(g, stream) : dispatch<ACT_NONE, false, bf16>(g, stream);
+  return g.act ? dispatch<ACT_GELU, false, float>(g, stream) : dispatch<ACT_NONE, false, float>(g, stream);
+}
+
+}  // namespace cortex

@@ -261,6 +261,14 @@ using Q128x128s3 = PTile<128, 128, 2, 2, 3, 2>;
 using Q128x64s3 = PTile<128, 64, 2, 1, 3, 2>;
 using Q64x128s3 = PTile<64, 128, 1, 2, 3, 2>;
 
+int residual_tile() {
+  static int v = [] {
+    const char* s = getenv("CORTEX_RES_TILE");
+    return s ? atoi(s) : -1;
+  }();
+  return v;
+}
+
 int pipe_tile() {
   static int v = [] {
     const char* s = getenv("CORTEX_PIPE_TILE");
@@ -292,8 +300,11 @@ template <int ACT, bool RES, class TOUT>
 int dispatch_bf16(const GemmArgs& g, hipStream_t stream) {
   int t = pipe_tile();
   if (t < 0) {
-    const int64_t tiles = cdiv(g.M, 128) * cdiv(g.N, 128);
-    t = tiles < 512 ? 12 : 10;
+    // residual GEMMs (memory bound): 64-row tiles, twice the workgroups per CU;
+    // otherwise 128x128 with two stages (two workgroups per CU)
+    t = RES ? 12 : 11;
+    const int r = residual_tile();
+    if (RES && r >= 10) t = r;
   }
   switch (t) {
     case 11:

@@ -524,6 +524,7 @@ int cortex_norm_linear(int64_t M, int64_t N, int64_t K, int x_dtype, const void*
                    ((ld_w * ws) % 16 == 0) && (ws != 1 || ((uintptr_t)w % 8 == 0 && (ld_w % 8) == 0));
   g.vec = vec ? 1 : 0;
   int fast = try_rowdot(g, x_dtype, w_dtype, w_layout, compute, stream);
+  if (fast == 0) fast = try_gemm_bf16(g, x_dtype, w_dtype, w_layout, compute, stream);
   if (fast == 0) fast = try_gemm_pipe(g, x_dtype, w_dtype, w_layout, compute, stream);
   if (fast == 0) fast = try_gemm_fast(g, x_dtype, w_dtype, w_layout, compute, stream);
   if (fast != 0) return fast > 0 ? OK : fast;
