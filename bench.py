@@ -1,14 +1,22 @@
-"""Cortex-S INT8 inference forward on one MI355X: samples/s at B=32 x 512 events,
-p50/p99 latency at B=1, the dominant kernel's roofline fraction, and the CPU
-oracle timed on the host cores.
+"""Cortex-S INT8 inference forward on one MI355X.
 
-A step is one forward of the fixed workload (CORTEX_S, weights quantised to INT8
-per channel on the GPU, bf16 MFMA with fp32 accumulation, B = 32 samples x 512
-synthetic events) replayed from a HIP graph; its inputs are already resident in
-HBM and are copied into the graph's input buffers inside the step.
+Headline: samples/s of the Cortex-S INT8 forward at B = 32 x 512 synthetic events,
+p50/p99 latency at B = 1, the roofline fraction of the dominant kernel and of the
+other hot kernels, and the CPU oracle timed on the host cores.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
-Prints exactly one JSON line on stdout.
+A step is one forward of the fixed workload (CORTEX_S, weights quantised to INT8 per
+channel on the GPU, bf16 MFMA with fp32 accumulation and an fp32 residual stream,
+B = 32 samples x 512 events) replayed from a HIP graph; its inputs are already
+resident in HBM and are copied into the graph's input buffers inside the step.
+
+Usage:
+  python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--quick]
+      prints exactly one JSON line on stdout
+  python bench.py --kernel NAME [--iters N]
+      launches one hot kernel N times on synthetic operands of its forward shape (for
+      rocprofv3 --kernel-trace / --pmc runs); NAME in KERNELS
+  python bench.py --copy-calibration [--iters N]
+      a plain 64 MiB device-to-device copy N times (the reference for PMC byte counters)
 """
 
 from __future__ import annotations
@@ -16,6 +24,7 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import re
 import sys
 import time
 from pathlib import Path
@@ -30,18 +39,23 @@ import torch  # noqa: E402
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
 METRIC = "Cortex-S INT8 samples/s @B=32,512 ev; p99 latency @B=1; % HBM/MFMA peak"
+B_MAIN, PER_MAIN, L, D, H, DH = 32, 512, 256, 512, 8, 64
+M_ROWS = B_MAIN * L
 
 
 def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
 
 
-def make_events(batch: int, per_sample: int, seed: int):
-    """Synthetic spike events: nid U[0,137), time bin U[0,600), value = clip(Poisson(1)+1, 0, 7)."""
+def make_events(batch: int, per_sample, seed: int):
+    """Synthetic spike events: nid U[0,137), time bin U[0,600), value = clip(Poisson(1)+1, 0, 7).
+
+    ``per_sample`` is an int (same count for every sample) or a per-sample array."""
     rng = np.random.default_rng(seed)
-    E = batch * per_sample
+    counts = np.full(batch, per_sample) if np.isscalar(per_sample) else np.asarray(per_sample)
+    E = int(counts.sum())
     return (rng.integers(0, 137, E), rng.integers(0, 600, E), np.clip(rng.poisson(1.0, E) + 1, 0, 7),
-            np.repeat(np.arange(batch), per_sample))
+            np.repeat(np.arange(batch), counts))
 
 
 def build_model(dev):
@@ -60,39 +74,170 @@ def build_model(dev):
     return convert_model(model, derive_scales(model, hooks), inplace=True)
 
 
-def time_dominant_kernel(model, dev, iters: int = 50):
-    """Average duration of the MLP-up GEMM as the forward runs it (bf16 LayerNorm rows x the
-    int8 weight's bf16 image, 2048x512, per-channel scale + GELU epilogue, bf16 out) at
-    M = 32*256 rows, timed with HIP events on the stream it is launched on."""
+# --------------------------------------------------------------------------- hot kernels
+
+
+def _int8_image(n: int, k: int, dev, seed: int):
+    """An INT8 per-channel weight (as QuantizedLinear holds it) and its bf16 execution image."""
     from cortex.kernels import ops
-    from cortex.models._layers import exec_weights
 
-    blk = model.encoder.self_attn_blocks[0]
-    M, K, N = 32 * 256, 512, 2048
-    x = torch.randn(M, K, device=dev).bfloat16()
-    out = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
-    w = exec_weights(blk.mlp[0], torch.bfloat16)
+    g = torch.Generator(device="cpu").manual_seed(seed)
+    w = torch.randn(n, k, generator=g) * 0.02
+    q, s = ops.quantize_int8(w.to(dev))
+    return ops.convert(q, torch.bfloat16), s
 
-    def launch():
-        ops.norm_linear(x, **w, act="gelu", out_dtype=torch.bfloat16, compute_dtype=torch.bfloat16, out=out)
 
-    for _ in range(5):
-        launch()
-    stream = torch.cuda.current_stream(dev)
+def make_kernel(name: str, dev):
+    """(launch callable, launches per forward, bound, algorithmic flops, algorithmic bytes, label)
+    for one hot kernel at its Cortex-S B=32 x 512-event shape, on synthetic operands."""
+    from cortex.kernels import ops
+
+    g = torch.Generator(device="cpu").manual_seed(7)
+    bf = torch.bfloat16
+
+    def rnd(*shape, dtype=torch.float32, scale=1.0):
+        return (torch.randn(*shape, generator=g) * scale).to(dtype).to(dev)
+
+    def gemm(n, k, act=None, residual=False, seed=1):
+        x = rnd(M_ROWS, k, dtype=bf)
+        w, s = _int8_image(n, k, dev, seed)
+        res = rnd(M_ROWS, n) if residual else None
+        out = torch.empty(M_ROWS, n, dtype=torch.float32 if residual else bf, device=dev)
+        fn = lambda: ops.norm_linear(x, weight=w, weight_scale=s, act=act, residual=res,  # noqa: E731
+                                     out_dtype=out.dtype, compute_dtype=bf, out=out)
+        flops = 2.0 * M_ROWS * n * k
+        # compulsory bytes: activations, the INT8 weight and its scales, residual, output
+        byts = M_ROWS * k * 2 + n * k + 4 * n + (M_ROWS * n * 4 if residual else 0) + M_ROWS * n * out.element_size()
+        return fn, flops, byts
+
+    if name == "gemm_mlp2_residual":
+        fn, fl, by = gemm(512, 2048, residual=True)
+        return fn, 7, "hbm", fl, by, "MLP down 2048->512 + fp32 residual, M=8192 (gemm_pipe_kernel)"
+    if name == "gemm_mlp0_gelu":
+        fn, fl, by = gemm(2048, 512, act="gelu")
+        return fn, 7, "mfma", fl, by, "MLP up 512->2048 + GELU, bf16 out, M=8192 (gemm_bf16_kernel)"
+    if name == "gemm_qkv":
+        fn, fl, by = gemm(1536, 512)
+        return fn, 7, "mfma", fl, by, "QKV 512->1536, bf16 out, M=8192 (gemm_bf16_kernel)"
+    if name == "gemm_out_residual":
+        fn, fl, by = gemm(512, 512, residual=True)
+        return fn, 8, "hbm", fl, by, "attention out 512->512 + fp32 residual, M=8192 (gemm_pipe_kernel)"
+    if name == "attention_self":
+        qkv = rnd(M_ROWS, 3 * D, dtype=bf, scale=0.3)
+        o_buf, o = ops.merge_heads_out(B_MAIN, L, H, DH, bf, dev)
+        fn = lambda: ops.attention(ops.heads_view(qkv, B_MAIN, L, H, 0, D),  # noqa: E731
+                                   ops.heads_view(qkv, B_MAIN, L, H, D, D),
+                                   ops.heads_view(qkv, B_MAIN, L, H, 2 * D, D), out=o)
+        fl = 4.0 * B_MAIN * H * L * L * DH
+        by = 3 * M_ROWS * D * 2 + M_ROWS * D * 2
+        return fn, 7, "mfma", fl, by, "self-attention B=32 H=8 L=256 Dh=64 (attention_fast_kernel)"
+    if name == "attention_cross":
+        E = B_MAIN * PER_MAIN
+        kv = rnd(E, 2 * D, dtype=bf)
+        q = rnd(1, H, L, DH, dtype=bf, scale=0.25)
+        off = torch.arange(0, E + 1, PER_MAIN, device=dev)
+        o_buf, o = ops.merge_heads_out(B_MAIN, L, H, DH, bf, dev)
+        fn = lambda: ops.attention(q, ops.heads_view(kv, 1, E, H, 0, D),  # noqa: E731
+                                   ops.heads_view(kv, 1, E, H, D, D), kv_offsets=off, out=o, batch=B_MAIN)
+        fl = 4.0 * H * L * DH * E
+        by = L * D * 2 + E * 2 * D * 2 + M_ROWS * D * 2
+        return fn, 1, "mfma", fl, by, "cross-attention latents x 512 CSR events/sample (attention_fast_kernel)"
+    if name == "ln_rows":
+        x = rnd(M_ROWS, D)
+        w, b = rnd(D), rnd(D)
+        out = torch.empty(M_ROWS, D, dtype=bf, device=dev)
+
+        def fn():
+            ops.ln_rows(x, (w, b, 1e-5))
+        by = M_ROWS * D * 4 + M_ROWS * D * 2 + 2 * D * 4
+        del out
+        return fn, 14, "hbm", 0.0, by, "LayerNorm rows fp32 -> bf16, M=8192 K=512 (ln_rows_kernel)"
+    if name == "tokenize":
+        E = B_MAIN * PER_MAIN
+        nid, tb, val, bidx = (torch.from_numpy(a).to(dev) for a in make_events(B_MAIN, PER_MAIN, seed=3))
+        ne, te, ve = rnd(512, D, scale=0.02), rnd(1024, D, scale=0.02), rnd(8, D, scale=0.02)
+        offsets, order, _ = ops.pack_plan(bidx, B_MAIN)
+        fn = lambda: ops.tokenize(ne, te, ve, nid, tb, val, order=order, csr_offsets=offsets)  # noqa: E731
+        by = E * (D * 4 + 4 * 8) + (137 + 600 + 8) * D * 4 + (B_MAIN + 1) * 8
+        return fn, 1, "hbm", 0.0, by, "fused tokenizer into CSR rows, E=16384 D=512 fp32 (row_writer_kernel)"
+    raise ValueError(f"unknown kernel {name}")
+
+
+KERNELS = ("gemm_mlp2_residual", "gemm_mlp0_gelu", "gemm_qkv", "gemm_out_residual", "attention_self",
+           "attention_cross", "ln_rows", "tokenize")
+
+
+def time_launches(fn, iters: int = 20, reps: int = 5) -> float:
+    """Average seconds per launch: `iters` launches captured in a HIP graph (so host launch
+    cost does not enter), replayed `reps` times between HIP events on the current stream."""
+    for _ in range(3):
+        fn()
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        fn()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(iters):
+            fn()
+    graph.replay()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
     t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize(dev)
     t0.record(stream)
-    for _ in range(iters):
-        launch()
+    for _ in range(reps):
+        graph.replay()
     t1.record(stream)
     t1.synchronize()
-    sec = t0.elapsed_time(t1) / 1e3 / iters
-    flops = 2.0 * M * N * K
-    achieved = flops / sec / 1e12
-    return {"bound": "mfma", "achieved": round(achieved, 2), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-            "frac": round(achieved / BF16_PEAK_TFLOPS, 4), "traffic": None,
-            "kernel": "gemm_pipe_kernel (bf16 x bf16-image of int8 W, scale + GELU -> bf16), M=8192 K=512 N=2048",
-            "avg_us": round(sec * 1e6, 2), "flops_per_launch": flops}
+    return t0.elapsed_time(t1) / 1e3 / (iters * reps)
+
+
+def traffic_from_profiles(name: str):
+    """HBM bytes per launch measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE (scaled by the
+    counters' reading for a plain copy of known size), as recorded in profiles/<name>_pmc.txt."""
+    p = ROOT / "profiles" / f"{name}_pmc.txt"
+    if not p.exists():
+        return None
+    m = re.search(r"^traffic_bytes_per_launch:\s*([0-9.eE+]+)", p.read_text(), re.M)
+    return float(m.group(1)) if m else None
+
+
+def kernel_rooflines(dev):
+    rows = {}
+    for name in KERNELS:
+        fn, per_fwd, bound, flops, byts, label = make_kernel(name, dev)
+        sec = time_launches(fn)
+        r = {"kernel": label, "avg_us": round(sec * 1e6, 2), "launches_per_forward": per_fwd, "bound": bound,
+             "hbm_gbs": round(byts / sec / 1e9, 1), "hbm_frac": round(byts / sec / 1e9 / HBM_PEAK_GBS, 4),
+             "bytes_per_launch": int(byts)}
+        if flops:
+            r["tflops"] = round(flops / sec / 1e12, 2)
+            r["mfma_frac"] = round(flops / sec / 1e12 / BF16_PEAK_TFLOPS, 4)
+            r["flops_per_launch"] = flops
+        rows[name] = r
+        del fn
+    torch.cuda.empty_cache()
+    return rows
+
+
+def roofline_of(name: str, r: dict) -> dict:
+    if r["bound"] == "hbm":
+        out = {"bound": "hbm", "achieved": r["hbm_gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+               "frac": r["hbm_frac"]}
+    else:
+        out = {"bound": "mfma", "achieved": r["tflops"], "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+               "frac": r["mfma_frac"]}
+    out["traffic"] = traffic_from_profiles(name)
+    out.update({"name": name, "kernel": r["kernel"], "avg_us": r["avg_us"],
+                "algorithmic_bytes": r["bytes_per_launch"]})
+    if "flops_per_launch" in r:
+        out["algorithmic_flops"] = r["flops_per_launch"]
+    return out
+
+
+# --------------------------------------------------------------------------- forward-level
 
 
 def section_breakdown(model, inputs, dev, iters: int = 20):
@@ -101,9 +246,8 @@ def section_breakdown(model, inputs, dev, iters: int = 20):
     from cortex.models._layers import apply_linear
 
     nid, tb, val, bidx = inputs
-    B, cfg = 32, model.config
+    B, cfg = B_MAIN, model.config
     enc, xa, tok = model.encoder, model.encoder.cross_attn, model.tokenizer
-    D, L, H = cfg.latent_dim, cfg.num_latents, xa.num_heads
     comp = cfg.compute_dtype
     ev = lambda: torch.cuda.Event(enable_timing=True)  # noqa: E731
     times: dict[str, float] = {}
@@ -135,9 +279,9 @@ def section_breakdown(model, inputs, dev, iters: int = 20):
                             compute=comp)
 
     x = timed("cross_attn", cross)
-    lat = timed("self_attn_all", lambda: enc.encode_rows(x, B))
+    lat = timed("self_attn_all", lambda: enc.encode_rows(x, B, final_norm=False))
     timed("self_attn_single", lambda: enc.self_attn_blocks[0].forward_rows(x, B, L))
-    timed("behavior_head", lambda: model.behavior_head.forward_rows(lat, B))
+    timed("behavior_head", lambda: model.behavior_head.forward_rows(lat, B, pre_norm=enc.final_norm))
     return times
 
 
@@ -162,7 +306,32 @@ def latency_b1(model, dev, n_requests: int, per_sample: int = 512):
             lat.append((time.perf_counter() - t0) * 1e3)
     lat.sort()
     return {"p50_ms": round(lat[len(lat) // 2], 4), "p99_ms": round(lat[int(len(lat) * 0.99) - 1], 4),
-            "requests": n_requests, "events_per_request": per_sample}
+            "requests": n_requests, "events_per_request": per_sample, "path": "hip graph replay"}
+
+
+def serving_sweep(model, dev, batches=(1, 8, 32, 128, 256), reps: int = 20):
+    """Serving-shaped forward: E_b = clip(Poisson(512), 64, 2048) per sample, one graph per batch."""
+    from cortex.runtime import CapturedForward
+
+    rng = np.random.default_rng(11)
+    out = []
+    for B in batches:
+        counts = np.clip(rng.poisson(512, B), 64, 2048)
+        inputs = [torch.from_numpy(a).to(dev) for a in make_events(B, counts, seed=100 + B)]
+        cap = CapturedForward(model, batch_size=B, n_events=int(counts.sum()))
+        for _ in range(3):
+            cap(*inputs)
+        torch.cuda.synchronize(dev)
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            cap(*inputs)
+        torch.cuda.synchronize(dev)
+        sec = (time.perf_counter() - t0) / reps
+        out.append({"batch": B, "events": int(counts.sum()), "ms_per_forward": round(sec * 1e3, 4),
+                    "samples_per_s": round(B / sec, 1)})
+        del cap, inputs
+        torch.cuda.empty_cache()
+    return out
 
 
 def cpu_baseline(model, budget_s: float = 20.0):
@@ -172,7 +341,7 @@ def cpu_baseline(model, budget_s: float = 20.0):
 
     torch.set_num_threads(os.cpu_count() or 1)
     sd = {k: v.detach().cpu() for k, v in model.state_dict().items()}
-    arrs = make_events(32, 512, seed=0)
+    arrs = make_events(B_MAIN, PER_MAIN, seed=0)
     O.forward(sd, O.CORTEX_S_SHAPE, *arrs)  # warm-up
     n, t0 = 0, time.perf_counter()
     while True:
@@ -181,9 +350,43 @@ def cpu_baseline(model, budget_s: float = 20.0):
         el = time.perf_counter() - t0
         if el >= budget_s or n >= 30:
             break
-    return {"value": round(32 * n / el, 2), "unit": "samples/s", "cores": torch.get_num_threads(),
-            "kind": "port", "sample": f"{n} forwards of B=32 x 512 events (CORTEX_S INT8-dequant, fp32) "
-                                      f"in {el:.1f} s"}
+    cpu = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                cpu = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"value": round(B_MAIN * n / el, 2), "unit": "samples/s", "cores": torch.get_num_threads(),
+            "kind": "port", "sample": f"{n} forwards of B=32 x 512 events (CORTEX_S, INT8 dequantised to fp32, "
+                                      f"oracle restatement) in {el:.1f} s", "cpu": cpu}
+
+
+# --------------------------------------------------------------------------- modes
+
+
+def run_kernel_only(name: str, iters: int) -> int:
+    dev = torch.device("cuda:0")
+    fn, _, _, _, _, label = make_kernel(name, dev)
+    for _ in range(3):
+        fn()
+    torch.cuda.synchronize()
+    sec = time_launches(fn, iters, reps=3)
+    print(f"{name}: {label}: {sec * 1e6:.2f} us/launch over {3 * iters} graph-replayed launches", flush=True)
+    return 0
+
+
+def run_copy_calibration(iters: int) -> int:
+    dev = torch.device("cuda:0")
+    n = 64 << 20
+    a = torch.ones(n, dtype=torch.uint8, device=dev)
+    b = torch.empty_like(a)
+    for _ in range(iters):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    print(f"copy: {iters} x {n} bytes read + {n} bytes written", flush=True)
+    return 0
 
 
 def main() -> int:
@@ -193,7 +396,10 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--latency-requests", type=int, default=1000)
-    ap.add_argument("--quick", action="store_true", help="skip latency, breakdown and CPU baseline")
+    ap.add_argument("--quick", action="store_true", help="skip latency, sweep, breakdown and CPU baseline")
+    ap.add_argument("--kernel", choices=KERNELS, help="launch one hot kernel only (profiling)")
+    ap.add_argument("--copy-calibration", action="store_true", help="64 MiB copies only (PMC calibration)")
+    ap.add_argument("--iters", type=int, default=20)
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU: the Cortex forward is measured per GPU (got --gpus {args.gpus}); "
@@ -202,12 +408,16 @@ def main() -> int:
     if not torch.cuda.is_available():
         print("bench.py needs a ROCm GPU", file=sys.stderr)
         return 2
+    if args.kernel:
+        return run_kernel_only(args.kernel, args.iters)
+    if args.copy_calibration:
+        return run_copy_calibration(args.iters)
     dev = torch.device("cuda:0")
     from cortex.runtime import CapturedForward
 
     log("bench: building CORTEX_S INT8 model")
     model = build_model(dev)
-    B, per = 32, 512
+    B, per = B_MAIN, PER_MAIN
     inputs = [torch.from_numpy(a).to(dev) for a in make_events(B, per, seed=0)]
     cap = CapturedForward(model, batch_size=B, n_events=B * per)
     log("bench: graph captured; warmup")
@@ -223,8 +433,7 @@ def main() -> int:
     value = B * args.steps / elapsed
     log(f"bench: {ms_step:.4f} ms/step, {value:.1f} samples/s")
 
-    # eager (no graph) forward time, for reference
-    with torch.no_grad():
+    with torch.no_grad():  # eager (no graph) forward, for reference
         for _ in range(3):
             model(*inputs, batch_size=B)
         torch.cuda.synchronize(dev)
@@ -234,8 +443,10 @@ def main() -> int:
         torch.cuda.synchronize(dev)
     eager_ms = (time.perf_counter() - t0) / 10 * 1e3
 
-    roof = time_dominant_kernel(model, dev)
-    log(f"bench: dominant kernel {roof['avg_us']} us, {roof['achieved']} TFLOP/s")
+    kern = kernel_rooflines(dev)
+    dominant = max(kern, key=lambda k: kern[k]["avg_us"] * kern[k]["launches_per_forward"])
+    roof = roofline_of(dominant, kern[dominant])
+    log(f"bench: dominant kernel {dominant}: {roof['avg_us']} us, {roof['achieved']} {roof['unit']}")
     extra = {}
     if not args.quick:
         with torch.no_grad():
@@ -243,6 +454,8 @@ def main() -> int:
         log(f"bench: sections {extra['sections_ms']}")
         extra["latency_b1"] = latency_b1(model, dev, args.latency_requests)
         log(f"bench: latency {extra['latency_b1']}")
+        extra["serving_sweep"] = serving_sweep(model, dev)
+        log(f"bench: serving {extra['serving_sweep']}")
     cpu = None
     if not (args.no_cpu_baseline or args.quick):
         log("bench: CPU baseline")
@@ -254,12 +467,13 @@ def main() -> int:
         "metric": METRIC, "value": round(value, 2), "unit": "samples/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(ms_step, 4), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
-        "config": {"workload": "cortex_s_int8_forward", "model": "CORTEX_S (random init, seed 0, INT8 per-channel)",
-                   "batch": B, "events_per_sample": per, "compute": "bf16 MFMA, fp32 accumulate, fp32 residual",
-                   "graph": "hip graph replay"},
+        "config": {"workload": "cortex_s_int8_forward_b32x512", "model": "CORTEX_S (random init, seed 0, INT8 "
+                   "per-channel)", "batch": B, "events_per_sample": per,
+                   "compute": "bf16 MFMA, fp32 accumulate, fp32 residual", "graph": "hip graph replay"},
         "forward_tflops": round(fwd_flops / (ms_step * 1e-3) / 1e12, 2),
+        "forward_mfma_frac": round(fwd_flops / (ms_step * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4),
         "eager_ms_per_forward": round(eager_ms, 4),
-        "roofline": roof, "cpu_baseline": cpu, **extra,
+        "roofline": roof, "kernels": kern, "cpu_baseline": cpu, **extra,
     }
     print(json.dumps(line), flush=True)
     return 0
