@@ -50,6 +50,11 @@ _SIGNATURES = {
         [_int, _i64, _ptr, _i64, _i64, _ptr, _i64, _i64, _ptr, _i64, _i64, _ptr, _i64, _ptr, _i64, _ptr, _i64,
          _i64, _ptr, _ptr, _ptr, _i64, _i64, _ptr, _i64, _ptr, _ptr, _ptr],
     ),
+    "cortex_tokenize_ln": (
+        _int,
+        [_i64, _ptr, _i64, _i64, _ptr, _i64, _i64, _ptr, _i64, _i64, _ptr, _i64, _ptr, _i64, _ptr, _i64, _i64,
+         _ptr, _ptr, _ptr, _ptr, _f32, _ptr, _i64, _ptr, _ptr],
+    ),
     "cortex_pack_rows": (
         _int, [_int, _i64, _ptr, _i64, _i64, _ptr, _ptr, _ptr, _i64, _i64, _ptr, _i64, _ptr, _ptr]),
     "cortex_quantize_int8": (_int, [_ptr, _i64, _i64, _i64, _ptr, _ptr, _ptr, _i64, _ptr]),

@@ -80,6 +80,30 @@ def tokenize(neuron_emb, time_emb, value_emb, neuron_ids, time_bins, values, *, 
     return (out, mask) if padded else out
 
 
+def tokenize_ln(neuron_emb, time_emb, value_emb, neuron_ids, time_bins, values, ln, *, order=None,
+                csr_offsets=None, err=None, out=None) -> torch.Tensor:
+    """``LN((N[nid] + T[tb]) + V[val])`` as bf16 CSR rows (one launch, fp32 tokens never stored).
+
+    ``ln`` is ``(weight, bias, eps)``; rows follow ``order`` (the pack plan) and rows past
+    ``csr_offsets[B]`` come out as ``LN(0)``."""
+    dev = nat.require_gpu(neuron_emb, time_emb, value_emb, neuron_ids, time_bins, values, order, err,
+                          what="tokenize_ln")
+    for t in (neuron_emb, time_emb, value_emb):
+        if t.dtype != torch.float32 or t.stride(-1) != 1:
+            raise ValueError("tokenize_ln needs fp32 tables with unit column stride")
+    E, D = neuron_ids.shape[0], neuron_emb.shape[1]
+    g, b, eps = ln
+    if out is None:
+        out = torch.empty((E, D), dtype=torch.bfloat16, device=dev)
+    nat.call("cortex_tokenize_ln", D, nat.ptr(neuron_emb), neuron_emb.shape[0], neuron_emb.stride(0),
+             nat.ptr(time_emb), time_emb.shape[0], time_emb.stride(0), nat.ptr(value_emb), value_emb.shape[0],
+             value_emb.stride(0), nat.ptr(neuron_ids), neuron_ids.stride(0) if E else 1, nat.ptr(time_bins),
+             time_bins.stride(0) if E else 1, nat.ptr(values), values.stride(0) if E else 1, E, nat.ptr(order),
+             _end_ptr(csr_offsets), nat.ptr(g), nat.ptr(b), float(eps), nat.ptr(out), out.stride(0),
+             nat.ptr(err), nat.stream_of(dev))
+    return out
+
+
 def _end_ptr(offsets) -> int | None:
     """Device address of offsets[B] (the number of valid CSR rows)."""
     if offsets is None:

@@ -81,8 +81,18 @@ def batch_invariant(owner: nn.Module, name: str, inputs: list, mods: list, fn):
     return val
 
 
-def _ln_params(norm: nn.LayerNorm):
+def ln_params(norm: nn.LayerNorm):
+    """``(weight, bias, eps)`` of a LayerNorm, as the row kernels take it."""
     return (norm.weight, norm.bias, norm.eps)
+
+
+def fused_tokens_ok(tables, norm: nn.LayerNorm) -> bool:
+    """Whether the tokenizer + LayerNorm kernel covers these embedding tables and norm."""
+    D = tables[0].shape[1]
+    if D not in _LN_ROWS_K or any(t.dtype != torch.float32 or t.stride(-1) != 1 or t.data_ptr() % 16
+                                  or t.stride(0) % 4 for t in tables):
+        return False
+    return all(p is not None and p.dtype == torch.float32 and p.data_ptr() % 16 == 0 for p in (norm.weight, norm.bias))
 
 
 def ln_rows_ok(x: torch.Tensor, *norms: nn.LayerNorm) -> bool:
@@ -101,7 +111,7 @@ def normalize_bf16(x: torch.Tensor, norm: nn.LayerNorm, norm2: nn.LayerNorm | No
     x2 = x.reshape(-1, x.shape[-1])
     if x2.data_ptr() % 16 or (x2.shape[0] > 1 and x2.stride(0) % 4) or x2.stride(-1) != 1:
         x2 = x2.contiguous()
-    return ops.ln_rows(x2, _ln_params(norm), _ln_params(norm2) if norm2 is not None else None)
+    return ops.ln_rows(x2, ln_params(norm), ln_params(norm2) if norm2 is not None else None)
 
 
 def apply_linear(lin: nn.Module, x: torch.Tensor, *, norm: nn.LayerNorm | None = None, stats=None,

@@ -26,7 +26,8 @@ from torch import nn
 
 from cortex.kernels import ops
 from cortex.kernels.pack import pack_events as _device_pack_events
-from cortex.models._layers import apply_linear, batch_invariant, exec_weights, ln_rows_ok, normalize_bf16
+from cortex.models._layers import (apply_linear, batch_invariant, exec_weights, fused_tokens_ok, ln_params,
+                                   ln_rows_ok, normalize_bf16)
 from cortex.models.config import CortexConfig
 from cortex.models.perceiver import PerceiverEncoder
 from cortex.models.tokenizer import SpikeTokenizer
@@ -131,12 +132,19 @@ class CortexModel(nn.Module):
         xa = enc.cross_attn
         D, L, H = cfg.latent_dim, cfg.num_latents, xa.num_heads
         offsets, order, _ = ops.pack_plan(batch_indices, B, err=err_flag)
-        tokens = ops.tokenize(tok.neuron_emb.weight, tok.time_emb.weight, tok.value_emb.weight, neuron_ids,
-                              time_bins, values, order=order, csr_offsets=offsets, err=err_flag)  # CSR rows
-        E = tokens.shape[0]
-        kv = apply_linear(xa.kv_proj, tokens, norm=xa.norm_kv, out_dtype=compute, compute=compute)  # (E, 2D)
+        tables = (tok.neuron_emb.weight, tok.time_emb.weight, tok.value_emb.weight)
+        E = neuron_ids.shape[0]
+        if compute == torch.bfloat16 and not xa.kv_proj._forward_pre_hooks and fused_tokens_ok(tables, xa.norm_kv):
+            # tokens -> norm_kv -> bf16 operand in one pass; the fp32 tokens are never stored
+            xn = ops.tokenize_ln(*tables, neuron_ids, time_bins, values, ln_params(xa.norm_kv), order=order,
+                                 csr_offsets=offsets, err=err_flag)
+            kv = ops.norm_linear(xn, **exec_weights(xa.kv_proj, compute), out_dtype=compute, compute_dtype=compute)
+        else:
+            tokens = ops.tokenize(*tables, neuron_ids, time_bins, values, order=order, csr_offsets=offsets,
+                                  err=err_flag)  # CSR rows
+            kv = apply_linear(xa.kv_proj, tokens, norm=xa.norm_kv, out_dtype=compute, compute=compute)  # (E, 2D)
         q = xa.project_queries(enc.latents, compute)  # (L, D), shared by every sample
-        o_buf, o = ops.merge_heads_out(B, L, H, D // H, compute, tokens.device)
+        o_buf, o = ops.merge_heads_out(B, L, H, D // H, compute, kv.device)
         ops.attention(ops.heads_view(q, 1, L, H), ops.heads_view(kv, 1, E, H, 0, D),
                       ops.heads_view(kv, 1, E, H, D, D), kv_offsets=offsets, out=o, batch=B)
         x = apply_linear(xa.out_proj, o_buf, residual=enc.latents, res_rows=L, out_dtype=torch.float32,

@@ -47,6 +47,30 @@ __device__ __forceinline__ void ln_regs(float (&v)[EPL], float inv_k, float eps,
   }
 }
 
+struct TokLnArgs {
+  const float* neuron;
+  int64_t n_neuron, ld_neuron;
+  const float* time;
+  int64_t n_time, ld_time;
+  const float* value;
+  int64_t n_value, ld_value;
+  const int64_t* nid;
+  int64_t s_nid;
+  const int64_t* tb;
+  int64_t s_tb;
+  const int64_t* val;
+  int64_t s_val;
+  int64_t E;
+  const int64_t* order;
+  const int64_t* csr_end;
+  const float* gamma;
+  const float* beta;
+  float eps;
+  void* out;
+  int64_t ld_out;
+  int32_t* err;
+};
+
 // Row r: lane l holds elements (j/4)*256 + 4l + (j%4), loaded as float4 (coalesced).
 template <int EPL>
 __global__ __launch_bounds__(256) void ln_rows_kernel(const float* __restrict__ x, int64_t M, int64_t ld_x,
@@ -83,6 +107,64 @@ __global__ __launch_bounds__(256) void ln_rows_kernel(const float* __restrict__ 
       *reinterpret_cast<bf16x4*>(out_bf + m * ld_bf + k) = b;
     }
     if (out_f) *reinterpret_cast<float4*>(out_f + m * ld_f + k) = make_float4(v[j], v[j + 1], v[j + 2], v[j + 3]);
+  }
+}
+
+
+// Spike tokens straight to the LayerNorm'd bf16 operand of the cross-attention kv
+// projection: row r of the CSR token matrix is
+//   x = (neuron_emb[nid[e]] + time_emb[tb[e]]) + value_emb[val[e]]   (fp32, left to right)
+// with e = order[r] (rows past *csr_end, or with an index outside its table, are x = 0
+// and the latter set bit 1 of err), then LN(x) with gamma/beta/eps is written as bf16.
+// The fp32 tokens are never stored.  Same lane layout as ln_rows_kernel.
+template <int EPL>
+__global__ __launch_bounds__(256) void tokenize_ln_kernel(TokLnArgs a) {
+  constexpr int K = 64 * EPL;
+  const int lane = threadIdx.x & 63;
+  const int64_t r = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  if (r >= a.E) return;
+  int64_t e = (a.csr_end && r >= *a.csr_end) ? -1 : (a.order ? a.order[r] : r);
+  if (e >= a.E) e = -1;  // defensive: never follow a corrupt order entry
+  const float* s0 = nullptr;
+  const float* s1 = nullptr;
+  const float* s2 = nullptr;
+  if (e >= 0) {
+    const int64_t i0 = a.nid[e * a.s_nid], i1 = a.tb[e * a.s_tb], i2 = a.val[e * a.s_val];
+    if (i0 < 0 || i0 >= a.n_neuron || i1 < 0 || i1 >= a.n_time || i2 < 0 || i2 >= a.n_value) {
+      if (lane == 0 && a.err) atomicOr(a.err, 1);
+      e = -1;
+    } else {
+      s0 = a.neuron + i0 * a.ld_neuron;
+      s1 = a.time + i1 * a.ld_time;
+      s2 = a.value + i2 * a.ld_value;
+    }
+  }
+  float v[EPL];
+#pragma unroll
+  for (int j = 0; j < EPL; j += 4) {
+    const int k = (j >> 2) * 256 + lane * 4;
+    if (e < 0) {
+      v[j] = v[j + 1] = v[j + 2] = v[j + 3] = 0.0f;
+    } else {
+      const float4 x = *reinterpret_cast<const float4*>(s0 + k);
+      const float4 y = *reinterpret_cast<const float4*>(s1 + k);
+      const float4 z = *reinterpret_cast<const float4*>(s2 + k);
+      v[j] = (x.x + y.x) + z.x;
+      v[j + 1] = (x.y + y.y) + z.y;
+      v[j + 2] = (x.z + y.z) + z.z;
+      v[j + 3] = (x.w + y.w) + z.w;
+    }
+  }
+  ln_regs<EPL>(v, 1.0f / (float)K, a.eps, a.gamma, a.beta, lane);
+  bf16* out = reinterpret_cast<bf16*>(a.out) + r * a.ld_out;
+#pragma unroll
+  for (int j = 0; j < EPL; j += 4) {
+    bf16x4 b;
+    b[0] = (bf16)v[j];
+    b[1] = (bf16)v[j + 1];
+    b[2] = (bf16)v[j + 2];
+    b[3] = (bf16)v[j + 3];
+    *reinterpret_cast<bf16x4*>(out + (j >> 2) * 256 + lane * 4) = b;
   }
 }
 
@@ -148,6 +230,39 @@ int cortex_ln_rows(int64_t M, int64_t K, const float* x, int64_t ld_x, const flo
   }
 #undef CORTEX_LNR
   CORTEX_CHECK_LAUNCH("ln_rows_kernel");
+  return OK;
+}
+
+int cortex_tokenize_ln(int64_t D, const float* neuron_emb, int64_t n_neuron, int64_t ld_neuron, const float* time_emb,
+                       int64_t n_time, int64_t ld_time, const float* value_emb, int64_t n_value, int64_t ld_value,
+                       const int64_t* neuron_ids, int64_t s_nid, const int64_t* time_bins, int64_t s_tb,
+                       const int64_t* values, int64_t s_val, int64_t E, const int64_t* order, const int64_t* csr_end,
+                       const float* gamma, const float* beta, float eps, void* out_bf16, int64_t ld_out,
+                       int32_t* err_flag, hipStream_t stream) {
+  CORTEX_CHECK_ARG(E >= 0, "cortex_tokenize_ln: negative E");
+  if (E == 0) return OK;
+  CORTEX_CHECK_ARG(D == 256 || D == 512 || D == 768 || D == 1024, "cortex_tokenize_ln: D=%lld not in {256, 512, 768, 1024}",
+                   (long long)D);
+  CORTEX_CHECK_ARG(neuron_emb && time_emb && value_emb && neuron_ids && time_bins && values && out_bf16,
+                   "cortex_tokenize_ln: null pointer");
+  CORTEX_CHECK_ARG(ld_out >= D && ld_neuron >= D && ld_time >= D && ld_value >= D, "cortex_tokenize_ln: ld < D");
+  auto al16 = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
+  CORTEX_CHECK_ARG(al16(neuron_emb) && al16(time_emb) && al16(value_emb) && ld_neuron % 4 == 0 && ld_time % 4 == 0 &&
+                       ld_value % 4 == 0 && ((uintptr_t)out_bf16 & 7) == 0 && ld_out % 4 == 0 &&
+                       (!gamma || al16(gamma)) && (!beta || al16(beta)),
+                   "cortex_tokenize_ln: tables, gamma, beta need 16-byte aligned rows and out 8-byte aligned rows");
+  CORTEX_CHECK_ARG(cdiv(E, 4) <= 0x7fffffffLL, "cortex_tokenize_ln: E too large");
+  TokLnArgs a = {neuron_emb, n_neuron, ld_neuron, time_emb, n_time, ld_time, value_emb, n_value, ld_value,
+                 neuron_ids, s_nid, time_bins, s_tb, values, s_val, E, order, csr_end, gamma, beta, eps,
+                 out_bf16, ld_out, err_flag};
+  const dim3 grid((unsigned)cdiv(E, 4));
+  switch (D) {
+    case 256: hipLaunchKernelGGL(tokenize_ln_kernel<4>, grid, dim3(256), 0, stream, a); break;
+    case 512: hipLaunchKernelGGL(tokenize_ln_kernel<8>, grid, dim3(256), 0, stream, a); break;
+    case 768: hipLaunchKernelGGL(tokenize_ln_kernel<12>, grid, dim3(256), 0, stream, a); break;
+    default: hipLaunchKernelGGL(tokenize_ln_kernel<16>, grid, dim3(256), 0, stream, a); break;
+  }
+  CORTEX_CHECK_LAUNCH("tokenize_ln_kernel");
   return OK;
 }
 

@@ -67,6 +67,22 @@ int cortex_tokenize(int dtype, int64_t D, const void* neuron_emb, int64_t n_neur
                     const int64_t* csr_end, const int64_t* offsets, int64_t B, int64_t E_max, void* out,
                     int64_t ld_out, uint8_t* mask, int32_t* err_flag, hipStream_t stream);
 
+/* ---- a1 + a3: tokens straight to the kv-projection operand -------------------
+ * Replaces SpikeTokenizer.forward (cortex/models/tokenizer.py:90-93) followed by
+ * CrossAttentionBlock.norm_kv (cortex/models/perceiver.py:67) in the model forward,
+ * without storing the fp32 tokens:
+ *   row r = LN((neuron_emb[nid[e]] + time_emb[tb[e]]) + value_emb[val[e]]) in bf16,
+ *   e = order[r] (order NULL: e = r), the sum in fp32 left to right, LN with
+ *   gamma/beta/eps.  Rows r >= *csr_end (when csr_end is given) and rows with an index
+ *   outside its table take x = 0 (LN gives beta); the latter OR 1 into err_flag.
+ * fp32 tables, gamma, beta with 16-byte aligned rows; D in {256, 512, 768, 1024}. */
+int cortex_tokenize_ln(int64_t D, const float* neuron_emb, int64_t n_neuron, int64_t ld_neuron, const float* time_emb,
+                       int64_t n_time, int64_t ld_time, const float* value_emb, int64_t n_value, int64_t ld_value,
+                       const int64_t* neuron_ids, int64_t s_nid, const int64_t* time_bins, int64_t s_tb,
+                       const int64_t* values, int64_t s_val, int64_t E, const int64_t* order, const int64_t* csr_end,
+                       const float* gamma, const float* beta, float eps, void* out_bf16, int64_t ld_out,
+                       int32_t* err_flag, hipStream_t stream);
+
 /* ---- a2: pack existing token rows ------------------------------------------
  * Replaces the gather/scatter of _pack_events (cortex/models/cortex.py:150-164)
  * for already-tokenized (E, D) rows; same row mapping as cortex_tokenize. */

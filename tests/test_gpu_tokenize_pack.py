@@ -164,3 +164,41 @@ def test_invalid_batch_index_sets_flag_and_stays_in_bounds():
     valid = (bidx >= 0) & (bidx < 4)
     assert int(off[-1].item()) == int(valid.sum())
     assert (tok[int(valid.sum()):] == 0).all()
+
+
+def _bf16_ulp(x: torch.Tensor) -> torch.Tensor:
+    e = torch.floor(torch.log2(x.abs().clamp_min(1e-30)))
+    return torch.pow(2.0, e - 7)
+
+
+@pytest.mark.parametrize("D", [256, 512])
+def test_tokenize_ln_matches_tokens_then_layernorm(D):
+    """Tokens (bit-exact oracle sum, CSR order of shuffled events) -> LayerNorm -> bf16, one pass;
+    an out-of-range index gives LN(0) = beta and sets the error flag."""
+    from cortex.kernels import ops
+
+    B, per = 6, 300
+    E = B * per
+    n, t, v = _tables(512, 1024, 8, D, torch.float32)
+    nid, tb, val = _ids(E, 512, 1024, 8, seed=5)
+    nid[17] = 4096  # out of range
+    g = torch.Generator().manual_seed(8)
+    bidx = torch.repeat_interleave(torch.arange(B), per)[torch.randperm(E, generator=g)]
+    w, b = 1 + 0.1 * torch.randn(D, generator=g), 0.1 * torch.randn(D, generator=g)
+    err = torch.zeros(1, dtype=torch.int32, device=DEV)
+    offsets, order, _ = ops.pack_plan(bidx.to(DEV), B)
+    out = ops.tokenize_ln(n.to(DEV), t.to(DEV), v.to(DEV), nid.to(DEV), tb.to(DEV), val.to(DEV),
+                          (w.to(DEV), b.to(DEV), 1e-5), order=order, csr_offsets=offsets, err=err)
+    assert out.dtype == torch.bfloat16 and out.shape == (E, D)
+    assert int(err.item()) & 1
+    ordr = order.cpu().numpy()
+    nid_ok = nid.clone()
+    bad = nid_ok >= 512
+    nid_ok[bad] = 0
+    tok = torch.from_numpy(O.tokenize(n.numpy(), t.numpy(), v.numpy(), nid_ok.numpy(), tb.numpy(), val.numpy()))
+    tok[bad] = 0.0
+    ref = torch.nn.functional.layer_norm(tok[torch.from_numpy(ordr)], (D,), w, b, 1e-5)
+    diff = (out.float().cpu() - ref).abs()
+    assert bool((diff <= _bf16_ulp(ref) + 1e-5 * float(ref.abs().max())).all())
+    r_bad = int(np.nonzero(ordr == 17)[0][0])
+    torch.testing.assert_close(out[r_bad].float().cpu(), b.bfloat16().float(), rtol=0, atol=0)
