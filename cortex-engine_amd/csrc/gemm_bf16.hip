@@ -289,6 +289,18 @@ using B256x128s2 = BTile<256, 128, 2, 4, 2>;
 using B128x256s2 = BTile<128, 256, 2, 2, 4>;
 using B256x256s2 = BTile<256, 256, 2, 4, 2>;
 using B64x128s2 = BTile<64, 128, 2, 1, 2>;
+using B256x192s2 = BTile<256, 192, 2, 4, 2>;
+
+int cu_count() {
+  static int v = [] {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      n = 256;
+    return n;
+  }();
+  return v;
+}
 
 int bf16_tile() {
   static int v = [] {
@@ -302,10 +314,18 @@ template <int ACT, bool RES, class TOUT>
 int dispatch(const GemmArgs& g, hipStream_t stream) {
   int t = bf16_tile();
   if (t < 0) {
-    // 256x256 tiles halve the operand traffic per MFMA; take them while they still
-    // give at least three quarters of a workgroup per CU
-    const int64_t big = cdiv(g.M, 256) * cdiv(g.N, 256);
-    t = big >= 192 ? 4 : 0;
+    // 256-row tiles halve the operand traffic per MFMA; take the widest tile that still
+    // fills (nearly) every CU once, else 128x128 (two workgroups per CU)
+    const int64_t t256 = cdiv(g.M, 256) * cdiv(g.N, 256), t192 = cdiv(g.M, 256) * cdiv(g.N, 192);
+    const int ncu = cu_count();
+    if (g.N % 256 == 0 && t256 >= ncu * 15 / 16)
+      t = 4;
+    else if (g.N % 192 == 0 && t192 >= ncu * 15 / 16 && t192 <= ncu)
+      t = 6;
+    else if (t256 >= ncu * 3 / 4)
+      t = 4;
+    else
+      t = 0;
   }
   switch (t) {
     case 1:
@@ -318,6 +338,8 @@ int dispatch(const GemmArgs& g, hipStream_t stream) {
       return launch<B256x256s2, ACT, RES, TOUT>(g, stream);
     case 5:
       return launch<B64x128s2, ACT, RES, TOUT>(g, stream);
+    case 6:
+      return launch<B256x192s2, ACT, RES, TOUT>(g, stream);
     default:
       return launch<B128x128s2, ACT, RES, TOUT>(g, stream);
   }
