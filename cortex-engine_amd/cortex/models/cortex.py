@@ -149,8 +149,12 @@ class CortexModel(nn.Module):
                       ops.heads_view(kv, 1, E, H, D, D), kv_offsets=offsets, out=o, batch=B)
         x = apply_linear(xa.out_proj, o_buf, residual=enc.latents, res_rows=L, out_dtype=torch.float32,
                          compute=compute)  # (B*L, D) fp32 residual stream
-        x = enc.encode_rows(x, B, final_norm=False)
+        x = self._encode(x, B)
         return self.behavior_head.forward_rows(x, B, pre_norm=enc.final_norm)
+
+    def _encode(self, x: torch.Tensor, B: int) -> torch.Tensor:
+        """The self-attention stack on the fresh residual buffer ``x`` (updated in place)."""
+        return self.encoder.encode_rows(x, B, final_norm=False, inplace=True)
 
 
 def _pack_events(flat_tokens: torch.Tensor, batch_indices: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:

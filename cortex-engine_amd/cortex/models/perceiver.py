@@ -79,8 +79,9 @@ class SelfAttentionBlock(nn.Module):
             nn.Linear(mlp_hidden, config.latent_dim, bias=False),
         )
 
-    def forward_rows(self, x: torch.Tensor, batch: int, length: int) -> torch.Tensor:
-        """Block on a (B*L, D) fp32 residual buffer; returns the new residual buffer."""
+    def forward_rows(self, x: torch.Tensor, batch: int, length: int, inplace: bool = False) -> torch.Tensor:
+        """Block on a (B*L, D) fp32 residual buffer; returns the new residual buffer
+        (``x`` itself, updated in place, when ``inplace``)."""
         compute = self.config.compute_dtype
         D = x.shape[1]
         H = self.num_heads
@@ -88,9 +89,12 @@ class SelfAttentionBlock(nn.Module):
         o_buf, o = ops.merge_heads_out(batch, length, H, D // H, compute, x.device)
         ops.attention(ops.heads_view(qkv, batch, length, H, 0, D), ops.heads_view(qkv, batch, length, H, D, D),
                       ops.heads_view(qkv, batch, length, H, 2 * D, D), out=o)
-        x = apply_linear(self.out_proj, o_buf, residual=x, out_dtype=x.dtype, compute=compute)
+        # each residual element is read and then written by the same lane: in place is safe
+        x = apply_linear(self.out_proj, o_buf, residual=x, out_dtype=x.dtype, compute=compute,
+                         out=x if inplace else None)
         h = apply_linear(self.mlp[0], x, norm=self.norm_mlp, act="gelu", out_dtype=compute, compute=compute)
-        return apply_linear(self.mlp[2], h, residual=x, out_dtype=x.dtype, compute=compute)
+        return apply_linear(self.mlp[2], h, residual=x, out_dtype=x.dtype, compute=compute,
+                            out=x if inplace else None)
 
     def forward(self, latents: torch.Tensor) -> torch.Tensor:
         """(B, L, D) -> (B, L, D)."""
@@ -110,11 +114,11 @@ class PerceiverEncoder(nn.Module):
         self.self_attn_blocks = nn.ModuleList([SelfAttentionBlock(config) for _ in range(config.num_layers)])
         self.final_norm = nn.LayerNorm(config.latent_dim)
 
-    def encode_rows(self, x: torch.Tensor, batch: int, final_norm: bool = True) -> torch.Tensor:
+    def encode_rows(self, x: torch.Tensor, batch: int, final_norm: bool = True, inplace: bool = False) -> torch.Tensor:
         """Self-attention stack (+ final norm) on the (B*L, D) residual after cross-attention."""
         L = self.config.num_latents
         for block in self.self_attn_blocks:
-            x = block.forward_rows(x, batch, L)
+            x = block.forward_rows(x, batch, L, inplace=inplace)
         if not final_norm:
             return x
         return ops.layer_norm(x, self.final_norm.weight, self.final_norm.bias, self.final_norm.eps)
