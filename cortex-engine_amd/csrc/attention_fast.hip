@@ -3,11 +3,11 @@
 // queries).  Every attention of the Cortex forward runs here; per-key padding
 // masks, block masks, fp32 and other head dims use the general kernel.
 //
-// Workgroup: 8 wavefronts x 16 queries of one (sample, head).  Keys are taken in
+// Workgroup: 8 wavefronts x 16 or 32 queries of one (sample, head).  Keys are taken in
 // chunks of up to 4 tiles of 64: every load of a chunk is issued at once (one
-// memory round trip per chunk, not per tile), then its tiles are multiplied with
-// no further synchronisation.  Two workgroups share a CU (68 KiB LDS each), so one
-// loads while the other multiplies.
+// memory round trip per chunk, not per tile), and each tile is multiplied as soon
+// as its own loads have landed, while the later tiles' loads are still in flight.
+// Two workgroups share a CU (68 KiB LDS each).
 //
 //   scores  S^T = K Q^T    (A = K rows from LDS, B = Q held in registers): a lane
 //           holds 4 keys x 1 query per 16x16 sub-tile, so the softmax statistics of
@@ -21,7 +21,7 @@
 // so a lane of group g ends up with the 8 CONSECUTIVE keys 32c + 8g .. +7 for
 // key step c; V^T is then read as one 16-byte LDS word per fragment.
 //
-// Staging.  K: global -> LDS by direct transfers (global_load_lds_dwordx4), rows of
+// Staging.  K: global -> LDS by direct transfers (buffer_load_dwordx4 ... lds), rows of
 // 128 B with the 16-byte chunk c of row r stored at c ^ f(r), f chosen so that the
 // 16 rows of one fragment read cover all 16 bank groups.  V: each lane loads 4 head
 // dims of a pair of keys, packs (key, key+1) dwords and writes them transposed as
@@ -44,7 +44,6 @@ constexpr int AF_KT = 64;                        // keys per tile
 constexpr int AF_CH = 4;                         // tiles per chunk
 constexpr int AF_WAVES = 8;
 constexpr int AF_THREADS = 64 * AF_WAVES;
-constexpr int AF_QB = 16 * AF_WAVES;             // 128 queries per workgroup
 constexpr int AF_KTILE = AF_KT * 128;            // bytes of one K tile (64 keys x 64 bf16)
 constexpr int AF_VP = 144;                       // bytes per V^T row (64 keys + 16 B pad)
 constexpr int AF_VTILE = 64 * AF_VP;             // bytes of one V^T tile (64 head dims)
@@ -61,8 +60,20 @@ __device__ __forceinline__ int key_of(int st, int r) {
   return 32 * (st >> 1) + 8 * (r >> 2) + 4 * (st & 1) + (r & 3);
 }
 
-__global__ __launch_bounds__(AF_THREADS) __attribute__((amdgpu_waves_per_eu(4)))
+// s_waitcnt vmcnt(n) for the n of an unrolled tile index (lgkmcnt, expcnt untouched)
+__device__ __forceinline__ void af_wait_vm(int n) {
+  switch (n) {
+    case 0: __builtin_amdgcn_s_waitcnt(0 | 0x70 | 0xF00); break;
+    case 3: __builtin_amdgcn_s_waitcnt(3 | 0x70 | 0xF00); break;
+    case 6: __builtin_amdgcn_s_waitcnt(6 | 0x70 | 0xF00); break;
+    default: __builtin_amdgcn_s_waitcnt(9 | 0x70 | 0xF00); break;
+  }
+}
+
+template <int QG>  // 16-query groups per wavefront: each K/V fragment read feeds QG MFMAs
+__global__ __launch_bounds__(AF_THREADS) __attribute__((amdgpu_waves_per_eu(QG == 1 ? 4 : 2)))
 void attention_fast_kernel(AttnArgs a) {
+  constexpr int AF_QB = 16 * QG * AF_WAVES;  // queries per workgroup
   __shared__ __attribute__((aligned(1024))) unsigned char smem[AF_LDS];  // K tiles, then V^T tiles
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int fr = lane & 15, g = lane >> 4;
@@ -74,7 +85,7 @@ void attention_fast_kernel(AttnArgs a) {
   const int64_t bh = id / nqb;
   const int qblk = id % nqb;
   const int64_t b = bh / a.H, h = bh - b * a.H;
-  const int64_t q0 = (int64_t)qblk * AF_QB + wid * 16;
+  const int64_t q0 = (int64_t)qblk * AF_QB + wid * (16 * QG);
 
   int64_t len = a.Lk;
   const bf16* Kb;
@@ -92,18 +103,24 @@ void attention_fast_kernel(AttnArgs a) {
   if (len < 0) len = 0;
   const int nt = (int)cdiv(len, AF_KT);
 
-  // Q fragments: query q0 + fr, head-dim slice [32 ks + 8 g, +8)
-  bf16x8 qf[2];
-  {
-    const int64_t q = min(q0 + fr, a.Lq - 1);
+  // Q fragments: query q0 + 16 qg + fr, head-dim slice [32 ks + 8 g, +8)
+  bf16x8 qf[QG][2];
+#pragma unroll
+  for (int qg = 0; qg < QG; ++qg) {
+    const int64_t q = min(q0 + 16 * qg + fr, a.Lq - 1);
     const bf16* Qp = reinterpret_cast<const bf16*>(a.q) + b * a.q_sb + h * a.q_sh + q * a.q_sl;
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) qf[ks] = *reinterpret_cast<const bf16x8*>(Qp + ks * 32 + g * 8);
+    for (int ks = 0; ks < 2; ++ks) qf[qg][ks] = *reinterpret_cast<const bf16x8*>(Qp + ks * 32 + g * 8);
   }
 
-  // K transfer of this lane: 1 KiB block `wid` of a tile = rows 8 wid .. 8 wid + 7
+  // K transfer of this lane: 1 KiB block `wid` of a tile = rows 8 wid .. 8 wid + 7,
+  // through a buffer resource based at the (sample, head) start: the byte offsets
+  // stay below 2^32 (checked at launch).  Buffer transfers, unlike the global form,
+  // leave the compiler's load counting exact for the V register loads.
   const int k_row = wid * 8 + (lane >> 3);
-  const bf16* k_src = Kb + ((lane & 7) ^ kswz(k_row)) * 8;
+  const int64_t k_col = ((lane & 7) ^ kswz(k_row)) * 8;
+  const __amdgpu_buffer_rsrc_t k_rsrc =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<bf16*>(Kb), (short)0, (int)0xffffffffu, 0x00020000);
   // V of this lane: keys 2 kp, 2 kp + 1, head dims 4 dq .. 4 dq + 3; the two half-waves
   // take head-dim quads two apart (V^T rows 8 apart).
   const int half = lane >> 5, kp = lane & 31;
@@ -126,10 +143,15 @@ void attention_fast_kernel(AttnArgs a) {
 #pragma unroll
     for (int t = 0; t < 4; ++t) v_off[c][t] = (16 * t + fr) * AF_VP + (4 * c + g) * 16;
 
-  float m_run = -INFINITY;
-  f32x4 o_acc[4], l_acc = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+  float m_run[QG];
+  f32x4 o_acc[QG][4], l_acc[QG];
 #pragma unroll
-  for (int t = 0; t < 4; ++t) o_acc[t] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+  for (int qg = 0; qg < QG; ++qg) {
+    m_run[qg] = -INFINITY;
+    l_acc[qg] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int t = 0; t < 4; ++t) o_acc[qg][t] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+  }
   bf16x8 ones;
 #pragma unroll
   for (int j = 0; j < 8; ++j) ones[j] = (bf16)1.0f;
@@ -138,24 +160,30 @@ void attention_fast_kernel(AttnArgs a) {
   for (int kc = 0; kc < nt; kc += AF_CH) {
     const int nc = min(AF_CH, nt - kc);
     if (kc > 0) __syncthreads();  // every wave is done with the previous chunk's stages
-    // ---- issue every load of the chunk
+    // ---- issue every load of the chunk. Stages past the sample's last tile are filled
+    // too (with its last key, clamped) and never read: unconditional issue keeps the
+    // load counter exact, so each tile below waits for its own loads only.
     uint2 va[AF_CH], vb[AF_CH];
 #pragma unroll
     for (int j = 0; j < AF_CH; ++j) {
-      if (j < nc) {
-        const int64_t k0 = (int64_t)(kc + j) * AF_KT;
-        const int64_t kr = min(k0 + k_row, len - 1);
-        __builtin_amdgcn_global_load_lds(static_cast<const void*>(k_src + kr * a.k_sl),
-                                         static_cast<void*>(k_stage(j) + wid * 1024), 16, 0, 0);
-        const int64_t ka = min(k0 + 2 * kp, len - 1), kb = min(k0 + 2 * kp + 1, len - 1);
-        va[j] = *reinterpret_cast<const uint2*>(v_src + ka * a.v_sl);
-        vb[j] = *reinterpret_cast<const uint2*>(v_src + kb * a.v_sl);
-      }
+      const int64_t k0 = (int64_t)(kc + j) * AF_KT;
+      const int64_t kr = min(k0 + k_row, len - 1);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          k_rsrc, (__attribute__((address_space(3))) void*)(k_stage(j) + wid * 1024), 16,
+          (int)(uint32_t)((kr * a.k_sl + k_col) * 2), 0, 0, 0);
+      const int64_t ka = min(k0 + 2 * kp, len - 1), kb = min(k0 + 2 * kp + 1, len - 1);
+      va[j] = *reinterpret_cast<const uint2*>(v_src + ka * a.v_sl);
+      vb[j] = *reinterpret_cast<const uint2*>(v_src + kb * a.v_sl);
+      __builtin_amdgcn_sched_barrier(0);  // keep the issue order tile by tile (vmcnt below)
     }
-    // ---- V^T: dword (V[2kp][4dq+e], V[2kp+1][4dq+e]) into row 4dq+e, column kp
+    // Tiles are handed to the MFMAs one by one as their loads land: vmcnt counts the 3
+    // loads per tile in issue order, so vmcnt(3 (AF_CH-1-j)) means tile j's K transfer
+    // and V registers are in, and the raw barrier does not drain the later tiles' loads.
 #pragma unroll
     for (int j = 0; j < AF_CH; ++j) {
-      if (j < nc) {
+      if (j >= nc) break;
+      af_wait_vm(3 * (AF_CH - 1 - j));
+      {  // V^T: dword (V[2kp][4dq+e], V[2kp+1][4dq+e]) into row 4dq+e, column kp
         unsigned char* base = v_stage(j) + (4 * dq) * AF_VP + kp * 4;
         const uint32_t a0 = va[j].x, a1 = va[j].y, b0 = vb[j].x, b1 = vb[j].y;
         *reinterpret_cast<uint32_t*>(base + 0 * AF_VP) = (a0 & 0xffffu) | (b0 << 16);
@@ -163,21 +191,22 @@ void attention_fast_kernel(AttnArgs a) {
         *reinterpret_cast<uint32_t*>(base + 2 * AF_VP) = (a1 & 0xffffu) | (b1 << 16);
         *reinterpret_cast<uint32_t*>(base + 3 * AF_VP) = (a1 >> 16) | (b1 & 0xffff0000u);
       }
-    }
-    __syncthreads();  // K transfers landed and V^T written, for every wave
-
-    for (int j = 0; j < nc; ++j) {
+      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's V^T stores are done
+      __builtin_amdgcn_s_barrier();        // tile j's K transfers and V^T rows visible to all
       const int kt = kc + j;
       const unsigned char* ks_ = k_stage(j);
       const unsigned char* vs_ = v_stage(j);
-      f32x4 s[4];
+      f32x4 s[QG][4];
 #pragma unroll
       for (int st = 0; st < 4; ++st) {
         const bf16x8 k0f = *reinterpret_cast<const bf16x8*>(ks_ + k_off[st][0]);
         const bf16x8 k1f = *reinterpret_cast<const bf16x8*>(ks_ + k_off[st][1]);
-        f32x4 acc = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k0f, qf[0], acc, 0, 0, 0);
-        s[st] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k1f, qf[1], acc, 0, 0, 0);
+#pragma unroll
+        for (int qg = 0; qg < QG; ++qg) {
+          f32x4 acc = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k0f, qf[qg][0], acc, 0, 0, 0);
+          s[qg][st] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k1f, qf[qg][1], acc, 0, 0, 0);
+        }
       }
       const int64_t rem64 = len - (int64_t)kt * AF_KT;
       if (rem64 < AF_KT) {  // last, partial tile: mask keys past the sample's length
@@ -186,57 +215,75 @@ void attention_fast_kernel(AttnArgs a) {
         for (int st = 0; st < 4; ++st)
 #pragma unroll
           for (int i = 0; i < 4; ++i)
-            if (32 * (st >> 1) + 8 * g + 4 * (st & 1) + i >= rem) s[st][i] = -INFINITY;
+            if (32 * (st >> 1) + 8 * g + 4 * (st & 1) + i >= rem) {
+#pragma unroll
+              for (int qg = 0; qg < QG; ++qg) s[qg][st][i] = -INFINITY;
+            }
       }
-      float mx = s[0][0];
+      bf16x8 pf[QG][2];
 #pragma unroll
-      for (int st = 0; st < 4; ++st)
+      for (int qg = 0; qg < QG; ++qg) {
+        // Lane-local max first: the reference max only has to move (and the lane groups
+        // only have to agree on a new one) when some score exceeds it by AF_RESCALE.
+        float mx = s[qg][0][0];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) mx = fmaxf(mx, s[st][i]);
-      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-      const float m_tile = mx * sl;  // finite: every tile holds at least one valid key
-      if (kt == 0) {
-        m_run = m_tile;
-      } else if (__any(m_tile > m_run + AF_RESCALE)) {  // wave-uniform: rare after the first tile
-        const float m_new = fmaxf(m_run, m_tile);
-        const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
-        m_run = m_new;
-        l_acc *= alpha;
+        for (int st = 0; st < 4; ++st)
 #pragma unroll
-        for (int t = 0; t < 4; ++t) o_acc[t] *= alpha;
-      }
-      bf16x8 pf[2];
+          for (int i = 0; i < 4; ++i) mx = fmaxf(mx, s[qg][st][i]);
+        if (kt == 0 || __any(mx * sl > m_run[qg] + AF_RESCALE)) {  // wave-uniform: rare after the first tile
+          mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+          mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+          const float m_tile = mx * sl;  // finite: every tile holds at least one valid key
+          if (kt == 0) {
+            m_run[qg] = m_tile;
+          } else {
+            const float m_new = fmaxf(m_run[qg], m_tile);
+            const float alpha = __builtin_amdgcn_exp2f(m_run[qg] - m_new);
+            m_run[qg] = m_new;
+            l_acc[qg] *= alpha;
 #pragma unroll
-      for (int c = 0; c < 2; ++c)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          pf[c][i] = (bf16)__builtin_amdgcn_exp2f(fmaf(s[2 * c][i], sl, -m_run));  // -inf -> 0
-          pf[c][4 + i] = (bf16)__builtin_amdgcn_exp2f(fmaf(s[2 * c + 1][i], sl, -m_run));
+            for (int t = 0; t < 4; ++t) o_acc[qg][t] *= alpha;
+          }
         }
 #pragma unroll
+        for (int c = 0; c < 2; ++c)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            pf[qg][c][i] = (bf16)__builtin_amdgcn_exp2f(fmaf(s[qg][2 * c][i], sl, -m_run[qg]));  // -inf -> 0
+            pf[qg][c][4 + i] = (bf16)__builtin_amdgcn_exp2f(fmaf(s[qg][2 * c + 1][i], sl, -m_run[qg]));
+          }
+      }
+#pragma unroll
       for (int c = 0; c < 2; ++c) {
-        l_acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pf[c], l_acc, 0, 0, 0);
+#pragma unroll
+        for (int qg = 0; qg < QG; ++qg)
+          l_acc[qg] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pf[qg][c], l_acc[qg], 0, 0, 0);
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
           const bf16x8 vf = *reinterpret_cast<const bf16x8*>(vs_ + v_off[c][t]);
-          o_acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pf[c], o_acc[t], 0, 0, 0);
+#pragma unroll
+          for (int qg = 0; qg < QG; ++qg)
+            o_acc[qg][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pf[qg][c], o_acc[qg][t], 0, 0, 0);
         }
       }
     }
   }
+  af_wait_vm(0);  // the last chunk's unused stages: no transfer into LDS outlives the workgroup
 
-  const float l = l_acc[0];
-  const float inv = l > 0.0f ? 1.0f / l : 0.0f;
-  const int64_t q = q0 + fr;
-  if (q < a.Lq) {
-    bf16* O = reinterpret_cast<bf16*>(a.out) + b * a.o_sb + h * a.o_sh + q * a.o_sl;
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      bf16x4 v;
+  for (int qg = 0; qg < QG; ++qg) {
+    const float l = l_acc[qg][0];
+    const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+    const int64_t q = q0 + 16 * qg + fr;
+    if (q < a.Lq) {
+      bf16* O = reinterpret_cast<bf16*>(a.out) + b * a.o_sb + h * a.o_sh + q * a.o_sl;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) v[i] = (bf16)(o_acc[t][i] * inv);
-      *reinterpret_cast<bf16x4*>(O + 16 * t + 4 * g) = v;
+      for (int t = 0; t < 4; ++t) {
+        bf16x4 v;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] = (bf16)(o_acc[qg][t][i] * inv);
+        *reinterpret_cast<bf16x4*>(O + 16 * t + 4 * g) = v;
+      }
     }
   }
 }
@@ -253,9 +300,22 @@ int try_attention_fast(const AttnArgs& a, int dtype, hipStream_t stream) {
     if (s % 8) return 0;
   for (int64_t s : {a.o_sb, a.o_sh, a.o_sl})
     if (s % 4) return 0;
-  const int64_t nbh = a.B * a.H, nqb = cdiv(a.Lq, AF_QB);
+  const int64_t nbh = a.B * a.H;
+  // 32 queries per wavefront (K/V fragments read once per two MFMAs) while that still
+  // gives every CU a workgroup; 16 otherwise
+  static const int env_qg = [] {
+    const char* e = getenv("CORTEX_ATTN_QG");
+    return e ? atoi(e) : 0;
+  }();
+  const int qg = env_qg ? env_qg : (cdiv(a.Lq, 16 * 2 * AF_WAVES) * nbh >= 256 ? 2 : 1);
+  const int64_t nqb = cdiv(a.Lq, 16 * qg * AF_WAVES);
   if (nbh > 65535 || nqb * nbh > 0x7fffffffLL) return 0;
-  hipLaunchKernelGGL(attention_fast_kernel, dim3((unsigned)nqb, (unsigned)nbh), dim3(AF_THREADS), 0, stream, a);
+  // K byte offsets from a (sample, head) start are 32-bit buffer offsets
+  if (a.Lk > 0 && (a.Lk - 1) * a.k_sl * 2 + 128 > 0xffffffffLL) return 0;
+  if (qg == 2)
+    hipLaunchKernelGGL(attention_fast_kernel<2>, dim3((unsigned)nqb, (unsigned)nbh), dim3(AF_THREADS), 0, stream, a);
+  else
+    hipLaunchKernelGGL(attention_fast_kernel<1>, dim3((unsigned)nqb, (unsigned)nbh), dim3(AF_THREADS), 0, stream, a);
   CORTEX_CHECK_LAUNCH("attention_fast_kernel");
   return 1;
 }

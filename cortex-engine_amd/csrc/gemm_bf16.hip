@@ -35,15 +35,22 @@ __device__ __forceinline__ void wait_vm() {
   __builtin_amdgcn_s_waitcnt((n & 15) | 0x70 | 0xF00 | ((n >> 4) << 14));
 }
 
-template <int BM_, int BN_, int STAGES_, int WM_, int WN_>
+// KS > 1 splits K over KS groups of WM x WN wavefronts, each streaming its own part of
+// K through its own LDS ring; the partial tiles are summed through LDS before the
+// epilogue.  This doubles the wavefronts per CU for narrow outputs (N = 512) without
+// shrinking the wavefront tiles.
+template <int BM_, int BN_, int STAGES_, int WM_, int WN_, int KS_ = 1>
 struct BTile {
-  static constexpr int BM = BM_, BN = BN_, BK = 64, STAGES = STAGES_, WM = WM_, WN = WN_;
-  static constexpr int WAVES = WM * WN, THREADS = 64 * WAVES;
+  static constexpr int BM = BM_, BN = BN_, BK = 64, STAGES = STAGES_, WM = WM_, WN = WN_, KS = KS_;
+  static constexpr int WAVES = WM * WN, THREADS = 64 * WAVES * KS;  // WAVES: per K group
   static constexpr int TM = BM / WM / 16, TN = BN / WN / 16;  // 16x16 tiles per wavefront
   static constexpr int A_STAGE = BM * 128, W_STAGE = BN * 128;  // bytes (rows of 64 bf16)
   static constexpr int A_BLOCKS = A_STAGE / 1024 / WAVES, W_BLOCKS = W_STAGE / 1024 / WAVES;
   static constexpr int PER = A_BLOCKS + W_BLOCKS;              // transfers per wavefront per step
-  static constexpr int LDS = STAGES * (A_STAGE + W_STAGE);
+  static constexpr int RING = STAGES * (A_STAGE + W_STAGE);     // bytes per K group
+  static constexpr int RED = (KS > 1) ? WAVES * TM * TN * 4 * 64 * 4 : 0;  // partial tile exchange
+  static constexpr int LDS = (KS * RING > RED) ? KS * RING : RED;
+  static_assert(KS == 1 || KS == 2, "K split");
   static_assert(A_STAGE % (1024 * WAVES) == 0 && W_STAGE % (1024 * WAVES) == 0, "transfer split");
   static_assert(TM >= 1 && TN >= 2 && TN % 2 == 0 && STAGES >= 2, "shape");
   static_assert(PER * (STAGES - 1) < 64, "vmcnt range");
@@ -70,12 +77,14 @@ __global__ __launch_bounds__(TL::THREADS) void gemm_bf16_kernel(GemmArgs g) {
   constexpr bool IL = sizeof(TOUT) == 2;
   __shared__ __attribute__((aligned(1024))) unsigned char smem[TL::LDS];
 
-  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int kg = (tid >> 6) / TL::WAVES, wid = (tid >> 6) % TL::WAVES;  // K group, wave within it
   const int wm = wid / TL::WN, wn = wid % TL::WN;
   const int nbx = gridDim.x, total = gridDim.x * gridDim.y;
   int id = blockIdx.x + nbx * blockIdx.y;
   if ((total & 7) == 0) id = (id & 7) * (total >> 3) + (id >> 3);  // contiguous tiles per XCD
   const int m0 = (id / nbx) * BM, n0 = (id % nbx) * BN;
+  unsigned char* const ring = smem + kg * TL::RING;
   const int M = (int)g.M, N = (int)g.N, K = (int)g.K;
   const bf16* __restrict__ A = reinterpret_cast<const bf16*>(g.x);
   const bf16* __restrict__ W = reinterpret_cast<const bf16*>(g.w);
@@ -95,10 +104,12 @@ __global__ __launch_bounds__(TL::THREADS) void gemm_bf16_kernel(GemmArgs g) {
     const int r = (wid * WB + i) * 8 + (lane >> 3);
     w_src[i] = W + (int64_t)min(n0 + r, N - 1) * g.ld_w + ((lane & 7) ^ (IL ? swz_w(r) : swz_a(r))) * 8;
   }
-  auto a_stage = [&](int s) { return smem + s * TL::A_STAGE; };
-  auto w_stage = [&](int s) { return smem + S * TL::A_STAGE + s * TL::W_STAGE; };
+  auto a_stage = [&](int s) { return ring + s * TL::A_STAGE; };
+  auto w_stage = [&](int s) { return ring + S * TL::A_STAGE + s * TL::W_STAGE; };
+  const int nk = K / TL::BK / TL::KS;  // K steps of this group
+  const int kbase = kg * nk * TL::BK;
   auto issue = [&](int kt) {
-    const int s = kt % S, k0 = kt * TL::BK;
+    const int s = kt % S, k0 = kbase + kt * TL::BK;
 #pragma unroll
     for (int i = 0; i < AB; ++i)
       __builtin_amdgcn_global_load_lds(static_cast<const void*>(a_src[i] + k0),
@@ -148,7 +159,6 @@ __global__ __launch_bounds__(TL::THREADS) void gemm_bf16_kernel(GemmArgs g) {
       for (int j = 0; j < TN; ++j)
         acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf[j], af[i], acc[i][j], 0, 0, 0);
   };
-  const int nk = K / TL::BK;
 
   // The residual tile is fetched into registers before the main loop, so its latency
   // hides behind the MFMAs instead of stalling the epilogue.
@@ -156,6 +166,7 @@ __global__ __launch_bounds__(TL::THREADS) void gemm_bf16_kernel(GemmArgs g) {
   const int res_rows = g.res_rows > 0 ? (int)g.res_rows : M;
   float4 rv[RES ? TM : 1][RES ? TN : 1];
   if constexpr (RES && !IL) {
+    if (kg == 0) {
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
       const int m = min(m0 + wrow + i * 16 + fr, M - 1);
@@ -164,6 +175,7 @@ __global__ __launch_bounds__(TL::THREADS) void gemm_bf16_kernel(GemmArgs g) {
         const int n = min(n0 + wcol + 16 * j + 4 * g4, N - 4);
         rv[i][j] = *reinterpret_cast<const float4*>(res + (int64_t)(m % res_rows) * g.ld_res + n);
       }
+    }
     }
   }
 
@@ -206,6 +218,28 @@ __global__ __launch_bounds__(TL::THREADS) void gemm_bf16_kernel(GemmArgs g) {
       read_frags((kt + 1) % S, 0, af0, wf0);
     }
     mma(af1, wf1);
+  }
+
+  if constexpr (TL::KS > 1) {
+    // group 1 hands its partial tile to group 0 through LDS (lane-contiguous: conflict free)
+    float* red = reinterpret_cast<float*>(smem);
+    __syncthreads();  // every ring read is done; the exchange area may overwrite the rings
+    if (kg == 1) {
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) red[(((wid * TM + i) * TN + j) * 4 + r) * 64 + lane] = acc[i][j][r];
+    }
+    __syncthreads();
+    if (kg == 1) return;
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[i][j][r] += red[(((wid * TM + i) * TN + j) * 4 + r) * 64 + lane];
   }
 
   // ---- epilogue from registers.  Row m0 + wrow + 16 i + fr; columns
@@ -290,6 +324,7 @@ using B128x256s2 = BTile<128, 256, 2, 2, 4>;
 using B256x256s2 = BTile<256, 256, 2, 4, 2>;
 using B64x128s2 = BTile<64, 128, 2, 1, 2>;
 using B256x192s2 = BTile<256, 192, 2, 4, 2>;
+using B128x128s2k2 = BTile<128, 128, 2, 2, 2, 2>;
 
 int cu_count() {
   static int v = [] {
@@ -347,6 +382,8 @@ int dispatch(const GemmArgs& g, hipStream_t stream) {
 
 int dispatch_res(const GemmArgs& g, int t, hipStream_t stream) {
   switch (t) {
+    case 7:
+      return g.K % 128 ? 0 : launch<B128x128s2k2, ACT_NONE, true, float>(g, stream);
     case 1:
       return launch<B128x128s3, ACT_NONE, true, float>(g, stream);
     case 2:
@@ -376,13 +413,15 @@ int try_gemm_bf16(const GemmArgs& g, int x_dtype, int w_dtype, int w_layout, int
   const bool out_bf16 = g.out_dtype == DT_BF16;
   if (!out_bf16 && g.out_dtype != DT_F32) return 0;
   if (!aligned16(g.out) || g.ld_out % 8) return 0;
-  // Residual (fp32 in/out) GEMMs are memory bound and go to the pipelined kernel
-  // (LDS-staged epilogue, fully coalesced residual reads and stores) unless a tile of
-  // this kernel is asked for.
+  // Residual (fp32 in/out) GEMMs are memory bound.
   if (res) {
+    if (g.act) return 0;
     const char* e = getenv("CORTEX_RES_TILE");
-    const int t = e ? atoi(e) : -1;
-    if (t < 0 || t >= 10 || g.act) return 0;
+    int t = e ? atoi(e) : -1;
+    // default: 128x128 tiles with K split over two wave groups (eight wavefronts per CU)
+    // while the grid is at most one workgroup per CU; larger grids go to the pipelined kernel
+    if (t < 0) t = (g.K % 128 == 0 && cdiv(g.M, 128) * cdiv(g.N, 128) <= cu_count()) ? 7 : 10;
+    if (t >= 10) return 0;
     return dispatch_res(g, t, stream);
   }
   if (out_bf16)
