@@ -301,7 +301,11 @@ def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, scale: float
         km_sb = key_mask.stride(0) if key_mask.dim() == 2 else 0
     bm_sb = n_qt = n_kt = 0
     if block_mask is not None:
-        block_mask = block_mask.to(device=dev, dtype=torch.uint8).contiguous()
+        block_mask = block_mask.to(device=dev)
+        block_mask = (block_mask.view(torch.uint8) if block_mask.dtype == torch.bool
+                      else block_mask.to(torch.uint8)).contiguous()
+        if block_mask.dim() not in (2, 3) or (block_mask.dim() == 3 and block_mask.shape[0] != B):
+            raise ValueError(f"block_mask must be (n_q, n_k) or ({B}, n_q, n_k), got {tuple(block_mask.shape)}")
         n_qt, n_kt = block_mask.shape[-2], block_mask.shape[-1]
         bm_sb = block_mask.stride(0) if block_mask.dim() == 3 else 0
     qsb = q.stride(0) if q.shape[0] > 1 else 0
@@ -312,6 +316,38 @@ def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, scale: float
              nat.ptr(kv_offsets), nat.ptr(kv_lengths), nat.ptr(key_mask), km_sb,
              nat.ptr(block_mask), bm_sb, n_qt, n_kt, int(block_l), int(block_e), s,
              nat.ptr(out), out.stride(0), out.stride(1), out.stride(2), nat.stream_of(dev))
+    return out
+
+
+def temporal_block_mask(event_times: torch.Tensor, n_latents: int, max_time_bins: int, window_bins: int = 30,
+                        block_l: int = 64, block_e: int = 64, *, offsets: torch.Tensor | None = None,
+                        n_k: int | None = None) -> torch.Tensor:
+    """Device tile mask of reference sparse_xattn.py:152-200, as a bool tensor on the GPU.
+
+    Without ``offsets``: ``(n_q, ceil(E / block_e))`` over the E events, as the
+    reference.  With (B+1) CSR ``offsets``: ``(B, n_q, n_k)`` per-sample masks whose key
+    tiles start at each sample's first event; ``n_k`` defaults to ``ceil(E / block_e)``
+    (no host read of the per-sample counts) and tiles past a sample's end are False.
+    """
+    dev = nat.require_gpu(event_times, offsets, what="temporal_block_mask")
+    t = event_times.reshape(-1)
+    if t.dtype != torch.int64:
+        t = t.to(torch.int64)
+    E = t.shape[0]
+    n_q = math.ceil(n_latents / block_l)
+    if n_k is None:
+        n_k = math.ceil(E / block_e)
+    if offsets is None:
+        out = torch.empty((n_q, n_k), dtype=torch.bool, device=dev)
+        B, out_sb = 1, 0
+    else:
+        offsets = offsets.to(torch.int64).contiguous()
+        B = offsets.shape[0] - 1
+        out = torch.empty((B, n_q, n_k), dtype=torch.bool, device=dev)
+        out_sb = n_q * n_k
+    nat.call("cortex_temporal_block_mask", nat.ptr(t), t.stride(0) if E > 0 else 1, E, nat.ptr(offsets), B,
+             int(n_latents), int(max_time_bins), int(window_bins), int(block_l), int(block_e), n_q, n_k,
+             nat.ptr(out), out_sb, nat.stream_of(dev))
     return out
 
 

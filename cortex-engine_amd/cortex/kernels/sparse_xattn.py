@@ -52,9 +52,14 @@ def build_temporal_block_mask(event_times: torch.Tensor, n_latents: int, max_tim
     Same definition as reference sparse_xattn.py:152-200: latent i sits at
     ``i / L * T`` (fp32); a latent tile covers ``[int(min) - w, int(max) + w]``; an
     event tile covers the [min, max] time of its events; keep the pair iff the
-    intervals overlap.  Vectorised over tiles (the centres increase with i, so a
-    tile's min/max are its first/last centre).
+    intervals overlap.  Event times on a GPU are reduced there
+    (``ops.temporal_block_mask``, one kernel) and only the small mask is copied back;
+    host event times, as in the reference, are reduced on the host, vectorised over
+    tiles (the centres increase with i, so a tile's min/max are its first/last centre).
     """
+    if event_times.is_cuda:
+        return ops.temporal_block_mask(event_times, n_latents, max_time_bins, window_bins, BLOCK_L,
+                                       BLOCK_E).cpu()
     t = event_times.detach().to("cpu", torch.int64).reshape(-1)
     E = t.shape[0]
     n_q = math.ceil(n_latents / BLOCK_L)

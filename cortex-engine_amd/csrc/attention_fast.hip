@@ -1,7 +1,8 @@
-// Attention fast path for gfx950: bf16 operands, head dim 64, keys bounded only by
-// a per-sample length (dense self-attention, CSR cross-attention, broadcast
-// queries).  Every attention of the Cortex forward runs here; per-key padding
-// masks, block masks, fp32 and other head dims use the general kernel.
+// Attention fast path for gfx950: bf16 operands, head dim 64, keys bounded by a
+// per-sample length (dense self-attention, CSR cross-attention, broadcast queries)
+// and optionally by a (block_l, block_e) tile mask with block_l % 16 == 0 and
+// block_e % 64 == 0.  Every attention of the Cortex forward runs here; per-key
+// padding masks, other tile shapes, fp32 and other head dims use the general kernel.
 //
 // Workgroup: 8 wavefronts x 16 or 32 queries of one (sample, head).  Keys are taken in
 // chunks of up to 4 tiles of 64: every load of a chunk is issued at once (one
@@ -70,7 +71,20 @@ __device__ __forceinline__ void af_wait_vm(int n) {
   }
 }
 
-template <int QG>  // 16-query groups per wavefront: each K/V fragment read feeds QG MFMAs
+// Block-mask view of one sample: tile (qi, kj) is allowed iff m[qi * n_kt + kj] != 0;
+// kj of a 64-key tile t is t / kpt (block_e = 64 kpt).
+struct AfMask {
+  const uint8_t* m;
+  int64_t n_qt, n_kt, kpt;
+  __device__ bool at(int64_t qi, int64_t kj) const {
+    return qi >= 0 && qi < n_qt && kj < n_kt && m[qi * n_kt + kj] != 0;
+  }
+};
+
+// 16-query groups per wavefront (QG): each K/V fragment read feeds QG MFMAs.  MASK: a
+// (block_l, block_e) tile mask; the workgroup visits only the 64-key tiles that one of
+// its query tiles allows, and a wavefront multiplies only those its own queries allow.
+template <int QG, bool MASK>
 __global__ __launch_bounds__(AF_THREADS) __attribute__((amdgpu_waves_per_eu(QG == 1 ? 4 : 2)))
 void attention_fast_kernel(AttnArgs a) {
   constexpr int AF_QB = 16 * QG * AF_WAVES;  // queries per workgroup
@@ -157,16 +171,64 @@ void attention_fast_kernel(AttnArgs a) {
   for (int j = 0; j < 8; ++j) ones[j] = (bf16)1.0f;
   const float sl = a.scale_log2;
 
-  for (int kc = 0; kc < nt; kc += AF_CH) {
-    const int nc = min(AF_CH, nt - kc);
-    if (kc > 0) __syncthreads();  // every wave is done with the previous chunk's stages
-    // ---- issue every load of the chunk. Stages past the sample's last tile are filled
-    // too (with its last key, clamped) and never read: unconditional issue keeps the
-    // load counter exact, so each tile below waits for its own loads only.
+  // ---- tile schedule: the dense case takes tiles in order; with a mask, the tiles one
+  // of the workgroup's query tiles allows, found 64 at a time by a ballot (every wave
+  // computes the same, wave-uniform schedule).
+  AfMask mk{};
+  int64_t qrow[QG];  // query tile of each 16-query group
+  int64_t qa = 0, qb = -1;  // query tiles of the workgroup
+  if (MASK) {
+    mk = AfMask{a.block_mask + b * a.bm_sb, a.n_qt, a.n_kt, a.block_e / AF_KT};
+#pragma unroll
+    for (int qg = 0; qg < QG; ++qg) qrow[qg] = (q0 + 16 * qg) / a.block_l;
+    qa = (int64_t)qblk * AF_QB / a.block_l;
+    qb = min((int64_t)qblk * AF_QB + AF_QB - 1, a.Lq - 1) / a.block_l;
+  }
+  auto wg_window = [&](int base) -> uint64_t {  // allowed tiles base .. base + 63
+    const int t = base + lane;
+    bool ok = false;
+    if (t < nt) {
+      const int64_t kj = t / mk.kpt;
+      for (int64_t qi = qa; qi <= qb && !ok; ++qi) ok = mk.at(qi, kj);
+    }
+    return __ballot(ok);
+  };
+  int wbase = 0, kc = 0;
+  uint64_t pend = MASK ? wg_window(0) : 0;
+
+  for (bool first = true;; first = false) {
+    int tl[AF_CH];
+    int nc = 0;
+    if (MASK) {
+#pragma unroll
+      for (int j = 0; j < AF_CH; ++j) {
+        while (pend == 0 && wbase + 64 < nt) {
+          wbase += 64;
+          pend = wg_window(wbase);
+        }
+        if (pend != 0) {
+          tl[j] = wbase + __builtin_ctzll(pend);
+          pend &= pend - 1;
+          nc = j + 1;
+        } else {
+          tl[j] = j > 0 ? tl[j - 1] : 0;  // loaded, never used
+        }
+      }
+    } else {
+      nc = min(AF_CH, nt - kc);
+#pragma unroll
+      for (int j = 0; j < AF_CH; ++j) tl[j] = kc + j;
+      kc += AF_CH;
+    }
+    if (nc <= 0) break;
+    if (!first) __syncthreads();  // every wave is done with the previous chunk's stages
+    // ---- issue every load of the chunk. Stages past the chunk's last tile are filled
+    // too (clamped keys) and never read: unconditional issue keeps the load counter
+    // exact, so each tile below waits for its own loads only.
     uint2 va[AF_CH], vb[AF_CH];
 #pragma unroll
     for (int j = 0; j < AF_CH; ++j) {
-      const int64_t k0 = (int64_t)(kc + j) * AF_KT;
+      const int64_t k0 = (int64_t)tl[j] * AF_KT;
       const int64_t kr = min(k0 + k_row, len - 1);
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
           k_rsrc, (__attribute__((address_space(3))) void*)(k_stage(j) + wid * 1024), 16,
@@ -193,7 +255,15 @@ void attention_fast_kernel(AttnArgs a) {
       }
       __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's V^T stores are done
       __builtin_amdgcn_s_barrier();        // tile j's K transfers and V^T rows visible to all
-      const int kt = kc + j;
+      const int kt = tl[j];
+      bool okq[QG];  // this 16-query group multiplies tile kt
+      bool any = !MASK;
+#pragma unroll
+      for (int qg = 0; qg < QG; ++qg) {
+        okq[qg] = !MASK || mk.at(qrow[qg], kt / mk.kpt);
+        any = any || okq[qg];
+      }
+      if (!any) continue;
       const unsigned char* ks_ = k_stage(j);
       const unsigned char* vs_ = v_stage(j);
       f32x4 s[QG][4];
@@ -204,6 +274,7 @@ void attention_fast_kernel(AttnArgs a) {
 #pragma unroll
         for (int qg = 0; qg < QG; ++qg) {
           f32x4 acc = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+          if (!okq[qg]) continue;
           acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k0f, qf[qg][0], acc, 0, 0, 0);
           s[qg][st] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k1f, qf[qg][1], acc, 0, 0, 0);
         }
@@ -223,6 +294,7 @@ void attention_fast_kernel(AttnArgs a) {
       bf16x8 pf[QG][2];
 #pragma unroll
       for (int qg = 0; qg < QG; ++qg) {
+        if (!okq[qg]) continue;
         // Lane-local max first: the reference max only has to move (and the lane groups
         // only have to agree on a new one) when some score exceeds it by AF_RESCALE.
         float mx = s[qg][0][0];
@@ -230,11 +302,12 @@ void attention_fast_kernel(AttnArgs a) {
         for (int st = 0; st < 4; ++st)
 #pragma unroll
           for (int i = 0; i < 4; ++i) mx = fmaxf(mx, s[qg][st][i]);
-        if (kt == 0 || __any(mx * sl > m_run[qg] + AF_RESCALE)) {  // wave-uniform: rare after the first tile
+        // wave-uniform, rare after the group's first tile (m_run = -inf always enters)
+        if (__any(mx * sl > m_run[qg] + AF_RESCALE)) {
           mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
           mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
           const float m_tile = mx * sl;  // finite: every tile holds at least one valid key
-          if (kt == 0) {
+          if (m_run[qg] == -INFINITY) {
             m_run[qg] = m_tile;
           } else {
             const float m_new = fmaxf(m_run[qg], m_tile);
@@ -257,13 +330,13 @@ void attention_fast_kernel(AttnArgs a) {
       for (int c = 0; c < 2; ++c) {
 #pragma unroll
         for (int qg = 0; qg < QG; ++qg)
-          l_acc[qg] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pf[qg][c], l_acc[qg], 0, 0, 0);
+          if (okq[qg]) l_acc[qg] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pf[qg][c], l_acc[qg], 0, 0, 0);
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
           const bf16x8 vf = *reinterpret_cast<const bf16x8*>(vs_ + v_off[c][t]);
 #pragma unroll
           for (int qg = 0; qg < QG; ++qg)
-            o_acc[qg][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pf[qg][c], o_acc[qg][t], 0, 0, 0);
+            if (okq[qg]) o_acc[qg][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pf[qg][c], o_acc[qg][t], 0, 0, 0);
         }
       }
     }
@@ -293,7 +366,10 @@ bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 }  // namespace
 
 int try_attention_fast(const AttnArgs& a, int dtype, hipStream_t stream) {
-  if (dtype != DT_BF16 || a.Dh != 64 || a.key_mask || a.block_mask) return 0;
+  if (dtype != DT_BF16 || a.Dh != 64 || a.key_mask) return 0;
+  // a tile mask must give each 16-query group and each 64-key tile one mask entry
+  const bool mask = a.block_mask != nullptr;
+  if (mask && (a.block_l % 16 != 0 || a.block_e % AF_KT != 0 || a.n_qt <= 0 || a.n_kt <= 0)) return 0;
   if (!(a.scale_log2 > 0.0f) || !(a.scale_log2 < INFINITY)) return 0;
   if (!al16(a.q) || !al16(a.k) || !al16(a.v) || ((uintptr_t)a.out & 7)) return 0;
   for (int64_t s : {a.q_sb, a.q_sh, a.q_sl, a.k_sb, a.k_sh, a.k_sl, a.v_sb, a.v_sh, a.v_sl})
@@ -307,15 +383,20 @@ int try_attention_fast(const AttnArgs& a, int dtype, hipStream_t stream) {
     const char* e = getenv("CORTEX_ATTN_QG");
     return e ? atoi(e) : 0;
   }();
-  const int qg = env_qg ? env_qg : (cdiv(a.Lq, 16 * 2 * AF_WAVES) * nbh >= 256 ? 2 : 1);
+  const int qg = env_qg == 1 || env_qg == 2 ? env_qg : (cdiv(a.Lq, 16 * 2 * AF_WAVES) * nbh >= 256 ? 2 : 1);
   const int64_t nqb = cdiv(a.Lq, 16 * qg * AF_WAVES);
   if (nbh > 65535 || nqb * nbh > 0x7fffffffLL) return 0;
   // K byte offsets from a (sample, head) start are 32-bit buffer offsets
   if (a.Lk > 0 && (a.Lk - 1) * a.k_sl * 2 + 128 > 0xffffffffLL) return 0;
-  if (qg == 2)
-    hipLaunchKernelGGL(attention_fast_kernel<2>, dim3((unsigned)nqb, (unsigned)nbh), dim3(AF_THREADS), 0, stream, a);
+  const dim3 grid((unsigned)nqb, (unsigned)nbh);
+  if (qg == 2 && mask)
+    hipLaunchKernelGGL((attention_fast_kernel<2, true>), grid, dim3(AF_THREADS), 0, stream, a);
+  else if (qg == 2)
+    hipLaunchKernelGGL((attention_fast_kernel<2, false>), grid, dim3(AF_THREADS), 0, stream, a);
+  else if (mask)
+    hipLaunchKernelGGL((attention_fast_kernel<1, true>), grid, dim3(AF_THREADS), 0, stream, a);
   else
-    hipLaunchKernelGGL(attention_fast_kernel<1>, dim3((unsigned)nqb, (unsigned)nbh), dim3(AF_THREADS), 0, stream, a);
+    hipLaunchKernelGGL((attention_fast_kernel<1, false>), grid, dim3(AF_THREADS), 0, stream, a);
   CORTEX_CHECK_LAUNCH("attention_fast_kernel");
   return 1;
 }

@@ -177,6 +177,18 @@ int cortex_attention(int dtype, int64_t B, int64_t H, int64_t Lq, int64_t Lk, in
                      int64_t block_e, float scale, void* out, int64_t o_sb, int64_t o_sh, int64_t o_sl,
                      hipStream_t stream);
 
+/* build_temporal_block_mask (reference cortex/kernels/sparse_xattn.py:152-200) on the
+ * device.  out[b * out_sb + qi * n_k + kj] = 1 iff query tile qi's window
+ * [int(c(first)) - w, int(c(last)) + w], c(i) = float32(i) / n_latents * max_time_bins,
+ * overlaps [min t, max t] of key tile kj's events (block_e events from the sample's
+ * start).  offsets == NULL: one sample of E events (the reference's (n_q, n_k) mask);
+ * otherwise (B+1) CSR offsets and a per-sample mask, key tiles past a sample's end 0.
+ * Bit-exact with the reference's CPU loop. */
+int cortex_temporal_block_mask(const int64_t* event_times, int64_t t_stride, int64_t E, const int64_t* offsets,
+                               int64_t B, int64_t n_latents, int64_t max_time_bins, int64_t window_bins,
+                               int64_t block_l, int64_t block_e, int64_t n_q, int64_t n_k, uint8_t* out,
+                               int64_t out_sb, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif
