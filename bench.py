@@ -309,6 +309,44 @@ def latency_b1(model, dev, n_requests: int, per_sample: int = 512):
             "requests": n_requests, "events_per_request": per_sample, "path": "hip graph replay"}
 
 
+def worker_latency(model, dev, n_requests: int, per_sample: int = 512):
+    """The serving worker end to end, one B=1 request at a time (reference payload contract:
+    a list of event dicts), and a B=256 batch of columnar payloads: host packing, one pinned
+    H2D, graph replay, D2H of the behaviour, wall clock."""
+    from cortex.models.config import CORTEX_S
+    from cortex.serve import InferenceWorker
+
+    w = InferenceWorker(model, CORTEX_S, dev, max_batch_size=256)
+    nid, tb, val, _ = make_events(1, per_sample, seed=8)
+    one = [{"request_id": "r0", "events": [{"neuron_id": int(a), "time_bin": int(b), "value": int(c)}
+                                           for a, b, c in zip(nid, tb, val)]}]
+    lat = []
+    for i in range(n_requests + 20):
+        t0 = time.perf_counter()
+        w._run_batch_sync(one)
+        if i >= 20:
+            lat.append((time.perf_counter() - t0) * 1e3)
+    lat.sort()
+    rng = np.random.default_rng(12)
+    counts = np.clip(rng.poisson(512, 256), 64, 2048)
+    nid, tb, val, _ = make_events(256, counts, seed=13)
+    cuts = np.cumsum(counts)[:-1]
+    batch = [{"request_id": f"r{i}", "events": {"neuron_id": a, "time_bin": b, "value": c}}
+             for i, (a, b, c) in enumerate(zip(np.split(nid, cuts), np.split(tb, cuts), np.split(val, cuts)))]
+    for _ in range(3):
+        w._run_batch_sync(batch)
+    reps = 10
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        w._run_batch_sync(batch)
+    sec = (time.perf_counter() - t0) / reps
+    w.shutdown()
+    return {"b1_p50_ms": round(lat[len(lat) // 2], 4), "b1_p99_ms": round(lat[int(len(lat) * 0.99) - 1], 4),
+            "b1_requests": n_requests, "b1_events": per_sample, "b1_payload": "list of event dicts",
+            "b256_ms_per_batch": round(sec * 1e3, 3), "b256_samples_per_s": round(256 / sec, 1),
+            "b256_events": int(counts.sum()), "b256_payload": "columnar arrays"}
+
+
 def serving_sweep(model, dev, batches=(1, 8, 32, 128, 256), reps: int = 20):
     """Serving-shaped forward: E_b = clip(Poisson(512), 64, 2048) per sample, one graph per batch."""
     from cortex.runtime import CapturedForward
@@ -456,6 +494,8 @@ def main() -> int:
         log(f"bench: latency {extra['latency_b1']}")
         extra["serving_sweep"] = serving_sweep(model, dev)
         log(f"bench: serving {extra['serving_sweep']}")
+        extra["serve_worker"] = worker_latency(model, dev, args.latency_requests)
+        log(f"bench: serve worker {extra['serve_worker']}")
     cpu = None
     if not (args.no_cpu_baseline or args.quick):
         log("bench: CPU baseline")

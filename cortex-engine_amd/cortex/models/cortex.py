@@ -124,14 +124,33 @@ class CortexModel(nn.Module):
         return {"behavior": self._forward_csr(neuron_ids, time_bins, values, batch_indices, int(batch_size),
                                               err_flag)}
 
+    def forward_csr(self, neuron_ids: torch.Tensor, time_bins: torch.Tensor, values: torch.Tensor,
+                    offsets: torch.Tensor, *, err_flag: torch.Tensor | None = None) -> torch.Tensor:
+        """Events already grouped by sample -> behaviour ``(B, behavior_dim)`` fp32.
+
+        Sample b owns events ``[offsets[b], offsets[b+1])`` (``offsets``: (B+1,) int64 on
+        the device, non-decreasing from 0).  Events past ``offsets[B]`` (padding of a
+        fixed-size buffer) are ignored.  Skips the pack plan: a server that builds the
+        batch sample by sample has the CSR layout for free.
+        """
+        if not (neuron_ids.shape == time_bins.shape == values.shape):
+            raise ValueError(
+                f"shape mismatch: neuron_ids={neuron_ids.shape}, time_bins={time_bins.shape}, values={values.shape}")
+        return self._forward_planned(neuron_ids, time_bins, values, offsets, None, offsets.shape[0] - 1, err_flag)
+
     def _forward_csr(self, neuron_ids, time_bins, values, batch_indices, B: int, err_flag=None) -> torch.Tensor:
+        offsets, order, _ = ops.pack_plan(batch_indices, B, err=err_flag)
+        return self._forward_planned(neuron_ids, time_bins, values, offsets, order, B, err_flag)
+
+    def _forward_planned(self, neuron_ids, time_bins, values, offsets, order, B: int, err_flag) -> torch.Tensor:
+        """The forward from a CSR plan: row r of the packed events is event ``order[r]``
+        (``r`` itself when ``order`` is None); rows past ``offsets[B]`` are ignored."""
         cfg = self.config
         compute = cfg.compute_dtype
         tok = self.tokenizer
         enc = self.encoder
         xa = enc.cross_attn
         D, L, H = cfg.latent_dim, cfg.num_latents, xa.num_heads
-        offsets, order, _ = ops.pack_plan(batch_indices, B, err=err_flag)
         tables = (tok.neuron_emb.weight, tok.time_emb.weight, tok.value_emb.weight)
         E = neuron_ids.shape[0]
         if compute == torch.bfloat16 and not xa.kv_proj._forward_pre_hooks and fused_tokens_ok(tables, xa.norm_kv):

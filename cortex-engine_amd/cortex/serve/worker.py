@@ -1,0 +1,267 @@
+"""Batched inference worker on gfx950 (reference cortex/serve/worker.py:95-249).
+
+Same surface as the reference's ``InferenceWorker``: ``run_batch`` (async, one
+single-thread executor so forward passes never overlap), ``_run_batch_sync``,
+``warmup``, ``ready``, ``shutdown``, and the payload and result dicts of its
+contract (worker.py:22-31).  What changes is the way a batch reaches the GPU:
+
+* The payloads are already grouped by request, so the batch is CSR by
+  construction: the host writes the events sample after sample plus the (B+1)
+  offsets; the device never sorts ``batch_indices``.
+* Neuron ids, time bins, values and offsets go into ONE pinned host buffer laid
+  out like the device input buffer, and cross in one asynchronous copy.
+* The forward for a given (B, event bucket) is captured once as a HIP graph and
+  replayed (about 60 launches become one); event counts are rounded up to a
+  bucket, the padding events lie past ``offsets[B]`` and are never attended.
+* The (B, behavior_dim) result comes back through a pinned buffer; the only host
+  synchronisation is the one wait for that copy.
+
+Payload ``events`` may be the reference's list of ``{"neuron_id", "time_bin",
+"value"}`` dicts or, as an extension, a mapping of three equal-length integer
+arrays ``{"neuron_id": ..., "time_bin": ..., "value": ...}`` (no per-event Python
+work).  Request metrics (the reference's Prometheus gauges) are not kept here.
+"""
+
+from __future__ import annotations
+
+import asyncio
+import time
+from collections import OrderedDict
+from concurrent.futures import ThreadPoolExecutor
+from typing import Any
+
+import numpy as np
+import torch
+from torch import nn
+
+from cortex.models.config import CortexConfig
+
+_FIELDS = ("neuron_id", "time_bin", "value")
+
+
+def load_model(config: CortexConfig, checkpoint_path: str | None = None,
+               device: torch.device | None = None) -> nn.Module:
+    """``CortexModel`` on ``device`` (reference worker.py:62-92).
+
+    A checkpoint is read with ``torch.load(weights_only=True)``: plain tensors and
+    containers only.  The reference's ``{"model_state_dict": ...}`` wrapper and a bare
+    state dict are both accepted; missing or unexpected keys are tolerated
+    (``strict=False``) as there.
+    """
+    from cortex.models.cortex import CortexModel
+
+    if device is None:
+        if not torch.cuda.is_available():
+            raise RuntimeError("the Cortex gfx950 forward needs a ROCm device")
+        device = torch.device("cuda")
+    model = CortexModel(config).to(device).eval()
+    if checkpoint_path:
+        try:
+            payload = torch.load(checkpoint_path, map_location=device, weights_only=True)
+        except FileNotFoundError:
+            return model
+        state = payload.get("model_state_dict", payload)
+        model.load_state_dict(state, strict=False)
+    return model
+
+
+def event_bucket(n: int, fine: int = 4096) -> int:
+    """Padded event count of a batch: the next power of two up to 16384 (at least
+    256), then the next multiple of ``fine``; the padding costs at most 2x of the
+    event-side work (tokenizer, kv projection) for small batches and < ``fine``
+    rows for large ones, and bounds the number of distinct captured graphs."""
+    if n <= 256:
+        return 256
+    if n <= 16384:
+        return 1 << (n - 1).bit_length()
+    return -(-n // fine) * fine
+
+
+def _as_columns(events: Any) -> tuple[np.ndarray, np.ndarray, np.ndarray]:
+    if isinstance(events, dict):
+        cols = [np.asarray(events[f], dtype=np.int64).reshape(-1) for f in _FIELDS]
+        if not (cols[0].shape == cols[1].shape == cols[2].shape):
+            raise ValueError("columnar events need equal-length neuron_id, time_bin and value arrays")
+        return cols[0], cols[1], cols[2]
+    n = len(events)
+    out = np.empty((3, n), dtype=np.int64)
+    for i, ev in enumerate(events):
+        out[0, i] = int(ev["neuron_id"])
+        out[1, i] = int(ev["time_bin"])
+        out[2, i] = int(ev["value"])
+    return out[0], out[1], out[2]
+
+
+def pack_payloads(payloads: list[dict[str, Any]], bucket: bool = True,
+                  out: np.ndarray | None = None) -> tuple[np.ndarray, int, int, int]:
+    """Payloads -> the flat int64 input ``[nid (Eb) | tb (Eb) | val (Eb) | offsets (B+1)]``.
+
+    Returns ``(flat, B, E, Eb)``: B ends at the last payload with events (the
+    reference's ``max(batch_indices) + 1``, worker.py:174-181 and cortex.py:140), E is
+    the number of real events, Eb the padded count (``event_bucket(E)`` when
+    ``bucket``, else E).  Events keep the payload order, so sample b owns rows
+    ``[offsets[b], offsets[b+1])``; padding rows are zeros.  B = 0 when no payload has
+    an event.  ``out`` receives the data when it is long enough (``3 Eb + B + 1``).
+    """
+    cols = [_as_columns(p.get("events", [])) for p in payloads]
+    counts = np.array([c[0].shape[0] for c in cols], dtype=np.int64)
+    nonempty = np.flatnonzero(counts)
+    if nonempty.size == 0:
+        return np.zeros(1, dtype=np.int64), 0, 0, 0
+    B = int(nonempty[-1]) + 1
+    E = int(counts[:B].sum())
+    Eb = event_bucket(E) if bucket else E
+    n = 3 * Eb + B + 1
+    h = out[:n] if out is not None and out.shape[0] >= n else np.empty(n, dtype=np.int64)
+    for f in range(3):
+        np.concatenate([c[f] for c in cols[:B]], out=h[f * Eb:f * Eb + E])
+        h[f * Eb + E:(f + 1) * Eb] = 0  # padding events: valid table rows, never attended
+    h[3 * Eb] = 0
+    np.cumsum(counts[:B], out=h[3 * Eb + 1:n])
+    return h, B, E, Eb
+
+
+class _CsrGraph:
+    """The forward for one (batch, event bucket), captured on ``stream``.
+
+    ``inp`` is the device input buffer ``[nid (E) | tb (E) | val (E) | offsets (B+1)]``.
+    """
+
+    def __init__(self, model: nn.Module, batch: int, events: int, device: torch.device,
+                 stream: torch.cuda.Stream, pool: Any) -> None:
+        self.batch, self.events = batch, events
+        self.inp = torch.zeros(3 * events + batch + 1, dtype=torch.int64, device=device)  # empty samples
+        self.err = torch.zeros(1, dtype=torch.int32, device=device)
+        E = events
+        self._args = (self.inp[:E], self.inp[E:2 * E], self.inp[2 * E:3 * E], self.inp[3 * E:])
+        self.model = model
+        with torch.cuda.stream(stream), torch.inference_mode():
+            for _ in range(2):  # weights images, batch-invariant projections, allocator warm
+                self._run()
+        stream.synchronize()
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph, pool=pool, stream=stream), torch.inference_mode():
+            self.out = self._run()
+
+    def _run(self) -> torch.Tensor:
+        nid, tb, val, off = self._args
+        return self.model.forward_csr(nid, tb, val, off, err_flag=self.err)
+
+
+class InferenceWorker:
+    """Batched inference worker (reference worker.py:95-249); one model, one GPU.
+
+    ``use_graphs`` replays a captured graph per (B, event bucket), keeping at most
+    ``max_graphs`` of them (least recently used evicted); all share one memory pool,
+    which is safe because batches never overlap.
+    """
+
+    def __init__(self, model: nn.Module, config: CortexConfig, device: torch.device, max_batch_size: int = 32,
+                 *, use_graphs: bool = True, max_graphs: int = 64) -> None:
+        device = torch.device(device)
+        if device.type != "cuda":
+            raise RuntimeError("InferenceWorker runs the gfx950 forward; it needs a ROCm device")
+        if device.index is None:
+            device = torch.device("cuda", torch.cuda.current_device())
+        self.model = model
+        self.config = config
+        self.device = device
+        self.max_batch_size = max_batch_size
+        self.use_graphs = use_graphs
+        self.max_graphs = max_graphs
+        self._executor = ThreadPoolExecutor(max_workers=1, thread_name_prefix="inference")
+        self._stream = torch.cuda.Stream(device=device)  # default priority
+        self._graphs: OrderedDict[tuple[int, int], _CsrGraph] = OrderedDict()
+        self._pool = torch.cuda.graph_pool_handle() if use_graphs else None
+        self._host_in = torch.empty(1 << 16, dtype=torch.int64).pin_memory()
+        self._host_out = torch.empty(1024, dtype=torch.float32).pin_memory()
+        self._host_err = torch.zeros(1, dtype=torch.int32).pin_memory()
+        self._done = torch.cuda.Event()
+        self._loaded = False
+
+    # ------------------------------------------------------------------ API
+
+    def warmup(self, n_iters: int = 3) -> None:
+        """Dummy batches of 64 events each (reference worker.py:136-149)."""
+        dummy = [{"request_id": f"warmup_{i}", "events": [{"neuron_id": 0, "time_bin": 0, "value": 0}] * 64}
+                 for i in range(min(n_iters, self.max_batch_size))]
+        for _ in range(n_iters):
+            self._run_batch_sync(dummy)
+        self._loaded = True
+
+    @property
+    def ready(self) -> bool:
+        return self._loaded
+
+    async def run_batch(self, payloads: list[dict[str, Any]]) -> list[dict[str, Any]]:
+        """Async entry point: the batch runs on the worker's executor thread."""
+        if not payloads:
+            return []
+        loop = asyncio.get_running_loop()
+        return await loop.run_in_executor(self._executor, self._run_batch_sync, payloads)
+
+    def shutdown(self) -> None:
+        self._executor.shutdown(wait=False)
+
+    # ------------------------------------------------------------------ batch
+
+    def _run_batch_sync(self, payloads: list[dict[str, Any]]) -> list[dict[str, Any]]:
+        """One synchronous forward over ``payloads`` (runs on the executor thread).
+
+        As in the reference, the model batch ends at the last payload that has
+        events (``max(batch_indices) + 1``); later payloads get zeros.
+        """
+        t0 = time.perf_counter()
+        dim = self.config.behavior_dim
+        flat, B, E, Eb = pack_payloads(payloads, self.use_graphs, self._host_in.numpy())
+        if B == 0:
+            ms = (time.perf_counter() - t0) * 1000
+            return [{"request_id": p["request_id"], "behavior": [0.0] * dim, "inference_ms": ms} for p in payloads]
+        n_in = 3 * Eb + B + 1
+        if flat.ctypes.data != self._host_in.data_ptr():  # did not fit: grow the pinned buffer
+            self._host_in = torch.empty(max(n_in, 2 * self._host_in.numel()), dtype=torch.int64).pin_memory()
+            self._host_in.numpy()[:n_in] = flat[:n_in]
+        behavior = self._forward(B, Eb, n_in)
+        ms = (time.perf_counter() - t0) * 1000
+        rows = behavior.tolist()
+        return [{"request_id": p["request_id"], "behavior": rows[i] if i < B else [0.0] * dim, "inference_ms": ms}
+                for i, p in enumerate(payloads)]
+
+    def _forward(self, B: int, Eb: int, n_in: int) -> np.ndarray:
+        dim = self.config.behavior_dim
+        if self._host_out.numel() < B * dim:
+            self._host_out = torch.empty(max(B * dim, 2 * self._host_out.numel()), dtype=torch.float32).pin_memory()
+        src = self._host_in[:n_in]
+        with torch.cuda.device(self.device), torch.cuda.stream(self._stream):
+            if self.use_graphs:
+                g = self._graph(B, Eb)
+                g.inp.copy_(src, non_blocking=True)
+                g.err.zero_()
+                g.graph.replay()
+                out, err = g.out, g.err
+            else:
+                inp = src.to(self.device, non_blocking=True)
+                err = torch.zeros(1, dtype=torch.int32, device=self.device)
+                with torch.inference_mode():
+                    out = self.model.forward_csr(inp[:Eb], inp[Eb:2 * Eb], inp[2 * Eb:3 * Eb], inp[3 * Eb:],
+                                                 err_flag=err)
+            host = self._host_out[:B * dim].view(B, dim)
+            host.copy_(out, non_blocking=True)
+            self._host_err.copy_(err, non_blocking=True)
+            self._done.record(self._stream)
+        self._done.synchronize()
+        if int(self._host_err[0]) != 0:
+            raise IndexError("event index out of range (neuron_id, time_bin or value outside its embedding table)")
+        return host.numpy().copy()
+
+    def _graph(self, B: int, Eb: int) -> _CsrGraph:
+        key = (B, Eb)
+        g = self._graphs.get(key)
+        if g is None:
+            if len(self._graphs) >= self.max_graphs:
+                self._graphs.popitem(last=False)
+            g = _CsrGraph(self.model, B, Eb, self.device, self._stream, self._pool)
+            self._graphs[key] = g
+        else:
+            self._graphs.move_to_end(key)
+        return g
