@@ -347,6 +347,61 @@ def worker_latency(model, dev, n_requests: int, per_sample: int = 512):
             "b256_events": int(counts.sum()), "b256_payload": "columnar arrays"}
 
 
+def streaming_windows(model, dev, sessions: int = 256, steps: int = 12, b1_requests: int = 200):
+    """Streaming decode with the device event-page cache: every step each session sends one
+    new 50-bin stride of events (host -> device page write), then one batch of 600-bin windows
+    is assembled on the device and decoded; pages that left every window age out by LRU.
+    Poisson spike counts over 137 neurons at ~512 events per window.  Reports ms per step (page writes + gather + forward + D2H) for the
+    whole batch, and p50/p99 for a single session (B=1)."""
+    from cortex.cache import EventWindowCache
+    from cortex.models.config import CORTEX_S
+    from cortex.serve import InferenceWorker
+
+    stride, window = 50, 600
+    T = window + (steps + 4) * stride + b1_requests * stride
+    rate = 512 / (window * 137)
+    rng = np.random.default_rng(21)
+    w = InferenceWorker(model, CORTEX_S, dev, max_batch_size=sessions)
+    cache = EventWindowCache(num_pages=sessions * 16 + 64, page_events=512, bins_per_page=stride, device=dev)
+
+    def page(counts, b0):
+        t, n = np.nonzero(counts[b0:b0 + stride])
+        return n.astype(np.int64), t.astype(np.int64) + b0, np.clip(counts[t + b0, n], 1, 7).astype(np.int64)
+
+    data = {f"s{i}": rng.poisson(rate, (window + (steps + 4) * stride, 137)) for i in range(sessions)}
+    for sid, c in data.items():
+        for b0 in range(0, window - stride, stride):
+            cache.write(sid, b0, *page(c, b0))
+    times = []
+    for step in range(steps + 3):
+        t0 = time.perf_counter()
+        b0 = window - stride + step * stride
+        for sid, c in data.items():
+            cache.write(sid, b0, *page(c, b0))
+        w.run_windows_sync([{"request_id": sid, "session_id": sid, "window_start": b0 + stride - window}
+                            for sid in data], cache, window)
+        if step >= 3:
+            times.append(time.perf_counter() - t0)
+    one = rng.poisson(rate, (T, 137))
+    for b0 in range(0, window - stride, stride):
+        cache.write("solo", b0, *page(one, b0))
+    lat = []
+    for i in range(b1_requests + 10):
+        t0 = time.perf_counter()
+        b0 = window - stride + i * stride
+        cache.write("solo", b0, *page(one, b0))
+        w.run_windows_sync([{"request_id": "solo", "session_id": "solo", "window_start": b0 + stride - window}],
+                           cache, window)
+        if i >= 10:
+            lat.append((time.perf_counter() - t0) * 1e3)
+    lat.sort()
+    sec = float(np.mean(times))
+    w.shutdown()
+    return {"sessions": sessions, "ms_per_step": round(sec * 1e3, 3), "samples_per_s": round(sessions / sec, 1),
+            "b1_p50_ms": round(lat[len(lat) // 2], 4), "b1_p99_ms": round(lat[int(len(lat) * 0.99) - 1], 4),
+            "b1_requests": b1_requests, "hit_rate": round(cache.hit_rate, 4)}
+
+
 def serving_sweep(model, dev, batches=(1, 8, 32, 128, 256), reps: int = 20):
     """Serving-shaped forward: E_b = clip(Poisson(512), 64, 2048) per sample, one graph per batch."""
     from cortex.runtime import CapturedForward
@@ -496,6 +551,8 @@ def main() -> int:
         log(f"bench: serving {extra['serving_sweep']}")
         extra["serve_worker"] = worker_latency(model, dev, args.latency_requests)
         log(f"bench: serve worker {extra['serve_worker']}")
+        extra["streaming"] = streaming_windows(model, dev)
+        log(f"bench: streaming {extra['streaming']}")
     cpu = None
     if not (args.no_cpu_baseline or args.quick):
         log("bench: CPU baseline")

@@ -1,0 +1,241 @@
+"""Paged LRU caches for streaming inference (reference cortex/cache/streaming.py:79-236).
+
+``StreamingKVCache`` keeps the reference's API and bookkeeping exactly -- ``read`` /
+``write`` / ``evict_session`` / ``hit_rate`` / ``pages_used``, one page per
+``(session_id, bin_start)``, a free list, least-recently-used eviction across
+sessions, ``write`` truncating to ``page_size`` rows and overwriting an existing
+page -- with the page pool on the GPU.
+
+What it caches is the reference's premise, and that premise does not hold for the
+Cortex input: a window's time bins are relative to the window start
+(cortex/data/nlb.py:253-256), so the same spike gets a different time embedding in
+the next window and cached tokens are not reusable.  ``EventWindowCache`` is the
+cache a streaming server can use: pages of RAW events (neuron id, absolute bin,
+value) for ``bins_per_page`` consecutive bins, stored once on the device; a decode
+window is assembled from its pages by one gather kernel that rewrites the bins
+relative to the window start, straight into the forward's input buffer.  Only the
+newest stride's events ever cross PCIe.  Events inside a page keep their arrival
+order, so a window assembled from time-ordered pages equals the window built from
+scratch (events ordered by time bin, as ``np.nonzero`` over (T, N) counts gives).
+
+Neither cache is thread-safe; like the reference, they are meant for the single
+inference executor thread.  Prometheus gauges of the reference are not kept.
+"""
+
+from __future__ import annotations
+
+import time
+from collections import OrderedDict
+from dataclasses import dataclass
+from typing import Any
+
+import numpy as np
+import torch
+
+from cortex import _native as nat
+
+
+@dataclass
+class PageMeta:
+    """Metadata of one cache page (reference streaming.py:67-75)."""
+
+    page_id: int
+    session_id: str
+    bin_start: int
+    n_events: int
+    last_used_at: float
+
+
+class _PagedLRU:
+    """Page table, free list and LRU order shared by both caches."""
+
+    def __init__(self, num_pages: int) -> None:
+        if num_pages < 1:
+            raise ValueError("num_pages must be >= 1")
+        self.num_pages = num_pages
+        self._table: dict[tuple[str, int], int] = {}
+        self._meta: dict[int, PageMeta] = {}
+        self._free: list[int] = list(range(num_pages))
+        self._lru: OrderedDict[int, None] = OrderedDict()
+        self._hits = 0
+        self._misses = 0
+
+    def _lookup(self, session_id: str, bin_start: int) -> int | None:
+        """Page of the key, touching LRU and counting a hit; None (a miss) otherwise."""
+        page_id = self._table.get((session_id, bin_start))
+        if page_id is None:
+            self._misses += 1
+            return None
+        self._lru.move_to_end(page_id)
+        self._meta[page_id].last_used_at = time.monotonic()
+        self._hits += 1
+        return page_id
+
+    def _page_for_write(self, session_id: str, bin_start: int) -> int:
+        page_id = self._table.get((session_id, bin_start))
+        if page_id is None:
+            page_id = self._allocate()
+            self._table[(session_id, bin_start)] = page_id
+            self._meta[page_id] = PageMeta(page_id, session_id, bin_start, 0, time.monotonic())
+            self._lru[page_id] = None
+        return page_id
+
+    def _written(self, page_id: int, n: int) -> None:
+        self._meta[page_id].n_events = n
+        self._meta[page_id].last_used_at = time.monotonic()
+        self._lru.move_to_end(page_id)
+
+    def evict_session(self, session_id: str) -> int:
+        """Free every page of ``session_id``; returns how many were freed."""
+        keys = [k for k in self._table if k[0] == session_id]
+        for key in keys:
+            self._free_page(self._table.pop(key))
+        return len(keys)
+
+    @property
+    def hit_rate(self) -> float:
+        total = self._hits + self._misses
+        return self._hits / total if total > 0 else 0.0
+
+    @property
+    def pages_used(self) -> int:
+        return len(self._meta)
+
+    def _allocate(self) -> int:
+        """A free page id, evicting the least recently used page when none is free."""
+        if self._free:
+            return self._free.pop()
+        lru_id, _ = self._lru.popitem(last=False)
+        self._free_page(lru_id)
+        return self._free.pop()
+
+    def _free_page(self, page_id: int) -> None:
+        meta = self._meta.pop(page_id, None)
+        if meta is not None:
+            self._table.pop((meta.session_id, meta.bin_start), None)
+        self._lru.pop(page_id, None)
+        self._free.append(page_id)
+
+
+class StreamingKVCache(_PagedLRU):
+    """Paged embedding cache, API of reference streaming.py:79-236 (pool on ``device``)."""
+
+    def __init__(self, num_pages: int = 128, page_size: int = 64, hidden_dim: int = 512,
+                 dtype: torch.dtype = torch.float32, device: str | torch.device = "cpu") -> None:
+        super().__init__(num_pages)
+        self.page_size = page_size
+        self.hidden_dim = hidden_dim
+        self.device = torch.device(device)
+        self._pool = torch.zeros(num_pages, page_size, hidden_dim, dtype=dtype, device=self.device)
+
+    def read(self, session_id: str, bin_start: int) -> torch.Tensor | None:
+        """The cached rows of ``(session_id, bin_start)`` (a view into the pool), or None."""
+        page_id = self._lookup(session_id, bin_start)
+        if page_id is None:
+            return None
+        return self._pool[page_id, :self._meta[page_id].n_events, :]
+
+    def write(self, session_id: str, bin_start: int, embeddings: torch.Tensor) -> None:
+        """Store the first ``page_size`` rows of ``embeddings`` (E, hidden_dim), replacing
+        an existing page of the key; evicts the least recently used page when full."""
+        n = min(embeddings.shape[0], self.page_size)
+        page_id = self._page_for_write(session_id, bin_start)
+        self._pool[page_id, :n, :] = embeddings[:n].detach().to(dtype=self._pool.dtype, device=self.device)
+        self._written(page_id, n)
+
+
+class EventWindowCache(_PagedLRU):
+    """Device pages of raw spike events keyed by ``(session_id, absolute first bin)``.
+
+    Page ``(s, b0)`` holds the events of bins ``[b0, b0 + bins_per_page)``, at most
+    ``page_events`` of them, as int64 rows (neuron id, absolute bin, value).  A
+    window ``[w0, w0 + window_bins)`` with ``w0`` and ``window_bins`` multiples of
+    ``bins_per_page`` is the concatenation of its pages in bin order.
+    """
+
+    def __init__(self, num_pages: int = 4096, page_events: int = 1024, bins_per_page: int = 50,
+                 device: str | torch.device = "cuda") -> None:
+        super().__init__(num_pages)
+        self.page_events = page_events
+        self.bins_per_page = bins_per_page
+        self.device = torch.device(device)
+        nat.require_gpu(torch.empty(0, device=self.device), what="EventWindowCache")
+        self._pool = torch.zeros(num_pages, 3, page_events, dtype=torch.int64, device=self.device)
+
+    def write(self, session_id: str, bin_start: int, neuron_ids: Any, time_bins: Any, values: Any) -> None:
+        """Store the events of bins ``[bin_start, bin_start + bins_per_page)``; ``time_bins``
+        are absolute.  Raises ValueError for a misaligned page, events outside its bins or
+        more than ``page_events`` events (a page never drops events)."""
+        if bin_start % self.bins_per_page:
+            raise ValueError(f"bin_start {bin_start} is not a multiple of bins_per_page={self.bins_per_page}")
+        cols = [torch.as_tensor(np.asarray(x) if not torch.is_tensor(x) else x).reshape(-1).to(torch.int64)
+                for x in (neuron_ids, time_bins, values)]
+        n = cols[0].shape[0]
+        if not (cols[1].shape[0] == cols[2].shape[0] == n):
+            raise ValueError("neuron_ids, time_bins and values must have the same length")
+        if n > self.page_events:
+            raise ValueError(f"{n} events exceed page_events={self.page_events}")
+        if n and cols[1].device.type == "cpu":
+            lo, hi = int(cols[1].min()), int(cols[1].max())
+            if lo < bin_start or hi >= bin_start + self.bins_per_page:
+                raise ValueError(f"time bins [{lo}, {hi}] outside page [{bin_start}, {bin_start + self.bins_per_page})")
+        page_id = self._page_for_write(session_id, bin_start)
+        if n:
+            self._pool[page_id, :, :n] = torch.stack(cols).to(self.device, non_blocking=False)
+        self._written(page_id, n)
+
+    def read(self, session_id: str, bin_start: int) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor] | None:
+        """(neuron ids, absolute bins, values) views of a page, or None."""
+        page_id = self._lookup(session_id, bin_start)
+        if page_id is None:
+            return None
+        n = self._meta[page_id].n_events
+        p = self._pool[page_id]
+        return p[0, :n], p[1, :n], p[2, :n]
+
+    def window_pages(self, session_id: str, window_start: int, window_bins: int) -> list[tuple[int, int]]:
+        """``[(page_id, n_events)]`` of a window in bin order (touching LRU); KeyError names the
+        missing pages."""
+        if window_start % self.bins_per_page or window_bins % self.bins_per_page:
+            raise ValueError("window_start and window_bins must be multiples of bins_per_page")
+        starts = range(window_start, window_start + window_bins, self.bins_per_page)
+        pages = [self._lookup(session_id, b) for b in starts]
+        missing = [b for b, p in zip(starts, pages) if p is None]
+        if missing:
+            raise KeyError(f"session {session_id!r}: no page for bins starting at {missing}")
+        return [(p, self._meta[p].n_events) for p in pages]
+
+    def plan(self, windows: list[tuple[str, int]], window_bins: int) -> tuple[np.ndarray, np.ndarray]:
+        """Gather plan of a batch of windows: ``(items (n, 4) int64, offsets (B+1) int64)``.
+
+        Item = (page id, events, first output row, bin shift = window start); window b
+        owns output rows ``[offsets[b], offsets[b+1])``.
+        """
+        items, offsets, row = [], [0], 0
+        for session_id, w0 in windows:
+            for page_id, n in self.window_pages(session_id, w0, window_bins):
+                if n:
+                    items.append((page_id, n, row, w0))
+                    row += n
+            offsets.append(row)
+        return np.asarray(items, dtype=np.int64).reshape(-1, 4), np.asarray(offsets, dtype=np.int64)
+
+    def gather(self, items: torch.Tensor, out: torch.Tensor, field_stride: int, out_rows: int,
+               err: torch.Tensor | None = None) -> None:
+        """Run a device plan (``items`` (n, 4) int64 on the GPU) into ``out``: field f of
+        row r at ``out[f * field_stride + r]``, bins relative to each window's start."""
+        nat.call("cortex_gather_event_pages", nat.ptr(self._pool), self.num_pages, self.page_events,
+                 nat.ptr(items), items.shape[0], nat.ptr(out), field_stride, out_rows, nat.ptr(err),
+                 nat.stream_of(self.device))
+
+    def assemble(self, windows: list[tuple[str, int]], window_bins: int
+                 ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
+        """Device CSR input of a batch of windows: ``(neuron_ids, time_bins, values, offsets)``
+        with bins relative to each window's start."""
+        items, offsets = self.plan(windows, window_bins)
+        E = int(offsets[-1])
+        out = torch.empty(3 * max(E, 1), dtype=torch.int64, device=self.device)
+        if items.shape[0]:
+            self.gather(torch.from_numpy(items).to(self.device), out, max(E, 1), E)
+        S = max(E, 1)
+        return out[:E], out[S:S + E], out[2 * S:2 * S + E], torch.from_numpy(offsets).to(self.device)

@@ -176,6 +176,7 @@ class InferenceWorker:
         self._host_in = torch.empty(1 << 16, dtype=torch.int64).pin_memory()
         self._host_out = torch.empty(1024, dtype=torch.float32).pin_memory()
         self._host_err = torch.zeros(1, dtype=torch.int32).pin_memory()
+        self._plan_dev: torch.Tensor | None = None
         self._done = torch.cuda.Event()
         self._loaded = False
 
@@ -221,27 +222,66 @@ class InferenceWorker:
         if flat.ctypes.data != self._host_in.data_ptr():  # did not fit: grow the pinned buffer
             self._host_in = torch.empty(max(n_in, 2 * self._host_in.numel()), dtype=torch.int64).pin_memory()
             self._host_in.numpy()[:n_in] = flat[:n_in]
-        behavior = self._forward(B, Eb, n_in)
+        src = self._host_in[:n_in]
+        behavior = self._forward(B, Eb, lambda inp, err: inp.copy_(src, non_blocking=True))
         ms = (time.perf_counter() - t0) * 1000
         rows = behavior.tolist()
         return [{"request_id": p["request_id"], "behavior": rows[i] if i < B else [0.0] * dim, "inference_ms": ms}
                 for i, p in enumerate(payloads)]
 
-    def _forward(self, B: int, Eb: int, n_in: int) -> np.ndarray:
+    def run_windows_sync(self, requests: list[dict[str, Any]], cache: Any, window_bins: int = 600
+                         ) -> list[dict[str, Any]]:
+        """Streaming batch: each request ``{"request_id", "session_id", "window_start"}`` names a
+        decode window whose event pages are already in ``cache`` (an ``EventWindowCache`` on this
+        device).  The window inputs are gathered on the device into the forward's input buffer;
+        only the gather plan and the offsets cross PCIe.  Same result dicts as ``run_batch``."""
+        t0 = time.perf_counter()
+        if not requests:
+            return []
+        items, offsets = cache.plan([(r["session_id"], int(r["window_start"])) for r in requests], window_bins)
+        B, E = len(requests), int(offsets[-1])
+        Eb = event_bucket(E) if self.use_graphs else max(E, 1)
+        n_host = B + 1 + items.size
+        if self._host_in.numel() < n_host:
+            self._host_in = torch.empty(max(n_host, 2 * self._host_in.numel()), dtype=torch.int64).pin_memory()
+        h = self._host_in.numpy()
+        h[:B + 1] = offsets
+        h[B + 1:n_host] = items.reshape(-1)
+        have = 0 if self._plan_dev is None else self._plan_dev.numel()
+        if have < max(items.size, 4):
+            self._plan_dev = torch.empty(max(items.size, 4, 2 * have), dtype=torch.int64, device=self.device)
+        plan_dev = self._plan_dev[:items.size].view(-1, 4)
+        off_host, plan_host = self._host_in[:B + 1], self._host_in[B + 1:n_host]
+
+        def fill(inp: torch.Tensor, err: torch.Tensor) -> None:
+            inp[3 * Eb:3 * Eb + B + 1].copy_(off_host, non_blocking=True)
+            if items.shape[0]:
+                plan_dev.view(-1).copy_(plan_host, non_blocking=True)
+                cache.gather(plan_dev, inp, Eb, E, err)
+
+        behavior = self._forward(B, Eb, fill)
+        ms = (time.perf_counter() - t0) * 1000
+        rows = behavior.tolist()
+        return [{"request_id": r["request_id"], "behavior": rows[i], "inference_ms": ms}
+                for i, r in enumerate(requests)]
+
+    def _forward(self, B: int, Eb: int, fill) -> np.ndarray:
+        """``fill(inp, err)`` writes the (B, Eb) input buffer on the worker stream; then the
+        forward runs and the (B, dim) behaviour comes back to the host."""
         dim = self.config.behavior_dim
         if self._host_out.numel() < B * dim:
             self._host_out = torch.empty(max(B * dim, 2 * self._host_out.numel()), dtype=torch.float32).pin_memory()
-        src = self._host_in[:n_in]
         with torch.cuda.device(self.device), torch.cuda.stream(self._stream):
             if self.use_graphs:
                 g = self._graph(B, Eb)
-                g.inp.copy_(src, non_blocking=True)
                 g.err.zero_()
+                fill(g.inp, g.err)
                 g.graph.replay()
                 out, err = g.out, g.err
             else:
-                inp = src.to(self.device, non_blocking=True)
+                inp = torch.empty(3 * Eb + B + 1, dtype=torch.int64, device=self.device)
                 err = torch.zeros(1, dtype=torch.int32, device=self.device)
+                fill(inp, err)
                 with torch.inference_mode():
                     out = self.model.forward_csr(inp[:Eb], inp[Eb:2 * Eb], inp[2 * Eb:3 * Eb], inp[3 * Eb:],
                                                  err_flag=err)
@@ -250,7 +290,10 @@ class InferenceWorker:
             self._host_err.copy_(err, non_blocking=True)
             self._done.record(self._stream)
         self._done.synchronize()
-        if int(self._host_err[0]) != 0:
+        e = int(self._host_err[0])
+        if e & 4:  # the host plan and the device pool disagree: a bug, not bad input
+            raise RuntimeError("event page gather got a malformed plan item")
+        if e:
             raise IndexError("event index out of range (neuron_id, time_bin or value outside its embedding table)")
         return host.numpy().copy()
 

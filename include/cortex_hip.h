@@ -189,6 +189,20 @@ int cortex_temporal_block_mask(const int64_t* event_times, int64_t t_stride, int
                                int64_t block_l, int64_t block_e, int64_t n_q, int64_t n_k, uint8_t* out,
                                int64_t out_sb, hipStream_t stream);
 
+/* Streaming window assembly from device event pages.  No single reference
+ * counterpart: it serves StreamingKVCache's role (cortex/cache/streaming.py:79-236)
+ * with pages of raw events keyed by ABSOLUTE time bin, since the reference's window
+ * time bins are relative to the window start (cortex/data/nlb.py:253-256), so cached
+ * tokens would not be reusable.  pool: (num_pages, 3, page_events) int64 rows of
+ * neuron id, absolute bin, value.  plan: (n_items, 4) int64 of (page, count,
+ * first output row, bin shift); item i writes rows [dst, dst+count) of
+ * out[f * field_stride + row] with the bin rewritten as bin - shift.  A malformed
+ * item (page or rows out of range) writes nothing and sets bit 2 of *err (when
+ * given).  Bit-exact copies. */
+int cortex_gather_event_pages(const int64_t* pool, int64_t num_pages, int64_t page_events, const int64_t* plan,
+                              int64_t n_items, int64_t* out, int64_t field_stride, int64_t out_rows, int32_t* err,
+                              hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

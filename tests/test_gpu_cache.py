@@ -1,0 +1,99 @@
+"""Streaming windows from device event pages (the D7 fix of the reference's
+StreamingKVCache premise, cortex/cache/streaming.py:79-236, cortex/data/nlb.py:249-256).
+
+Windows assembled on the device from absolute-bin pages must equal, bit for bit,
+the window built from scratch the reference's way (events of the window's (T, N)
+counts via np.nonzero, bins relative to the window start); the worker's result for
+cached windows must equal its result for the same windows sent as payloads.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+STRIDE, WINDOW = 50, 600
+
+
+def _events(counts):
+    """(T, N) spike counts -> (neuron, bin, value) ordered by bin, then neuron."""
+    t, n = np.nonzero(counts)
+    return n.astype(np.int64), t.astype(np.int64), np.clip(counts[t, n], 1, 7).astype(np.int64)
+
+
+def _session(seed, T=1200, N=137, rate=0.007):
+    return np.random.default_rng(seed).poisson(rate, (T, N))
+
+
+def _fill(cache, sid, counts, upto):
+    for b0 in range(0, upto, STRIDE):
+        nid, tb, val = _events(counts[b0:b0 + STRIDE])
+        cache.write(sid, b0, nid, tb + b0, val)  # absolute bins
+
+
+def test_assembled_windows_equal_scratch_windows():
+    from cortex.cache import EventWindowCache
+
+    cache = EventWindowCache(num_pages=256, page_events=512, bins_per_page=STRIDE, device=DEV)
+    sessions = {f"s{i}": _session(i) for i in range(3)}
+    for sid, counts in sessions.items():
+        _fill(cache, sid, counts, 1200)
+    windows = [("s0", 0), ("s1", 300), ("s2", 600), ("s0", 550), ("s1", 0)]
+    nid, tb, val, off = cache.assemble(windows, WINDOW)
+    off = off.cpu().numpy()
+    for b, (sid, w0) in enumerate(windows):
+        ref = _events(sessions[sid][w0:w0 + WINDOW])
+        for got, want in zip((nid, tb, val), ref):
+            np.testing.assert_array_equal(got[off[b]:off[b + 1]].cpu().numpy(), want, err_msg=f"window {b}")
+    assert cache.hit_rate == 1.0 and cache.pages_used == 3 * 24
+
+
+def test_page_cache_errors_and_eviction():
+    from cortex.cache import EventWindowCache
+
+    cache = EventWindowCache(num_pages=4, page_events=8, bins_per_page=STRIDE, device=DEV)
+    with pytest.raises(ValueError):
+        cache.write("s", 10, [1], [10], [1])  # not aligned to a page
+    with pytest.raises(ValueError):
+        cache.write("s", 0, [1], [STRIDE], [1])  # bin outside the page
+    with pytest.raises(ValueError):
+        cache.write("s", 0, np.zeros(9), np.zeros(9), np.ones(9))  # more than page_events
+    for b0 in range(0, 5 * STRIDE, STRIDE):  # 5 pages into 4: the first is evicted
+        cache.write("s", b0, [b0 // STRIDE], [b0], [1])
+    with pytest.raises(KeyError):
+        cache.window_pages("s", 0, 2 * STRIDE)
+    got = cache.read("s", 4 * STRIDE)
+    assert [int(x[0]) for x in got] == [4, 4 * STRIDE, 1]
+    assert cache.evict_session("s") == 4 and cache.pages_used == 0
+
+
+@pytest.mark.parametrize("use_graphs", [True, False])
+def test_worker_windows_equal_payloads(use_graphs):
+    from cortex.cache import EventWindowCache
+    from cortex.models import CortexModel
+    from cortex.models.config import CORTEX_S
+    from cortex.serve import InferenceWorker
+
+    torch.manual_seed(0)
+    model = CortexModel(CORTEX_S).to(DEV).eval()
+    w = InferenceWorker(model, CORTEX_S, torch.device(DEV), use_graphs=use_graphs)
+    cache = EventWindowCache(num_pages=512, page_events=512, bins_per_page=STRIDE, device=DEV)
+    sessions = {f"s{i}": _session(10 + i, rate=0.01) for i in range(4)}
+    for step in range(3):  # a stride of new events per session, then one batch of windows
+        upto = WINDOW + step * STRIDE
+        for sid, counts in sessions.items():
+            _fill(cache, sid, counts, upto)
+        reqs = [{"request_id": sid, "session_id": sid, "window_start": upto - WINDOW} for sid in sessions]
+        got = w.run_windows_sync(reqs, cache, WINDOW)
+        payloads = []
+        for r in reqs:
+            nid, tb, val = _events(sessions[r["session_id"]][r["window_start"]:r["window_start"] + WINDOW])
+            payloads.append({"request_id": r["request_id"],
+                             "events": {"neuron_id": nid, "time_bin": tb, "value": val}})
+        want = w._run_batch_sync(payloads)
+        assert [g["request_id"] for g in got] == [x["request_id"] for x in want]
+        assert [g["behavior"] for g in got] == [x["behavior"] for x in want]
+    w.shutdown()
