@@ -74,6 +74,7 @@ _SIGNATURES = {
          _i64, _ptr, _ptr, _ptr, _i64, _ptr, _i64, _i64, _i64, _i64, _i64, _f32, _ptr, _i64, _i64, _i64, _ptr],
     ),
     "cortex_gather_event_pages": (_int, [_ptr, _i64, _i64, _ptr, _i64, _ptr, _i64, _i64, _ptr, _ptr]),
+    "cortex_scatter_event_pages": (_int, [_ptr, _i64, _i64, _ptr, _i64, _ptr, _i64, _i64, _ptr, _ptr]),
     "cortex_temporal_block_mask": (
         _int, [_ptr, _i64, _i64, _ptr, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _ptr, _i64, _ptr]),
 }

@@ -14,7 +14,8 @@ cache a streaming server can use: pages of RAW events (neuron id, absolute bin,
 value) for ``bins_per_page`` consecutive bins, stored once on the device; a decode
 window is assembled from its pages by one gather kernel that rewrites the bins
 relative to the window start, straight into the forward's input buffer.  Only the
-newest stride's events ever cross PCIe.  Events inside a page keep their arrival
+newest stride's events ever cross PCIe, as one pinned copy for all sessions' new
+pages plus one scatter launch (``write_many``).  Events inside a page keep their arrival
 order, so a window assembled from time-ordered pages equals the window built from
 scratch (events ordered by time bin, as ``np.nonzero`` over (T, N) counts gives).
 
@@ -161,28 +162,62 @@ class EventWindowCache(_PagedLRU):
         self.device = torch.device(device)
         nat.require_gpu(torch.empty(0, device=self.device), what="EventWindowCache")
         self._pool = torch.zeros(num_pages, 3, page_events, dtype=torch.int64, device=self.device)
+        self._stage_host = torch.empty(1 << 15, dtype=torch.int64).pin_memory()
+        self._stage_dev = torch.empty_like(self._stage_host, device=self.device)
+        self._staged = torch.cuda.Event()
 
     def write(self, session_id: str, bin_start: int, neuron_ids: Any, time_bins: Any, values: Any) -> None:
         """Store the events of bins ``[bin_start, bin_start + bins_per_page)``; ``time_bins``
         are absolute.  Raises ValueError for a misaligned page, events outside its bins or
         more than ``page_events`` events (a page never drops events)."""
-        if bin_start % self.bins_per_page:
-            raise ValueError(f"bin_start {bin_start} is not a multiple of bins_per_page={self.bins_per_page}")
-        cols = [torch.as_tensor(np.asarray(x) if not torch.is_tensor(x) else x).reshape(-1).to(torch.int64)
-                for x in (neuron_ids, time_bins, values)]
-        n = cols[0].shape[0]
-        if not (cols[1].shape[0] == cols[2].shape[0] == n):
-            raise ValueError("neuron_ids, time_bins and values must have the same length")
-        if n > self.page_events:
-            raise ValueError(f"{n} events exceed page_events={self.page_events}")
-        if n and cols[1].device.type == "cpu":
-            lo, hi = int(cols[1].min()), int(cols[1].max())
-            if lo < bin_start or hi >= bin_start + self.bins_per_page:
-                raise ValueError(f"time bins [{lo}, {hi}] outside page [{bin_start}, {bin_start + self.bins_per_page})")
-        page_id = self._page_for_write(session_id, bin_start)
-        if n:
-            self._pool[page_id, :, :n] = torch.stack(cols).to(self.device, non_blocking=False)
-        self._written(page_id, n)
+        self.write_many([(session_id, bin_start, neuron_ids, time_bins, values)])
+
+    def write_many(self, pages: list[tuple[str, int, Any, Any, Any]]) -> None:
+        """Several page writes as one pinned host->device copy and one scatter launch, on the
+        current stream.  Entries are ``(session_id, bin_start, neuron_ids, time_bins, values)``
+        with host integer arrays; a key given twice keeps its last entry."""
+        last: dict[tuple[str, int], tuple[np.ndarray, ...]] = {}
+        for session_id, bin_start, nid, tb, val in pages:
+            if bin_start % self.bins_per_page:
+                raise ValueError(f"bin_start {bin_start} is not a multiple of bins_per_page={self.bins_per_page}")
+            cols = tuple(np.asarray(x.cpu() if torch.is_tensor(x) else x).reshape(-1).astype(np.int64, copy=False)
+                         for x in (nid, tb, val))
+            n = cols[0].shape[0]
+            if not (cols[1].shape[0] == cols[2].shape[0] == n):
+                raise ValueError("neuron_ids, time_bins and values must have the same length")
+            if n > self.page_events:
+                raise ValueError(f"{n} events exceed page_events={self.page_events}")
+            if n and (cols[1].min() < bin_start or cols[1].max() >= bin_start + self.bins_per_page):
+                raise ValueError(f"time bins [{cols[1].min()}, {cols[1].max()}] outside page "
+                                 f"[{bin_start}, {bin_start + self.bins_per_page})")
+            last[(session_id, bin_start)] = cols
+        if len(last) > self.num_pages:
+            raise ValueError(f"{len(last)} pages in one write exceed the pool's {self.num_pages}")
+        total = sum(c[0].shape[0] for c in last.values())
+        items, row = [], 0
+        for key, cols in last.items():
+            page_id = self._page_for_write(*key)
+            n = cols[0].shape[0]
+            if n:
+                items.append((page_id, n, row))
+            row += n
+            self._written(page_id, n)
+        if not items:
+            return
+        need = 3 * total + 3 * len(items)
+        self._staged.synchronize()  # the previous write's copy has left the pinned buffer
+        if self._stage_host.numel() < need:
+            self._stage_host = torch.empty(max(need, 2 * self._stage_host.numel()), dtype=torch.int64).pin_memory()
+            self._stage_dev = torch.empty_like(self._stage_host, device=self.device)
+        h = self._stage_host.numpy()
+        for f in range(3):
+            np.concatenate([c[f] for c in last.values()], out=h[f * total:(f + 1) * total])
+        h[3 * total:need] = np.asarray(items, dtype=np.int64).reshape(-1)
+        dev = self._stage_dev[:need]
+        dev.copy_(self._stage_host[:need], non_blocking=True)
+        self._staged.record()
+        nat.call("cortex_scatter_event_pages", nat.ptr(dev), total, total, nat.ptr(dev[3 * total:]), len(items),
+                 nat.ptr(self._pool), self.num_pages, self.page_events, None, nat.stream_of(self.device))
 
     def read(self, session_id: str, bin_start: int) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor] | None:
         """(neuron ids, absolute bins, values) views of a page, or None."""

@@ -259,6 +259,7 @@ class InferenceWorker:
                 plan_dev.view(-1).copy_(plan_host, non_blocking=True)
                 cache.gather(plan_dev, inp, Eb, E, err)
 
+        self._stream.wait_stream(torch.cuda.current_stream(self.device))  # page writes issued on it
         behavior = self._forward(B, Eb, fill)
         ms = (time.perf_counter() - t0) * 1000
         rows = behavior.tolist()

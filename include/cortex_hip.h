@@ -203,6 +203,15 @@ int cortex_gather_event_pages(const int64_t* pool, int64_t num_pages, int64_t pa
                               int64_t n_items, int64_t* out, int64_t field_stride, int64_t out_rows, int32_t* err,
                               hipStream_t stream);
 
+/* The page write of the same cache (reference StreamingKVCache.write,
+ * cortex/cache/streaming.py:157-194, batched): plan (n_items, 3) int64 of (page,
+ * count, first staged row); item i copies staged rows [s0, s0+count) of
+ * src[f * field_stride + row] into page `page` of the pool.  A malformed item writes
+ * nothing and sets bit 2 of *err (when given).  Bit-exact copies. */
+int cortex_scatter_event_pages(const int64_t* src, int64_t field_stride, int64_t src_rows, const int64_t* plan,
+                               int64_t n_items, int64_t* pool, int64_t num_pages, int64_t page_events, int32_t* err,
+                               hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

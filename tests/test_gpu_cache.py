@@ -24,6 +24,11 @@ def _events(counts):
     return n.astype(np.int64), t.astype(np.int64), np.clip(counts[t, n], 1, 7).astype(np.int64)
 
 
+def _events_abs(counts, b0):
+    nid, tb, val = _events(counts[b0:b0 + STRIDE])
+    return nid, tb + b0, val
+
+
 def _session(seed, T=1200, N=137, rate=0.007):
     return np.random.default_rng(seed).poisson(rate, (T, N))
 
@@ -39,8 +44,15 @@ def test_assembled_windows_equal_scratch_windows():
 
     cache = EventWindowCache(num_pages=256, page_events=512, bins_per_page=STRIDE, device=DEV)
     sessions = {f"s{i}": _session(i) for i in range(3)}
-    for sid, counts in sessions.items():
-        _fill(cache, sid, counts, 1200)
+    _fill(cache, "s0", sessions["s0"], 1200)  # one page per call
+    batch = []
+    for sid in ("s1", "s2"):  # every page of two sessions in one batched write
+        for b0 in range(0, 1200, STRIDE):
+            nid, tb, val = _events(sessions[sid][b0:b0 + STRIDE])
+            batch.append((sid, b0, nid, tb + b0, val))
+    batch.append(("s1", 0, [5], [3], [2]))  # a key given twice: the last entry is kept ...
+    batch.append(("s1", 0, *_events_abs(sessions["s1"], 0)))  # ... so this one
+    cache.write_many(batch)
     windows = [("s0", 0), ("s1", 300), ("s2", 600), ("s0", 550), ("s1", 0)]
     nid, tb, val, off = cache.assemble(windows, WINDOW)
     off = off.cpu().numpy()
