@@ -192,6 +192,42 @@ def ln_rows(x: torch.Tensor, ln1, ln2=None, out_bf16: bool = True, out_f32: bool
     return ob if out_bf16 else of
 
 
+def head_prep(q: torch.Tensor, kv_weight: torch.Tensor, kv_scale, out_weight: torch.Tensor, out_scale,
+              num_heads: int) -> torch.Tensor:
+    """Folded behaviour-head matrix (32, D) bf16 (see ``cortex_head_prep``) from the projected
+    queries ``q`` (Q, D) bf16 and the bf16 weight images of kv_proj (2D, D) and out_proj (1, D)
+    with their optional per-row scales."""
+    dev = nat.require_gpu(q, kv_weight, out_weight, kv_scale, out_scale, what="head_prep")
+    Q, D = q.shape
+    for t in (q, kv_weight, out_weight):
+        if t.dtype != torch.bfloat16 or t.stride(-1) != 1:
+            raise ValueError("head_prep needs bf16 operands with unit column stride")
+    ac = torch.empty((32, D), dtype=torch.bfloat16, device=dev)
+    nat.call("cortex_head_prep", nat.ptr(q), q.stride(0), Q, int(num_heads), D, nat.ptr(kv_weight),
+             nat.ptr(kv_scale), kv_weight.stride(0), nat.ptr(out_weight), nat.ptr(out_scale), nat.ptr(ac),
+             nat.stream_of(dev))
+    return ac
+
+
+def behavior_head(x: torch.Tensor, batch: int, ln1, ln2, ac: torch.Tensor, num_queries: int, num_heads: int,
+                  out: torch.Tensor | None = None) -> torch.Tensor:
+    """Fused behaviour head: ``(B, Q)`` fp32 from the (B*L, D) fp32 latents, the two
+    LayerNorms ``ln1`` then ``ln2`` (``(weight, bias, eps)``) and the folded matrix ``ac``."""
+    dev = nat.require_gpu(x, ac, out, what="behavior_head")
+    x2 = _row_major_2d(x.reshape(-1, x.shape[-1]))
+    M, D = x2.shape
+    L = M // batch
+    if out is None:
+        out = torch.empty((batch, num_queries), dtype=torch.float32, device=dev)
+    (g1, b1, e1), (g2, b2, e2) = ln1, ln2
+    ws_bytes = int(nat.load().cortex_behavior_head_workspace_bytes(batch, L))
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+    nat.call("cortex_behavior_head", nat.ptr(x2), x2.stride(0) if M > 1 else D, batch, L, D, int(num_queries),
+             int(num_heads), nat.ptr(g1), nat.ptr(b1), float(e1), nat.ptr(g2), nat.ptr(b2), float(e2), nat.ptr(ac),
+             nat.ptr(out), nat.ptr(ws), ws_bytes, nat.stream_of(dev))
+    return out
+
+
 def convert(t: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
     """Elementwise dtype conversion on the GPU (int8/f32/bf16/f16 -> f32/bf16)."""
     dev = nat.require_gpu(t, what="convert")

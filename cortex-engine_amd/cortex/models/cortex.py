@@ -12,8 +12,9 @@ the gfx950 kernels without padding the events:
    not exist, so they are never visited;
 5. ``out_proj`` with the learned latents as a broadcast residual, 7 fused
    self-attention blocks, ``final_norm``;
-6. behaviour head: ``norm`` + ``kv_proj`` fused, the 2 batch-invariant queries
-   projected once, attention, ``out_proj`` to (B, behavior_dim).
+6. behaviour head in one kernel: both LayerNorms, then the weights folded into the
+   2 batch-invariant queries and into ``out_proj`` (once per parameter state), so
+   only 32 dot products per latent row remain.
 
 Results equal the reference forward (padded SDPA with a key-padding mask) up to
 floating-point rounding; with ``config.dtype='float32'`` every operand is fp32.
@@ -50,14 +51,20 @@ class BehaviorDecoder(nn.Module):
     def forward_rows(self, lat: torch.Tensor, batch: int, pre_norm: nn.LayerNorm | None = None) -> torch.Tensor:
         """(B*L, D) latents -> (B, behavior_dim) fp32.
 
-        ``pre_norm`` (the encoder's final norm) is applied to ``lat`` first; with bf16
-        compute both LayerNorms run in one row kernel that writes the kv_proj operand.
+        ``pre_norm`` (the encoder's final norm) is applied to ``lat`` first.  With bf16
+        compute the whole head is one kernel (``cortex_behavior_head``): both LayerNorms,
+        then the weights folded into the queries and the output projection -- scores
+        ``(W_k^T q) . n`` and values ``(W_v^T w_out) . n`` -- so the kv projection, the
+        attention and ``out_proj`` are never materialised.  Otherwise (fp32, calibration
+        hooks, shapes outside the kernel) the head runs as written.
         """
         compute = self.config.compute_dtype
         L = self.config.num_latents
         D = lat.shape[1]
         H = self.num_heads
         Q = self.query.shape[0]
+        if pre_norm is not None and self._fused_ok(lat, pre_norm):
+            return ops.behavior_head(lat, batch, ln_params(pre_norm), ln_params(self.norm), self._folded(), Q, H)
         if (pre_norm is not None and compute == torch.bfloat16 and not self.kv_proj._forward_pre_hooks
                 and ln_rows_ok(lat, pre_norm, self.norm)):
             kv = ops.norm_linear(normalize_bf16(lat, pre_norm, self.norm), **exec_weights(self.kv_proj, compute),
@@ -73,6 +80,28 @@ class BehaviorDecoder(nn.Module):
                       ops.heads_view(kv, batch, L, H, D, D), out=o, batch=batch)
         out = apply_linear(self.out_proj, o_buf, out_dtype=torch.float32, compute=compute)
         return out.reshape(batch, Q)
+
+    def _fused_ok(self, lat: torch.Tensor, pre_norm: nn.LayerNorm) -> bool:
+        """Whether the fused head kernel covers this call: bf16 compute, no calibration hooks,
+        no biases on the folded projections, Q*H <= 16 and D in {256, 512, 768}."""
+        mods = (self.q_proj, self.kv_proj, self.out_proj, self.norm, pre_norm)
+        return (self.config.compute_dtype == torch.bfloat16 and not any(m._forward_pre_hooks for m in mods)
+                and self.kv_proj.bias is None and self.out_proj.bias is None
+                and self.query.shape[0] * self.num_heads <= 16 and lat.shape[1] in (256, 512, 768)
+                and lat.shape[1] % self.num_heads == 0 and ln_rows_ok(lat, pre_norm, self.norm)
+                and lat.data_ptr() % 16 == 0 and lat.stride(0) % 4 == 0)
+
+    def _folded(self) -> torch.Tensor:
+        """The (32, D) folded query / value-output matrix, once per parameter state."""
+        compute = torch.bfloat16
+
+        def build():
+            q = apply_linear(self.q_proj, self.query, out_dtype=compute, compute=compute)
+            kv, ow = exec_weights(self.kv_proj, compute), exec_weights(self.out_proj, compute)
+            return ops.head_prep(q, kv["weight"], kv["weight_scale"], ow["weight"], ow["weight_scale"],
+                                 self.num_heads)
+
+        return batch_invariant(self, "head_folded", [self.query], [self.q_proj, self.kv_proj, self.out_proj], build)
 
     def forward(self, latents: torch.Tensor) -> torch.Tensor:
         """latents (B, L, D) -> behaviour (B, behavior_dim)."""

@@ -1,8 +1,9 @@
 // Spike tokenizer and ragged-event pack for gfx950.
 //
 //   * pack plan: a device-side stable counting sort of the events by batch index
-//     (three short launches, no host synchronisation): per-chunk histograms,
-//     one scan over (chunk, sample), then in-order ranking inside each chunk.
+//     (no host synchronisation): per-chunk histograms, one scan over (chunk,
+//     sample), then in-order ranking inside each chunk -- one launch for small
+//     plans, three for large ones.
 //     It yields CSR offsets (B+1), the CSR row of every event and the source
 //     event of every CSR row -- exactly the stable argsort + exclusive cumsum of
 //     the reference pack (cortex/models/cortex.py:140-160).
@@ -48,12 +49,26 @@ __global__ __launch_bounds__(256) void pack_count_kernel(const int64_t* __restri
   const int64_t beg = (int64_t)chunk * C;
   const int64_t end = min(E, beg + C);
   bool bad = false;
-  for (int64_t i = beg + threadIdx.x; i < end; i += blockDim.x) {
-    int64_t b = bidx[i * s_bidx];
-    if (b < 0 || b >= B) {
-      bad = true;
-    } else {
-      atomicAdd(&hist[b], 1);
+  const int lane = threadIdx.x & 63;
+  for (int64_t i0 = beg; i0 < end; i0 += blockDim.x) {  // every lane runs the same trip count
+    const int64_t i = i0 + threadIdx.x;
+    int64_t b = -1;
+    if (i < end) {
+      b = bidx[i * s_bidx];
+      if (b < 0 || b >= B) {
+        bad = true;
+        b = -1;
+      }
+    }
+    // one atomic per distinct sample among the wave's 64 events (sorted batches would
+    // otherwise send 64 atomics to one LDS word)
+    uint64_t active = __ballot(b >= 0);
+    while (active) {
+      const int leader = __ffsll((unsigned long long)active) - 1;
+      const int64_t lb = __shfl(b, leader, 64);
+      const uint64_t same = __ballot(b == lb) & active;
+      if (lane == leader) atomicAdd(&hist[lb], (int)__popcll(same));
+      active &= ~same;
     }
   }
   if (bad && err) atomicOr(err, ERR_BATCH_INDEX);
@@ -137,6 +152,120 @@ __global__ __launch_bounds__(64) void pack_rank_kernel(const int64_t* __restrict
       if (lane == leader) next[lb] = row0 + __popcll(same);
       __syncthreads();
       active &= ~same;
+    }
+  }
+}
+
+// Small plans (B <= 1024, E <= 65536) in ONE launch: one workgroup of 16 waves, wave w
+// owning the contiguous event chunk w.  Per-wave histograms in LDS, the two scans
+// (over waves per sample, then over samples), then the same in-order ranking as
+// pack_rank_kernel.  Same results as the three-launch path, a third of its launches.
+constexpr int PS_WAVES = 16;
+constexpr int PS_MAX_B = 1024;
+constexpr int64_t PS_MAX_E = 65536;
+constexpr int PS_UNROLL = 8;
+
+__global__ __launch_bounds__(1024) void pack_small_kernel(const int64_t* __restrict__ bidx, int64_t s_bidx, int64_t E,
+                                                          int B, int64_t* __restrict__ offsets,
+                                                          int64_t* __restrict__ order, int64_t* __restrict__ dst_rows,
+                                                          int64_t* __restrict__ rank, int32_t* __restrict__ err) {
+  __shared__ int cnt[PS_WAVES * PS_MAX_B];  // per-wave counts, then per-wave next CSR row
+  __shared__ int first[PS_MAX_B];           // CSR offset of each sample
+  __shared__ int wsum[PS_WAVES];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  for (int i = tid; i < PS_WAVES * B; i += blockDim.x) cnt[i] = 0;
+  __syncthreads();
+  const int64_t C = cdiv(E, (int64_t)PS_WAVES);
+  const int64_t beg = w * C, end = min(E, beg + C);
+  int* mine = cnt + w * B;
+  bool bad = false;
+  for (int64_t base = beg; base < end; base += 64 * PS_UNROLL) {  // PS_UNROLL loads in flight per lane
+    int64_t bv[PS_UNROLL];
+#pragma unroll
+    for (int u = 0; u < PS_UNROLL; ++u) {
+      const int64_t i = base + 64 * u + lane;
+      bv[u] = i < end ? bidx[i * s_bidx] : (int64_t)B;
+    }
+#pragma unroll
+    for (int u = 0; u < PS_UNROLL; ++u) {
+      int64_t b = bv[u];
+      if (base + 64 * u + lane < end && (b < 0 || b >= B)) bad = true;
+      if (b < 0 || b >= B) b = -1;
+      // one update per distinct sample in the 64 events: sorted batches (the common
+      // case) would otherwise send 64 atomics to one LDS word
+      uint64_t active = __ballot(b >= 0);
+      while (active) {
+        const int leader = __ffsll((unsigned long long)active) - 1;
+        const int lb = __builtin_amdgcn_readlane((int)b, leader);  // wave-uniform, b < B <= 1024
+        const uint64_t same = __ballot(b == lb) & active;
+        if (lane == leader) mine[lb] += __popcll(same);
+        active &= ~same;
+      }
+    }
+  }
+  if (bad && err) atomicOr(err, ERR_BATCH_INDEX);
+  __syncthreads();
+  // per sample: exclusive prefix over the waves (in place) and the sample's total
+  int total_b = 0;
+  if (tid < B) {
+    for (int ww = 0; ww < PS_WAVES; ++ww) {
+      const int t = cnt[ww * B + tid];
+      cnt[ww * B + tid] = total_b;
+      total_b += t;
+    }
+  }
+  // exclusive scan of the totals over samples: lane scan, then over the 16 wave sums
+  int incl = total_b;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int y = __shfl_up(incl, o, 64);
+    if (lane >= o) incl += y;
+  }
+  if (lane == 63) wsum[w] = incl;
+  __syncthreads();
+  int wbase = 0;
+  for (int ww = 0; ww < w; ++ww) wbase += wsum[ww];
+  if (tid < B) {
+    const int excl = wbase + incl - total_b;
+    first[tid] = excl;
+    offsets[tid] = excl;
+  }
+  if (tid == 0) {
+    int all = 0;
+    for (int ww = 0; ww < PS_WAVES; ++ww) all += wsum[ww];
+    offsets[B] = all;
+  }
+  __syncthreads();
+  for (int i = tid; i < PS_WAVES * B; i += blockDim.x) cnt[i] += first[i % B];
+  __syncthreads();
+  // in-order ranking inside the chunk; only this wave touches its row of `cnt`
+  const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  for (int64_t base = beg; base < end; base += 64 * PS_UNROLL) {
+    int64_t bv[PS_UNROLL];
+#pragma unroll
+    for (int u = 0; u < PS_UNROLL; ++u) {
+      const int64_t i = base + 64 * u + lane;
+      bv[u] = i < end ? bidx[i * s_bidx] : -1;
+    }
+#pragma unroll
+    for (int u = 0; u < PS_UNROLL; ++u) {
+      const int64_t i = base + 64 * u + lane;
+      const int64_t b = bv[u] >= B ? -1 : bv[u];
+      uint64_t active = __ballot(b >= 0);
+      while (active) {
+        const int leader = __ffsll((unsigned long long)active) - 1;
+        const int lb = __builtin_amdgcn_readlane((int)b, leader);  // wave-uniform, b < B <= 1024
+        const uint64_t same = __ballot(b == lb) & active;
+        const int row0 = mine[lb];  // one LDS word for the whole wave; read before the update below
+        if (b == lb) {
+          const int64_t row = row0 + __popcll(same & lt_mask);
+          order[row] = i;
+          if (dst_rows) dst_rows[i] = row;
+          if (rank) rank[i] = row - first[lb];
+        }
+        if (lane == leader) mine[lb] = row0 + __popcll(same);
+        active &= ~same;
+      }
     }
   }
 }
@@ -338,6 +467,12 @@ int cortex_pack_plan(const int64_t* batch_indices, int64_t s_bidx, int64_t E, in
     set_error("cortex_pack_plan: workspace of %lld bytes is smaller than the required %lld",
               (long long)workspace_bytes, (long long)need);
     return E_WORKSPACE;
+  }
+  if (B <= PS_MAX_B && E <= PS_MAX_E) {
+    hipLaunchKernelGGL(pack_small_kernel, dim3(1), dim3(64 * PS_WAVES), 0, stream, batch_indices, s_bidx, E, (int)B,
+                       offsets, order, dst_rows, rank, err_flag);
+    CORTEX_CHECK_LAUNCH("pack_small_kernel");
+    return OK;
   }
   const int64_t C = pack_chunk_size(E);
   const int nchunks = (int)cdiv(E, C);

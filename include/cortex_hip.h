@@ -189,6 +189,32 @@ int cortex_temporal_block_mask(const int64_t* event_times, int64_t t_stride, int
                                int64_t block_l, int64_t block_e, int64_t n_q, int64_t n_k, uint8_t* out,
                                int64_t out_sb, hipStream_t stream);
 
+/* Behaviour head (BehaviorDecoder.forward, cortex/models/cortex.py:29-53) with its
+ * batch-invariant factors folded: cortex_head_prep builds, once per parameter state,
+ * the (32, D) bf16 matrix ac of rows a_{q,h} = W_k[h]^T q_h * log2(e)/sqrt(Dh) (rows
+ * r = q*H + h < Q*H) and c_{h} = W_v[h]^T w_out[h] (rows 16 + r, h = r % H), from the
+ * projected queries qv (Q, D) bf16, the kv weight image (2D, D) bf16 with optional
+ * per-row scale s_kv (2D), and the output weight image (1, D) with optional scale.
+ * Requires Q*H <= 16, Dh = D / H. */
+int cortex_head_prep(const void* qv, int64_t ld_q, int64_t Q, int64_t H, int64_t D, const void* wkv,
+                     const float* s_kv, int64_t ld_w, const void* wout, const float* s_out, void* ac,
+                     hipStream_t stream);
+
+/* cortex_behavior_head: out[b, q] (B, Q) fp32 from the fp32 latents x (B*L rows of D,
+ * row b*L + l at x + (b*L + l) * ld_x): n_l = LN2(LN1(x_l)) (gamma/beta/eps each, rounded
+ * to bf16), s = ac[r] . n_l, t = ac[16 + r] . n_l, out[b,q] = sum_h sum_l 2^s t / sum_l 2^s
+ * over rows r = q*H + h -- the reference head's value up to rounding (softmax weights
+ * sum to one, so V and out_proj commute with the sum over latents).  D in {256, 512,
+ * 768}; rows and parameters 16-byte aligned; workspace of
+ * cortex_behavior_head_workspace_bytes(B, L) bytes for the per-split partials. */
+int cortex_behavior_head(const float* x, int64_t ld_x, int64_t B, int64_t L, int64_t D, int64_t Q, int64_t H,
+                         const float* gamma1, const float* beta1, float eps1, const float* gamma2,
+                         const float* beta2, float eps2, const void* ac, float* out, void* workspace,
+                         int64_t workspace_bytes, hipStream_t stream);
+
+/* Bytes of the partials workspace cortex_behavior_head needs for B samples of L latents. */
+int64_t cortex_behavior_head_workspace_bytes(int64_t B, int64_t L);
+
 /* Streaming window assembly from device event pages.  No single reference
  * counterpart: it serves StreamingKVCache's role (cortex/cache/streaming.py:79-236)
  * with pages of raw events keyed by ABSOLUTE time bin, since the reference's window

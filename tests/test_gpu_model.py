@@ -153,3 +153,35 @@ def test_batch_invariant_queries_follow_parameter_updates():
         d = model(*inputs, batch_size=3)["behavior"].clone()
     assert not torch.equal(a, c)
     torch.testing.assert_close(c, d, rtol=0, atol=0)
+
+
+@pytest.mark.parametrize("name", ["xs", "s"])
+def test_fused_behavior_head_matches_oracle_and_unfused(name):
+    """The folded one-kernel head (both LayerNorms, folded query/value-output rows) against
+    the float32 oracle head on the same latents and against the head run as written
+    (forced by a calibration-style pre-hook).  Bar: the decoded-velocity 2e-2 max-abs."""
+    arrs = _config3_inputs(2, 64)
+    model = _int8(_model(name, "bfloat16"), [torch.from_numpy(a).to(DEV) for a in arrs])
+    cfg = model.config
+    B, L, D = 5, cfg.num_latents, cfg.latent_dim
+    g = torch.Generator().manual_seed(3)
+    lat = (torch.randn(B * L, D, generator=g) * 1.5 + 0.2).to(DEV)
+    head, fn = model.behavior_head, model.encoder.final_norm
+    with torch.no_grad():
+        fused = head.forward_rows(lat, B, pre_norm=fn)
+        hook = head.q_proj.register_forward_pre_hook(lambda m, a: None)
+        try:
+            plain = head.forward_rows(lat, B, pre_norm=fn)
+        finally:
+            hook.remove()
+        again = head.forward_rows(lat, B, pre_norm=fn)  # the folded rows come from the cache
+    sd = {k: v.detach().cpu() for k, v in model.state_dict().items()}
+    shape = O.CORTEX_S_SHAPE if name == "s" else O.CORTEX_XS_SHAPE
+    x = torch.nn.functional.layer_norm(lat.cpu().reshape(B, L, D), (D,), sd["encoder.final_norm.weight"],
+                                       sd["encoder.final_norm.bias"], fn.eps)
+    ref = O.behavior_head(sd, shape, x).numpy()
+    f, p = fused.cpu().numpy(), plain.cpu().numpy()
+    assert f.shape == (B, 2) and np.isfinite(f).all()
+    assert np.abs(f - ref).max() <= 2e-2, (np.abs(f - ref).max(), np.abs(ref).max())
+    assert np.abs(f - p).max() <= 2e-2
+    assert torch.equal(fused, again)

@@ -133,6 +133,20 @@ def test_pack_plan_large_multi_chunk():
         np.testing.assert_array_equal(order.cpu().numpy(), p.order)
 
 
+@pytest.mark.parametrize("E,B", [(65536, 1024), (65537, 1024), (5000, 1025), (64, 1), (65536, 3)])
+def test_pack_plan_path_boundaries(E, B):
+    """Either side of the one-launch plan's limits (B <= 1024, E <= 65536): same results."""
+    from cortex.kernels.pack import pack_plan
+
+    rng = np.random.default_rng(E + B)
+    bidx = rng.integers(0, B, E)
+    p = O.pack_events(np.zeros((E, 1), np.float32), bidx, batch_size=B)
+    off, order, rank = pack_plan(torch.from_numpy(bidx).to(DEV), B)
+    np.testing.assert_array_equal(off.cpu().numpy(), p.offsets)
+    np.testing.assert_array_equal(order.cpu().numpy(), p.order)
+    np.testing.assert_array_equal(rank.cpu().numpy(), p.rank)
+
+
 def test_pack_events_drop_in_matches_oracle():
     from cortex.models.cortex import _pack_events
 
