@@ -38,7 +38,7 @@ from cortex import _native as nat
 
 @dataclass
 class PageMeta:
-    """Metadata of one cache page (reference streaming.py:67-75)."""
+    """Metadata of one cache page (reference streaming.py:65-76)."""
 
     page_id: int
     session_id: str

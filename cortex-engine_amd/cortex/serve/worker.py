@@ -1,9 +1,9 @@
-"""Batched inference worker on gfx950 (reference cortex/serve/worker.py:95-249).
+"""Batched inference worker on gfx950 (reference cortex/serve/worker.py:92-253).
 
 Same surface as the reference's ``InferenceWorker``: ``run_batch`` (async, one
 single-thread executor so forward passes never overlap), ``_run_batch_sync``,
 ``warmup``, ``ready``, ``shutdown``, and the payload and result dicts of its
-contract (worker.py:22-31).  What changes is the way a batch reaches the GPU:
+contract (worker.py:22-32).  What changes is the way a batch reaches the GPU:
 
 * The payloads are already grouped by request, so the batch is CSR by
   construction: the host writes the events sample after sample plus the (B+1)
@@ -41,7 +41,7 @@ _FIELDS = ("neuron_id", "time_bin", "value")
 
 def load_model(config: CortexConfig, checkpoint_path: str | None = None,
                device: torch.device | None = None) -> nn.Module:
-    """``CortexModel`` on ``device`` (reference worker.py:62-92).
+    """``CortexModel`` on ``device`` (reference worker.py:61-89).
 
     A checkpoint is read with ``torch.load(weights_only=True)``: plain tensors and
     containers only.  The reference's ``{"model_state_dict": ...}`` wrapper and a bare
@@ -97,7 +97,7 @@ def pack_payloads(payloads: list[dict[str, Any]], bucket: bool = True,
     """Payloads -> the flat int64 input ``[nid (Eb) | tb (Eb) | val (Eb) | offsets (B+1)]``.
 
     Returns ``(flat, B, E, Eb)``: B ends at the last payload with events (the
-    reference's ``max(batch_indices) + 1``, worker.py:174-181 and cortex.py:140), E is
+    reference's ``max(batch_indices) + 1``, worker.py:171-177,238 and cortex.py:140), E is
     the number of real events, Eb the padded count (``event_bucket(E)`` when
     ``bucket``, else E).  Events keep the payload order, so sample b owns rows
     ``[offsets[b], offsets[b+1])``; padding rows are zeros.  B = 0 when no payload has
@@ -149,7 +149,7 @@ class _CsrGraph:
 
 
 class InferenceWorker:
-    """Batched inference worker (reference worker.py:95-249); one model, one GPU.
+    """Batched inference worker (reference worker.py:92-253); one model, one GPU.
 
     ``use_graphs`` replays a captured graph per (B, event bucket), keeping at most
     ``max_graphs`` of them (least recently used evicted); all share one memory pool,
@@ -183,7 +183,7 @@ class InferenceWorker:
     # ------------------------------------------------------------------ API
 
     def warmup(self, n_iters: int = 3) -> None:
-        """Dummy batches of 64 events each (reference worker.py:136-149)."""
+        """Dummy batches of 64 events each (reference worker.py:135-147)."""
         dummy = [{"request_id": f"warmup_{i}", "events": [{"neuron_id": 0, "time_bin": 0, "value": 0}] * 64}
                  for i in range(min(n_iters, self.max_batch_size))]
         for _ in range(n_iters):
