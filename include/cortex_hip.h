@@ -230,7 +230,7 @@ int cortex_gather_event_pages(const int64_t* pool, int64_t num_pages, int64_t pa
                               hipStream_t stream);
 
 /* The page write of the same cache (reference StreamingKVCache.write,
- * cortex/cache/streaming.py:157-194, batched): plan (n_items, 3) int64 of (page,
+ * cortex/cache/streaming.py:155-190, batched): plan (n_items, 3) int64 of (page,
  * count, first staged row); item i copies staged rows [s0, s0+count) of
  * src[f * field_stride + row] into page `page` of the pool.  A malformed item writes
  * nothing and sets bit 2 of *err (when given).  Bit-exact copies. */
