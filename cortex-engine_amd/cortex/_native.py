@@ -73,6 +73,10 @@ _SIGNATURES = {
         [_int, _i64, _i64, _i64, _i64, _i64, _ptr, _i64, _i64, _i64, _ptr, _i64, _i64, _i64, _ptr, _i64, _i64,
          _i64, _ptr, _ptr, _ptr, _i64, _ptr, _i64, _i64, _i64, _i64, _i64, _f32, _ptr, _i64, _i64, _i64, _ptr],
     ),
+    "cortex_linear_residual_ln": (
+        _int,
+        [_i64, _i64, _i64, _ptr, _i64, _ptr, _i64, _ptr, _ptr, _ptr, _i64, _i64, _ptr, _i64, _ptr, _ptr, _f32, _ptr,
+         _i64, _ptr]),
     "cortex_head_prep": (_int, [_ptr, _i64, _i64, _i64, _i64, _ptr, _ptr, _i64, _ptr, _ptr, _ptr, _ptr]),
     "cortex_behavior_head_workspace_bytes": (_i64, [_i64, _i64]),
     "cortex_behavior_head": (

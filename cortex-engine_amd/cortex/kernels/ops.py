@@ -192,6 +192,25 @@ def ln_rows(x: torch.Tensor, ln1, ln2=None, out_bf16: bool = True, out_f32: bool
     return ob if out_bf16 else of
 
 
+def linear_residual_ln(x: torch.Tensor, weight: torch.Tensor, weight_scale=None, bias=None, *,
+                       residual: torch.Tensor, ln, res_rows: int = 0, out: torch.Tensor | None = None):
+    """``out = residual + x @ (weight * scale)^T + bias`` (fp32) and ``LN(out)`` (bf16) in one
+    kernel; ``x`` (M, K) and ``weight`` (N, K) bf16, N in {256, 512}.  ``out`` may be
+    ``residual`` itself.  Returns ``(out, xn)``."""
+    dev = nat.require_gpu(x, weight, weight_scale, bias, residual, out, what="linear_residual_ln")
+    M, K = x.shape
+    N = weight.shape[0]
+    if out is None:
+        out = torch.empty((M, N), dtype=torch.float32, device=dev)
+    xn = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+    g, b, eps = ln
+    nat.call("cortex_linear_residual_ln", M, N, K, nat.ptr(x), x.stride(0), nat.ptr(weight), weight.stride(0),
+             nat.ptr(weight_scale), nat.ptr(bias), nat.ptr(residual), residual.stride(0), int(res_rows),
+             nat.ptr(out), out.stride(0), nat.ptr(g), nat.ptr(b), float(eps), nat.ptr(xn), xn.stride(0),
+             nat.stream_of(dev))
+    return out, xn
+
+
 def head_prep(q: torch.Tensor, kv_weight: torch.Tensor, kv_scale, out_weight: torch.Tensor, out_scale,
               num_heads: int) -> torch.Tensor:
     """Folded behaviour-head matrix (32, D) bf16 (see ``cortex_head_prep``) from the projected

@@ -114,6 +114,33 @@ def normalize_bf16(x: torch.Tensor, norm: nn.LayerNorm, norm2: nn.LayerNorm | No
     return ops.ln_rows(x2, ln_params(norm), ln_params(norm2) if norm2 is not None else None)
 
 
+def residual_ln_ok(lin: nn.Module, norm: nn.LayerNorm, consumer: nn.Module, x: torch.Tensor,
+                   compute: torch.dtype) -> bool:
+    """Whether ``residual + lin(a)`` followed by ``norm`` (feeding ``consumer``) can run as
+    one ``cortex_linear_residual_ln`` launch: bf16 compute, no calibration hooks on the
+    linear, the norm's consumer or the norm, D in {256, 512}, fp32 aligned norm parameters."""
+    if compute != torch.bfloat16 or lin._forward_pre_hooks or consumer._forward_pre_hooks or norm._forward_pre_hooks:
+        return False
+    D = x.shape[-1]
+    src = lin.weight_int8 if hasattr(lin, "weight_int8") else lin.weight
+    if D not in (256, 512) or src.shape[0] != D or src.shape[1] % 64 or x.dtype != torch.float32:
+        return False
+    if x.data_ptr() % 16 or x.stride(-1) != 1 or (x.dim() > 1 and x.stride(0) % 4):
+        return False
+    if lin.bias is not None and (lin.bias.dtype != torch.float32 or lin.bias.data_ptr() % 16):
+        return False
+    return ln_rows_ok(x, norm) and INT8_WEIGHTS == "image"
+
+
+def linear_residual_ln(lin: nn.Module, a: torch.Tensor, residual: torch.Tensor, norm: nn.LayerNorm, *,
+                       res_rows: int = 0, out: torch.Tensor | None = None):
+    """``x = residual + lin(a)`` (fp32) and ``norm(x)`` (bf16) in one launch (see
+    ``residual_ln_ok``).  Returns ``(x, norm(x))``."""
+    w = exec_weights(lin, torch.bfloat16)
+    return ops.linear_residual_ln(a, w["weight"], w["weight_scale"], w["bias"], residual=residual,
+                                  ln=ln_params(norm), res_rows=res_rows, out=out)
+
+
 def apply_linear(lin: nn.Module, x: torch.Tensor, *, norm: nn.LayerNorm | None = None, stats=None,
                  act: str | None = None, residual: torch.Tensor | None = None, res_rows: int = 0,
                  out_dtype: torch.dtype, compute: torch.dtype, out: torch.Tensor | None = None) -> torch.Tensor:

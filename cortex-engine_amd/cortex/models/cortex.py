@@ -27,8 +27,8 @@ from torch import nn
 
 from cortex.kernels import ops
 from cortex.kernels.pack import pack_events as _device_pack_events
-from cortex.models._layers import (apply_linear, batch_invariant, exec_weights, fused_tokens_ok, ln_params,
-                                   ln_rows_ok, normalize_bf16)
+from cortex.models._layers import (apply_linear, batch_invariant, exec_weights, fused_tokens_ok, linear_residual_ln,
+                                   ln_params, ln_rows_ok, normalize_bf16, residual_ln_ok)
 from cortex.models.config import CortexConfig
 from cortex.models.perceiver import PerceiverEncoder
 from cortex.models.tokenizer import SpikeTokenizer
@@ -195,14 +195,21 @@ class CortexModel(nn.Module):
         o_buf, o = ops.merge_heads_out(B, L, H, D // H, compute, kv.device)
         ops.attention(ops.heads_view(q, 1, L, H), ops.heads_view(kv, 1, E, H, 0, D),
                       ops.heads_view(kv, 1, E, H, D, D), kv_offsets=offsets, out=o, batch=B)
-        x = apply_linear(xa.out_proj, o_buf, residual=enc.latents, res_rows=L, out_dtype=torch.float32,
-                         compute=compute)  # (B*L, D) fp32 residual stream
-        x = self._encode(x, B)
+        first = enc.self_attn_blocks[0] if len(enc.self_attn_blocks) else None
+        xn = None
+        if first is not None and residual_ln_ok(xa.out_proj, first.norm_attn, first.qkv_proj, enc.latents, compute):
+            # latents + out_proj(attn) and the first block's norm_attn in one launch
+            x, xn = linear_residual_ln(xa.out_proj, o_buf, enc.latents, first.norm_attn, res_rows=L,
+                                       out=torch.empty(B * L, D, dtype=torch.float32, device=kv.device))
+        else:
+            x = apply_linear(xa.out_proj, o_buf, residual=enc.latents, res_rows=L, out_dtype=torch.float32,
+                             compute=compute)  # (B*L, D) fp32 residual stream
+        x = self._encode(x, B, xn)
         return self.behavior_head.forward_rows(x, B, pre_norm=enc.final_norm)
 
-    def _encode(self, x: torch.Tensor, B: int) -> torch.Tensor:
+    def _encode(self, x: torch.Tensor, B: int, xn: torch.Tensor | None = None) -> torch.Tensor:
         """The self-attention stack on the fresh residual buffer ``x`` (updated in place)."""
-        return self.encoder.encode_rows(x, B, final_norm=False, inplace=True)
+        return self.encoder.encode_rows(x, B, final_norm=False, inplace=True, xn=xn)
 
 
 def _pack_events(flat_tokens: torch.Tensor, batch_indices: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:

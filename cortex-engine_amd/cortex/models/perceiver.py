@@ -15,7 +15,7 @@ import torch
 from torch import nn
 
 from cortex.kernels import ops
-from cortex.models._layers import apply_linear, batch_invariant
+from cortex.models._layers import apply_linear, batch_invariant, exec_weights, linear_residual_ln, residual_ln_ok
 from cortex.models.config import CortexConfig
 
 
@@ -79,20 +79,34 @@ class SelfAttentionBlock(nn.Module):
             nn.Linear(mlp_hidden, config.latent_dim, bias=False),
         )
 
-    def forward_rows(self, x: torch.Tensor, batch: int, length: int, inplace: bool = False) -> torch.Tensor:
+    def forward_rows(self, x: torch.Tensor, batch: int, length: int, inplace: bool = False,
+                     xn: torch.Tensor | None = None) -> torch.Tensor:
         """Block on a (B*L, D) fp32 residual buffer; returns the new residual buffer
-        (``x`` itself, updated in place, when ``inplace``)."""
+        (``x`` itself, updated in place, when ``inplace``).  ``xn``: ``norm_attn(x)`` as bf16
+        rows when the producer of ``x`` already wrote it.
+
+        With bf16 compute, ``x + out_proj(attn)`` and ``norm_mlp`` of the result run as one
+        kernel (``ops.linear_residual_ln``); the LayerNorm'd rows feed ``mlp.0`` directly.
+        """
         compute = self.config.compute_dtype
         D = x.shape[1]
         H = self.num_heads
-        qkv = apply_linear(self.qkv_proj, x, norm=self.norm_attn, out_dtype=compute, compute=compute)
+        if xn is not None:
+            qkv = ops.norm_linear(xn, **exec_weights(self.qkv_proj, compute), out_dtype=compute, compute_dtype=compute)
+        else:
+            qkv = apply_linear(self.qkv_proj, x, norm=self.norm_attn, out_dtype=compute, compute=compute)
         o_buf, o = ops.merge_heads_out(batch, length, H, D // H, compute, x.device)
         ops.attention(ops.heads_view(qkv, batch, length, H, 0, D), ops.heads_view(qkv, batch, length, H, D, D),
                       ops.heads_view(qkv, batch, length, H, 2 * D, D), out=o)
         # each residual element is read and then written by the same lane: in place is safe
-        x = apply_linear(self.out_proj, o_buf, residual=x, out_dtype=x.dtype, compute=compute,
-                         out=x if inplace else None)
-        h = apply_linear(self.mlp[0], x, norm=self.norm_mlp, act="gelu", out_dtype=compute, compute=compute)
+        if residual_ln_ok(self.out_proj, self.norm_mlp, self.mlp[0], x, compute):
+            x, hn = linear_residual_ln(self.out_proj, o_buf, x, self.norm_mlp, out=x if inplace else None)
+            h = ops.norm_linear(hn, **exec_weights(self.mlp[0], compute), act="gelu", out_dtype=compute,
+                                compute_dtype=compute)
+        else:
+            x = apply_linear(self.out_proj, o_buf, residual=x, out_dtype=x.dtype, compute=compute,
+                             out=x if inplace else None)
+            h = apply_linear(self.mlp[0], x, norm=self.norm_mlp, act="gelu", out_dtype=compute, compute=compute)
         return apply_linear(self.mlp[2], h, residual=x, out_dtype=x.dtype, compute=compute,
                             out=x if inplace else None)
 
@@ -114,11 +128,13 @@ class PerceiverEncoder(nn.Module):
         self.self_attn_blocks = nn.ModuleList([SelfAttentionBlock(config) for _ in range(config.num_layers)])
         self.final_norm = nn.LayerNorm(config.latent_dim)
 
-    def encode_rows(self, x: torch.Tensor, batch: int, final_norm: bool = True, inplace: bool = False) -> torch.Tensor:
-        """Self-attention stack (+ final norm) on the (B*L, D) residual after cross-attention."""
+    def encode_rows(self, x: torch.Tensor, batch: int, final_norm: bool = True, inplace: bool = False,
+                    xn: torch.Tensor | None = None) -> torch.Tensor:
+        """Self-attention stack (+ final norm) on the (B*L, D) residual after cross-attention;
+        ``xn`` is the first block's ``norm_attn(x)`` when already computed."""
         L = self.config.num_latents
-        for block in self.self_attn_blocks:
-            x = block.forward_rows(x, batch, L, inplace=inplace)
+        for i, block in enumerate(self.self_attn_blocks):
+            x = block.forward_rows(x, batch, L, inplace=inplace, xn=xn if i == 0 else None)
         if not final_norm:
             return x
         return ops.layer_norm(x, self.final_norm.weight, self.final_norm.bias, self.final_norm.eps)

@@ -1,0 +1,300 @@
+// Residual linear + the LayerNorm that follows it, in one kernel (gfx950):
+//
+//   out[m, :] = res[m % res_rows, :] + (A[m, :] . W^T) * w_scale (+ bias)     fp32
+//   xn[m, :]  = LN(out[m, :]) * gamma + beta                                   bf16
+//
+// This is SelfAttentionBlock's  x = x + out_proj(attn);  h_in = norm_mlp(x)
+// (reference cortex/models/perceiver.py:121-124), and the cross-attention block's
+// residual followed by the first self-attention block's norm_attn.  A LayerNorm
+// needs whole rows, so a workgroup owns full rows: 32 rows x all N (<= 512) columns,
+// 8 wavefronts of 32 x N/8.  With K = 512 the weight (N x K bf16, 512 KiB) is
+// re-read by every workgroup from L2, which costs less than a separate LayerNorm
+// pass over the fp32 residual stream (read 4 B + write 2 B per element, and a launch).
+//
+// Operand streaming as in gemm_bf16.hip: direct-to-LDS transfers through a ring of
+// STAGES, early stage release, double-buffered fragments, C^T tiles so a lane holds 4
+// consecutive columns of one row.  The residual tile is prefetched into registers.
+// Row statistics: lane sums -> xor-shuffles over the 4 lane groups -> the 8
+// wavefronts' partials through LDS; two passes (mean, then squared deviations) as
+// the LayerNorm row kernel.
+#include <hip/hip_runtime.h>
+
+#include "common.h"
+
+namespace cortex {
+
+namespace {
+
+constexpr int RL_BM = 32, RL_BK = 64, RL_WAVES = 8, RL_THREADS = 64 * RL_WAVES;
+
+template <int n>
+__device__ __forceinline__ void rl_wait_vm() {
+  static_assert(n >= 0 && n < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((n & 15) | 0x70 | 0xF00 | ((n >> 4) << 14));
+}
+
+__device__ __forceinline__ int rl_swz(int r) { return (r >> 1) & 7; }
+
+struct RowLnArgs {
+  int64_t M, N, K;
+  const bf16* x;
+  int64_t ld_x;
+  const bf16* w;
+  int64_t ld_w;
+  const float* w_scale;
+  const float* bias;
+  const float* res;
+  int64_t ld_res, res_rows;
+  float* out;
+  int64_t ld_out;
+  const float* gamma;
+  const float* beta;
+  float eps;
+  bf16* xn;
+  int64_t ld_xn;
+};
+
+template <int BN, int S>
+__global__ __launch_bounds__(RL_THREADS) void gemm_rowln_kernel(RowLnArgs g) {
+  constexpr int WN = BN / RL_WAVES;   // columns per wavefront
+  constexpr int TM = RL_BM / 16, TN = WN / 16;
+  constexpr int A_STAGE = RL_BM * 128, W_STAGE = BN * 128;  // bytes
+  constexpr int WB = W_STAGE / 1024 / RL_WAVES;             // W transfers per wavefront and step
+  constexpr int PER = 1 + WB;                                // + one A transfer (blocks shared 2:1)
+  constexpr int RING = S * (A_STAGE + W_STAGE);
+  static_assert(A_STAGE == 4 * 1024 && W_STAGE % (1024 * RL_WAVES) == 0 && TN >= 1, "shape");
+  static_assert(PER * (S - 1) < 64, "vmcnt range");
+  __shared__ __attribute__((aligned(1024))) unsigned char smem[RING];
+
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int fr = lane & 15, g4 = lane >> 4;
+  const int M = (int)g.M, K = (int)g.K;
+  const int m0 = blockIdx.x * RL_BM;
+  const int wcol = wid * WN;
+
+  // transfer sources: A block (wid & 3) = rows 8 (wid & 3) .. +7 (waves 4..7 repeat
+  // waves 0..3: identical bytes to identical addresses); W blocks wid * WB + i
+  const int ar = (wid & 3) * 8 + (lane >> 3);
+  const bf16* a_src = g.x + (int64_t)min(m0 + ar, M - 1) * g.ld_x + ((lane & 7) ^ rl_swz(ar)) * 8;
+  const bf16* w_src[WB];
+#pragma unroll
+  for (int i = 0; i < WB; ++i) {
+    const int r = (wid * WB + i) * 8 + (lane >> 3);
+    w_src[i] = g.w + (int64_t)r * g.ld_w + ((lane & 7) ^ rl_swz(r)) * 8;
+  }
+  auto a_stage = [&](int s) { return smem + s * A_STAGE; };
+  auto w_stage = [&](int s) { return smem + S * A_STAGE + s * W_STAGE; };
+  const int nk = K / RL_BK;
+  auto issue = [&](int kt) {
+    const int s = kt % S, k0 = kt * RL_BK;
+    __builtin_amdgcn_global_load_lds(static_cast<const void*>(a_src + k0),
+                                     static_cast<void*>(a_stage(s) + (wid & 3) * 1024), 16, 0, 0);
+#pragma unroll
+    for (int i = 0; i < WB; ++i)
+      __builtin_amdgcn_global_load_lds(static_cast<const void*>(w_src[i] + k0),
+                                       static_cast<void*>(w_stage(s) + (wid * WB + i) * 1024), 16, 0, 0);
+  };
+
+  f32x4 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) acc[i][j] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+  int a_off[TM], a_sw[TM], w_off[TN], w_sw[TN];
+#pragma unroll
+  for (int t = 0; t < TM; ++t) {
+    const int r = t * 16 + fr;
+    a_off[t] = r * 128;
+    a_sw[t] = rl_swz(r);
+  }
+#pragma unroll
+  for (int t = 0; t < TN; ++t) {
+    const int r = wcol + t * 16 + fr;
+    w_off[t] = r * 128;
+    w_sw[t] = rl_swz(r);
+  }
+  auto read_frags = [&](int stage, int ks, bf16x8 (&af)[TM], bf16x8 (&wf)[TN]) {
+    const unsigned char* as = a_stage(stage);
+    const unsigned char* ws = w_stage(stage);
+#pragma unroll
+    for (int t = 0; t < TM; ++t)
+      af[t] = *reinterpret_cast<const bf16x8*>(as + a_off[t] + (((ks * 4 + g4) ^ a_sw[t]) << 4));
+#pragma unroll
+    for (int t = 0; t < TN; ++t)
+      wf[t] = *reinterpret_cast<const bf16x8*>(ws + w_off[t] + (((ks * 4 + g4) ^ w_sw[t]) << 4));
+  };
+  auto mma = [&](const bf16x8 (&af)[TM], const bf16x8 (&wf)[TN]) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf[j], af[i], acc[i][j], 0, 0, 0);
+  };
+
+  // residual tile into registers first: its latency hides behind the main loop
+  const int res_rows = g.res_rows > 0 ? (int)g.res_rows : M;
+  float4 rv[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+    const int m = min(m0 + i * 16 + fr, M - 1);
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+      rv[i][j] = *reinterpret_cast<const float4*>(g.res + (int64_t)(m % res_rows) * g.ld_res + wcol + 16 * j + 4 * g4);
+  }
+
+#pragma unroll
+  for (int p = 0; p < S; ++p)
+    if (p < nk) issue(p);
+  auto wait_step = [&](int j, int last) {  // this wave's transfers of step j landed
+    const int ahead = min(nk - 1, last) - j;
+    if constexpr (S >= 3) {
+      if (ahead >= 2)
+        rl_wait_vm<2 * PER>();
+      else if (ahead == 1)
+        rl_wait_vm<PER>();
+      else
+        rl_wait_vm<0>();
+    } else {
+      if (ahead >= 1)
+        rl_wait_vm<PER>();
+      else
+        rl_wait_vm<0>();
+    }
+  };
+  bf16x8 af0[TM], wf0[TN], af1[TM], wf1[TN];
+  wait_step(0, S - 1);
+  __builtin_amdgcn_s_barrier();
+  read_frags(0, 0, af0, wf0);
+  for (int kt = 0; kt < nk; ++kt) {
+    const int st = kt % S;
+    read_frags(st, 1, af1, wf1);
+    mma(af0, wf0);
+    if (kt + 1 < nk) {
+      __builtin_amdgcn_s_waitcnt(0xC07F);  // this wave's reads of stage st are in registers
+      wait_step(kt + 1, kt + S - 1);
+      __builtin_amdgcn_s_barrier();        // all waves done with stage st; step kt+1 visible
+      if (kt + S < nk) issue(kt + S);
+      read_frags((kt + 1) % S, 0, af0, wf0);
+    }
+    mma(af1, wf1);
+  }
+
+  // ---- epilogue.  Lane (fr, g4), tile (i, j): row m0 + 16 i + fr, columns
+  // wcol + 16 j + 4 g4 .. +3.
+  float v[TM][TN][4];
+#pragma unroll
+  for (int j = 0; j < TN; ++j) {
+    const int n = wcol + 16 * j + 4 * g4;
+    const float4 sc = g.w_scale ? *reinterpret_cast<const float4*>(g.w_scale + n) : make_float4(1.f, 1.f, 1.f, 1.f);
+    const float4 bi = g.bias ? *reinterpret_cast<const float4*>(g.bias + n) : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      v[i][j][0] = acc[i][j][0] * sc.x + bi.x + rv[i][j].x;
+      v[i][j][1] = acc[i][j][1] * sc.y + bi.y + rv[i][j].y;
+      v[i][j][2] = acc[i][j][2] * sc.z + bi.z + rv[i][j].z;
+      v[i][j][3] = acc[i][j][3] * sc.w + bi.w + rv[i][j].w;
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+    const int m = m0 + i * 16 + fr;
+    if (m < M) {
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+        *reinterpret_cast<float4*>(g.out + (int64_t)m * g.ld_out + wcol + 16 * j + 4 * g4) =
+            make_float4(v[i][j][0], v[i][j][1], v[i][j][2], v[i][j][3]);
+    }
+  }
+
+  // row statistics: this wave's part of each row, then the 8 wavefronts through LDS
+  float* red = reinterpret_cast<float*>(smem);  // [RL_WAVES][RL_BM]
+  const float inv_n = 1.0f / (float)BN;
+  float mean[TM], rstd[TM];
+  __syncthreads();  // every ring read is done: the LDS may be reused
+#pragma unroll
+  for (int pass = 0; pass < 2; ++pass) {
+    float part[TM];
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      float s = 0.0f;
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float d = pass == 0 ? v[i][j][r] : v[i][j][r] - mean[i];
+          s += pass == 0 ? d : d * d;
+        }
+      s += __shfl_xor(s, 16, 64);
+      s += __shfl_xor(s, 32, 64);
+      part[i] = s;
+    }
+    if (g4 == 0) {
+#pragma unroll
+      for (int i = 0; i < TM; ++i) red[(pass * RL_WAVES + wid) * RL_BM + i * 16 + fr] = part[i];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      float t = 0.0f;
+#pragma unroll
+      for (int w = 0; w < RL_WAVES; ++w) t += red[(pass * RL_WAVES + w) * RL_BM + i * 16 + fr];
+      if (pass == 0)
+        mean[i] = t * inv_n;
+      else
+        rstd[i] = 1.0f / sqrtf(t * inv_n + g.eps);
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < TN; ++j) {
+    const int n = wcol + 16 * j + 4 * g4;
+    const float4 gm = *reinterpret_cast<const float4*>(g.gamma + n);
+    const float4 be = *reinterpret_cast<const float4*>(g.beta + n);
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      const int m = m0 + i * 16 + fr;
+      if (m >= M) continue;
+      bf16x4 o;
+      o[0] = (bf16)((v[i][j][0] - mean[i]) * rstd[i] * gm.x + be.x);
+      o[1] = (bf16)((v[i][j][1] - mean[i]) * rstd[i] * gm.y + be.y);
+      o[2] = (bf16)((v[i][j][2] - mean[i]) * rstd[i] * gm.z + be.z);
+      o[3] = (bf16)((v[i][j][3] - mean[i]) * rstd[i] * gm.w + be.w);
+      *reinterpret_cast<bf16x4*>(g.xn + (int64_t)m * g.ld_xn + n) = o;
+    }
+  }
+}
+
+bool a16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+}  // namespace
+
+}  // namespace cortex
+
+using namespace cortex;
+
+extern "C" int cortex_linear_residual_ln(int64_t M, int64_t N, int64_t K, const void* x, int64_t ld_x, const void* w,
+                                         int64_t ld_w, const float* w_scale, const float* bias, const float* res,
+                                         int64_t ld_res, int64_t res_rows, float* out, int64_t ld_out,
+                                         const float* gamma, const float* beta, float eps, void* xn, int64_t ld_xn,
+                                         hipStream_t stream) {
+  CORTEX_CHECK_ARG(M >= 0 && K > 0, "cortex_linear_residual_ln: need M >= 0 and K > 0");
+  CORTEX_CHECK_ARG(N == 256 || N == 512, "cortex_linear_residual_ln: N must be 256 or 512 (got %lld)", (long long)N);
+  CORTEX_CHECK_ARG(K % RL_BK == 0 && K <= 0x7fffffffLL, "cortex_linear_residual_ln: K must be a multiple of 64");
+  if (M == 0) return OK;
+  CORTEX_CHECK_ARG(M <= 0x7fffffffLL - RL_BM, "cortex_linear_residual_ln: M too large");
+  CORTEX_CHECK_ARG(x && w && res && out && gamma && beta && xn, "cortex_linear_residual_ln: null pointer");
+  CORTEX_CHECK_ARG(res_rows >= 0, "cortex_linear_residual_ln: res_rows must be >= 0");
+  CORTEX_CHECK_ARG(ld_x >= K && ld_w >= K && ld_res >= N && ld_out >= N && ld_xn >= N,
+                   "cortex_linear_residual_ln: row strides too small");
+  CORTEX_CHECK_ARG(a16(x) && a16(w) && a16(res) && a16(out) && a16(xn) && a16(gamma) && a16(beta) &&
+                       (!w_scale || a16(w_scale)) && (!bias || a16(bias)) && ld_x % 8 == 0 && ld_w % 8 == 0 &&
+                       ld_res % 4 == 0 && ld_out % 4 == 0 && ld_xn % 8 == 0,
+                   "cortex_linear_residual_ln: operands must be 16-byte aligned rows");
+  RowLnArgs a{M, N, K, reinterpret_cast<const bf16*>(x), ld_x, reinterpret_cast<const bf16*>(w), ld_w, w_scale,
+              bias, res, ld_res, res_rows, out, ld_out, gamma, beta, eps, reinterpret_cast<bf16*>(xn), ld_xn};
+  const dim3 grid((unsigned)cdiv(M, (int64_t)RL_BM));
+  if (N == 512)
+    hipLaunchKernelGGL((gemm_rowln_kernel<512, 2>), grid, dim3(RL_THREADS), 0, stream, a);
+  else
+    hipLaunchKernelGGL((gemm_rowln_kernel<256, 3>), grid, dim3(RL_THREADS), 0, stream, a);
+  CORTEX_CHECK_LAUNCH("gemm_rowln_kernel");
+  return OK;
+}

@@ -189,6 +189,19 @@ int cortex_temporal_block_mask(const int64_t* event_times, int64_t t_stride, int
                                int64_t block_l, int64_t block_e, int64_t n_q, int64_t n_k, uint8_t* out,
                                int64_t out_sb, hipStream_t stream);
 
+/* Residual linear followed by a LayerNorm (SelfAttentionBlock, cortex/models/perceiver.py:
+ * 121-124: x = x + out_proj(attn); norm_mlp(x); and the cross-attention residual followed
+ * by the first block's norm_attn):
+ *   out[m, n] = res[(m % res_rows) * ld_res + n] + (sum_k x[m, k] w[n, k]) * w_scale[n] + bias[n]
+ *   xn[m, :]  = LN(out[m, :]; gamma, beta, eps)   (bf16)
+ * x (M, K) and w (N, K) bf16 (the weight's bf16 image; w_scale/bias optional, fp32);
+ * res/out fp32 (out may alias res: in-place residual update); res_rows 0 means M.
+ * N in {256, 512}, K % 64 == 0, 16-byte aligned rows. */
+int cortex_linear_residual_ln(int64_t M, int64_t N, int64_t K, const void* x, int64_t ld_x, const void* w,
+                              int64_t ld_w, const float* w_scale, const float* bias, const float* res,
+                              int64_t ld_res, int64_t res_rows, float* out, int64_t ld_out, const float* gamma,
+                              const float* beta, float eps, void* xn, int64_t ld_xn, hipStream_t stream);
+
 /* Behaviour head (BehaviorDecoder.forward, cortex/models/cortex.py:29-53) with its
  * batch-invariant factors folded: cortex_head_prep builds, once per parameter state,
  * the (32, D) bf16 matrix ac of rows a_{q,h} = W_k[h]^T q_h * log2(e)/sqrt(Dh) (rows

@@ -203,3 +203,32 @@ def test_narrow_output_rows(N, form):
         ref = x.bfloat16().double() @ w.bfloat16().double().T
     assert y.shape == (M, N)
     assert float((y.cpu().double() - ref).abs().max()) <= 1e-5 * float(ref.abs().max())
+
+
+@pytest.mark.parametrize("M,N,K,res_rows", [(8192, 512, 512, 0), (300, 512, 512, 0), (8192, 512, 512, 256),
+                                            (77, 256, 256, 0), (1024, 256, 2048, 0), (40, 512, 128, 8)])
+@pytest.mark.parametrize("inplace", [False, True])
+def test_linear_residual_ln(M, N, K, res_rows, inplace):
+    """Residual linear + LayerNorm in one kernel (out_proj + norm_mlp): the fp32 residual
+    output within 1e-5 of a float64 contraction of the same operands; the bf16 LayerNorm
+    of it within one bf16 rounding of the fp32 LayerNorm of the kernel's own output."""
+    from cortex.kernels import ops
+
+    a, q, s = _operands(M, N, K, seed=M + N + K)
+    g = torch.Generator().manual_seed(5)
+    bias = 0.1 * torch.randn(N, generator=g)
+    res = torch.randn(res_rows or M, N, generator=g) * 2.0 + 0.3
+    gam, bet = 1 + 0.2 * torch.randn(N, generator=g), 0.2 * torch.randn(N, generator=g)
+    w_img = ops.convert(q.to(DEV), torch.bfloat16)
+    res_d = res.to(DEV)
+    out = res_d if (inplace and not res_rows) else None
+    x, xn = ops.linear_residual_ln(a.to(DEV), w_img, s.to(DEV), bias.to(DEV), residual=res_d,
+                                   ln=(gam.to(DEV), bet.to(DEV), 1e-5), res_rows=res_rows, out=out)
+    if out is not None:
+        assert x.data_ptr() == res_d.data_ptr()
+    ref = _ref(a, q, s, bias=bias, res=res, res_rows=res_rows)
+    xc = x.cpu()
+    assert (xc.double() - ref).abs().max() <= 1e-5 * ref.abs().max()
+    ln = F.layer_norm(xc, (N,), gam, bet, 1e-5)
+    err = (xn.cpu().float() - ln).abs()
+    assert (err <= _bf16_ulp(ln) + 1e-5 * float(ln.abs().max())).all(), float(err.max())
