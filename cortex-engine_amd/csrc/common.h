@@ -85,18 +85,22 @@ __device__ __forceinline__ float gelu_erf(float x) { return 0.5f * x * (1.0f + e
 // eq. 7.1.26: erf(z) = 1 - (a1 t + a2 t^2 + a3 t^3 + a4 t^4 + a5 t^5) exp(-z^2),
 // t = 1 / (1 + p z), z >= 0, |error| <= 1.5e-7.  Used where the result is rounded
 // to bf16 (relative step 2^-8), so the approximation is far below the output
-// resolution; about a dozen VALU operations instead of the library's erff.
+// resolution.  With q = poly(t) exp(-z^2), z = |x| / sqrt 2, both signs reduce to
+//   GELU(x) = max(x, 0) - |x| q / 2
+// (x >= 0: x (1 - q/2); x < 0: x q / 2), about a dozen VALU operations.
 __device__ __forceinline__ float gelu_erf_bf16out(float x) {
-  const float z = fabsf(x) * 0.70710678118654752440f;
-  const float t = __builtin_amdgcn_rcpf(1.0f + 0.3275911f * z);
-  float poly = 1.061405429f;
-  poly = poly * t - 1.453152027f;
-  poly = poly * t + 1.421413741f;
-  poly = poly * t - 0.284496736f;
-  poly = poly * t + 0.254829592f;
+  const float a = fminf(fabsf(x), 3.0e38f);  // finite, so |x| q stays finite for x = +-inf
+  const float t = __builtin_amdgcn_rcpf(fmaf(a, 0.3275911f * 0.70710678118654752440f, 1.0f));
+  // 0.5 * (a1 .. a5)
+  float poly = 0.5f * 1.061405429f;
+  poly = fmaf(poly, t, 0.5f * -1.453152027f);
+  poly = fmaf(poly, t, 0.5f * 1.421413741f);
+  poly = fmaf(poly, t, 0.5f * -0.284496736f);
+  poly = fmaf(poly, t, 0.5f * 0.254829592f);
   poly *= t;
-  const float e = 1.0f - poly * __expf(-z * z);
-  return 0.5f * x * (1.0f + copysignf(e, x));
+  // exp(-x^2 / 2) = 2^(x^2 * (-log2(e) / 2))
+  const float e = __builtin_amdgcn_exp2f(x * (x * -0.72134752044448170368f));
+  return fmaf(-(a * poly), e, fmaxf(x, 0.0f));
 }
 
 }  // namespace cortex
