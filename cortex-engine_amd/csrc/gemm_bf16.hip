@@ -249,27 +249,28 @@ __global__ __launch_bounds__(TL::THREADS) void gemm_bf16_kernel(GemmArgs g) {
   TOUT* out = reinterpret_cast<TOUT*>(g.out);
   constexpr int NV = IL ? 8 : 4;           // consecutive columns per lane and group
   constexpr int NG = IL ? TN / 2 : TN;     // column groups per lane
+  // Every scale and bias load first, then one wait: a wait left to the compiler would
+  // sit at each row's branch and also drain the previous row's stores.
+  float sca[NG][NV], bia[NG][NV];
+#pragma unroll
+  for (int p = 0; p < NG; ++p) {
+    const int n = min(n0 + wcol + (IL ? 32 * p + 8 * g4 : 16 * p + 4 * g4), N - NV);
+#pragma unroll
+    for (int h = 0; h < NV / 4; ++h) {
+      const float4 s4 = g.w_scale ? *reinterpret_cast<const float4*>(g.w_scale + n + 4 * h)
+                                  : make_float4(1.f, 1.f, 1.f, 1.f);
+      const float4 b4 = bias ? *reinterpret_cast<const float4*>(bias + n + 4 * h) : make_float4(0.f, 0.f, 0.f, 0.f);
+      sca[p][4 * h] = s4.x; sca[p][4 * h + 1] = s4.y; sca[p][4 * h + 2] = s4.z; sca[p][4 * h + 3] = s4.w;
+      bia[p][4 * h] = b4.x; bia[p][4 * h + 1] = b4.y; bia[p][4 * h + 2] = b4.z; bia[p][4 * h + 3] = b4.w;
+    }
+  }
+  wait_vm<0>();
 #pragma unroll
   for (int p = 0; p < NG; ++p) {
     const int n = n0 + wcol + (IL ? 32 * p + 8 * g4 : 16 * p + 4 * g4);
     if (n >= N) continue;  // N % 8 == 0: a lane's columns are all in or all out
-    float sc[NV], bi[NV];
-#pragma unroll
-    for (int e = 0; e < NV; ++e) {
-      sc[e] = 1.0f;
-      bi[e] = 0.0f;
-    }
-#pragma unroll
-    for (int h = 0; h < NV / 4; ++h) {
-      if (g.w_scale) {
-        const float4 s4 = *reinterpret_cast<const float4*>(g.w_scale + n + 4 * h);
-        sc[4 * h] = s4.x; sc[4 * h + 1] = s4.y; sc[4 * h + 2] = s4.z; sc[4 * h + 3] = s4.w;
-      }
-      if (bias) {
-        const float4 b4 = *reinterpret_cast<const float4*>(bias + n + 4 * h);
-        bi[4 * h] = b4.x; bi[4 * h + 1] = b4.y; bi[4 * h + 2] = b4.z; bi[4 * h + 3] = b4.w;
-      }
-    }
+    const float* sc = sca[p];
+    const float* bi = bia[p];
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
       const int m = m0 + wrow + i * 16 + fr;
