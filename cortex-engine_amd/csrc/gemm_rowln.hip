@@ -179,13 +179,34 @@ __global__ __launch_bounds__(RL_THREADS) void gemm_rowln_kernel(RowLnArgs g) {
   }
 
   // ---- epilogue.  Lane (fr, g4), tile (i, j): row m0 + 16 i + fr, columns
-  // wcol + 16 j + 4 g4 .. +3.
-  float v[TM][TN][4];
+  // wcol + 16 j + 4 g4 .. +3.  Every per-column parameter is loaded before the first
+  // store, so no wait for them drains stores.
+  float4 scv[TN], biv[TN], gmv[TN], bev[TN];
+  // absent scale / bias: load any valid row (gamma) and select the neutral value, so
+  // the loads stay unconditional (no branch, no extra wait at its merge)
+  const float* sp = g.w_scale ? g.w_scale : g.gamma;
+  const float* bp = g.bias ? g.bias : g.gamma;
 #pragma unroll
   for (int j = 0; j < TN; ++j) {
     const int n = wcol + 16 * j + 4 * g4;
-    const float4 sc = g.w_scale ? *reinterpret_cast<const float4*>(g.w_scale + n) : make_float4(1.f, 1.f, 1.f, 1.f);
-    const float4 bi = g.bias ? *reinterpret_cast<const float4*>(g.bias + n) : make_float4(0.f, 0.f, 0.f, 0.f);
+    scv[j] = *reinterpret_cast<const float4*>(sp + n);
+    biv[j] = *reinterpret_cast<const float4*>(bp + n);
+    gmv[j] = *reinterpret_cast<const float4*>(g.gamma + n);
+    bev[j] = *reinterpret_cast<const float4*>(g.beta + n);
+  }
+  rl_wait_vm<0>();
+  if (!g.w_scale) {
+#pragma unroll
+    for (int j = 0; j < TN; ++j) scv[j] = make_float4(1.f, 1.f, 1.f, 1.f);
+  }
+  if (!g.bias) {
+#pragma unroll
+    for (int j = 0; j < TN; ++j) biv[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+  float v[TM][TN][4];
+#pragma unroll
+  for (int j = 0; j < TN; ++j) {
+    const float4 sc = scv[j], bi = biv[j];
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
       v[i][j][0] = acc[i][j][0] * sc.x + bi.x + rv[i][j].x;
@@ -246,8 +267,7 @@ __global__ __launch_bounds__(RL_THREADS) void gemm_rowln_kernel(RowLnArgs g) {
 #pragma unroll
   for (int j = 0; j < TN; ++j) {
     const int n = wcol + 16 * j + 4 * g4;
-    const float4 gm = *reinterpret_cast<const float4*>(g.gamma + n);
-    const float4 be = *reinterpret_cast<const float4*>(g.beta + n);
+    const float4 gm = gmv[j], be = bev[j];
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
       const int m = m0 + i * 16 + fr;
