@@ -73,6 +73,8 @@ _SIGNATURES = {
         [_int, _i64, _i64, _i64, _i64, _i64, _ptr, _i64, _i64, _i64, _ptr, _i64, _i64, _i64, _ptr, _i64, _i64,
          _i64, _ptr, _ptr, _ptr, _i64, _ptr, _i64, _i64, _i64, _i64, _i64, _f32, _ptr, _i64, _i64, _i64, _ptr],
     ),
+    "cortex_qkv_attention": (
+        _int, [_i64, _i64, _i64, _i64, _ptr, _i64, _ptr, _i64, _ptr, _ptr, _f32, _ptr, _i64, _ptr]),
     "cortex_linear_residual_ln": (
         _int,
         [_i64, _i64, _i64, _ptr, _i64, _ptr, _i64, _ptr, _ptr, _ptr, _i64, _i64, _ptr, _i64, _ptr, _ptr, _f32, _ptr,

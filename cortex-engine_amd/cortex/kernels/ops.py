@@ -192,6 +192,21 @@ def ln_rows(x: torch.Tensor, ln1, ln2=None, out_bf16: bool = True, out_f32: bool
     return ob if out_bf16 else of
 
 
+def qkv_attention(xn: torch.Tensor, weight: torch.Tensor, weight_scale, bias, batch: int, length: int,
+                  heads: int, scale: float | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
+    """Self-attention with its QKV projection fused (``cortex_qkv_attention``): ``xn`` (B*L, D)
+    bf16 rows, ``weight`` the (3D, D) bf16 image; returns the merged-head (B*L, D) bf16 output."""
+    dev = nat.require_gpu(xn, weight, weight_scale, bias, out, what="qkv_attention")
+    M, D = xn.shape
+    if out is None:
+        out = torch.empty((M, D), dtype=torch.bfloat16, device=dev)
+    s = float(scale) if scale is not None else (D // heads) ** -0.5
+    nat.call("cortex_qkv_attention", batch, length, D, heads, nat.ptr(xn), xn.stride(0), nat.ptr(weight),
+             weight.stride(0), nat.ptr(weight_scale), nat.ptr(bias), s, nat.ptr(out), out.stride(0),
+             nat.stream_of(dev))
+    return out
+
+
 def linear_residual_ln(x: torch.Tensor, weight: torch.Tensor, weight_scale=None, bias=None, *,
                        residual: torch.Tensor, ln, res_rows: int = 0, out: torch.Tensor | None = None):
     """``out = residual + x @ (weight * scale)^T + bias`` (fp32) and ``LN(out)`` (bf16) in one

@@ -15,7 +15,8 @@ import torch
 from torch import nn
 
 from cortex.kernels import ops
-from cortex.models._layers import apply_linear, batch_invariant, exec_weights, linear_residual_ln, residual_ln_ok
+from cortex.models._layers import (INT8_WEIGHTS, apply_linear, batch_invariant, exec_weights, linear_residual_ln,
+                                   ln_rows_ok, normalize_bf16, residual_ln_ok)
 from cortex.models.config import CortexConfig
 
 
@@ -91,13 +92,21 @@ class SelfAttentionBlock(nn.Module):
         compute = self.config.compute_dtype
         D = x.shape[1]
         H = self.num_heads
-        if xn is not None:
-            qkv = ops.norm_linear(xn, **exec_weights(self.qkv_proj, compute), out_dtype=compute, compute_dtype=compute)
+        if self._fused_attention_ok(x, length):
+            # qkv projection + attention per (head, sample) on chip: qkv never reaches HBM
+            if xn is None:
+                xn = normalize_bf16(x, self.norm_attn)
+            w = exec_weights(self.qkv_proj, compute)
+            o_buf = ops.qkv_attention(xn, w["weight"], w["weight_scale"], w["bias"], batch, length, H)
         else:
-            qkv = apply_linear(self.qkv_proj, x, norm=self.norm_attn, out_dtype=compute, compute=compute)
-        o_buf, o = ops.merge_heads_out(batch, length, H, D // H, compute, x.device)
-        ops.attention(ops.heads_view(qkv, batch, length, H, 0, D), ops.heads_view(qkv, batch, length, H, D, D),
-                      ops.heads_view(qkv, batch, length, H, 2 * D, D), out=o)
+            if xn is not None:
+                qkv = ops.norm_linear(xn, **exec_weights(self.qkv_proj, compute), out_dtype=compute,
+                                      compute_dtype=compute)
+            else:
+                qkv = apply_linear(self.qkv_proj, x, norm=self.norm_attn, out_dtype=compute, compute=compute)
+            o_buf, o = ops.merge_heads_out(batch, length, H, D // H, compute, x.device)
+            ops.attention(ops.heads_view(qkv, batch, length, H, 0, D), ops.heads_view(qkv, batch, length, H, D, D),
+                          ops.heads_view(qkv, batch, length, H, 2 * D, D), out=o)
         # each residual element is read and then written by the same lane: in place is safe
         if residual_ln_ok(self.out_proj, self.norm_mlp, self.mlp[0], x, compute):
             x, hn = linear_residual_ln(self.out_proj, o_buf, x, self.norm_mlp, out=x if inplace else None)
@@ -109,6 +118,17 @@ class SelfAttentionBlock(nn.Module):
             h = apply_linear(self.mlp[0], x, norm=self.norm_mlp, act="gelu", out_dtype=compute, compute=compute)
         return apply_linear(self.mlp[2], h, residual=x, out_dtype=x.dtype, compute=compute,
                             out=x if inplace else None)
+
+    def _fused_attention_ok(self, x: torch.Tensor, length: int) -> bool:
+        """Whether ``cortex_qkv_attention`` covers this block: bf16 compute, no calibration
+        hooks on qkv_proj or norm_attn, head dim 64, at most 256 latents, an fp32 bias (or none)."""
+        lin = self.qkv_proj
+        D = x.shape[1]
+        return (self.config.compute_dtype == torch.bfloat16 and not lin._forward_pre_hooks
+                and not self.norm_attn._forward_pre_hooks and D == 64 * self.num_heads and D % 64 == 0
+                and 1 <= length <= 256 and INT8_WEIGHTS == "image"
+                and (lin.bias is None or (lin.bias.dtype == torch.float32 and lin.bias.data_ptr() % 16 == 0))
+                and ln_rows_ok(x, self.norm_attn))
 
     def forward(self, latents: torch.Tensor) -> torch.Tensor:
         """(B, L, D) -> (B, L, D)."""

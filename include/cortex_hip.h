@@ -189,6 +189,17 @@ int cortex_temporal_block_mask(const int64_t* event_times, int64_t t_stride, int
                                int64_t block_l, int64_t block_e, int64_t n_q, int64_t n_k, uint8_t* out,
                                int64_t out_sb, hipStream_t stream);
 
+/* Self-attention with its QKV projection (SelfAttentionBlock, cortex/models/perceiver.py:
+ * 113-121: qkv_proj on the norm_attn rows, split into heads, SDPA), one workgroup per
+ * (head, sample), the projected q/k/v kept on chip:
+ *   [q|k|v]_h[l] = xn[b*L + l] . W[{0,D,2D} + 64h + d]^T * w_scale (+ bias)
+ *   out[b*L + l, 64h + d] = softmax_j(scale q_h[l] . k_h[j]) v_h[j]      (bf16)
+ * xn (B*L, D) bf16 rows; w the (3D, D) bf16 weight image with optional per-row scale
+ * and bias (3D, fp32).  Head dim 64 (D = 64 H), L <= 256, 16-byte aligned rows. */
+int cortex_qkv_attention(int64_t B, int64_t L, int64_t D, int64_t H, const void* xn, int64_t ld_x, const void* w,
+                         int64_t ld_w, const float* w_scale, const float* bias, float scale, void* out, int64_t ld_o,
+                         hipStream_t stream);
+
 /* Residual linear followed by a LayerNorm (SelfAttentionBlock, cortex/models/perceiver.py:
  * 121-124: x = x + out_proj(attn); norm_mlp(x); and the cross-attention residual followed
  * by the first block's norm_attn):

@@ -102,3 +102,30 @@ def test_fast_and_general_kernels_agree():
     general = sparse_cross_attention(q, k, v, mask, BLOCK_L=64, BLOCK_E=64, key_padding_mask=kpm).float()
     err = float((fast - general).abs().max())
     assert err <= 1e-2 * float(general.abs().max())
+
+
+@pytest.mark.parametrize("B,L,D", [(3, 256, 512), (2, 200, 512), (4, 64, 256), (2, 1, 512), (33, 256, 512)])
+@pytest.mark.parametrize("with_bias", [False, True])
+def test_fused_qkv_attention(B, L, D, with_bias):
+    """QKV projection + self-attention in one kernel: against a float64 projection of the
+    same bf16/int8 operands (rounded to bf16, as the projection's output is) followed by the
+    float64 attention oracle; 1e-2 of the largest output."""
+    from cortex.kernels import ops
+
+    Hh = D // 64
+    g = torch.Generator().manual_seed(B * 7 + L + D)
+    xn = torch.randn(B * L, D, generator=g).bfloat16()
+    w = torch.randn(3 * D, D, generator=g) * 0.04
+    q8, s = O.quantize_int8(w.numpy())
+    q8, s = torch.from_numpy(q8), torch.from_numpy(s)
+    bias = 0.05 * torch.randn(3 * D, generator=g) if with_bias else None
+    img = ops.convert(q8.to(DEV), torch.bfloat16)
+    out = ops.qkv_attention(xn.to(DEV), img, s.to(DEV), bias.to(DEV) if with_bias else None, B, L, Hh)
+    qkv = xn.double() @ q8.double().T * s.double()
+    if with_bias:
+        qkv = qkv + bias.double()
+    qkv = qkv.bfloat16().float().reshape(B, L, 3, Hh, 64)
+    q, k, v = (qkv[:, :, i].permute(0, 2, 1, 3) for i in range(3))
+    ref = O.attention_bruteforce_f64(q, k, v)  # (B, H, L, 64)
+    got = out.float().cpu().reshape(B, L, Hh, 64).permute(0, 2, 1, 3).numpy()
+    _close(got, ref)
