@@ -117,22 +117,25 @@ def make_kernel(name: str, dev):
     if name == "gemm_mlp0_gelu":
         fn, fl, by = gemm(2048, 512, act="gelu")
         return fn, 7, "mfma", fl, by, "MLP up 512->2048 + GELU, bf16 out, M=8192 (gemm_bf16_kernel)"
-    if name == "gemm_qkv":
-        fn, fl, by = gemm(1536, 512)
-        return fn, 7, "mfma", fl, by, "QKV 512->1536, bf16 out, M=8192 (gemm_bf16_kernel)"
-    if name == "gemm_out_residual":
-        fn, fl, by = gemm(512, 512, residual=True)
-        return fn, 8, "hbm", fl, by, ("attention out 512->512 + fp32 residual, M=8192 (gemm_bf16_kernel, "
-                                      "128x128 tiles, K split over two wave groups)")
-    if name == "attention_self":
-        qkv = rnd(M_ROWS, 3 * D, dtype=bf, scale=0.3)
-        o_buf, o = ops.merge_heads_out(B_MAIN, L, H, DH, bf, dev)
-        fn = lambda: ops.attention(ops.heads_view(qkv, B_MAIN, L, H, 0, D),  # noqa: E731
-                                   ops.heads_view(qkv, B_MAIN, L, H, D, D),
-                                   ops.heads_view(qkv, B_MAIN, L, H, 2 * D, D), out=o)
-        fl = 4.0 * B_MAIN * H * L * L * DH
-        by = 3 * M_ROWS * D * 2 + M_ROWS * D * 2
-        return fn, 7, "mfma", fl, by, "self-attention B=32 H=8 L=256 Dh=64 (attention_fast_kernel)"
+    if name == "qkv_attention":
+        xn = rnd(M_ROWS, D, dtype=bf)
+        w, sc = _int8_image(3 * D, D, dev, 2)
+        out = torch.empty(M_ROWS, D, dtype=bf, device=dev)
+        fn = lambda: ops.qkv_attention(xn, w, sc, None, B_MAIN, L, H, out=out)  # noqa: E731
+        fl = 2.0 * M_ROWS * 3 * D * D + 4.0 * B_MAIN * H * L * L * DH  # projection + attention
+        by = M_ROWS * D * 2 + 3 * D * D + 3 * D * 4 + M_ROWS * D * 2  # xn, int8 weight, scales, output
+        return fn, 7, "mfma", fl, by, ("QKV projection 512->1536 + self-attention B=32 H=8 L=256 Dh=64, "
+                                      "per (head, sample) (qkv_attention_kernel)")
+    if name == "out_residual_ln":
+        a = rnd(M_ROWS, D, dtype=bf)
+        w, sc = _int8_image(D, D, dev, 3)
+        res = rnd(M_ROWS, D)
+        g_, b_ = rnd(D), rnd(D)
+        fn = lambda: ops.linear_residual_ln(a, w, sc, None, residual=res, ln=(g_, b_, 1e-5), out=res)  # noqa: E731
+        fl = 2.0 * M_ROWS * D * D
+        by = M_ROWS * D * 2 + D * D + 4 * D + M_ROWS * D * 4 * 2 + M_ROWS * D * 2 + 2 * D * 4
+        return fn, 8, "hbm", fl, by, ("attention out 512->512 + fp32 residual + the next LayerNorm, M=8192 "
+                                      "(gemm_rowln_kernel, 32-row full-width tiles)")
     if name == "attention_cross":
         E = B_MAIN * PER_MAIN
         kv = rnd(E, 2 * D, dtype=bf)
@@ -153,7 +156,7 @@ def make_kernel(name: str, dev):
             ops.ln_rows(x, (w, b, 1e-5))
         by = M_ROWS * D * 4 + M_ROWS * D * 2 + 2 * D * 4
         del out
-        return fn, 14, "hbm", 0.0, by, "LayerNorm rows fp32 -> bf16, M=8192 K=512 (ln_rows_kernel)"
+        return fn, 6, "hbm", 0.0, by, "LayerNorm rows fp32 -> bf16, M=8192 K=512 (ln_rows_kernel)"
     if name == "tokenize":
         E = B_MAIN * PER_MAIN
         nid, tb, val, bidx = (torch.from_numpy(a).to(dev) for a in make_events(B_MAIN, PER_MAIN, seed=3))
@@ -170,8 +173,8 @@ def make_kernel(name: str, dev):
     raise ValueError(f"unknown kernel {name}")
 
 
-KERNELS = ("gemm_mlp2_residual", "gemm_mlp0_gelu", "gemm_qkv", "gemm_out_residual", "attention_self",
-           "attention_cross", "ln_rows", "tokenize")
+KERNELS = ("gemm_mlp2_residual", "gemm_mlp0_gelu", "qkv_attention", "out_residual_ln", "attention_cross", "ln_rows",
+           "tokenize")
 
 
 def time_launches(fn, iters: int = 20, reps: int = 5) -> float:
