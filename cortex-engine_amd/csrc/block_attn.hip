@@ -148,29 +148,31 @@ __global__ __launch_bounds__(BA_THREADS) void qkv_attention_kernel(QkvAttnArgs a
         acc[i][j] = j < 4 ? __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf[j], af[i], acc[i][j], 0, 0, 0)
                           : __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[i], wf[j], acc[i][j], 0, 0, 0);
   };
-  // Both stages in flight; a step waits for its own transfers, multiplies its two
-  // K halves with single-buffered fragments (registers go to the 96 accumulators),
-  // then all waves release the stage and it is refilled two steps ahead.
+  // Both stages in flight; a stage is refilled as soon as every wave holds its last
+  // fragments in registers.  Fragments are double-buffered in registers, so the LDS
+  // reads of the next K half overlap the MFMAs.
 #pragma unroll
   for (int p = 0; p < BA_S; ++p)
     if (p < nk) issue(p);
-  bf16x8 af[BA_TM], wf[BA_TN];
+  bf16x8 af0[BA_TM], wf0[BA_TN], af1[BA_TM], wf1[BA_TN];
+  if (nk > 1)
+    ba_wait_vm<BA_PER>();
+  else
+    ba_wait_vm<0>();
+  __builtin_amdgcn_s_barrier();
+  read_frags(0, 0, af0, wf0);
   for (int kt = 0; kt < nk; ++kt) {
     const int st = kt % BA_S;
-    if (kt + 1 < nk)
-      ba_wait_vm<BA_PER>();  // step kt landed; step kt+1 may still be in flight
-    else
-      ba_wait_vm<0>();
-    __builtin_amdgcn_s_barrier();  // step kt visible to every wave
-    read_frags(st, 0, af, wf);
-    mma(af, wf);
-    read_frags(st, 1, af, wf);
-    mma(af, wf);
-    if (kt + BA_S < nk) {
+    read_frags(st, 1, af1, wf1);
+    mma(af0, wf0);
+    if (kt + 1 < nk) {
       __builtin_amdgcn_s_waitcnt(0xC07F);  // this wave's reads of stage st are in registers
-      __builtin_amdgcn_s_barrier();        // ... and every other wave's
-      issue(kt + BA_S);
+      ba_wait_vm<0>();                     // step kt+1 landed (two stages: nothing newer in flight)
+      __builtin_amdgcn_s_barrier();        // all waves done with stage st; step kt+1 visible
+      if (kt + BA_S < nk) issue(kt + BA_S);
+      read_frags((kt + 1) % BA_S, 0, af0, wf0);
     }
+    mma(af1, wf1);
   }
 
   // ---- scale / bias per column, round to bf16, write Q, K rows and V^T into LDS
@@ -254,7 +256,11 @@ __global__ __launch_bounds__(BA_THREADS) void qkv_attention_kernel(QkvAttnArgs a
   for (int j = 0; j < 8; ++j) ones[j] = (bf16)1.0f;
   const float sl = a.scale_log2;
   const int nt = (L + 63) / 64;
-  for (int kt = 0; kt < nt; ++kt) {
+  // fully unrolled over the (at most 4) key tiles, so one tile's fragment reads and
+  // score MFMAs can be scheduled under the previous tile's softmax
+#pragma unroll
+  for (int kt = 0; kt < BA_L / 64; ++kt) {
+    if (kt >= nt) break;
     const unsigned char* ks_ = smem + BA_K + kt * 64 * 128;
     const unsigned char* vs_ = smem + BA_VT + kt * BA_VTILE;
     f32x4 s[QG][4];
