@@ -96,6 +96,26 @@ def test_config3_int8_bf16_forward_vs_oracle():
     assert np.abs(beh - ref).max() <= 2e-2, np.abs(beh - ref).max()
 
 
+def test_cortex_m_int8_bf16_forward_vs_oracle():
+    """CORTEX_M (D=768, 12 heads, 384 latents) runs the general kernels wherever the fused ones
+    do not apply (384 latents, 12 heads x 2 behaviour queries, N=768 rows): INT8, bf16 compute,
+    decoded velocity within 2e-2 max-abs of the float32 oracle."""
+    from cortex.models import CortexModel
+    from cortex.models.config import CORTEX_M
+
+    arrs = _config3_inputs(B=2, per=200, seed=4)
+    inputs = [torch.from_numpy(a).to(DEV) for a in arrs]
+    torch.manual_seed(0)
+    model = _int8(CortexModel(CORTEX_M).to(DEV).eval(), inputs)
+    with torch.no_grad():
+        beh = model(*inputs, batch_size=2)["behavior"].cpu().numpy()
+    sd = {k: v.detach().cpu() for k, v in model.state_dict().items()}
+    shape = O.ModelShape(768, 11, 12, 384, 768, 12)
+    ref = O.forward(sd, shape, *arrs).numpy()
+    assert beh.shape == (2, 2) and np.isfinite(beh).all()
+    assert np.abs(beh - ref).max() <= 2e-2, np.abs(beh - ref).max()
+
+
 def test_module_path_equals_fused_csr_path_fp32():
     """tokenizer -> _pack_events -> encoder -> behavior_head (padded modules) == fused CSR forward."""
     from cortex.models.cortex import _pack_events
