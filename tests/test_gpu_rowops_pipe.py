@@ -140,6 +140,35 @@ def test_pipe_gemm_gelu_bf16_out(wform):
     assert bool((err <= _bf16_ulp(ref) + 1e-5 * float(ref.abs().max())).all())
 
 
+@pytest.mark.parametrize("wform", ["int8", "image"])
+def test_gelu_epilogue_dense_grid(wform):
+    """The bf16-output GELU epilogue on every bf16 value in [-12, 12] (and +-inf): a
+    K=64 GEMM whose rows hold x in column 0 and whose weight rows are e_0 (scale 1)
+    returns GELU(x) rounded to bf16.  Bar: within half a bf16 step of the float64
+    erf-GELU plus 1e-4 relative (approximation) and 1e-8 absolute (the far
+    negative tail, where |GELU| < 6e-9); GELU(+inf) = +inf."""
+    from cortex.kernels import ops
+
+    v = torch.arange(-32768, 32768, dtype=torch.int32).to(torch.int16).view(torch.bfloat16).float()
+    x = torch.unique(v[torch.isfinite(v) & (v.abs() <= 12)])
+    x = torch.cat([x, torch.tensor([float("inf")])])
+    M, N, K = x.numel(), 16, 64
+    a = torch.zeros(M, K)
+    a[:, 0] = x
+    q = torch.zeros(N, K, dtype=torch.int8)
+    q[:, 0] = 1
+    ad, qd, sd = a.to(torch.bfloat16).to(DEV), q.to(DEV), torch.ones(N, device=DEV)
+    w = {"weight_int8": qd} if wform == "int8" else {"weight": ops.convert(qd, torch.bfloat16)}
+    y = ops.norm_linear(ad, **w, weight_scale=sd, act="gelu", out_dtype=torch.bfloat16).cpu().double()
+    xd = x.double()
+    ref = 0.5 * xd * (1 + torch.erf(xd / 2 ** 0.5))
+    fin = torch.isfinite(xd)
+    assert bool((y[~fin] == float("inf")).all())
+    err = (y[fin] - ref[fin, None]).abs()
+    bound = 0.5 * _bf16_ulp(ref[fin, None]) + 1e-4 * ref[fin, None].abs() + 1e-8
+    assert bool((err <= bound).all()), float((err - bound).max())
+
+
 def test_pipe_gemm_bias_and_broadcast_residual():
     """Bias epilogue, and the latents residual broadcast every 256 rows into fp32 output."""
     from cortex.kernels import ops
