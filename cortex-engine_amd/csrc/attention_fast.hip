@@ -94,8 +94,7 @@ void attention_fast_kernel(AttnArgs a) {
 
   // Keep the query blocks of one (sample, head) on one XCD (shared K/V in its L2).
   const int nqb = gridDim.x, total = gridDim.x * gridDim.y;
-  int id = blockIdx.x + nqb * blockIdx.y;
-  if ((total & 7) == 0) id = (id & 7) * (total >> 3) + (id >> 3);
+  const int id = xcd_affine(blockIdx.x + nqb * blockIdx.y, total);
   const int64_t bh = id / nqb;
   const int qblk = id % nqb;
   const int64_t b = bh / a.H, h = bh - b * a.H;

@@ -69,8 +69,7 @@ __global__ __launch_bounds__(BA_THREADS) void qkv_attention_kernel(QkvAttnArgs a
   const int fr = lane & 15, g4 = lane >> 4;
   // the heads of one sample run on one XCD (shared activation panel in its L2)
   const int nh = gridDim.x, total = gridDim.x * gridDim.y;
-  int id = blockIdx.x + nh * blockIdx.y;
-  if ((total & 7) == 0) id = (id & 7) * (total >> 3) + (id >> 3);
+  const int id = xcd_affine(blockIdx.x + nh * blockIdx.y, total);
   const int h = id % nh;
   const int64_t b = id / nh;
   const int L = (int)a.L, D = (int)a.D;

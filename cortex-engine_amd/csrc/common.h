@@ -76,6 +76,15 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
+// Workgroups go to the 8 XCDs round-robin by linear id (id % 8).  A kernel whose
+// neighbouring work items share operands (the column tiles of one row panel, the
+// query blocks or heads of one sample) indexes them by xcd_affine(id, total): XCD x
+// then takes the x-th contiguous eighth, and the shared operands are fetched into
+// one XCD's L2 instead of eight.  (A bijection on [0, total); identity unless 8 | total.)
+__device__ __forceinline__ int xcd_affine(int id, int total) {
+  return (total & 7) ? id : (id & 7) * (total >> 3) + (id >> 3);
+}
+
 __host__ __device__ __forceinline__ int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 // erf-form GELU, as torch.nn.GELU() with approximate='none': 0.5 x (1 + erf(x / sqrt 2)).

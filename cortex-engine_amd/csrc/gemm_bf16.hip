@@ -81,8 +81,7 @@ __global__ __launch_bounds__(TL::THREADS) void gemm_bf16_kernel(GemmArgs g) {
   const int kg = (tid >> 6) / TL::WAVES, wid = (tid >> 6) % TL::WAVES;  // K group, wave within it
   const int wm = wid / TL::WN, wn = wid % TL::WN;
   const int nbx = gridDim.x, total = gridDim.x * gridDim.y;
-  int id = blockIdx.x + nbx * blockIdx.y;
-  if ((total & 7) == 0) id = (id & 7) * (total >> 3) + (id >> 3);  // contiguous tiles per XCD
+  const int id = xcd_affine(blockIdx.x + nbx * blockIdx.y, total);  // contiguous row tiles per XCD
   const int m0 = (id / nbx) * BM, n0 = (id % nbx) * BN;
   unsigned char* const ring = smem + kg * TL::RING;
   const int M = (int)g.M, N = (int)g.N, K = (int)g.K;

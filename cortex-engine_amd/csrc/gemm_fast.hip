@@ -114,8 +114,7 @@ __global__ __launch_bounds__(TL::THREADS, 2) void gemm_fast_kernel(GemmArgs g) {
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int wm = wid / TL::WN, wn = wid % TL::WN;
   const int nbx = gridDim.x, total = gridDim.x * gridDim.y;
-  int id = blockIdx.x + nbx * blockIdx.y;
-  if ((total & 7) == 0) id = (id & 7) * (total >> 3) + (id >> 3);
+  const int id = xcd_affine(blockIdx.x + nbx * blockIdx.y, total);
   const int m0 = (id / nbx) * BM, n0 = (id % nbx) * BN;
   const int M = (int)g.M, N = (int)g.N, K = (int)g.K;
   const TX* __restrict__ X = reinterpret_cast<const TX*>(g.x);
