@@ -30,10 +30,12 @@ def _row_major_2d(x: torch.Tensor) -> torch.Tensor:
 # --------------------------------------------------------------------------- pack
 
 
-def pack_plan(batch_indices: torch.Tensor, batch_size: int, err: torch.Tensor | None = None):
+def pack_plan(batch_indices: torch.Tensor, batch_size: int, err: torch.Tensor | None = None, *,
+              with_rank: bool = True):
     """Stable CSR plan of ragged events: ``(offsets (B+1), order (E), rank (E))``.
 
-    offsets/order/rank are int64 device tensors; see ``cortex_pack_plan``.
+    offsets/order/rank are int64 device tensors; see ``cortex_pack_plan``.  With
+    ``with_rank=False`` the rank is not written and ``None`` is returned in its place.
     """
     dev = nat.require_gpu(batch_indices, what="pack_plan")
     if batch_indices.dtype != torch.int64 or batch_indices.dim() != 1:
@@ -42,7 +44,7 @@ def pack_plan(batch_indices: torch.Tensor, batch_size: int, err: torch.Tensor | 
     B = int(batch_size)
     offsets = torch.empty(B + 1, dtype=torch.int64, device=dev)
     order = torch.empty(E, dtype=torch.int64, device=dev)
-    rank = torch.empty(E, dtype=torch.int64, device=dev)
+    rank = torch.empty(E, dtype=torch.int64, device=dev) if with_rank else None
     ws_bytes = nat.load().cortex_pack_workspace_bytes(E, B)
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
     nat.call("cortex_pack_plan", nat.ptr(batch_indices), batch_indices.stride(0) if E else 1, E, B,

@@ -33,7 +33,7 @@ def pack_events(flat_tokens: torch.Tensor, batch_indices: torch.Tensor, *, batch
         raise ValueError("flat_tokens and batch_indices disagree on the number of events")
     if batch_size is None:
         batch_size = int(batch_indices.max().item()) + 1 if E > 0 else 1
-    offsets, order, _ = ops.pack_plan(batch_indices, batch_size)
+    offsets, order, _ = ops.pack_plan(batch_indices, batch_size, with_rank=False)
     if max_events is None:
         max_events = int((offsets[1:] - offsets[:-1]).max().item()) if E > 0 else 0
     return ops.pack_rows(flat_tokens.reshape(E, flat_tokens.shape[-1]), order, offsets, batch_size, max_events)
@@ -42,7 +42,7 @@ def pack_events(flat_tokens: torch.Tensor, batch_indices: torch.Tensor, *, batch
 def pack_csr(flat_tokens: torch.Tensor, batch_indices: torch.Tensor, batch_size: int):
     """CSR form: ``(rows (E, D) in stable batch order, offsets (B+1,))``."""
     nat.require_gpu(flat_tokens, batch_indices, what="pack_csr")
-    offsets, order, _ = ops.pack_plan(batch_indices, batch_size)
+    offsets, order, _ = ops.pack_plan(batch_indices, batch_size, with_rank=False)
     E = batch_indices.shape[0]
     dev = flat_tokens.device
     out = torch.empty_like(flat_tokens.reshape(E, flat_tokens.shape[-1]))

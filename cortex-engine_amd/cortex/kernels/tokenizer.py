@@ -88,7 +88,7 @@ def tokenize_and_pack(neuron_emb, time_emb, value_emb, neuron_ids, time_bins, va
     E = neuron_ids.shape[0]
     if batch_size is None:
         batch_size = int(batch_indices.max().item()) + 1 if E > 0 else 1
-    offsets, order, _ = ops.pack_plan(batch_indices, batch_size, err=err)
+    offsets, order, _ = ops.pack_plan(batch_indices, batch_size, err=err, with_rank=False)
     if layout == "csr":
         tok = ops.tokenize(neuron_emb, time_emb, value_emb, neuron_ids, time_bins, values, order=order,
                            csr_offsets=offsets, err=err)

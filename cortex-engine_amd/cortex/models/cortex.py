@@ -168,7 +168,7 @@ class CortexModel(nn.Module):
         return self._forward_planned(neuron_ids, time_bins, values, offsets, None, offsets.shape[0] - 1, err_flag)
 
     def _forward_csr(self, neuron_ids, time_bins, values, batch_indices, B: int, err_flag=None) -> torch.Tensor:
-        offsets, order, _ = ops.pack_plan(batch_indices, B, err=err_flag)
+        offsets, order, _ = ops.pack_plan(batch_indices, B, err=err_flag, with_rank=False)
         return self._forward_planned(neuron_ids, time_bins, values, offsets, order, B, err_flag)
 
     def _forward_planned(self, neuron_ids, time_bins, values, offsets, order, B: int, err_flag) -> torch.Tensor:

@@ -117,54 +117,102 @@ __global__ __launch_bounds__(256) void ln_rows_kernel(const float* __restrict__ 
 // with e = order[r] (rows past *csr_end, or with an index outside its table, are x = 0
 // and the latter set bit 1 of err), then LN(x) with gamma/beta/eps is written as bf16.
 // The fp32 tokens are never stored.  Same lane layout as ln_rows_kernel.
+//
+// A row is a chain of dependent loads (order -> indices -> table rows), so each
+// wavefront takes TL_ROWS rows and issues every load of one link for all of them
+// (and gamma / beta, which depend on nothing) before waiting on any.
+constexpr int TL_ROWS = 2;
+
 template <int EPL>
 __global__ __launch_bounds__(256) void tokenize_ln_kernel(TokLnArgs a) {
-  constexpr int K = 64 * EPL;
+  constexpr int K = 64 * EPL, R = TL_ROWS;
   const int lane = threadIdx.x & 63;
-  const int64_t r = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
-  if (r >= a.E) return;
-  int64_t e = (a.csr_end && r >= *a.csr_end) ? -1 : (a.order ? a.order[r] : r);
-  if (e >= a.E) e = -1;  // defensive: never follow a corrupt order entry
-  const float* s0 = nullptr;
-  const float* s1 = nullptr;
-  const float* s2 = nullptr;
-  if (e >= 0) {
-    const int64_t i0 = a.nid[e * a.s_nid], i1 = a.tb[e * a.s_tb], i2 = a.val[e * a.s_val];
-    if (i0 < 0 || i0 >= a.n_neuron || i1 < 0 || i1 >= a.n_time || i2 < 0 || i2 >= a.n_value) {
-      if (lane == 0 && a.err) atomicOr(a.err, 1);
-      e = -1;
-    } else {
-      s0 = a.neuron + i0 * a.ld_neuron;
-      s1 = a.time + i1 * a.ld_time;
-      s2 = a.value + i2 * a.ld_value;
-    }
+  const int64_t r0 = ((int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6)) * R;
+  if (r0 >= a.E) return;
+  const int64_t end = a.csr_end ? *a.csr_end : a.E;
+  int64_t e[R];
+#pragma unroll
+  for (int i = 0; i < R; ++i) {
+    const int64_t r = r0 + i;
+    e[i] = r < a.E ? (a.order ? a.order[r] : r) : -1;
   }
-  float v[EPL];
+  float4 gm[EPL / 4], bt[EPL / 4];
 #pragma unroll
   for (int j = 0; j < EPL; j += 4) {
     const int k = (j >> 2) * 256 + lane * 4;
-    if (e < 0) {
-      v[j] = v[j + 1] = v[j + 2] = v[j + 3] = 0.0f;
-    } else {
-      const float4 x = *reinterpret_cast<const float4*>(s0 + k);
-      const float4 y = *reinterpret_cast<const float4*>(s1 + k);
-      const float4 z = *reinterpret_cast<const float4*>(s2 + k);
-      v[j] = (x.x + y.x) + z.x;
-      v[j + 1] = (x.y + y.y) + z.y;
-      v[j + 2] = (x.z + y.z) + z.z;
-      v[j + 3] = (x.w + y.w) + z.w;
+    gm[j >> 2] = a.gamma ? *reinterpret_cast<const float4*>(a.gamma + k) : make_float4(1.f, 1.f, 1.f, 1.f);
+    bt[j >> 2] = a.beta ? *reinterpret_cast<const float4*>(a.beta + k) : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+  int64_t i0[R], i1[R], i2[R];
+#pragma unroll
+  for (int i = 0; i < R; ++i) {
+    if (r0 + i >= end || e[i] >= a.E) e[i] = -1;  // past the CSR end, or a corrupt order entry
+    i0[i] = i1[i] = i2[i] = 0;
+    if (e[i] >= 0) {
+      i0[i] = a.nid[e[i] * a.s_nid];
+      i1[i] = a.tb[e[i] * a.s_tb];
+      i2[i] = a.val[e[i] * a.s_val];
     }
   }
-  ln_regs<EPL>(v, 1.0f / (float)K, a.eps, a.gamma, a.beta, lane);
-  bf16* out = reinterpret_cast<bf16*>(a.out) + r * a.ld_out;
+  const float* s0[R];
+  const float* s1[R];
+  const float* s2[R];
 #pragma unroll
-  for (int j = 0; j < EPL; j += 4) {
-    bf16x4 b;
-    b[0] = (bf16)v[j];
-    b[1] = (bf16)v[j + 1];
-    b[2] = (bf16)v[j + 2];
-    b[3] = (bf16)v[j + 3];
-    *reinterpret_cast<bf16x4*>(out + (j >> 2) * 256 + lane * 4) = b;
+  for (int i = 0; i < R; ++i) {
+    if (e[i] >= 0 && (i0[i] < 0 || i0[i] >= a.n_neuron || i1[i] < 0 || i1[i] >= a.n_time || i2[i] < 0 ||
+                      i2[i] >= a.n_value)) {
+      if (lane == 0 && a.err) atomicOr(a.err, 1);
+      e[i] = -1;
+    }
+    // a row without a valid event reads row 0 of each table and is zeroed below
+    s0[i] = a.neuron + (e[i] >= 0 ? i0[i] : 0) * a.ld_neuron;
+    s1[i] = a.time + (e[i] >= 0 ? i1[i] : 0) * a.ld_time;
+    s2[i] = a.value + (e[i] >= 0 ? i2[i] : 0) * a.ld_value;
+  }
+  float v[R][EPL];
+#pragma unroll
+  for (int i = 0; i < R; ++i)
+#pragma unroll
+    for (int j = 0; j < EPL; j += 4) {
+      const int k = (j >> 2) * 256 + lane * 4;
+      const float4 x = *reinterpret_cast<const float4*>(s0[i] + k);
+      const float4 y = *reinterpret_cast<const float4*>(s1[i] + k);
+      const float4 z = *reinterpret_cast<const float4*>(s2[i] + k);
+      v[i][j] = (x.x + y.x) + z.x;
+      v[i][j + 1] = (x.y + y.y) + z.y;
+      v[i][j + 2] = (x.z + y.z) + z.z;
+      v[i][j + 3] = (x.w + y.w) + z.w;
+    }
+  const float inv_k = 1.0f / (float)K;
+#pragma unroll
+  for (int i = 0; i < R; ++i) {
+    if (r0 + i >= a.E) break;
+    if (e[i] < 0) {
+#pragma unroll
+      for (int j = 0; j < EPL; ++j) v[i][j] = 0.0f;
+    }
+    float sum = 0.0f;
+#pragma unroll
+    for (int j = 0; j < EPL; ++j) sum += v[i][j];
+    const float mean = wave_sum(sum) * inv_k;
+    float ss = 0.0f;
+#pragma unroll
+    for (int j = 0; j < EPL; ++j) {
+      const float d = v[i][j] - mean;
+      ss += d * d;
+    }
+    const float rstd = 1.0f / sqrtf(wave_sum(ss) * inv_k + a.eps);
+    bf16* out = reinterpret_cast<bf16*>(a.out) + (r0 + i) * a.ld_out;
+#pragma unroll
+    for (int j = 0; j < EPL; j += 4) {
+      const float4 g = gm[j >> 2], b = bt[j >> 2];
+      bf16x4 o;
+      o[0] = (bf16)((v[i][j] - mean) * rstd * g.x + b.x);
+      o[1] = (bf16)((v[i][j + 1] - mean) * rstd * g.y + b.y);
+      o[2] = (bf16)((v[i][j + 2] - mean) * rstd * g.z + b.z);
+      o[3] = (bf16)((v[i][j + 3] - mean) * rstd * g.w + b.w);
+      *reinterpret_cast<bf16x4*>(out + (j >> 2) * 256 + lane * 4) = o;
+    }
   }
 }
 
@@ -246,16 +294,17 @@ int cortex_tokenize_ln(int64_t D, const float* neuron_emb, int64_t n_neuron, int
   CORTEX_CHECK_ARG(neuron_emb && time_emb && value_emb && neuron_ids && time_bins && values && out_bf16,
                    "cortex_tokenize_ln: null pointer");
   CORTEX_CHECK_ARG(ld_out >= D && ld_neuron >= D && ld_time >= D && ld_value >= D, "cortex_tokenize_ln: ld < D");
+  CORTEX_CHECK_ARG(n_neuron > 0 && n_time > 0 && n_value > 0, "cortex_tokenize_ln: empty embedding table");
   auto al16 = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
   CORTEX_CHECK_ARG(al16(neuron_emb) && al16(time_emb) && al16(value_emb) && ld_neuron % 4 == 0 && ld_time % 4 == 0 &&
                        ld_value % 4 == 0 && ((uintptr_t)out_bf16 & 7) == 0 && ld_out % 4 == 0 &&
                        (!gamma || al16(gamma)) && (!beta || al16(beta)),
                    "cortex_tokenize_ln: tables, gamma, beta need 16-byte aligned rows and out 8-byte aligned rows");
-  CORTEX_CHECK_ARG(cdiv(E, 4) <= 0x7fffffffLL, "cortex_tokenize_ln: E too large");
+  CORTEX_CHECK_ARG(cdiv(E, 4 * TL_ROWS) <= 0x7fffffffLL, "cortex_tokenize_ln: E too large");
   TokLnArgs a = {neuron_emb, n_neuron, ld_neuron, time_emb, n_time, ld_time, value_emb, n_value, ld_value,
                  neuron_ids, s_nid, time_bins, s_tb, values, s_val, E, order, csr_end, gamma, beta, eps,
                  out_bf16, ld_out, err_flag};
-  const dim3 grid((unsigned)cdiv(E, 4));
+  const dim3 grid((unsigned)cdiv(E, 4 * TL_ROWS));
   switch (D) {
     case 256: hipLaunchKernelGGL(tokenize_ln_kernel<4>, grid, dim3(256), 0, stream, a); break;
     case 512: hipLaunchKernelGGL(tokenize_ln_kernel<8>, grid, dim3(256), 0, stream, a); break;

@@ -32,6 +32,31 @@ __host__ __device__ inline int64_t pack_chunk_size(int64_t E) {
   return c;
 }
 
+// Lanes of the wavefront whose sample index equals this lane's, among the lanes with
+// `valid` set (0 <= b < 2^bits).  One test covers the common case of a single sample;
+// otherwise one ballot per bit of b, so the cost does not grow with the number of
+// distinct samples the 64 events hold (up to 64 for shuffled events).
+__device__ __forceinline__ uint64_t same_sample_lanes(int b, bool valid, int bits) {
+  uint64_t same = __ballot(valid);
+  if (same == 0) return 0ull;
+  // sorted batches: the 64 events usually belong to one sample
+  const int b0 = __builtin_amdgcn_readlane(b, __ffsll((unsigned long long)same) - 1);
+  if (__ballot(valid && b == b0) == same) return valid ? same : 0ull;
+  for (int k = 0; k < bits; ++k) {
+    const bool bit = (b >> k) & 1;
+    const uint64_t m = __ballot(bit);
+    same &= bit ? m : ~m;
+  }
+  return valid ? same : 0ull;
+}
+
+// Bits of a sample index below B.
+__host__ __device__ inline int sample_bits(int B) {
+  int bits = 0;
+  while ((1 << bits) < B) ++bits;
+  return bits;
+}
+
 // Small fill (kept as a kernel so that callers may capture it in a graph).
 __global__ void fill_i64_kernel(int64_t* p, int64_t n, int64_t v) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -49,7 +74,8 @@ __global__ __launch_bounds__(256) void pack_count_kernel(const int64_t* __restri
   const int64_t beg = (int64_t)chunk * C;
   const int64_t end = min(E, beg + C);
   bool bad = false;
-  const int lane = threadIdx.x & 63;
+  const int lane = threadIdx.x & 63, bits = sample_bits(B);
+  const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
   for (int64_t i0 = beg; i0 < end; i0 += blockDim.x) {  // every lane runs the same trip count
     const int64_t i = i0 + threadIdx.x;
     int64_t b = -1;
@@ -60,16 +86,10 @@ __global__ __launch_bounds__(256) void pack_count_kernel(const int64_t* __restri
         b = -1;
       }
     }
-    // one atomic per distinct sample among the wave's 64 events (sorted batches would
-    // otherwise send 64 atomics to one LDS word)
-    uint64_t active = __ballot(b >= 0);
-    while (active) {
-      const int leader = __ffsll((unsigned long long)active) - 1;
-      const int64_t lb = __shfl(b, leader, 64);
-      const uint64_t same = __ballot(b == lb) & active;
-      if (lane == leader) atomicAdd(&hist[lb], (int)__popcll(same));
-      active &= ~same;
-    }
+    // one atomic per distinct sample among the wave's 64 events, by its lowest lane
+    // (sorted batches would otherwise send 64 atomics to one LDS word)
+    const uint64_t same = same_sample_lanes((int)b, b >= 0, bits);
+    if (b >= 0 && (same & lt_mask) == 0) atomicAdd(&hist[b], (int)__popcll(same));
   }
   if (bad && err) atomicOr(err, ERR_BATCH_INDEX);
   __syncthreads();
@@ -129,30 +149,26 @@ __global__ __launch_bounds__(64) void pack_rank_kernel(const int64_t* __restrict
   const int64_t beg = (int64_t)chunk * C;
   const int64_t end = min(E, beg + C);
   const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  const int bits = sample_bits(B);
   for (int64_t base = beg; base < end; base += 64) {
     const int64_t i = base + lane;
     int64_t b = -1;
     if (i < end) {
       b = bidx[i * s_bidx];
-      if (b >= B) b = -1;  // counted as an error by pack_count_kernel
+      if (b < 0 || b >= B) b = -1;  // counted as an error by pack_count_kernel
     }
-    uint64_t active = __ballot(b >= 0);
-    while (active) {
-      const int leader = __ffsll((unsigned long long)active) - 1;
-      const int64_t lb = __shfl(b, leader, 64);
-      const uint64_t same = __ballot(b == lb) & active;
-      const int64_t row0 = next[lb];
-      if (b == lb) {
-        const int64_t row = row0 + __popcll(same & lt_mask);
-        order[row] = i;
-        if (dst_rows) dst_rows[i] = row;
-        if (rank) rank[i] = row - offsets[lb];
-      }
-      __syncthreads();  // single wavefront: orders the LDS read above before the update below
-      if (lane == leader) next[lb] = row0 + __popcll(same);
-      __syncthreads();
-      active &= ~same;
+    const uint64_t same = same_sample_lanes((int)b, b >= 0, bits);
+    int64_t row0 = 0;
+    if (b >= 0) {
+      row0 = next[b];  // every lane of a sample reads the same word ...
+      const int64_t row = row0 + __popcll(same & lt_mask);
+      order[row] = i;
+      if (dst_rows) dst_rows[i] = row;
+      if (rank) rank[i] = row - offsets[b];
     }
+    __syncthreads();  // single wavefront: the reads above complete before the update
+    if (b >= 0 && (same & lt_mask) == 0) next[b] = row0 + __popcll(same);  // ... and its lowest lane advances it
+    __syncthreads();
   }
 }
 
@@ -163,7 +179,7 @@ __global__ __launch_bounds__(64) void pack_rank_kernel(const int64_t* __restrict
 constexpr int PS_WAVES = 16;
 constexpr int PS_MAX_B = 1024;
 constexpr int64_t PS_MAX_E = 65536;
-constexpr int PS_UNROLL = 8;
+constexpr int PS_UNROLL = 16;
 
 __global__ __launch_bounds__(1024) void pack_small_kernel(const int64_t* __restrict__ bidx, int64_t s_bidx, int64_t E,
                                                           int B, int64_t* __restrict__ offsets,
@@ -178,6 +194,8 @@ __global__ __launch_bounds__(1024) void pack_small_kernel(const int64_t* __restr
   const int64_t C = cdiv(E, (int64_t)PS_WAVES);
   const int64_t beg = w * C, end = min(E, beg + C);
   int* mine = cnt + w * B;
+  const int bits = sample_bits(B);
+  const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
   bool bad = false;
   for (int64_t base = beg; base < end; base += 64 * PS_UNROLL) {  // PS_UNROLL loads in flight per lane
     int64_t bv[PS_UNROLL];
@@ -191,16 +209,10 @@ __global__ __launch_bounds__(1024) void pack_small_kernel(const int64_t* __restr
       int64_t b = bv[u];
       if (base + 64 * u + lane < end && (b < 0 || b >= B)) bad = true;
       if (b < 0 || b >= B) b = -1;
-      // one update per distinct sample in the 64 events: sorted batches (the common
-      // case) would otherwise send 64 atomics to one LDS word
-      uint64_t active = __ballot(b >= 0);
-      while (active) {
-        const int leader = __ffsll((unsigned long long)active) - 1;
-        const int lb = __builtin_amdgcn_readlane((int)b, leader);  // wave-uniform, b < B <= 1024
-        const uint64_t same = __ballot(b == lb) & active;
-        if (lane == leader) mine[lb] += __popcll(same);
-        active &= ~same;
-      }
+      // one update per distinct sample in the 64 events, by its lowest lane (distinct
+      // samples: distinct words of this wave's own row of cnt)
+      const uint64_t same = same_sample_lanes((int)b, b >= 0, bits);
+      if (b >= 0 && (same & lt_mask) == 0) mine[b] += __popcll(same);
     }
   }
   if (bad && err) atomicOr(err, ERR_BATCH_INDEX);
@@ -239,7 +251,6 @@ __global__ __launch_bounds__(1024) void pack_small_kernel(const int64_t* __restr
   for (int i = tid; i < PS_WAVES * B; i += blockDim.x) cnt[i] += first[i % B];
   __syncthreads();
   // in-order ranking inside the chunk; only this wave touches its row of `cnt`
-  const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
   for (int64_t base = beg; base < end; base += 64 * PS_UNROLL) {
     int64_t bv[PS_UNROLL];
 #pragma unroll
@@ -250,21 +261,17 @@ __global__ __launch_bounds__(1024) void pack_small_kernel(const int64_t* __restr
 #pragma unroll
     for (int u = 0; u < PS_UNROLL; ++u) {
       const int64_t i = base + 64 * u + lane;
-      const int64_t b = bv[u] >= B ? -1 : bv[u];
-      uint64_t active = __ballot(b >= 0);
-      while (active) {
-        const int leader = __ffsll((unsigned long long)active) - 1;
-        const int lb = __builtin_amdgcn_readlane((int)b, leader);  // wave-uniform, b < B <= 1024
-        const uint64_t same = __ballot(b == lb) & active;
-        const int row0 = mine[lb];  // one LDS word for the whole wave; read before the update below
-        if (b == lb) {
-          const int64_t row = row0 + __popcll(same & lt_mask);
-          order[row] = i;
-          if (dst_rows) dst_rows[i] = row;
-          if (rank) rank[i] = row - first[lb];
-        }
-        if (lane == leader) mine[lb] = row0 + __popcll(same);
-        active &= ~same;
+      const int64_t b = (bv[u] < 0 || bv[u] >= B) ? -1 : bv[u];
+      const uint64_t same = same_sample_lanes((int)b, b >= 0, bits);
+      if (b >= 0) {
+        // all lanes of a sample read its word before its lowest lane advances it (one
+        // wavefront's LDS operations complete in program order)
+        const int row0 = mine[b];
+        const int64_t row = row0 + __popcll(same & lt_mask);
+        order[row] = i;
+        if (dst_rows) dst_rows[i] = row;
+        if (rank) rank[i] = row - first[b];
+        if ((same & lt_mask) == 0) mine[b] = row0 + __popcll(same);
       }
     }
   }
