@@ -26,6 +26,7 @@ inference executor thread.  Prometheus gauges of the reference are not kept.
 from __future__ import annotations
 
 import time
+import weakref
 from collections import OrderedDict
 from dataclasses import dataclass
 from typing import Any
@@ -145,26 +146,105 @@ class StreamingKVCache(_PagedLRU):
         self._written(page_id, n)
 
 
-class EventWindowCache(_PagedLRU):
+class _NativePageTable:
+    """The page table, free list and LRU order of ``EventWindowCache`` in native code
+    (``cortex_page_table_*``): the policy of ``_PagedLRU`` with a whole batch of page
+    writes or window lookups per call.  Session names map to int64 ids here."""
+
+    def __init__(self, num_pages: int) -> None:
+        lib = nat.load()
+        box = np.zeros(1, dtype=np.uint64)
+        nat.call("cortex_page_table_create", num_pages, box.ctypes.data)
+        self._h = int(box[0])
+        self._ids: dict[str, int] = {}
+        self._finalizer = weakref.finalize(self, lib.cortex_page_table_destroy, self._h)
+        self._i64 = np.zeros(3, dtype=np.int64)  # scalar outputs
+
+    def session(self, name: str) -> int:
+        sid = self._ids.get(name)
+        if sid is None:
+            sid = self._ids[name] = len(self._ids)
+        return sid
+
+    def write(self, sessions: np.ndarray, bin_starts: np.ndarray, counts: np.ndarray) -> np.ndarray:
+        pages = np.empty(sessions.shape[0], dtype=np.int64)
+        nat.call("cortex_page_table_write", self._h, sessions.shape[0], sessions.ctypes.data,
+                 bin_starts.ctypes.data, counts.ctypes.data, pages.ctypes.data)
+        return pages
+
+    def lookup(self, name: str, bin_start: int) -> tuple[int, int]:
+        """(page, events) of a key, touched and counted; page -1 (a miss) when absent."""
+        out = self._i64
+        nat.call("cortex_page_table_lookup", self._h, self.session(name), bin_start, out[0:].ctypes.data,
+                 out[1:].ctypes.data)
+        return int(out[0]), int(out[1])
+
+    def plan(self, names: list[str], starts: np.ndarray, window_bins: int, bins_per_page: int):
+        n = len(names)
+        per = window_bins // bins_per_page
+        sessions = np.fromiter((self.session(x) for x in names), dtype=np.int64, count=n)
+        items = np.empty((max(n * per, 1), 4), dtype=np.int64)
+        offsets = np.empty(n + 1, dtype=np.int64)
+        missing = np.empty(max(per, 1), dtype=np.int64)
+        out = np.zeros(3, dtype=np.int64)  # n_items, missing window, n_missing
+        nat.call("cortex_page_table_plan", self._h, n, sessions.ctypes.data, starts.ctypes.data, window_bins,
+                 bins_per_page, items.ctypes.data, items.shape[0], out[0:].ctypes.data, offsets.ctypes.data,
+                 out[1:].ctypes.data, missing.ctypes.data, out[2:].ctypes.data)
+        if out[1] >= 0:
+            raise KeyError(f"session {names[int(out[1])]!r}: no page for bins starting at "
+                           f"{missing[:int(out[2])].tolist()}")
+        return items[:int(out[0])], offsets
+
+    def evict_session(self, name: str) -> int:
+        if name not in self._ids:
+            return 0
+        out = self._i64
+        nat.call("cortex_page_table_evict_session", self._h, self._ids[name], out.ctypes.data)
+        return int(out[0])
+
+    def stats(self) -> tuple[int, int, int]:
+        out = np.zeros(3, dtype=np.int64)
+        nat.call("cortex_page_table_stats", self._h, out[0:].ctypes.data, out[1:].ctypes.data, out[2:].ctypes.data)
+        return int(out[0]), int(out[1]), int(out[2])
+
+
+class EventWindowCache:
     """Device pages of raw spike events keyed by ``(session_id, absolute first bin)``.
 
     Page ``(s, b0)`` holds the events of bins ``[b0, b0 + bins_per_page)``, at most
     ``page_events`` of them, as int64 rows (neuron id, absolute bin, value).  A
     window ``[w0, w0 + window_bins)`` with ``w0`` and ``window_bins`` multiples of
-    ``bins_per_page`` is the concatenation of its pages in bin order.
+    ``bins_per_page`` is the concatenation of its pages in bin order.  The page table
+    (lookups, LRU eviction) is native; its policy is ``StreamingKVCache``'s.
     """
 
     def __init__(self, num_pages: int = 4096, page_events: int = 1024, bins_per_page: int = 50,
                  device: str | torch.device = "cuda") -> None:
-        super().__init__(num_pages)
+        if num_pages < 1:
+            raise ValueError("num_pages must be >= 1")
+        self.num_pages = num_pages
         self.page_events = page_events
         self.bins_per_page = bins_per_page
         self.device = torch.device(device)
         nat.require_gpu(torch.empty(0, device=self.device), what="EventWindowCache")
+        self._table = _NativePageTable(num_pages)
         self._pool = torch.zeros(num_pages, 3, page_events, dtype=torch.int64, device=self.device)
         self._stage_host = torch.empty(1 << 15, dtype=torch.int64).pin_memory()
         self._stage_dev = torch.empty_like(self._stage_host, device=self.device)
         self._staged = torch.cuda.Event()
+
+    @property
+    def hit_rate(self) -> float:
+        hits, misses, _ = self._table.stats()
+        return hits / (hits + misses) if hits + misses > 0 else 0.0
+
+    @property
+    def pages_used(self) -> int:
+        return self._table.stats()[2]
+
+    def evict_session(self, session_id: str) -> int:
+        """Free every page of ``session_id``; returns how many were freed."""
+        return self._table.evict_session(session_id)
 
     def write(self, session_id: str, bin_start: int, neuron_ids: Any, time_bins: Any, values: Any) -> None:
         """Store the events of bins ``[bin_start, bin_start + bins_per_page)``; ``time_bins``
@@ -175,56 +255,68 @@ class EventWindowCache(_PagedLRU):
     def write_many(self, pages: list[tuple[str, int, Any, Any, Any]]) -> None:
         """Several page writes as one pinned host->device copy and one scatter launch, on the
         current stream.  Entries are ``(session_id, bin_start, neuron_ids, time_bins, values)``
-        with host integer arrays; a key given twice keeps its last entry."""
+        with host integer arrays; a key given twice keeps its last entry.  Every entry is
+        checked before any page is written."""
         last: dict[tuple[str, int], tuple[np.ndarray, ...]] = {}
         for session_id, bin_start, nid, tb, val in pages:
-            if bin_start % self.bins_per_page:
-                raise ValueError(f"bin_start {bin_start} is not a multiple of bins_per_page={self.bins_per_page}")
-            cols = tuple(np.asarray(x.cpu() if torch.is_tensor(x) else x).reshape(-1).astype(np.int64, copy=False)
-                         for x in (nid, tb, val))
-            n = cols[0].shape[0]
-            if not (cols[1].shape[0] == cols[2].shape[0] == n):
-                raise ValueError("neuron_ids, time_bins and values must have the same length")
-            if n > self.page_events:
-                raise ValueError(f"{n} events exceed page_events={self.page_events}")
-            if n and (cols[1].min() < bin_start or cols[1].max() >= bin_start + self.bins_per_page):
-                raise ValueError(f"time bins [{cols[1].min()}, {cols[1].max()}] outside page "
-                                 f"[{bin_start}, {bin_start + self.bins_per_page})")
-            last[(session_id, bin_start)] = cols
+            last[(session_id, int(bin_start))] = tuple(
+                np.asarray(x.cpu() if torch.is_tensor(x) else x).reshape(-1) for x in (nid, tb, val))
+        if not last:
+            return
         if len(last) > self.num_pages:
             raise ValueError(f"{len(last)} pages in one write exceed the pool's {self.num_pages}")
-        total = sum(c[0].shape[0] for c in last.values())
-        items, row = [], 0
-        for key, cols in last.items():
-            page_id = self._page_for_write(*key)
-            n = cols[0].shape[0]
-            if n:
-                items.append((page_id, n, row))
-            row += n
-            self._written(page_id, n)
-        if not items:
+        keys = list(last)
+        starts = np.fromiter((k[1] for k in keys), dtype=np.int64, count=len(keys))
+        bad = starts % self.bins_per_page != 0
+        if bad.any():
+            raise ValueError(f"bin_start {int(starts[bad][0])} is not a multiple of "
+                             f"bins_per_page={self.bins_per_page}")
+        counts = np.fromiter((c[0].shape[0] for c in last.values()), dtype=np.int64, count=len(keys))
+        for c in last.values():
+            if not (c[1].shape[0] == c[2].shape[0] == c[0].shape[0]):
+                raise ValueError("neuron_ids, time_bins and values must have the same length")
+        if counts.max() > self.page_events:
+            raise ValueError(f"{int(counts.max())} events exceed page_events={self.page_events}")
+        total = int(counts.sum())
+        cols = [np.concatenate([c[f] for c in last.values()]).astype(np.int64, copy=False) if total
+                else np.zeros(0, dtype=np.int64) for f in range(3)]
+        if total:
+            lo = np.repeat(starts, counts)
+            outside = (cols[1] < lo) | (cols[1] >= lo + self.bins_per_page)
+            if outside.any():
+                i = int(np.argmax(outside))
+                k = int(np.searchsorted(np.cumsum(counts), i, side="right"))
+                b0 = int(starts[k])
+                tb = cols[1][int(counts[:k].sum()):int(counts[:k + 1].sum())]
+                raise ValueError(f"time bins [{tb.min()}, {tb.max()}] outside page "
+                                 f"[{b0}, {b0 + self.bins_per_page})")
+        sessions = np.fromiter((self._table.session(k[0]) for k in keys), dtype=np.int64, count=len(keys))
+        page_ids = self._table.write(sessions, starts, counts)
+        nz = counts > 0
+        if not nz.any():
             return
-        need = 3 * total + 3 * len(items)
+        first_row = np.cumsum(counts) - counts
+        items = np.stack([page_ids[nz], counts[nz], first_row[nz]], axis=1)
+        need = 3 * total + items.size
         self._staged.synchronize()  # the previous write's copy has left the pinned buffer
         if self._stage_host.numel() < need:
             self._stage_host = torch.empty(max(need, 2 * self._stage_host.numel()), dtype=torch.int64).pin_memory()
             self._stage_dev = torch.empty_like(self._stage_host, device=self.device)
         h = self._stage_host.numpy()
         for f in range(3):
-            np.concatenate([c[f] for c in last.values()], out=h[f * total:(f + 1) * total])
-        h[3 * total:need] = np.asarray(items, dtype=np.int64).reshape(-1)
+            h[f * total:(f + 1) * total] = cols[f]
+        h[3 * total:need] = items.reshape(-1)
         dev = self._stage_dev[:need]
         dev.copy_(self._stage_host[:need], non_blocking=True)
         self._staged.record()
-        nat.call("cortex_scatter_event_pages", nat.ptr(dev), total, total, nat.ptr(dev[3 * total:]), len(items),
+        nat.call("cortex_scatter_event_pages", nat.ptr(dev), total, total, nat.ptr(dev[3 * total:]), items.shape[0],
                  nat.ptr(self._pool), self.num_pages, self.page_events, None, nat.stream_of(self.device))
 
     def read(self, session_id: str, bin_start: int) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor] | None:
         """(neuron ids, absolute bins, values) views of a page, or None."""
-        page_id = self._lookup(session_id, bin_start)
-        if page_id is None:
+        page_id, n = self._table.lookup(session_id, bin_start)
+        if page_id < 0:
             return None
-        n = self._meta[page_id].n_events
         p = self._pool[page_id]
         return p[0, :n], p[1, :n], p[2, :n]
 
@@ -234,26 +326,25 @@ class EventWindowCache(_PagedLRU):
         if window_start % self.bins_per_page or window_bins % self.bins_per_page:
             raise ValueError("window_start and window_bins must be multiples of bins_per_page")
         starts = range(window_start, window_start + window_bins, self.bins_per_page)
-        pages = [self._lookup(session_id, b) for b in starts]
-        missing = [b for b, p in zip(starts, pages) if p is None]
+        pages = [self._table.lookup(session_id, b) for b in starts]
+        missing = [b for b, (p, _) in zip(starts, pages) if p < 0]
         if missing:
             raise KeyError(f"session {session_id!r}: no page for bins starting at {missing}")
-        return [(p, self._meta[p].n_events) for p in pages]
+        return pages
 
     def plan(self, windows: list[tuple[str, int]], window_bins: int) -> tuple[np.ndarray, np.ndarray]:
         """Gather plan of a batch of windows: ``(items (n, 4) int64, offsets (B+1) int64)``.
 
         Item = (page id, events, first output row, bin shift = window start); window b
-        owns output rows ``[offsets[b], offsets[b+1])``.
+        owns output rows ``[offsets[b], offsets[b+1])``.  KeyError names the first window's
+        missing pages.
         """
-        items, offsets, row = [], [0], 0
-        for session_id, w0 in windows:
-            for page_id, n in self.window_pages(session_id, w0, window_bins):
-                if n:
-                    items.append((page_id, n, row, w0))
-                    row += n
-            offsets.append(row)
-        return np.asarray(items, dtype=np.int64).reshape(-1, 4), np.asarray(offsets, dtype=np.int64)
+        if window_bins % self.bins_per_page:
+            raise ValueError("window_bins must be a multiple of bins_per_page")
+        starts = np.fromiter((w[1] for w in windows), dtype=np.int64, count=len(windows))
+        if (starts % self.bins_per_page).any():
+            raise ValueError("window starts must be multiples of bins_per_page")
+        return self._table.plan([w[0] for w in windows], starts, window_bins, self.bins_per_page)
 
     def gather(self, items: torch.Tensor, out: torch.Tensor, field_stride: int, out_rows: int,
                err: torch.Tensor | None = None) -> None:

@@ -262,6 +262,37 @@ int cortex_scatter_event_pages(const int64_t* src, int64_t field_stride, int64_t
                                int64_t n_items, int64_t* pool, int64_t num_pages, int64_t page_events, int32_t* err,
                                hipStream_t stream);
 
+/* Host page table of that cache (no device work; not thread-safe, one caller per
+ * table).  Replaces the Python bookkeeping of StreamingKVCache with the same policy
+ * (cortex/cache/streaming.py:133-233): a lookup of a present key touches its page
+ * (most recently used) and counts a hit, an absent key counts a miss; a write reuses
+ * the key's page or allocates one, from the free list (last freed first) or by
+ * evicting the least recently used page, records its event count and touches it;
+ * evicting a session frees its pages in first-write order.  Keys are
+ * (session id, first bin) with session ids chosen by the caller. */
+int cortex_page_table_create(int64_t num_pages, void** table);
+int cortex_page_table_destroy(void* table);
+/* n page writes in order; page_ids[i] receives the page of entry i. */
+int cortex_page_table_write(void* table, int64_t n, const int64_t* sessions, const int64_t* bin_starts,
+                            const int64_t* n_events, int64_t* page_ids);
+/* *page_id = the key's page (touched) or -1; *n_events its event count (0 if absent). */
+int cortex_page_table_lookup(void* table, int64_t session, int64_t bin_start, int64_t* page_id, int64_t* n_events);
+/* Gather plan of n_windows windows [window_starts[w], + window_bins): every page of
+ * each window, in order, is looked up; items (capacity items_cap >= n_windows *
+ * window_bins / bins_per_page rows of 4) receive (page, count, first output row,
+ * window start) for the non-empty pages, offsets (n_windows + 1) the first output
+ * row of each window.  If window w lacks pages, *missing_window = w, missing[0 ..
+ * *n_missing) hold the first bins of its absent pages, and no window after w is
+ * looked up; otherwise *missing_window = -1.  Replaces the per-page lookups of
+ * StreamingKVCache.read (cortex/cache/streaming.py:133-153) for a batch of windows. */
+int cortex_page_table_plan(void* table, int64_t n_windows, const int64_t* sessions, const int64_t* window_starts,
+                           int64_t window_bins, int64_t bins_per_page, int64_t* items, int64_t items_cap,
+                           int64_t* n_items, int64_t* offsets, int64_t* missing_window, int64_t* missing,
+                           int64_t* n_missing);
+/* StreamingKVCache.evict_session (cortex/cache/streaming.py:192-201): *freed = pages freed. */
+int cortex_page_table_evict_session(void* table, int64_t session, int64_t* freed);
+int cortex_page_table_stats(void* table, int64_t* hits, int64_t* misses, int64_t* pages_used);
+
 #ifdef __cplusplus
 }
 #endif
