@@ -437,15 +437,18 @@ def serving_sweep(model, dev, batches=(1, 8, 32, 128, 256), reps: int = 20):
     return out
 
 
-def cpu_baseline(model, budget_s: float = 20.0):
+def cpu_baseline(model, budget_s: float = 12.0, b1_budget_s: float = 18.0):
     """The CPU oracle (fp32 activations, INT8 weights dequantised as the reference's QuantizedLinear)
-    on the host cores: B=32 x 512-event forwards until the time budget is spent."""
+    on the host cores, with the reference's protocol (profile_inference.py: 5 warmup + up to 30 timed
+    B=32 x 512-event forwards, mean), bounded by ``budget_s``; the per-section split of one forward;
+    and p50/p99 over up to 1000 B=1 requests within ``b1_budget_s``."""
     from oracle import cortex_oracle as O
 
     torch.set_num_threads(os.cpu_count() or 1)
     sd = {k: v.detach().cpu() for k, v in model.state_dict().items()}
     arrs = make_events(B_MAIN, PER_MAIN, seed=0)
-    O.forward(sd, O.CORTEX_S_SHAPE, *arrs)  # warm-up
+    for _ in range(5):
+        O.forward(sd, O.CORTEX_S_SHAPE, *arrs)
     n, t0 = 0, time.perf_counter()
     while True:
         O.forward(sd, O.CORTEX_S_SHAPE, *arrs)
@@ -453,6 +456,17 @@ def cpu_baseline(model, budget_s: float = 20.0):
         el = time.perf_counter() - t0
         if el >= budget_s or n >= 30:
             break
+    sections: dict = {}
+    O.forward(sd, O.CORTEX_S_SHAPE, *arrs, sections=sections)
+    one = make_events(1, PER_MAIN, seed=7)
+    for _ in range(5):
+        O.forward(sd, O.CORTEX_S_SHAPE, *one)
+    lat, t1 = [], time.perf_counter()
+    while len(lat) < 1000 and time.perf_counter() - t1 < b1_budget_s:
+        t = time.perf_counter()
+        O.forward(sd, O.CORTEX_S_SHAPE, *one)
+        lat.append((time.perf_counter() - t) * 1e3)
+    lat.sort()
     cpu = "unknown"
     try:
         for line in open("/proc/cpuinfo"):
@@ -463,7 +477,10 @@ def cpu_baseline(model, budget_s: float = 20.0):
         pass
     return {"value": round(B_MAIN * n / el, 2), "unit": "samples/s", "cores": torch.get_num_threads(),
             "kind": "port", "sample": f"{n} forwards of B=32 x 512 events (CORTEX_S, INT8 dequantised to fp32, "
-                                      f"oracle restatement) in {el:.1f} s", "cpu": cpu}
+                                      f"oracle restatement) in {el:.1f} s after 5 warmup",
+            "cpu": cpu, "sections_ms": {k: round(v * 1e3, 2) for k, v in sections.items()},
+            "b1_p50_ms": round(lat[len(lat) // 2], 3), "b1_p99_ms": round(lat[max(int(len(lat) * 0.99) - 1, 0)], 3),
+            "b1_requests": len(lat)}
 
 
 # --------------------------------------------------------------------------- modes

@@ -43,6 +43,7 @@ forward / forward_int8      behavior goldens written by importing the reference
 from __future__ import annotations
 
 import math
+import time
 from dataclasses import dataclass
 
 import numpy as np
@@ -336,9 +337,13 @@ def _merge(x: torch.Tensor) -> torch.Tensor:
     return x.permute(0, 2, 1, 3).reshape(b, l, h * d)
 
 
-def encode(sd: dict, shape: ModelShape, tokens: torch.Tensor, mask: torch.Tensor) -> torch.Tensor:
+def encode(sd: dict, shape: ModelShape, tokens: torch.Tensor, mask: torch.Tensor,
+           sections: dict | None = None) -> torch.Tensor:
     """PerceiverEncoder.forward (reference perceiver.py:145-158) with the
-    cross-attention block (:54-82) and self-attention blocks (:107-126)."""
+    cross-attention block (:54-82) and self-attention blocks (:107-126).  ``sections``,
+    when given, receives the wall seconds of the cross-attention block and of the
+    self-attention blocks (timing only; the result does not depend on it)."""
+    t0 = time.perf_counter()
     B = tokens.shape[0]
     lat = sd["encoder.latents"].unsqueeze(0).expand(B, -1, -1)
     p = "encoder.cross_attn"
@@ -349,6 +354,7 @@ def encode(sd: dict, shape: ModelShape, tokens: torch.Tensor, mask: torch.Tensor
     o = F.scaled_dot_product_attention(_heads(q, h), _heads(k, h), _heads(v, h),
                                        attn_mask=mask[:, None, None, :])
     x = lat + _linear(sd, f"{p}.out_proj", _merge(o))
+    t1 = time.perf_counter()
     for i in range(shape.num_layers):
         p = f"encoder.self_attn_blocks.{i}"
         qkv = _linear(sd, f"{p}.qkv_proj", _ln(sd, f"{p}.norm_attn", x))
@@ -358,6 +364,9 @@ def encode(sd: dict, shape: ModelShape, tokens: torch.Tensor, mask: torch.Tensor
         x = x + _linear(sd, f"{p}.out_proj", _merge(o))
         hmid = F.gelu(_linear(sd, f"{p}.mlp.0", _ln(sd, f"{p}.norm_mlp", x)))
         x = x + _linear(sd, f"{p}.mlp.2", hmid)
+    if sections is not None:
+        sections["cross_attn"] = t1 - t0
+        sections["self_attn_all"] = time.perf_counter() - t1
     return _ln(sd, "encoder.final_norm", x)
 
 
@@ -376,25 +385,36 @@ def behavior_head(sd: dict, shape: ModelShape, latents: torch.Tensor) -> torch.T
 
 
 def forward(sd: dict, shape: ModelShape, neuron_ids, time_bins, values, batch_indices,
-            batch_size: int | None = None) -> torch.Tensor:
+            batch_size: int | None = None, sections: dict | None = None) -> torch.Tensor:
     """CortexModel.forward (reference cortex/models/cortex.py:90-122) in fp32 on the CPU.
 
     ``sd`` is a CPU state_dict of a float model or of a model after the reference's
     ``convert_model`` (int8 ``weight_int8`` + fp32 ``weight_scale`` buffers).
-    Returns ``behavior`` (B, behavior_dim).
+    Returns ``behavior`` (B, behavior_dim).  ``sections``, when given, receives wall
+    seconds per section (tokenizer, pack_events, cross_attn, self_attn_all,
+    behavior_head), as the reference's profile_inference.py sections.
     """
+    t0 = time.perf_counter()
     sd = {k: v.detach().cpu() for k, v in sd.items()}
     nid = np.asarray(neuron_ids, dtype=np.int64)
     tb = np.asarray(time_bins, dtype=np.int64)
     val = np.asarray(values, dtype=np.int64)
     tok = tokenize(sd["tokenizer.neuron_emb.weight"].numpy(), sd["tokenizer.time_emb.weight"].numpy(),
                    sd["tokenizer.value_emb.weight"].numpy(), nid, tb, val)
+    t1 = time.perf_counter()
     packed = pack_events(tok, batch_indices, batch_size)
     tokens = torch.from_numpy(packed.padded)
     mask = torch.from_numpy(packed.mask)
+    t2 = time.perf_counter()
     with torch.no_grad():
-        lat = encode(sd, shape, tokens, mask)
-        return behavior_head(sd, shape, lat)
+        lat = encode(sd, shape, tokens, mask, sections)
+        t3 = time.perf_counter()
+        out = behavior_head(sd, shape, lat)
+    if sections is not None:
+        sections["tokenizer"] = t1 - t0
+        sections["pack_events"] = t2 - t1
+        sections["behavior_head"] = time.perf_counter() - t3
+    return out
 
 
 def quantize_state_dict(sd: dict, skip_prefixes=("masked_spike_head.",)) -> dict:
