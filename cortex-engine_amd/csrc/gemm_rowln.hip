@@ -14,9 +14,9 @@
 // Operand streaming as in gemm_bf16.hip: direct-to-LDS transfers through a ring of
 // STAGES, early stage release, double-buffered fragments, C^T tiles so a lane holds 4
 // consecutive columns of one row.  The residual tile is prefetched into registers.
-// Row statistics: lane sums -> xor-shuffles over the 4 lane groups -> the 8
-// wavefronts' partials through LDS; two passes (mean, then squared deviations) as
-// the LayerNorm row kernel.
+// Row statistics: per wavefront the mean and squared deviations of its columns (lane
+// sums, xor-shuffles over the 4 lane groups), combined across the 8 wavefronts through
+// LDS in one exchange.
 #include <hip/hip_runtime.h>
 
 #include "common.h"
@@ -31,6 +31,22 @@ template <int n>
 __device__ __forceinline__ void rl_wait_vm() {
   static_assert(n >= 0 && n < 64, "vmcnt range");
   __builtin_amdgcn_s_waitcnt((n & 15) | 0x70 | 0xF00 | ((n >> 4) << 14));
+}
+
+// Wait until a ring step's transfers landed when `ahead` later steps (PER transfers
+// each, at most S - 1) and X other loads were issued after it.
+template <int PER, int S, int X>
+__device__ __forceinline__ void rl_wait_ahead(int ahead) {
+  if constexpr (S >= 3) {
+    if (ahead >= 2) {
+      rl_wait_vm<2 * PER + X>();
+      return;
+    }
+  }
+  if (ahead >= 1)
+    rl_wait_vm<PER + X>();
+  else
+    rl_wait_vm<X>();
 }
 
 __device__ __forceinline__ int rl_swz(int r) { return (r >> 1) & 7; }
@@ -130,7 +146,14 @@ __global__ __launch_bounds__(RL_THREADS) void gemm_rowln_kernel(RowLnArgs g) {
       for (int j = 0; j < TN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf[j], af[i], acc[i][j], 0, 0, 0);
   };
 
-  // residual tile into registers first: its latency hides behind the main loop
+#pragma unroll
+  for (int p = 0; p < S; ++p)
+    if (p < nk) issue(p);
+  // The residual tile goes into registers right after the first ring stages: the first
+  // MFMAs do not wait for it and its latency hides behind the main loop.  Its RV loads
+  // sit behind the prologue's transfers in the wave's vmcnt (the scheduling barrier keeps
+  // the compiler from moving them in front).
+  __builtin_amdgcn_sched_barrier(0);
   const int res_rows = g.res_rows > 0 ? (int)g.res_rows : M;
   float4 rv[TM][TN];
 #pragma unroll
@@ -141,24 +164,13 @@ __global__ __launch_bounds__(RL_THREADS) void gemm_rowln_kernel(RowLnArgs g) {
       rv[i][j] = *reinterpret_cast<const float4*>(g.res + (int64_t)(m % res_rows) * g.ld_res + wcol + 16 * j + 4 * g4);
   }
 
-#pragma unroll
-  for (int p = 0; p < S; ++p)
-    if (p < nk) issue(p);
+  constexpr int RV = TM * TN;
   auto wait_step = [&](int j, int last) {  // this wave's transfers of step j landed
     const int ahead = min(nk - 1, last) - j;
-    if constexpr (S >= 3) {
-      if (ahead >= 2)
-        rl_wait_vm<2 * PER>();
-      else if (ahead == 1)
-        rl_wait_vm<PER>();
-      else
-        rl_wait_vm<0>();
-    } else {
-      if (ahead >= 1)
-        rl_wait_vm<PER>();
-      else
-        rl_wait_vm<0>();
-    }
+    if (j < S)
+      rl_wait_ahead<PER, S, RV>(ahead);  // prologue step: the residual loads came after it
+    else
+      rl_wait_ahead<PER, S, 0>(ahead);
   };
   bf16x8 af0[TM], wf0[TN], af1[TM], wf1[TN];
   wait_step(0, S - 1);
@@ -226,43 +238,57 @@ __global__ __launch_bounds__(RL_THREADS) void gemm_rowln_kernel(RowLnArgs g) {
     }
   }
 
-  // row statistics: this wave's part of each row, then the 8 wavefronts through LDS
-  float* red = reinterpret_cast<float*>(smem);  // [RL_WAVES][RL_BM]
-  const float inv_n = 1.0f / (float)BN;
+  // Row statistics with one exchange between the 8 wavefronts: each wavefront takes
+  // the mean and the sum of squared deviations (M2) of its WN columns of every row
+  // (lane sums, then xor-shuffles over the 4 lane groups), and the 8 equal-sized
+  // parts combine as mean = avg(mean_w), M2 = sum(M2_w) + WN * sum((mean_w - mean)^2)
+  // (Chan, Golub and LeVeque's pairwise update), as stable as two full passes.
+  float2* red = reinterpret_cast<float2*>(smem);  // [RL_WAVES][RL_BM]
+  constexpr float inv_wn = 1.0f / (float)WN;
   float mean[TM], rstd[TM];
   __syncthreads();  // every ring read is done: the LDS may be reused
 #pragma unroll
-  for (int pass = 0; pass < 2; ++pass) {
-    float part[TM];
+  for (int i = 0; i < TM; ++i) {
+    float sum = 0.0f;
 #pragma unroll
-    for (int i = 0; i < TM; ++i) {
-      float s = 0.0f;
+    for (int j = 0; j < TN; ++j)
 #pragma unroll
-      for (int j = 0; j < TN; ++j)
+      for (int r = 0; r < 4; ++r) sum += v[i][j][r];
+    sum += __shfl_xor(sum, 16, 64);
+    sum += __shfl_xor(sum, 32, 64);
+    const float mw = sum * inv_wn;
+    float m2 = 0.0f;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const float d = pass == 0 ? v[i][j][r] : v[i][j][r] - mean[i];
-          s += pass == 0 ? d : d * d;
-        }
-      s += __shfl_xor(s, 16, 64);
-      s += __shfl_xor(s, 32, 64);
-      part[i] = s;
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float d = v[i][j][r] - mw;
+        m2 += d * d;
+      }
+    m2 += __shfl_xor(m2, 16, 64);
+    m2 += __shfl_xor(m2, 32, 64);
+    if (g4 == 0) red[wid * RL_BM + i * 16 + fr] = make_float2(mw, m2);
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+    float2 part[RL_WAVES];
+    float msum = 0.0f;
+#pragma unroll
+    for (int w = 0; w < RL_WAVES; ++w) {
+      part[w] = red[w * RL_BM + i * 16 + fr];
+      msum += part[w].x;
     }
-    if (g4 == 0) {
+    const float mu = msum * (1.0f / (float)RL_WAVES);
+    float m2 = 0.0f, dev = 0.0f;
 #pragma unroll
-      for (int i = 0; i < TM; ++i) red[(pass * RL_WAVES + wid) * RL_BM + i * 16 + fr] = part[i];
+    for (int w = 0; w < RL_WAVES; ++w) {
+      const float d = part[w].x - mu;
+      m2 += part[w].y;
+      dev += d * d;
     }
-    __syncthreads();
-#pragma unroll
-    for (int i = 0; i < TM; ++i) {
-      float t = 0.0f;
-#pragma unroll
-      for (int w = 0; w < RL_WAVES; ++w) t += red[(pass * RL_WAVES + w) * RL_BM + i * 16 + fr];
-      if (pass == 0)
-        mean[i] = t * inv_n;
-      else
-        rstd[i] = 1.0f / sqrtf(t * inv_n + g.eps);
-    }
+    mean[i] = mu;
+    rstd[i] = 1.0f / sqrtf(fmaf(dev, (float)WN, m2) * (1.0f / (float)BN) + g.eps);
   }
 #pragma unroll
   for (int j = 0; j < TN; ++j) {
