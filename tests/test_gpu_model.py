@@ -96,6 +96,28 @@ def test_config3_int8_bf16_forward_vs_oracle():
     assert np.abs(beh - ref).max() <= 2e-2, np.abs(beh - ref).max()
 
 
+@pytest.mark.parametrize("B,lo,hi,seed", [(1, 1, 1, 11), (1, 2048, 2048, 12), (3, 64, 2048, 13), (17, 1, 700, 14),
+                                         (64, 64, 900, 15)])
+def test_ragged_batches_int8_bf16_vs_oracle(B, lo, hi, seed):
+    """Serving-shaped batches: B samples with U[lo, hi] events each (a single event, a
+    2048-event sample, 17 ragged samples ...), events in random order; the INT8 bf16
+    forward (graph-free) is within 2e-2 max-abs of the float32 oracle."""
+    rng = np.random.default_rng(seed)
+    counts = rng.integers(lo, hi + 1, B)
+    E = int(counts.sum())
+    bidx = np.repeat(np.arange(B), counts)
+    perm = rng.permutation(E)
+    arrs = (rng.integers(0, 137, E), rng.integers(0, 600, E), np.clip(rng.poisson(1.0, E) + 1, 0, 7), bidx[perm])
+    inputs = [torch.from_numpy(np.ascontiguousarray(a)).to(DEV) for a in arrs]
+    model = _int8(_model("s", "bfloat16"), inputs)
+    with torch.no_grad():
+        beh = model(*inputs, batch_size=B)["behavior"].cpu().numpy()
+    sd = {k: v.detach().cpu() for k, v in model.state_dict().items()}
+    ref = O.forward(sd, O.CORTEX_S_SHAPE, *arrs, batch_size=B).numpy()
+    assert beh.shape == (B, 2) and np.isfinite(beh).all()
+    assert np.abs(beh - ref).max() <= 2e-2, np.abs(beh - ref).max()
+
+
 def test_cortex_m_int8_bf16_forward_vs_oracle():
     """CORTEX_M (D=768, 12 heads, 384 latents) runs the general kernels wherever the fused ones
     do not apply (384 latents, 12 heads x 2 behaviour queries, N=768 rows): INT8, bf16 compute,
