@@ -87,6 +87,13 @@ _SIGNATURES = {
          _ptr]),
     "cortex_gather_event_pages": (_int, [_ptr, _i64, _i64, _ptr, _i64, _ptr, _i64, _i64, _ptr, _ptr]),
     "cortex_scatter_event_pages": (_int, [_ptr, _i64, _i64, _ptr, _i64, _ptr, _i64, _i64, _ptr, _ptr]),
+    "cortex_splitk_workspace_bytes": (_i64, [_i64, _i64, _i64]),
+    "cortex_linear_residual_splitk": (
+        _int, [_i64, _i64, _i64, _ptr, _i64, _ptr, _i64, _ptr, _ptr, _ptr, _i64, _i64, _ptr, _i64, _i64, _ptr, _i64,
+               _ptr]),
+    "cortex_linear_residual_ln_splitk": (
+        _int, [_i64, _i64, _i64, _ptr, _i64, _ptr, _i64, _ptr, _ptr, _ptr, _i64, _i64, _ptr, _i64, _ptr, _ptr, _f32,
+               _ptr, _i64, _i64, _ptr, _i64, _ptr]),
     "cortex_page_table_create": (_int, [_i64, _ptr]),
     "cortex_page_table_destroy": (_int, [_ptr]),
     "cortex_page_table_write": (_int, [_ptr, _i64, _ptr, _ptr, _ptr, _ptr]),

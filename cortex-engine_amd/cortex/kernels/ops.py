@@ -16,6 +16,24 @@ import torch
 from cortex import _native as nat
 
 NORM = {None: 0, "none": 0, "layer": 1, "rms": 2}
+_CU_COUNT: dict[int, int] = {}
+
+
+def splitk_splits(M: int, N: int, K: int, device: torch.device) -> int:
+    """K slabs for a residual linear with few rows (0: no split).  Split when the 128 x 128
+    output tiles fill at most a quarter of the CUs: the largest of 2, 4, 8 slabs that keeps
+    tiles x slabs within one workgroup per CU and K a multiple of 64 per slab."""
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    cus = _CU_COUNT.get(idx)
+    if cus is None:
+        cus = _CU_COUNT[idx] = torch.cuda.get_device_properties(idx).multi_processor_count
+    tiles = math.ceil(M / 128) * math.ceil(N / 128)
+    if M < 1 or tiles * 4 > cus or K < 128:
+        return 0
+    s = 1
+    while s < 8 and tiles * s * 2 <= cus and K % (64 * s * 2) == 0:
+        s *= 2
+    return s if s > 1 else 0
 ACT = {None: 0, "none": 0, "gelu": 1}
 
 
@@ -221,6 +239,14 @@ def linear_residual_ln(x: torch.Tensor, weight: torch.Tensor, weight_scale=None,
         out = torch.empty((M, N), dtype=torch.float32, device=dev)
     xn = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
     g, b, eps = ln
+    splits = splitk_splits(M, N, K, dev)
+    if splits:  # few rows: K split across workgroups, slabs summed in order, then the LayerNorm
+        ws_t = torch.empty(nat.load().cortex_splitk_workspace_bytes(M, N, splits), dtype=torch.uint8, device=dev)
+        nat.call("cortex_linear_residual_ln_splitk", M, N, K, nat.ptr(x), x.stride(0), nat.ptr(weight),
+                 weight.stride(0), nat.ptr(weight_scale), nat.ptr(bias), nat.ptr(residual), residual.stride(0),
+                 int(res_rows), nat.ptr(out), out.stride(0), nat.ptr(g), nat.ptr(b), float(eps), nat.ptr(xn),
+                 xn.stride(0), splits, nat.ptr(ws_t), ws_t.numel(), nat.stream_of(dev))
+        return out, xn
     nat.call("cortex_linear_residual_ln", M, N, K, nat.ptr(x), x.stride(0), nat.ptr(weight), weight.stride(0),
              nat.ptr(weight_scale), nat.ptr(bias), nat.ptr(residual), residual.stride(0), int(res_rows),
              nat.ptr(out), out.stride(0), nat.ptr(g), nat.ptr(b), float(eps), nat.ptr(xn), xn.stride(0),
@@ -326,6 +352,20 @@ def norm_linear(x: torch.Tensor, *, weight: torch.Tensor | None = None, weight_i
         res2 = residual.reshape(-1, N) if residual.dim() != 2 else residual
         res2 = _row_major_2d(res2)
     ld_w = w2.stride(0) if w2.shape[0] > 1 else w2.shape[1]
+    if (res2 is not None and not nrm and not ACT[act] and layout == 0 and weight is not None
+            and w2.dtype == torch.bfloat16 and x2.dtype == torch.bfloat16 and res2.dtype == torch.float32
+            and out2.dtype == torch.float32 and (bias is None or bias.dtype == torch.float32)
+            and all(t is None or t.data_ptr() % 16 == 0 for t in (x2, w2, ws, bias, res2, out2))
+            and (M == 1 or (x2.stride(0) % 8 == 0 and out2.stride(0) % 4 == 0))
+            and (w2.shape[0] == 1 or w2.stride(0) % 8 == 0) and (res2.shape[0] == 1 or res2.stride(0) % 4 == 0)):
+        splits = splitk_splits(M, N, K, dev)
+        if splits:  # few rows: K split across workgroups, slabs summed in order
+            ws_t = torch.empty(nat.load().cortex_splitk_workspace_bytes(M, N, splits), dtype=torch.uint8, device=dev)
+            nat.call("cortex_linear_residual_splitk", M, N, K, nat.ptr(x2), x2.stride(0) if M > 1 else K,
+                     nat.ptr(w2), ld_w, nat.ptr(ws), nat.ptr(bias), nat.ptr(res2),
+                     res2.stride(0) if res2.shape[0] > 1 else N, int(res_rows), nat.ptr(out2),
+                     out2.stride(0) if M > 1 else N, splits, nat.ptr(ws_t), ws_t.numel(), nat.stream_of(dev))
+            return out
     gdt = nat.code(gamma.dtype) if gamma is not None else nat.F32
     nat.call("cortex_norm_linear", M, N, K, nat.code(x2.dtype), nat.ptr(x2), x2.stride(0) if M > 1 else K, nrm,
              nat.ptr(stats), nat.ptr(gamma), nat.ptr(beta), gdt, nat.code(compute_dtype),

@@ -85,6 +85,35 @@ __device__ __forceinline__ int xcd_affine(int id, int total) {
   return (total & 7) ? id : (id & 7) * (total >> 3) + (id >> 3);
 }
 
+// One LayerNorm pass over the EPL values a lane holds of one row spread over a wavefront:
+// element (j / 4) * 256 + 4 lane + j % 4 in v[j]; two passes (mean, then squared deviations).
+template <int EPL>
+__device__ __forceinline__ void ln_regs(float (&v)[EPL], float inv_k, float eps, const float* __restrict__ gamma,
+                                        const float* __restrict__ beta, int lane) {
+  float s = 0.0f;
+#pragma unroll
+  for (int j = 0; j < EPL; ++j) s += v[j];
+  const float mean = wave_sum(s) * inv_k;
+  float ss = 0.0f;
+#pragma unroll
+  for (int j = 0; j < EPL; ++j) {
+    const float d = v[j] - mean;
+    ss += d * d;
+  }
+  const float rstd = 1.0f / sqrtf(wave_sum(ss) * inv_k + eps);
+#pragma unroll
+  for (int j = 0; j < EPL; j += 4) {
+    // element k = (j / 4) * 256 + lane * 4 + (j % 4)
+    const int k = (j >> 2) * 256 + lane * 4;
+    const float4 gm = gamma ? *reinterpret_cast<const float4*>(gamma + k) : make_float4(1.f, 1.f, 1.f, 1.f);
+    const float4 bt = beta ? *reinterpret_cast<const float4*>(beta + k) : make_float4(0.f, 0.f, 0.f, 0.f);
+    v[j] = (v[j] - mean) * rstd * gm.x + bt.x;
+    v[j + 1] = (v[j + 1] - mean) * rstd * gm.y + bt.y;
+    v[j + 2] = (v[j + 2] - mean) * rstd * gm.z + bt.z;
+    v[j + 3] = (v[j + 3] - mean) * rstd * gm.w + bt.w;
+  }
+}
+
 __host__ __device__ __forceinline__ int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 // erf-form GELU, as torch.nn.GELU() with approximate='none': 0.5 x (1 + erf(x / sqrt 2)).

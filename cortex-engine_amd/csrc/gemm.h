@@ -41,6 +41,12 @@ int try_gemm_fast(const GemmArgs& g, int x_dtype, int w_dtype, int w_layout, int
 // bf16 x bf16 path with a register epilogue (gemm_bf16.hip), same return convention.
 int try_gemm_bf16(const GemmArgs& g, int x_dtype, int w_dtype, int w_layout, int compute, hipStream_t stream);
 
+// K split over gridDim.z = splits workgroup slabs (gemm_bf16.hip): slab z computes
+// (x[:, zK:(z+1)K] . w[:, zK:(z+1)K]^T) * w_scale into g.out + z * M * ld_out (fp32), where
+// K = g.K is the per-slab depth (a multiple of 64) and g.x / g.w are the full rows.  No
+// bias, activation or residual.  Returns 1 when launched, 0 when the grid is too large.
+int split_k_partials(const GemmArgs& g, int splits, hipStream_t stream);
+
 // Pipelined bf16 x int8 path (gemm_pipe.hip), same return convention.
 int try_gemm_pipe(const GemmArgs& g, int x_dtype, int w_dtype, int w_layout, int compute, hipStream_t stream);
 

@@ -85,8 +85,10 @@ __global__ __launch_bounds__(TL::THREADS) void gemm_bf16_kernel(GemmArgs g) {
   const int m0 = (id / nbx) * BM, n0 = (id % nbx) * BN;
   unsigned char* const ring = smem + kg * TL::RING;
   const int M = (int)g.M, N = (int)g.N, K = (int)g.K;
-  const bf16* __restrict__ A = reinterpret_cast<const bf16*>(g.x);
-  const bf16* __restrict__ W = reinterpret_cast<const bf16*>(g.w);
+  // K split across workgroups (split_k_partials): slice z of K into output slab z
+  const int kz = blockIdx.z;
+  const bf16* __restrict__ A = reinterpret_cast<const bf16*>(g.x) + (int64_t)kz * K;
+  const bf16* __restrict__ W = reinterpret_cast<const bf16*>(g.w) + (int64_t)kz * K;
 
   // Global source of each of this lane's transfers (K offset added per step).  Lane i
   // of a transfer writes LDS bytes [16 i, 16 i + 16) of its 1 KiB block: row i / 8,
@@ -245,7 +247,7 @@ __global__ __launch_bounds__(TL::THREADS) void gemm_bf16_kernel(GemmArgs g) {
   //   IL:  tiles 2p, 2p+1 -> n0 + wcol + 32 p + 8 g4 .. +7
   //   !IL: tile j         -> n0 + wcol + 16 j + 4 g4 .. +3
   const float* bias = reinterpret_cast<const float*>(g.bias);
-  TOUT* out = reinterpret_cast<TOUT*>(g.out);
+  TOUT* out = reinterpret_cast<TOUT*>(g.out) + (int64_t)kz * M * g.ld_out;
   constexpr int NV = IL ? 8 : 4;           // consecutive columns per lane and group
   constexpr int NG = IL ? TN / 2 : TN;     // column groups per lane
   // Every scale and bias load first, then one wait: a wait left to the compiler would
@@ -400,6 +402,16 @@ int dispatch_res(const GemmArgs& g, int t, hipStream_t stream) {
 bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
 }  // namespace
+
+int split_k_partials(const GemmArgs& g, int splits, hipStream_t stream) {
+  using TL = B128x128s2;
+  const int64_t gy = cdiv(g.M, TL::BM), gx = cdiv(g.N, TL::BN);
+  if (gy > 65535 || gx * gy * splits > 0x7fffffffLL || splits > 65535) return 0;
+  hipLaunchKernelGGL((gemm_bf16_kernel<TL, ACT_NONE, false, float>), dim3((unsigned)gx, (unsigned)gy, (unsigned)splits),
+                     dim3(TL::THREADS), 0, stream, g);
+  CORTEX_CHECK_LAUNCH("gemm_bf16_kernel (K split)");
+  return 1;
+}
 
 int try_gemm_bf16(const GemmArgs& g, int x_dtype, int w_dtype, int w_layout, int compute, hipStream_t stream) {
   if (compute != DT_BF16 || w_layout != 0 || x_dtype != DT_BF16 || w_dtype != DT_BF16) return 0;

@@ -19,34 +19,6 @@ __global__ __launch_bounds__(256) void convert_kernel(const TI* __restrict__ in,
     out[i] = from_f32<TO>(to_f32(in[i]));
 }
 
-// One LayerNorm pass over the EPL values a lane holds (row spread over the wave).
-template <int EPL>
-__device__ __forceinline__ void ln_regs(float (&v)[EPL], float inv_k, float eps, const float* __restrict__ gamma,
-                                        const float* __restrict__ beta, int lane) {
-  float s = 0.0f;
-#pragma unroll
-  for (int j = 0; j < EPL; ++j) s += v[j];
-  const float mean = wave_sum(s) * inv_k;
-  float ss = 0.0f;
-#pragma unroll
-  for (int j = 0; j < EPL; ++j) {
-    const float d = v[j] - mean;
-    ss += d * d;
-  }
-  const float rstd = 1.0f / sqrtf(wave_sum(ss) * inv_k + eps);
-#pragma unroll
-  for (int j = 0; j < EPL; j += 4) {
-    // element k = (j / 4) * 256 + lane * 4 + (j % 4)
-    const int k = (j >> 2) * 256 + lane * 4;
-    const float4 gm = gamma ? *reinterpret_cast<const float4*>(gamma + k) : make_float4(1.f, 1.f, 1.f, 1.f);
-    const float4 bt = beta ? *reinterpret_cast<const float4*>(beta + k) : make_float4(0.f, 0.f, 0.f, 0.f);
-    v[j] = (v[j] - mean) * rstd * gm.x + bt.x;
-    v[j + 1] = (v[j + 1] - mean) * rstd * gm.y + bt.y;
-    v[j + 2] = (v[j + 2] - mean) * rstd * gm.z + bt.z;
-    v[j + 3] = (v[j + 3] - mean) * rstd * gm.w + bt.w;
-  }
-}
-
 struct TokLnArgs {
   const float* neuron;
   int64_t n_neuron, ld_neuron;

@@ -262,6 +262,27 @@ int cortex_scatter_event_pages(const int64_t* src, int64_t field_stride, int64_t
                                int64_t n_items, int64_t* pool, int64_t num_pages, int64_t page_events, int32_t* err,
                                hipStream_t stream);
 
+/* Residual linears for small row counts, K split across workgroups: the same results
+ * as cortex_norm_linear with a residual (QuantizedLinear.forward plus the residual
+ * add, cortex/quantization/calibrate.py:225-228, cortex/models/perceiver.py:121-125)
+ * and as cortex_linear_residual_ln, up to the order of the fp32 sums.  K is cut into
+ * `splits` slabs (K a multiple of 64 * splits); each slab's scaled partial product
+ * goes to its fp32 (M, N) slab of the workspace, and the slabs are then summed in slab
+ * order with bias and residual (row m % res_rows; out may be res).  The LayerNorm
+ * variant also writes LN(out) * gamma + beta as bf16 rows (N in {256, 512, 768, 1024}).
+ * x (M, K) and w (N, K) are bf16 rows; the workspace holds
+ * cortex_splitk_workspace_bytes(M, N, splits) bytes, 16-byte aligned. */
+int64_t cortex_splitk_workspace_bytes(int64_t M, int64_t N, int64_t splits);
+int cortex_linear_residual_splitk(int64_t M, int64_t N, int64_t K, const void* x, int64_t ld_x, const void* w,
+                                  int64_t ld_w, const float* w_scale, const float* bias, const float* res,
+                                  int64_t ld_res, int64_t res_rows, float* out, int64_t ld_out, int64_t splits,
+                                  void* workspace, int64_t workspace_bytes, hipStream_t stream);
+int cortex_linear_residual_ln_splitk(int64_t M, int64_t N, int64_t K, const void* x, int64_t ld_x, const void* w,
+                                     int64_t ld_w, const float* w_scale, const float* bias, const float* res,
+                                     int64_t ld_res, int64_t res_rows, float* out, int64_t ld_out,
+                                     const float* gamma, const float* beta, float eps, void* xn, int64_t ld_xn,
+                                     int64_t splits, void* workspace, int64_t workspace_bytes, hipStream_t stream);
+
 /* Host page table of that cache (no device work; not thread-safe, one caller per
  * table).  Replaces the Python bookkeeping of StreamingKVCache with the same policy
  * (cortex/cache/streaming.py:133-233): a lookup of a present key touches its page

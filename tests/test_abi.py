@@ -58,6 +58,10 @@ def test_invalid_arguments_return_status_and_message():
     assert lib.cortex_version() == 1
     rc = lib.cortex_quantize_int8(None, -1, 4, 4, None, None, None, 4, None)
     assert rc == -1 and b"negative shape" in lib.cortex_last_error()
+    # a K split that does not divide K (no pointer is dereferenced before the check)
+    rc = lib.cortex_linear_residual_splitk(256, 512, 2048, 16, 2048, 16, 2048, None, None, 16, 512, 0, 16, 512, 3,
+                                           16, 1 << 30, None)
+    assert rc == -1 and b"multiple of 64 * splits" in lib.cortex_last_error()
     rc = lib.cortex_attention(1, 1, 1, 1, 1, 0, *([None, 0, 0, 0] * 3), None, None, None, 0, None, 0, 0, 0, 0, 0,
                               ctypes.c_float(1.0), None, 0, 0, 0, None)
     assert rc == -1 and b"head dim" in lib.cortex_last_error()

@@ -261,3 +261,43 @@ def test_linear_residual_ln(M, N, K, res_rows, inplace):
     ln = F.layer_norm(xc, (N,), gam, bet, 1e-5)
     err = (xn.cpu().float() - ln).abs()
     assert (err <= _bf16_ulp(ln) + 1e-5 * float(ln.abs().max())).all(), float(err.max())
+
+
+@pytest.mark.parametrize("M,N,K,splits,res_rows", [(256, 512, 2048, 8, 0), (256, 512, 512, 8, 0), (1, 512, 2048, 4, 0),
+                                                  (300, 512, 1024, 2, 0), (512, 256, 512, 4, 256), (2048, 512, 2048, 4, 0)])
+@pytest.mark.parametrize("ln", [False, True])
+def test_split_k_residual_linears(M, N, K, splits, res_rows, ln):
+    """K split across workgroups through the C-ABI at explicit slab counts (ragged M,
+    one row, broadcast residual, in place): the fp32 output within 1e-5 of a float64
+    contraction; with the LayerNorm, the bf16 rows within one bf16 rounding of the fp32
+    LayerNorm of the kernel's own output."""
+    from cortex import _native as nat
+    from cortex.kernels import ops
+
+    a, q, s = _operands(M, N, K, seed=M + K + splits)
+    g = torch.Generator().manual_seed(9)
+    bias = 0.1 * torch.randn(N, generator=g)
+    res = torch.randn(res_rows or M, N, generator=g) * 2.0 + 0.3
+    gam, bet = 1 + 0.2 * torch.randn(N, generator=g), 0.2 * torch.randn(N, generator=g)
+    ad, w_img, sd, bd = a.to(DEV), ops.convert(q.to(DEV), torch.bfloat16), s.to(DEV), bias.to(DEV)
+    res_d = res.to(DEV)
+    out = res_d if not res_rows else torch.empty(M, N, device=DEV)
+    ws = torch.empty(nat.load().cortex_splitk_workspace_bytes(M, N, splits), dtype=torch.uint8, device=DEV)
+    stream = nat.stream_of(torch.device(DEV))
+    if ln:
+        gd, bt = gam.to(DEV), bet.to(DEV)
+        xn = torch.empty(M, N, dtype=torch.bfloat16, device=DEV)
+        nat.call("cortex_linear_residual_ln_splitk", M, N, K, nat.ptr(ad), K, nat.ptr(w_img), K, nat.ptr(sd),
+                 nat.ptr(bd), nat.ptr(res_d), N, res_rows, nat.ptr(out), N, nat.ptr(gd), nat.ptr(bt), 1e-5,
+                 nat.ptr(xn), N, splits, nat.ptr(ws), ws.numel(), stream)
+    else:
+        nat.call("cortex_linear_residual_splitk", M, N, K, nat.ptr(ad), K, nat.ptr(w_img), K, nat.ptr(sd),
+                 nat.ptr(bd), nat.ptr(res_d), N, res_rows, nat.ptr(out), N, splits, nat.ptr(ws), ws.numel(), stream)
+    ref = _ref(a, q, s, bias=bias, res=res, res_rows=res_rows)
+    xc = out.cpu()
+    assert (xc.double() - ref).abs().max() <= 1e-5 * ref.abs().max()
+    if ln:
+        lnr = F.layer_norm(xc, (N,), gam, bet, 1e-5)
+        err = (xn.cpu().float() - lnr).abs()
+        assert (err <= _bf16_ulp(lnr) + 1e-5 * float(lnr.abs().max())).all(), float(err.max())
+
