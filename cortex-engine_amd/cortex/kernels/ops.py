@@ -194,6 +194,33 @@ def layer_norm(x: torch.Tensor, weight, bias, eps: float, out_dtype=None, out=No
     return out
 
 
+_LN_ROWS_K = (256, 512, 768, 1024)
+
+
+def norm_rows(x: torch.Tensor, norm: str, gamma=None, beta=None, eps: float = 1e-6) -> torch.Tensor:
+    """RMSNorm (``norm='rms'``) or LayerNorm (``'layer'``) of the rows of ``x`` (fp32 or
+    bf16, K in {256, 512, 768, 1024}) as bf16 rows (``cortex_norm_rows``)."""
+    dev = nat.require_gpu(x, gamma, beta, what="norm_rows")
+    x2 = _row_major_2d(x.reshape(-1, x.shape[-1]))
+    M, K = x2.shape
+    out = torch.empty((M, K), dtype=torch.bfloat16, device=dev)
+    gdt = nat.code(gamma.dtype) if gamma is not None else (nat.code(beta.dtype) if beta is not None else nat.F32)
+    nat.call("cortex_norm_rows", M, K, nat.code(x2.dtype), nat.ptr(x2), x2.stride(0) if M > 1 else K, NORM[norm],
+             nat.ptr(gamma), nat.ptr(beta), gdt, float(eps), nat.ptr(out), K, nat.stream_of(dev))
+    return out
+
+
+def transpose_bf16(w: torch.Tensor) -> torch.Tensor:
+    """``w.T`` of a bf16 (R, C) matrix as contiguous (C, R) rows (``cortex_transpose_bf16``)."""
+    dev = nat.require_gpu(w, what="transpose_bf16")
+    w2 = _row_major_2d(w)
+    R, C = w2.shape
+    out = torch.empty((C, R), dtype=torch.bfloat16, device=dev)
+    nat.call("cortex_transpose_bf16", R, C, nat.ptr(w2), w2.stride(0) if R > 1 else C, nat.ptr(out), R,
+             nat.stream_of(dev))
+    return out
+
+
 def ln_rows(x: torch.Tensor, ln1, ln2=None, out_bf16: bool = True, out_f32: bool = False):
     """LayerNorm over rows of fp32 ``x`` (K in {256, 512, 768, 1024}); ``ln1``/``ln2``
     are ``(weight, bias, eps)`` triples (``ln2`` applied after ``ln1`` when given).
@@ -345,6 +372,24 @@ def norm_linear(x: torch.Tensor, *, weight: torch.Tensor | None = None, weight_i
     if out2.data_ptr() != out.data_ptr() or (M > 1 and out2.stride(0) < N) or out2.stride(-1) != 1:
         raise ValueError("out must be row-major contiguous over its last dim")
     nrm = NORM[norm]
+    if (nrm and stats is None and compute_dtype == torch.bfloat16 and K in _LN_ROWS_K
+            and x2.dtype in (torch.bfloat16, torch.float32) and x2.data_ptr() % 16 == 0
+            and (M == 1 or x2.stride(0) % 4 == 0)
+            and (gamma is None or beta is None or gamma.dtype == beta.dtype)
+            and all(p is None or (p.dtype in (torch.float32, torch.bfloat16) and p.is_contiguous())
+                    for p in (gamma, beta))):
+        # the normalised rows once as bf16 rows (the MFMA operand is that rounding either way),
+        # then the bf16 GEMM streaming (N, K) weight rows
+        xn = norm_rows(x2, norm, gamma, beta, eps)
+        if weight_int8 is not None:
+            kw = {"weight": convert(w2, torch.bfloat16), "weight_scale": ws}
+        elif layout == 1:
+            kw = {"weight": transpose_bf16(w2.to(torch.bfloat16) if w2.dtype != torch.bfloat16 else w2),
+                  "weight_scale": ws}
+        else:
+            kw = {"weight": w2, "weight_scale": ws}
+        return norm_linear(xn, **kw, bias=bias, act=act, residual=residual, res_rows=res_rows,
+                           out_dtype=out_dtype, compute_dtype=compute_dtype, out=out)
     if nrm and stats is None:
         stats = row_stats(x2, "layer" if nrm == 1 else "rms", eps)
     res2 = None

@@ -83,6 +83,97 @@ __global__ __launch_bounds__(256) void ln_rows_kernel(const float* __restrict__ 
 }
 
 
+// Normalised rows as the bf16 operand of a linear (the norm half of the fused
+// norm + linear, reference cortex/kernels/fused_rmsnorm.py:100-106, and LayerNorm):
+//   RMS:   y = (x / sqrt(mean(x^2) + eps)) * gamma
+//   layer: y = (x - mean) * (1 / sqrt(var + eps)) * gamma + beta
+// in fp32 from bf16 or fp32 x, gamma / beta in fp32 or bf16 (gdt), rounded once to bf16 --
+// the same arithmetic as the norm prologue of gemm_kernel.  One wavefront per row,
+// lane l holding elements (j / 4) * 256 + 4 l + j % 4.
+template <class TX, int EPL>
+__global__ __launch_bounds__(256) void norm_rows_kernel(const TX* __restrict__ x, int64_t M, int64_t ld_x, int norm,
+                                                        const void* gamma, const void* beta, int gdt, float eps,
+                                                        bf16* __restrict__ out, int64_t ld_out) {
+  constexpr int K = 64 * EPL;
+  const int lane = threadIdx.x & 63;
+  const int64_t m = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  if (m >= M) return;
+  const TX* row = x + m * ld_x;
+  float v[EPL];
+#pragma unroll
+  for (int j = 0; j < EPL; j += 4) {
+    const int k = (j >> 2) * 256 + lane * 4;
+    if constexpr (sizeof(TX) == 4) {
+      const float4 q = *reinterpret_cast<const float4*>(row + k);
+      v[j] = q.x; v[j + 1] = q.y; v[j + 2] = q.z; v[j + 3] = q.w;
+    } else {
+      const bf16x4 q = *reinterpret_cast<const bf16x4*>(row + k);
+      v[j] = (float)q[0]; v[j + 1] = (float)q[1]; v[j + 2] = (float)q[2]; v[j + 3] = (float)q[3];
+    }
+  }
+  float g[EPL], b[EPL];
+#pragma unroll
+  for (int j = 0; j < EPL; ++j) {
+    const int k = (j >> 2) * 256 + lane * 4 + (j & 3);
+    g[j] = !gamma ? 1.0f : gdt == DT_BF16 ? (float)reinterpret_cast<const bf16*>(gamma)[k]
+                                          : reinterpret_cast<const float*>(gamma)[k];
+    b[j] = !beta ? 0.0f : gdt == DT_BF16 ? (float)reinterpret_cast<const bf16*>(beta)[k]
+                                         : reinterpret_cast<const float*>(beta)[k];
+  }
+  const float inv_k = 1.0f / (float)K;
+  if (norm == 2) {
+    float ss = 0.0f;
+#pragma unroll
+    for (int j = 0; j < EPL; ++j) ss += v[j] * v[j];
+    const float rms = sqrtf(wave_sum(ss) * inv_k + eps);
+#pragma unroll
+    for (int j = 0; j < EPL; ++j) v[j] = (v[j] / rms) * g[j];
+  } else {
+    float s = 0.0f;
+#pragma unroll
+    for (int j = 0; j < EPL; ++j) s += v[j];
+    const float mean = wave_sum(s) * inv_k;
+    float ss = 0.0f;
+#pragma unroll
+    for (int j = 0; j < EPL; ++j) {
+      const float d = v[j] - mean;
+      ss += d * d;
+    }
+    const float rstd = 1.0f / sqrtf(wave_sum(ss) * inv_k + eps);
+#pragma unroll
+    for (int j = 0; j < EPL; ++j) v[j] = (v[j] - mean) * rstd * g[j] + b[j];
+  }
+#pragma unroll
+  for (int j = 0; j < EPL; j += 4) {
+    bf16x4 o;
+    o[0] = (bf16)v[j];
+    o[1] = (bf16)v[j + 1];
+    o[2] = (bf16)v[j + 2];
+    o[3] = (bf16)v[j + 3];
+    *reinterpret_cast<bf16x4*>(out + m * ld_out + (j >> 2) * 256 + lane * 4) = o;
+  }
+}
+
+// out[c, r] = in[r, c] for a (R, C) bf16 matrix, through 64 x 64 LDS tiles (the
+// (K, N) weight of rms_norm_linear into the (N, K) rows the GEMM streams).  Exact copies.
+__global__ __launch_bounds__(256) void transpose_bf16_kernel(const bf16* __restrict__ in, int64_t R, int64_t C,
+                                                             int64_t ld_in, bf16* __restrict__ out, int64_t ld_out) {
+  __shared__ bf16 tile[64][66];
+  const int64_t r0 = (int64_t)blockIdx.y * 64, c0 = (int64_t)blockIdx.x * 64;
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;  // 64 x 4 threads
+#pragma unroll
+  for (int i = 0; i < 64; i += 4) {
+    const int64_t r = r0 + ty + i, c = c0 + tx;
+    if (r < R && c < C) tile[ty + i][tx] = in[r * ld_in + c];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < 64; i += 4) {
+    const int64_t c = c0 + ty + i, r = r0 + tx;
+    if (r < R && c < C) out[c * ld_out + r] = tile[tx][ty + i];
+  }
+}
+
 // Spike tokens straight to the LayerNorm'd bf16 operand of the cross-attention kv
 // projection: row r of the CSR token matrix is
 //   x = (neuron_emb[nid[e]] + time_emb[tb[e]]) + value_emb[val[e]]   (fp32, left to right)
@@ -284,6 +375,53 @@ int cortex_tokenize_ln(int64_t D, const float* neuron_emb, int64_t n_neuron, int
     default: hipLaunchKernelGGL(tokenize_ln_kernel<16>, grid, dim3(256), 0, stream, a); break;
   }
   CORTEX_CHECK_LAUNCH("tokenize_ln_kernel");
+  return OK;
+}
+
+int cortex_norm_rows(int64_t M, int64_t K, int x_dtype, const void* x, int64_t ld_x, int norm, const void* gamma,
+                     const void* beta, int gamma_dtype, float eps, void* out, int64_t ld_out, hipStream_t stream) {
+  CORTEX_CHECK_ARG(M >= 0, "cortex_norm_rows: negative M");
+  if (M == 0) return OK;
+  CORTEX_CHECK_ARG(norm == 1 || norm == 2, "cortex_norm_rows: norm must be 1 (layer) or 2 (rms)");
+  CORTEX_CHECK_ARG(K == 256 || K == 512 || K == 768 || K == 1024, "cortex_norm_rows: K=%lld not one of 256, 512, 768, 1024",
+                   (long long)K);
+  CORTEX_CHECK_ARG(x_dtype == DT_F32 || x_dtype == DT_BF16, "cortex_norm_rows: x must be fp32 or bf16");
+  CORTEX_CHECK_ARG(gamma_dtype == DT_F32 || gamma_dtype == DT_BF16, "cortex_norm_rows: gamma must be fp32 or bf16");
+  CORTEX_CHECK_ARG(x && out && ld_x >= K && ld_out >= K, "cortex_norm_rows: null pointer or short rows");
+  const int xa = x_dtype == DT_F32 ? 15 : 7;
+  CORTEX_CHECK_ARG(((uintptr_t)x & xa) == 0 && ld_x % 4 == 0 && ((uintptr_t)out & 7) == 0 && ld_out % 4 == 0,
+                   "cortex_norm_rows: x and out rows must be aligned to 4 elements");
+  const dim3 grid((unsigned)cdiv(M, 4));
+#define CORTEX_NR(TX, EPL)                                                                                      \
+  hipLaunchKernelGGL((norm_rows_kernel<TX, EPL>), grid, dim3(256), 0, stream, (const TX*)x, M, ld_x, norm, gamma, \
+                     beta, gamma_dtype, eps, (bf16*)out, ld_out)
+#define CORTEX_NR_K(TX)              \
+  switch (K) {                       \
+    case 256: CORTEX_NR(TX, 4); break;  \
+    case 512: CORTEX_NR(TX, 8); break;  \
+    case 768: CORTEX_NR(TX, 12); break; \
+    default: CORTEX_NR(TX, 16); break;  \
+  }
+  if (x_dtype == DT_F32) {
+    CORTEX_NR_K(float)
+  } else {
+    CORTEX_NR_K(bf16)
+  }
+#undef CORTEX_NR_K
+#undef CORTEX_NR
+  CORTEX_CHECK_LAUNCH("norm_rows_kernel");
+  return OK;
+}
+
+int cortex_transpose_bf16(int64_t R, int64_t C, const void* in, int64_t ld_in, void* out, int64_t ld_out,
+                          hipStream_t stream) {
+  CORTEX_CHECK_ARG(R >= 0 && C >= 0, "cortex_transpose_bf16: negative size");
+  if (R == 0 || C == 0) return OK;
+  CORTEX_CHECK_ARG(in && out && ld_in >= C && ld_out >= R, "cortex_transpose_bf16: null pointer or short rows");
+  CORTEX_CHECK_ARG(cdiv(R, 64) <= 65535 && cdiv(C, 64) <= 0x7fffffffLL, "cortex_transpose_bf16: too large");
+  hipLaunchKernelGGL(transpose_bf16_kernel, dim3((unsigned)cdiv(C, 64), (unsigned)cdiv(R, 64)), dim3(256), 0, stream,
+                     (const bf16*)in, R, C, ld_in, (bf16*)out, ld_out);
+  CORTEX_CHECK_LAUNCH("transpose_bf16_kernel");
   return OK;
 }
 

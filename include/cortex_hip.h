@@ -116,6 +116,18 @@ int cortex_layer_norm(int64_t M, int64_t K, int x_dtype, const void* x, int64_t 
                       const void* beta, int gamma_dtype, float eps, int out_dtype, void* out, int64_t ld_out,
                       hipStream_t stream);
 
+/* ---- a6: the norm half of a fused norm + linear, as bf16 rows --------------
+ * The RMSNorm of rms_norm_linear (cortex/kernels/fused_rmsnorm.py:100-106:
+ * ((x_f32 / sqrt(mean(x^2) + eps)) * gamma).to(bf16)) or a LayerNorm (norm = 1), for
+ * the bf16 operand of the linear that follows; x fp32 or bf16, gamma/beta fp32 or bf16
+ * (gamma_dtype), K in {256, 512, 768, 1024}.  The linear then runs on the bf16 GEMM. */
+int cortex_norm_rows(int64_t M, int64_t K, int x_dtype, const void* x, int64_t ld_x, int norm, const void* gamma,
+                     const void* beta, int gamma_dtype, float eps, void* out, int64_t ld_out, hipStream_t stream);
+/* out[c, r] = in[r, c] for bf16 (R, C): rms_norm_linear's (K, N) weight
+ * (fused_rmsnorm.py:239-245) as the (N, K) rows the GEMM streams.  Exact copies. */
+int cortex_transpose_bf16(int64_t R, int64_t C, const void* in, int64_t ld_in, void* out, int64_t ld_out,
+                          hipStream_t stream);
+
 /* ---- a5/a8: LayerNorm rows to bf16 ----------------------------------------
  * Replaces nn.LayerNorm feeding a bf16 linear (cortex/models/perceiver.py:67-68,
  * 113,125,158; cortex/models/cortex.py:37), K in {256, 512, 768, 1024}:

@@ -131,3 +131,46 @@ def test_layer_norm_kernel_and_row_stats():
     torch.testing.assert_close(y.cpu(), F.layer_norm(x, (512,), w, b, 1e-5), rtol=1e-5, atol=2e-5)
     st = ops.row_stats(x.to(DEV), "rms", 1e-6).cpu()
     torch.testing.assert_close(st[:, 1], torch.sqrt(x.pow(2).mean(-1) + 1e-6), rtol=1e-6, atol=1e-6)
+
+
+@pytest.mark.parametrize("K", [256, 512, 768, 1024])
+@pytest.mark.parametrize("xdt", [torch.bfloat16, torch.float32])
+def test_norm_rows_vs_torch(K, xdt):
+    """The norm half of the bf16 fused path: RMS/LayerNorm rows rounded once to bf16.
+
+    Against torch fp32 on the CPU: at most one bf16 step apart (the fp32 sums differ
+    only in order, so a rounding boundary can fall either way)."""
+    from cortex.kernels import ops
+
+    torch.manual_seed(K)
+    x = (torch.randn(517, K) * 2 + 0.3).to(xdt)
+    g, b = 1 + 0.1 * torch.randn(K), 0.1 * torch.randn(K)
+    xf = x.float()
+    ref_rms = (xf / torch.sqrt(xf.pow(2).mean(-1, keepdim=True) + 1e-6)) * g
+    ref_ln = F.layer_norm(xf, (K,), g, b, 1e-5)
+    for norm, ref, kw in (("rms", ref_rms, {"gamma": g, "eps": 1e-6}),
+                          ("layer", ref_ln, {"gamma": g, "beta": b, "eps": 1e-5})):
+        kw = {k: (v.to(DEV) if torch.is_tensor(v) else v) for k, v in kw.items()}
+        y = ops.norm_rows(x.to(DEV), norm, **kw).cpu()
+        assert y.dtype == torch.bfloat16 and y.shape == (517, K)
+        step = ref.abs() * 2.0 ** -7 + 1e-5  # one bf16 step, plus fp32 cancellation near 0
+        assert bool(((y.float() - ref).abs() <= step).all()), norm
+        exact = float((y == ref.bfloat16()).float().mean())
+        assert exact > 0.99, (norm, exact)
+    # bf16 gamma, strided rows
+    xs = torch.randn(64, 2 * K).to(xdt)[:, :K]
+    y = ops.norm_rows(xs.to(DEV), "rms", g.bfloat16().to(DEV)).cpu()
+    xsf = xs.float()
+    ref = (xsf / torch.sqrt(xsf.pow(2).mean(-1, keepdim=True) + 1e-6)) * g.bfloat16().float()
+    assert bool(((y.float() - ref).abs() <= ref.abs() * 2.0 ** -7 + 1e-5).all())
+
+
+@pytest.mark.parametrize("R,C", [(512, 1536), (512, 2048), (70, 97), (1, 5), (64, 64), (129, 1)])
+def test_transpose_bf16_exact(R, C):
+    from cortex.kernels import ops
+
+    torch.manual_seed(R * 7 + C)
+    w = torch.randn(R, C).bfloat16()
+    t = ops.transpose_bf16(w.to(DEV)).cpu()
+    assert t.shape == (C, R) and t.is_contiguous()
+    assert torch.equal(t.view(torch.int16), w.T.contiguous().view(torch.int16))
