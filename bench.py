@@ -437,6 +437,30 @@ def serving_sweep(model, dev, batches=(1, 8, 32, 128, 256), reps: int = 20):
     return out
 
 
+def norm_linear_api(dev, M: int = 8192, K: int = 512, widths=(1536, 2048, 512)) -> dict:
+    """Standalone RMSNorm (eps 1e-6) + linear through the public API, bf16 rows (M, K): the
+    ``(K, N)`` bf16 weight of ``rms_norm_linear`` and the INT8 per-channel weight of
+    ``norm_linear_int8``; microseconds per call, graph-replayed."""
+    from cortex.kernels import ops
+    from cortex.kernels.fused_rmsnorm import norm_linear_int8, rms_norm_linear
+
+    g = torch.Generator(device="cpu").manual_seed(2)
+    x = torch.randn(M, K, generator=g).bfloat16().to(dev)
+    gam = (1 + 0.02 * torch.randn(K, generator=g)).to(dev)
+    out = {}
+    for n in widths:
+        w = (0.02 * torch.randn(n, K, generator=g)).to(dev)
+        q, sc = ops.quantize_int8(w)
+        wkn = w.t().contiguous().bfloat16()
+        t_kn = time_launches(lambda: rms_norm_linear(x, gam, wkn))
+        t_i8 = time_launches(lambda: norm_linear_int8(x, q, sc, norm="rms", gamma=gam, eps=1e-6,
+                                                      out_dtype=torch.bfloat16))
+        out[f"N{n}"] = {"rms_norm_linear_kn_bf16_us": round(t_kn * 1e6, 2),
+                        "norm_linear_int8_us": round(t_i8 * 1e6, 2),
+                        "int8_tflops": round(2 * M * n * K / t_i8 / 1e12, 1)}
+    return {"M": M, "K": K, **out}
+
+
 def cpu_baseline(model, budget_s: float = 12.0, b1_budget_s: float = 18.0):
     """The CPU oracle (fp32 activations, INT8 weights dequantised as the reference's QuantizedLinear)
     on the host cores, with the reference's protocol (profile_inference.py: 5 warmup + up to 30 timed
@@ -580,6 +604,8 @@ def main() -> int:
         log(f"bench: serve worker {extra['serve_worker']}")
         extra["streaming"] = streaming_windows(model, dev)
         log(f"bench: streaming {extra['streaming']}")
+        extra["norm_linear_api"] = norm_linear_api(dev)
+        log(f"bench: norm + linear API {extra['norm_linear_api']}")
     cpu = None
     if not (args.no_cpu_baseline or args.quick):
         log("bench: CPU baseline")
