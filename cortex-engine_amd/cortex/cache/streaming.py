@@ -15,9 +15,12 @@ value) for ``bins_per_page`` consecutive bins, stored once on the device; a deco
 window is assembled from its pages by one gather kernel that rewrites the bins
 relative to the window start, straight into the forward's input buffer.  Only the
 newest stride's events ever cross PCIe, as one pinned copy for all sessions' new
-pages plus one scatter launch (``write_many``).  Events inside a page keep their arrival
-order, so a window assembled from time-ordered pages equals the window built from
-scratch (events ordered by time bin, as ``np.nonzero`` over (T, N) counts gives).
+pages plus one scatter launch (``write_many``, or ``write_columns`` for pages already in
+columns).  A write's scatter waits on the device for the last gather, so a page reused by
+LRU eviction is never overwritten under a window still being assembled on another stream.
+Events inside a page keep their arrival order, so a window assembled from time-ordered
+pages equals the window built from scratch (events ordered by time bin, as
+``np.nonzero`` over (T, N) counts gives).
 
 Neither cache is thread-safe; like the reference, they are meant for the single
 inference executor thread.  Prometheus gauges of the reference are not kept.
@@ -232,6 +235,7 @@ class EventWindowCache:
         self._stage_host = torch.empty(1 << 15, dtype=torch.int64).pin_memory()
         self._stage_dev = torch.empty_like(self._stage_host, device=self.device)
         self._staged = torch.cuda.Event()
+        self._gathered: torch.cuda.Event | None = None  # the last gather, on its stream
 
     @property
     def hit_rate(self) -> float:
@@ -263,23 +267,49 @@ class EventWindowCache:
                 np.asarray(x.cpu() if torch.is_tensor(x) else x).reshape(-1) for x in (nid, tb, val))
         if not last:
             return
-        if len(last) > self.num_pages:
-            raise ValueError(f"{len(last)} pages in one write exceed the pool's {self.num_pages}")
+        for c in last.values():
+            if not (c[1].shape[0] == c[2].shape[0] == c[0].shape[0]):
+                raise ValueError("neuron_ids, time_bins and values must have the same length")
         keys = list(last)
-        starts = np.fromiter((k[1] for k in keys), dtype=np.int64, count=len(keys))
+        counts = np.fromiter((c[0].shape[0] for c in last.values()), dtype=np.int64, count=len(keys))
+        total = int(counts.sum())
+        cols = [np.concatenate([c[f] for c in last.values()]).astype(np.int64, copy=False) if total
+                else np.zeros(0, dtype=np.int64) for f in range(3)]
+        self._write_pages([k[0] for k in keys], np.fromiter((k[1] for k in keys), dtype=np.int64, count=len(keys)),
+                          counts, cols)
+
+    def write_columns(self, session_ids: list[str], bin_starts: Any, counts: Any, neuron_ids: Any,
+                      time_bins: Any, values: Any) -> None:
+        """``write_many`` for pages already laid out as columns: page i is
+        ``(session_ids[i], bin_starts[i])`` and owns the next ``counts[i]`` entries of the
+        flat ``neuron_ids`` / ``time_bins`` / ``values`` (absolute bins), pages in order.
+        Keys must be distinct.  One pinned copy and one scatter launch, on the current stream."""
+        starts = np.asarray(bin_starts, dtype=np.int64).reshape(-1)
+        cnt = np.asarray(counts, dtype=np.int64).reshape(-1)
+        if not (len(session_ids) == starts.shape[0] == cnt.shape[0]):
+            raise ValueError("session_ids, bin_starts and counts must have one entry per page")
+        cols = [np.asarray(x.cpu() if torch.is_tensor(x) else x).reshape(-1).astype(np.int64, copy=False)
+                for x in (neuron_ids, time_bins, values)]
+        if (cnt < 0).any() or not (cols[0].shape[0] == cols[1].shape[0] == cols[2].shape[0] == int(cnt.sum())):
+            raise ValueError("neuron_ids, time_bins and values must hold sum(counts) events each")
+        if not session_ids:
+            return
+        self._write_pages(list(session_ids), starts, cnt, cols, distinct=False)
+
+    def _write_pages(self, names: list[str], starts: np.ndarray, counts: np.ndarray, cols: list[np.ndarray],
+                     distinct: bool = True) -> None:
+        """Check, then write pages ``(names[i], starts[i])`` holding ``counts[i]`` consecutive
+        events of ``cols`` each (``distinct``: the keys are known to differ)."""
+        P = len(names)
+        if P > self.num_pages:
+            raise ValueError(f"{P} pages in one write exceed the pool's {self.num_pages}")
         bad = starts % self.bins_per_page != 0
         if bad.any():
             raise ValueError(f"bin_start {int(starts[bad][0])} is not a multiple of "
                              f"bins_per_page={self.bins_per_page}")
-        counts = np.fromiter((c[0].shape[0] for c in last.values()), dtype=np.int64, count=len(keys))
-        for c in last.values():
-            if not (c[1].shape[0] == c[2].shape[0] == c[0].shape[0]):
-                raise ValueError("neuron_ids, time_bins and values must have the same length")
         if counts.max() > self.page_events:
             raise ValueError(f"{int(counts.max())} events exceed page_events={self.page_events}")
         total = int(counts.sum())
-        cols = [np.concatenate([c[f] for c in last.values()]).astype(np.int64, copy=False) if total
-                else np.zeros(0, dtype=np.int64) for f in range(3)]
         if total:
             lo = np.repeat(starts, counts)
             outside = (cols[1] < lo) | (cols[1] >= lo + self.bins_per_page)
@@ -290,7 +320,13 @@ class EventWindowCache:
                 tb = cols[1][int(counts[:k].sum()):int(counts[:k + 1].sum())]
                 raise ValueError(f"time bins [{tb.min()}, {tb.max()}] outside page "
                                  f"[{b0}, {b0 + self.bins_per_page})")
-        sessions = np.fromiter((self._table.session(k[0]) for k in keys), dtype=np.int64, count=len(keys))
+        sessions = np.fromiter((self._table.session(x) for x in names), dtype=np.int64, count=P)
+        if not distinct and P > 1:
+            order = np.lexsort((starts, sessions))
+            same = (sessions[order][1:] == sessions[order][:-1]) & (starts[order][1:] == starts[order][:-1])
+            if same.any():
+                i = int(order[int(np.argmax(same))])
+                raise ValueError(f"page ({names[i]!r}, {int(starts[i])}) is given twice")
         page_ids = self._table.write(sessions, starts, counts)
         nz = counts > 0
         if not nz.any():
@@ -309,6 +345,9 @@ class EventWindowCache:
         dev = self._stage_dev[:need]
         dev.copy_(self._stage_host[:need], non_blocking=True)
         self._staged.record()
+        if self._gathered is not None and not self._gathered.query():
+            # a gather still queued on another stream may read a page this write reuses
+            torch.cuda.current_stream(self.device).wait_event(self._gathered)
         nat.call("cortex_scatter_event_pages", nat.ptr(dev), total, total, nat.ptr(dev[3 * total:]), items.shape[0],
                  nat.ptr(self._pool), self.num_pages, self.page_events, None, nat.stream_of(self.device))
 
@@ -353,6 +392,9 @@ class EventWindowCache:
         nat.call("cortex_gather_event_pages", nat.ptr(self._pool), self.num_pages, self.page_events,
                  nat.ptr(items), items.shape[0], nat.ptr(out), field_stride, out_rows, nat.ptr(err),
                  nat.stream_of(self.device))
+        if self._gathered is None:
+            self._gathered = torch.cuda.Event()
+        self._gathered.record(torch.cuda.current_stream(self.device))
 
     def assemble(self, windows: list[tuple[str, int]], window_bins: int
                  ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:

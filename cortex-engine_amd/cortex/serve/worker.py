@@ -148,6 +148,48 @@ class _CsrGraph:
         return self.model.forward_csr(nid, tb, val, off, err_flag=self.err)
 
 
+class _Slot:
+    """Pinned host buffers of one batch in flight (input staging, result, error flag) and
+    the event after its last copy; two slots let the host prepare one batch while the GPU
+    runs the other."""
+
+    def __init__(self) -> None:
+        self.host_in = torch.empty(1 << 16, dtype=torch.int64).pin_memory()
+        self.host_out = torch.empty(1024, dtype=torch.float32).pin_memory()
+        self.host_err = torch.zeros(1, dtype=torch.int32).pin_memory()
+        self.done = torch.cuda.Event()
+        self.pending: PendingBatch | None = None
+
+
+class PendingBatch:
+    """A streaming batch submitted by ``InferenceWorker.submit_windows``; pass it to
+    ``collect`` for the result dicts."""
+
+    def __init__(self, slot: _Slot, requests: list[dict[str, Any]], batch: int, dim: int, t0: float) -> None:
+        self._slot, self.requests, self._B, self._dim, self._t0 = slot, requests, batch, dim, t0
+        self._rows: np.ndarray | None = None
+        self._error: Exception | None = None
+        self._ms = 0.0
+
+    def _settle(self) -> None:
+        """Wait for the batch and move its result out of the pinned slot."""
+        if self._rows is not None or self._error is not None:
+            return
+        slot = self._slot
+        slot.done.synchronize()
+        e = int(slot.host_err[0])
+        if e & 4:  # the host plan and the device pool disagree: a bug, not bad input
+            self._error = RuntimeError("event page gather got a malformed plan item")
+        elif e:
+            self._error = IndexError("event index out of range (neuron_id, time_bin or value outside its "
+                                     "embedding table)")
+        else:
+            self._rows = slot.host_out[:self._B * self._dim].view(self._B, self._dim).numpy().copy()
+        self._ms = (time.perf_counter() - self._t0) * 1000
+        if slot.pending is self:
+            slot.pending = None
+
+
 class InferenceWorker:
     """Batched inference worker (reference worker.py:92-253); one model, one GPU.
 
@@ -173,11 +215,9 @@ class InferenceWorker:
         self._stream = torch.cuda.Stream(device=device)  # default priority
         self._graphs: OrderedDict[tuple[int, int], _CsrGraph] = OrderedDict()
         self._pool = torch.cuda.graph_pool_handle() if use_graphs else None
-        self._host_in = torch.empty(1 << 16, dtype=torch.int64).pin_memory()
-        self._host_out = torch.empty(1024, dtype=torch.float32).pin_memory()
-        self._host_err = torch.zeros(1, dtype=torch.int32).pin_memory()
+        self._slots = (_Slot(), _Slot())
+        self._next_slot = 0
         self._plan_dev: torch.Tensor | None = None
-        self._done = torch.cuda.Event()
         self._loaded = False
 
     # ------------------------------------------------------------------ API
@@ -214,16 +254,17 @@ class InferenceWorker:
         """
         t0 = time.perf_counter()
         dim = self.config.behavior_dim
-        flat, B, E, Eb = pack_payloads(payloads, self.use_graphs, self._host_in.numpy())
+        slot = self._acquire_slot()
+        flat, B, E, Eb = pack_payloads(payloads, self.use_graphs, slot.host_in.numpy())
         if B == 0:
             ms = (time.perf_counter() - t0) * 1000
             return [{"request_id": p["request_id"], "behavior": [0.0] * dim, "inference_ms": ms} for p in payloads]
         n_in = 3 * Eb + B + 1
-        if flat.ctypes.data != self._host_in.data_ptr():  # did not fit: grow the pinned buffer
-            self._host_in = torch.empty(max(n_in, 2 * self._host_in.numel()), dtype=torch.int64).pin_memory()
-            self._host_in.numpy()[:n_in] = flat[:n_in]
-        src = self._host_in[:n_in]
-        behavior = self._forward(B, Eb, lambda inp, err: inp.copy_(src, non_blocking=True))
+        if flat.ctypes.data != slot.host_in.data_ptr():  # did not fit: grow the pinned buffer
+            slot.host_in = torch.empty(max(n_in, 2 * slot.host_in.numel()), dtype=torch.int64).pin_memory()
+            slot.host_in.numpy()[:n_in] = flat[:n_in]
+        src = slot.host_in[:n_in]
+        behavior = self._forward(slot, B, Eb, lambda inp, err: inp.copy_(src, non_blocking=True))
         ms = (time.perf_counter() - t0) * 1000
         rows = behavior.tolist()
         return [{"request_id": p["request_id"], "behavior": rows[i] if i < B else [0.0] * dim, "inference_ms": ms}
@@ -235,23 +276,35 @@ class InferenceWorker:
         decode window whose event pages are already in ``cache`` (an ``EventWindowCache`` on this
         device).  The window inputs are gathered on the device into the forward's input buffer;
         only the gather plan and the offsets cross PCIe.  Same result dicts as ``run_batch``."""
-        t0 = time.perf_counter()
         if not requests:
             return []
+        return self.collect(self.submit_windows(requests, cache, window_bins))
+
+    def submit_windows(self, requests: list[dict[str, Any]], cache: Any, window_bins: int = 600) -> PendingBatch:
+        """``run_windows_sync`` without the wait: plans the batch, queues the page gather,
+        the forward and the result copy on the worker stream, and returns at once.  While it
+        runs the host can write the next stride's pages and submit the next batch (two
+        batches in flight; submitting a third first settles the oldest).  ``collect`` gives
+        the result dicts.  Not thread-safe, like the cache."""
+        t0 = time.perf_counter()
+        if not requests:
+            raise ValueError("submit_windows needs at least one request")
         items, offsets = cache.plan([(r["session_id"], int(r["window_start"])) for r in requests], window_bins)
         B, E = len(requests), int(offsets[-1])
         Eb = event_bucket(E) if self.use_graphs else max(E, 1)
         n_host = B + 1 + items.size
-        if self._host_in.numel() < n_host:
-            self._host_in = torch.empty(max(n_host, 2 * self._host_in.numel()), dtype=torch.int64).pin_memory()
-        h = self._host_in.numpy()
+        slot = self._acquire_slot()
+        if slot.host_in.numel() < n_host:
+            slot.host_in = torch.empty(max(n_host, 2 * slot.host_in.numel()), dtype=torch.int64).pin_memory()
+        h = slot.host_in.numpy()
         h[:B + 1] = offsets
         h[B + 1:n_host] = items.reshape(-1)
         have = 0 if self._plan_dev is None else self._plan_dev.numel()
         if have < max(items.size, 4):
+            self._stream.synchronize()  # the old plan buffer may still be read by a queued gather
             self._plan_dev = torch.empty(max(items.size, 4, 2 * have), dtype=torch.int64, device=self.device)
         plan_dev = self._plan_dev[:items.size].view(-1, 4)
-        off_host, plan_host = self._host_in[:B + 1], self._host_in[B + 1:n_host]
+        off_host, plan_host = slot.host_in[:B + 1], slot.host_in[B + 1:n_host]
 
         def fill(inp: torch.Tensor, err: torch.Tensor) -> None:
             inp[3 * Eb:3 * Eb + B + 1].copy_(off_host, non_blocking=True)
@@ -260,18 +313,36 @@ class InferenceWorker:
                 cache.gather(plan_dev, inp, Eb, E, err)
 
         self._stream.wait_stream(torch.cuda.current_stream(self.device))  # page writes issued on it
-        behavior = self._forward(B, Eb, fill)
-        ms = (time.perf_counter() - t0) * 1000
-        rows = behavior.tolist()
-        return [{"request_id": r["request_id"], "behavior": rows[i], "inference_ms": ms}
-                for i, r in enumerate(requests)]
+        self._launch(slot, B, Eb, fill)
+        pending = PendingBatch(slot, requests, B, self.config.behavior_dim, t0)
+        slot.pending = pending
+        return pending
 
-    def _forward(self, B: int, Eb: int, fill) -> np.ndarray:
+    def collect(self, pending: PendingBatch) -> list[dict[str, Any]]:
+        """Result dicts of a submitted streaming batch (waits for it)."""
+        pending._settle()
+        if pending._error is not None:
+            raise pending._error
+        rows = pending._rows.tolist()
+        return [{"request_id": r["request_id"], "behavior": rows[i], "inference_ms": pending._ms}
+                for i, r in enumerate(pending.requests)]
+
+    def _acquire_slot(self) -> _Slot:
+        """The next pinned slot, once the batch that used it last is off the GPU (its result,
+        if nobody collected it yet, moves to host memory first)."""
+        slot = self._slots[self._next_slot]
+        self._next_slot ^= 1
+        if slot.pending is not None:
+            slot.pending._settle()
+        slot.done.synchronize()
+        return slot
+
+    def _launch(self, slot: _Slot, B: int, Eb: int, fill) -> None:
         """``fill(inp, err)`` writes the (B, Eb) input buffer on the worker stream; then the
-        forward runs and the (B, dim) behaviour comes back to the host."""
+        forward runs and the (B, dim) behaviour is copied into ``slot`` (no host wait)."""
         dim = self.config.behavior_dim
-        if self._host_out.numel() < B * dim:
-            self._host_out = torch.empty(max(B * dim, 2 * self._host_out.numel()), dtype=torch.float32).pin_memory()
+        if slot.host_out.numel() < B * dim:
+            slot.host_out = torch.empty(max(B * dim, 2 * slot.host_out.numel()), dtype=torch.float32).pin_memory()
         with torch.cuda.device(self.device), torch.cuda.stream(self._stream):
             if self.use_graphs:
                 g = self._graph(B, Eb)
@@ -286,23 +357,26 @@ class InferenceWorker:
                 with torch.inference_mode():
                     out = self.model.forward_csr(inp[:Eb], inp[Eb:2 * Eb], inp[2 * Eb:3 * Eb], inp[3 * Eb:],
                                                  err_flag=err)
-            host = self._host_out[:B * dim].view(B, dim)
-            host.copy_(out, non_blocking=True)
-            self._host_err.copy_(err, non_blocking=True)
-            self._done.record(self._stream)
-        self._done.synchronize()
-        e = int(self._host_err[0])
-        if e & 4:  # the host plan and the device pool disagree: a bug, not bad input
-            raise RuntimeError("event page gather got a malformed plan item")
-        if e:
-            raise IndexError("event index out of range (neuron_id, time_bin or value outside its embedding table)")
-        return host.numpy().copy()
+            slot.host_out[:B * dim].view(B, dim).copy_(out, non_blocking=True)
+            slot.host_err.copy_(err, non_blocking=True)
+            slot.done.record(self._stream)
+
+    def _forward(self, slot: _Slot, B: int, Eb: int, fill) -> np.ndarray:
+        """``_launch`` and wait: the (B, dim) behaviour on the host."""
+        pending = PendingBatch(slot, [], B, self.config.behavior_dim, time.perf_counter())
+        slot.pending = pending
+        self._launch(slot, B, Eb, fill)
+        pending._settle()
+        if pending._error is not None:
+            raise pending._error
+        return pending._rows
 
     def _graph(self, B: int, Eb: int) -> _CsrGraph:
         key = (B, Eb)
         g = self._graphs.get(key)
         if g is None:
             if len(self._graphs) >= self.max_graphs:
+                self._stream.synchronize()  # the evicted graph may still be replaying
                 self._graphs.popitem(last=False)
             g = _CsrGraph(self.model, B, Eb, self.device, self._stream, self._pool)
             self._graphs[key] = g

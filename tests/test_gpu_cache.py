@@ -109,3 +109,89 @@ def test_worker_windows_equal_payloads(use_graphs):
         assert [g["request_id"] for g in got] == [x["request_id"] for x in want]
         assert [g["behavior"] for g in got] == [x["behavior"] for x in want]
     w.shutdown()
+
+
+def _stride_columns(sessions, names, b0):
+    """One stride of every session as page columns: counts per page, then the events."""
+    parts = [_events_abs(sessions[s], b0) for s in names]
+    cnt = np.array([p[0].shape[0] for p in parts], dtype=np.int64)
+    return cnt, *(np.concatenate([p[f] for p in parts]) for f in range(3))
+
+
+def test_write_columns_equals_write_many():
+    from cortex.cache import EventWindowCache
+
+    names = [f"s{i}" for i in range(5)]
+    sessions = {s: _session(40 + i) for i, s in enumerate(names)}
+    a = EventWindowCache(num_pages=256, page_events=512, bins_per_page=STRIDE, device=DEV)
+    b = EventWindowCache(num_pages=256, page_events=512, bins_per_page=STRIDE, device=DEV)
+    for b0 in range(0, 900, STRIDE):
+        cnt, nid, tb, val = _stride_columns(sessions, names, b0)
+        a.write_columns(names, np.full(len(names), b0), cnt, nid, tb, val)
+        b.write_many([(s, b0, *_events_abs(sessions[s], b0)) for s in names])
+    windows = [(s, w0) for s in names for w0 in (0, 150, 300)]
+    got, want = a.assemble(windows, WINDOW), b.assemble(windows, WINDOW)
+    for x, y in zip(got, want):
+        assert torch.equal(x, y)
+    cnt, nid, tb, val = _stride_columns(sessions, names[:2], 900)
+    with pytest.raises(ValueError):  # a key given twice
+        a.write_columns([names[0], names[0]], [900, 900], cnt, nid, tb, val)
+    with pytest.raises(ValueError):  # counts do not cover the events
+        a.write_columns(names[:2], [900, 900], cnt + 1, nid, tb, val)
+    with pytest.raises(ValueError):  # a bin outside its page
+        a.write_columns(names[:2], [950, 900], cnt, nid, tb, val)
+    a.write_columns([], [], [], [], [], [])
+
+
+@pytest.mark.parametrize("use_graphs", [True, False])
+def test_pipelined_windows_equal_sync(use_graphs):
+    """submit_windows / collect with the next stride written while a batch runs: the same
+    results as the synchronous path, with LRU eviction on every step, and with a third
+    submission settling the oldest uncollected batch."""
+    from cortex.cache import EventWindowCache
+    from cortex.models import CortexModel
+    from cortex.models.config import CORTEX_S
+    from cortex.serve import InferenceWorker
+
+    torch.manual_seed(0)
+    model = CortexModel(CORTEX_S).to(DEV).eval()
+    w = InferenceWorker(model, CORTEX_S, torch.device(DEV), use_graphs=use_graphs)
+    names = [f"s{i}" for i in range(6)]
+    sessions = {s: _session(60 + i, T=1600, rate=0.01) for i, s in enumerate(names)}
+    per = WINDOW // STRIDE
+    piped = EventWindowCache(num_pages=(per + 1) * len(names), page_events=512, bins_per_page=STRIDE, device=DEV)
+    sync = EventWindowCache(num_pages=(per + 1) * len(names), page_events=512, bins_per_page=STRIDE, device=DEV)
+    for b0 in range(0, WINDOW - STRIDE, STRIDE):
+        cnt, nid, tb, val = _stride_columns(sessions, names, b0)
+        piped.write_columns(names, np.full(len(names), b0), cnt, nid, tb, val)
+        for s in names:
+            sync.write(s, b0, *_events_abs(sessions[s], b0))
+    steps = 8
+    reqs = [[{"request_id": f"{s}:{k}", "session_id": s, "window_start": k * STRIDE} for s in names]
+            for k in range(steps)]
+    got, pending = [], None
+    for k in range(steps):
+        cnt, nid, tb, val = _stride_columns(sessions, names, WINDOW - STRIDE + k * STRIDE)
+        piped.write_columns(names, np.full(len(names), WINDOW - STRIDE + k * STRIDE), cnt, nid, tb, val)
+        nxt = w.submit_windows(reqs[k], piped, WINDOW)
+        if pending is not None:
+            got.append(w.collect(pending))
+        pending = nxt
+    got.append(w.collect(pending))
+    want = []
+    for k in range(steps):
+        for s in names:
+            sync.write(s, WINDOW - STRIDE + k * STRIDE, *_events_abs(sessions[s], WINDOW - STRIDE + k * STRIDE))
+        want.append(w.run_windows_sync(reqs[k], sync, WINDOW))
+    assert [[r["behavior"] for r in g] for g in got] == [[r["behavior"] for r in x] for x in want]
+    assert [[r["request_id"] for r in g] for g in got] == [[r["request_id"] for r in x] for x in want]
+    # three in flight: the third submission settles the first, results unchanged
+    b0 = WINDOW + (steps - 1) * STRIDE
+    last = [[{"request_id": s, "session_id": s, "window_start": w0} for s in names]
+            for w0 in (b0 - WINDOW, b0 - WINDOW - STRIDE, b0 - WINDOW)]  # pages still in the pool
+    ps = [w.submit_windows(r, sync, WINDOW) for r in last]
+    outs = [w.collect(p) for p in ps]
+    assert [r["behavior"] for r in outs[0]] == [r["behavior"] for r in want[-1]]
+    for r, o in zip(last, outs):
+        assert [x["behavior"] for x in o] == [x["behavior"] for x in w.run_windows_sync(r, sync, WINDOW)]
+    w.shutdown()
