@@ -58,7 +58,9 @@ def make_events(batch: int, per_sample, seed: int):
             np.repeat(np.arange(batch), counts))
 
 
-def build_model(dev):
+def build_model(dev, with_scales: bool = False):
+    """CORTEX_S, seed 0, calibrated on one batch of 8 x 512 synthetic events and converted
+    to INT8 weights; with ``with_scales`` also the calibration scales (for the W8A8 mode)."""
     from cortex.models import CortexModel
     from cortex.models.config import CORTEX_S
     from cortex.quantization.calibrate import (attach_calibration_hooks, convert_model, derive_scales,
@@ -71,7 +73,9 @@ def build_model(dev):
     with torch.no_grad():
         model(*calib, batch_size=8)
     remove_calibration_hooks(hooks)
-    return convert_model(model, derive_scales(model, hooks), inplace=True)
+    scales = derive_scales(model, hooks)
+    model = convert_model(model, scales, inplace=True)
+    return (model, scales) if with_scales else model
 
 
 # --------------------------------------------------------------------------- hot kernels
@@ -487,6 +491,33 @@ def norm_linear_api(dev, M: int = 8192, K: int = 512, widths=(1536, 2048, 512)) 
     return {"M": M, "K": K, **out}
 
 
+def w8a8_forward(model, scales, dev, inputs, reference: torch.Tensor, reps: int = 50) -> dict:
+    """The opt-in W8A8 MLPs (cortex.quantization.w8a8) on the same B = 32 x 512 forward:
+    samples/s (graph replay) and the largest difference to the default path's behaviour."""
+    from cortex.quantization.w8a8 import disable_w8a8, enable_w8a8
+    from cortex.runtime import CapturedForward
+
+    n = enable_w8a8(model, scales)
+    try:
+        cap = CapturedForward(model, batch_size=B_MAIN, n_events=B_MAIN * PER_MAIN)
+        out = cap(*inputs).clone()
+        for _ in range(5):
+            cap(*inputs)
+        torch.cuda.synchronize(dev)
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            cap(*inputs)
+        torch.cuda.synchronize(dev)
+        sec = (time.perf_counter() - t0) / reps
+        del cap
+    finally:
+        disable_w8a8(model)
+    return {"blocks": n, "ms_per_forward": round(sec * 1e3, 4), "samples_per_s": round(B_MAIN / sec, 1),
+            "max_abs_diff_vs_default": float((out - reference).abs().max()),
+            "note": "int8 activations in the self-attention MLPs (calibrated act_scale); not the reference's "
+                    "arithmetic, opt-in"}
+
+
 def cpu_baseline(model, budget_s: float = 12.0, b1_budget_s: float = 18.0):
     """The CPU oracle (fp32 activations, INT8 weights dequantised as the reference's QuantizedLinear)
     on the host cores, with the reference's protocol (profile_inference.py: 5 warmup + up to 30 timed
@@ -586,7 +617,7 @@ def main() -> int:
     from cortex.runtime import CapturedForward
 
     log("bench: building CORTEX_S INT8 model")
-    model = build_model(dev)
+    model, scales = build_model(dev, with_scales=True)
     B, per = B_MAIN, PER_MAIN
     inputs = [torch.from_numpy(a).to(dev) for a in make_events(B, per, seed=0)]
     cap = CapturedForward(model, batch_size=B, n_events=B * per)
@@ -632,6 +663,8 @@ def main() -> int:
         log(f"bench: streaming {extra['streaming']}")
         extra["norm_linear_api"] = norm_linear_api(dev)
         log(f"bench: norm + linear API {extra['norm_linear_api']}")
+        extra["w8a8"] = w8a8_forward(model, scales, dev, inputs, cap(*inputs).clone())
+        log(f"bench: w8a8 {extra['w8a8']}")
     cpu = None
     if not (args.no_cpu_baseline or args.quick):
         log("bench: CPU baseline")

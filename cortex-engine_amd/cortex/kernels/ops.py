@@ -255,17 +255,26 @@ def qkv_attention(xn: torch.Tensor, weight: torch.Tensor, weight_scale, bias, ba
 
 
 def linear_residual_ln(x: torch.Tensor, weight: torch.Tensor, weight_scale=None, bias=None, *,
-                       residual: torch.Tensor, ln, res_rows: int = 0, out: torch.Tensor | None = None):
+                       residual: torch.Tensor, ln, res_rows: int = 0, out: torch.Tensor | None = None,
+                       xq_scale: float | None = None):
     """``out = residual + x @ (weight * scale)^T + bias`` (fp32) and ``LN(out)`` (bf16) in one
     kernel; ``x`` (M, K) and ``weight`` (N, K) bf16, N in {256, 512}.  ``out`` may be
-    ``residual`` itself.  Returns ``(out, xn)``."""
+    ``residual`` itself.  Returns ``(out, xn)``.  With ``xq_scale`` (the W8A8 mode) ``xn`` is
+    int8: ``clamp(rint(LN(out) * (1 / xq_scale)), -127, 127)``."""
     dev = nat.require_gpu(x, weight, weight_scale, bias, residual, out, what="linear_residual_ln")
     M, K = x.shape
     N = weight.shape[0]
     if out is None:
         out = torch.empty((M, N), dtype=torch.float32, device=dev)
-    xn = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
     g, b, eps = ln
+    if xq_scale is not None:
+        xq = torch.empty((M, N), dtype=torch.int8, device=dev)
+        nat.call("cortex_linear_residual_ln_i8", M, N, K, nat.ptr(x), x.stride(0), nat.ptr(weight), weight.stride(0),
+                 nat.ptr(weight_scale), nat.ptr(bias), nat.ptr(residual), residual.stride(0), int(res_rows),
+                 nat.ptr(out), out.stride(0), nat.ptr(g), nat.ptr(b), float(eps), nat.ptr(xq), xq.stride(0),
+                 float(xq_scale), nat.stream_of(dev))
+        return out, xq
+    xn = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
     splits = splitk_splits(M, N, K, dev)
     if splits:  # few rows: K split across workgroups, slabs summed in order, then the LayerNorm
         ws_t = torch.empty(nat.load().cortex_splitk_workspace_bytes(M, N, splits), dtype=torch.uint8, device=dev)
@@ -279,6 +288,36 @@ def linear_residual_ln(x: torch.Tensor, weight: torch.Tensor, weight_scale=None,
              nat.ptr(out), out.stride(0), nat.ptr(g), nat.ptr(b), float(eps), nat.ptr(xn), xn.stride(0),
              nat.stream_of(dev))
     return out, xn
+
+
+def linear_w8a8(xq: torch.Tensor, a_scale: float, weight_int8: torch.Tensor, weight_scale=None, bias=None, *,
+                act: str | None = None, residual: torch.Tensor | None = None, res_rows: int = 0,
+                out_dtype: torch.dtype = torch.float32, out_scale: float | None = None,
+                out: torch.Tensor | None = None) -> torch.Tensor:
+    """The opt-in W8A8 linear (``cortex_linear_w8a8``): int8 activations ``xq`` (M, K) at
+    per-tensor scale ``a_scale`` times the int8 weight (N, K), exact int32 sums, then
+    ``* a_scale * weight_scale + bias`` (and GELU).  ``out_dtype`` float32 (optionally plus
+    ``residual``; ``out`` may be the residual) or int8 at ``out_scale``."""
+    dev = nat.require_gpu(xq, weight_int8, weight_scale, bias, residual, out, what="linear_w8a8")
+    if xq.dtype != torch.int8 or weight_int8.dtype != torch.int8:
+        raise ValueError("linear_w8a8 takes int8 activations and an int8 weight")
+    x2 = _row_major_2d(xq.reshape(-1, xq.shape[-1]))
+    w2 = _row_major_2d(weight_int8)
+    M, K = x2.shape
+    N = w2.shape[0]
+    if w2.shape[1] != K:
+        raise ValueError(f"inner dims differ: x has K={K}, weight has K={w2.shape[1]}")
+    if out_dtype not in (torch.float32, torch.int8):
+        raise ValueError("out_dtype must be float32 or int8")
+    if out is None:
+        out = torch.empty((*xq.shape[:-1], N), dtype=out_dtype, device=dev)
+    out2 = out.reshape(-1, N)
+    res2 = None if residual is None else _row_major_2d(residual.reshape(-1, N))
+    nat.call("cortex_linear_w8a8", M, N, K, nat.ptr(x2), x2.stride(0) if M > 1 else K, float(a_scale), nat.ptr(w2),
+             w2.stride(0) if N > 1 else K, nat.ptr(weight_scale), nat.ptr(bias), ACT[act], nat.ptr(res2),
+             (res2.stride(0) if res2.shape[0] > 1 else N) if res2 is not None else 0, int(res_rows), nat.ptr(out2),
+             nat.code(out_dtype), float(out_scale or 0.0), out2.stride(0) if M > 1 else N, nat.stream_of(dev))
+    return out
 
 
 def head_prep(q: torch.Tensor, kv_weight: torch.Tensor, kv_scale, out_weight: torch.Tensor, out_scale,

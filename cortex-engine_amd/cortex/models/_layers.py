@@ -133,12 +133,12 @@ def residual_ln_ok(lin: nn.Module, norm: nn.LayerNorm, consumer: nn.Module, x: t
 
 
 def linear_residual_ln(lin: nn.Module, a: torch.Tensor, residual: torch.Tensor, norm: nn.LayerNorm, *,
-                       res_rows: int = 0, out: torch.Tensor | None = None):
-    """``x = residual + lin(a)`` (fp32) and ``norm(x)`` (bf16) in one launch (see
-    ``residual_ln_ok``).  Returns ``(x, norm(x))``."""
+                       res_rows: int = 0, out: torch.Tensor | None = None, xq_scale: float | None = None):
+    """``x = residual + lin(a)`` (fp32) and ``norm(x)`` (bf16; int8 at ``xq_scale`` when given)
+    in one launch (see ``residual_ln_ok``).  Returns ``(x, norm(x))``."""
     w = exec_weights(lin, torch.bfloat16)
     return ops.linear_residual_ln(a, w["weight"], w["weight_scale"], w["bias"], residual=residual,
-                                  ln=ln_params(norm), res_rows=res_rows, out=out)
+                                  ln=ln_params(norm), res_rows=res_rows, out=out, xq_scale=xq_scale)
 
 
 def apply_linear(lin: nn.Module, x: torch.Tensor, *, norm: nn.LayerNorm | None = None, stats=None,

@@ -108,6 +108,14 @@ class SelfAttentionBlock(nn.Module):
             ops.attention(ops.heads_view(qkv, batch, length, H, 0, D), ops.heads_view(qkv, batch, length, H, D, D),
                           ops.heads_view(qkv, batch, length, H, 2 * D, D), out=o)
         # each residual element is read and then written by the same lane: in place is safe
+        w8 = self._w8a8(x, compute)
+        if w8 is not None:  # opt-in W8A8 MLP (cortex.quantization.w8a8): int8 activations end to end
+            up, down = self.mlp[0], self.mlp[2]
+            x, xq = linear_residual_ln(self.out_proj, o_buf, x, self.norm_mlp, out=x if inplace else None,
+                                       xq_scale=w8[0])
+            hq = ops.linear_w8a8(xq, w8[0], up.weight_int8, up.weight_scale, up.bias, act="gelu",
+                                 out_dtype=torch.int8, out_scale=w8[1])
+            return ops.linear_w8a8(hq, w8[1], down.weight_int8, down.weight_scale, down.bias, residual=x, out=x)
         if residual_ln_ok(self.out_proj, self.norm_mlp, self.mlp[0], x, compute):
             x, hn = linear_residual_ln(self.out_proj, o_buf, x, self.norm_mlp, out=x if inplace else None)
             h = ops.norm_linear(hn, **exec_weights(self.mlp[0], compute), act="gelu", out_dtype=compute,
@@ -118,6 +126,23 @@ class SelfAttentionBlock(nn.Module):
             h = apply_linear(self.mlp[0], x, norm=self.norm_mlp, act="gelu", out_dtype=compute, compute=compute)
         return apply_linear(self.mlp[2], h, residual=x, out_dtype=x.dtype, compute=compute,
                             out=x if inplace else None)
+
+    def _w8a8(self, x: torch.Tensor, compute: torch.dtype) -> tuple[float, float] | None:
+        """The MLP's activation scales when this block runs it as W8A8 (enabled, bf16 compute,
+        no calibration hooks, int8 weights with K a multiple of 128, fp32 biases)."""
+        from cortex.quantization.w8a8 import w8a8_scales
+
+        w8 = w8a8_scales(self)
+        if w8 is None or not residual_ln_ok(self.out_proj, self.norm_mlp, self.mlp[0], x, compute):
+            return None
+        up, down = self.mlp[0], self.mlp[2]
+        if up._forward_pre_hooks or down._forward_pre_hooks or not hasattr(up, "weight_int8"):
+            return None
+        if up.weight_int8.shape[1] % 128 or down.weight_int8.shape[1] % 128 or up.weight_int8.shape[0] % 8:
+            return None
+        if any(b is not None and b.dtype != torch.float32 for b in (up.bias, down.bias)):
+            return None
+        return w8
 
     def _fused_attention_ok(self, x: torch.Tensor, length: int) -> bool:
         """Whether ``cortex_qkv_attention`` covers this block: bf16 compute, no calibration

@@ -31,6 +31,10 @@ struct GemmArgs {
   int out_dtype;
   int64_t ld_out;
   int vec;  // 1: 16-byte aligned rows, vector loads allowed
+  // int8 x int8 kernels only (gemm_bf16.hip, TIN = int8_t): x holds round(x_f / a_scale),
+  // and an int8 output is written as clamp(rint(y * out_inv_scale), -127, 127)
+  float a_scale;
+  float out_inv_scale;
 };
 
 // Fast path for aligned bf16-compute GEMMs (gemm_fast.hip).  Returns 1 when it

@@ -1,5 +1,5 @@
-// bf16 x bf16 GEMM for gfx950 with direct-to-LDS operand streaming and a
-// register epilogue:
+// bf16 x bf16 (and int8 x int8) GEMM for gfx950 with direct-to-LDS operand streaming
+// and a register epilogue:
 //
 //   C[m, n] = epi( sum_k A[m, k] * W[n, k] ),  A (M, K) bf16 rows, W (N, K) bf16 rows
 //   epi: * w_scale[n] (+ bias[n]) (-> erf-GELU) -> bf16 | fp32, or (+ fp32 residual) -> fp32
@@ -7,11 +7,18 @@
 // W is the bf16 execution image of a QuantizedLinear's int8 weight (exact) with the
 // per-channel scale applied in the epilogue, or a float weight rounded to bf16.
 //
+// The int8 form (TIN = int8_t: the opt-in W8A8 mode) takes int8 activation rows
+// x = round(x_f / a_scale) and the int8 weight itself, accumulates exactly in int32 on
+// v_mfma_i32_16x16x64_i8 and applies a_scale * w_scale[n] in the epilogue; its outputs
+// are fp32 (with the residual) or int8 at the next linear's activation scale.  Both
+// MFMAs read 16 bytes per lane per operand, so the LDS ring, swizzles and transfers are
+// byte-for-byte the same; a 128-byte LDS row holds 64 bf16 or 128 int8 of K.
+//
 // Operands travel global -> LDS with global_load_lds_dwordx4 (1 KiB per wavefront
 // instruction, no VGPRs held while in flight) through a STAGES-deep ring; a step
 // waits only for its own transfers (vmcnt) plus a raw s_barrier.
 //
-// LDS rows hold 64 bf16 of K (128 bytes); the 16-byte chunk c of row r is stored at
+// LDS rows hold 128 bytes of K; the 16-byte chunk c of row r is stored at
 // c ^ sw(r), with sw chosen so that the 16 rows read by one MFMA fragment cover all
 // 16 four-bank groups.
 //
@@ -56,6 +63,30 @@ struct BTile {
   static_assert(PER * (STAGES - 1) < 64, "vmcnt range");
 };
 
+// Operand element type: a 16-byte fragment per lane and the MFMA that consumes it.
+template <class TIN>
+struct Operand;
+template <>
+struct Operand<bf16> {
+  typedef bf16x8 frag;
+  typedef f32x4 accum;
+  typedef float elem;
+  static constexpr int EPC = 8;  // elements per 16-byte chunk
+  static __device__ __forceinline__ accum mma(const frag& w, const frag& a, const accum& c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(w, a, c, 0, 0, 0);
+  }
+};
+template <>
+struct Operand<int8_t> {
+  typedef i32x4 frag;
+  typedef i32x4 accum;
+  typedef int elem;
+  static constexpr int EPC = 16;
+  static __device__ __forceinline__ accum mma(const frag& w, const frag& a, const accum& c) {
+    return __builtin_amdgcn_mfma_i32_16x16x64_i8(w, a, c, 0, 0, 0);
+  }
+};
+
 // 16-byte chunk swizzles of the 128-byte LDS rows.  A fragments read 16 consecutive
 // rows; W fragments read rows 8q + 4jj + i (q, i in 0..3) -- see the column order
 // below.  Each swizzle puts its fragment's 16 rows into the 16 distinct (row parity,
@@ -68,13 +99,16 @@ __device__ __forceinline__ int swz_w(int r) { return ((r >> 1) & 1) | ((r >> 2) 
 // tiles 2p and 2p+1 give lane group g4 the 8 consecutive columns 32 p + 8 g4 .. +7.
 __device__ __forceinline__ int wrow_of(int p, int jj, int rho) { return 32 * p + 8 * (rho >> 2) + 4 * jj + (rho & 3); }
 
-template <class TL, int ACT, bool RES, class TOUT>
+template <class TL, int ACT, bool RES, class TOUT, class TIN = bf16>
 __global__ __launch_bounds__(TL::THREADS) void gemm_bf16_kernel(GemmArgs g) {
   constexpr int BM = TL::BM, BN = TL::BN, TM = TL::TM, TN = TL::TN, S = TL::STAGES;
   constexpr int AB = TL::A_BLOCKS, WB = TL::W_BLOCKS, PER = TL::PER;
-  // bf16 output: interleaved W rows, 8 consecutive columns (16 bytes) per lane;
+  // bf16 / int8 output: interleaved W rows, 8 consecutive columns per lane;
   // fp32 output: natural order, 4 consecutive columns (16 bytes) per lane and tile.
-  constexpr bool IL = sizeof(TOUT) == 2;
+  constexpr bool IL = sizeof(TOUT) <= 2;
+  using OP = Operand<TIN>;
+  typedef typename OP::frag frag;
+  constexpr int EPC = OP::EPC, BK = 8 * EPC;  // K elements per 16-byte chunk and per 128-byte row
   __shared__ __attribute__((aligned(1024))) unsigned char smem[TL::LDS];
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -87,30 +121,30 @@ __global__ __launch_bounds__(TL::THREADS) void gemm_bf16_kernel(GemmArgs g) {
   const int M = (int)g.M, N = (int)g.N, K = (int)g.K;
   // K split across workgroups (split_k_partials): slice z of K into output slab z
   const int kz = blockIdx.z;
-  const bf16* __restrict__ A = reinterpret_cast<const bf16*>(g.x) + (int64_t)kz * K;
-  const bf16* __restrict__ W = reinterpret_cast<const bf16*>(g.w) + (int64_t)kz * K;
+  const TIN* __restrict__ A = reinterpret_cast<const TIN*>(g.x) + (int64_t)kz * K;
+  const TIN* __restrict__ W = reinterpret_cast<const TIN*>(g.w) + (int64_t)kz * K;
 
   // Global source of each of this lane's transfers (K offset added per step).  Lane i
   // of a transfer writes LDS bytes [16 i, 16 i + 16) of its 1 KiB block: row i / 8,
   // stored chunk i % 8, which holds logical chunk (i % 8) ^ swizzle(row).
-  const bf16* a_src[AB];
+  const TIN* a_src[AB];
 #pragma unroll
   for (int i = 0; i < AB; ++i) {
     const int r = (wid * AB + i) * 8 + (lane >> 3);
-    a_src[i] = A + (int64_t)min(m0 + r, M - 1) * g.ld_x + ((lane & 7) ^ swz_a(r)) * 8;
+    a_src[i] = A + (int64_t)min(m0 + r, M - 1) * g.ld_x + ((lane & 7) ^ swz_a(r)) * EPC;
   }
-  const bf16* w_src[WB];
+  const TIN* w_src[WB];
 #pragma unroll
   for (int i = 0; i < WB; ++i) {
     const int r = (wid * WB + i) * 8 + (lane >> 3);
-    w_src[i] = W + (int64_t)min(n0 + r, N - 1) * g.ld_w + ((lane & 7) ^ (IL ? swz_w(r) : swz_a(r))) * 8;
+    w_src[i] = W + (int64_t)min(n0 + r, N - 1) * g.ld_w + ((lane & 7) ^ (IL ? swz_w(r) : swz_a(r))) * EPC;
   }
   auto a_stage = [&](int s) { return ring + s * TL::A_STAGE; };
   auto w_stage = [&](int s) { return ring + S * TL::A_STAGE + s * TL::W_STAGE; };
-  const int nk = K / TL::BK / TL::KS;  // K steps of this group
-  const int kbase = kg * nk * TL::BK;
+  const int nk = K / BK / TL::KS;  // K steps of this group
+  const int kbase = kg * nk * BK;
   auto issue = [&](int kt) {
-    const int s = kt % S, k0 = kbase + kt * TL::BK;
+    const int s = kt % S, k0 = kbase + kt * BK;
 #pragma unroll
     for (int i = 0; i < AB; ++i)
       __builtin_amdgcn_global_load_lds(static_cast<const void*>(a_src[i] + k0),
@@ -121,11 +155,11 @@ __global__ __launch_bounds__(TL::THREADS) void gemm_bf16_kernel(GemmArgs g) {
                                        static_cast<void*>(w_stage(s) + (wid * WB + i) * 1024), 16, 0, 0);
   };
 
-  f32x4 acc[TM][TN];
+  typename OP::accum acc[TM][TN];
 #pragma unroll
   for (int i = 0; i < TM; ++i)
 #pragma unroll
-    for (int j = 0; j < TN; ++j) acc[i][j] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+    for (int j = 0; j < TN; ++j) acc[i][j] = (typename OP::accum){0, 0, 0, 0};
 
   const int fr = lane & 15, g4 = lane >> 4;
   const int wrow = wm * (BM / TL::WM), wcol = wn * (BN / TL::WN);
@@ -143,22 +177,22 @@ __global__ __launch_bounds__(TL::THREADS) void gemm_bf16_kernel(GemmArgs g) {
     w_off[t] = r * 128;
     w_sw[t] = IL ? swz_w(r) : swz_a(r);
   }
-  auto read_frags = [&](int stage, int ks, bf16x8 (&af)[TM], bf16x8 (&wf)[TN]) {
+  auto read_frags = [&](int stage, int ks, frag (&af)[TM], frag (&wf)[TN]) {
     const unsigned char* as = a_stage(stage);
     const unsigned char* ws = w_stage(stage);
 #pragma unroll
     for (int t = 0; t < TM; ++t)
-      af[t] = *reinterpret_cast<const bf16x8*>(as + a_off[t] + (((ks * 4 + g4) ^ a_sw[t]) << 4));
+      af[t] = *reinterpret_cast<const frag*>(as + a_off[t] + (((ks * 4 + g4) ^ a_sw[t]) << 4));
 #pragma unroll
     for (int t = 0; t < TN; ++t)
-      wf[t] = *reinterpret_cast<const bf16x8*>(ws + w_off[t] + (((ks * 4 + g4) ^ w_sw[t]) << 4));
+      wf[t] = *reinterpret_cast<const frag*>(ws + w_off[t] + (((ks * 4 + g4) ^ w_sw[t]) << 4));
   };
-  auto mma = [&](const bf16x8 (&af)[TM], const bf16x8 (&wf)[TN]) {
+  auto mma = [&](const frag (&af)[TM], const frag (&wf)[TN]) {
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
       for (int j = 0; j < TN; ++j)
-        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf[j], af[i], acc[i][j], 0, 0, 0);
+        acc[i][j] = OP::mma(wf[j], af[i], acc[i][j]);
   };
 
   // The residual tile is fetched into registers before the main loop, so its latency
@@ -203,7 +237,7 @@ __global__ __launch_bounds__(TL::THREADS) void gemm_bf16_kernel(GemmArgs g) {
         wait_vm<0>();
     }
   };
-  bf16x8 af0[TM], wf0[TN], af1[TM], wf1[TN];
+  frag af0[TM], wf0[TN], af1[TM], wf1[TN];
   wait_step(0, S - 1);
   __builtin_amdgcn_s_barrier();
   read_frags(0, 0, af0, wf0);
@@ -223,7 +257,7 @@ __global__ __launch_bounds__(TL::THREADS) void gemm_bf16_kernel(GemmArgs g) {
 
   if constexpr (TL::KS > 1) {
     // group 1 hands its partial tile to group 0 through LDS (lane-contiguous: conflict free)
-    float* red = reinterpret_cast<float*>(smem);
+    typename OP::elem* red = reinterpret_cast<typename OP::elem*>(smem);
     __syncthreads();  // every ring read is done; the exchange area may overwrite the rings
     if (kg == 1) {
 #pragma unroll
@@ -258,8 +292,11 @@ __global__ __launch_bounds__(TL::THREADS) void gemm_bf16_kernel(GemmArgs g) {
     const int n = min(n0 + wcol + (IL ? 32 * p + 8 * g4 : 16 * p + 4 * g4), N - NV);
 #pragma unroll
     for (int h = 0; h < NV / 4; ++h) {
-      const float4 s4 = g.w_scale ? *reinterpret_cast<const float4*>(g.w_scale + n + 4 * h)
-                                  : make_float4(1.f, 1.f, 1.f, 1.f);
+      float4 s4 = g.w_scale ? *reinterpret_cast<const float4*>(g.w_scale + n + 4 * h)
+                            : make_float4(1.f, 1.f, 1.f, 1.f);
+      if constexpr (sizeof(TIN) == 1) {  // int8 activations: x_f = a_scale * x
+        s4.x *= g.a_scale; s4.y *= g.a_scale; s4.z *= g.a_scale; s4.w *= g.a_scale;
+      }
       const float4 b4 = bias ? *reinterpret_cast<const float4*>(bias + n + 4 * h) : make_float4(0.f, 0.f, 0.f, 0.f);
       sca[p][4 * h] = s4.x; sca[p][4 * h + 1] = s4.y; sca[p][4 * h + 2] = s4.z; sca[p][4 * h + 3] = s4.w;
       bia[p][4 * h] = b4.x; bia[p][4 * h + 1] = b4.y; bia[p][4 * h + 2] = b4.z; bia[p][4 * h + 3] = b4.w;
@@ -288,7 +325,7 @@ __global__ __launch_bounds__(TL::THREADS) void gemm_bf16_kernel(GemmArgs g) {
       }
       if (ACT == ACT_GELU) {
 #pragma unroll
-        for (int e = 0; e < NV; ++e) v[e] = sizeof(TOUT) == 2 ? gelu_erf_bf16out(v[e]) : gelu_erf(v[e]);
+        for (int e = 0; e < NV; ++e) v[e] = sizeof(TOUT) <= 2 ? gelu_erf_bf16out(v[e]) : gelu_erf(v[e]);
       }
       if constexpr (RES && !IL) {
         const float4 x = rv[i][p];
@@ -300,6 +337,16 @@ __global__ __launch_bounds__(TL::THREADS) void gemm_bf16_kernel(GemmArgs g) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) o[e] = (bf16)v[e];
         *reinterpret_cast<bf16x8*>(op) = o;
+      } else if constexpr (sizeof(TOUT) == 1) {  // int8 at the next linear's activation scale
+        uint32_t lo = 0, hi = 0;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int q0 = (int)fminf(fmaxf(rintf(v[e] * g.out_inv_scale), -127.0f), 127.0f);
+          const int q1 = (int)fminf(fmaxf(rintf(v[4 + e] * g.out_inv_scale), -127.0f), 127.0f);
+          lo |= (uint32_t)(q0 & 0xff) << (8 * e);
+          hi |= (uint32_t)(q1 & 0xff) << (8 * e);
+        }
+        *reinterpret_cast<uint2*>(op) = make_uint2(lo, hi);
       } else {
 #pragma unroll
         for (int h = 0; h < NV / 4; ++h)
@@ -309,12 +356,12 @@ __global__ __launch_bounds__(TL::THREADS) void gemm_bf16_kernel(GemmArgs g) {
   }
 }
 
-template <class TL, int ACT, bool RES, class TOUT>
+template <class TL, int ACT, bool RES, class TOUT, class TIN = bf16>
 int launch(const GemmArgs& g, hipStream_t stream) {
   const int64_t gy = cdiv(g.M, TL::BM), gx = cdiv(g.N, TL::BN);
   if (gy > 65535 || gx * gy > 0x7fffffffLL) return 0;
-  hipLaunchKernelGGL((gemm_bf16_kernel<TL, ACT, RES, TOUT>), dim3((unsigned)gx, (unsigned)gy), dim3(TL::THREADS), 0,
-                     stream, g);
+  hipLaunchKernelGGL((gemm_bf16_kernel<TL, ACT, RES, TOUT, TIN>), dim3((unsigned)gx, (unsigned)gy),
+                     dim3(TL::THREADS), 0, stream, g);
   CORTEX_CHECK_LAUNCH("gemm_bf16_kernel");
   return 1;
 }
@@ -442,3 +489,73 @@ int try_gemm_bf16(const GemmArgs& g, int x_dtype, int w_dtype, int w_layout, int
 }
 
 }  // namespace cortex
+
+using namespace cortex;
+
+extern "C" int cortex_linear_w8a8(int64_t M, int64_t N, int64_t K, const int8_t* x, int64_t ld_x, float a_scale,
+                                  const int8_t* w, int64_t ld_w, const float* w_scale, const float* bias, int act,
+                                  const float* res, int64_t ld_res, int64_t res_rows, void* out, int out_dtype,
+                                  float out_scale, int64_t ld_out, hipStream_t stream) {
+  const char* who = "cortex_linear_w8a8";
+  CORTEX_CHECK_ARG(M >= 0 && N > 0 && K > 0, "%s: need M >= 0, N > 0, K > 0", who);
+  if (M == 0) return OK;
+  CORTEX_CHECK_ARG(M <= 0x7fffffffLL && N <= 0x7fffffffLL && K <= 0x7fffffffLL, "%s: size too large", who);
+  CORTEX_CHECK_ARG(K % 128 == 0 && N % 8 == 0, "%s: K must be a multiple of 128 and N of 8", who);
+  CORTEX_CHECK_ARG(act == ACT_NONE || act == ACT_GELU, "%s: act must be 0 (none) or 1 (GELU)", who);
+  CORTEX_CHECK_ARG(out_dtype == DT_F32 || out_dtype == DT_I8, "%s: out must be fp32 or int8", who);
+  CORTEX_CHECK_ARG(!(res && (out_dtype != DT_F32 || act != ACT_NONE)), "%s: a residual needs fp32 out and no act", who);
+  CORTEX_CHECK_ARG(x && w && out && a_scale > 0.0f && (out_dtype == DT_F32 || out_scale > 0.0f),
+                   "%s: null pointer or non-positive scale", who);
+  CORTEX_CHECK_ARG(res_rows >= 0 && ld_x >= K && ld_w >= K && ld_out >= N && (!res || ld_res >= N),
+                   "%s: row strides too small", who);
+  CORTEX_CHECK_ARG(aligned16(x) && aligned16(w) && ld_x % 16 == 0 && ld_w % 16 == 0 && aligned16(out) &&
+                       ld_out % 8 == 0 && (!w_scale || aligned16(w_scale)) && (!bias || aligned16(bias)) &&
+                       (!res || (aligned16(res) && ld_res % 4 == 0)),
+                   "%s: operands must be 16-byte aligned rows", who);
+  GemmArgs g = {};
+  g.M = M;
+  g.N = N;
+  g.K = K;
+  g.x = x;
+  g.ld_x = ld_x;
+  g.w = w;
+  g.ld_w = ld_w;
+  g.w_scale = w_scale;
+  g.bias = bias;
+  g.bias_dtype = DT_F32;
+  g.act = act;
+  g.res = res;
+  g.res_dtype = DT_F32;
+  g.ld_res = ld_res;
+  g.res_rows = res_rows;
+  g.out = out;
+  g.out_dtype = out_dtype;
+  g.ld_out = ld_out;
+  g.vec = 1;
+  g.a_scale = a_scale;
+  g.out_inv_scale = out_dtype == DT_I8 ? 1.0f / out_scale : 0.0f;
+  const int ncu = cu_count();
+  const int64_t t128 = cdiv(M, 128) * cdiv(N, 128), t256 = cdiv(M, 256) * cdiv(N, 256);
+  int st;
+  if (out_dtype == DT_I8) {
+    const bool big = N % 256 == 0 && t256 >= ncu * 15 / 16;
+    if (act == ACT_GELU)
+      st = big ? launch<B256x256s2, ACT_GELU, false, int8_t, int8_t>(g, stream)
+               : launch<B128x128s2, ACT_GELU, false, int8_t, int8_t>(g, stream);
+    else
+      st = big ? launch<B256x256s2, ACT_NONE, false, int8_t, int8_t>(g, stream)
+               : launch<B128x128s2, ACT_NONE, false, int8_t, int8_t>(g, stream);
+  } else if (res) {
+    st = (K % 256 == 0 && t128 <= ncu) ? launch<B128x128s2k2, ACT_NONE, true, float, int8_t>(g, stream)
+                                       : launch<B128x128s2, ACT_NONE, true, float, int8_t>(g, stream);
+  } else {
+    st = act == ACT_GELU ? launch<B128x128s2, ACT_GELU, false, float, int8_t>(g, stream)
+                         : launch<B128x128s2, ACT_NONE, false, float, int8_t>(g, stream);
+  }
+  if (st < 0) return st;
+  if (st == 0) {
+    set_error("%s: grid too large", who);
+    return E_INVALID;
+  }
+  return OK;
+}

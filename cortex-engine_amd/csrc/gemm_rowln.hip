@@ -2,6 +2,7 @@
 //
 //   out[m, :] = res[m % res_rows, :] + (A[m, :] . W^T) * w_scale (+ bias)     fp32
 //   xn[m, :]  = LN(out[m, :]) * gamma + beta                                   bf16
+//               (or, for the opt-in W8A8 mode, int8: clamp(rint(LN(..) / xq_scale), +-127))
 //
 // This is SelfAttentionBlock's  x = x + out_proj(attn);  h_in = norm_mlp(x)
 // (reference cortex/models/perceiver.py:121-124), and the cross-attention block's
@@ -66,11 +67,12 @@ struct RowLnArgs {
   const float* gamma;
   const float* beta;
   float eps;
-  bf16* xn;
+  void* xn;  // bf16, or int8 when Q8
   int64_t ld_xn;
+  float xq_inv_scale;  // Q8: 1 / activation scale of the consumer
 };
 
-template <int BN, int S>
+template <int BN, int S, bool Q8 = false>
 __global__ __launch_bounds__(RL_THREADS) void gemm_rowln_kernel(RowLnArgs g) {
   constexpr int WN = BN / RL_WAVES;   // columns per wavefront
   constexpr int TM = RL_BM / 16, TN = WN / 16;
@@ -298,12 +300,24 @@ __global__ __launch_bounds__(RL_THREADS) void gemm_rowln_kernel(RowLnArgs g) {
     for (int i = 0; i < TM; ++i) {
       const int m = m0 + i * 16 + fr;
       if (m >= M) continue;
-      bf16x4 o;
-      o[0] = (bf16)((v[i][j][0] - mean[i]) * rstd[i] * gm.x + be.x);
-      o[1] = (bf16)((v[i][j][1] - mean[i]) * rstd[i] * gm.y + be.y);
-      o[2] = (bf16)((v[i][j][2] - mean[i]) * rstd[i] * gm.z + be.z);
-      o[3] = (bf16)((v[i][j][3] - mean[i]) * rstd[i] * gm.w + be.w);
-      *reinterpret_cast<bf16x4*>(g.xn + (int64_t)m * g.ld_xn + n) = o;
+      const float y0 = (v[i][j][0] - mean[i]) * rstd[i] * gm.x + be.x;
+      const float y1 = (v[i][j][1] - mean[i]) * rstd[i] * gm.y + be.y;
+      const float y2 = (v[i][j][2] - mean[i]) * rstd[i] * gm.z + be.z;
+      const float y3 = (v[i][j][3] - mean[i]) * rstd[i] * gm.w + be.w;
+      if constexpr (Q8) {
+        auto q = [&](float y) {
+          return (uint32_t)((int)fminf(fmaxf(rintf(y * g.xq_inv_scale), -127.0f), 127.0f) & 0xff);
+        };
+        *reinterpret_cast<uint32_t*>(reinterpret_cast<int8_t*>(g.xn) + (int64_t)m * g.ld_xn + n) =
+            q(y0) | (q(y1) << 8) | (q(y2) << 16) | (q(y3) << 24);
+      } else {
+        bf16x4 o;
+        o[0] = (bf16)y0;
+        o[1] = (bf16)y1;
+        o[2] = (bf16)y2;
+        o[3] = (bf16)y3;
+        *reinterpret_cast<bf16x4*>(reinterpret_cast<bf16*>(g.xn) + (int64_t)m * g.ld_xn + n) = o;
+      }
     }
   }
 }
@@ -316,31 +330,61 @@ bool a16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
 using namespace cortex;
 
+namespace {
+
+int residual_ln(const char* who, int64_t M, int64_t N, int64_t K, const void* x, int64_t ld_x, const void* w,
+                int64_t ld_w, const float* w_scale, const float* bias, const float* res, int64_t ld_res,
+                int64_t res_rows, float* out, int64_t ld_out, const float* gamma, const float* beta, float eps,
+                void* xn, int64_t ld_xn, float xq_scale, bool q8, hipStream_t stream) {
+  CORTEX_CHECK_ARG(M >= 0 && K > 0, "%s: need M >= 0 and K > 0", who);
+  CORTEX_CHECK_ARG(N == 256 || N == 512, "%s: N must be 256 or 512 (got %lld)", who, (long long)N);
+  CORTEX_CHECK_ARG(K % RL_BK == 0 && K <= 0x7fffffffLL, "%s: K must be a multiple of 64", who);
+  if (M == 0) return OK;
+  CORTEX_CHECK_ARG(M <= 0x7fffffffLL - RL_BM, "%s: M too large", who);
+  CORTEX_CHECK_ARG(x && w && res && out && gamma && beta && xn, "%s: null pointer", who);
+  CORTEX_CHECK_ARG(res_rows >= 0, "%s: res_rows must be >= 0", who);
+  CORTEX_CHECK_ARG(!q8 || xq_scale > 0.0f, "%s: the int8 scale must be positive", who);
+  CORTEX_CHECK_ARG(ld_x >= K && ld_w >= K && ld_res >= N && ld_out >= N && ld_xn >= N, "%s: row strides too small",
+                   who);
+  CORTEX_CHECK_ARG(a16(x) && a16(w) && a16(res) && a16(out) && a16(xn) && a16(gamma) && a16(beta) &&
+                       (!w_scale || a16(w_scale)) && (!bias || a16(bias)) && ld_x % 8 == 0 && ld_w % 8 == 0 &&
+                       ld_res % 4 == 0 && ld_out % 4 == 0 && ld_xn % (q8 ? 16 : 8) == 0,
+                   "%s: operands must be 16-byte aligned rows", who);
+  RowLnArgs a{M,     N,      K,      reinterpret_cast<const bf16*>(x), ld_x, reinterpret_cast<const bf16*>(w),
+              ld_w,  w_scale, bias,  res,   ld_res, res_rows, out,  ld_out, gamma, beta, eps, xn, ld_xn,
+              q8 ? 1.0f / xq_scale : 0.0f};
+  const dim3 grid((unsigned)cdiv(M, (int64_t)RL_BM));
+  if (N == 512) {
+    if (q8)
+      hipLaunchKernelGGL((gemm_rowln_kernel<512, 2, true>), grid, dim3(RL_THREADS), 0, stream, a);
+    else
+      hipLaunchKernelGGL((gemm_rowln_kernel<512, 2>), grid, dim3(RL_THREADS), 0, stream, a);
+  } else {
+    if (q8)
+      hipLaunchKernelGGL((gemm_rowln_kernel<256, 3, true>), grid, dim3(RL_THREADS), 0, stream, a);
+    else
+      hipLaunchKernelGGL((gemm_rowln_kernel<256, 3>), grid, dim3(RL_THREADS), 0, stream, a);
+  }
+  CORTEX_CHECK_LAUNCH("gemm_rowln_kernel");
+  return OK;
+}
+
+}  // namespace
+
 extern "C" int cortex_linear_residual_ln(int64_t M, int64_t N, int64_t K, const void* x, int64_t ld_x, const void* w,
                                          int64_t ld_w, const float* w_scale, const float* bias, const float* res,
                                          int64_t ld_res, int64_t res_rows, float* out, int64_t ld_out,
                                          const float* gamma, const float* beta, float eps, void* xn, int64_t ld_xn,
                                          hipStream_t stream) {
-  CORTEX_CHECK_ARG(M >= 0 && K > 0, "cortex_linear_residual_ln: need M >= 0 and K > 0");
-  CORTEX_CHECK_ARG(N == 256 || N == 512, "cortex_linear_residual_ln: N must be 256 or 512 (got %lld)", (long long)N);
-  CORTEX_CHECK_ARG(K % RL_BK == 0 && K <= 0x7fffffffLL, "cortex_linear_residual_ln: K must be a multiple of 64");
-  if (M == 0) return OK;
-  CORTEX_CHECK_ARG(M <= 0x7fffffffLL - RL_BM, "cortex_linear_residual_ln: M too large");
-  CORTEX_CHECK_ARG(x && w && res && out && gamma && beta && xn, "cortex_linear_residual_ln: null pointer");
-  CORTEX_CHECK_ARG(res_rows >= 0, "cortex_linear_residual_ln: res_rows must be >= 0");
-  CORTEX_CHECK_ARG(ld_x >= K && ld_w >= K && ld_res >= N && ld_out >= N && ld_xn >= N,
-                   "cortex_linear_residual_ln: row strides too small");
-  CORTEX_CHECK_ARG(a16(x) && a16(w) && a16(res) && a16(out) && a16(xn) && a16(gamma) && a16(beta) &&
-                       (!w_scale || a16(w_scale)) && (!bias || a16(bias)) && ld_x % 8 == 0 && ld_w % 8 == 0 &&
-                       ld_res % 4 == 0 && ld_out % 4 == 0 && ld_xn % 8 == 0,
-                   "cortex_linear_residual_ln: operands must be 16-byte aligned rows");
-  RowLnArgs a{M, N, K, reinterpret_cast<const bf16*>(x), ld_x, reinterpret_cast<const bf16*>(w), ld_w, w_scale,
-              bias, res, ld_res, res_rows, out, ld_out, gamma, beta, eps, reinterpret_cast<bf16*>(xn), ld_xn};
-  const dim3 grid((unsigned)cdiv(M, (int64_t)RL_BM));
-  if (N == 512)
-    hipLaunchKernelGGL((gemm_rowln_kernel<512, 2>), grid, dim3(RL_THREADS), 0, stream, a);
-  else
-    hipLaunchKernelGGL((gemm_rowln_kernel<256, 3>), grid, dim3(RL_THREADS), 0, stream, a);
-  CORTEX_CHECK_LAUNCH("gemm_rowln_kernel");
-  return OK;
+  return residual_ln("cortex_linear_residual_ln", M, N, K, x, ld_x, w, ld_w, w_scale, bias, res, ld_res, res_rows,
+                     out, ld_out, gamma, beta, eps, xn, ld_xn, 0.0f, false, stream);
+}
+
+extern "C" int cortex_linear_residual_ln_i8(int64_t M, int64_t N, int64_t K, const void* x, int64_t ld_x,
+                                            const void* w, int64_t ld_w, const float* w_scale, const float* bias,
+                                            const float* res, int64_t ld_res, int64_t res_rows, float* out,
+                                            int64_t ld_out, const float* gamma, const float* beta, float eps,
+                                            int8_t* xq, int64_t ld_xq, float xq_scale, hipStream_t stream) {
+  return residual_ln("cortex_linear_residual_ln_i8", M, N, K, x, ld_x, w, ld_w, w_scale, bias, res, ld_res,
+                     res_rows, out, ld_out, gamma, beta, eps, xq, ld_xq, xq_scale, true, stream);
 }

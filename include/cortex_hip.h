@@ -225,6 +225,31 @@ int cortex_linear_residual_ln(int64_t M, int64_t N, int64_t K, const void* x, in
                               int64_t ld_res, int64_t res_rows, float* out, int64_t ld_out, const float* gamma,
                               const float* beta, float eps, void* xn, int64_t ld_xn, hipStream_t stream);
 
+/* Opt-in W8A8 mode.  The reference derives a per-tensor activation scale per linear
+ * (derive_scales, cortex/quantization/calibrate.py:145-150: 99th-percentile absmax / 127)
+ * and never applies it (QuantizedLinear.forward dequantises the weight, :225-228); these
+ * entry points apply it, for callers that accept int8 activations:
+ *   q(y; s) = clamp(rint(y * (1 / s)), -127, 127)   (round half to even; 1/s in fp32)
+ *
+ * cortex_linear_residual_ln_i8: cortex_linear_residual_ln with the LayerNorm'd row
+ * written as int8, xq[m, n] = q(LN(out[m, :])[n]; xq_scale); ld_xq a multiple of 16. */
+int cortex_linear_residual_ln_i8(int64_t M, int64_t N, int64_t K, const void* x, int64_t ld_x, const void* w,
+                                 int64_t ld_w, const float* w_scale, const float* bias, const float* res,
+                                 int64_t ld_res, int64_t res_rows, float* out, int64_t ld_out, const float* gamma,
+                                 const float* beta, float eps, int8_t* xq, int64_t ld_xq, float xq_scale,
+                                 hipStream_t stream);
+
+/* cortex_linear_w8a8: y[m, n] = a_scale * w_scale[n] * sum_k x[m, k] w[n, k] + bias[n]
+ * with x (M, K) int8 activations and w the (N, K) int8 weight of a QuantizedLinear, summed
+ * exactly in int32 (v_mfma_i32_16x16x64_i8); act 1 applies the erf-GELU.  out_dtype 0:
+ * fp32 out[m, n] = y (+ res[(m % res_rows), n], act 0 only; out may be res); out_dtype 3:
+ * int8 out[m, n] = q(y; out_scale), the next linear's activation.  K % 128 == 0, N % 8 == 0;
+ * 16-byte aligned rows (ld_x, ld_w multiples of 16, ld_out of 8). */
+int cortex_linear_w8a8(int64_t M, int64_t N, int64_t K, const int8_t* x, int64_t ld_x, float a_scale, const int8_t* w,
+                       int64_t ld_w, const float* w_scale, const float* bias, int act, const float* res,
+                       int64_t ld_res, int64_t res_rows, void* out, int out_dtype, float out_scale, int64_t ld_out,
+                       hipStream_t stream);
+
 /* Behaviour head (BehaviorDecoder.forward, cortex/models/cortex.py:29-53) with its
  * batch-invariant factors folded: cortex_head_prep builds, once per parameter state,
  * the (32, D) bf16 matrix ac of rows a_{q,h} = W_k[h]^T q_h * log2(e)/sqrt(Dh) (rows
