@@ -536,18 +536,36 @@ extern "C" int cortex_linear_w8a8(int64_t M, int64_t N, int64_t K, const int8_t*
   g.out_inv_scale = out_dtype == DT_I8 ? 1.0f / out_scale : 0.0f;
   const int ncu = cu_count();
   const int64_t t128 = cdiv(M, 128) * cdiv(N, 128), t256 = cdiv(M, 256) * cdiv(N, 256);
+  static const int tile_env = [] {
+    const char* e = getenv("CORTEX_W8A8_TILE");
+    return e ? atoi(e) : -1;
+  }();
   int st;
   if (out_dtype == DT_I8) {
-    const bool big = N % 256 == 0 && t256 >= ncu * 15 / 16;
-    if (act == ACT_GELU)
-      st = big ? launch<B256x256s2, ACT_GELU, false, int8_t, int8_t>(g, stream)
-               : launch<B128x128s2, ACT_GELU, false, int8_t, int8_t>(g, stream);
-    else
-      st = big ? launch<B256x256s2, ACT_NONE, false, int8_t, int8_t>(g, stream)
-               : launch<B128x128s2, ACT_NONE, false, int8_t, int8_t>(g, stream);
+    int t = tile_env;
+    if (t < 0) t = (N % 256 == 0 && t256 >= ncu * 15 / 16) ? 4 : 0;
+    if (act == ACT_GELU) {
+      switch (t) {
+        case 4: st = launch<B256x256s2, ACT_GELU, false, int8_t, int8_t>(g, stream); break;
+        case 2: st = launch<B256x128s2, ACT_GELU, false, int8_t, int8_t>(g, stream); break;
+        case 3: st = launch<B128x256s2, ACT_GELU, false, int8_t, int8_t>(g, stream); break;
+        case 1: st = launch<B128x128s3, ACT_GELU, false, int8_t, int8_t>(g, stream); break;
+        default: st = launch<B128x128s2, ACT_GELU, false, int8_t, int8_t>(g, stream); break;
+      }
+    } else {
+      st = t == 4 ? launch<B256x256s2, ACT_NONE, false, int8_t, int8_t>(g, stream)
+                  : launch<B128x128s2, ACT_NONE, false, int8_t, int8_t>(g, stream);
+    }
   } else if (res) {
-    st = (K % 256 == 0 && t128 <= ncu) ? launch<B128x128s2k2, ACT_NONE, true, float, int8_t>(g, stream)
-                                       : launch<B128x128s2, ACT_NONE, true, float, int8_t>(g, stream);
+    int t = tile_env;
+    if (t < 0) t = (K % 256 == 0 && t128 <= ncu) ? 7 : 0;
+    switch (t) {
+      case 7: st = K % 256 ? 0 : launch<B128x128s2k2, ACT_NONE, true, float, int8_t>(g, stream); break;
+      case 2: st = launch<B256x128s2, ACT_NONE, true, float, int8_t>(g, stream); break;
+      case 5: st = launch<B64x128s2, ACT_NONE, true, float, int8_t>(g, stream); break;
+      case 1: st = launch<B128x128s3, ACT_NONE, true, float, int8_t>(g, stream); break;
+      default: st = launch<B128x128s2, ACT_NONE, true, float, int8_t>(g, stream); break;
+    }
   } else {
     st = act == ACT_GELU ? launch<B128x128s2, ACT_GELU, false, float, int8_t>(g, stream)
                          : launch<B128x128s2, ACT_NONE, false, float, int8_t>(g, stream);
