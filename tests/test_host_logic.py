@@ -125,3 +125,32 @@ def test_kernels_refuse_cpu_tensors():
         model(i, i, i, i)
     with pytest.raises(ValueError, match="shape mismatch"):
         model.tokenizer(i, i[:-1], i)
+
+
+def test_w8a8_enable_disable_bookkeeping():
+    """enable_w8a8 switches exactly the blocks whose two MLP linears are QuantizedLinear with
+    positive calibrated scales, keeps the state_dict unchanged, and disable_w8a8 undoes it."""
+    from cortex.models import CortexModel
+    from cortex.models.config import CORTEX_XS
+    from cortex.quantization.calibrate import LayerScales, QuantizedLinear
+    from cortex.quantization.w8a8 import disable_w8a8, enable_w8a8, w8a8_scales
+
+    model = CortexModel(CORTEX_XS)
+    blocks = list(model.encoder.self_attn_blocks)
+    scales = {}
+    for i, blk in enumerate(blocks):
+        for j in (0, 2):
+            lin = blk.mlp[j]
+            q, s = O.quantize_int8(lin.weight.detach().numpy())
+            bias = None if lin.bias is None else lin.bias.detach().clone()
+            blk.mlp[j] = QuantizedLinear(torch.from_numpy(q), torch.from_numpy(s), bias)
+            scales[f"encoder.self_attn_blocks.{i}.mlp.{j}"] = LayerScales(torch.from_numpy(s), 0.01 * (i + 1) + j)
+    keys = set(model.state_dict())
+    del scales["encoder.self_attn_blocks.1.mlp.2"]  # no calibration data for one linear: that block stays
+    scales["encoder.self_attn_blocks.2.mlp.0"] = LayerScales(torch.ones(1), 0.0)  # a zero scale: stays too
+    assert enable_w8a8(model, scales) == len(blocks) - 2
+    assert w8a8_scales(blocks[0]) == (0.01, 2.01) and w8a8_scales(blocks[1]) is None
+    assert w8a8_scales(blocks[2]) is None
+    assert set(model.state_dict()) == keys
+    disable_w8a8(model)
+    assert all(w8a8_scales(b) is None for b in blocks)
