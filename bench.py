@@ -491,6 +491,44 @@ def norm_linear_api(dev, M: int = 8192, K: int = 512, widths=(1536, 2048, 512)) 
     return {"M": M, "K": K, **out}
 
 
+def api_configs(dev) -> dict:
+    """The kernel-level workloads through the public API (graph-replayed, microseconds per
+    call), each with the roofline fraction of its algorithmic work:
+
+    * tokenize + pack, fp32 tables 137/600/8 x 512, B = 32 with E_b ~ U{128..512}: bytes =
+      E (D 4 + 4 x 8) + tables + (B + 1) 8 (token rows written, four int64 indices read);
+      CSR rows and the padded (B, E_max, D) + mask layout;
+    * sparse cross-attention, bf16, q (32, 8, 256, 64), k / v (32, 8, 512, 64) ~ N(0,1)/8,
+      true lengths U{128..512} per sample: FLOPs = 4 H L Dh sum(E_b) (the padding is skipped)."""
+    from cortex.kernels.sparse_xattn import sparse_cross_attention
+    from cortex.kernels.tokenizer import tokenize_and_pack
+
+    rng = np.random.default_rng(0)
+    B, D = 32, 512
+    counts = rng.integers(128, 513, B)
+    E = int(counts.sum())
+    ev = [torch.from_numpy(a).to(dev) for a in (rng.integers(0, 137, E), rng.integers(0, 600, E),
+                                                 np.clip(rng.poisson(1.0, E) + 1, 0, 7), np.repeat(np.arange(B), counts))]
+    tables = [torch.from_numpy(rng.normal(0, 0.02, (n, D)).astype(np.float32)).to(dev) for n in (137, 600, 8)]
+    t_csr = time_launches(lambda: tokenize_and_pack(*tables, *ev, batch_size=B))
+    t_pad = time_launches(lambda: tokenize_and_pack(*tables, *ev, batch_size=B, layout="padded",
+                                                    max_events=int(counts.max())))
+    bytes0 = E * (D * 4 + 4 * 8) + (137 + 600 + 8) * D * 4 + (B + 1) * 8
+    H, L, Dh, Ek = 8, 256, 64, 512
+    g = torch.Generator(device="cpu").manual_seed(1)
+    q, k, v = ((torch.randn(B, H, n, Dh, generator=g) / 8).bfloat16().to(dev) for n in (L, Ek, Ek))
+    lens = torch.from_numpy(rng.integers(128, 513, B)).to(dev)
+    t_x = time_launches(lambda: sparse_cross_attention(q, k, v, kv_lengths=lens))
+    fl = 4.0 * H * L * Dh * float(lens.sum())
+    return {
+        "tokenize_pack_fp32": {"events": E, "csr_us": round(t_csr * 1e6, 2), "padded_us": round(t_pad * 1e6, 2),
+                               "algorithmic_bytes": bytes0, "csr_GBps": round(bytes0 / t_csr / 1e9, 1),
+                               "csr_hbm_frac": round(bytes0 / t_csr / 1e9 / HBM_PEAK_GBS, 4)},
+        "sparse_cross_attention_bf16": {"us": round(t_x * 1e6, 2), "flops": fl, "tflops": round(fl / t_x / 1e12, 1),
+                                        "mfma_frac": round(fl / t_x / 1e12 / BF16_PEAK_TFLOPS, 4)},
+    }
+
+
 def w8a8_forward(model, scales, dev, inputs, reference: torch.Tensor, reps: int = 50) -> dict:
     """The opt-in W8A8 MLPs (cortex.quantization.w8a8) on the same B = 32 x 512 forward:
     samples/s (graph replay) and the largest difference to the default path's behaviour."""
@@ -663,6 +701,8 @@ def main() -> int:
         log(f"bench: streaming {extra['streaming']}")
         extra["norm_linear_api"] = norm_linear_api(dev)
         log(f"bench: norm + linear API {extra['norm_linear_api']}")
+        extra["api_configs"] = api_configs(dev)
+        log(f"bench: API configurations {extra['api_configs']}")
         extra["w8a8"] = w8a8_forward(model, scales, dev, inputs, cap(*inputs).clone())
         log(f"bench: w8a8 {extra['w8a8']}")
     cpu = None

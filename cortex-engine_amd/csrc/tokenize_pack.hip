@@ -181,14 +181,62 @@ constexpr int PS_MAX_B = 1024;
 constexpr int64_t PS_MAX_E = 65536;
 constexpr int PS_UNROLL = 16;
 
+// Sorted batch indices (the collate order) need no sort: the plan is the identity and
+// offsets[s] is the first event of sample s.  One workgroup per PS_SORTED_EV events writes
+// order / dst_rows = identity and the offsets of the sample boundaries inside its range
+// (each offsets[s] is written by exactly one event when the whole array is sorted), and
+// records in status[blockIdx.x] whether its range (with the event before it) was sorted
+// and in range: 1 yes, 2 no.  pack_small_kernel then returns at once when every status is 1
+// and otherwise recomputes the whole plan.
+constexpr int PS_SORTED_EV = 1024;
+
+__global__ __launch_bounds__(256) void pack_sorted_kernel(const int64_t* __restrict__ bidx, int64_t s_bidx,
+                                                          int64_t E, int B, int64_t* __restrict__ offsets,
+                                                          int64_t* __restrict__ order, int64_t* __restrict__ dst_rows,
+                                                          int* __restrict__ status) {
+  __shared__ int bad;
+  if (threadIdx.x == 0) bad = 0;
+  __syncthreads();
+  const int64_t c0 = (int64_t)blockIdx.x * PS_SORTED_EV;
+  bool my_bad = false;
+  for (int k = threadIdx.x; k < PS_SORTED_EV; k += blockDim.x) {
+    const int64_t e = c0 + k;
+    if (e >= E) break;
+    const int64_t b = bidx[e * s_bidx];
+    const int64_t bp = e > 0 ? bidx[(e - 1) * s_bidx] : -1;
+    if (b < 0 || b >= B || bp > b) {
+      my_bad = true;
+      continue;
+    }
+    order[e] = e;
+    if (dst_rows) dst_rows[e] = e;
+    for (int64_t s = bp + 1; s <= b; ++s) offsets[s] = e;  // samples bp+1 .. b start at e (empty ones too)
+    if (e == E - 1)
+      for (int64_t s = b + 1; s <= B; ++s) offsets[s] = E;
+  }
+  if (my_bad) bad = 1;
+  __syncthreads();
+  if (threadIdx.x == 0) status[blockIdx.x] = bad ? 2 : 1;
+}
+
 __global__ __launch_bounds__(1024) void pack_small_kernel(const int64_t* __restrict__ bidx, int64_t s_bidx, int64_t E,
                                                           int B, int64_t* __restrict__ offsets,
                                                           int64_t* __restrict__ order, int64_t* __restrict__ dst_rows,
-                                                          int64_t* __restrict__ rank, int32_t* __restrict__ err) {
+                                                          int64_t* __restrict__ rank, int32_t* __restrict__ err,
+                                                          const int* __restrict__ status, int n_status) {
   __shared__ int cnt[PS_WAVES * PS_MAX_B];  // per-wave counts, then per-wave next CSR row
   __shared__ int first[PS_MAX_B];           // CSR offset of each sample
   __shared__ int wsum[PS_WAVES];
+  __shared__ int unsorted;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  if (status) {  // after pack_sorted_kernel: nothing left to do when every range was sorted
+    if (tid == 0) unsorted = 0;
+    __syncthreads();
+    for (int i = tid; i < n_status; i += blockDim.x)
+      if (status[i] != 1) unsorted = 1;
+    __syncthreads();
+    if (!unsorted) return;
+  }
   for (int i = tid; i < PS_WAVES * B; i += blockDim.x) cnt[i] = 0;
   __syncthreads();
   const int64_t C = cdiv(E, (int64_t)PS_WAVES);
@@ -476,8 +524,19 @@ int cortex_pack_plan(const int64_t* batch_indices, int64_t s_bidx, int64_t E, in
     return E_WORKSPACE;
   }
   if (B <= PS_MAX_B && E <= PS_MAX_E) {
+    // without ranks, try the sorted fast path first (one status word per 1024 events, in the
+    // workspace: cortex_pack_workspace_bytes covers them); pack_small_kernel finishes the
+    // plan only when some range was not sorted
+    int* status = nullptr;
+    const int n_status = (int)cdiv(E, (int64_t)PS_SORTED_EV);
+    if (rank == nullptr && workspace != nullptr && workspace_bytes >= n_status * (int64_t)sizeof(int)) {
+      status = reinterpret_cast<int*>(workspace);
+      hipLaunchKernelGGL(pack_sorted_kernel, dim3((unsigned)n_status), dim3(256), 0, stream, batch_indices, s_bidx, E,
+                         (int)B, offsets, order, dst_rows, status);
+      CORTEX_CHECK_LAUNCH("pack_sorted_kernel");
+    }
     hipLaunchKernelGGL(pack_small_kernel, dim3(1), dim3(64 * PS_WAVES), 0, stream, batch_indices, s_bidx, E, (int)B,
-                       offsets, order, dst_rows, rank, err_flag);
+                       offsets, order, dst_rows, rank, err_flag, status, n_status);
     CORTEX_CHECK_LAUNCH("pack_small_kernel");
     return OK;
   }

@@ -41,7 +41,10 @@ const char* cortex_last_error(void);
  *   order    (E)    source event of every CSR row (stable in event order)
  *   dst_rows (E)    CSR row of every event (nullable)
  *   rank     (E)    position of every event inside its sample (nullable)
- * workspace: at least cortex_pack_workspace_bytes(E, B) bytes of device memory. */
+ * workspace: at least cortex_pack_workspace_bytes(E, B) bytes of device memory.
+ * Sorted batch indices (the collate order) are recognised on the device when rank is
+ * null: the identity plan is written by one launch over all events and the general plan
+ * runs only where some 1024-event range was not sorted or held an index out of range. */
 int64_t cortex_pack_workspace_bytes(int64_t E, int64_t B);
 int cortex_pack_plan(const int64_t* batch_indices, int64_t s_bidx, int64_t E, int64_t B, int64_t* offsets,
                      int64_t* order, int64_t* dst_rows, int64_t* rank, void* workspace, int64_t workspace_bytes,

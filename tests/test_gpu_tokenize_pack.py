@@ -216,3 +216,43 @@ def test_tokenize_ln_matches_tokens_then_layernorm(D):
     assert bool((diff <= _bf16_ulp(ref) + 1e-5 * float(ref.abs().max())).all())
     r_bad = int(np.nonzero(ordr == 17)[0][0])
     torch.testing.assert_close(out[r_bad].float().cpu(), b.bfloat16().float(), rtol=0, atol=0)
+
+
+def _sorted_cases():
+    rng = np.random.default_rng(5)
+    cases = {}
+    b = np.sort(rng.integers(3, 40, 5000))  # empty samples 0-2, gaps in the middle, empty tail up to B = 50
+    cases["gaps"] = (b, 50)
+    b = np.sort(rng.integers(0, 8, 4096))
+    b[1023], b[1024] = b[1024], b[1023] - 1 if b[1023] > 0 else 1  # one inversion across the 1024-event boundary
+    cases["inversion_at_range_edge"] = (b, 8)
+    b = np.sort(rng.integers(0, 16, 3000))
+    b[2999] = 16  # sorted but the last index is out of range
+    cases["out_of_range_tail"] = (b, 16)
+    cases["single_event"] = (np.array([2]), 5)
+    cases["one_sample"] = (np.zeros(65536, dtype=np.int64), 1)
+    cases["all_distinct_1024"] = (np.arange(1024), 1024)
+    return cases
+
+
+@pytest.mark.parametrize("name", list(_sorted_cases()))
+def test_pack_plan_sorted_fast_path(name):
+    """Sorted batch indices take the identity plan (pack_sorted_kernel); anything else found
+    there -- an inversion, an index out of range -- falls back to the full plan.  Same
+    results as the oracle either way, with and without ranks."""
+    from cortex.kernels import ops
+
+    bidx, B = _sorted_cases()[name]
+    valid = (bidx >= 0) & (bidx < B)
+    p = O.pack_events(np.zeros((int(valid.sum()), 1), np.float32), bidx[valid], batch_size=B)
+    t = torch.from_numpy(bidx.astype(np.int64)).to(DEV)
+    for with_rank in (False, True):
+        err = torch.zeros(1, dtype=torch.int32, device=DEV)
+        off, order, rank = ops.pack_plan(t, B, err=err, with_rank=with_rank)
+        torch.cuda.synchronize()
+        assert bool(int(err.item()) & 2) == (not valid.all())
+        np.testing.assert_array_equal(off.cpu().numpy(), p.offsets)
+        n = int(p.offsets[-1])
+        np.testing.assert_array_equal(order.cpu().numpy()[:n], np.flatnonzero(valid)[p.order])
+        if with_rank:
+            np.testing.assert_array_equal(rank.cpu().numpy()[valid], p.rank)
