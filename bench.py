@@ -530,7 +530,7 @@ def api_configs(dev) -> dict:
 
 
 def w8a8_forward(model, scales, dev, inputs, reference: torch.Tensor, reps: int = 50) -> dict:
-    """The opt-in W8A8 MLPs (cortex.quantization.w8a8) on the same B = 32 x 512 forward:
+    """The opt-in W8A8 blocks (cortex.quantization.w8a8) on the same B = 32 x 512 forward:
     samples/s (graph replay) and the largest difference to the default path's behaviour."""
     from cortex.quantization.w8a8 import disable_w8a8, enable_w8a8
     from cortex.runtime import CapturedForward
@@ -552,8 +552,8 @@ def w8a8_forward(model, scales, dev, inputs, reference: torch.Tensor, reps: int 
         disable_w8a8(model)
     return {"blocks": n, "ms_per_forward": round(sec * 1e3, 4), "samples_per_s": round(B_MAIN / sec, 1),
             "max_abs_diff_vs_default": float((out - reference).abs().max()),
-            "note": "int8 activations in the self-attention MLPs (calibrated act_scale); not the reference's "
-                    "arithmetic, opt-in"}
+            "note": "int8 activations in the self-attention blocks (qkv, out_proj, both MLP linears; calibrated "
+                    "act_scale); not the reference's arithmetic, opt-in"}
 
 
 def cpu_baseline(model, budget_s: float = 12.0, b1_budget_s: float = 18.0):

@@ -320,6 +320,51 @@ def linear_w8a8(xq: torch.Tensor, a_scale: float, weight_int8: torch.Tensor, wei
     return out
 
 
+def qkv_attention_w8a8(xq: torch.Tensor, a_scale: float, w_int8: torch.Tensor, w_scale, bias, batch: int,
+                       length: int, heads: int, *, out_dtype: torch.dtype = torch.bfloat16,
+                       out_scale: float | None = None) -> torch.Tensor:
+    """``qkv_attention`` in the W8A8 mode: int8 ``xq`` rows at ``a_scale`` and the int8 qkv
+    weight; the merged-head output as bf16 or, with ``out_dtype=torch.int8``, int8 at
+    ``out_scale``."""
+    dev = nat.require_gpu(xq, w_int8, w_scale, bias, what="qkv_attention_w8a8")
+    M, D = xq.shape
+    out = torch.empty((M, D), dtype=out_dtype, device=dev)
+    nat.call("cortex_qkv_attention_w8a8", int(batch), int(length), D, int(heads), nat.ptr(xq), xq.stride(0),
+             float(a_scale), nat.ptr(w_int8), w_int8.stride(0), nat.ptr(w_scale), nat.ptr(bias),
+             1.0 / math.sqrt(D // int(heads)), nat.ptr(out), nat.code(out_dtype), float(out_scale or 0.0),
+             out.stride(0), nat.stream_of(dev))
+    return out
+
+
+def linear_residual_ln_w8a8(xq: torch.Tensor, a_scale: float, w_int8: torch.Tensor, w_scale=None, bias=None, *,
+                            residual: torch.Tensor, ln, res_rows: int = 0, out: torch.Tensor | None = None,
+                            xn_dtype: torch.dtype = torch.bfloat16, xn_scale: float | None = None):
+    """``linear_residual_ln`` with int8 ``xq`` rows at ``a_scale`` and the int8 weight (W8A8);
+    ``LN(out)`` as bf16 or, with ``xn_dtype=torch.int8``, int8 at ``xn_scale``."""
+    dev = nat.require_gpu(xq, w_int8, w_scale, bias, residual, out, what="linear_residual_ln_w8a8")
+    M, K = xq.shape
+    N = w_int8.shape[0]
+    if out is None:
+        out = torch.empty((M, N), dtype=torch.float32, device=dev)
+    xn = torch.empty((M, N), dtype=xn_dtype, device=dev)
+    g, b, eps = ln
+    nat.call("cortex_linear_residual_ln_w8a8", M, N, K, nat.ptr(xq), xq.stride(0), float(a_scale), nat.ptr(w_int8),
+             w_int8.stride(0), nat.ptr(w_scale), nat.ptr(bias), nat.ptr(residual), residual.stride(0), int(res_rows),
+             nat.ptr(out), out.stride(0), nat.ptr(g), nat.ptr(b), float(eps), nat.ptr(xn), nat.code(xn_dtype),
+             float(xn_scale or 0.0), xn.stride(0), nat.stream_of(dev))
+    return out, xn
+
+
+def ln_rows_i8(x: torch.Tensor, gamma, beta, eps: float, scale: float) -> torch.Tensor:
+    """``clamp(rint(LayerNorm(x) * (1 / scale)), -127, 127)`` as int8 rows (W8A8 operand)."""
+    dev = nat.require_gpu(x, gamma, beta, what="ln_rows_i8")
+    M, K = x.shape
+    out = torch.empty((M, K), dtype=torch.int8, device=dev)
+    nat.call("cortex_ln_rows_i8", M, K, nat.ptr(x), x.stride(0), nat.ptr(gamma), nat.ptr(beta), float(eps),
+             nat.ptr(out), out.stride(0), float(scale), nat.stream_of(dev))
+    return out
+
+
 def head_prep(q: torch.Tensor, kv_weight: torch.Tensor, kv_scale, out_weight: torch.Tensor, out_scale,
               num_heads: int) -> torch.Tensor:
     """Folded behaviour-head matrix (32, D) bf16 (see ``cortex_head_prep``) from the projected

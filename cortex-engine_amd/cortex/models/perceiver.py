@@ -92,6 +92,9 @@ class SelfAttentionBlock(nn.Module):
         compute = self.config.compute_dtype
         D = x.shape[1]
         H = self.num_heads
+        w8 = self._w8a8(x, compute)
+        if w8 is not None and w8[2] is not None and self._fused_attention_ok(x, length):
+            return self._forward_rows_w8a8(x, batch, length, inplace, w8)
         if self._fused_attention_ok(x, length):
             # qkv projection + attention per (head, sample) on chip: qkv never reaches HBM
             if xn is None:
@@ -108,7 +111,6 @@ class SelfAttentionBlock(nn.Module):
             ops.attention(ops.heads_view(qkv, batch, length, H, 0, D), ops.heads_view(qkv, batch, length, H, D, D),
                           ops.heads_view(qkv, batch, length, H, 2 * D, D), out=o)
         # each residual element is read and then written by the same lane: in place is safe
-        w8 = self._w8a8(x, compute)
         if w8 is not None:  # opt-in W8A8 MLP (cortex.quantization.w8a8): int8 activations end to end
             up, down = self.mlp[0], self.mlp[2]
             x, xq = linear_residual_ln(self.out_proj, o_buf, x, self.norm_mlp, out=x if inplace else None,
@@ -127,9 +129,11 @@ class SelfAttentionBlock(nn.Module):
         return apply_linear(self.mlp[2], h, residual=x, out_dtype=x.dtype, compute=compute,
                             out=x if inplace else None)
 
-    def _w8a8(self, x: torch.Tensor, compute: torch.dtype) -> tuple[float, float] | None:
-        """The MLP's activation scales when this block runs it as W8A8 (enabled, bf16 compute,
-        no calibration hooks, int8 weights with K a multiple of 128, fp32 biases)."""
+    def _w8a8(self, x: torch.Tensor, compute: torch.dtype) -> tuple | None:
+        """``(s_up, s_down, attn)`` activation scales when this block runs its MLP as W8A8
+        (enabled, bf16 compute, no calibration hooks, int8 weights with K a multiple of 128,
+        fp32 biases); ``attn`` = ``(s_qkv, s_out)`` when the attention half qualifies too
+        (int8 qkv / out weights, D = 512, no hooks on them or on norm_attn), else None."""
         from cortex.quantization.w8a8 import w8a8_scales
 
         w8 = w8a8_scales(self)
@@ -140,9 +144,34 @@ class SelfAttentionBlock(nn.Module):
             return None
         if up.weight_int8.shape[1] % 128 or down.weight_int8.shape[1] % 128 or up.weight_int8.shape[0] % 8:
             return None
-        if any(b is not None and b.dtype != torch.float32 for b in (up.bias, down.bias)):
+        lins = (up, down, self.qkv_proj, self.out_proj)
+        if any(getattr(m, "bias", None) is not None and m.bias.dtype != torch.float32 for m in lins):
             return None
-        return w8
+        attn = w8[2]
+        if attn is not None:
+            qkv, out = self.qkv_proj, self.out_proj
+            if (x.shape[1] != 512 or qkv._forward_pre_hooks or out._forward_pre_hooks
+                    or self.norm_attn._forward_pre_hooks or not hasattr(qkv, "weight_int8")
+                    or not hasattr(out, "weight_int8")):
+                attn = None
+        return (w8[0], w8[1], attn)
+
+    def _forward_rows_w8a8(self, x: torch.Tensor, batch: int, length: int, inplace: bool, w8: tuple) -> torch.Tensor:
+        """The whole block on int8 activations (W8A8 mode): norm_attn -> int8, qkv projection +
+        attention on int8 operands -> int8 output, out_proj + residual + norm_mlp -> int8, the
+        MLP as in forward_rows.  The fp32 residual stream and the softmax stay as they are."""
+        s_up, s_down, (s_qkv, s_out) = w8
+        qkv, outp, up, down = self.qkv_proj, self.out_proj, self.mlp[0], self.mlp[2]
+        na, nm = self.norm_attn, self.norm_mlp
+        xq = ops.ln_rows_i8(x, na.weight, na.bias, na.eps, s_qkv)
+        oq = ops.qkv_attention_w8a8(xq, s_qkv, qkv.weight_int8, qkv.weight_scale, qkv.bias, batch, length,
+                                    self.num_heads, out_dtype=torch.int8, out_scale=s_out)
+        x, hq_in = ops.linear_residual_ln_w8a8(oq, s_out, outp.weight_int8, outp.weight_scale, outp.bias, residual=x,
+                                               ln=(nm.weight, nm.bias, nm.eps), out=x if inplace else None,
+                                               xn_dtype=torch.int8, xn_scale=s_up)
+        hq = ops.linear_w8a8(hq_in, s_up, up.weight_int8, up.weight_scale, up.bias, act="gelu",
+                             out_dtype=torch.int8, out_scale=s_down)
+        return ops.linear_w8a8(hq, s_down, down.weight_int8, down.weight_scale, down.bias, residual=x, out=x)
 
     def _fused_attention_ok(self, x: torch.Tensor, length: int) -> bool:
         """Whether ``cortex_qkv_attention`` covers this block: bf16 compute, no calibration

@@ -15,6 +15,11 @@
 //
 // Attention as in attention_fast.hip: S^T = K Q^T, lane-local online softmax in the
 // exp2 domain with a lazily moved reference max, O^T = V^T P^T, row sums on the MFMA.
+//
+// The opt-in W8A8 form (TIN = int8_t) projects int8 xn rows (xn_f = a_scale * xn) with the
+// int8 qkv weight on v_mfma_i32_16x16x64_i8 (exact int32 sums, a_scale * w_scale in the
+// epilogue); the attention itself stays bf16.  With Q8OUT the merged-head output is written
+// as int8 at out_proj's activation scale, clamp(rint(o * out_inv_scale), -127, 127).
 #include <hip/hip_runtime.h>
 
 #include "common.h"
@@ -52,18 +57,24 @@ __device__ __forceinline__ int ba_key_of(int st, int r) { return 32 * (st >> 1) 
 
 struct QkvAttnArgs {
   int64_t B, L, D, H;
-  const bf16* xn;  // (B*L, D) rows
+  const void* xn;  // (B*L, D) rows, bf16 (int8 in the W8A8 form)
   int64_t ld_x;
-  const bf16* w;   // (3D, D) qkv weight image
+  const void* w;   // (3D, D) qkv weight image (the int8 weight in the W8A8 form)
   int64_t ld_w;
   const float* w_scale;  // (3D) or null
   const float* bias;     // (3D) or null
   float scale_log2;
-  bf16* out;  // o[b*L + l, h*64 + d]
+  void* out;  // o[b*L + l, h*64 + d], bf16 (or int8 with Q8OUT)
   int64_t ld_o;
+  float a_scale;        // W8A8: xn_f = a_scale * xn
+  float out_inv_scale;  // Q8OUT
 };
 
+template <class TIN = bf16, bool Q8OUT = false>
 __global__ __launch_bounds__(BA_THREADS) void qkv_attention_kernel(QkvAttnArgs a) {
+  using OP = Operand<TIN>;
+  typedef typename OP::frag frag;
+  constexpr int EPC = OP::EPC, BK = 8 * EPC;  // K elements per 16-byte chunk and per 128-byte LDS row
   __shared__ __attribute__((aligned(1024))) unsigned char smem[BA_LDS];
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int fr = lane & 15, g4 = lane >> 4;
@@ -82,24 +93,24 @@ __global__ __launch_bounds__(BA_THREADS) void qkv_attention_kernel(QkvAttnArgs a
   const int wm = wid / BA_WN, wn = wid % BA_WN;
   const int wrow = wm * (BA_L / BA_WM);
   auto tcol = [&](int j) { return 16 * (2 * j + wn); };
-  const bf16* a_src[BA_AB];
+  const TIN* a_src[BA_AB];
 #pragma unroll
   for (int i = 0; i < BA_AB; ++i) {
     const int r = (wid * BA_AB + i) * 8 + (lane >> 3);
-    a_src[i] = a.xn + (row0 + min(r, L - 1)) * a.ld_x + ((lane & 7) ^ ba_swz(r)) * 8;
+    a_src[i] = reinterpret_cast<const TIN*>(a.xn) + (row0 + min(r, L - 1)) * a.ld_x + ((lane & 7) ^ ba_swz(r)) * EPC;
   }
-  const bf16* w_src[BA_WB];
+  const TIN* w_src[BA_WB];
 #pragma unroll
   for (int i = 0; i < BA_WB; ++i) {
     const int r = (wid * BA_WB + i) * 8 + (lane >> 3);  // LDS row: q 0..63, k 64..127, v 128..191
     const int64_t grow = (int64_t)(r >> 6) * D + h * 64 + (r & 63);
-    w_src[i] = a.w + grow * a.ld_w + ((lane & 7) ^ ba_swz(r)) * 8;
+    w_src[i] = reinterpret_cast<const TIN*>(a.w) + grow * a.ld_w + ((lane & 7) ^ ba_swz(r)) * EPC;
   }
   auto a_stage = [&](int s) { return smem + s * BA_A_STAGE; };
   auto w_stage = [&](int s) { return smem + BA_S * BA_A_STAGE + s * BA_W_STAGE; };
-  const int nk = D / BA_BK;
+  const int nk = D / BK;
   auto issue = [&](int kt) {
-    const int s = kt % BA_S, k0 = kt * BA_BK;
+    const int s = kt % BA_S, k0 = kt * BK;
 #pragma unroll
     for (int i = 0; i < BA_AB; ++i)
       __builtin_amdgcn_global_load_lds(static_cast<const void*>(a_src[i] + k0),
@@ -109,11 +120,11 @@ __global__ __launch_bounds__(BA_THREADS) void qkv_attention_kernel(QkvAttnArgs a
       __builtin_amdgcn_global_load_lds(static_cast<const void*>(w_src[i] + k0),
                                        static_cast<void*>(w_stage(s) + (wid * BA_WB + i) * 1024), 16, 0, 0);
   };
-  f32x4 acc[BA_TM][BA_TN];
+  typename OP::accum acc[BA_TM][BA_TN];
 #pragma unroll
   for (int i = 0; i < BA_TM; ++i)
 #pragma unroll
-    for (int j = 0; j < BA_TN; ++j) acc[i][j] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+    for (int j = 0; j < BA_TN; ++j) acc[i][j] = (typename OP::accum){0, 0, 0, 0};
   int a_off[BA_TM], a_sw[BA_TM], w_off[BA_TN], w_sw[BA_TN];
 #pragma unroll
   for (int t = 0; t < BA_TM; ++t) {
@@ -127,25 +138,23 @@ __global__ __launch_bounds__(BA_THREADS) void qkv_attention_kernel(QkvAttnArgs a
     w_off[t] = r * 128;
     w_sw[t] = ba_swz(r);
   }
-  auto read_frags = [&](int stage, int ks, bf16x8 (&af)[BA_TM], bf16x8 (&wf)[BA_TN]) {
+  auto read_frags = [&](int stage, int ks, frag (&af)[BA_TM], frag (&wf)[BA_TN]) {
     const unsigned char* as = a_stage(stage);
     const unsigned char* ws = w_stage(stage);
 #pragma unroll
     for (int t = 0; t < BA_TM; ++t)
-      af[t] = *reinterpret_cast<const bf16x8*>(as + a_off[t] + (((ks * 4 + g4) ^ a_sw[t]) << 4));
+      af[t] = *reinterpret_cast<const frag*>(as + a_off[t] + (((ks * 4 + g4) ^ a_sw[t]) << 4));
 #pragma unroll
     for (int t = 0; t < BA_TN; ++t)
-      wf[t] = *reinterpret_cast<const bf16x8*>(ws + w_off[t] + (((ks * 4 + g4) ^ w_sw[t]) << 4));
+      wf[t] = *reinterpret_cast<const frag*>(ws + w_off[t] + (((ks * 4 + g4) ^ w_sw[t]) << 4));
   };
   // q and k tiles as C^T (a lane holds 4 consecutive head dims of one latent), v tiles
   // as C (4 consecutive latents of one head dim)
-  auto mma = [&](const bf16x8 (&af)[BA_TM], const bf16x8 (&wf)[BA_TN]) {
+  auto mma = [&](const frag (&af)[BA_TM], const frag (&wf)[BA_TN]) {
 #pragma unroll
     for (int i = 0; i < BA_TM; ++i)
 #pragma unroll
-      for (int j = 0; j < BA_TN; ++j)
-        acc[i][j] = j < 4 ? __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf[j], af[i], acc[i][j], 0, 0, 0)
-                          : __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[i], wf[j], acc[i][j], 0, 0, 0);
+      for (int j = 0; j < BA_TN; ++j) acc[i][j] = j < 4 ? OP::mma(wf[j], af[i], acc[i][j]) : OP::mma(af[i], wf[j], acc[i][j]);
   };
   // Both stages in flight; a stage is refilled as soon as every wave holds its last
   // fragments in registers.  Fragments are double-buffered in registers, so the LDS
@@ -153,7 +162,7 @@ __global__ __launch_bounds__(BA_THREADS) void qkv_attention_kernel(QkvAttnArgs a
 #pragma unroll
   for (int p = 0; p < BA_S; ++p)
     if (p < nk) issue(p);
-  bf16x8 af0[BA_TM], wf0[BA_TN], af1[BA_TM], wf1[BA_TN];
+  frag af0[BA_TM], wf0[BA_TN], af1[BA_TM], wf1[BA_TN];
   if (nk > 1)
     ba_wait_vm<BA_PER>();
   else
@@ -184,6 +193,10 @@ __global__ __launch_bounds__(BA_THREADS) void qkv_attention_kernel(QkvAttnArgs a
     scv[j] = a.w_scale ? *reinterpret_cast<const float4*>(a.w_scale + gc + 4 * g4) : make_float4(1.f, 1.f, 1.f, 1.f);
     biv[j] = a.bias ? *reinterpret_cast<const float4*>(a.bias + gc + 4 * g4) : make_float4(0.f, 0.f, 0.f, 0.f);
     scs[j] = a.w_scale ? a.w_scale[gc + fr] : 1.0f;
+    if constexpr (sizeof(TIN) == 1) {  // int8 activations: xn_f = a_scale * xn
+      scv[j].x *= a.a_scale; scv[j].y *= a.a_scale; scv[j].z *= a.a_scale; scv[j].w *= a.a_scale;
+      scs[j] *= a.a_scale;
+    }
     bis[j] = a.bias ? a.bias[gc + fr] : 0.0f;
   }
   __syncthreads();  // every ring read is done: the LDS becomes Q | K | V^T
@@ -336,13 +349,27 @@ __global__ __launch_bounds__(BA_THREADS) void qkv_attention_kernel(QkvAttnArgs a
     const float inv = l > 0.0f ? 1.0f / l : 0.0f;
     const int q = q0 + 16 * qg + fr;
     if (q < L) {
-      bf16* O = a.out + (row0 + q) * a.ld_o + h * 64;
+      if constexpr (Q8OUT) {
+        int8_t* O = reinterpret_cast<int8_t*>(a.out) + (row0 + q) * a.ld_o + h * 64;
 #pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        bf16x4 v;
+        for (int t = 0; t < 4; ++t) {
+          uint32_t pk = 0;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) v[i] = (bf16)(o_acc[qg][t][i] * inv);
-        *reinterpret_cast<bf16x4*>(O + 16 * t + 4 * g4) = v;
+          for (int i = 0; i < 4; ++i) {
+            const float y = o_acc[qg][t][i] * inv;
+            pk |= (uint32_t)((int)fminf(fmaxf(rintf(y * a.out_inv_scale), -127.0f), 127.0f) & 0xff) << (8 * i);
+          }
+          *reinterpret_cast<uint32_t*>(O + 16 * t + 4 * g4) = pk;
+        }
+      } else {
+        bf16* O = reinterpret_cast<bf16*>(a.out) + (row0 + q) * a.ld_o + h * 64;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          bf16x4 v;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) v[i] = (bf16)(o_acc[qg][t][i] * inv);
+          *reinterpret_cast<bf16x4*>(O + 16 * t + 4 * g4) = v;
+        }
       }
     }
   }
@@ -369,9 +396,37 @@ extern "C" int cortex_qkv_attention(int64_t B, int64_t L, int64_t D, int64_t H, 
                    "cortex_qkv_attention: operands must be 16-byte aligned rows");
   CORTEX_CHECK_ARG(scale > 0.0f && scale < INFINITY, "cortex_qkv_attention: scale must be positive");
   CORTEX_CHECK_ARG(B * H <= 0x7fffffffLL && B <= 65535 && H <= 65535, "cortex_qkv_attention: grid too large");
-  QkvAttnArgs a{B, L, D, H, reinterpret_cast<const bf16*>(xn), ld_x, reinterpret_cast<const bf16*>(w), ld_w,
-                w_scale, bias, scale * 1.4426950408889634f, reinterpret_cast<bf16*>(out), ld_o};
-  hipLaunchKernelGGL(qkv_attention_kernel, dim3((unsigned)H, (unsigned)B), dim3(BA_THREADS), 0, stream, a);
+  QkvAttnArgs a{B, L, D, H, xn, ld_x, w, ld_w, w_scale, bias, scale * 1.4426950408889634f, out, ld_o, 1.0f, 0.0f};
+  hipLaunchKernelGGL((qkv_attention_kernel<bf16, false>), dim3((unsigned)H, (unsigned)B), dim3(BA_THREADS), 0, stream,
+                     a);
   CORTEX_CHECK_LAUNCH("qkv_attention_kernel");
+  return OK;
+}
+
+extern "C" int cortex_qkv_attention_w8a8(int64_t B, int64_t L, int64_t D, int64_t H, const int8_t* xq, int64_t ld_x,
+                                         float a_scale, const int8_t* w, int64_t ld_w, const float* w_scale,
+                                         const float* bias, float scale, void* out, int out_dtype, float out_scale,
+                                         int64_t ld_o, hipStream_t stream) {
+  const char* who = "cortex_qkv_attention_w8a8";
+  CORTEX_CHECK_ARG(B >= 0 && L >= 1 && L <= BA_L, "%s: need 1 <= L <= %d", who, BA_L);
+  CORTEX_CHECK_ARG(H >= 1 && D == 64 * H && D % 128 == 0, "%s: need D = 64 * H, a multiple of 128", who);
+  CORTEX_CHECK_ARG(out_dtype == DT_BF16 || out_dtype == DT_I8, "%s: out must be bf16 or int8", who);
+  if (B == 0) return OK;
+  CORTEX_CHECK_ARG(xq && w && out, "%s: null pointer", who);
+  CORTEX_CHECK_ARG(a_scale > 0.0f && (out_dtype == DT_BF16 || out_scale > 0.0f), "%s: scales must be positive", who);
+  CORTEX_CHECK_ARG(ld_x >= D && ld_w >= D && ld_o >= D, "%s: row strides too small", who);
+  CORTEX_CHECK_ARG(ba_al16(xq) && ba_al16(w) && ld_x % 16 == 0 && ld_w % 16 == 0 && ((uintptr_t)out & 7) == 0 &&
+                       ld_o % 4 == 0 && (!w_scale || ba_al16(w_scale)) && (!bias || ba_al16(bias)),
+                   "%s: operands must be 16-byte aligned rows", who);
+  CORTEX_CHECK_ARG(scale > 0.0f && scale < INFINITY, "%s: scale must be positive", who);
+  CORTEX_CHECK_ARG(B * H <= 0x7fffffffLL && B <= 65535 && H <= 65535, "%s: grid too large", who);
+  QkvAttnArgs a{B, L, D, H, xq, ld_x, w, ld_w, w_scale, bias, scale * 1.4426950408889634f, out, ld_o, a_scale,
+                out_dtype == DT_I8 ? 1.0f / out_scale : 0.0f};
+  const dim3 grid((unsigned)H, (unsigned)B);
+  if (out_dtype == DT_I8)
+    hipLaunchKernelGGL((qkv_attention_kernel<int8_t, true>), grid, dim3(BA_THREADS), 0, stream, a);
+  else
+    hipLaunchKernelGGL((qkv_attention_kernel<int8_t, false>), grid, dim3(BA_THREADS), 0, stream, a);
+  CORTEX_CHECK_LAUNCH("qkv_attention_kernel (int8)");
   return OK;
 }

@@ -64,6 +64,32 @@ __device__ __forceinline__ void mfma_16x16x32(f32x4& acc, const Frag<float>& a, 
   for (int j = 0; j < 8; ++j) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.v[j], b.v[j], acc, 0, 0, 0);
 }
 
+// Operand element type of the direct-to-LDS GEMM loops: a 16-byte fragment per lane and the
+// MFMA that consumes it (bf16: 8 K-elements, fp32 accumulators; int8: 16 K-elements, int32
+// accumulators).  Both read 16 bytes per lane per operand, so LDS layouts carry over.
+template <class TIN>
+struct Operand;
+template <>
+struct Operand<bf16> {
+  typedef bf16x8 frag;
+  typedef f32x4 accum;
+  typedef float elem;
+  static constexpr int EPC = 8;  // elements per 16-byte chunk
+  static __device__ __forceinline__ accum mma(const frag& w, const frag& a, const accum& c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(w, a, c, 0, 0, 0);
+  }
+};
+template <>
+struct Operand<int8_t> {
+  typedef i32x4 frag;
+  typedef i32x4 accum;
+  typedef int elem;
+  static constexpr int EPC = 16;
+  static __device__ __forceinline__ accum mma(const frag& w, const frag& a, const accum& c) {
+    return __builtin_amdgcn_mfma_i32_16x16x64_i8(w, a, c, 0, 0, 0);
+  }
+};
+
 // Cross-lane reductions inside one wavefront.
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll

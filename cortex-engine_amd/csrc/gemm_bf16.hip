@@ -63,30 +63,6 @@ struct BTile {
   static_assert(PER * (STAGES - 1) < 64, "vmcnt range");
 };
 
-// Operand element type: a 16-byte fragment per lane and the MFMA that consumes it.
-template <class TIN>
-struct Operand;
-template <>
-struct Operand<bf16> {
-  typedef bf16x8 frag;
-  typedef f32x4 accum;
-  typedef float elem;
-  static constexpr int EPC = 8;  // elements per 16-byte chunk
-  static __device__ __forceinline__ accum mma(const frag& w, const frag& a, const accum& c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(w, a, c, 0, 0, 0);
-  }
-};
-template <>
-struct Operand<int8_t> {
-  typedef i32x4 frag;
-  typedef i32x4 accum;
-  typedef int elem;
-  static constexpr int EPC = 16;
-  static __device__ __forceinline__ accum mma(const frag& w, const frag& a, const accum& c) {
-    return __builtin_amdgcn_mfma_i32_16x16x64_i8(w, a, c, 0, 0, 0);
-  }
-};
-
 // 16-byte chunk swizzles of the 128-byte LDS rows.  A fragments read 16 consecutive
 // rows; W fragments read rows 8q + 4jj + i (q, i in 0..3) -- see the column order
 // below.  Each swizzle puts its fragment's 16 rows into the 16 distinct (row parity,

@@ -3,6 +3,8 @@
 //   out[m, :] = res[m % res_rows, :] + (A[m, :] . W^T) * w_scale (+ bias)     fp32
 //   xn[m, :]  = LN(out[m, :]) * gamma + beta                                   bf16
 //               (or, for the opt-in W8A8 mode, int8: clamp(rint(LN(..) / xq_scale), +-127))
+// The W8A8 form also takes int8 A rows (A_f = a_scale * A) and the int8 weight (TIN =
+// int8_t: v_mfma_i32_16x16x64_i8, exact int32 sums, a_scale * w_scale in the epilogue).
 //
 // This is SelfAttentionBlock's  x = x + out_proj(attn);  h_in = norm_mlp(x)
 // (reference cortex/models/perceiver.py:121-124), and the cross-attention block's
@@ -54,9 +56,9 @@ __device__ __forceinline__ int rl_swz(int r) { return (r >> 1) & 7; }
 
 struct RowLnArgs {
   int64_t M, N, K;
-  const bf16* x;
+  const void* x;  // bf16 rows (int8 in the W8A8 form)
   int64_t ld_x;
-  const bf16* w;
+  const void* w;
   int64_t ld_w;
   const float* w_scale;
   const float* bias;
@@ -70,10 +72,14 @@ struct RowLnArgs {
   void* xn;  // bf16, or int8 when Q8
   int64_t ld_xn;
   float xq_inv_scale;  // Q8: 1 / activation scale of the consumer
+  float a_scale;       // int8 A rows: A_f = a_scale * A
 };
 
-template <int BN, int S, bool Q8 = false>
+template <int BN, int S, bool Q8 = false, class TIN = bf16>
 __global__ __launch_bounds__(RL_THREADS) void gemm_rowln_kernel(RowLnArgs g) {
+  using OP = Operand<TIN>;
+  typedef typename OP::frag frag;
+  constexpr int EPC = OP::EPC, BK = 8 * EPC;  // K elements per 16-byte chunk and per 128-byte LDS row
   constexpr int WN = BN / RL_WAVES;   // columns per wavefront
   constexpr int TM = RL_BM / 16, TN = WN / 16;
   constexpr int A_STAGE = RL_BM * 128, W_STAGE = BN * 128;  // bytes
@@ -93,18 +99,19 @@ __global__ __launch_bounds__(RL_THREADS) void gemm_rowln_kernel(RowLnArgs g) {
   // transfer sources: A block (wid & 3) = rows 8 (wid & 3) .. +7 (waves 4..7 repeat
   // waves 0..3: identical bytes to identical addresses); W blocks wid * WB + i
   const int ar = (wid & 3) * 8 + (lane >> 3);
-  const bf16* a_src = g.x + (int64_t)min(m0 + ar, M - 1) * g.ld_x + ((lane & 7) ^ rl_swz(ar)) * 8;
-  const bf16* w_src[WB];
+  const TIN* a_src = reinterpret_cast<const TIN*>(g.x) + (int64_t)min(m0 + ar, M - 1) * g.ld_x +
+                     ((lane & 7) ^ rl_swz(ar)) * EPC;
+  const TIN* w_src[WB];
 #pragma unroll
   for (int i = 0; i < WB; ++i) {
     const int r = (wid * WB + i) * 8 + (lane >> 3);
-    w_src[i] = g.w + (int64_t)r * g.ld_w + ((lane & 7) ^ rl_swz(r)) * 8;
+    w_src[i] = reinterpret_cast<const TIN*>(g.w) + (int64_t)r * g.ld_w + ((lane & 7) ^ rl_swz(r)) * EPC;
   }
   auto a_stage = [&](int s) { return smem + s * A_STAGE; };
   auto w_stage = [&](int s) { return smem + S * A_STAGE + s * W_STAGE; };
-  const int nk = K / RL_BK;
+  const int nk = K / BK;
   auto issue = [&](int kt) {
-    const int s = kt % S, k0 = kt * RL_BK;
+    const int s = kt % S, k0 = kt * BK;
     __builtin_amdgcn_global_load_lds(static_cast<const void*>(a_src + k0),
                                      static_cast<void*>(a_stage(s) + (wid & 3) * 1024), 16, 0, 0);
 #pragma unroll
@@ -113,11 +120,11 @@ __global__ __launch_bounds__(RL_THREADS) void gemm_rowln_kernel(RowLnArgs g) {
                                        static_cast<void*>(w_stage(s) + (wid * WB + i) * 1024), 16, 0, 0);
   };
 
-  f32x4 acc[TM][TN];
+  typename OP::accum acc[TM][TN];
 #pragma unroll
   for (int i = 0; i < TM; ++i)
 #pragma unroll
-    for (int j = 0; j < TN; ++j) acc[i][j] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+    for (int j = 0; j < TN; ++j) acc[i][j] = (typename OP::accum){0, 0, 0, 0};
   int a_off[TM], a_sw[TM], w_off[TN], w_sw[TN];
 #pragma unroll
   for (int t = 0; t < TM; ++t) {
@@ -131,21 +138,21 @@ __global__ __launch_bounds__(RL_THREADS) void gemm_rowln_kernel(RowLnArgs g) {
     w_off[t] = r * 128;
     w_sw[t] = rl_swz(r);
   }
-  auto read_frags = [&](int stage, int ks, bf16x8 (&af)[TM], bf16x8 (&wf)[TN]) {
+  auto read_frags = [&](int stage, int ks, frag (&af)[TM], frag (&wf)[TN]) {
     const unsigned char* as = a_stage(stage);
     const unsigned char* ws = w_stage(stage);
 #pragma unroll
     for (int t = 0; t < TM; ++t)
-      af[t] = *reinterpret_cast<const bf16x8*>(as + a_off[t] + (((ks * 4 + g4) ^ a_sw[t]) << 4));
+      af[t] = *reinterpret_cast<const frag*>(as + a_off[t] + (((ks * 4 + g4) ^ a_sw[t]) << 4));
 #pragma unroll
     for (int t = 0; t < TN; ++t)
-      wf[t] = *reinterpret_cast<const bf16x8*>(ws + w_off[t] + (((ks * 4 + g4) ^ w_sw[t]) << 4));
+      wf[t] = *reinterpret_cast<const frag*>(ws + w_off[t] + (((ks * 4 + g4) ^ w_sw[t]) << 4));
   };
-  auto mma = [&](const bf16x8 (&af)[TM], const bf16x8 (&wf)[TN]) {
+  auto mma = [&](const frag (&af)[TM], const frag (&wf)[TN]) {
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
-      for (int j = 0; j < TN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf[j], af[i], acc[i][j], 0, 0, 0);
+      for (int j = 0; j < TN; ++j) acc[i][j] = OP::mma(wf[j], af[i], acc[i][j]);
   };
 
 #pragma unroll
@@ -174,7 +181,7 @@ __global__ __launch_bounds__(RL_THREADS) void gemm_rowln_kernel(RowLnArgs g) {
     else
       rl_wait_ahead<PER, S, 0>(ahead);
   };
-  bf16x8 af0[TM], wf0[TN], af1[TM], wf1[TN];
+  frag af0[TM], wf0[TN], af1[TM], wf1[TN];
   wait_step(0, S - 1);
   __builtin_amdgcn_s_barrier();
   read_frags(0, 0, af0, wf0);
@@ -212,6 +219,12 @@ __global__ __launch_bounds__(RL_THREADS) void gemm_rowln_kernel(RowLnArgs g) {
   if (!g.w_scale) {
 #pragma unroll
     for (int j = 0; j < TN; ++j) scv[j] = make_float4(1.f, 1.f, 1.f, 1.f);
+  }
+  if constexpr (sizeof(TIN) == 1) {  // int8 A rows: A_f = a_scale * A
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      scv[j].x *= g.a_scale; scv[j].y *= g.a_scale; scv[j].z *= g.a_scale; scv[j].w *= g.a_scale;
+    }
   }
   if (!g.bias) {
 #pragma unroll
@@ -335,10 +348,12 @@ namespace {
 int residual_ln(const char* who, int64_t M, int64_t N, int64_t K, const void* x, int64_t ld_x, const void* w,
                 int64_t ld_w, const float* w_scale, const float* bias, const float* res, int64_t ld_res,
                 int64_t res_rows, float* out, int64_t ld_out, const float* gamma, const float* beta, float eps,
-                void* xn, int64_t ld_xn, float xq_scale, bool q8, hipStream_t stream) {
+                void* xn, int64_t ld_xn, float xq_scale, bool q8, hipStream_t stream, float a_scale = 0.0f) {
+  const bool i8in = a_scale > 0.0f;  // int8 A rows and weight (W8A8)
   CORTEX_CHECK_ARG(M >= 0 && K > 0, "%s: need M >= 0 and K > 0", who);
   CORTEX_CHECK_ARG(N == 256 || N == 512, "%s: N must be 256 or 512 (got %lld)", who, (long long)N);
-  CORTEX_CHECK_ARG(K % RL_BK == 0 && K <= 0x7fffffffLL, "%s: K must be a multiple of 64", who);
+  CORTEX_CHECK_ARG(K % (i8in ? 2 * RL_BK : RL_BK) == 0 && K <= 0x7fffffffLL, "%s: K must be a multiple of %d", who,
+                   i8in ? 2 * RL_BK : RL_BK);
   if (M == 0) return OK;
   CORTEX_CHECK_ARG(M <= 0x7fffffffLL - RL_BM, "%s: M too large", who);
   CORTEX_CHECK_ARG(x && w && res && out && gamma && beta && xn, "%s: null pointer", who);
@@ -347,14 +362,20 @@ int residual_ln(const char* who, int64_t M, int64_t N, int64_t K, const void* x,
   CORTEX_CHECK_ARG(ld_x >= K && ld_w >= K && ld_res >= N && ld_out >= N && ld_xn >= N, "%s: row strides too small",
                    who);
   CORTEX_CHECK_ARG(a16(x) && a16(w) && a16(res) && a16(out) && a16(xn) && a16(gamma) && a16(beta) &&
-                       (!w_scale || a16(w_scale)) && (!bias || a16(bias)) && ld_x % 8 == 0 && ld_w % 8 == 0 &&
+                       (!w_scale || a16(w_scale)) && (!bias || a16(bias)) && ld_x % (i8in ? 16 : 8) == 0 &&
+                       ld_w % (i8in ? 16 : 8) == 0 &&
                        ld_res % 4 == 0 && ld_out % 4 == 0 && ld_xn % (q8 ? 16 : 8) == 0,
                    "%s: operands must be 16-byte aligned rows", who);
-  RowLnArgs a{M,     N,      K,      reinterpret_cast<const bf16*>(x), ld_x, reinterpret_cast<const bf16*>(w),
-              ld_w,  w_scale, bias,  res,   ld_res, res_rows, out,  ld_out, gamma, beta, eps, xn, ld_xn,
-              q8 ? 1.0f / xq_scale : 0.0f};
+  RowLnArgs a{M,     N,     K,     x,   ld_x, w,     ld_w, w_scale, bias, res, ld_res, res_rows, out, ld_out,
+              gamma, beta,  eps,   xn,  ld_xn, q8 ? 1.0f / xq_scale : 0.0f, a_scale};
   const dim3 grid((unsigned)cdiv(M, (int64_t)RL_BM));
-  if (N == 512) {
+  if (i8in) {
+    CORTEX_CHECK_ARG(N == 512, "%s: the int8 form needs N = 512", who);
+    if (q8)
+      hipLaunchKernelGGL((gemm_rowln_kernel<512, 2, true, int8_t>), grid, dim3(RL_THREADS), 0, stream, a);
+    else
+      hipLaunchKernelGGL((gemm_rowln_kernel<512, 2, false, int8_t>), grid, dim3(RL_THREADS), 0, stream, a);
+  } else if (N == 512) {
     if (q8)
       hipLaunchKernelGGL((gemm_rowln_kernel<512, 2, true>), grid, dim3(RL_THREADS), 0, stream, a);
     else
@@ -387,4 +408,17 @@ extern "C" int cortex_linear_residual_ln_i8(int64_t M, int64_t N, int64_t K, con
                                             int8_t* xq, int64_t ld_xq, float xq_scale, hipStream_t stream) {
   return residual_ln("cortex_linear_residual_ln_i8", M, N, K, x, ld_x, w, ld_w, w_scale, bias, res, ld_res,
                      res_rows, out, ld_out, gamma, beta, eps, xq, ld_xq, xq_scale, true, stream);
+}
+
+extern "C" int cortex_linear_residual_ln_w8a8(int64_t M, int64_t N, int64_t K, const int8_t* xq, int64_t ld_x,
+                                              float a_scale, const int8_t* w, int64_t ld_w, const float* w_scale,
+                                              const float* bias, const float* res, int64_t ld_res, int64_t res_rows,
+                                              float* out, int64_t ld_out, const float* gamma, const float* beta,
+                                              float eps, void* xn, int xn_dtype, float xn_scale, int64_t ld_xn,
+                                              hipStream_t stream) {
+  const char* who = "cortex_linear_residual_ln_w8a8";
+  CORTEX_CHECK_ARG(a_scale > 0.0f, "%s: a_scale must be positive", who);
+  CORTEX_CHECK_ARG(xn_dtype == DT_BF16 || xn_dtype == DT_I8, "%s: xn must be bf16 or int8", who);
+  return residual_ln(who, M, N, K, xq, ld_x, w, ld_w, w_scale, bias, res, ld_res, res_rows, out, ld_out, gamma, beta,
+                     eps, xn, ld_xn, xn_scale, xn_dtype == DT_I8, stream, a_scale);
 }

@@ -49,7 +49,9 @@ __global__ __launch_bounds__(256) void ln_rows_kernel(const float* __restrict__ 
                                                        const float* g1, const float* b1, float eps1,
                                                        const float* g2, const float* b2, float eps2, int two,
                                                        bf16* __restrict__ out_bf, int64_t ld_bf,
-                                                       float* __restrict__ out_f, int64_t ld_f) {
+                                                       float* __restrict__ out_f, int64_t ld_f,
+                                                       int8_t* __restrict__ out_q = nullptr, int64_t ld_q = 0,
+                                                       float q_inv = 0.0f) {
   constexpr int K = 64 * EPL;
   const int lane = threadIdx.x & 63;
   const int64_t m = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
@@ -79,6 +81,13 @@ __global__ __launch_bounds__(256) void ln_rows_kernel(const float* __restrict__ 
       *reinterpret_cast<bf16x4*>(out_bf + m * ld_bf + k) = b;
     }
     if (out_f) *reinterpret_cast<float4*>(out_f + m * ld_f + k) = make_float4(v[j], v[j + 1], v[j + 2], v[j + 3]);
+    if (out_q) {  // W8A8: clamp(rint(y * q_inv), -127, 127)
+      uint32_t pk = 0;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        pk |= (uint32_t)((int)fminf(fmaxf(rintf(v[j + i] * q_inv), -127.0f), 127.0f) & 0xff) << (8 * i);
+      *reinterpret_cast<uint32_t*>(out_q + m * ld_q + k) = pk;
+    }
   }
 }
 
@@ -422,6 +431,34 @@ int cortex_transpose_bf16(int64_t R, int64_t C, const void* in, int64_t ld_in, v
   hipLaunchKernelGGL(transpose_bf16_kernel, dim3((unsigned)cdiv(C, 64), (unsigned)cdiv(R, 64)), dim3(256), 0, stream,
                      (const bf16*)in, R, C, ld_in, (bf16*)out, ld_out);
   CORTEX_CHECK_LAUNCH("transpose_bf16_kernel");
+  return OK;
+}
+
+int cortex_ln_rows_i8(int64_t M, int64_t K, const float* x, int64_t ld_x, const float* gamma, const float* beta,
+                      float eps, int8_t* out, int64_t ld_out, float out_scale, hipStream_t stream) {
+  CORTEX_CHECK_ARG(M >= 0, "cortex_ln_rows_i8: negative M");
+  if (M == 0) return OK;
+  CORTEX_CHECK_ARG(x && out && out_scale > 0.0f, "cortex_ln_rows_i8: null pointer or non-positive scale");
+  CORTEX_CHECK_ARG(K == 256 || K == 512 || K == 768 || K == 1024,
+                   "cortex_ln_rows_i8: K=%lld not one of 256, 512, 768, 1024", (long long)K);
+  CORTEX_CHECK_ARG(((uintptr_t)x & 15) == 0 && ld_x % 4 == 0 && ((uintptr_t)out & 3) == 0 && ld_out % 4 == 0 &&
+                       ld_out >= K && ld_x >= K,
+                   "cortex_ln_rows_i8: rows must be aligned (x 16 bytes, out 4 bytes)");
+  for (const float* p : {gamma, beta})
+    CORTEX_CHECK_ARG(((uintptr_t)p & 15) == 0, "cortex_ln_rows_i8: gamma/beta must be 16-byte aligned fp32");
+  const dim3 grid((unsigned)cdiv(M, 4));
+  const float inv = 1.0f / out_scale;
+#define CORTEX_LNQ(EPL)                                                                                           \
+  hipLaunchKernelGGL((ln_rows_kernel<EPL>), grid, dim3(256), 0, stream, x, M, ld_x, gamma, beta, eps, nullptr, \
+                     nullptr, 0.0f, 0, nullptr, 0, nullptr, 0, out, ld_out, inv)
+  switch (K) {
+    case 256: CORTEX_LNQ(4); break;
+    case 512: CORTEX_LNQ(8); break;
+    case 768: CORTEX_LNQ(12); break;
+    default: CORTEX_LNQ(16); break;
+  }
+#undef CORTEX_LNQ
+  CORTEX_CHECK_LAUNCH("ln_rows_kernel (int8)");
   return OK;
 }
 

@@ -253,6 +253,28 @@ int cortex_linear_w8a8(int64_t M, int64_t N, int64_t K, const int8_t* x, int64_t
                        int64_t ld_res, int64_t res_rows, void* out, int out_dtype, float out_scale, int64_t ld_out,
                        hipStream_t stream);
 
+/* The rest of a self-attention block in the W8A8 mode (same q(.) as above):
+ * cortex_qkv_attention_w8a8: cortex_qkv_attention with int8 xn rows at a_scale and the int8
+ * qkv weight (exact int32 projection sums, a_scale * w_scale applied before the bf16
+ * attention); out_dtype 1: bf16 o, 3: int8 o = q(o; out_scale) (out_proj's activation).
+ * D a multiple of 128; ld_x, ld_w multiples of 16.
+ * cortex_linear_residual_ln_w8a8: cortex_linear_residual_ln with int8 x rows at a_scale and
+ * the int8 weight (N = 512, K % 128 == 0); xn bf16 (xn_dtype 1) or int8 = q(LN(out); xn_scale)
+ * (xn_dtype 3).
+ * cortex_ln_rows_i8: out = q(LN(x) * gamma + beta; out_scale) as int8 rows (K in {256, 512,
+ * 768, 1024}; out 4-byte aligned, ld_out % 4 == 0). */
+int cortex_qkv_attention_w8a8(int64_t B, int64_t L, int64_t D, int64_t H, const int8_t* xq, int64_t ld_x,
+                              float a_scale, const int8_t* w, int64_t ld_w, const float* w_scale, const float* bias,
+                              float scale, void* out, int out_dtype, float out_scale, int64_t ld_o,
+                              hipStream_t stream);
+int cortex_linear_residual_ln_w8a8(int64_t M, int64_t N, int64_t K, const int8_t* xq, int64_t ld_x, float a_scale,
+                                   const int8_t* w, int64_t ld_w, const float* w_scale, const float* bias,
+                                   const float* res, int64_t ld_res, int64_t res_rows, float* out, int64_t ld_out,
+                                   const float* gamma, const float* beta, float eps, void* xn, int xn_dtype,
+                                   float xn_scale, int64_t ld_xn, hipStream_t stream);
+int cortex_ln_rows_i8(int64_t M, int64_t K, const float* x, int64_t ld_x, const float* gamma, const float* beta,
+                      float eps, int8_t* out, int64_t ld_out, float out_scale, hipStream_t stream);
+
 /* Behaviour head (BehaviorDecoder.forward, cortex/models/cortex.py:29-53) with its
  * batch-invariant factors folded: cortex_head_prep builds, once per parameter state,
  * the (32, D) bf16 matrix ac of rows a_{q,h} = W_k[h]^T q_h * log2(e)/sqrt(Dh) (rows

@@ -99,14 +99,17 @@ def test_residual_ln_int8_rows():
 
 
 def test_model_w8a8_within_parity_bar():
-    """CORTEX_S, INT8 weights, W8A8 MLPs in all 7 blocks, B = 32 x 512: max-abs against the
-    oracle's fp32 forward (reference arithmetic) within 2e-2; eager equals graph replay."""
+    """CORTEX_S, INT8 weights, all 7 self-attention blocks on int8 activations (qkv, out_proj
+    and both MLP linears), B = 32 x 512: max-abs against the oracle's fp32 forward (the
+    reference arithmetic) within 2e-2; eager equals graph replay."""
     import bench
     from cortex.quantization.w8a8 import disable_w8a8, enable_w8a8
     from cortex.runtime import CapturedForward
 
     model, scales = bench.build_model(torch.device(DEV), with_scales=True)
     assert enable_w8a8(model, scales) == 7
+    from cortex.quantization.w8a8 import w8a8_scales
+    assert all(w8a8_scales(b)[2] is not None for b in model.encoder.self_attn_blocks)
     try:
         nid, tb, val, bidx = bench.make_events(32, 512, seed=3)
         ev = [torch.from_numpy(a).to(DEV) for a in (nid, tb, val, bidx)]
@@ -120,3 +123,63 @@ def test_model_w8a8_within_parity_bar():
         assert torch.equal(cap(*ev).cpu(), got)
     finally:
         disable_w8a8(model)
+
+
+def test_ln_rows_i8():
+    from cortex.kernels import ops
+
+    torch.manual_seed(8)
+    x = (torch.randn(3001, 512) * 2 + 0.5).to(DEV)
+    g, b = (1 + 0.1 * torch.randn(512)).to(DEV), (0.1 * torch.randn(512)).to(DEV)
+    q = ops.ln_rows_i8(x, g, b, 1e-5, 0.03).cpu().numpy()
+    y = F.layer_norm(x.cpu(), (512,), g.cpu(), b.cpu(), 1e-5).numpy()
+    diff = np.abs(q.astype(np.int32) - _q(y, 0.03).astype(np.int32))
+    assert diff.max() <= 1 and (diff == 0).mean() > 0.999
+
+
+def test_linear_residual_ln_w8a8():
+    from cortex.kernels import ops
+
+    M, N, K = 8192, 512, 512
+    xq, wq, ws, b = _operands(M, N, K, seed=21)
+    res = np.random.default_rng(2).normal(0, 1, (M, N)).astype(np.float32)
+    a_scale = 0.01
+    want = res + _exact(xq, wq, a_scale, ws, b)
+    d = {k: torch.from_numpy(v).to(DEV) for k, v in dict(x=xq, w=wq, ws=ws, b=b, r=res).items()}
+    g, be = (1 + 0.1 * torch.randn(N)).to(DEV), (0.1 * torch.randn(N)).to(DEV)
+    out, xn = ops.linear_residual_ln_w8a8(d["x"], a_scale, d["w"], d["ws"], d["b"], residual=d["r"], ln=(g, be, 1e-5))
+    np.testing.assert_allclose(out.cpu().numpy(), want, rtol=1e-6, atol=1e-6 * np.abs(want).max())
+    y = F.layer_norm(out.cpu(), (N,), g.cpu(), be.cpu(), 1e-5)
+    torch.testing.assert_close(xn.cpu().float(), y.bfloat16().float(), rtol=2 ** -7, atol=1e-5)
+    out2, xq2 = ops.linear_residual_ln_w8a8(d["x"], a_scale, d["w"], d["ws"], d["b"], residual=d["r"],
+                                            ln=(g, be, 1e-5), xn_dtype=torch.int8, xn_scale=0.05)
+    assert torch.equal(out2, out)
+    diff = np.abs(xq2.cpu().numpy().astype(np.int32) - _q(y.numpy(), 0.05).astype(np.int32))
+    assert diff.max() <= 1 and (diff == 0).mean() > 0.999
+
+
+def test_qkv_attention_w8a8_vs_float64():
+    """int8 projection (exact int32 sums) then bf16 attention, against float64 attention of
+    the same dequantised operands (q, k, v rounded to bf16 as the kernel keeps them)."""
+    from cortex.kernels import ops
+
+    B, L, D, H = 4, 256, 512, 8
+    rng = np.random.default_rng(4)
+    xq = rng.integers(-127, 128, (B * L, D)).astype(np.int8)
+    wq, ws = O.quantize_int8(rng.normal(0, 0.02, (3 * D, D)).astype(np.float32))
+    bias = rng.normal(0, 0.1, 3 * D).astype(np.float32)
+    a_scale = 0.02
+    d = {k: torch.from_numpy(v).to(DEV) for k, v in dict(x=xq, w=wq, ws=ws, b=bias).items()}
+    got = ops.qkv_attention_w8a8(d["x"], a_scale, d["w"], d["ws"], d["b"], B, L, H).cpu().float()
+    proj = (xq.astype(np.float64) @ wq.astype(np.float64).T) * (a_scale * ws.astype(np.float64)) + bias
+    qkv = torch.from_numpy(proj).bfloat16().double().reshape(B, L, 3, H, D // H).permute(2, 0, 3, 1, 4)
+    q, k, v = qkv[0], qkv[1], qkv[2]
+    att = torch.softmax(q @ k.transpose(-1, -2) / 8.0, dim=-1) @ v  # (B, H, L, Dh)
+    ref = att.permute(0, 2, 1, 3).reshape(B * L, D)
+    assert float((got - ref).abs().max()) <= 2e-2 * float(ref.abs().max())
+    oq = ops.qkv_attention_w8a8(d["x"], a_scale, d["w"], d["ws"], d["b"], B, L, H, out_dtype=torch.int8,
+                                out_scale=0.01).cpu().numpy()
+    # the kernel quantises the fp32 attention output; `got` is that output rounded to bf16
+    # (0.4 % relative), so about one element in a hundred sits across a rounding boundary
+    diff = np.abs(oq.astype(np.int32) - _q(got.numpy(), 0.01).astype(np.int32))
+    assert diff.max() <= 1 and (diff == 0).mean() > 0.97

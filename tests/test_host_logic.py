@@ -145,11 +145,18 @@ def test_w8a8_enable_disable_bookkeeping():
             bias = None if lin.bias is None else lin.bias.detach().clone()
             blk.mlp[j] = QuantizedLinear(torch.from_numpy(q), torch.from_numpy(s), bias)
             scales[f"encoder.self_attn_blocks.{i}.mlp.{j}"] = LayerScales(torch.from_numpy(s), 0.01 * (i + 1) + j)
+    for name in ("qkv_proj", "out_proj"):  # block 0's attention linears too: its attention half goes int8
+        lin = getattr(blocks[0], name)
+        q, s = O.quantize_int8(lin.weight.detach().numpy())
+        bias = None if lin.bias is None else lin.bias.detach().clone()
+        setattr(blocks[0], name, QuantizedLinear(torch.from_numpy(q), torch.from_numpy(s), bias))
+        scales[f"encoder.self_attn_blocks.0.{name}"] = LayerScales(torch.from_numpy(s), 0.5 if name == "qkv_proj" else 0.25)
     keys = set(model.state_dict())
     del scales["encoder.self_attn_blocks.1.mlp.2"]  # no calibration data for one linear: that block stays
     scales["encoder.self_attn_blocks.2.mlp.0"] = LayerScales(torch.ones(1), 0.0)  # a zero scale: stays too
     assert enable_w8a8(model, scales) == len(blocks) - 2
-    assert w8a8_scales(blocks[0]) == (0.01, 2.01) and w8a8_scales(blocks[1]) is None
+    assert w8a8_scales(blocks[0]) == (0.01, 2.01, (0.5, 0.25)) and w8a8_scales(blocks[1]) is None
+    assert w8a8_scales(blocks[3]) == (0.04, 2.04, None)  # float attention linears: MLP only
     assert w8a8_scales(blocks[2]) is None
     assert set(model.state_dict()) == keys
     disable_w8a8(model)
