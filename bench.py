@@ -529,6 +529,43 @@ def api_configs(dev) -> dict:
     }
 
 
+def w8a8_kernels(dev) -> dict:
+    """The int8 kernels of the W8A8 blocks alone at the B = 32 x 512 shapes (graph-replayed):
+    microseconds and the fraction of the 5.0 POP/s dense int8 MFMA peak (2 M N K per GEMM)."""
+    from cortex.kernels import ops
+
+    g = torch.Generator(device="cpu").manual_seed(3)
+
+    def i8(*shape):
+        return torch.randint(-127, 128, shape, generator=g, dtype=torch.int8).to(dev)
+
+    M = M_ROWS
+    s = {n: (torch.rand(n, generator=g) * 1e-3 + 1e-4).to(dev) for n in (D, 3 * D, 4 * D)}
+    x, h, o = i8(M, D), i8(M, 4 * D), i8(M, D)
+    w_up, w_down, w_qkv, w_out = i8(4 * D, D), i8(D, 4 * D), i8(3 * D, D), i8(D, D)
+    res = torch.randn(M, D, generator=g).to(dev)
+    ln = (torch.ones(D, device=dev), torch.zeros(D, device=dev), 1e-5)
+    cases = {
+        "mlp_up_gelu_int8": (lambda: ops.linear_w8a8(x, 0.02, w_up, s[4 * D], act="gelu", out_dtype=torch.int8,
+                                                     out_scale=0.05), 2.0 * M * 4 * D * D),
+        "mlp_down_residual": (lambda: ops.linear_w8a8(h, 0.02, w_down, s[D], residual=res, out=res),
+                              2.0 * M * D * 4 * D),
+        "qkv_attention": (lambda: ops.qkv_attention_w8a8(x, 0.02, w_qkv, s[3 * D], None, B_MAIN, L, H,
+                                                         out_dtype=torch.int8, out_scale=0.01),
+                          2.0 * M * 3 * D * D),
+        "out_residual_ln": (lambda: ops.linear_residual_ln_w8a8(o, 0.02, w_out, s[D], residual=res, ln=ln, out=res,
+                                                                xn_dtype=torch.int8, xn_scale=0.05),
+                            2.0 * M * D * D),
+    }
+    out = {}
+    for name, (fn, ops_) in cases.items():
+        sec = time_launches(fn)
+        out[name] = {"us": round(sec * 1e6, 2), "int8_tops": round(ops_ / sec / 1e12, 1),
+                     "int8_frac": round(ops_ / sec / 1e12 / 5000.0, 4)}
+    out["note"] = "qkv_attention counts the projection only (its bf16 attention part is not int8 work)"
+    return out
+
+
 def w8a8_forward(model, scales, dev, inputs, reference: torch.Tensor, reps: int = 50) -> dict:
     """The opt-in W8A8 blocks (cortex.quantization.w8a8) on the same B = 32 x 512 forward:
     samples/s (graph replay) and the largest difference to the default path's behaviour."""
@@ -550,8 +587,9 @@ def w8a8_forward(model, scales, dev, inputs, reference: torch.Tensor, reps: int 
         del cap
     finally:
         disable_w8a8(model)
+    kern = w8a8_kernels(dev)
     return {"blocks": n, "ms_per_forward": round(sec * 1e3, 4), "samples_per_s": round(B_MAIN / sec, 1),
-            "max_abs_diff_vs_default": float((out - reference).abs().max()),
+            "max_abs_diff_vs_default": float((out - reference).abs().max()), "kernels": kern,
             "note": "int8 activations in the self-attention blocks (qkv, out_proj, both MLP linears; calibrated "
                     "act_scale); not the reference's arithmetic, opt-in"}
 
