@@ -34,9 +34,10 @@ _ATTR = "_cortex_w8a8"
 
 
 def enable_w8a8(model: nn.Module, scales: dict[str, LayerScales]) -> int:
-    """Run the MLP of every self-attention block whose ``mlp.0`` and ``mlp.2`` are
+    """Switch to W8A8 every self-attention block whose ``mlp.0`` and ``mlp.2`` are
     ``QuantizedLinear`` with calibrated scales in ``scales`` (module name -> LayerScales,
-    as ``derive_scales`` returns for the float model) as W8A8.  Returns the number of
+    as ``derive_scales`` returns for the float model): its MLP, and also its attention half
+    when ``qkv_proj`` and ``out_proj`` are quantised with scales too.  Returns the number of
     blocks switched."""
     from cortex.models.perceiver import SelfAttentionBlock
 
