@@ -246,6 +246,29 @@ class InferenceWorker:
 
     # ------------------------------------------------------------------ batch
 
+    def submit_batch(self, payloads: list[dict[str, Any]]) -> PendingBatch:
+        """``_run_batch_sync`` without the wait: packs the payloads into a pinned slot, queues
+        the copy, the forward and the result copy on the worker stream and returns at once,
+        so the host can pack the next batch while this one runs (two in flight, as
+        ``submit_windows``).  ``collect`` gives the result dicts.  Not thread-safe."""
+        t0 = time.perf_counter()
+        slot = self._acquire_slot()
+        flat, B, E, Eb = pack_payloads(payloads, self.use_graphs, slot.host_in.numpy())
+        dim = self.config.behavior_dim
+        pending = PendingBatch(slot, payloads, B, dim, t0)
+        if B == 0:
+            pending._rows = np.zeros((0, dim), dtype=np.float32)
+            pending._ms = (time.perf_counter() - t0) * 1000
+            return pending
+        n_in = 3 * Eb + B + 1
+        if flat.ctypes.data != slot.host_in.data_ptr():  # did not fit: grow the pinned buffer
+            slot.host_in = torch.empty(max(n_in, 2 * slot.host_in.numel()), dtype=torch.int64).pin_memory()
+            slot.host_in.numpy()[:n_in] = flat[:n_in]
+        src = slot.host_in[:n_in]
+        self._launch(slot, B, Eb, lambda inp, err: inp.copy_(src, non_blocking=True))
+        slot.pending = pending
+        return pending
+
     def _run_batch_sync(self, payloads: list[dict[str, Any]]) -> list[dict[str, Any]]:
         """One synchronous forward over ``payloads`` (runs on the executor thread).
 
@@ -319,13 +342,15 @@ class InferenceWorker:
         return pending
 
     def collect(self, pending: PendingBatch) -> list[dict[str, Any]]:
-        """Result dicts of a submitted streaming batch (waits for it)."""
+        """Result dicts of a submitted batch (waits for it).  As in ``_run_batch_sync``,
+        requests past the model batch (no events) get zeros."""
         pending._settle()
         if pending._error is not None:
             raise pending._error
         rows = pending._rows.tolist()
-        return [{"request_id": r["request_id"], "behavior": rows[i], "inference_ms": pending._ms}
-                for i, r in enumerate(pending.requests)]
+        zero = [0.0] * self.config.behavior_dim
+        return [{"request_id": r["request_id"], "behavior": rows[i] if i < len(rows) else zero,
+                 "inference_ms": pending._ms} for i, r in enumerate(pending.requests)]
 
     def _acquire_slot(self) -> _Slot:
         """The next pinned slot, once the batch that used it last is off the GPU (its result,

@@ -118,6 +118,32 @@ def test_worker_columnar_payloads_and_async(model):
     w.shutdown()
 
 
+def test_worker_pipelined_batches_equal_sync(model):
+    """submit_batch / collect with the next batch packed while one runs (and a third
+    submission settling the oldest uncollected batch): the same result dicts as
+    _run_batch_sync, including trailing and all-empty payloads."""
+    from cortex.models.config import CORTEX_S
+    from cortex.serve import InferenceWorker
+
+    w = InferenceWorker(model, CORTEX_S, torch.device(DEV))
+    batches = [_payloads([100, 600, 3], seed=5), _payloads([50, 0, 700, 0], seed=6, columnar=True),
+               [{"request_id": "e", "events": []}], _payloads([300] * 8, seed=7)]
+    want = [w._run_batch_sync(b) for b in batches]
+    got, pending = [], None
+    for b in batches:
+        nxt = w.submit_batch(b)
+        if pending is not None:
+            got.append(w.collect(pending))
+        pending = nxt
+    got.append(w.collect(pending))
+    ps = [w.submit_batch(b) for b in batches[:3]]  # three in flight: the first is settled early
+    got3 = [w.collect(p) for p in ps]
+    for g, x in zip(got + got3, want + want[:3]):
+        assert [r["request_id"] for r in g] == [r["request_id"] for r in x]
+        assert [r["behavior"] for r in g] == [r["behavior"] for r in x]
+    w.shutdown()
+
+
 def test_worker_rejects_out_of_range_events(model):
     from cortex.models.config import CORTEX_S
     from cortex.serve import InferenceWorker
