@@ -183,3 +183,33 @@ def test_qkv_attention_w8a8_vs_float64():
     # (0.4 % relative), so about one element in a hundred sits across a rounding boundary
     diff = np.abs(oq.astype(np.int32) - _q(got.numpy(), 0.01).astype(np.int32))
     assert diff.max() <= 1 and (diff == 0).mean() > 0.97
+
+
+@pytest.mark.parametrize("B", [1, 8])
+def test_model_w8a8_small_batches(B):
+    """W8A8 blocks at the serving batch sizes where the default path splits K across
+    workgroups: still within 2e-2 of the oracle, and the worker's graph path agrees."""
+    import bench
+    from cortex.models.config import CORTEX_S
+    from cortex.quantization.w8a8 import disable_w8a8, enable_w8a8
+    from cortex.serve import InferenceWorker
+
+    model, scales = bench.build_model(torch.device(DEV), with_scales=True)
+    enable_w8a8(model, scales)
+    try:
+        nid, tb, val, bidx = bench.make_events(B, 512, seed=30 + B)
+        ev = [torch.from_numpy(a).to(DEV) for a in (nid, tb, val, bidx)]
+        with torch.no_grad():
+            got = model(*ev, batch_size=B)["behavior"].cpu()
+        sd = {k: v.detach().cpu() for k, v in model.state_dict().items()}
+        ref = O.forward(sd, O.CORTEX_S_SHAPE, nid, tb, val, bidx, batch_size=B)
+        assert float((got - torch.as_tensor(ref)).abs().max()) <= 2e-2
+        w = InferenceWorker(model, CORTEX_S, torch.device(DEV), max_batch_size=B)
+        cuts = np.flatnonzero(np.diff(bidx)) + 1
+        payloads = [{"request_id": i, "events": {"neuron_id": a, "time_bin": t, "value": v}}
+                    for i, (a, t, v) in enumerate(zip(np.split(nid, cuts), np.split(tb, cuts), np.split(val, cuts)))]
+        rows = torch.tensor([r["behavior"] for r in w._run_batch_sync(payloads)])
+        assert float((rows - got).abs().max()) <= 1e-5
+        w.shutdown()
+    finally:
+        disable_w8a8(model)
