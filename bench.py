@@ -683,8 +683,8 @@ def run_copy_calibration(iters: int) -> int:
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--latency-requests", type=int, default=1000)
     ap.add_argument("--quick", action="store_true", help="skip latency, sweep, breakdown and CPU baseline")
