@@ -155,6 +155,12 @@ def test_worker_rejects_out_of_range_events(model):
         w._run_batch_sync(p)
     ok = _payloads([40, 40], seed=6)  # the next batch on the same graph is clean again
     _check(w._run_batch_sync(ok), ok, _expected(model, ok))
+    # pipelined: the bad batch raises at its collect, the batches around it are unaffected
+    first, bad, last = w.submit_batch(ok), w.submit_batch(p), w.submit_batch(ok)
+    _check(w.collect(first), ok, _expected(model, ok))
+    with pytest.raises(IndexError):
+        w.collect(bad)
+    _check(w.collect(last), ok, _expected(model, ok))
     w.shutdown()
 
 
