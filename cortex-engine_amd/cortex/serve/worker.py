@@ -162,8 +162,10 @@ class _Slot:
 
 
 class PendingBatch:
-    """A streaming batch submitted by ``InferenceWorker.submit_windows``; pass it to
-    ``collect`` for the result dicts."""
+    """A batch in flight, from ``InferenceWorker.submit_batch`` (payloads) or
+    ``submit_windows`` (cached streaming windows); pass it to ``collect`` for the result
+    dicts.  Its result stays in its pinned slot until collected, or until a later
+    submission needs the slot (then it moves to host memory)."""
 
     def __init__(self, slot: _Slot, requests: list[dict[str, Any]], batch: int, dim: int, t0: float) -> None:
         self._slot, self.requests, self._B, self._dim, self._t0 = slot, requests, batch, dim, t0
