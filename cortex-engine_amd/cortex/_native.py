@@ -85,6 +85,9 @@ _SIGNATURES = {
         _int,
         [_ptr, _i64, _i64, _i64, _i64, _i64, _i64, _ptr, _ptr, _f32, _ptr, _ptr, _f32, _ptr, _ptr, _ptr, _i64,
          _ptr]),
+    "cortex_pooled_linear": (
+        _int,
+        [_ptr, _i64, _i64, _i64, _i64, _ptr, _ptr, _f32, _i64, _int, _ptr, _i64, _ptr, _ptr, _ptr, _ptr, _ptr]),
     "cortex_gather_event_pages": (_int, [_ptr, _i64, _i64, _ptr, _i64, _ptr, _i64, _i64, _ptr, _ptr]),
     "cortex_scatter_event_pages": (_int, [_ptr, _i64, _i64, _ptr, _i64, _ptr, _i64, _i64, _ptr, _ptr]),
     "cortex_linear_residual_ln_i8": (_int, [_i64, _i64, _i64, _ptr, _i64, _ptr, _i64, _ptr, _ptr, _ptr, _i64, _i64,

@@ -401,6 +401,51 @@ def behavior_head(x: torch.Tensor, batch: int, ln1, ln2, ac: torch.Tensor, num_q
     return out
 
 
+def pooled_linear(x: torch.Tensor, batch: int, ln=None, weight: torch.Tensor | None = None,
+                  weight_scale: torch.Tensor | None = None, bias: torch.Tensor | None = None, *,
+                  pooled: bool = False):
+    """Masked-spike head: the mean over each sample's L rows of ``x`` (B*L, D) fp32, after the
+    LayerNorm ``ln`` = ``(weight, bias, eps)`` when given, then ``mean @ weight^T (* scale) + bias``
+    with ``weight`` (N, D) fp32, or int8 with its per-row ``weight_scale``.  Returns
+    ``(B, N)`` fp32, or ``(out, mean)`` with ``pooled=True``; ``weight=None`` returns the
+    (B, D) mean alone (see ``cortex_pooled_linear``)."""
+    dev = nat.require_gpu(x, weight, weight_scale, bias, what="pooled_linear")
+    x2 = _row_major_2d(x.reshape(-1, x.shape[-1]))
+    if x2.dtype != torch.float32:
+        raise ValueError("pooled_linear takes fp32 rows")
+    if x2.data_ptr() % 16 or (x2.shape[0] > 1 and x2.stride(0) % 4):
+        x2 = x2.contiguous()
+    M, D = x2.shape
+    if batch < 1 or M % batch:
+        raise ValueError(f"{M} rows do not split into {batch} samples")
+    L = M // batch
+    g = b = None
+    eps = 0.0
+    if ln is not None:
+        g, b, eps = ln
+        g, b = g.detach().float().contiguous(), b.detach().float().contiguous()
+    N = 0
+    w = None
+    if weight is not None:
+        if weight.dtype not in (torch.float32, torch.int8) or weight.shape[1] != D:
+            raise ValueError("pooled_linear weight must be (N, D) fp32 or int8")
+        if weight.dtype == torch.int8 and weight_scale is None:
+            raise ValueError("an int8 weight needs its per-row scale")
+        w = weight.detach().contiguous()
+        N = w.shape[0]
+    out = torch.empty((batch, N), dtype=torch.float32, device=dev)
+    mean = torch.empty((batch, D), dtype=torch.float32, device=dev) if (pooled or w is None) else None
+    sc = weight_scale.detach().float().contiguous() if weight_scale is not None and w is not None else None
+    bs = bias.detach().float().contiguous() if bias is not None and w is not None else None
+    nat.call("cortex_pooled_linear", nat.ptr(x2), x2.stride(0) if M > 1 else D, batch, L, D, nat.ptr(g),
+             nat.ptr(b), float(eps), N, nat.code(w.dtype) if w is not None else nat.F32, nat.ptr(w),
+             w.stride(0) if w is not None else D, nat.ptr(sc), nat.ptr(bs), nat.ptr(mean), nat.ptr(out),
+             nat.stream_of(dev))
+    if w is None:
+        return mean
+    return (out, mean) if pooled else out
+
+
 def convert(t: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
     """Elementwise dtype conversion on the GPU (int8/f32/bf16/f16 -> f32/bf16)."""
     dev = nat.require_gpu(t, what="convert")

@@ -28,7 +28,7 @@ from torch import nn
 from cortex.kernels import ops
 from cortex.kernels.pack import pack_events as _device_pack_events
 from cortex.models._layers import (apply_linear, batch_invariant, exec_weights, fused_tokens_ok, linear_residual_ln,
-                                   ln_params, ln_rows_ok, normalize_bf16, residual_ln_ok)
+                                   linear_weights, ln_params, ln_rows_ok, normalize_bf16, residual_ln_ok)
 from cortex.models.config import CortexConfig
 from cortex.models.perceiver import PerceiverEncoder
 from cortex.models.tokenizer import SpikeTokenizer
@@ -110,14 +110,33 @@ class BehaviorDecoder(nn.Module):
 
 
 class MaskedSpikeHead(nn.Module):
-    """Self-supervised pretraining head (reference :56-69); not part of inference."""
+    """Masked-spike logits: ``proj(latents.mean(dim=1))`` (reference :56-69).
+
+    One kernel (``cortex_pooled_linear``): the mean over each sample's latent rows, with the
+    encoder's final LayerNorm applied to every row first when it is passed, then the
+    N = spike_value_buckets projection with bias, fp32 throughout.  ``proj`` may be an
+    ``nn.Linear`` or a ``QuantizedLinear`` (int8 weight widened with its per-row scale in
+    fp32, as ``QuantizedLinear.forward`` does on fp32 latents).
+    """
 
     def __init__(self, config: CortexConfig) -> None:
         super().__init__()
         self.proj = nn.Linear(config.latent_dim, config.spike_value_buckets)
 
     def forward(self, latents: torch.Tensor) -> torch.Tensor:
-        raise NotImplementedError("the masked spike head is a training head; the HIP path covers inference")
+        """latents (B, L, D) -> (B, spike_value_buckets) fp32."""
+        B, L, D = latents.shape
+        return self.forward_rows(latents.reshape(B * L, D).float(), B)
+
+    def forward_rows(self, lat: torch.Tensor, batch: int, pre_norm: nn.LayerNorm | None = None) -> torch.Tensor:
+        """(B*L, D) fp32 latent rows (``pre_norm`` applied to each row first) -> (B, N) fp32."""
+        ln = ln_params(pre_norm) if pre_norm is not None else None
+        if self.proj._forward_pre_hooks:  # calibration: the hooks see the pooled rows, as in the reference
+            mean = ops.pooled_linear(lat, batch, ln)
+            return apply_linear(self.proj, mean, out_dtype=torch.float32, compute=torch.float32)
+        w = linear_weights(self.proj)
+        return ops.pooled_linear(lat, batch, ln, w.get("weight_int8", w.get("weight")), w.get("weight_scale"),
+                                 w.get("bias"))
 
 
 class CortexModel(nn.Module):
@@ -133,15 +152,18 @@ class CortexModel(nn.Module):
 
     def forward(self, neuron_ids: torch.Tensor, time_bins: torch.Tensor, values: torch.Tensor,
                 batch_indices: torch.Tensor, return_aux: bool = False, *, batch_size: int | None = None,
-                err_flag: torch.Tensor | None = None) -> dict[str, torch.Tensor]:
-        """Spike events -> ``{"behavior": (B, behavior_dim)}``.
+                err_flag: torch.Tensor | None = None, check_indices: bool = False) -> dict[str, torch.Tensor]:
+        """Spike events -> ``{"behavior": (B, behavior_dim)}``, plus ``"masked_spike_logits"``
+        (B, spike_value_buckets) when ``return_aux`` is set and the model has that head.
 
         ``batch_size`` (keyword-only) avoids reading ``max(batch_indices)+1`` back to the
         host; ``err_flag`` (int32 device tensor) collects index-range violations
-        without a synchronisation.
+        without a synchronisation.  By default an event index outside its table gives a
+        zero token row and a batch index outside [0, B) drops the event, flagged in
+        ``err_flag`` only; ``check_indices=True`` reads the flag back after the forward
+        (one synchronisation) and raises ``IndexError`` as the eager embedding lookup
+        of the reference does (cortex/models/tokenizer.py:90-93).
         """
-        if return_aux:
-            raise NotImplementedError("return_aux (masked spike head) is a training output; not on the HIP path")
         if not (neuron_ids.shape == time_bins.shape == values.shape == batch_indices.shape):
             raise ValueError(
                 f"shape mismatch: neuron_ids={neuron_ids.shape}, time_bins={time_bins.shape}, "
@@ -150,28 +172,37 @@ class CortexModel(nn.Module):
         E = neuron_ids.shape[0]
         if batch_size is None:
             batch_size = int(batch_indices.max().item()) + 1 if E > 0 else 1
-        return {"behavior": self._forward_csr(neuron_ids, time_bins, values, batch_indices, int(batch_size),
-                                              err_flag)}
+        err_flag = _checked_flag(err_flag, check_indices, neuron_ids.device)
+        offsets, order, _ = ops.pack_plan(batch_indices, int(batch_size), err=err_flag, with_rank=False)
+        out = self._forward_planned(neuron_ids, time_bins, values, offsets, order, int(batch_size), err_flag,
+                                    aux=return_aux)
+        if check_indices:
+            _raise_on_flag(err_flag)
+        return out
 
     def forward_csr(self, neuron_ids: torch.Tensor, time_bins: torch.Tensor, values: torch.Tensor,
-                    offsets: torch.Tensor, *, err_flag: torch.Tensor | None = None) -> torch.Tensor:
+                    offsets: torch.Tensor, *, err_flag: torch.Tensor | None = None,
+                    check_indices: bool = False) -> torch.Tensor:
         """Events already grouped by sample -> behaviour ``(B, behavior_dim)`` fp32.
 
         Sample b owns events ``[offsets[b], offsets[b+1])`` (``offsets``: (B+1,) int64 on
         the device, non-decreasing from 0).  Events past ``offsets[B]`` (padding of a
         fixed-size buffer) are ignored.  Skips the pack plan: a server that builds the
-        batch sample by sample has the CSR layout for free.
+        batch sample by sample has the CSR layout for free.  ``check_indices`` as in
+        ``forward``.
         """
         if not (neuron_ids.shape == time_bins.shape == values.shape):
             raise ValueError(
                 f"shape mismatch: neuron_ids={neuron_ids.shape}, time_bins={time_bins.shape}, values={values.shape}")
-        return self._forward_planned(neuron_ids, time_bins, values, offsets, None, offsets.shape[0] - 1, err_flag)
+        err_flag = _checked_flag(err_flag, check_indices, neuron_ids.device)
+        out = self._forward_planned(neuron_ids, time_bins, values, offsets, None, offsets.shape[0] - 1,
+                                    err_flag)["behavior"]
+        if check_indices:
+            _raise_on_flag(err_flag)
+        return out
 
-    def _forward_csr(self, neuron_ids, time_bins, values, batch_indices, B: int, err_flag=None) -> torch.Tensor:
-        offsets, order, _ = ops.pack_plan(batch_indices, B, err=err_flag, with_rank=False)
-        return self._forward_planned(neuron_ids, time_bins, values, offsets, order, B, err_flag)
-
-    def _forward_planned(self, neuron_ids, time_bins, values, offsets, order, B: int, err_flag) -> torch.Tensor:
+    def _forward_planned(self, neuron_ids, time_bins, values, offsets, order, B: int, err_flag,
+                         aux: bool = False) -> dict[str, torch.Tensor]:
         """The forward from a CSR plan: row r of the packed events is event ``order[r]``
         (``r`` itself when ``order`` is None); rows past ``offsets[B]`` are ignored."""
         cfg = self.config
@@ -205,11 +236,32 @@ class CortexModel(nn.Module):
             x = apply_linear(xa.out_proj, o_buf, residual=enc.latents, res_rows=L, out_dtype=torch.float32,
                              compute=compute)  # (B*L, D) fp32 residual stream
         x = self._encode(x, B, xn)
-        return self.behavior_head.forward_rows(x, B, pre_norm=enc.final_norm)
+        out = {"behavior": self.behavior_head.forward_rows(x, B, pre_norm=enc.final_norm)}
+        if aux and self.masked_spike_head is not None:
+            out["masked_spike_logits"] = self.masked_spike_head.forward_rows(x, B, pre_norm=enc.final_norm)
+        return out
 
     def _encode(self, x: torch.Tensor, B: int, xn: torch.Tensor | None = None) -> torch.Tensor:
         """The self-attention stack on the fresh residual buffer ``x`` (updated in place)."""
         return self.encoder.encode_rows(x, B, final_norm=False, inplace=True, xn=xn)
+
+
+def _checked_flag(err_flag: torch.Tensor | None, check: bool, device: torch.device) -> torch.Tensor | None:
+    """The error flag a checked forward reads back: the caller's (cleared), or a fresh one."""
+    if not check:
+        return err_flag
+    if err_flag is None:
+        return torch.zeros(1, dtype=torch.int32, device=device)
+    err_flag.zero_()
+    return err_flag
+
+
+def _raise_on_flag(err_flag: torch.Tensor) -> None:
+    e = int(err_flag.item())
+    if e & 2:
+        raise IndexError("batch index outside [0, batch_size)")
+    if e:
+        raise IndexError("event index out of range (neuron_id, time_bin or value outside its embedding table)")
 
 
 def _pack_events(flat_tokens: torch.Tensor, batch_indices: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:

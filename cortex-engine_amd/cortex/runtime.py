@@ -10,7 +10,7 @@ from __future__ import annotations
 
 import torch
 
-from cortex.models.cortex import CortexModel
+from cortex.models.cortex import CortexModel, _raise_on_flag
 
 
 class CapturedForward:
@@ -18,15 +18,20 @@ class CapturedForward:
 
     Inputs are copied into static device buffers before each replay; the returned
     tensor is the graph's static output (clone it to keep it past the next call).
+    ``err_flag`` is cleared before every replay, so after a call it holds that call's
+    index-range violations only; with ``check_indices=True`` each call reads it back
+    (one synchronisation) and raises ``IndexError`` as ``CortexModel.forward`` does.
     """
 
-    def __init__(self, model: CortexModel, batch_size: int, n_events: int, warmup: int = 2) -> None:
+    def __init__(self, model: CortexModel, batch_size: int, n_events: int, warmup: int = 2, *,
+                 check_indices: bool = False) -> None:
         if n_events < 1 or batch_size < 1:
             raise ValueError("need batch_size >= 1 and n_events >= 1")
         dev = next(model.parameters()).device
         if dev.type != "cuda":
             raise RuntimeError("CapturedForward needs the model on a ROCm device")
         self.model = model
+        self.check_indices = check_indices
         self.batch_size = batch_size
         self.n_events = n_events
         self.neuron_ids = torch.zeros(n_events, dtype=torch.int64, device=dev)
@@ -55,5 +60,8 @@ class CapturedForward:
         self.time_bins.copy_(time_bins, non_blocking=True)
         self.values.copy_(values, non_blocking=True)
         self.batch_indices.copy_(batch_indices, non_blocking=True)
+        self.err_flag.zero_()  # a fill kernel, outside the graph
         self.graph.replay()
+        if self.check_indices:
+            _raise_on_flag(self.err_flag)
         return self.output

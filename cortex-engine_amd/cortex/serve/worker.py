@@ -10,9 +10,13 @@ contract (worker.py:22-32).  What changes is the way a batch reaches the GPU:
   offsets; the device never sorts ``batch_indices``.
 * Neuron ids, time bins, values and offsets go into ONE pinned host buffer laid
   out like the device input buffer, and cross in one asynchronous copy.
-* The forward for a given (B, event bucket) is captured once as a HIP graph and
-  replayed (about 60 launches become one); event counts are rounded up to a
-  bucket, the padding events lie past ``offsets[B]`` and are never attended.
+* The forward for a given (batch bucket, event bucket) is captured once as a HIP
+  graph and replayed (about 60 launches become one).  Event counts are rounded up
+  to a bucket, the padding events lie past ``offsets[B]`` and are never attended;
+  batch sizes are rounded up to a bucket too (at most 25 % more samples), the extra
+  samples are empty (their offsets repeat ``offsets[B]``) and their rows are dropped,
+  so a dynamic batcher's mix of sizes reuses a few dozen graphs instead of
+  capturing one per exact size.
 * The (B, behavior_dim) result comes back through a pinned buffer; the only host
   synchronisation is the one wait for that copy.
 
@@ -77,6 +81,16 @@ def event_bucket(n: int, fine: int = 4096) -> int:
     return -(-n // fine) * fine
 
 
+def batch_bucket(b: int) -> int:
+    """Batch size a captured graph is built for: ``b`` itself up to 8, then ``b`` rounded up
+    to a quarter of its power of two (8, 10, 12, 14, 16, 20, 24, 28, 32, 40, ...): at
+    most 25 % padding samples, four graphs per doubling of the batch."""
+    if b <= 8:
+        return b
+    step = 1 << (b.bit_length() - 3)
+    return -(-b // step) * step
+
+
 def _as_columns(events: Any) -> tuple[np.ndarray, np.ndarray, np.ndarray]:
     if isinstance(events, dict):
         cols = [np.asarray(events[f], dtype=np.int64).reshape(-1) for f in _FIELDS]
@@ -93,15 +107,17 @@ def _as_columns(events: Any) -> tuple[np.ndarray, np.ndarray, np.ndarray]:
 
 
 def pack_payloads(payloads: list[dict[str, Any]], bucket: bool = True,
-                  out: np.ndarray | None = None) -> tuple[np.ndarray, int, int, int]:
-    """Payloads -> the flat int64 input ``[nid (Eb) | tb (Eb) | val (Eb) | offsets (B+1)]``.
+                  out: np.ndarray | None = None, *, batch_pad: bool = False) -> tuple[np.ndarray, int, int, int]:
+    """Payloads -> the flat int64 input ``[nid (Eb) | tb (Eb) | val (Eb) | offsets (Bb+1)]``.
 
     Returns ``(flat, B, E, Eb)``: B ends at the last payload with events (the
     reference's ``max(batch_indices) + 1``, worker.py:171-177,238 and cortex.py:140), E is
     the number of real events, Eb the padded count (``event_bucket(E)`` when
     ``bucket``, else E).  Events keep the payload order, so sample b owns rows
-    ``[offsets[b], offsets[b+1])``; padding rows are zeros.  B = 0 when no payload has
-    an event.  ``out`` receives the data when it is long enough (``3 Eb + B + 1``).
+    ``[offsets[b], offsets[b+1])``; padding rows are zeros.  Bb is ``batch_bucket(B)``
+    with ``batch_pad`` (empty samples B..Bb-1: their offsets are E), else B.  B = 0
+    when no payload has an event.  ``out`` receives the data when it is long enough
+    (``3 Eb + Bb + 1``).
     """
     cols = [_as_columns(p.get("events", [])) for p in payloads]
     counts = np.array([c[0].shape[0] for c in cols], dtype=np.int64)
@@ -109,15 +125,17 @@ def pack_payloads(payloads: list[dict[str, Any]], bucket: bool = True,
     if nonempty.size == 0:
         return np.zeros(1, dtype=np.int64), 0, 0, 0
     B = int(nonempty[-1]) + 1
+    Bb = batch_bucket(B) if batch_pad else B
     E = int(counts[:B].sum())
     Eb = event_bucket(E) if bucket else E
-    n = 3 * Eb + B + 1
+    n = 3 * Eb + Bb + 1
     h = out[:n] if out is not None and out.shape[0] >= n else np.empty(n, dtype=np.int64)
     for f in range(3):
         np.concatenate([c[f] for c in cols[:B]], out=h[f * Eb:f * Eb + E])
         h[f * Eb + E:(f + 1) * Eb] = 0  # padding events: valid table rows, never attended
     h[3 * Eb] = 0
-    np.cumsum(counts[:B], out=h[3 * Eb + 1:n])
+    np.cumsum(counts[:B], out=h[3 * Eb + 1:3 * Eb + B + 1])
+    h[3 * Eb + B + 1:n] = E  # padding samples: empty
     return h, B, E, Eb
 
 
@@ -195,13 +213,14 @@ class PendingBatch:
 class InferenceWorker:
     """Batched inference worker (reference worker.py:92-253); one model, one GPU.
 
-    ``use_graphs`` replays a captured graph per (B, event bucket), keeping at most
-    ``max_graphs`` of them (least recently used evicted); all share one memory pool,
-    which is safe because batches never overlap.
+    ``use_graphs`` replays a captured graph per (batch bucket, event bucket), keeping at
+    most ``max_graphs`` of them (least recently used evicted); all share one memory pool,
+    which is safe because batches never overlap.  ``captures`` counts the graphs
+    captured so far.
     """
 
     def __init__(self, model: nn.Module, config: CortexConfig, device: torch.device, max_batch_size: int = 32,
-                 *, use_graphs: bool = True, max_graphs: int = 64) -> None:
+                 *, use_graphs: bool = True, max_graphs: int = 128) -> None:
         device = torch.device(device)
         if device.type != "cuda":
             raise RuntimeError("InferenceWorker runs the gfx950 forward; it needs a ROCm device")
@@ -221,6 +240,7 @@ class InferenceWorker:
         self._next_slot = 0
         self._plan_dev: torch.Tensor | None = None
         self._loaded = False
+        self.captures = 0
 
     # ------------------------------------------------------------------ API
 
@@ -255,18 +275,14 @@ class InferenceWorker:
         ``submit_windows``).  ``collect`` gives the result dicts.  Not thread-safe."""
         t0 = time.perf_counter()
         slot = self._acquire_slot()
-        flat, B, E, Eb = pack_payloads(payloads, self.use_graphs, slot.host_in.numpy())
+        flat, B, E, Eb = pack_payloads(payloads, self.use_graphs, slot.host_in.numpy(), batch_pad=self.use_graphs)
         dim = self.config.behavior_dim
         pending = PendingBatch(slot, payloads, B, dim, t0)
         if B == 0:
             pending._rows = np.zeros((0, dim), dtype=np.float32)
             pending._ms = (time.perf_counter() - t0) * 1000
             return pending
-        n_in = 3 * Eb + B + 1
-        if flat.ctypes.data != slot.host_in.data_ptr():  # did not fit: grow the pinned buffer
-            slot.host_in = torch.empty(max(n_in, 2 * slot.host_in.numel()), dtype=torch.int64).pin_memory()
-            slot.host_in.numpy()[:n_in] = flat[:n_in]
-        src = slot.host_in[:n_in]
+        src = self._stage(slot, flat, 3 * Eb + self._bb(B) + 1)
         self._launch(slot, B, Eb, lambda inp, err: inp.copy_(src, non_blocking=True))
         slot.pending = pending
         return pending
@@ -280,15 +296,11 @@ class InferenceWorker:
         t0 = time.perf_counter()
         dim = self.config.behavior_dim
         slot = self._acquire_slot()
-        flat, B, E, Eb = pack_payloads(payloads, self.use_graphs, slot.host_in.numpy())
+        flat, B, E, Eb = pack_payloads(payloads, self.use_graphs, slot.host_in.numpy(), batch_pad=self.use_graphs)
         if B == 0:
             ms = (time.perf_counter() - t0) * 1000
             return [{"request_id": p["request_id"], "behavior": [0.0] * dim, "inference_ms": ms} for p in payloads]
-        n_in = 3 * Eb + B + 1
-        if flat.ctypes.data != slot.host_in.data_ptr():  # did not fit: grow the pinned buffer
-            slot.host_in = torch.empty(max(n_in, 2 * slot.host_in.numel()), dtype=torch.int64).pin_memory()
-            slot.host_in.numpy()[:n_in] = flat[:n_in]
-        src = slot.host_in[:n_in]
+        src = self._stage(slot, flat, 3 * Eb + self._bb(B) + 1)
         behavior = self._forward(slot, B, Eb, lambda inp, err: inp.copy_(src, non_blocking=True))
         ms = (time.perf_counter() - t0) * 1000
         rows = behavior.tolist()
@@ -316,23 +328,25 @@ class InferenceWorker:
             raise ValueError("submit_windows needs at least one request")
         items, offsets = cache.plan([(r["session_id"], int(r["window_start"])) for r in requests], window_bins)
         B, E = len(requests), int(offsets[-1])
+        Bb = self._bb(B)
         Eb = event_bucket(E) if self.use_graphs else max(E, 1)
-        n_host = B + 1 + items.size
+        n_host = Bb + 1 + items.size
         slot = self._acquire_slot()
         if slot.host_in.numel() < n_host:
             slot.host_in = torch.empty(max(n_host, 2 * slot.host_in.numel()), dtype=torch.int64).pin_memory()
         h = slot.host_in.numpy()
         h[:B + 1] = offsets
-        h[B + 1:n_host] = items.reshape(-1)
+        h[B + 1:Bb + 1] = E  # padding samples: empty
+        h[Bb + 1:n_host] = items.reshape(-1)
         have = 0 if self._plan_dev is None else self._plan_dev.numel()
         if have < max(items.size, 4):
             self._stream.synchronize()  # the old plan buffer may still be read by a queued gather
             self._plan_dev = torch.empty(max(items.size, 4, 2 * have), dtype=torch.int64, device=self.device)
         plan_dev = self._plan_dev[:items.size].view(-1, 4)
-        off_host, plan_host = slot.host_in[:B + 1], slot.host_in[B + 1:n_host]
+        off_host, plan_host = slot.host_in[:Bb + 1], slot.host_in[Bb + 1:n_host]
 
         def fill(inp: torch.Tensor, err: torch.Tensor) -> None:
-            inp[3 * Eb:3 * Eb + B + 1].copy_(off_host, non_blocking=True)
+            inp[3 * Eb:3 * Eb + Bb + 1].copy_(off_host, non_blocking=True)
             if items.shape[0]:
                 plan_dev.view(-1).copy_(plan_host, non_blocking=True)
                 cache.gather(plan_dev, inp, Eb, E, err)
@@ -364,19 +378,33 @@ class InferenceWorker:
         slot.done.synchronize()
         return slot
 
+    def _bb(self, B: int) -> int:
+        """Samples the forward runs for B real ones (the graph's batch bucket)."""
+        return batch_bucket(B) if self.use_graphs else B
+
+    @staticmethod
+    def _stage(slot: _Slot, flat: np.ndarray, n_in: int) -> torch.Tensor:
+        """The first ``n_in`` words of the packed batch in the slot's pinned buffer."""
+        if flat.ctypes.data != slot.host_in.data_ptr():  # did not fit: grow the pinned buffer
+            slot.host_in = torch.empty(max(n_in, 2 * slot.host_in.numel()), dtype=torch.int64).pin_memory()
+            slot.host_in.numpy()[:n_in] = flat[:n_in]
+        return slot.host_in[:n_in]
+
     def _launch(self, slot: _Slot, B: int, Eb: int, fill) -> None:
-        """``fill(inp, err)`` writes the (B, Eb) input buffer on the worker stream; then the
-        forward runs and the (B, dim) behaviour is copied into ``slot`` (no host wait)."""
+        """``fill(inp, err)`` writes the (Bb, Eb) input buffer on the worker stream (Bb =
+        ``_bb(B)``); then the forward runs and the first B rows of the behaviour are copied
+        into ``slot`` (no host wait)."""
         dim = self.config.behavior_dim
+        Bb = self._bb(B)
         if slot.host_out.numel() < B * dim:
             slot.host_out = torch.empty(max(B * dim, 2 * slot.host_out.numel()), dtype=torch.float32).pin_memory()
         with torch.cuda.device(self.device), torch.cuda.stream(self._stream):
             if self.use_graphs:
-                g = self._graph(B, Eb)
+                g = self._graph(Bb, Eb)
                 g.err.zero_()
                 fill(g.inp, g.err)
                 g.graph.replay()
-                out, err = g.out, g.err
+                out, err = g.out[:B], g.err
             else:
                 inp = torch.empty(3 * Eb + B + 1, dtype=torch.int64, device=self.device)
                 err = torch.zeros(1, dtype=torch.int32, device=self.device)
@@ -407,6 +435,7 @@ class InferenceWorker:
                 self._graphs.popitem(last=False)
             g = _CsrGraph(self.model, B, Eb, self.device, self._stream, self._pool)
             self._graphs[key] = g
+            self.captures += 1
         else:
             self._graphs.move_to_end(key)
         return g

@@ -96,8 +96,9 @@ __global__ __launch_bounds__(ATT_THREADS) void attention_kernel(AttnArgs a) {
   const T* Kb;
   const T* Vb;
   if (a.kv_off) {
-    const int64_t r0 = a.kv_off[b];
-    len = a.kv_off[b + 1] - r0;
+    // offsets come from the caller: clamp them to the Lk key rows of the view
+    const int64_t r0 = min(max(a.kv_off[b], (int64_t)0), a.Lk);
+    len = min(max(a.kv_off[b + 1], r0), a.Lk) - r0;
     Kb = reinterpret_cast<const T*>(a.k) + r0 * a.k_sl + h * a.k_sh;
     Vb = reinterpret_cast<const T*>(a.v) + r0 * a.v_sl + h * a.v_sh;
   } else {

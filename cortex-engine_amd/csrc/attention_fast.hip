@@ -104,8 +104,9 @@ void attention_fast_kernel(AttnArgs a) {
   const bf16* Kb;
   const bf16* Vb;
   if (a.kv_off) {
-    const int64_t r0 = a.kv_off[b];
-    len = a.kv_off[b + 1] - r0;
+    // offsets come from the caller: clamp them to the Lk key rows of the view
+    const int64_t r0 = min(max(a.kv_off[b], (int64_t)0), a.Lk);
+    len = min(max(a.kv_off[b + 1], r0), a.Lk) - r0;
     Kb = reinterpret_cast<const bf16*>(a.k) + r0 * a.k_sl + h * a.k_sh;
     Vb = reinterpret_cast<const bf16*>(a.v) + r0 * a.v_sl + h * a.v_sh;
   } else {

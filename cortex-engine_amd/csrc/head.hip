@@ -272,6 +272,78 @@ __global__ __launch_bounds__(256) void head_merge_kernel(HeadArgs a) {
   }
 }
 
+// Masked-spike head (reference cortex/models/cortex.py:56-69): the mean over a sample's
+// L latent rows (after an optional LayerNorm, the encoder's final norm) and a small
+// linear N x D (+ bias) on that mean.  One workgroup per sample; wavefront w takes rows
+// w, w + 4, ... and keeps its column sums in registers (EPL = D / 64 per lane, the
+// ln_regs layout), so rows are read once and no barrier sits inside the row loop.
+struct PoolArgs {
+  const float* x;
+  int64_t ld_x, L;
+  const float* gamma;  // LayerNorm applied to each row first when non-null
+  const float* beta;
+  float eps;
+  int N;
+  int w_dtype;       // DT_F32 or DT_I8
+  const void* w;     // (N, D) rows, ld_w apart; null: pooled rows only
+  int64_t ld_w;
+  const float* w_scale;  // (N) per-row scale of an int8 weight
+  const float* bias;     // (N) or null
+  float* pooled;         // (B, D) mean rows, or null
+  float* out;            // (B, N)
+};
+
+template <int EPL>
+__global__ __launch_bounds__(256) void pooled_linear_kernel(PoolArgs a) {
+  constexpr int D = EPL * 64;
+  __shared__ float part[4][D];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int64_t b = blockIdx.x;
+  float acc[EPL];
+#pragma unroll
+  for (int j = 0; j < EPL; ++j) acc[j] = 0.0f;
+  const float inv_k = 1.0f / (float)D;
+  for (int64_t l = w; l < a.L; l += 4) {
+    const float* row = a.x + (b * a.L + l) * a.ld_x;
+    float v[EPL];
+#pragma unroll
+    for (int j = 0; j < EPL; j += 4) {
+      const float4 t = *reinterpret_cast<const float4*>(row + (j >> 2) * 256 + lane * 4);
+      v[j] = t.x;
+      v[j + 1] = t.y;
+      v[j + 2] = t.z;
+      v[j + 3] = t.w;
+    }
+    if (a.gamma) ln_regs<EPL>(v, inv_k, a.eps, a.gamma, a.beta, lane);
+#pragma unroll
+    for (int j = 0; j < EPL; ++j) acc[j] += v[j];
+  }
+#pragma unroll
+  for (int j = 0; j < EPL; ++j) part[w][(j >> 2) * 256 + lane * 4 + (j & 3)] = acc[j];
+  __syncthreads();
+  const float inv_l = 1.0f / (float)a.L;
+  for (int k = threadIdx.x; k < D; k += 256) {
+    const float m = ((part[0][k] + part[1][k]) + (part[2][k] + part[3][k])) * inv_l;
+    part[0][k] = m;
+    if (a.pooled) a.pooled[b * D + k] = m;
+  }
+  __syncthreads();
+  if (!a.w) return;
+  for (int n = w; n < a.N; n += 4) {
+    float dot = 0.0f;
+    if (a.w_dtype == DT_I8) {
+      const int8_t* wr = reinterpret_cast<const int8_t*>(a.w) + (int64_t)n * a.ld_w;
+      const float sc = a.w_scale[n];
+      for (int k = lane; k < D; k += 64) dot = fmaf(part[0][k], (float)(int)wr[k] * sc, dot);
+    } else {
+      const float* wr = reinterpret_cast<const float*>(a.w) + (int64_t)n * a.ld_w;
+      for (int k = lane; k < D; k += 64) dot = fmaf(part[0][k], wr[k], dot);
+    }
+    dot = wave_sum(dot);
+    if (lane == 0) a.out[b * a.N + n] = dot + (a.bias ? a.bias[n] : 0.0f);
+  }
+}
+
 bool al(const void* p, int n) { return ((uintptr_t)p % n) == 0; }
 
 }  // namespace
@@ -332,5 +404,34 @@ extern "C" int cortex_behavior_head(const float* x, int64_t ld_x, int64_t B, int
   CORTEX_CHECK_LAUNCH("head_partial_kernel");
   hipLaunchKernelGGL(head_merge_kernel, dim3((unsigned)B), dim3(256), 0, stream, a);
   CORTEX_CHECK_LAUNCH("head_merge_kernel");
+  return OK;
+}
+
+extern "C" int cortex_pooled_linear(const float* x, int64_t ld_x, int64_t B, int64_t L, int64_t D, const float* gamma,
+                                    const float* beta, float eps, int64_t N, int w_dtype, const void* w,
+                                    int64_t ld_w, const float* w_scale, const float* bias, float* pooled,
+                                    float* out, hipStream_t stream) {
+  CORTEX_CHECK_ARG(B >= 0 && L >= 1 && N >= 0, "cortex_pooled_linear: bad sizes");
+  CORTEX_CHECK_ARG(D == 256 || D == 512 || D == 768 || D == 1024, "cortex_pooled_linear: D must be 256, 512, 768 or 1024");
+  if (B == 0) return OK;
+  CORTEX_CHECK_ARG(x && ld_x >= D && ld_x % 4 == 0 && al(x, 16), "cortex_pooled_linear: x must be 16-byte aligned rows");
+  CORTEX_CHECK_ARG(!gamma || (beta && al(gamma, 16) && al(beta, 16)),
+                   "cortex_pooled_linear: LayerNorm needs 16-byte aligned gamma and beta");
+  CORTEX_CHECK_ARG(w || pooled, "cortex_pooled_linear: nothing to write (no weight and no pooled output)");
+  if (w) {
+    CORTEX_CHECK_ARG(out && ld_w >= D, "cortex_pooled_linear: null out or weight stride below D");
+    CORTEX_CHECK_ARG(w_dtype == DT_F32 || (w_dtype == DT_I8 && w_scale),
+                     "cortex_pooled_linear: weight must be fp32, or int8 with a per-row scale");
+  }
+  CORTEX_CHECK_ARG(B <= 0x7fffffffLL && N <= 0x7fffffffLL, "cortex_pooled_linear: B or N too large");
+  PoolArgs a{x, ld_x, L, gamma, beta, eps, (int)N, w_dtype, w, ld_w, w_scale, bias, pooled, out};
+  const dim3 grid((unsigned)B), block(256);
+  switch (D) {
+    case 256: hipLaunchKernelGGL(pooled_linear_kernel<4>, grid, block, 0, stream, a); break;
+    case 512: hipLaunchKernelGGL(pooled_linear_kernel<8>, grid, block, 0, stream, a); break;
+    case 768: hipLaunchKernelGGL(pooled_linear_kernel<12>, grid, block, 0, stream, a); break;
+    default: hipLaunchKernelGGL(pooled_linear_kernel<16>, grid, block, 0, stream, a); break;
+  }
+  CORTEX_CHECK_LAUNCH("pooled_linear_kernel");
   return OK;
 }

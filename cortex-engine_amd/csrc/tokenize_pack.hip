@@ -204,7 +204,9 @@ __global__ __launch_bounds__(256) void pack_sorted_kernel(const int64_t* __restr
     if (e >= E) break;
     const int64_t b = bidx[e * s_bidx];
     const int64_t bp = e > 0 ? bidx[(e - 1) * s_bidx] : -1;
-    if (b < 0 || b >= B || bp > b) {
+    // bp is -1 only for the first event: a negative index before e is out of range, and
+    // taking it as the loop start below would write offsets[] below index 0.
+    if (b < 0 || b >= B || bp > b || (e > 0 && bp < 0)) {
       my_bad = true;
       continue;
     }

@@ -179,7 +179,8 @@ int cortex_norm_linear(int64_t M, int64_t N, int64_t K, int x_dtype, const void*
  *   out[b,h,i,:] = softmax_j(scale * q[b,h,i,:].k[b,h,j,:] | allowed) v[b,h,j,:]
  * Element (b,h,i,j) = base + b*s_b + h*s_h + i*s_l + d (q batch stride may be 0).
  * With kv_offsets (B+1), sample b's keys are CSR rows [kv_offsets[b], kv_offsets[b+1])
- * (row r at base + r*s_l + h*s_h); otherwise Lk keys per sample.
+ * (row r at base + r*s_l + h*s_h), both ends clamped to [0, Lk] with Lk the number
+ * of key rows of the view; otherwise Lk keys per sample.
  * Key j is allowed iff j < length (kv_lengths[b] when given), key_mask[b*km_sb + j]
  * != 0 (when given) and block_mask[b*bm_sb + (i/block_l)*n_kt + j/block_e] != 0
  * (when given; bm_sb 0 shares one tile mask across the batch).  Rows with no
@@ -300,6 +301,19 @@ int cortex_behavior_head(const float* x, int64_t ld_x, int64_t B, int64_t L, int
 
 /* Bytes of the partials workspace cortex_behavior_head needs for B samples of L latents. */
 int64_t cortex_behavior_head_workspace_bytes(int64_t B, int64_t L);
+
+/* Masked-spike head (MaskedSpikeHead.forward, cortex/models/cortex.py:56-69, returned as
+ * masked_spike_logits by CortexModel.forward(return_aux=True), :119-120):
+ *   m_b = mean_l LN(x[b*L + l])          (LN skipped when gamma is null)
+ *   out[b, n] = m_b . w[n] (* w_scale[n] for int8) + bias[n]
+ * x: B*L fp32 rows of D (16-byte aligned, ld_x apart); w: (N, D) fp32, or int8 with its
+ * per-row scale (QuantizedLinear, calibrate.py:225-228); bias optional.  pooled (B, D)
+ * receives the mean rows when non-null (w may then be null: the mean alone).
+ * D in {256, 512, 768, 1024}. */
+int cortex_pooled_linear(const float* x, int64_t ld_x, int64_t B, int64_t L, int64_t D, const float* gamma,
+                         const float* beta, float eps, int64_t N, int w_dtype, const void* w, int64_t ld_w,
+                         const float* w_scale, const float* bias, float* pooled, float* out,
+                         hipStream_t stream);
 
 /* Streaming window assembly from device event pages.  No single reference
  * counterpart: it serves StreamingKVCache's role (cortex/cache/streaming.py:79-236)

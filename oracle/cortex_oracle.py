@@ -37,6 +37,8 @@ rms_norm_linear             torch.nn.functional.rms_norm + matmul (library
                             routine); gamma=1 and large-x known answers
 forward / forward_int8      behavior goldens written by importing the reference
                             (seeded CORTEX_XS and CORTEX_S, fp32 and INT8)
+masked_spike_head           masked_spike_logits goldens from the same import
+                            (return_aux=True, fp32 and INT8 models)
 ==========================  ==================================================
 """
 
@@ -384,15 +386,22 @@ def behavior_head(sd: dict, shape: ModelShape, latents: torch.Tensor) -> torch.T
     return _linear(sd, f"{p}.out_proj", _merge(o)).squeeze(-1)
 
 
+def masked_spike_head(sd: dict, latents: torch.Tensor) -> torch.Tensor:
+    """MaskedSpikeHead.forward (reference cortex/models/cortex.py:56-69): ``proj`` (with
+    bias) of the mean over latents; returned as ``masked_spike_logits`` (:119-120)."""
+    return _linear(sd, "masked_spike_head.proj", latents.mean(dim=1))
+
+
 def forward(sd: dict, shape: ModelShape, neuron_ids, time_bins, values, batch_indices,
-            batch_size: int | None = None, sections: dict | None = None) -> torch.Tensor:
+            batch_size: int | None = None, sections: dict | None = None, aux: dict | None = None) -> torch.Tensor:
     """CortexModel.forward (reference cortex/models/cortex.py:90-122) in fp32 on the CPU.
 
     ``sd`` is a CPU state_dict of a float model or of a model after the reference's
     ``convert_model`` (int8 ``weight_int8`` + fp32 ``weight_scale`` buffers).
     Returns ``behavior`` (B, behavior_dim).  ``sections``, when given, receives wall
     seconds per section (tokenizer, pack_events, cross_attn, self_attn_all,
-    behavior_head), as the reference's profile_inference.py sections.
+    behavior_head), as the reference's profile_inference.py sections.  ``aux``, when
+    given, receives ``masked_spike_logits`` (the ``return_aux`` output, :119-120).
     """
     t0 = time.perf_counter()
     sd = {k: v.detach().cpu() for k, v in sd.items()}
@@ -410,6 +419,8 @@ def forward(sd: dict, shape: ModelShape, neuron_ids, time_bins, values, batch_in
         lat = encode(sd, shape, tokens, mask, sections)
         t3 = time.perf_counter()
         out = behavior_head(sd, shape, lat)
+        if aux is not None:
+            aux["masked_spike_logits"] = masked_spike_head(sd, lat)
     if sections is not None:
         sections["tokenizer"] = t1 - t0
         sections["pack_events"] = t2 - t1

@@ -14,7 +14,10 @@ things that no closed form can pin:
 3. the INT8 model produced by attach_calibration_hooks -> derive_scales ->
    convert_model (reference cortex/quantization/calibrate.py:99-279) and its
    forward with fp32 activations -- stored as per-layer int8/scale checksums and
-   ``behavior`` outputs.
+   ``behavior`` outputs;
+4. the ``return_aux`` output ``masked_spike_logits`` (reference cortex/models/cortex.py:
+   56-69,119-120) of both models, whose ``masked_spike_head.proj`` stays float because
+   calibration forwards never call that head.
 
 Outputs are data only (inputs and expected outputs); no reference source is copied.
 """
@@ -98,12 +101,11 @@ def main() -> None:
         for iname, inp in input_sets.items():
             t = {k: torch.from_numpy(v) for k, v in inp.items()}
             with torch.no_grad():
-                beh = model(t["neuron_ids"], t["time_bins"], t["values"], t["batch_indices"])[
-                    "behavior"
-                ]
+                out = model(t["neuron_ids"], t["time_bins"], t["values"], t["batch_indices"], return_aux=True)
             for k, v in inp.items():
                 arrays[f"{cfg_name}_{iname}_{k}"] = v
-            arrays[f"{cfg_name}_{iname}_behavior_fp32"] = beh.numpy().astype(np.float32)
+            arrays[f"{cfg_name}_{iname}_behavior_fp32"] = out["behavior"].numpy().astype(np.float32)
+            arrays[f"{cfg_name}_{iname}_aux_fp32"] = out["masked_spike_logits"].numpy().astype(np.float32)
             case["inputs"][iname] = {"n_events": int(inp["neuron_ids"].shape[0])}
 
         # INT8: one calibration forward on the "sorted" inputs, then convert.
@@ -122,10 +124,9 @@ def main() -> None:
         for iname, inp in input_sets.items():
             t = {k: torch.from_numpy(v) for k, v in inp.items()}
             with torch.no_grad():
-                beh = qmodel(t["neuron_ids"], t["time_bins"], t["values"], t["batch_indices"])[
-                    "behavior"
-                ]
-            arrays[f"{cfg_name}_{iname}_behavior_int8"] = beh.numpy().astype(np.float32)
+                out = qmodel(t["neuron_ids"], t["time_bins"], t["values"], t["batch_indices"], return_aux=True)
+            arrays[f"{cfg_name}_{iname}_behavior_int8"] = out["behavior"].numpy().astype(np.float32)
+            arrays[f"{cfg_name}_{iname}_aux_int8"] = out["masked_spike_logits"].numpy().astype(np.float32)
 
         # Exact int8 rows of a few layers (small slices) so a one-off rounding slip shows.
         for key in (

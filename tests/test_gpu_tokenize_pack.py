@@ -232,6 +232,12 @@ def _sorted_cases():
     cases["single_event"] = (np.array([2]), 5)
     cases["one_sample"] = (np.zeros(65536, dtype=np.int64), 1)
     cases["all_distinct_1024"] = (np.arange(1024), 1024)
+    # a negative index just before a valid one: the boundary loop must not start below 0
+    cases["negative_before_valid"] = (np.array([-2, 0, 0, 1]), 4)
+    cases["very_negative_before_valid"] = (np.array([-(1 << 40), 0]), 2)
+    b = np.sort(rng.integers(0, 6, 2500))
+    b[1024] = -7  # first event of the second range
+    cases["negative_at_range_start"] = (b, 6)
     return cases
 
 

@@ -93,6 +93,24 @@ def test_oracle_forward_int8_matches_reference(golden, name, inputs):
     np.testing.assert_allclose(beh.numpy(), arr[p + "behavior_int8"], rtol=1e-5, atol=1e-6)
 
 
+@pytest.mark.parametrize("name", ["xs", "s"])
+@pytest.mark.parametrize("inputs", ["sorted", "shuffled"])
+@pytest.mark.parametrize("quant", ["fp32", "int8"])
+def test_oracle_masked_spike_logits_match_reference(golden, name, inputs, quant):
+    """``return_aux`` output of the reference (masked_spike_head.proj stays float in the INT8
+    model: calibration forwards never reach it)."""
+    meta, arr = golden
+    sd = _product_model(name, meta["cases"][name]["seed"]).state_dict()
+    if quant == "int8":
+        sd = O.quantize_state_dict(sd)
+    shape = O.CORTEX_XS_SHAPE if name == "xs" else O.CORTEX_S_SHAPE
+    p = f"{name}_{inputs}_"
+    aux: dict = {}
+    O.forward(sd, shape, arr[p + "neuron_ids"], arr[p + "time_bins"], arr[p + "values"], arr[p + "batch_indices"],
+              aux=aux)
+    np.testing.assert_allclose(aux["masked_spike_logits"].numpy(), arr[p + f"aux_{quant}"], rtol=1e-5, atol=1e-6)
+
+
 def test_golden_int8_differs_from_fp32(golden):
     """The INT8 goldens are a different model from the fp32 ones (guards a no-op convert)."""
     _, arr = golden

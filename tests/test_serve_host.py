@@ -6,7 +6,7 @@ from __future__ import annotations
 import numpy as np
 import pytest
 
-from cortex.serve.worker import event_bucket, pack_payloads
+from cortex.serve.worker import batch_bucket, event_bucket, pack_payloads
 
 
 def _payload(i, n, rng):
@@ -70,3 +70,29 @@ def test_pack_payloads_columnar_and_buffer_reuse():
 def test_pack_payloads_no_events():
     flat, B, E, Eb = pack_payloads([{"request_id": "a", "events": []}, {"request_id": "b"}])
     assert (B, E, Eb) == (0, 0, 0)
+
+
+def test_batch_bucket_bounds():
+    """At most 25 % padding samples, monotone, and few distinct sizes (four per doubling)."""
+    prev = 0
+    for b in range(1, 2049):
+        bb = batch_bucket(b)
+        assert bb >= b and bb >= prev and (bb == b if b <= 8 else bb <= 1.25 * b)
+        prev = bb
+    assert len({batch_bucket(b) for b in range(1, 257)}) <= 8 + 4 * 5
+    assert [batch_bucket(b) for b in (8, 9, 11, 17, 33, 100, 256, 257)] == [8, 10, 12, 20, 40, 112, 256, 320]
+
+
+def test_pack_payloads_batch_pad_appends_empty_samples():
+    rng = np.random.default_rng(6)
+    payloads = [_payload(i, n, rng) for i, n in enumerate([3, 0, 9, 4, 1, 1, 2, 5, 7, 2, 0])]
+    a, B, E, Eb = pack_payloads(payloads)
+    b, B2, E2, Eb2 = pack_payloads(payloads, batch_pad=True)
+    assert (B, E, Eb) == (B2, E2, Eb2) == (10, 34, 256)
+    Bb = batch_bucket(B)
+    assert Bb == 10 and b.shape[0] == 3 * Eb + Bb + 1
+    np.testing.assert_array_equal(b[:3 * Eb + B + 1], a)
+    payloads.append(_payload(11, 3, rng))  # B = 12 -> bucket 12; B = 9 below pads to 10
+    c, B3, E3, _ = pack_payloads(payloads[:9], batch_pad=True)
+    assert B3 == 9 and c.shape[0] == 3 * 256 + 10 + 1
+    assert c[-1] == c[-2] == E3
