@@ -14,6 +14,8 @@
 //     padded (B, E_max) layout with its bool mask (cortex.py:146-147,163-164).
 #include <hip/hip_runtime.h>
 
+#include <mutex>
+
 #include "common.h"
 
 namespace cortex {
@@ -504,25 +506,30 @@ int64_t cortex_pack_workspace_bytes(int64_t E, int64_t B) {
   return nchunks * B * (int64_t)sizeof(int);
 }
 
-int cortex_pack_plan(const int64_t* batch_indices, int64_t s_bidx, int64_t E, int64_t B, int64_t* offsets,
-                     int64_t* order, int64_t* dst_rows, int64_t* rank, void* workspace, int64_t workspace_bytes,
-                     int32_t* err_flag, hipStream_t stream) {
-  CORTEX_CHECK_ARG(E >= 0 && B >= 1, "cortex_pack_plan: need E >= 0 and B >= 1 (got E=%lld B=%lld)",
-                   (long long)E, (long long)B);
-  CORTEX_CHECK_ARG(B <= PACK_MAX_B, "cortex_pack_plan: B=%lld exceeds the supported maximum %d", (long long)B,
-                   PACK_MAX_B);
-  CORTEX_CHECK_ARG(offsets != nullptr, "cortex_pack_plan: offsets must not be null");
+}  // extern "C"
+
+// The plan itself, shared by cortex_pack_plan (caller's workspace) and
+// cortex_pack_plan_noalloc (the library's static scratch).  Every workspace word a
+// launch reads was written by an earlier launch of the same call, so nothing in it
+// needs clearing between calls.
+static int pack_plan_impl(const char* who, const int64_t* batch_indices, int64_t s_bidx, int64_t E, int64_t B,
+                          int64_t* offsets, int64_t* order, int64_t* dst_rows, int64_t* rank, void* workspace,
+                          int64_t workspace_bytes, int32_t* err_flag, hipStream_t stream) {
+  CORTEX_CHECK_ARG(E >= 0 && B >= 1, "%s: need E >= 0 and B >= 1 (got E=%lld B=%lld)", who, (long long)E,
+                   (long long)B);
+  CORTEX_CHECK_ARG(B <= PACK_MAX_B, "%s: B=%lld exceeds the supported maximum %d", who, (long long)B, PACK_MAX_B);
+  CORTEX_CHECK_ARG(offsets != nullptr, "%s: offsets must not be null", who);
   if (E == 0) {
     hipLaunchKernelGGL(fill_i64_kernel, dim3((unsigned)cdiv(B + 1, 256)), dim3(256), 0, stream, offsets, B + 1,
                        (int64_t)0);
     CORTEX_CHECK_LAUNCH("cortex_pack_plan(E=0)");
     return OK;
   }
-  CORTEX_CHECK_ARG(batch_indices && order, "cortex_pack_plan: batch_indices and order must not be null");
+  CORTEX_CHECK_ARG(batch_indices && order, "%s: batch_indices and order must not be null", who);
   const int64_t need = cortex_pack_workspace_bytes(E, B);
   if (workspace_bytes < need || (need > 0 && workspace == nullptr)) {
-    set_error("cortex_pack_plan: workspace of %lld bytes is smaller than the required %lld",
-              (long long)workspace_bytes, (long long)need);
+    set_error("%s: workspace of %lld bytes is smaller than the required %lld", who, (long long)workspace_bytes,
+              (long long)need);
     return E_WORKSPACE;
   }
   if (B <= PS_MAX_B && E <= PS_MAX_E) {
@@ -554,6 +561,80 @@ int cortex_pack_plan(const int64_t* batch_indices, int64_t s_bidx, int64_t E, in
                      counts, offsets, order, dst_rows, rank);
   CORTEX_CHECK_LAUNCH("pack_rank_kernel");
   return OK;
+}
+
+// Scratch of cortex_pack_plan_noalloc: the per-chunk counts (three-launch plan) or the
+// per-range status words (sorted fast path) that cortex_pack_plan keeps in the caller's
+// workspace.  One copy per GPU, held until the process ends.  In host code `scratch`
+// only names the symbol: its device address comes from hipGetSymbolAddress, once per
+// device, and only that address is ever handed to a kernel.
+constexpr int64_t PACK_SCRATCH_BYTES = (int64_t)4 << 20;
+static __device__ __align__(256) int scratch[PACK_SCRATCH_BYTES / sizeof(int)];
+
+constexpr int PACK_SCRATCH_MAX_DEVICES = 64;
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[PACK_SCRATCH_MAX_DEVICES];
+
+// Device address of `scratch` on `dev`, looked up once per device with `dev` current.
+static int pack_scratch_ptr(int dev, void** out) {
+  if (dev < 0 || dev >= PACK_SCRATCH_MAX_DEVICES) {
+    set_error("cortex_pack_plan_noalloc: device %d outside [0, %d)", dev, PACK_SCRATCH_MAX_DEVICES);
+    return E_INVALID;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    int cur = -1;
+    hipError_t e = hipGetDevice(&cur);
+    if (e == hipSuccess && cur != dev) e = hipSetDevice(dev);
+    void* p = nullptr;
+    if (e == hipSuccess) e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (cur >= 0 && cur != dev) {
+      const hipError_t r = hipSetDevice(cur);
+      if (e == hipSuccess) e = r;
+    }
+    if (e != hipSuccess || p == nullptr) {
+      set_error("cortex_pack_plan_noalloc: scratch address on device %d: %s", dev,
+                e != hipSuccess ? hipGetErrorString(e) : "null");
+      return E_LAUNCH;
+    }
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return OK;
+}
+
+extern "C" {
+
+int cortex_pack_plan(const int64_t* batch_indices, int64_t s_bidx, int64_t E, int64_t B, int64_t* offsets,
+                     int64_t* order, int64_t* dst_rows, int64_t* rank, void* workspace, int64_t workspace_bytes,
+                     int32_t* err_flag, hipStream_t stream) {
+  return pack_plan_impl("cortex_pack_plan", batch_indices, s_bidx, E, B, offsets, order, dst_rows, rank, workspace,
+                        workspace_bytes, err_flag, stream);
+}
+
+int64_t cortex_pack_noalloc_max_workspace_bytes(void) { return PACK_SCRATCH_BYTES; }
+
+int cortex_pack_plan_noalloc(const int64_t* batch_indices, int64_t s_bidx, int64_t E, int64_t B, int64_t* offsets,
+                             int64_t* order, int64_t* dst_rows, int64_t* rank, int32_t* err_flag,
+                             hipStream_t stream) {
+  const int64_t need = cortex_pack_workspace_bytes(E, B);
+  if (need > PACK_SCRATCH_BYTES) {
+    set_error("cortex_pack_plan_noalloc: E=%lld, B=%lld needs %lld bytes of scratch, above its maximum of %lld "
+              "(use cortex_pack_plan with a workspace)",
+              (long long)E, (long long)B, (long long)need, (long long)PACK_SCRATCH_BYTES);
+    return E_WORKSPACE;
+  }
+  int dev = -1;
+  hipError_t e = stream ? hipStreamGetDevice(stream, &dev) : hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    set_error("cortex_pack_plan_noalloc: device of the stream: %s", hipGetErrorString(e));
+    return E_LAUNCH;
+  }
+  void* ws = nullptr;
+  const int rc = pack_scratch_ptr(dev, &ws);
+  if (rc != OK) return rc;
+  return pack_plan_impl("cortex_pack_plan_noalloc", batch_indices, s_bidx, E, B, offsets, order, dst_rows, rank, ws,
+                        PACK_SCRATCH_BYTES, err_flag, stream);
 }
 
 int cortex_tokenize(int dtype, int64_t D, const void* neuron_emb, int64_t n_neuron, int64_t ld_neuron,

@@ -50,6 +50,19 @@ int cortex_pack_plan(const int64_t* batch_indices, int64_t s_bidx, int64_t E, in
                      int64_t* order, int64_t* dst_rows, int64_t* rank, void* workspace, int64_t workspace_bytes,
                      int32_t* err_flag, hipStream_t stream);
 
+/* cortex_pack_plan without a workspace argument and without any allocation.  No
+ * counterpart in the reference: it is for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * The workspace is a static device array of cortex_pack_noalloc_max_workspace_bytes()
+ * (4 MiB) per GPU, held until the process ends; sizes with
+ * cortex_pack_workspace_bytes(E, B) above it return -4 before any launch.  Every call on
+ * one GPU uses that GPU's one array: calls that overlap on a GPU (concurrent streams)
+ * race.  Outputs and semantics equal cortex_pack_plan's. */
+int64_t cortex_pack_noalloc_max_workspace_bytes(void);
+int cortex_pack_plan_noalloc(const int64_t* batch_indices, int64_t s_bidx, int64_t E, int64_t B, int64_t* offsets,
+                             int64_t* order, int64_t* dst_rows, int64_t* rank, int32_t* err_flag,
+                             hipStream_t stream);
+
 /* ---- a1 (+a2): fused spike tokenizer --------------------------------------
  * Replaces fused_tokenizer (cortex/kernels/tokenizer.py:177-249) and the eager
  * embedding sum of SpikeTokenizer.forward (cortex/models/tokenizer.py:90-93):
