@@ -608,6 +608,68 @@ def w8a8_forward(model, scales, dev, inputs, reference: torch.Tensor, reps: int 
                     "act_scale); not the reference's arithmetic, opt-in"}
 
 
+def _time_captured(model, dev, inputs, reps: int = 50) -> tuple[float, torch.Tensor]:
+    """Seconds per B = 32 x 512 forward replayed from a HIP graph, and its output."""
+    from cortex.runtime import CapturedForward
+
+    cap = CapturedForward(model, batch_size=B_MAIN, n_events=B_MAIN * PER_MAIN)
+    out = cap(*inputs).clone()
+    for _ in range(5):
+        cap(*inputs)
+    torch.cuda.synchronize(dev)
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        cap(*inputs)
+    torch.cuda.synchronize(dev)
+    sec = (time.perf_counter() - t0) / reps
+    del cap
+    return sec, out
+
+
+def weights_and_modes(model, dev, inputs, reference: torch.Tensor) -> dict:
+    """Resident weight bytes of the default forward (INT8 weights + their bf16 execution images)
+    and of the widen mode (INT8 weights streamed and widened on chip, no images), with the widen
+    mode's time; and the float32-compute forward (the reference's own arithmetic: fp32
+    activations, INT8 weights dequantised) on the same weights and events."""
+    from cortex.models import CortexModel, _layers
+    from cortex.models.config import CORTEX_S, CortexConfig
+
+    wb = _layers.resident_weight_bytes(model)
+    prev = _layers.INT8_WEIGHTS
+    _layers.INT8_WEIGHTS = "widen"
+    try:
+        sec_w, out_w = _time_captured(model, dev, inputs)
+    finally:
+        _layers.INT8_WEIGHTS = prev
+    res = {"resident_weight_bytes": wb["total"], "int8_weight_bytes": wb["int8_weights"],
+           "bf16_image_bytes": wb["bf16_images"],
+           "widen": {"resident_weight_bytes": wb["parameters_and_buffers"], "ms_per_forward": round(sec_w * 1e3, 4),
+                     "samples_per_s": round(B_MAIN / sec_w, 1),
+                     "max_abs_diff_vs_default": float((out_w - reference).abs().max()),
+                     "note": "CORTEX_INT8_WEIGHTS=widen: every kernel reads the int8 weights and widens them "
+                             "on chip; the default keeps bf16 images because they were measured faster"},
+           "reference_int8_bytes_note": "the reference's INT8 model holds 27.8 MB (benchmarks/quantization/"
+                                        "results.md:15-18)"}
+    torch.manual_seed(0)
+    f32 = CortexModel(CortexConfig(**{**CORTEX_S.model_dump(), "dtype": "float32"})).to(dev).eval()
+    f32.load_state_dict({k: v for k, v in model.state_dict().items()}, strict=False)
+    from cortex.quantization.calibrate import QuantizedLinear
+
+    for name, mod in list(model.named_modules()):  # the same INT8 linears in the fp32-compute model
+        if isinstance(mod, QuantizedLinear):
+            parent_name, _, leaf = name.rpartition(".")
+            parent = f32.get_submodule(parent_name) if parent_name else f32
+            setattr(parent, leaf, mod)
+    sec_f, out_f = _time_captured(f32, dev, inputs, reps=20)
+    res["fp32_compute"] = {"ms_per_forward": round(sec_f * 1e3, 4), "samples_per_s": round(B_MAIN / sec_f, 1),
+                           "max_abs_diff_vs_default": float((out_f - reference).abs().max()),
+                           "note": "fp32 activations and fp32 MFMA with the INT8 weights dequantised in the "
+                                   "kernel: the reference QuantizedLinear arithmetic (1e-5 parity bar)"}
+    del f32
+    torch.cuda.empty_cache()
+    return res
+
+
 def cpu_baseline(model, budget_s: float = 12.0, b1_budget_s: float = 18.0):
     """The CPU oracle (fp32 activations, INT8 weights dequantised as the reference's QuantizedLinear)
     on the host cores, with the reference's protocol (profile_inference.py: 5 warmup + up to 30 timed
@@ -757,6 +819,11 @@ def main() -> int:
         log(f"bench: API configurations {extra['api_configs']}")
         extra["w8a8"] = w8a8_forward(model, scales, dev, inputs, cap(*inputs).clone())
         log(f"bench: w8a8 {extra['w8a8']}")
+        try:
+            extra["weights"] = weights_and_modes(model, dev, inputs, cap(*inputs).clone())
+        except Exception as e:  # a secondary line: never lose the headline for it
+            extra["weights"] = {"error": f"{type(e).__name__}: {e}"}
+        log(f"bench: weights and modes {extra['weights']}")
     cpu = None
     if not (args.no_cpu_baseline or args.quick):
         log("bench: CPU baseline")
@@ -771,8 +838,10 @@ def main() -> int:
         "config": {"workload": "cortex_s_int8_forward_b32x512", "model": "CORTEX_S (random init, seed 0, INT8 "
                    "per-channel)", "batch": B, "events_per_sample": per,
                    "compute": "bf16 MFMA, fp32 accumulate, fp32 residual", "graph": "hip graph replay"},
-        "forward_tflops": round(fwd_flops / (ms_step * 1e-3) / 1e12, 2),
-        "forward_mfma_frac": round(fwd_flops / (ms_step * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4),
+        # algorithmic rate: the reference forward's FLOPs (including the batch-invariant latent
+        # q projection and the behaviour kv projection, which this forward folds away) per step
+        "forward_tflops_algorithmic": round(fwd_flops / (ms_step * 1e-3) / 1e12, 2),
+        "forward_mfma_frac_algorithmic": round(fwd_flops / (ms_step * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4),
         "eager_ms_per_forward": round(eager_ms, 4),
         "roofline": roof, "kernels": kern, "cpu_baseline": cpu, **extra,
     }

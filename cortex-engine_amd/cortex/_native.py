@@ -76,11 +76,11 @@ _SIGNATURES = {
          _i64, _ptr, _ptr, _ptr, _i64, _ptr, _i64, _i64, _i64, _i64, _i64, _f32, _ptr, _i64, _i64, _i64, _ptr],
     ),
     "cortex_qkv_attention": (
-        _int, [_i64, _i64, _i64, _i64, _ptr, _i64, _ptr, _i64, _ptr, _ptr, _f32, _ptr, _i64, _ptr]),
+        _int,
+        [_i64, _i64, _i64, _i64, _ptr, _i64, _int, _ptr, _i64, _ptr, _ptr, _f32, _ptr, _i64, _ptr]),
     "cortex_linear_residual_ln": (
         _int,
-        [_i64, _i64, _i64, _ptr, _i64, _ptr, _i64, _ptr, _ptr, _ptr, _i64, _i64, _ptr, _i64, _ptr, _ptr, _f32, _ptr,
-         _i64, _ptr]),
+        [_i64, _i64, _i64, _ptr, _i64, _int, _ptr, _i64, _ptr, _ptr, _ptr, _i64, _i64, _ptr, _i64, _ptr, _ptr, _f32, _ptr, _i64, _ptr]),
     "cortex_head_prep": (_int, [_ptr, _i64, _i64, _i64, _i64, _ptr, _ptr, _i64, _ptr, _ptr, _ptr, _ptr]),
     "cortex_behavior_head_workspace_bytes": (_i64, [_i64, _i64]),
     "cortex_behavior_head": (
@@ -92,8 +92,9 @@ _SIGNATURES = {
         [_ptr, _i64, _i64, _i64, _i64, _ptr, _ptr, _f32, _i64, _int, _ptr, _i64, _ptr, _ptr, _ptr, _ptr, _ptr]),
     "cortex_gather_event_pages": (_int, [_ptr, _i64, _i64, _ptr, _i64, _ptr, _i64, _i64, _ptr, _ptr]),
     "cortex_scatter_event_pages": (_int, [_ptr, _i64, _i64, _ptr, _i64, _ptr, _i64, _i64, _ptr, _ptr]),
-    "cortex_linear_residual_ln_i8": (_int, [_i64, _i64, _i64, _ptr, _i64, _ptr, _i64, _ptr, _ptr, _ptr, _i64, _i64,
-                                            _ptr, _i64, _ptr, _ptr, _f32, _ptr, _i64, _f32, _ptr]),
+    "cortex_linear_residual_ln_i8": (
+        _int,
+        [_i64, _i64, _i64, _ptr, _i64, _int, _ptr, _i64, _ptr, _ptr, _ptr, _i64, _i64, _ptr, _i64, _ptr, _ptr, _f32, _ptr, _i64, _f32, _ptr]),
     "cortex_linear_w8a8": (_int, [_i64, _i64, _i64, _ptr, _i64, _f32, _ptr, _i64, _ptr, _ptr, _int, _ptr, _i64, _i64,
                                   _ptr, _int, _f32, _i64, _ptr]),
     "cortex_qkv_attention_w8a8": (_int, [_i64, _i64, _i64, _i64, _ptr, _i64, _f32, _ptr, _i64, _ptr, _ptr, _f32, _ptr,

@@ -242,14 +242,15 @@ def ln_rows(x: torch.Tensor, ln1, ln2=None, out_bf16: bool = True, out_f32: bool
 def qkv_attention(xn: torch.Tensor, weight: torch.Tensor, weight_scale, bias, batch: int, length: int,
                   heads: int, scale: float | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
     """Self-attention with its QKV projection fused (``cortex_qkv_attention``): ``xn`` (B*L, D)
-    bf16 rows, ``weight`` the (3D, D) bf16 image; returns the merged-head (B*L, D) bf16 output."""
+    bf16 rows, ``weight`` the (3D, D) bf16 image or the int8 weight itself (widened in the
+    kernel); returns the merged-head (B*L, D) bf16 output."""
     dev = nat.require_gpu(xn, weight, weight_scale, bias, out, what="qkv_attention")
     M, D = xn.shape
     if out is None:
         out = torch.empty((M, D), dtype=torch.bfloat16, device=dev)
     s = float(scale) if scale is not None else (D // heads) ** -0.5
-    nat.call("cortex_qkv_attention", batch, length, D, heads, nat.ptr(xn), xn.stride(0), nat.ptr(weight),
-             weight.stride(0), nat.ptr(weight_scale), nat.ptr(bias), s, nat.ptr(out), out.stride(0),
+    nat.call("cortex_qkv_attention", batch, length, D, heads, nat.ptr(xn), xn.stride(0), nat.code(weight.dtype),
+             nat.ptr(weight), weight.stride(0), nat.ptr(weight_scale), nat.ptr(bias), s, nat.ptr(out), out.stride(0),
              nat.stream_of(dev))
     return out
 
@@ -258,9 +259,10 @@ def linear_residual_ln(x: torch.Tensor, weight: torch.Tensor, weight_scale=None,
                        residual: torch.Tensor, ln, res_rows: int = 0, out: torch.Tensor | None = None,
                        xq_scale: float | None = None):
     """``out = residual + x @ (weight * scale)^T + bias`` (fp32) and ``LN(out)`` (bf16) in one
-    kernel; ``x`` (M, K) and ``weight`` (N, K) bf16, N in {256, 512}.  ``out`` may be
-    ``residual`` itself.  Returns ``(out, xn)``.  With ``xq_scale`` (the W8A8 mode) ``xn`` is
-    int8: ``clamp(rint(LN(out) * (1 / xq_scale)), -127, 127)``."""
+    kernel; ``x`` (M, K) bf16, ``weight`` (N, K) the bf16 image or the int8 weight itself
+    (widened in the kernel), N in {256, 512}.  ``out`` may be ``residual`` itself.  Returns
+    ``(out, xn)``.  With ``xq_scale`` (the W8A8 mode) ``xn`` is int8:
+    ``clamp(rint(LN(out) * (1 / xq_scale)), -127, 127)``."""
     dev = nat.require_gpu(x, weight, weight_scale, bias, residual, out, what="linear_residual_ln")
     M, K = x.shape
     N = weight.shape[0]
@@ -269,13 +271,14 @@ def linear_residual_ln(x: torch.Tensor, weight: torch.Tensor, weight_scale=None,
     g, b, eps = ln
     if xq_scale is not None:
         xq = torch.empty((M, N), dtype=torch.int8, device=dev)
-        nat.call("cortex_linear_residual_ln_i8", M, N, K, nat.ptr(x), x.stride(0), nat.ptr(weight), weight.stride(0),
+        nat.call("cortex_linear_residual_ln_i8", M, N, K, nat.ptr(x), x.stride(0), nat.code(weight.dtype),
+                 nat.ptr(weight), weight.stride(0),
                  nat.ptr(weight_scale), nat.ptr(bias), nat.ptr(residual), residual.stride(0), int(res_rows),
                  nat.ptr(out), out.stride(0), nat.ptr(g), nat.ptr(b), float(eps), nat.ptr(xq), xq.stride(0),
                  float(xq_scale), nat.stream_of(dev))
         return out, xq
     xn = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
-    splits = splitk_splits(M, N, K, dev)
+    splits = splitk_splits(M, N, K, dev) if weight.dtype == torch.bfloat16 else 0
     if splits:  # few rows: K split across workgroups, slabs summed in order, then the LayerNorm
         ws_t = torch.empty(nat.load().cortex_splitk_workspace_bytes(M, N, splits), dtype=torch.uint8, device=dev)
         nat.call("cortex_linear_residual_ln_splitk", M, N, K, nat.ptr(x), x.stride(0), nat.ptr(weight),
@@ -283,7 +286,8 @@ def linear_residual_ln(x: torch.Tensor, weight: torch.Tensor, weight_scale=None,
                  int(res_rows), nat.ptr(out), out.stride(0), nat.ptr(g), nat.ptr(b), float(eps), nat.ptr(xn),
                  xn.stride(0), splits, nat.ptr(ws_t), ws_t.numel(), nat.stream_of(dev))
         return out, xn
-    nat.call("cortex_linear_residual_ln", M, N, K, nat.ptr(x), x.stride(0), nat.ptr(weight), weight.stride(0),
+    nat.call("cortex_linear_residual_ln", M, N, K, nat.ptr(x), x.stride(0), nat.code(weight.dtype), nat.ptr(weight),
+             weight.stride(0),
              nat.ptr(weight_scale), nat.ptr(bias), nat.ptr(residual), residual.stride(0), int(res_rows),
              nat.ptr(out), out.stride(0), nat.ptr(g), nat.ptr(b), float(eps), nat.ptr(xn), xn.stride(0),
              nat.stream_of(dev))

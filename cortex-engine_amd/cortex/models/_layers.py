@@ -8,10 +8,13 @@ bf16 compute (the default):
     version changes).  For a QuantizedLinear the image holds the int8 values
     themselves -- every int8 value is exactly a bf16 value -- and the per-channel
     scale is applied to the fp32 accumulator in the epilogue, so results are
-    identical to widening the int8 weight inside the kernel (set
-    ``CORTEX_INT8_WEIGHTS=widen`` to stream the int8 weight instead).  For a float
-    nn.Linear the image is the weight rounded to bf16, as ``F.linear`` on bf16
-    inputs would use it.
+    identical to widening the int8 weight inside the kernel.  With
+    ``CORTEX_INT8_WEIGHTS=widen`` no image is kept: every kernel (the GEMMs, the fused
+    QKV projection + attention, the residual linear + LayerNorm) streams the int8
+    weight and widens it on chip, bit-identical results with a third of the resident
+    weight bytes, at some cost in time (the images are the measured-faster default).
+    For a float nn.Linear the image is the weight rounded to bf16, as ``F.linear`` on
+    bf16 inputs would use it.
 fp32 compute: int8 or fp32 weights, fp32 operands, fused norm prologue.
 """
 
@@ -47,6 +50,38 @@ def exec_weights(lin: nn.Module, compute: torch.dtype) -> dict:
         cached = (key, ops.convert(src, torch.bfloat16))
         lin.__dict__["_cortex_exec"] = cached
     return {"weight": cached[1], "weight_scale": lin.weight_scale if quant else None, "bias": lin.bias}
+
+
+def fused_weight(lin: nn.Module) -> tuple:
+    """``(weight, weight_scale, bias)`` for the fused bf16 kernels (QKV + attention, residual
+    linear + LayerNorm): the bf16 image, or with ``CORTEX_INT8_WEIGHTS=widen`` the int8 weight
+    itself, which those kernels widen on chip."""
+    if hasattr(lin, "weight_int8") and INT8_WEIGHTS == "widen":
+        return lin.weight_int8, lin.weight_scale, lin.bias
+    w = exec_weights(lin, torch.bfloat16)
+    return w["weight"], w["weight_scale"], w["bias"]
+
+
+def bf16_weight(lin: nn.Module) -> tuple:
+    """``(bf16 weight, weight_scale)`` for one-time preparation kernels that read bf16 rows:
+    the cached image, or in the widen mode a temporary widened copy (not kept)."""
+    if hasattr(lin, "weight_int8") and INT8_WEIGHTS == "widen":
+        return ops.convert(lin.weight_int8, torch.bfloat16), lin.weight_scale
+    w = exec_weights(lin, torch.bfloat16)
+    return w["weight"], w["weight_scale"]
+
+
+def resident_weight_bytes(model: nn.Module) -> dict:
+    """Device bytes the model holds for weights: its parameters and buffers (int8 weights and
+    scales, embeddings, norms, latents) and the bf16 execution images cached on its linears."""
+    own = sum(t.numel() * t.element_size() for t in list(model.parameters()) + list(model.buffers()))
+    images = 0
+    for m in model.modules():
+        c = m.__dict__.get("_cortex_exec")
+        if c is not None:
+            images += c[1].numel() * c[1].element_size()
+    int8 = sum(b.numel() for n, b in model.named_buffers() if n.endswith("weight_int8"))
+    return {"total": own + images, "parameters_and_buffers": own, "int8_weights": int8, "bf16_images": images}
 
 
 def _state_key(tensors) -> tuple:
@@ -129,16 +164,16 @@ def residual_ln_ok(lin: nn.Module, norm: nn.LayerNorm, consumer: nn.Module, x: t
         return False
     if lin.bias is not None and (lin.bias.dtype != torch.float32 or lin.bias.data_ptr() % 16):
         return False
-    return ln_rows_ok(x, norm) and INT8_WEIGHTS == "image"
+    return ln_rows_ok(x, norm)
 
 
 def linear_residual_ln(lin: nn.Module, a: torch.Tensor, residual: torch.Tensor, norm: nn.LayerNorm, *,
                        res_rows: int = 0, out: torch.Tensor | None = None, xq_scale: float | None = None):
     """``x = residual + lin(a)`` (fp32) and ``norm(x)`` (bf16; int8 at ``xq_scale`` when given)
     in one launch (see ``residual_ln_ok``).  Returns ``(x, norm(x))``."""
-    w = exec_weights(lin, torch.bfloat16)
-    return ops.linear_residual_ln(a, w["weight"], w["weight_scale"], w["bias"], residual=residual,
-                                  ln=ln_params(norm), res_rows=res_rows, out=out, xq_scale=xq_scale)
+    w, scale, bias = fused_weight(lin)
+    return ops.linear_residual_ln(a, w, scale, bias, residual=residual, ln=ln_params(norm), res_rows=res_rows,
+                                  out=out, xq_scale=xq_scale)
 
 
 def apply_linear(lin: nn.Module, x: torch.Tensor, *, norm: nn.LayerNorm | None = None, stats=None,

@@ -27,8 +27,9 @@ from torch import nn
 
 from cortex.kernels import ops
 from cortex.kernels.pack import pack_events as _device_pack_events
-from cortex.models._layers import (apply_linear, batch_invariant, exec_weights, fused_tokens_ok, linear_residual_ln,
-                                   linear_weights, ln_params, ln_rows_ok, normalize_bf16, residual_ln_ok)
+from cortex.models._layers import (apply_linear, batch_invariant, bf16_weight, exec_weights, fused_tokens_ok,
+                                   linear_residual_ln, linear_weights, ln_params, ln_rows_ok, normalize_bf16,
+                                   residual_ln_ok)
 from cortex.models.config import CortexConfig
 from cortex.models.perceiver import PerceiverEncoder
 from cortex.models.tokenizer import SpikeTokenizer
@@ -97,9 +98,8 @@ class BehaviorDecoder(nn.Module):
 
         def build():
             q = apply_linear(self.q_proj, self.query, out_dtype=compute, compute=compute)
-            kv, ow = exec_weights(self.kv_proj, compute), exec_weights(self.out_proj, compute)
-            return ops.head_prep(q, kv["weight"], kv["weight_scale"], ow["weight"], ow["weight_scale"],
-                                 self.num_heads)
+            (kv, kv_s), (ow, ow_s) = bf16_weight(self.kv_proj), bf16_weight(self.out_proj)
+            return ops.head_prep(q, kv, kv_s, ow, ow_s, self.num_heads)
 
         return batch_invariant(self, "head_folded", [self.query], [self.q_proj, self.kv_proj, self.out_proj], build)
 

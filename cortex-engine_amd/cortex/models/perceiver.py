@@ -15,7 +15,7 @@ import torch
 from torch import nn
 
 from cortex.kernels import ops
-from cortex.models._layers import (INT8_WEIGHTS, apply_linear, batch_invariant, exec_weights, linear_residual_ln,
+from cortex.models._layers import (apply_linear, batch_invariant, exec_weights, fused_weight, linear_residual_ln,
                                    ln_rows_ok, normalize_bf16, residual_ln_ok)
 from cortex.models.config import CortexConfig
 
@@ -99,8 +99,7 @@ class SelfAttentionBlock(nn.Module):
             # qkv projection + attention per (head, sample) on chip: qkv never reaches HBM
             if xn is None:
                 xn = normalize_bf16(x, self.norm_attn)
-            w = exec_weights(self.qkv_proj, compute)
-            o_buf = ops.qkv_attention(xn, w["weight"], w["weight_scale"], w["bias"], batch, length, H)
+            o_buf = ops.qkv_attention(xn, *fused_weight(self.qkv_proj), batch, length, H)
         else:
             if xn is not None:
                 qkv = ops.norm_linear(xn, **exec_weights(self.qkv_proj, compute), out_dtype=compute,
@@ -180,7 +179,7 @@ class SelfAttentionBlock(nn.Module):
         D = x.shape[1]
         return (self.config.compute_dtype == torch.bfloat16 and not lin._forward_pre_hooks
                 and not self.norm_attn._forward_pre_hooks and D == 64 * self.num_heads and D % 64 == 0
-                and 1 <= length <= 256 and INT8_WEIGHTS == "image"
+                and 1 <= length <= 256
                 and (lin.bias is None or (lin.bias.dtype == torch.float32 and lin.bias.data_ptr() % 16 == 0))
                 and ln_rows_ok(x, self.norm_attn))
 

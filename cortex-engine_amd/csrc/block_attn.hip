@@ -70,11 +70,17 @@ struct QkvAttnArgs {
   float out_inv_scale;  // Q8OUT
 };
 
-template <class TIN = bf16, bool Q8OUT = false>
+// TW = int8_t with bf16 xn rows: the QuantizedLinear int8 qkv weight itself, loaded 8 bytes
+// per lane into registers one step ahead and widened exactly to bf16 into the LDS ring
+// before the step's barrier (lane (row r, chunk c): logical chunk c of LDS row r).
+template <class TIN = bf16, bool Q8OUT = false, class TW = TIN>
 __global__ __launch_bounds__(BA_THREADS) void qkv_attention_kernel(QkvAttnArgs a) {
   using OP = Operand<TIN>;
   typedef typename OP::frag frag;
   constexpr int EPC = OP::EPC, BK = 8 * EPC;  // K elements per 16-byte chunk and per 128-byte LDS row
+  constexpr bool WI8 = sizeof(TW) == 1 && sizeof(TIN) == 2;
+  constexpr int WL = BA_N / (8 * BA_WAVES);  // 8-byte int8 weight loads per lane and step (int8 weights)
+  static_assert(BA_N % (8 * BA_WAVES) == 0, "int8 weight staging shape");
   __shared__ __attribute__((aligned(1024))) unsigned char smem[BA_LDS];
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int fr = lane & 15, g4 = lane >> 4;
@@ -99,26 +105,44 @@ __global__ __launch_bounds__(BA_THREADS) void qkv_attention_kernel(QkvAttnArgs a
     const int r = (wid * BA_AB + i) * 8 + (lane >> 3);
     a_src[i] = reinterpret_cast<const TIN*>(a.xn) + (row0 + min(r, L - 1)) * a.ld_x + ((lane & 7) ^ ba_swz(r)) * EPC;
   }
-  const TIN* w_src[BA_WB];
+  constexpr int NW = WI8 ? WL : BA_WB;
+  const TW* w_src[NW];
 #pragma unroll
-  for (int i = 0; i < BA_WB; ++i) {
-    const int r = (wid * BA_WB + i) * 8 + (lane >> 3);  // LDS row: q 0..63, k 64..127, v 128..191
+  for (int i = 0; i < NW; ++i) {
+    // LDS row: q 0..63, k 64..127, v 128..191
+    const int r = WI8 ? (wid * WL + i) * 8 + (lane >> 3) : (wid * BA_WB + i) * 8 + (lane >> 3);
     const int64_t grow = (int64_t)(r >> 6) * D + h * 64 + (r & 63);
-    w_src[i] = reinterpret_cast<const TIN*>(a.w) + grow * a.ld_w + ((lane & 7) ^ ba_swz(r)) * EPC;
+    w_src[i] = reinterpret_cast<const TW*>(a.w) + grow * a.ld_w + (WI8 ? (lane & 7) * 8 : ((lane & 7) ^ ba_swz(r)) * EPC);
   }
   auto a_stage = [&](int s) { return smem + s * BA_A_STAGE; };
   auto w_stage = [&](int s) { return smem + BA_S * BA_A_STAGE + s * BA_W_STAGE; };
   const int nk = D / BK;
+  uint2 wreg[WI8 ? WL : 1];  // int8 weight rows of the last issued step
   auto issue = [&](int kt) {
     const int s = kt % BA_S, k0 = kt * BK;
+    if constexpr (WI8) {
+#pragma unroll
+      for (int i = 0; i < WL; ++i) wreg[i] = *reinterpret_cast<const uint2*>(w_src[i] + k0);
+    }
 #pragma unroll
     for (int i = 0; i < BA_AB; ++i)
       __builtin_amdgcn_global_load_lds(static_cast<const void*>(a_src[i] + k0),
                                        static_cast<void*>(a_stage(s) + (wid * BA_AB + i) * 1024), 16, 0, 0);
+    if constexpr (!WI8) {
 #pragma unroll
-    for (int i = 0; i < BA_WB; ++i)
-      __builtin_amdgcn_global_load_lds(static_cast<const void*>(w_src[i] + k0),
-                                       static_cast<void*>(w_stage(s) + (wid * BA_WB + i) * 1024), 16, 0, 0);
+      for (int i = 0; i < BA_WB; ++i)
+        __builtin_amdgcn_global_load_lds(static_cast<const void*>(w_src[i] + k0),
+                                         static_cast<void*>(w_stage(s) + (wid * BA_WB + i) * 1024), 16, 0, 0);
+    }
+  };
+  auto commit_w = [&](int s) {  // widen the registers into W stage s
+    if constexpr (WI8) {
+#pragma unroll
+      for (int i = 0; i < WL; ++i) {
+        const int r = (wid * WL + i) * 8 + (lane >> 3), c = lane & 7;
+        *reinterpret_cast<bf16x8*>(w_stage(s) + r * 128 + ((c ^ ba_swz(r)) << 4)) = widen_i8x8(wreg[i]);
+      }
+    }
   };
   typename OP::accum acc[BA_TM][BA_TN];
 #pragma unroll
@@ -159,14 +183,22 @@ __global__ __launch_bounds__(BA_THREADS) void qkv_attention_kernel(QkvAttnArgs a
   // Both stages in flight; a stage is refilled as soon as every wave holds its last
   // fragments in registers.  Fragments are double-buffered in registers, so the LDS
   // reads of the next K half overlap the MFMAs.
-#pragma unroll
-  for (int p = 0; p < BA_S; ++p)
-    if (p < nk) issue(p);
   frag af0[BA_TM], wf0[BA_TN], af1[BA_TM], wf1[BA_TN];
-  if (nk > 1)
-    ba_wait_vm<BA_PER>();
-  else
+  if constexpr (WI8) {
+    issue(0);
     ba_wait_vm<0>();
+    commit_w(0);
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): widened rows in LDS before the barrier
+    if (1 < nk) issue(1);
+  } else {
+#pragma unroll
+    for (int p = 0; p < BA_S; ++p)
+      if (p < nk) issue(p);
+    if (nk > 1)
+      ba_wait_vm<BA_PER>();
+    else
+      ba_wait_vm<0>();
+  }
   __builtin_amdgcn_s_barrier();
   read_frags(0, 0, af0, wf0);
   for (int kt = 0; kt < nk; ++kt) {
@@ -174,8 +206,9 @@ __global__ __launch_bounds__(BA_THREADS) void qkv_attention_kernel(QkvAttnArgs a
     read_frags(st, 1, af1, wf1);
     mma(af0, wf0);
     if (kt + 1 < nk) {
-      __builtin_amdgcn_s_waitcnt(0xC07F);  // this wave's reads of stage st are in registers
       ba_wait_vm<0>();                     // step kt+1 landed (two stages: nothing newer in flight)
+      commit_w((kt + 1) % BA_S);           // (int8 weights: widened into its W stage)
+      __builtin_amdgcn_s_waitcnt(0xC07F);  // this wave's reads of stage st (and W stores) are done
       __builtin_amdgcn_s_barrier();        // all waves done with stage st; step kt+1 visible
       if (kt + BA_S < nk) issue(kt + BA_S);
       read_frags((kt + 1) % BA_S, 0, af0, wf0);
@@ -384,21 +417,28 @@ bool ba_al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 using namespace cortex;
 
 extern "C" int cortex_qkv_attention(int64_t B, int64_t L, int64_t D, int64_t H, const void* xn, int64_t ld_x,
-                                    const void* w, int64_t ld_w, const float* w_scale, const float* bias,
+                                    int w_dtype, const void* w, int64_t ld_w, const float* w_scale, const float* bias,
                                     float scale, void* out, int64_t ld_o, hipStream_t stream) {
   CORTEX_CHECK_ARG(B >= 0 && L >= 1 && L <= BA_L, "cortex_qkv_attention: need 1 <= L <= %d", BA_L);
   CORTEX_CHECK_ARG(H >= 1 && D == 64 * H && D % BA_BK == 0, "cortex_qkv_attention: need D = 64 * H");
+  CORTEX_CHECK_ARG(w_dtype == DT_BF16 || w_dtype == DT_I8, "cortex_qkv_attention: weight must be bf16 or int8");
   if (B == 0) return OK;
+  const bool wi8 = w_dtype == DT_I8;
   CORTEX_CHECK_ARG(xn && w && out, "cortex_qkv_attention: null pointer");
   CORTEX_CHECK_ARG(ld_x >= D && ld_w >= D && ld_o >= D, "cortex_qkv_attention: row strides too small");
-  CORTEX_CHECK_ARG(ba_al16(xn) && ba_al16(w) && ld_x % 8 == 0 && ld_w % 8 == 0 && ((uintptr_t)out & 7) == 0 &&
-                       ld_o % 4 == 0 && (!w_scale || ba_al16(w_scale)) && (!bias || ba_al16(bias)),
+  CORTEX_CHECK_ARG(ba_al16(xn) && ba_al16(w) && ld_x % 8 == 0 && ld_w % (wi8 ? 16 : 8) == 0 &&
+                       ((uintptr_t)out & 7) == 0 && ld_o % 4 == 0 && (!w_scale || ba_al16(w_scale)) &&
+                       (!bias || ba_al16(bias)),
                    "cortex_qkv_attention: operands must be 16-byte aligned rows");
   CORTEX_CHECK_ARG(scale > 0.0f && scale < INFINITY, "cortex_qkv_attention: scale must be positive");
   CORTEX_CHECK_ARG(B * H <= 0x7fffffffLL && B <= 65535 && H <= 65535, "cortex_qkv_attention: grid too large");
   QkvAttnArgs a{B, L, D, H, xn, ld_x, w, ld_w, w_scale, bias, scale * 1.4426950408889634f, out, ld_o, 1.0f, 0.0f};
-  hipLaunchKernelGGL((qkv_attention_kernel<bf16, false>), dim3((unsigned)H, (unsigned)B), dim3(BA_THREADS), 0, stream,
-                     a);
+  if (wi8)
+    hipLaunchKernelGGL((qkv_attention_kernel<bf16, false, int8_t>), dim3((unsigned)H, (unsigned)B), dim3(BA_THREADS),
+                       0, stream, a);
+  else
+    hipLaunchKernelGGL((qkv_attention_kernel<bf16, false>), dim3((unsigned)H, (unsigned)B), dim3(BA_THREADS), 0,
+                       stream, a);
   CORTEX_CHECK_LAUNCH("qkv_attention_kernel");
   return OK;
 }

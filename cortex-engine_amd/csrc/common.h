@@ -90,6 +90,16 @@ struct Operand<int8_t> {
   }
 };
 
+// Exact int8 -> bf16 widening of 8 values (every int8 value is a bf16 value); the
+// compiler emits one sign-extending byte convert per value and one pack per pair.
+__device__ __forceinline__ bf16x8 widen_i8x8(uint2 raw) {
+  const int8_t* p = reinterpret_cast<const int8_t*>(&raw);
+  bf16x8 v;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) v[j] = (bf16)(float)(int)p[j];
+  return v;
+}
+
 // Cross-lane reductions inside one wavefront.
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll

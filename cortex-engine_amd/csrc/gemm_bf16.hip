@@ -75,7 +75,17 @@ __device__ __forceinline__ int swz_w(int r) { return ((r >> 1) & 1) | ((r >> 2) 
 // tiles 2p and 2p+1 give lane group g4 the 8 consecutive columns 32 p + 8 g4 .. +7.
 __device__ __forceinline__ int wrow_of(int p, int jj, int rho) { return 32 * p + 8 * (rho >> 2) + 4 * jj + (rho & 3); }
 
-template <class TL, int ACT, bool RES, class TOUT, class TIN = bf16>
+// int8 weight rows streamed into the bf16 LDS ring (TW = int8_t with bf16 activations):
+// lane (row r, chunk c) loads W[r, k0 + 16 c .. +15] (16 bytes) into registers one step
+// ahead, and before the step's barrier widens them exactly to bf16 (every int8 value is a
+// bf16 value) and stores them as the logical 16-byte chunks 2c, 2c+1 of LDS row r.  Each
+// weight element is widened once per workgroup, and half the weight bytes cross L2.
+__device__ __forceinline__ void widen_store_i8x16(unsigned char* row, int sw, int c, uint4 raw) {
+  *reinterpret_cast<bf16x8*>(row + (((2 * c) ^ sw) << 4)) = widen_i8x8(make_uint2(raw.x, raw.y));
+  *reinterpret_cast<bf16x8*>(row + (((2 * c + 1) ^ sw) << 4)) = widen_i8x8(make_uint2(raw.z, raw.w));
+}
+
+template <class TL, int ACT, bool RES, class TOUT, class TIN = bf16, class TW = TIN>
 __global__ __launch_bounds__(TL::THREADS) void gemm_bf16_kernel(GemmArgs g) {
   constexpr int BM = TL::BM, BN = TL::BN, TM = TL::TM, TN = TL::TN, S = TL::STAGES;
   constexpr int AB = TL::A_BLOCKS, WB = TL::W_BLOCKS, PER = TL::PER;
@@ -85,6 +95,13 @@ __global__ __launch_bounds__(TL::THREADS) void gemm_bf16_kernel(GemmArgs g) {
   using OP = Operand<TIN>;
   typedef typename OP::frag frag;
   constexpr int EPC = OP::EPC, BK = 8 * EPC;  // K elements per 16-byte chunk and per 128-byte row
+  // int8 weight rows widened through registers (see widen_store_i8x16): WL loads of 16 rows
+  // per wavefront and step, each in flight for one step (two-stage rings only)
+  constexpr bool WI8 = sizeof(TW) == 1 && sizeof(TIN) == 2;
+  constexpr int WL = WI8 ? BN / (16 * TL::WAVES) : 1;
+  static_assert(!WI8 || (BN % (16 * TL::WAVES) == 0 && S == 2), "int8 weight staging shape");
+  constexpr int WOPS = WI8 ? WL : WB;  // vector-memory operations per step for W
+  constexpr int STEP_OPS = AB + WOPS;
   __shared__ __attribute__((aligned(1024))) unsigned char smem[TL::LDS];
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -98,7 +115,7 @@ __global__ __launch_bounds__(TL::THREADS) void gemm_bf16_kernel(GemmArgs g) {
   // K split across workgroups (split_k_partials): slice z of K into output slab z
   const int kz = blockIdx.z;
   const TIN* __restrict__ A = reinterpret_cast<const TIN*>(g.x) + (int64_t)kz * K;
-  const TIN* __restrict__ W = reinterpret_cast<const TIN*>(g.w) + (int64_t)kz * K;
+  const TW* __restrict__ W = reinterpret_cast<const TW*>(g.w) + (int64_t)kz * K;
 
   // Global source of each of this lane's transfers (K offset added per step).  Lane i
   // of a transfer writes LDS bytes [16 i, 16 i + 16) of its 1 KiB block: row i / 8,
@@ -109,26 +126,53 @@ __global__ __launch_bounds__(TL::THREADS) void gemm_bf16_kernel(GemmArgs g) {
     const int r = (wid * AB + i) * 8 + (lane >> 3);
     a_src[i] = A + (int64_t)min(m0 + r, M - 1) * g.ld_x + ((lane & 7) ^ swz_a(r)) * EPC;
   }
-  const TIN* w_src[WB];
+  const TW* w_src[WI8 ? WL : WB];
+  int w_row[WI8 ? WL : 1];
+  if constexpr (WI8) {
 #pragma unroll
-  for (int i = 0; i < WB; ++i) {
-    const int r = (wid * WB + i) * 8 + (lane >> 3);
-    w_src[i] = W + (int64_t)min(n0 + r, N - 1) * g.ld_w + ((lane & 7) ^ (IL ? swz_w(r) : swz_a(r))) * EPC;
+    for (int i = 0; i < WL; ++i) {
+      const int r = (wid * WL + i) * 16 + (lane >> 2);
+      w_row[i] = r;
+      w_src[i] = W + (int64_t)min(n0 + r, N - 1) * g.ld_w + (lane & 3) * 16;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < WB; ++i) {
+      const int r = (wid * WB + i) * 8 + (lane >> 3);
+      w_src[i] = W + (int64_t)min(n0 + r, N - 1) * g.ld_w + ((lane & 7) ^ (IL ? swz_w(r) : swz_a(r))) * EPC;
+    }
   }
   auto a_stage = [&](int s) { return ring + s * TL::A_STAGE; };
   auto w_stage = [&](int s) { return ring + S * TL::A_STAGE + s * TL::W_STAGE; };
   const int nk = K / BK / TL::KS;  // K steps of this group
   const int kbase = kg * nk * BK;
+  uint4 wreg[WI8 ? WL : 1];  // int8 weight rows of the next step, before widening
   auto issue = [&](int kt) {
     const int s = kt % S, k0 = kbase + kt * BK;
+    if constexpr (WI8) {
+#pragma unroll
+      for (int i = 0; i < WL; ++i) wreg[i] = *reinterpret_cast<const uint4*>(w_src[i] + k0);
+    }
 #pragma unroll
     for (int i = 0; i < AB; ++i)
       __builtin_amdgcn_global_load_lds(static_cast<const void*>(a_src[i] + k0),
                                        static_cast<void*>(a_stage(s) + (wid * AB + i) * 1024), 16, 0, 0);
+    if constexpr (!WI8) {
 #pragma unroll
-    for (int i = 0; i < WB; ++i)
-      __builtin_amdgcn_global_load_lds(static_cast<const void*>(w_src[i] + k0),
-                                       static_cast<void*>(w_stage(s) + (wid * WB + i) * 1024), 16, 0, 0);
+      for (int i = 0; i < WB; ++i)
+        __builtin_amdgcn_global_load_lds(static_cast<const void*>(w_src[i] + k0),
+                                         static_cast<void*>(w_stage(s) + (wid * WB + i) * 1024), 16, 0, 0);
+    }
+  };
+  // widen the registers of the last issued step into its W stage
+  auto commit_w = [&](int s) {
+    if constexpr (WI8) {
+#pragma unroll
+      for (int i = 0; i < WL; ++i) {
+        const int r = w_row[i];
+        widen_store_i8x16(w_stage(s) + r * 128, IL ? swz_w(r) : swz_a(r), lane & 3, wreg[i]);
+      }
+    }
   };
 
   typename OP::accum acc[TM][TN];
@@ -192,23 +236,32 @@ __global__ __launch_bounds__(TL::THREADS) void gemm_bf16_kernel(GemmArgs g) {
 
   // Every stage of the ring is in flight at once; a stage is refilled as soon as all
   // wavefronts hold its last fragments in registers.  Fragments are double-buffered
-  // in registers, so the LDS reads of the next K sub-step overlap the MFMAs.
+  // in registers, so the LDS reads of the next K sub-step overlap the MFMAs.  With
+  // int8 weights, step 0's weight registers are widened before step 1 is issued.
+  if constexpr (WI8) {
+    issue(0);
+    wait_vm<0>();
+    commit_w(0);
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the widened rows are in LDS before the barrier
+    if (1 < nk) issue(1);
+  } else {
 #pragma unroll
-  for (int p = 0; p < S; ++p)
-    if (p < nk) issue(p);
+    for (int p = 0; p < S; ++p)
+      if (p < nk) issue(p);
+  }
   // wait until this wave's transfers of step j landed, steps up to `last` being issued
   auto wait_step = [&](int j, int last) {
     const int ahead = min(nk - 1, last) - j;  // steps issued after j
     if constexpr (S >= 3) {
       if (ahead >= 2)
-        wait_vm<2 * PER>();
+        wait_vm<2 * STEP_OPS>();
       else if (ahead == 1)
-        wait_vm<PER>();
+        wait_vm<STEP_OPS>();
       else
         wait_vm<0>();
     } else {
       if (ahead >= 1)
-        wait_vm<PER>();
+        wait_vm<STEP_OPS>();
       else
         wait_vm<0>();
     }
@@ -222,8 +275,13 @@ __global__ __launch_bounds__(TL::THREADS) void gemm_bf16_kernel(GemmArgs g) {
     read_frags(st, 1, af1, wf1);
     mma(af0, wf0);
     if (kt + 1 < nk) {
-      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's reads of stage st are in registers
-      wait_step(kt + 1, kt + S - 1);
+      if constexpr (WI8) {
+        wait_vm<0>();                      // step kt+1: A transfers and weight registers
+        commit_w((kt + 1) % S);
+      } else {
+        wait_step(kt + 1, kt + S - 1);
+      }
+      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's reads of stage st (and W stores) done
       __builtin_amdgcn_s_barrier();        // all waves done with stage st; step kt+1 visible
       if (kt + S < nk) issue(kt + S);      // refill stage st
       read_frags((kt + 1) % S, 0, af0, wf0);
@@ -332,11 +390,11 @@ __global__ __launch_bounds__(TL::THREADS) void gemm_bf16_kernel(GemmArgs g) {
   }
 }
 
-template <class TL, int ACT, bool RES, class TOUT, class TIN = bf16>
+template <class TL, int ACT, bool RES, class TOUT, class TIN = bf16, class TW = TIN>
 int launch(const GemmArgs& g, hipStream_t stream) {
   const int64_t gy = cdiv(g.M, TL::BM), gx = cdiv(g.N, TL::BN);
   if (gy > 65535 || gx * gy > 0x7fffffffLL) return 0;
-  hipLaunchKernelGGL((gemm_bf16_kernel<TL, ACT, RES, TOUT, TIN>), dim3((unsigned)gx, (unsigned)gy),
+  hipLaunchKernelGGL((gemm_bf16_kernel<TL, ACT, RES, TOUT, TIN, TW>), dim3((unsigned)gx, (unsigned)gy),
                      dim3(TL::THREADS), 0, stream, g);
   CORTEX_CHECK_LAUNCH("gemm_bf16_kernel");
   return 1;
@@ -370,8 +428,9 @@ int bf16_tile() {
   return v;
 }
 
-template <int ACT, bool RES, class TOUT>
+template <int ACT, bool RES, class TOUT, class TW = bf16>
 int dispatch(const GemmArgs& g, hipStream_t stream) {
+  constexpr bool W8 = sizeof(TW) == 1;  // int8 weights: two-stage rings without the 192-column tile
   int t = bf16_tile();
   if (t < 0) {
     // 256-row tiles halve the operand traffic per MFMA; take the widest tile that still
@@ -380,45 +439,62 @@ int dispatch(const GemmArgs& g, hipStream_t stream) {
     const int ncu = cu_count();
     if (g.N % 256 == 0 && t256 >= ncu * 15 / 16)
       t = 4;
-    else if (g.N % 192 == 0 && t192 >= ncu * 15 / 16 && t192 <= ncu)
+    else if (!W8 && g.N % 192 == 0 && t192 >= ncu * 15 / 16 && t192 <= ncu)
       t = 6;
     else if (t256 >= ncu * 3 / 4)
       t = 4;
     else
       t = 0;
   }
-  switch (t) {
-    case 1:
-      return launch<B128x128s3, ACT, RES, TOUT>(g, stream);
-    case 2:
-      return launch<B256x128s2, ACT, RES, TOUT>(g, stream);
-    case 3:
-      return launch<B128x256s2, ACT, RES, TOUT>(g, stream);
-    case 4:
-      return launch<B256x256s2, ACT, RES, TOUT>(g, stream);
-    case 5:
-      return launch<B64x128s2, ACT, RES, TOUT>(g, stream);
-    case 6:
-      return launch<B256x192s2, ACT, RES, TOUT>(g, stream);
-    default:
-      return launch<B128x128s2, ACT, RES, TOUT>(g, stream);
+  if constexpr (W8) {
+    // (the 256 x 256 tile has no room for the weight registers: 256 x 128 instead)
+    switch (t) {
+      case 2:
+      case 4:
+        return launch<B256x128s2, ACT, RES, TOUT, bf16, TW>(g, stream);
+      case 3:
+        return launch<B128x256s2, ACT, RES, TOUT, bf16, TW>(g, stream);
+      case 5:
+        return launch<B64x128s2, ACT, RES, TOUT, bf16, TW>(g, stream);
+      default:
+        return launch<B128x128s2, ACT, RES, TOUT, bf16, TW>(g, stream);
+    }
+  } else {
+    switch (t) {
+      case 1:
+        return launch<B128x128s3, ACT, RES, TOUT>(g, stream);
+      case 2:
+        return launch<B256x128s2, ACT, RES, TOUT>(g, stream);
+      case 3:
+        return launch<B128x256s2, ACT, RES, TOUT>(g, stream);
+      case 4:
+        return launch<B256x256s2, ACT, RES, TOUT>(g, stream);
+      case 5:
+        return launch<B64x128s2, ACT, RES, TOUT>(g, stream);
+      case 6:
+        return launch<B256x192s2, ACT, RES, TOUT>(g, stream);
+      default:
+        return launch<B128x128s2, ACT, RES, TOUT>(g, stream);
+    }
   }
 }
 
+template <class TW>
 int dispatch_res(const GemmArgs& g, int t, hipStream_t stream) {
   switch (t) {
     case 7:
-      return g.K % 128 ? 0 : launch<B128x128s2k2, ACT_NONE, true, float>(g, stream);
+      return g.K % 128 ? 0 : launch<B128x128s2k2, ACT_NONE, true, float, bf16, TW>(g, stream);
     case 1:
-      return launch<B128x128s3, ACT_NONE, true, float>(g, stream);
+      if constexpr (sizeof(TW) == 1) return 0;
+      else return launch<B128x128s3, ACT_NONE, true, float>(g, stream);
     case 2:
-      return launch<B256x128s2, ACT_NONE, true, float>(g, stream);
+      return launch<B256x128s2, ACT_NONE, true, float, bf16, TW>(g, stream);
     case 3:
-      return launch<B128x256s2, ACT_NONE, true, float>(g, stream);
+      return launch<B128x256s2, ACT_NONE, true, float, bf16, TW>(g, stream);
     case 5:
-      return launch<B64x128s2, ACT_NONE, true, float>(g, stream);
+      return launch<B64x128s2, ACT_NONE, true, float, bf16, TW>(g, stream);
     default:
-      return launch<B128x128s2, ACT_NONE, true, float>(g, stream);
+      return launch<B128x128s2, ACT_NONE, true, float, bf16, TW>(g, stream);
   }
 }
 
@@ -437,10 +513,11 @@ int split_k_partials(const GemmArgs& g, int splits, hipStream_t stream) {
 }
 
 int try_gemm_bf16(const GemmArgs& g, int x_dtype, int w_dtype, int w_layout, int compute, hipStream_t stream) {
-  if (compute != DT_BF16 || w_layout != 0 || x_dtype != DT_BF16 || w_dtype != DT_BF16) return 0;
+  if (compute != DT_BF16 || w_layout != 0 || x_dtype != DT_BF16 || (w_dtype != DT_BF16 && w_dtype != DT_I8)) return 0;
   if (g.norm != NORM_NONE || g.K % 64 != 0 || g.N % 8 != 0 || g.M <= 0 || g.N <= 0) return 0;
   if (g.M > 0x7fffffff || g.N > 0x7fffffff || g.K > 0x7fffffff) return 0;
-  if (!aligned16(g.x) || (g.ld_x * 2) % 16 || !aligned16(g.w) || (g.ld_w * 2) % 16) return 0;
+  const bool w8 = w_dtype == DT_I8;
+  if (!aligned16(g.x) || (g.ld_x * 2) % 16 || !aligned16(g.w) || (g.ld_w * (w8 ? 1 : 2)) % 16) return 0;
   if (g.w_scale && !aligned16(g.w_scale)) return 0;
   if (g.bias && (g.bias_dtype != DT_F32 || !aligned16(g.bias))) return 0;
   const bool res = g.res != nullptr;
@@ -457,7 +534,14 @@ int try_gemm_bf16(const GemmArgs& g, int x_dtype, int w_dtype, int w_layout, int
     // while the grid is at most one workgroup per CU; larger grids go to the pipelined kernel
     if (t < 0) t = (g.K % 128 == 0 && cdiv(g.M, 128) * cdiv(g.N, 128) <= cu_count()) ? 7 : 10;
     if (t >= 10) return 0;
-    return dispatch_res(g, t, stream);
+    return w8 ? dispatch_res<int8_t>(g, t, stream) : dispatch_res<bf16>(g, t, stream);
+  }
+  if (w8) {
+    if (out_bf16)
+      return g.act ? dispatch<ACT_GELU, false, bf16, int8_t>(g, stream)
+                   : dispatch<ACT_NONE, false, bf16, int8_t>(g, stream);
+    return g.act ? dispatch<ACT_GELU, false, float, int8_t>(g, stream)
+                 : dispatch<ACT_NONE, false, float, int8_t>(g, stream);
   }
   if (out_bf16)
     return g.act ? dispatch<ACT_GELU, false, bf16>(g, stream) : dispatch<ACT_NONE, false, bf16>(g, stream);

@@ -38,14 +38,6 @@ __device__ __forceinline__ void dma16(const void* g, void* lds_block) {
   __builtin_amdgcn_global_load_lds(g, lds_block, 16, 0, 0);
 }
 
-__device__ __forceinline__ bf16x8 widen_i8x8(uint2 raw) {
-  const int8_t* p = reinterpret_cast<const int8_t*>(&raw);
-  bf16x8 v;
-#pragma unroll
-  for (int j = 0; j < 8; ++j) v[j] = (bf16)(float)(int)p[j];
-  return v;
-}
-
 __device__ __forceinline__ void st_bf16x8(bf16* dst, const float (&f)[8]) {
   bf16x8 v;
 #pragma unroll

@@ -75,7 +75,11 @@ struct RowLnArgs {
   float a_scale;       // int8 A rows: A_f = a_scale * A
 };
 
-template <int BN, int S, bool Q8 = false, class TIN = bf16>
+// TW = int8_t with bf16 A rows: the QuantizedLinear int8 weight itself, loaded 8 bytes per
+// lane into registers one step ahead and widened exactly to bf16 into the LDS ring before
+// the step's barrier (lane (row r, chunk c): W[r, k0 + 8c .. +7] -> logical chunk c of LDS
+// row r), so the fragment reads are those of the bf16 weight.
+template <int BN, int S, bool Q8 = false, class TIN = bf16, class TW = TIN>
 __global__ __launch_bounds__(RL_THREADS) void gemm_rowln_kernel(RowLnArgs g) {
   using OP = Operand<TIN>;
   typedef typename OP::frag frag;
@@ -84,7 +88,10 @@ __global__ __launch_bounds__(RL_THREADS) void gemm_rowln_kernel(RowLnArgs g) {
   constexpr int TM = RL_BM / 16, TN = WN / 16;
   constexpr int A_STAGE = RL_BM * 128, W_STAGE = BN * 128;  // bytes
   constexpr int WB = W_STAGE / 1024 / RL_WAVES;             // W transfers per wavefront and step
-  constexpr int PER = 1 + WB;                                // + one A transfer (blocks shared 2:1)
+  constexpr bool WI8 = sizeof(TW) == 1 && sizeof(TIN) == 2;
+  constexpr int WL = WI8 ? BN / (8 * RL_WAVES) : 1;         // 8-byte int8 weight loads per lane and step
+  static_assert(!WI8 || S == 2, "int8 weights: two-stage ring");
+  constexpr int PER = 1 + (WI8 ? WL : WB);                   // + one A transfer (blocks shared 2:1)
   constexpr int RING = S * (A_STAGE + W_STAGE);
   static_assert(A_STAGE == 4 * 1024 && W_STAGE % (1024 * RL_WAVES) == 0 && TN >= 1, "shape");
   static_assert(PER * (S - 1) < 64, "vmcnt range");
@@ -101,23 +108,47 @@ __global__ __launch_bounds__(RL_THREADS) void gemm_rowln_kernel(RowLnArgs g) {
   const int ar = (wid & 3) * 8 + (lane >> 3);
   const TIN* a_src = reinterpret_cast<const TIN*>(g.x) + (int64_t)min(m0 + ar, M - 1) * g.ld_x +
                      ((lane & 7) ^ rl_swz(ar)) * EPC;
-  const TIN* w_src[WB];
+  const TW* w_src[WI8 ? WL : WB];
+  if constexpr (WI8) {
 #pragma unroll
-  for (int i = 0; i < WB; ++i) {
-    const int r = (wid * WB + i) * 8 + (lane >> 3);
-    w_src[i] = reinterpret_cast<const TIN*>(g.w) + (int64_t)r * g.ld_w + ((lane & 7) ^ rl_swz(r)) * EPC;
+    for (int i = 0; i < WL; ++i) {
+      const int r = (wid * WL + i) * 8 + (lane >> 3);
+      w_src[i] = reinterpret_cast<const TW*>(g.w) + (int64_t)r * g.ld_w + (lane & 7) * 8;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < WB; ++i) {
+      const int r = (wid * WB + i) * 8 + (lane >> 3);
+      w_src[i] = reinterpret_cast<const TW*>(g.w) + (int64_t)r * g.ld_w + ((lane & 7) ^ rl_swz(r)) * EPC;
+    }
   }
   auto a_stage = [&](int s) { return smem + s * A_STAGE; };
   auto w_stage = [&](int s) { return smem + S * A_STAGE + s * W_STAGE; };
   const int nk = K / BK;
+  uint2 wreg[WI8 ? WL : 1];  // int8 weight rows of the last issued step
   auto issue = [&](int kt) {
     const int s = kt % S, k0 = kt * BK;
+    if constexpr (WI8) {
+#pragma unroll
+      for (int i = 0; i < WL; ++i) wreg[i] = *reinterpret_cast<const uint2*>(w_src[i] + k0);
+    }
     __builtin_amdgcn_global_load_lds(static_cast<const void*>(a_src + k0),
                                      static_cast<void*>(a_stage(s) + (wid & 3) * 1024), 16, 0, 0);
+    if constexpr (!WI8) {
 #pragma unroll
-    for (int i = 0; i < WB; ++i)
-      __builtin_amdgcn_global_load_lds(static_cast<const void*>(w_src[i] + k0),
-                                       static_cast<void*>(w_stage(s) + (wid * WB + i) * 1024), 16, 0, 0);
+      for (int i = 0; i < WB; ++i)
+        __builtin_amdgcn_global_load_lds(static_cast<const void*>(w_src[i] + k0),
+                                         static_cast<void*>(w_stage(s) + (wid * WB + i) * 1024), 16, 0, 0);
+    }
+  };
+  auto commit_w = [&](int s) {  // widen the registers into W stage s
+    if constexpr (WI8) {
+#pragma unroll
+      for (int i = 0; i < WL; ++i) {
+        const int r = (wid * WL + i) * 8 + (lane >> 3), c = lane & 7;
+        *reinterpret_cast<bf16x8*>(w_stage(s) + r * 128 + ((c ^ rl_swz(r)) << 4)) = widen_i8x8(wreg[i]);
+      }
+    }
   };
 
   typename OP::accum acc[TM][TN];
@@ -155,9 +186,17 @@ __global__ __launch_bounds__(RL_THREADS) void gemm_rowln_kernel(RowLnArgs g) {
       for (int j = 0; j < TN; ++j) acc[i][j] = OP::mma(wf[j], af[i], acc[i][j]);
   };
 
+  if constexpr (WI8) {
+    issue(0);
+    rl_wait_vm<0>();
+    commit_w(0);
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): widened rows in LDS before the barrier
+    if (1 < nk) issue(1);
+  } else {
 #pragma unroll
-  for (int p = 0; p < S; ++p)
-    if (p < nk) issue(p);
+    for (int p = 0; p < S; ++p)
+      if (p < nk) issue(p);
+  }
   // The residual tile goes into registers right after the first ring stages: the first
   // MFMAs do not wait for it and its latency hides behind the main loop.  Its RV loads
   // sit behind the prologue's transfers in the wave's vmcnt (the scheduling barrier keeps
@@ -182,7 +221,7 @@ __global__ __launch_bounds__(RL_THREADS) void gemm_rowln_kernel(RowLnArgs g) {
       rl_wait_ahead<PER, S, 0>(ahead);
   };
   frag af0[TM], wf0[TN], af1[TM], wf1[TN];
-  wait_step(0, S - 1);
+  if constexpr (!WI8) wait_step(0, S - 1);  // (int8 weights: step 0 landed before it was widened)
   __builtin_amdgcn_s_barrier();
   read_frags(0, 0, af0, wf0);
   for (int kt = 0; kt < nk; ++kt) {
@@ -190,8 +229,13 @@ __global__ __launch_bounds__(RL_THREADS) void gemm_rowln_kernel(RowLnArgs g) {
     read_frags(st, 1, af1, wf1);
     mma(af0, wf0);
     if (kt + 1 < nk) {
-      __builtin_amdgcn_s_waitcnt(0xC07F);  // this wave's reads of stage st are in registers
-      wait_step(kt + 1, kt + S - 1);
+      if constexpr (WI8) {
+        rl_wait_vm<0>();  // step kt+1: A transfer and weight registers
+        commit_w((kt + 1) % S);
+      } else {
+        wait_step(kt + 1, kt + S - 1);
+      }
+      __builtin_amdgcn_s_waitcnt(0xC07F);  // this wave's reads of stage st (and W stores) done
       __builtin_amdgcn_s_barrier();        // all waves done with stage st; step kt+1 visible
       if (kt + S < nk) issue(kt + S);
       read_frags((kt + 1) % S, 0, af0, wf0);
@@ -348,8 +392,11 @@ namespace {
 int residual_ln(const char* who, int64_t M, int64_t N, int64_t K, const void* x, int64_t ld_x, const void* w,
                 int64_t ld_w, const float* w_scale, const float* bias, const float* res, int64_t ld_res,
                 int64_t res_rows, float* out, int64_t ld_out, const float* gamma, const float* beta, float eps,
-                void* xn, int64_t ld_xn, float xq_scale, bool q8, hipStream_t stream, float a_scale = 0.0f) {
+                void* xn, int64_t ld_xn, float xq_scale, bool q8, hipStream_t stream, float a_scale = 0.0f,
+                int w_dtype = DT_BF16) {
   const bool i8in = a_scale > 0.0f;  // int8 A rows and weight (W8A8)
+  const bool wi8 = !i8in && w_dtype == DT_I8;  // bf16 rows x the int8 weight (widened in the kernel)
+  CORTEX_CHECK_ARG(w_dtype == DT_BF16 || w_dtype == DT_I8, "%s: weight must be bf16 or int8 (got %d)", who, w_dtype);
   CORTEX_CHECK_ARG(M >= 0 && K > 0, "%s: need M >= 0 and K > 0", who);
   CORTEX_CHECK_ARG(N == 256 || N == 512, "%s: N must be 256 or 512 (got %lld)", who, (long long)N);
   CORTEX_CHECK_ARG(K % (i8in ? 2 * RL_BK : RL_BK) == 0 && K <= 0x7fffffffLL, "%s: K must be a multiple of %d", who,
@@ -363,7 +410,7 @@ int residual_ln(const char* who, int64_t M, int64_t N, int64_t K, const void* x,
                    who);
   CORTEX_CHECK_ARG(a16(x) && a16(w) && a16(res) && a16(out) && a16(xn) && a16(gamma) && a16(beta) &&
                        (!w_scale || a16(w_scale)) && (!bias || a16(bias)) && ld_x % (i8in ? 16 : 8) == 0 &&
-                       ld_w % (i8in ? 16 : 8) == 0 &&
+                       ld_w % (i8in || wi8 ? 16 : 8) == 0 &&
                        ld_res % 4 == 0 && ld_out % 4 == 0 && ld_xn % (q8 ? 16 : 8) == 0,
                    "%s: operands must be 16-byte aligned rows", who);
   RowLnArgs a{M,     N,     K,     x,   ld_x, w,     ld_w, w_scale, bias, res, ld_res, res_rows, out, ld_out,
@@ -375,6 +422,18 @@ int residual_ln(const char* who, int64_t M, int64_t N, int64_t K, const void* x,
       hipLaunchKernelGGL((gemm_rowln_kernel<512, 2, true, int8_t>), grid, dim3(RL_THREADS), 0, stream, a);
     else
       hipLaunchKernelGGL((gemm_rowln_kernel<512, 2, false, int8_t>), grid, dim3(RL_THREADS), 0, stream, a);
+  } else if (wi8) {
+    if (N == 512) {
+      if (q8)
+        hipLaunchKernelGGL((gemm_rowln_kernel<512, 2, true, bf16, int8_t>), grid, dim3(RL_THREADS), 0, stream, a);
+      else
+        hipLaunchKernelGGL((gemm_rowln_kernel<512, 2, false, bf16, int8_t>), grid, dim3(RL_THREADS), 0, stream, a);
+    } else {
+      if (q8)
+        hipLaunchKernelGGL((gemm_rowln_kernel<256, 2, true, bf16, int8_t>), grid, dim3(RL_THREADS), 0, stream, a);
+      else
+        hipLaunchKernelGGL((gemm_rowln_kernel<256, 2, false, bf16, int8_t>), grid, dim3(RL_THREADS), 0, stream, a);
+    }
   } else if (N == 512) {
     if (q8)
       hipLaunchKernelGGL((gemm_rowln_kernel<512, 2, true>), grid, dim3(RL_THREADS), 0, stream, a);
@@ -392,22 +451,23 @@ int residual_ln(const char* who, int64_t M, int64_t N, int64_t K, const void* x,
 
 }  // namespace
 
-extern "C" int cortex_linear_residual_ln(int64_t M, int64_t N, int64_t K, const void* x, int64_t ld_x, const void* w,
-                                         int64_t ld_w, const float* w_scale, const float* bias, const float* res,
-                                         int64_t ld_res, int64_t res_rows, float* out, int64_t ld_out,
-                                         const float* gamma, const float* beta, float eps, void* xn, int64_t ld_xn,
-                                         hipStream_t stream) {
+extern "C" int cortex_linear_residual_ln(int64_t M, int64_t N, int64_t K, const void* x, int64_t ld_x, int w_dtype,
+                                         const void* w, int64_t ld_w, const float* w_scale, const float* bias,
+                                         const float* res, int64_t ld_res, int64_t res_rows, float* out,
+                                         int64_t ld_out, const float* gamma, const float* beta, float eps, void* xn,
+                                         int64_t ld_xn, hipStream_t stream) {
   return residual_ln("cortex_linear_residual_ln", M, N, K, x, ld_x, w, ld_w, w_scale, bias, res, ld_res, res_rows,
-                     out, ld_out, gamma, beta, eps, xn, ld_xn, 0.0f, false, stream);
+                     out, ld_out, gamma, beta, eps, xn, ld_xn, 0.0f, false, stream, 0.0f, w_dtype);
 }
 
 extern "C" int cortex_linear_residual_ln_i8(int64_t M, int64_t N, int64_t K, const void* x, int64_t ld_x,
-                                            const void* w, int64_t ld_w, const float* w_scale, const float* bias,
-                                            const float* res, int64_t ld_res, int64_t res_rows, float* out,
-                                            int64_t ld_out, const float* gamma, const float* beta, float eps,
-                                            int8_t* xq, int64_t ld_xq, float xq_scale, hipStream_t stream) {
+                                            int w_dtype, const void* w, int64_t ld_w, const float* w_scale,
+                                            const float* bias, const float* res, int64_t ld_res, int64_t res_rows,
+                                            float* out, int64_t ld_out, const float* gamma, const float* beta,
+                                            float eps, int8_t* xq, int64_t ld_xq, float xq_scale,
+                                            hipStream_t stream) {
   return residual_ln("cortex_linear_residual_ln_i8", M, N, K, x, ld_x, w, ld_w, w_scale, bias, res, ld_res,
-                     res_rows, out, ld_out, gamma, beta, eps, xq, ld_xq, xq_scale, true, stream);
+                     res_rows, out, ld_out, gamma, beta, eps, xq, ld_xq, xq_scale, true, stream, 0.0f, w_dtype);
 }
 
 extern "C" int cortex_linear_residual_ln_w8a8(int64_t M, int64_t N, int64_t K, const int8_t* xq, int64_t ld_x,

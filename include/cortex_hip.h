@@ -223,22 +223,25 @@ int cortex_temporal_block_mask(const int64_t* event_times, int64_t t_stride, int
  * (head, sample), the projected q/k/v kept on chip:
  *   [q|k|v]_h[l] = xn[b*L + l] . W[{0,D,2D} + 64h + d]^T * w_scale (+ bias)
  *   out[b*L + l, 64h + d] = softmax_j(scale q_h[l] . k_h[j]) v_h[j]      (bf16)
- * xn (B*L, D) bf16 rows; w the (3D, D) bf16 weight image with optional per-row scale
- * and bias (3D, fp32).  Head dim 64 (D = 64 H), L <= 256, 16-byte aligned rows. */
-int cortex_qkv_attention(int64_t B, int64_t L, int64_t D, int64_t H, const void* xn, int64_t ld_x, const void* w,
-                         int64_t ld_w, const float* w_scale, const float* bias, float scale, void* out, int64_t ld_o,
-                         hipStream_t stream);
+ * xn (B*L, D) bf16 rows; w the (3D, D) weight with optional per-row scale and bias
+ * (3D, fp32): w_dtype 1 the bf16 image, or 3 the int8 weight of the QuantizedLinear
+ * (calibrate.py:170-235), widened exactly to bf16 inside the kernel (ld_w % 16 == 0).
+ * Head dim 64 (D = 64 H), L <= 256, 16-byte aligned rows. */
+int cortex_qkv_attention(int64_t B, int64_t L, int64_t D, int64_t H, const void* xn, int64_t ld_x, int w_dtype,
+                         const void* w, int64_t ld_w, const float* w_scale, const float* bias, float scale, void* out,
+                         int64_t ld_o, hipStream_t stream);
 
 /* Residual linear followed by a LayerNorm (SelfAttentionBlock, cortex/models/perceiver.py:
  * 121-124: x = x + out_proj(attn); norm_mlp(x); and the cross-attention residual followed
  * by the first block's norm_attn):
  *   out[m, n] = res[(m % res_rows) * ld_res + n] + (sum_k x[m, k] w[n, k]) * w_scale[n] + bias[n]
  *   xn[m, :]  = LN(out[m, :]; gamma, beta, eps)   (bf16)
- * x (M, K) and w (N, K) bf16 (the weight's bf16 image; w_scale/bias optional, fp32);
- * res/out fp32 (out may alias res: in-place residual update); res_rows 0 means M.
- * N in {256, 512}, K % 64 == 0, 16-byte aligned rows. */
-int cortex_linear_residual_ln(int64_t M, int64_t N, int64_t K, const void* x, int64_t ld_x, const void* w,
-                              int64_t ld_w, const float* w_scale, const float* bias, const float* res,
+ * x (M, K) bf16; w (N, K): w_dtype 1 the weight's bf16 image, or 3 the int8 weight of
+ * the QuantizedLinear, widened exactly to bf16 inside the kernel (ld_w % 16 == 0);
+ * w_scale/bias optional, fp32; res/out fp32 (out may alias res: in-place residual
+ * update); res_rows 0 means M.  N in {256, 512}, K % 64 == 0, 16-byte aligned rows. */
+int cortex_linear_residual_ln(int64_t M, int64_t N, int64_t K, const void* x, int64_t ld_x, int w_dtype,
+                              const void* w, int64_t ld_w, const float* w_scale, const float* bias, const float* res,
                               int64_t ld_res, int64_t res_rows, float* out, int64_t ld_out, const float* gamma,
                               const float* beta, float eps, void* xn, int64_t ld_xn, hipStream_t stream);
 
@@ -250,11 +253,11 @@ int cortex_linear_residual_ln(int64_t M, int64_t N, int64_t K, const void* x, in
  *
  * cortex_linear_residual_ln_i8: cortex_linear_residual_ln with the LayerNorm'd row
  * written as int8, xq[m, n] = q(LN(out[m, :])[n]; xq_scale); ld_xq a multiple of 16. */
-int cortex_linear_residual_ln_i8(int64_t M, int64_t N, int64_t K, const void* x, int64_t ld_x, const void* w,
-                                 int64_t ld_w, const float* w_scale, const float* bias, const float* res,
-                                 int64_t ld_res, int64_t res_rows, float* out, int64_t ld_out, const float* gamma,
-                                 const float* beta, float eps, int8_t* xq, int64_t ld_xq, float xq_scale,
-                                 hipStream_t stream);
+int cortex_linear_residual_ln_i8(int64_t M, int64_t N, int64_t K, const void* x, int64_t ld_x, int w_dtype,
+                                 const void* w, int64_t ld_w, const float* w_scale, const float* bias,
+                                 const float* res, int64_t ld_res, int64_t res_rows, float* out, int64_t ld_out,
+                                 const float* gamma, const float* beta, float eps, int8_t* xq, int64_t ld_xq,
+                                 float xq_scale, hipStream_t stream);
 
 /* cortex_linear_w8a8: y[m, n] = a_scale * w_scale[n] * sum_k x[m, k] w[n, k] + bias[n]
  * with x (M, K) int8 activations and w the (N, K) int8 weight of a QuantizedLinear, summed

@@ -121,6 +121,9 @@ def test_fused_qkv_attention(B, L, D, with_bias):
     bias = 0.05 * torch.randn(3 * D, generator=g) if with_bias else None
     img = ops.convert(q8.to(DEV), torch.bfloat16)
     out = ops.qkv_attention(xn.to(DEV), img, s.to(DEV), bias.to(DEV) if with_bias else None, B, L, Hh)
+    # the int8 weight itself, widened in the kernel: bit-identical to its bf16 image
+    out8 = ops.qkv_attention(xn.to(DEV), q8.to(DEV), s.to(DEV), bias.to(DEV) if with_bias else None, B, L, Hh)
+    torch.testing.assert_close(out8, out, rtol=0, atol=0)
     qkv = xn.double() @ q8.double().T * s.double()
     if with_bias:
         qkv = qkv + bias.double()

@@ -227,3 +227,43 @@ def test_fused_behavior_head_matches_oracle_and_unfused(name):
     assert np.abs(f - ref).max() <= 2e-2, (np.abs(f - ref).max(), np.abs(ref).max())
     assert np.abs(f - p).max() <= 2e-2
     assert torch.equal(fused, again)
+
+
+def test_widen_mode_streams_int8_weights_through_the_fused_path(monkeypatch):
+    """CORTEX_INT8_WEIGHTS=widen: no bf16 weight image is built; the GEMMs, the fused QKV +
+    attention and the residual linear + LayerNorm read the int8 weights and widen them on chip.
+    Config-3 shape (B=32 x 512 events): equal to the image mode (the same widened operands)
+    and within 2e-2 of the float32 oracle; the resident weight bytes drop to the int8 weights,
+    their scales and the float parameters."""
+    from cortex.kernels import ops
+    from cortex.models import _layers
+
+    arrs = _config3_inputs(seed=7)
+    inputs = [torch.from_numpy(a).to(DEV) for a in arrs]
+    monkeypatch.setattr(_layers, "INT8_WEIGHTS", "widen")
+    model = _int8(_model("s", "bfloat16"), [t[:2048] for t in inputs])
+    calls = {"qkv_attention": 0, "linear_residual_ln": 0}
+    for name in calls:
+        orig = getattr(ops, name)
+
+        def spy(*a, _orig=orig, _name=name, **k):
+            calls[_name] += 1
+            assert a[1].dtype == torch.int8, (_name, a[1].dtype)  # the weight argument
+            return _orig(*a, **k)
+        monkeypatch.setattr(ops, name, spy)
+    with torch.no_grad():
+        widen = model(*inputs, batch_size=32)["behavior"]
+        widen2 = model(*inputs, batch_size=32)["behavior"]
+    assert calls["qkv_attention"] == 2 * 7 and calls["linear_residual_ln"] >= 2 * 7
+    wb = _layers.resident_weight_bytes(model)
+    assert wb["bf16_images"] == 0 and 20e6 < wb["int8_weights"] < 30e6
+    monkeypatch.undo()
+    with torch.no_grad():
+        image = model(*inputs, batch_size=32)["behavior"]
+    # (the batch-invariant query projections and the folded head stay cached from the widen run)
+    assert 1.5 * wb["int8_weights"] < _layers.resident_weight_bytes(model)["bf16_images"] <= 2 * wb["int8_weights"]
+    torch.testing.assert_close(widen, widen2, rtol=0, atol=0)
+    torch.testing.assert_close(widen, image, rtol=0, atol=1e-5 * float(image.abs().max()))
+    sd = {k: v.detach().cpu() for k, v in model.state_dict().items()}
+    ref = O.forward(sd, O.CORTEX_S_SHAPE, *arrs).numpy()
+    assert np.abs(widen.cpu().numpy() - ref).max() <= 2e-2
