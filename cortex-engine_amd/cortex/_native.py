@@ -87,6 +87,10 @@ _SIGNATURES = {
         _int,
         [_ptr, _i64, _i64, _i64, _i64, _i64, _i64, _ptr, _ptr, _f32, _ptr, _ptr, _f32, _ptr, _ptr, _ptr, _i64,
          _ptr]),
+    "cortex_norm_linear_fused": (
+        _int,
+        [_i64, _i64, _i64, _ptr, _i64, _int, _ptr, _ptr, _int, _f32, _int, _ptr, _i64, _ptr, _ptr, _int, _int, _ptr,
+         _i64, _ptr]),
     "cortex_pooled_linear": (
         _int,
         [_ptr, _i64, _i64, _i64, _i64, _ptr, _ptr, _f32, _i64, _int, _ptr, _i64, _ptr, _ptr, _ptr, _ptr, _ptr]),

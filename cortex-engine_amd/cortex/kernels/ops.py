@@ -10,6 +10,7 @@ synchronises the host.
 from __future__ import annotations
 
 import math
+from collections import OrderedDict
 
 import torch
 
@@ -463,6 +464,48 @@ def convert(t: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
 # --------------------------------------------------------------------------- linear
 
 
+_KN_CACHE: "OrderedDict[tuple, tuple]" = OrderedDict()
+_KN_CACHE_SIZE = 16
+
+
+def kn_weight_rows(w: torch.Tensor) -> torch.Tensor:
+    """The (N, K) bf16 rows of a (K, N) weight (``rms_norm_linear``'s layout), cached per weight:
+    the cache holds the weight's storage (so its address is not reused while cached) and
+    rebuilds the rows when the weight's version counter moves (an in-place update)."""
+    key = (w.untyped_storage().data_ptr(), w.storage_offset(), tuple(w.shape), tuple(w.stride()), w.dtype,
+           w.device)
+    hit = _KN_CACHE.get(key)
+    if hit is not None and hit[1] == w._version:
+        _KN_CACHE.move_to_end(key)
+        return hit[2]
+    rows = transpose_bf16(w if w.dtype == torch.bfloat16 else w.to(torch.bfloat16))
+    _KN_CACHE[key] = (w.untyped_storage(), w._version, rows)
+    _KN_CACHE.move_to_end(key)
+    while len(_KN_CACHE) > _KN_CACHE_SIZE:
+        _KN_CACHE.popitem(last=False)
+    return rows
+
+
+def norm_linear_fused(x: torch.Tensor, w: torch.Tensor, w_scale=None, *, norm: str = "rms", gamma, beta=None,
+                      eps: float = 1e-6, bias=None, act: str | None = None,
+                      out: torch.Tensor | None = None, out_dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
+    """``act(norm(x) @ w^T * w_scale + bias)`` in one launch (``cortex_norm_linear_fused``): x (M, K)
+    bf16 rows (K a multiple of 64 up to 512), w (N, K) bf16 or int8, the RMS / LayerNorm
+    statistics computed in the kernel from the staged rows."""
+    dev = nat.require_gpu(x, w, w_scale, gamma, beta, bias, out, what="norm_linear_fused")
+    M, K = x.shape
+    N = w.shape[0]
+    if out is None:
+        out = torch.empty((M, N), dtype=out_dtype, device=dev)
+    g = gamma.detach().contiguous()
+    b = beta.detach().contiguous() if (beta is not None and norm == "layer") else None
+    nat.call("cortex_norm_linear_fused", M, N, K, nat.ptr(x), x.stride(0) if M > 1 else K, NORM[norm], nat.ptr(g),
+             nat.ptr(b), nat.code(g.dtype), float(eps), nat.code(w.dtype), nat.ptr(w), w.stride(0) if N > 1 else K,
+             nat.ptr(w_scale), nat.ptr(bias), ACT[act], nat.code(out.dtype), nat.ptr(out),
+             out.stride(0) if M > 1 else N, nat.stream_of(dev))
+    return out
+
+
 def norm_linear(x: torch.Tensor, *, weight: torch.Tensor | None = None, weight_int8: torch.Tensor | None = None,
                 weight_scale: torch.Tensor | None = None, w_layout: str = "nk", norm: str | None = None,
                 gamma=None, beta=None, eps: float = 1e-5, stats=None, bias=None, act: str | None = None,
@@ -505,6 +548,20 @@ def norm_linear(x: torch.Tensor, *, weight: torch.Tensor | None = None, weight_i
     if out2.data_ptr() != out.data_ptr() or (M > 1 and out2.stride(0) < N) or out2.stride(-1) != 1:
         raise ValueError("out must be row-major contiguous over its last dim")
     nrm = NORM[norm]
+    if (nrm and stats is None and residual is None and compute_dtype == torch.bfloat16 and x2.dtype == torch.bfloat16
+            and K % 64 == 0 and K <= 512 and N % 8 == 0 and out_dtype in (torch.bfloat16, torch.float32)
+            and (weight_int8 is not None or w2.dtype == torch.bfloat16 or layout == 1) and gamma is not None
+            and gamma.dtype in (torch.float32, torch.bfloat16) and (beta is None or beta.dtype == gamma.dtype)
+            and (bias is None or bias.dtype == torch.float32)
+            and x2.data_ptr() % 16 == 0 and (M == 1 or x2.stride(0) % 8 == 0)
+            and (layout == 1 or (w2.data_ptr() % 16 == 0 and (N == 1 or w2.stride(0) % 16 == 0)))
+            and all(t is None or t.data_ptr() % 16 == 0 for t in (ws, bias, out2, gamma, beta))
+            and gamma.is_contiguous() and (beta is None or beta.is_contiguous())):
+        # one launch: the statistics from the staged x panel, the contraction on (N, K) rows
+        if weight_int8 is None and layout == 1:
+            w2 = kn_weight_rows(w2)
+        return norm_linear_fused(x2, w2, ws, norm=norm, gamma=gamma, beta=beta, eps=eps, bias=bias, act=act,
+                                 out=out2).reshape(out.shape)
     if (nrm and stats is None and compute_dtype == torch.bfloat16 and K in _LN_ROWS_K
             and x2.dtype in (torch.bfloat16, torch.float32) and x2.data_ptr() % 16 == 0
             and (M == 1 or x2.stride(0) % 4 == 0)

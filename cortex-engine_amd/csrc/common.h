@@ -112,6 +112,26 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+
+// Sum over the 64 lanes, in every lane: DPP adds inside each 16-lane row (quad xor 1,
+// quad xor 2, row rotate 4, row rotate 8), then the four row sums read out as scalars.
+// A few cycles per step instead of an LDS round trip per shuffle (wave_sum).
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+  v += dpp_mov<0xB1>(v);
+  v += dpp_mov<0x4E>(v);
+  v += dpp_mov<0x124>(v);
+  v += dpp_mov<0x128>(v);
+  const int iv = __builtin_bit_cast(int, v);
+  return (__builtin_bit_cast(float, __builtin_amdgcn_readlane(iv, 0)) +
+          __builtin_bit_cast(float, __builtin_amdgcn_readlane(iv, 16))) +
+         (__builtin_bit_cast(float, __builtin_amdgcn_readlane(iv, 32)) +
+          __builtin_bit_cast(float, __builtin_amdgcn_readlane(iv, 48)));
+}
+
 // Workgroups go to the 8 XCDs round-robin by linear id (id % 8).  A kernel whose
 // neighbouring work items share operands (the column tiles of one row panel, the
 // query blocks or heads of one sample) indexes them by xcd_affine(id, total): XCD x

@@ -500,6 +500,418 @@ int dispatch_res(const GemmArgs& g, int t, hipStream_t stream) {
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
+// ---------------------------------------------------------------------------------------
+// Norm prologue + GEMM in one kernel (rms_norm_linear, reference cortex/kernels/
+// fused_rmsnorm.py:130-233, and its INT8-weight / LayerNorm forms):
+//
+//   C[m, n] = epi( sum_k y[m, k] W[n, k] ),  y = bf16( x / sqrt(mean(x^2) + eps) * gamma )   (RMS)
+//                                            y = bf16( (x - mu) / sqrt(var + eps) * gamma + beta ) (LN)
+//
+// A workgroup owns a panel of BM rows for all of K (K <= 512): the panel is transferred
+// into LDS once (swizzled 128-byte rows, one sub-panel per 64 K), each wavefront computes
+// the statistics of its rows from the staged values and writes the normalised bf16 rows
+// back in place, and the workgroup then walks its column tiles (tile g, g + G, ... of
+// the N / BN tiles) as one stream of (tile, K-step) steps, transferring only the weight,
+// direct to LDS, through an S-stage ring.  The int8 weight stays int8 in LDS (64-byte rows
+// per step, four stages) and each wavefront widens its fragments exactly after the LDS
+// read; a bf16 weight uses 128-byte rows (two stages).  The MFMA loop, the fragment
+// layouts and the register epilogue are those of gemm_bf16_kernel.
+template <int BM_, int BN_, int WM_, int WN_, int S8_, int S16_>
+struct NTile {
+  static constexpr int BM = BM_, BN = BN_, WM = WM_, WN = WN_, WAVES = WM * WN, THREADS = 64 * WAVES;
+  static constexpr int S8 = S8_, S16 = S16_;  // ring stages for int8 / bf16 weights
+  static constexpr int TM = BM / WM / 16, TN = BN / WN / 16;
+  static constexpr int KMAX = 512;
+  static constexpr int PANEL = BM * KMAX * 2;
+  static constexpr int LDS8 = PANEL + S8 * BN * 64, LDS16 = PANEL + S16 * BN * 128;
+  static_assert(TM >= 1 && TN >= 2 && TN % 2 == 0, "shape");
+  static_assert((BN * 64) % (1024 * WAVES) == 0, "transfer split");
+  static_assert(BM % 8 == 0 && LDS8 <= 160 * 1024 && LDS16 <= 160 * 1024, "LDS");
+};
+
+struct NormGemmArgs {
+  int64_t M, N, K;
+  const bf16* x;
+  int64_t ld_x;
+  int norm;  // NORM_RMS or NORM_LAYER
+  const void* gamma;
+  const void* beta;  // LayerNorm only (may be null)
+  int gamma_dtype;   // DT_F32 or DT_BF16 (beta the same)
+  float eps;
+  const void* w;  // (N, K) rows: bf16 or int8
+  int64_t ld_w;
+  const float* w_scale;
+  const float* bias;
+  void* out;
+  int64_t ld_out;
+  int groups;  // G: column-tile groups per row panel (gridDim.x)
+};
+
+// s_waitcnt vmcnt(n * PER) for a runtime n in [0, NMAX]
+template <int PER, int NMAX>
+__device__ __forceinline__ void wait_vm_steps(int n) {
+  if constexpr (NMAX > 0) {
+    if (n >= NMAX) {
+      wait_vm<(NMAX * PER < 63 ? NMAX * PER : 63)>();
+      return;
+    }
+    wait_vm_steps<PER, NMAX - 1>(n);
+  } else {
+    wait_vm<0>();
+  }
+}
+
+// Direct-to-LDS transfer of 16 bytes per lane (global_load_lds_dwordx4, LDS destination
+// lds_dst + 16 * lane) issued from inline assembly, so that the compiler does not treat
+// the LDS reads that follow as aliasing the transfer and wait for every transfer in
+// flight (it cannot tell ring stages apart).  The kernel's own vmcnt waits and barriers
+// order each stage's reads after its transfers; the compiler's waits for its own vector
+// loads stay conservative, as it counts fewer operations in flight than there are.  A
+// flat pointer to LDS carries the LDS offset in its low 32 bits (the aperture base is
+// 4 GiB aligned).
+__device__ __forceinline__ void lds_dma16(const void* gsrc, void* lds_dst) {
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds_dst);
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gsrc), "s"(m0) : "memory", "m0");
+}
+
+// 16-byte chunk swizzle of the 64-byte int8 weight rows: the 16 rows of a fragment read
+// (consecutive, or the interleaved order of wrow_of) land in 16 distinct four-bank groups.
+__device__ __forceinline__ int swz8(int r) { return ((r >> 3) ^ (r >> 2)) & 3; }
+
+template <class TL, class TW, int ACT, class TOUT>
+__global__ __launch_bounds__(TL::THREADS) void norm_gemm_kernel(NormGemmArgs g) {
+  constexpr int BM = TL::BM, BN = TL::BN, TM = TL::TM, TN = TL::TN, WAVES = TL::WAVES;
+  constexpr bool WI8 = sizeof(TW) == 1;
+  constexpr bool IL = sizeof(TOUT) == 2;  // bf16 out: interleaved W rows, 8 consecutive columns per lane
+  constexpr int S = WI8 ? TL::S8 : TL::S16;
+  constexpr int ROWB = WI8 ? 64 : 128;            // weight bytes per row and step (64 K)
+  constexpr int W_STAGE = BN * ROWB;
+  constexpr int WB = W_STAGE / 1024 / WAVES;      // 1 KiB transfers per wavefront and step
+  constexpr int RPB = 1024 / ROWB;                // rows per transfer: 16 or 8
+  static_assert(W_STAGE % (1024 * WAVES) == 0 && WB * S < 64, "weight transfer split");
+  __shared__ __attribute__((aligned(1024))) unsigned char smem[WI8 ? TL::LDS8 : TL::LDS16];
+  unsigned char* const panel = smem;                  // K / 64 sub-panels of BM x 128 bytes
+  unsigned char* const wring = smem + TL::PANEL;
+  auto sub = [&](int kt) { return panel + kt * (BM * 128); };
+  auto w_stage = [&](int s) { return wring + s * W_STAGE; };
+  auto wsw = [&](int r) { return WI8 ? swz8(r) : (IL ? swz_w(r) : swz_a(r)); };
+
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int M = (int)g.M, N = (int)g.N, K = (int)g.K;
+  const int nk = K / 64;
+  // row panel per blockIdx.y, column-tile group per blockIdx.x; the groups of one panel
+  // sit on one XCD (the panel's rows in one L2)
+  const int G = gridDim.x, total = gridDim.x * gridDim.y;
+  const int id = xcd_affine(blockIdx.x + G * blockIdx.y, total);
+  const int m0 = (id / G) * BM, grp = id % G;
+  const int ntiles = (N + BN - 1) / BN;
+  const int my_tiles = grp < ntiles ? (ntiles - 1 - grp) / G + 1 : 0;
+  const int nsteps = my_tiles * nk;
+
+  // weight rows of step j (tile grp + (j / nk) G, K step j % nk) into stage j % S: lane i of
+  // a transfer writes row i / (ROWB / 16), physical chunk i % (ROWB / 16), which holds the
+  // logical chunk (i % (ROWB / 16)) ^ swizzle(row)
+  auto issue = [&](int j) {
+    const int n0 = (grp + (j / nk) * G) * BN, k0 = (j % nk) * 64, s = j % S;
+    constexpr int CPR = ROWB / 16;
+#pragma unroll
+    for (int i = 0; i < WB; ++i) {
+      const int r = (wid * WB + i) * RPB + lane / CPR;
+      const int lc = (lane % CPR) ^ wsw(r);
+      const TW* src = reinterpret_cast<const TW*>(g.w) + (int64_t)min(n0 + r, N - 1) * g.ld_w + k0 +
+                      lc * (16 / (int)sizeof(TW));
+      lds_dma16(src, w_stage(s) + (wid * WB + i) * 1024);
+    }
+  };
+
+  // ---- prologue: the whole panel into LDS (sub-panel kt, 1 KiB blocks of 8 rows), this
+  // lane's gamma / beta columns, then the first S weight steps (in flight during the norm)
+  {
+    constexpr int BLK_PER_SUB = BM / 8;
+    const int nblk = BLK_PER_SUB * nk;
+    for (int b = wid; b < nblk; b += WAVES) {
+      const int kt = b / BLK_PER_SUB, r = (b % BLK_PER_SUB) * 8 + (lane >> 3);
+      const bf16* src = g.x + (int64_t)min(m0 + r, M - 1) * g.ld_x + kt * 64 + ((lane & 7) ^ swz_a(r)) * 8;
+      lds_dma16(src, sub(kt) + (b % BLK_PER_SUB) * 1024);
+    }
+  }
+  constexpr int CPL = TL::KMAX / 8 / 64;  // 16-byte chunks per lane at the largest K
+  float gm[CPL][8], bt[CPL][8];
+  {
+    const int nch = K / 8;
+    auto ld8 = [&](const void* p, int c, float (&dst)[8]) {
+      if (g.gamma_dtype == DT_BF16) {
+        const bf16x8 t = *reinterpret_cast<const bf16x8*>(reinterpret_cast<const bf16*>(p) + c * 8);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) dst[j] = (float)t[j];
+      } else {
+        const float4 a = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(p) + c * 8);
+        const float4 b = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(p) + c * 8 + 4);
+        dst[0] = a.x; dst[1] = a.y; dst[2] = a.z; dst[3] = a.w;
+        dst[4] = b.x; dst[5] = b.y; dst[6] = b.z; dst[7] = b.w;
+      }
+    };
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+      const int c = min(lane + 64 * i, nch - 1);  // lanes past K repeat a valid chunk (unused)
+      ld8(g.gamma, c, gm[i]);
+      if (g.beta) {
+        ld8(g.beta, c, bt[i]);
+      } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) bt[i][j] = 0.0f;
+      }
+    }
+  }
+  wait_vm<0>();  // the panel and gamma / beta (the weights are issued after: not waited for)
+#pragma unroll
+  for (int p = 0; p < S; ++p)
+    if (p < nsteps) issue(p);
+  __builtin_amdgcn_s_barrier();
+  // ---- statistics and normalisation in place: wavefront w takes NR rows at a time
+  // (rows w NR .. w NR + NR - 1, then + WAVES NR ...; NR independent reductions in flight);
+  // lane l the 16-byte chunks c = l, l + 64, ... (chunk c: sub-panel c / 8, logical chunk c % 8)
+  {
+    constexpr int NR = 8;
+    static_assert(BM % (WAVES * NR) == 0, "rows per wavefront");
+    const int nch = K / 8;
+    const float fk = (float)K;  // means as sum / K, as torch's mean
+    for (int r0 = wid * NR; r0 < BM; r0 += WAVES * NR) {
+      float v[NR][CPL][8];
+      float s1[NR], mu[NR], inv[NR];
+      // every read first (lanes past K read a valid chunk and drop it), then the sums
+      bf16x8 raw[NR][CPL];
+#pragma unroll
+      for (int q = 0; q < NR; ++q)
+#pragma unroll
+        for (int i = 0; i < CPL; ++i) {
+          const int r = r0 + q, c = min(lane + 64 * i, nch - 1);
+          raw[q][i] = *reinterpret_cast<const bf16x8*>(sub(c >> 3) + r * 128 + (((c & 7) ^ swz_a(r)) << 4));
+        }
+#pragma unroll
+      for (int q = 0; q < NR; ++q) {
+        s1[q] = 0.0f;
+#pragma unroll
+        for (int i = 0; i < CPL; ++i) {
+          const bool ok = lane + 64 * i < nch;
+#pragma unroll
+          for (int j = 0; j < 8; ++j) v[q][i][j] = ok ? (float)raw[q][i][j] : 0.0f;
+#pragma unroll
+          for (int j = 0; j < 8; ++j) s1[q] += (g.norm == NORM_RMS) ? v[q][i][j] * v[q][i][j] : v[q][i][j];
+        }
+      }
+#pragma unroll
+      for (int q = 0; q < NR; ++q) s1[q] = wave_sum_dpp(s1[q]);
+      if (g.norm == NORM_RMS) {
+#pragma unroll
+        for (int q = 0; q < NR; ++q) {
+          mu[q] = 0.0f;
+          inv[q] = 1.0f / sqrtf(s1[q] / fk + g.eps);
+        }
+      } else {
+        float s2[NR];
+#pragma unroll
+        for (int q = 0; q < NR; ++q) {
+          mu[q] = s1[q] / fk;
+          s2[q] = 0.0f;
+#pragma unroll
+          for (int i = 0; i < CPL; ++i) {
+            const bool ok = lane + 64 * i < nch;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+              const float d = ok ? v[q][i][j] - mu[q] : 0.0f;
+              s2[q] += d * d;
+            }
+          }
+        }
+#pragma unroll
+        for (int q = 0; q < NR; ++q) inv[q] = 1.0f / sqrtf(wave_sum_dpp(s2[q]) / fk + g.eps);
+      }
+#pragma unroll
+      for (int q = 0; q < NR; ++q) {
+        const int r = r0 + q;
+#pragma unroll
+        for (int i = 0; i < CPL; ++i) {
+          const int c = lane + 64 * i;
+          if (c < nch) {
+            bf16x8 t;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) t[j] = (bf16)fmaf((v[q][i][j] - mu[q]) * inv[q], gm[i][j], bt[i][j]);
+            *reinterpret_cast<bf16x8*>(sub(c >> 3) + r * 128 + (((c & 7) ^ swz_a(r)) << 4)) = t;
+          }
+        }
+      }
+    }
+  }
+
+  // ---- column tiles: the (tile, K step) sequence as one stream of steps
+  const int wm = wid / TL::WN, wn = wid % TL::WN;
+  const int fr = lane & 15, g4 = lane >> 4;
+  const int wrow = wm * (BM / TL::WM), wcol = wn * (BN / TL::WN);
+  int a_off[TM], a_sw[TM], w_off[TN], w_sw[TN];
+#pragma unroll
+  for (int t = 0; t < TM; ++t) {
+    const int r = wrow + t * 16 + fr;
+    a_off[t] = r * 128;
+    a_sw[t] = swz_a(r);
+  }
+#pragma unroll
+  for (int t = 0; t < TN; ++t) {
+    const int r = wcol + (IL ? wrow_of(t >> 1, t & 1, fr) : t * 16 + fr);
+    w_off[t] = r * ROWB;
+    w_sw[t] = wsw(r);
+  }
+  auto read_frags = [&](int j, int ks, bf16x8 (&af)[TM], bf16x8 (&wf)[TN]) {
+    const unsigned char* as = sub(j % nk);
+    const unsigned char* ws = w_stage(j % S);
+#pragma unroll
+    for (int t = 0; t < TM; ++t) af[t] = *reinterpret_cast<const bf16x8*>(as + a_off[t] + (((ks * 4 + g4) ^ a_sw[t]) << 4));
+#pragma unroll
+    for (int t = 0; t < TN; ++t) {
+      if constexpr (WI8) {  // K slice [32 ks + 8 g4, +8): half (g4 & 1) of logical chunk 2 ks + g4 / 2
+        const uint2 raw = *reinterpret_cast<const uint2*>(ws + w_off[t] + (((2 * ks + (g4 >> 1)) ^ w_sw[t]) << 4) +
+                                                          (g4 & 1) * 8);
+        wf[t] = widen_i8x8(raw);
+      } else {
+        wf[t] = *reinterpret_cast<const bf16x8*>(ws + w_off[t] + (((ks * 4 + g4) ^ w_sw[t]) << 4));
+      }
+    }
+  };
+  f32x4 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) acc[i][j] = (f32x4){0, 0, 0, 0};
+  auto mma = [&](const bf16x8 (&af)[TM], const bf16x8 (&wf)[TN]) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf[j], af[i], acc[i][j], 0, 0, 0);
+  };
+  auto epilogue = [&](int n0) {
+    constexpr int NV = IL ? 8 : 4, NG = IL ? TN / 2 : TN;
+    // every scale and bias load first (columns clamped into range, so no load is skipped
+    // and none is left in flight past the epilogue), then one wait, then the stores
+    float sca[NG][NV], bia[NG][NV];
+#pragma unroll
+    for (int p = 0; p < NG; ++p) {
+      const int n = min(n0 + wcol + (IL ? 32 * p + 8 * g4 : 16 * p + 4 * g4), N - NV);
+#pragma unroll
+      for (int h = 0; h < NV / 4; ++h) {
+        const float4 s4 = g.w_scale ? *reinterpret_cast<const float4*>(g.w_scale + n + 4 * h) : make_float4(1.f, 1.f, 1.f, 1.f);
+        const float4 b4 = g.bias ? *reinterpret_cast<const float4*>(g.bias + n + 4 * h) : make_float4(0.f, 0.f, 0.f, 0.f);
+        sca[p][4 * h] = s4.x; sca[p][4 * h + 1] = s4.y; sca[p][4 * h + 2] = s4.z; sca[p][4 * h + 3] = s4.w;
+        bia[p][4 * h] = b4.x; bia[p][4 * h + 1] = b4.y; bia[p][4 * h + 2] = b4.z; bia[p][4 * h + 3] = b4.w;
+      }
+    }
+    wait_vm<0>();
+#pragma unroll
+    for (int p = 0; p < NG; ++p) {
+      const int n = n0 + wcol + (IL ? 32 * p + 8 * g4 : 16 * p + 4 * g4);
+      if (n >= N) continue;  // N % 8 == 0: a lane's columns are all in or all out
+      const float* sc = sca[p];
+      const float* bi = bia[p];
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        const int m = m0 + wrow + i * 16 + fr;
+        if (m >= M) continue;
+        float v[NV];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          if constexpr (IL) {
+            v[r] = acc[i][2 * p][r] * sc[r] + bi[r];
+            v[4 + r] = acc[i][2 * p + 1][r] * sc[4 + r] + bi[4 + r];
+          } else {
+            v[r] = acc[i][p][r] * sc[r] + bi[r];
+          }
+        }
+        if (ACT == ACT_GELU) {
+#pragma unroll
+          for (int e = 0; e < NV; ++e) v[e] = IL ? gelu_erf_bf16out(v[e]) : gelu_erf(v[e]);
+        }
+        TOUT* op = reinterpret_cast<TOUT*>(g.out) + (int64_t)m * g.ld_out + n;
+        if constexpr (IL) {
+          bf16x8 o;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) o[e] = (bf16)v[e];
+          *reinterpret_cast<bf16x8*>(op) = o;
+        } else {
+          *reinterpret_cast<float4*>(op) = make_float4(v[0], v[1], v[2], v[3]);
+        }
+      }
+    }
+  };
+
+  // Every stage in flight; a stage is refilled as soon as all wavefronts hold its last
+  // fragments in registers (as gemm_bf16_kernel).  A step's wait counts only weight
+  // transfers after it; epilogue loads and stores issued in between make it wait longer,
+  // never shorter (vector-memory operations complete in order).
+  bf16x8 af0[TM], wf0[TN], af1[TM], wf1[TN];
+  if (nsteps > 0) wait_vm_steps<WB, S - 1>(min(S, nsteps) - 1);  // step 0 landed
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the normalised rows are stored
+  __builtin_amdgcn_s_barrier();        // ... and visible with step 0 to every wavefront
+  if (nsteps > 0) read_frags(0, 0, af0, wf0);
+  for (int j = 0; j < nsteps; ++j) {
+    read_frags(j, 1, af1, wf1);
+    mma(af0, wf0);
+    if (j + 1 < nsteps) {
+      __builtin_amdgcn_s_waitcnt(0xC07F);  // this wave's reads of stage j % S are in registers
+      wait_vm_steps<WB, S - 1>(min(j + S - 1, nsteps - 1) - (j + 1));  // step j+1 landed
+      __builtin_amdgcn_s_barrier();        // all waves done with stage j % S; step j+1 visible
+      if (j + S < nsteps) issue(j + S);    // refill stage j % S
+      read_frags(j + 1, 0, af0, wf0);
+    }
+    mma(af1, wf1);
+    if (j % nk == nk - 1) {  // last K step of a tile: its epilogue, then a fresh accumulator
+      epilogue((grp + (j / nk) * G) * BN);
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int t = 0; t < TN; ++t) acc[i][t] = (f32x4){0, 0, 0, 0};
+    }
+  }
+}
+
+using N128x128 = NTile<128, 128, 2, 4, 4, 2>;
+using N64x128 = NTile<64, 128, 2, 4, 8, 6>;
+using N64x256 = NTile<64, 256, 2, 4, 6, 3>;
+
+template <class TL, class TW, int ACT, class TOUT>
+int launch_norm(const NormGemmArgs& a0, hipStream_t stream) {
+  NormGemmArgs a = a0;
+  const int64_t panels = cdiv(a.M, TL::BM), ntiles = cdiv(a.N, TL::BN);
+  // column-tile groups: enough workgroups to fill the CUs once, each walking its tiles
+  int64_t G = cdiv((int64_t)cu_count(), panels);
+  G = G < 1 ? 1 : (G > ntiles ? ntiles : G);
+  if (panels > 65535 || G * panels > 0x7fffffffLL) return 0;
+  a.groups = (int)G;
+  hipLaunchKernelGGL((norm_gemm_kernel<TL, TW, ACT, TOUT>), dim3((unsigned)G, (unsigned)panels), dim3(TL::THREADS), 0,
+                     stream, a);
+  CORTEX_CHECK_LAUNCH("norm_gemm_kernel");
+  return 1;
+}
+
+template <class TW, int ACT, class TOUT>
+int dispatch_norm(const NormGemmArgs& a, hipStream_t stream) {
+  static const int tile = [] {
+    const char* e = getenv("CORTEX_NORM_TILE");
+    return e ? atoi(e) : -1;
+  }();
+  int t = tile;
+  // narrow outputs (N <= 512): 64-row panels, each workgroup one or two 256-column tiles
+  // (the normalisation is repeated per column-tile group, so fewer, wider groups); wider
+  // outputs: 128-row panels, half the weight re-reads
+  if (t < 0) t = a.N <= 512 ? 1 : 0;
+  switch (t) {
+    case 1:
+      return launch_norm<N64x256, TW, ACT, TOUT>(a, stream);
+    case 2:
+      return launch_norm<N64x128, TW, ACT, TOUT>(a, stream);
+    default:
+      return launch_norm<N128x128, TW, ACT, TOUT>(a, stream);
+  }
+}
+
 }  // namespace
 
 int split_k_partials(const GemmArgs& g, int splits, hipStream_t stream) {
@@ -629,6 +1041,45 @@ extern "C" int cortex_linear_w8a8(int64_t M, int64_t N, int64_t K, const int8_t*
   } else {
     st = act == ACT_GELU ? launch<B128x128s2, ACT_GELU, false, float, int8_t>(g, stream)
                          : launch<B128x128s2, ACT_NONE, false, float, int8_t>(g, stream);
+  }
+  if (st < 0) return st;
+  if (st == 0) {
+    set_error("%s: grid too large", who);
+    return E_INVALID;
+  }
+  return OK;
+}
+
+extern "C" int cortex_norm_linear_fused(int64_t M, int64_t N, int64_t K, const void* x, int64_t ld_x, int norm,
+                                        const void* gamma, const void* beta, int gamma_dtype, float eps, int w_dtype,
+                                        const void* w, int64_t ld_w, const float* w_scale, const float* bias, int act,
+                                        int out_dtype, void* out, int64_t ld_out, hipStream_t stream) {
+  const char* who = "cortex_norm_linear_fused";
+  CORTEX_CHECK_ARG(M >= 0 && N > 0 && K > 0, "%s: need M >= 0, N > 0, K > 0", who);
+  if (M == 0) return OK;
+  CORTEX_CHECK_ARG(M <= 0x7fffffffLL && N <= 0x7fffffffLL, "%s: size too large", who);
+  CORTEX_CHECK_ARG(K % 64 == 0 && K <= 512 && N % 8 == 0, "%s: need K a multiple of 64 up to 512 and N of 8", who);
+  CORTEX_CHECK_ARG(norm == NORM_RMS || norm == NORM_LAYER, "%s: norm must be 1 (layer) or 2 (rms)", who);
+  CORTEX_CHECK_ARG(gamma && (gamma_dtype == DT_F32 || gamma_dtype == DT_BF16), "%s: gamma must be fp32 or bf16", who);
+  CORTEX_CHECK_ARG(w_dtype == DT_BF16 || w_dtype == DT_I8, "%s: weight must be bf16 or int8", who);
+  CORTEX_CHECK_ARG(act == ACT_NONE || act == ACT_GELU, "%s: act must be 0 (none) or 1 (GELU)", who);
+  CORTEX_CHECK_ARG(out_dtype == DT_BF16 || out_dtype == DT_F32, "%s: out must be bf16 or fp32", who);
+  CORTEX_CHECK_ARG(x && w && out && eps >= 0.0f, "%s: null pointer or negative eps", who);
+  CORTEX_CHECK_ARG(ld_x >= K && ld_w >= K && ld_out >= N, "%s: row strides too small", who);
+  CORTEX_CHECK_ARG(aligned16(x) && ld_x % 8 == 0 && aligned16(w) && ld_w % (w_dtype == DT_I8 ? 16 : 8) == 0 &&
+                       aligned16(out) && ld_out % 8 == 0 && (!w_scale || aligned16(w_scale)) &&
+                       (!bias || aligned16(bias)) && aligned16(gamma) && (!beta || aligned16(beta)),
+                   "%s: operands must be 16-byte aligned rows", who);
+  NormGemmArgs a{M, N, K, reinterpret_cast<const bf16*>(x), ld_x, norm, gamma, norm == NORM_LAYER ? beta : nullptr,
+                 gamma_dtype, eps, w, ld_w, w_scale, bias, out, ld_out, 1};
+  int st;
+  const bool gelu = act == ACT_GELU, obf = out_dtype == DT_BF16;
+  if (w_dtype == DT_I8) {
+    st = obf ? (gelu ? dispatch_norm<int8_t, ACT_GELU, bf16>(a, stream) : dispatch_norm<int8_t, ACT_NONE, bf16>(a, stream))
+             : (gelu ? dispatch_norm<int8_t, ACT_GELU, float>(a, stream) : dispatch_norm<int8_t, ACT_NONE, float>(a, stream));
+  } else {
+    st = obf ? (gelu ? dispatch_norm<bf16, ACT_GELU, bf16>(a, stream) : dispatch_norm<bf16, ACT_NONE, bf16>(a, stream))
+             : (gelu ? dispatch_norm<bf16, ACT_GELU, float>(a, stream) : dispatch_norm<bf16, ACT_NONE, float>(a, stream));
   }
   if (st < 0) return st;
   if (st == 0) {

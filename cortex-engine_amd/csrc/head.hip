@@ -80,26 +80,9 @@ struct HeadArgs {
   float* out;      // (B, Q)
 };
 
-template <int CTRL>
-__device__ __forceinline__ float dpp_mov(float v) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
-}
-
-// Sum over the 64 lanes, in every lane: DPP adds inside each 16-lane row (quad xor 1,
-// quad xor 2, row rotate 4, row rotate 8), then the four row sums read out as scalars.
-// A few cycles per step instead of an LDS round trip per shuffle: the head runs one
-// wavefront per SIMD, with nothing else to hide reduction latency behind.
-__device__ __forceinline__ float hd_wave_sum(float v) {
-  v += dpp_mov<0xB1>(v);
-  v += dpp_mov<0x4E>(v);
-  v += dpp_mov<0x124>(v);
-  v += dpp_mov<0x128>(v);
-  const int iv = __builtin_bit_cast(int, v);
-  return (__builtin_bit_cast(float, __builtin_amdgcn_readlane(iv, 0)) +
-          __builtin_bit_cast(float, __builtin_amdgcn_readlane(iv, 16))) +
-         (__builtin_bit_cast(float, __builtin_amdgcn_readlane(iv, 32)) +
-          __builtin_bit_cast(float, __builtin_amdgcn_readlane(iv, 48)));
-}
+// The head runs one wavefront per SIMD, with nothing else to hide reduction latency behind:
+// its row sums use the DPP reduction (wave_sum_dpp), not LDS shuffles.
+__device__ __forceinline__ float hd_wave_sum(float v) { return wave_sum_dpp(v); }
 
 // LayerNorm parameters of one lane's EPL columns (k = (j / 4) * 256 + lane * 4 + j % 4)
 template <int EPL>

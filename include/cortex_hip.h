@@ -184,6 +184,22 @@ int cortex_norm_linear(int64_t M, int64_t N, int64_t K, int x_dtype, const void*
                        int64_t ld_res, int64_t res_rows, int out_dtype, void* out, int64_t ld_out,
                        hipStream_t stream);
 
+/* Norm + linear in ONE launch (rms_norm_linear, cortex/kernels/fused_rmsnorm.py:130-233 and
+ * :239-301, with QuantizedLinear's int8 weights, calibrate.py:170-235):
+ *   y[m, :]  = bf16( x[m, :] / sqrt(mean_k x[m, k]^2 + eps) * gamma )             (norm 2, RMS)
+ *            = bf16( (x[m, :] - mu) / sqrt(var + eps) * gamma + beta )             (norm 1, LayerNorm)
+ *   out[m, n] = act( (sum_k y[m, k] w[n, k]) * w_scale[n] + bias[n] )
+ * The row statistics are computed in the kernel's prologue from the x panel it stages in
+ * LDS (no stats pass, no normalised rows in HBM).  x (M, K) bf16 with K a multiple of 64 up
+ * to 512; w (N, K): w_dtype 1 bf16 or 3 int8 (widened exactly in the kernel); gamma/beta
+ * fp32 or bf16 (gamma_dtype, beta ignored for RMS, optional for LayerNorm); w_scale, bias
+ * optional fp32; act 0 or 1 (erf-GELU); out bf16 (1) or fp32 (0); N % 8 == 0; 16-byte
+ * aligned rows (ld_w % 16 for int8). */
+int cortex_norm_linear_fused(int64_t M, int64_t N, int64_t K, const void* x, int64_t ld_x, int norm,
+                             const void* gamma, const void* beta, int gamma_dtype, float eps, int w_dtype,
+                             const void* w, int64_t ld_w, const float* w_scale, const float* bias, int act,
+                             int out_dtype, void* out, int64_t ld_out, hipStream_t stream);
+
 /* ---- a3/a4/a5/a8: attention ------------------------------------------------
  * Replaces sparse_cross_attention (cortex/kernels/sparse_xattn.py:340-434) and
  * the scaled_dot_product_attention calls of CrossAttentionBlock

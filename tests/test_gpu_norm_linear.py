@@ -174,3 +174,105 @@ def test_transpose_bf16_exact(R, C):
     t = ops.transpose_bf16(w.to(DEV)).cpu()
     assert t.shape == (C, R) and t.is_contiguous()
     assert torch.equal(t.view(torch.int16), w.T.contiguous().view(torch.int16))
+
+
+def _exact_rows(M, K, seed):
+    """Rows x = c * s with s in {-1, +1}, c a power of two: with eps = 0 the RMS is |c| and
+    x / rms = s exactly, so the normalised row s * gamma is exact in bf16 (gamma bf16-valued)."""
+    g = torch.Generator().manual_seed(seed)
+    s = torch.randint(0, 2, (M, K), generator=g).float() * 2 - 1
+    c = 2.0 ** torch.randint(-3, 4, (M, 1), generator=g).float()
+    gam = (1 + 0.1 * torch.randn(K, generator=g)).bfloat16().float()
+    return (s * c).bfloat16(), s, gam
+
+
+@pytest.mark.parametrize("M,N,K,wform", [(8192, 1536, 512, "int8"), (8192, 512, 512, "int8"), (300, 200, 256, "int8"),
+                                         (1, 2048, 512, "int8"), (777, 1024, 448, "bf16"), (64, 64, 64, "bf16")])
+def test_fused_rms_linear_one_launch_exact_rows(M, N, K, wform):
+    """cortex_norm_linear_fused on rows whose normalisation is exact: fp32 output within 1e-5
+    of a float64 contraction of gamma * sign rows with the (widened) weight, scale and bias."""
+    from cortex.kernels import ops
+
+    x, sgn, gam = _exact_rows(M, K, seed=M + N + K)
+    g = torch.Generator().manual_seed(N)
+    w = torch.randn(N, K, generator=g) * 0.03
+    bias = torch.randn(N, generator=g) * 0.1
+    if wform == "int8":
+        q, s = O.quantize_int8(w.numpy())
+        wd, sd, wref = torch.from_numpy(q).to(DEV), torch.from_numpy(s).to(DEV), torch.from_numpy(O.dequantize(q, s))
+    else:
+        wd, sd, wref = w.bfloat16().to(DEV), None, w.bfloat16().float()
+    out = ops.norm_linear_fused(x.to(DEV), wd, sd, norm="rms", gamma=gam.to(DEV), eps=0.0, bias=bias.to(DEV),
+                                out_dtype=torch.float32)
+    ref = (sgn.double() * gam.double()) @ wref.double().T + bias.double()
+    assert out.shape == (M, N)
+    assert _rel_err(out.cpu(), ref) <= 1e-5
+
+
+@pytest.mark.parametrize("norm", ["rms", "layer"])
+@pytest.mark.parametrize("act", [None, "gelu"])
+def test_fused_norm_linear_vs_oracle(norm, act):
+    """The one-launch path with general rows: bf16 output against the normalised rows
+    rounded to bf16 (as the reference does) times the dequantised weight in float64; the
+    row statistics differ from torch's only in summation order, so a rounding of the
+    normalised row may flip by one bf16 step: within 2 bf16 steps of the output plus
+    1e-3 of the largest output everywhere, and within one step for 99 % of outputs."""
+    from cortex.kernels import ops
+
+    M, N, K = 1000, 768, 512
+    g = torch.Generator().manual_seed(11)
+    x = (torch.randn(M, K, generator=g) * 2 + 0.4).bfloat16()
+    gam = 1 + 0.05 * torch.randn(K, generator=g)
+    bet = 0.1 * torch.randn(K, generator=g)
+    w = torch.randn(N, K, generator=g) * 0.03
+    q, s = O.quantize_int8(w.numpy())
+    wdq = torch.from_numpy(O.dequantize(q, s)).double()
+    out = ops.norm_linear_fused(x.to(DEV), torch.from_numpy(q).to(DEV), torch.from_numpy(s).to(DEV), norm=norm,
+                                gamma=gam.to(DEV), beta=bet.to(DEV), eps=1e-6 if norm == "rms" else 1e-5, act=act)
+    xf = x.float()
+    if norm == "rms":
+        y = (xf / torch.sqrt(xf.pow(2).mean(-1, keepdim=True) + 1e-6)) * gam
+    else:
+        y = F.layer_norm(xf, (K,), gam, bet, 1e-5)
+    ref = y.bfloat16().double() @ wdq.T
+    if act == "gelu":
+        ref = F.gelu(ref)
+    got = out.double().cpu()
+    step = ref.abs() * 2.0 ** -8 + 1e-30
+    err = (got - ref).abs()
+    assert bool((err <= 2 * step + 1e-3 * float(ref.abs().max())).all()), float(err.max())
+    assert float((err <= step + 1e-5 * float(ref.abs().max())).float().mean()) >= 0.99
+
+
+def test_config2_is_one_launch_and_kn_weights_are_cached():
+    """Config 2 through the API: norm_linear_int8 and rms_norm_linear launch exactly one kernel
+    (the fused one, no norm rows or weight conversion), and the (K, N) weight's (N, K) rows
+    are rebuilt only when the weight changes in place."""
+    from cortex import _native as nat
+    from cortex.kernels import ops
+    from cortex.kernels.fused_rmsnorm import norm_linear_int8, rms_norm_linear
+
+    x, gam, q, s = _config2(1536)
+    xd, gd, qd, sd = x.to(DEV), gam.to(DEV), q.to(DEV), s.to(DEV)
+    names = []
+    real = nat.call
+
+    def spy(name, *a):
+        names.append(name)
+        return real(name, *a)
+    nat.call = spy
+    try:
+        norm_linear_int8(xd, qd, sd, norm="rms", gamma=gd, eps=1e-6)
+        assert names == ["cortex_norm_linear_fused"], names
+        w = (torch.randn(512, 1536) * 0.02).bfloat16().to(DEV)
+        names.clear()
+        a = rms_norm_linear(xd, gd, w)
+        b = rms_norm_linear(xd, gd, w)
+        assert names.count("cortex_norm_linear_fused") == 2 and names.count("cortex_transpose_bf16") == 1, names
+        torch.testing.assert_close(a, b, rtol=0, atol=0)
+        w.mul_(2)  # in place: the cached rows must follow
+        c = rms_norm_linear(xd, gd, w)
+        assert names.count("cortex_transpose_bf16") == 2, names
+        torch.testing.assert_close(c.float(), 2 * a.float(), rtol=1e-2, atol=1e-2)
+    finally:
+        nat.call = real
