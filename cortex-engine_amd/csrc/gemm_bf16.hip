@@ -29,6 +29,9 @@
 // an LDS round trip or a workgroup barrier.
 #include <hip/hip_runtime.h>
 
+#include <type_traits>
+#include <utility>
+
 #include "common.h"
 #include "gemm.h"
 
@@ -507,28 +510,6 @@ bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 //   C[m, n] = epi( sum_k y[m, k] W[n, k] ),  y = bf16( x / sqrt(mean(x^2) + eps) * gamma )   (RMS)
 //                                            y = bf16( (x - mu) / sqrt(var + eps) * gamma + beta ) (LN)
 //
-// A workgroup owns a panel of BM rows for all of K (K <= 512): the panel is transferred
-// into LDS once (swizzled 128-byte rows, one sub-panel per 64 K), each wavefront computes
-// the statistics of its rows from the staged values and writes the normalised bf16 rows
-// back in place, and the workgroup then walks its column tiles (tile g, g + G, ... of
-// the N / BN tiles) as one stream of (tile, K-step) steps, transferring only the weight,
-// direct to LDS, through an S-stage ring.  The int8 weight stays int8 in LDS (64-byte rows
-// per step, four stages) and each wavefront widens its fragments exactly after the LDS
-// read; a bf16 weight uses 128-byte rows (two stages).  The MFMA loop, the fragment
-// layouts and the register epilogue are those of gemm_bf16_kernel.
-template <int BM_, int BN_, int WM_, int WN_, int S8_, int S16_>
-struct NTile {
-  static constexpr int BM = BM_, BN = BN_, WM = WM_, WN = WN_, WAVES = WM * WN, THREADS = 64 * WAVES;
-  static constexpr int S8 = S8_, S16 = S16_;  // ring stages for int8 / bf16 weights
-  static constexpr int TM = BM / WM / 16, TN = BN / WN / 16;
-  static constexpr int KMAX = 512;
-  static constexpr int PANEL = BM * KMAX * 2;
-  static constexpr int LDS8 = PANEL + S8 * BN * 64, LDS16 = PANEL + S16 * BN * 128;
-  static_assert(TM >= 1 && TN >= 2 && TN % 2 == 0, "shape");
-  static_assert((BN * 64) % (1024 * WAVES) == 0, "transfer split");
-  static_assert(BM % 8 == 0 && LDS8 <= 160 * 1024 && LDS16 <= 160 * 1024, "LDS");
-};
-
 struct NormGemmArgs {
   int64_t M, N, K;
   const bf16* x;
@@ -547,20 +528,6 @@ struct NormGemmArgs {
   int groups;  // G: column-tile groups per row panel (gridDim.x)
 };
 
-// s_waitcnt vmcnt(n * PER) for a runtime n in [0, NMAX]
-template <int PER, int NMAX>
-__device__ __forceinline__ void wait_vm_steps(int n) {
-  if constexpr (NMAX > 0) {
-    if (n >= NMAX) {
-      wait_vm<(NMAX * PER < 63 ? NMAX * PER : 63)>();
-      return;
-    }
-    wait_vm_steps<PER, NMAX - 1>(n);
-  } else {
-    wait_vm<0>();
-  }
-}
-
 // Direct-to-LDS transfer of 16 bytes per lane (global_load_lds_dwordx4, LDS destination
 // lds_dst + 16 * lane) issued from inline assembly, so that the compiler does not treat
 // the LDS reads that follow as aliasing the transfer and wait for every transfer in
@@ -574,342 +541,399 @@ __device__ __forceinline__ void lds_dma16(const void* gsrc, void* lds_dst) {
   asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gsrc), "s"(m0) : "memory", "m0");
 }
 
-// 16-byte chunk swizzle of the 64-byte int8 weight rows: the 16 rows of a fragment read
-// (consecutive, or the interleaved order of wrow_of) land in 16 distinct four-bank groups.
-__device__ __forceinline__ int swz8(int r) { return ((r >> 3) ^ (r >> 2)) & 3; }
+// Register-resident rows.  Eight wavefronts (two per SIMD) on a 128-row panel for all of
+// K (K <= 512): wavefronts w and w + 4 share rows 32 (w % 4) .. + 31 and split every
+// 64-column tile between them (columns 16 (l / 16) + 8 (w / 4) + [0, 8) of lane l).
+// Each wavefront transfers half of its 32 rows into LDS (one 1 KiB row per transfer, full
+// cache lines), reads them in the MFMA operand layout, computes their statistics (a lane's
+// partial sums, then the four lanes that share a row), normalises them to bf16 in
+// registers and writes them back; it then reads its partner's normalised half, so every
+// row is normalised once per workgroup.  The rows stay in VGPRs while the workgroup walks
+// its column tiles.  Lane l holds row l % 16 of each 16-row group and, of each 64-wide K
+// step s, the slice 64 s + 16 (l / 16) + [0, 16): the two 8-value halves feed the two
+// 32-deep MFMAs of the step, and the weight fragments are read with the same slice, so
+// the contraction pairs the right k.  In the tile loop only the weight passes through
+// LDS, as bf16 rows: one whole 64 x K tile per buffer, two buffers, one barrier per tile,
+// the fragments of K step s + 1 read while step s multiplies.  A bf16 weight is
+// transferred direct to LDS; an int8 weight is loaded into registers during the previous
+// tile's multiplications, widened exactly and written as bf16 rows (once per workgroup).
+// The first tile comes through registers (its loads overlap the normalisation, whose
+// staging area the tile buffers reuse).  The tile's scales and biases ride along in a
+// 1 KiB transfer.
+//
+// LDS rows (the staged x rows and the weight rows) are 1024 + 16 bytes apart, so the 16
+// consecutive rows one fragment read touches start in 16 different four-bank groups and
+// every read address is a per-lane base plus a compile-time offset.
+//
+// Output columns: LDS weight row 16 f + i (fragment f, fragment row i) holds column
+// 16 (i / 4) + 8 (f / 2) + 4 (f % 2) + i % 4 of the tile, so lane l of wavefront w ends
+// with the eight consecutive columns 16 (l / 16) + 8 (w / 4) + [0, 8) of its row (one
+// 16-byte bf16 store).  Rows past M read row M - 1 and column groups past N read the last
+// eight columns, so every lane computes a valid output and stores it: duplicates are
+// bit-identical, and each tile issues a fixed number of stores, which the next tile's
+// vmcnt wait counts exactly.
+struct RTile {
+  static constexpr int RG = 2, WAVES = 8, THREADS = 512, BM = 128, BN = 64, KMAX = 512;
+  static constexpr int RP = KMAX * 2 + 16;  // LDS bytes from one bf16 row to the next
+  static constexpr int W_TILE = BN * RP;
+  static constexpr int XS = BM * RP;        // the panel's rows, staged once (aliases the tiles)
+  static constexpr int SB = 1024, GB = 2 * KMAX * 4;
+  static constexpr int BODY = XS > 2 * W_TILE ? XS : 2 * W_TILE;
+  static constexpr int LDS = BODY + 2 * SB + GB;
+  static_assert(LDS <= 160 * 1024 && 16 * 3 * RP + 128 * 7 + 16 < 65536, "LDS");
+};
 
-template <class TL, class TW, int ACT, class TOUT>
-__global__ __launch_bounds__(TL::THREADS) void norm_gemm_kernel(NormGemmArgs g) {
-  constexpr int BM = TL::BM, BN = TL::BN, TM = TL::TM, TN = TL::TN, WAVES = TL::WAVES;
-  constexpr bool WI8 = sizeof(TW) == 1;
-  constexpr bool IL = sizeof(TOUT) == 2;  // bf16 out: interleaved W rows, 8 consecutive columns per lane
-  constexpr int S = WI8 ? TL::S8 : TL::S16;
-  constexpr int ROWB = WI8 ? 64 : 128;            // weight bytes per row and step (64 K)
-  constexpr int W_STAGE = BN * ROWB;
-  constexpr int WB = W_STAGE / 1024 / WAVES;      // 1 KiB transfers per wavefront and step
-  constexpr int RPB = 1024 / ROWB;                // rows per transfer: 16 or 8
-  static_assert(W_STAGE % (1024 * WAVES) == 0 && WB * S < 64, "weight transfer split");
-  __shared__ __attribute__((aligned(1024))) unsigned char smem[WI8 ? TL::LDS8 : TL::LDS16];
-  unsigned char* const panel = smem;                  // K / 64 sub-panels of BM x 128 bytes
-  unsigned char* const wring = smem + TL::PANEL;
-  auto sub = [&](int kt) { return panel + kt * (BM * 128); };
-  auto w_stage = [&](int s) { return wring + s * W_STAGE; };
-  auto wsw = [&](int r) { return WI8 ? swz8(r) : (IL ? swz_w(r) : swz_a(r)); };
+// global weight row held by LDS row R of the tile at column n0 (see the column order above)
+__device__ __forceinline__ int rk_wrow(int R, int n0, int N) {
+  const int f = R >> 4, i = R & 15;
+  return min(n0 + 16 * (i >> 2) + 8 * (f >> 1), N - 8) + 4 * (f & 1) + (i & 3);
+}
+
+// f(integral_constant<int, 0>) ... f(integral_constant<int, N - 1>): indices that are
+// constants when the code is generated (register arrays indexed this way stay in VGPRs)
+template <class F, int... I>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ bf16x2_t pair_of(const bf16x8& v, int d) {
+  switch (d) {
+    case 0: return __builtin_shufflevector(v, v, 0, 1);
+    case 1: return __builtin_shufflevector(v, v, 2, 3);
+    case 2: return __builtin_shufflevector(v, v, 4, 5);
+    default: return __builtin_shufflevector(v, v, 6, 7);
+  }
+}
+
+template <int NORM, class TW, int ACT, class TOUT>
+__global__ __launch_bounds__(512) void norm_gemm_rk_kernel(NormGemmArgs g) {
+  using TL = RTile;
+  constexpr int BN = TL::BN, RP = TL::RP;
+  constexpr bool WI8 = sizeof(TW) == 1, OBF = sizeof(TOUT) == 2;
+  constexpr int EPI = 2 * (OBF ? 1 : 2);  // global stores per lane per tile
+  constexpr int NW0 = WI8 ? 4 : 8;        // 16-byte register loads per lane of one weight tile
+  __shared__ __attribute__((aligned(1024))) unsigned char smem[TL::LDS];
+  auto wbuf = [&](int b) { return smem + b * TL::W_TILE; };
+  auto sbuf = [&](int b) { return smem + TL::BODY + b * TL::SB; };
+  unsigned char* const gbuf = smem + TL::BODY + 2 * TL::SB;  // fp32 gamma at 0, beta at KMAX * 4
 
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
-  const int M = (int)g.M, N = (int)g.N, K = (int)g.K;
-  const int nk = K / 64;
-  // row panel per blockIdx.y, column-tile group per blockIdx.x; the groups of one panel
-  // sit on one XCD (the panel's rows in one L2)
+  const int pr = wid & 3, c2 = wid >> 2;  // row pair (rows 32 pr ..) and column half
+  const int M = (int)g.M, N = (int)g.N, K = (int)g.K, nk = K / 64;
   const int G = gridDim.x, total = gridDim.x * gridDim.y;
   const int id = xcd_affine(blockIdx.x + G * blockIdx.y, total);
-  const int m0 = (id / G) * BM, grp = id % G;
+  const int m0 = (id / G) * TL::BM, grp = id % G;
   const int ntiles = (N + BN - 1) / BN;
-  const int my_tiles = grp < ntiles ? (ntiles - 1 - grp) / G + 1 : 0;
-  const int nsteps = my_tiles * nk;
+  const int nt = grp < ntiles ? (ntiles - 1 - grp) / G + 1 : 0;
+  if (nt == 0) return;  // uniform over the workgroup
+  const int j16 = lane & 15, q = lane >> 4;
+  const unsigned ldb = (unsigned)(g.ld_w * (int64_t)sizeof(TW));  // N * ldb < 2^31 (checked by the host)
 
-  // weight rows of step j (tile grp + (j / nk) G, K step j % nk) into stage j % S: lane i of
-  // a transfer writes row i / (ROWB / 16), physical chunk i % (ROWB / 16), which holds the
-  // logical chunk (i % (ROWB / 16)) ^ swizzle(row)
-  auto issue = [&](int j) {
-    const int n0 = (grp + (j / nk) * G) * BN, k0 = (j % nk) * 64, s = j % S;
-    constexpr int CPR = ROWB / 16;
-#pragma unroll
-    for (int i = 0; i < WB; ++i) {
-      const int r = (wid * WB + i) * RPB + lane / CPR;
-      const int lc = (lane % CPR) ^ wsw(r);
-      const TW* src = reinterpret_cast<const TW*>(g.w) + (int64_t)min(n0 + r, N - 1) * g.ld_w + k0 +
-                      lc * (16 / (int)sizeof(TW));
-      lds_dma16(src, w_stage(s) + (wid * WB + i) * 1024);
+  // the tile's scales and biases: lanes 0-15 scale, 16-31 bias, 4 columns each (wavefront 0)
+  auto issue_sb = [&](int i, int b) {
+    if (wid == 0) {
+      const int n0 = (grp + i * G) * BN;
+      const float* base = (lane & 16) ? g.bias : g.w_scale;
+      const float* src = base ? base + min(n0 + 4 * (lane & 15), N - 4) : reinterpret_cast<const float*>(g.w);
+      lds_dma16(src, sbuf(b));
     }
   };
+  // bf16 weight direct to LDS: 8 rows (1 KiB each) per wavefront
+  auto issue_w16 = [&](int i, int b) {
+    const int n0 = (grp + i * G) * BN;
+    const unsigned char* wl = reinterpret_cast<const unsigned char*>(g.w) + min(lane, K / 8 - 1) * 16;
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      const int R = 8 * wid + t;
+      lds_dma16(wl + (unsigned)rk_wrow(R, n0, N) * ldb, wbuf(b) + R * RP);
+    }
+  };
+  // a weight tile through registers: bf16, one row per load (lane: 16-byte chunk); int8, two
+  // rows per load (lane / 32 the row, lane % 32 the chunk of 16 values, widened on the store)
+  typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+  u32x4 wr[NW0];  // a native vector type: a HIP uint4 array here ends up in scratch
+  auto wreg_row = [&](int t) { return WI8 ? 8 * wid + 2 * t + (lane >> 5) : 8 * wid + t; };
+  auto load_wreg = [&](int i) {
+    const int n0 = (grp + i * G) * BN;
+    const int c = WI8 ? min(lane & 31, K / 16 - 1) : min(lane, K / 8 - 1);
+    const unsigned char* wl = reinterpret_cast<const unsigned char*>(g.w) + c * 16;
+    static_for<NW0>([&](auto t) {
+      wr[t] = *reinterpret_cast<const u32x4*>(wl + (unsigned)rk_wrow(wreg_row(t), n0, N) * ldb);
+    });
+  };
+  auto store_wreg = [&](int b) {
+    static_for<NW0>([&](auto t) {
+      unsigned char* d = wbuf(b) + wreg_row(t) * RP;
+      if constexpr (WI8) {
+        d += (lane & 31) * 32;
+        *reinterpret_cast<bf16x8*>(d) = widen_i8x8(make_uint2(wr[t][0], wr[t][1]));
+        *reinterpret_cast<bf16x8*>(d + 16) = widen_i8x8(make_uint2(wr[t][2], wr[t][3]));
+      } else {
+        *reinterpret_cast<u32x4*>(d + lane * 16) = wr[t];
+      }
+    });
+  };
 
-  // ---- prologue: the whole panel into LDS (sub-panel kt, 1 KiB blocks of 8 rows), this
-  // lane's gamma / beta columns, then the first S weight steps (in flight during the norm)
+  // ---- prologue: tile 0's weight into registers and its scales into LDS, this wavefront's
+  // 16 rows (rows 32 pr + 16 c2 ..) into LDS, gamma / beta
+  load_wreg(0);
+  issue_sb(0, 0);
+  const int own = 32 * pr + 16 * c2;  // first staged row of this wavefront
   {
-    constexpr int BLK_PER_SUB = BM / 8;
-    const int nblk = BLK_PER_SUB * nk;
-    for (int b = wid; b < nblk; b += WAVES) {
-      const int kt = b / BLK_PER_SUB, r = (b % BLK_PER_SUB) * 8 + (lane >> 3);
-      const bf16* src = g.x + (int64_t)min(m0 + r, M - 1) * g.ld_x + kt * 64 + ((lane & 7) ^ swz_a(r)) * 8;
-      lds_dma16(src, sub(kt) + (b % BLK_PER_SUB) * 1024);
+    const bf16* xl = g.x + min(lane, K / 8 - 1) * 8;
+#pragma unroll
+    for (int t = 0; t < 16; ++t) lds_dma16(xl + (int64_t)min(m0 + own + t, M - 1) * g.ld_x, smem + (own + t) * RP);
+    // gamma / beta: fp32 straight into gbuf; bf16 into tile 1's scale area, widened below
+    const bool gbf = g.gamma_dtype == DT_BF16;
+    const int esz = gbf ? 2 : 4;
+    const int nb = esz * TL::KMAX / 1024;  // 1 KiB blocks per vector: 1 or 2
+    if (wid < 2 * nb) {
+      const int which = wid / nb, blk = wid % nb;
+      const void* base = (which && g.beta) ? g.beta : g.gamma;
+      const int c = min(blk * 64 + lane, K * esz / 16 - 1);
+      unsigned char* dst = gbf ? sbuf(1) + which * 1024 : gbuf + which * (TL::KMAX * 4) + blk * 1024;
+      lds_dma16(reinterpret_cast<const unsigned char*>(base) + c * 16, dst);
     }
   }
-  constexpr int CPL = TL::KMAX / 8 / 64;  // 16-byte chunks per lane at the largest K
-  float gm[CPL][8], bt[CPL][8];
+  wait_vm<0>();  // this wavefront's rows, tile 0's weight and scales, its gamma / beta block
+  // a[0]: this wavefront's own 16 rows (normalised here), a[1]: its partner's 16 rows
+  const int other = 32 * pr + 16 * (1 - c2);
+  bf16x8 a[2][8][2];
+  const unsigned char* xo = smem + (own + j16) * RP + 32 * q;
+  bf16x8 (&mine)[8][2] = a[0];
   {
-    const int nch = K / 8;
-    auto ld8 = [&](const void* p, int c, float (&dst)[8]) {
-      if (g.gamma_dtype == DT_BF16) {
-        const bf16x8 t = *reinterpret_cast<const bf16x8*>(reinterpret_cast<const bf16*>(p) + c * 8);
+    bf16x8 (&v)[8][2] = mine;  // raw rows, normalised in place
 #pragma unroll
-        for (int j = 0; j < 8; ++j) dst[j] = (float)t[j];
-      } else {
-        const float4 a = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(p) + c * 8);
-        const float4 b = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(p) + c * 8 + 4);
-        dst[0] = a.x; dst[1] = a.y; dst[2] = a.z; dst[3] = a.w;
-        dst[4] = b.x; dst[5] = b.y; dst[6] = b.z; dst[7] = b.w;
-      }
-    };
+    for (int s = 0; s < 8; ++s)
 #pragma unroll
-    for (int i = 0; i < CPL; ++i) {
-      const int c = min(lane + 64 * i, nch - 1);  // lanes past K repeat a valid chunk (unused)
-      ld8(g.gamma, c, gm[i]);
-      if (g.beta) {
-        ld8(g.beta, c, bt[i]);
-      } else {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) bt[i][j] = 0.0f;
-      }
-    }
-  }
-  wait_vm<0>();  // the panel and gamma / beta (the weights are issued after: not waited for)
-#pragma unroll
-  for (int p = 0; p < S; ++p)
-    if (p < nsteps) issue(p);
-  __builtin_amdgcn_s_barrier();
-  // ---- statistics and normalisation in place: wavefront w takes NR rows at a time
-  // (rows w NR .. w NR + NR - 1, then + WAVES NR ...; NR independent reductions in flight);
-  // lane l the 16-byte chunks c = l, l + 64, ... (chunk c: sub-panel c / 8, logical chunk c % 8)
-  {
-    constexpr int NR = 8;
-    static_assert(BM % (WAVES * NR) == 0, "rows per wavefront");
-    const int nch = K / 8;
+      for (int h = 0; h < 2; ++h) v[s][h] = *reinterpret_cast<const bf16x8*>(xo + s * 128 + h * 16);
+    // statistics: a lane's partial sums over its 8 x 16 values, then the four lanes of the
+    // row (l, l ^ 16, l ^ 32, l ^ 48)
     const float fk = (float)K;  // means as sum / K, as torch's mean
-    for (int r0 = wid * NR; r0 < BM; r0 += WAVES * NR) {
-      float v[NR][CPL][8];
-      float s1[NR], mu[NR], inv[NR];
-      // every read first (lanes past K read a valid chunk and drop it), then the sums
-      bf16x8 raw[NR][CPL];
+    const bf16x2_t ones = {(__bf16)1.0f, (__bf16)1.0f};
+    float p[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-      for (int q = 0; q < NR; ++q)
+    for (int s = 0; s < 8; ++s) {
+      if (s < nk) {
 #pragma unroll
-        for (int i = 0; i < CPL; ++i) {
-          const int r = r0 + q, c = min(lane + 64 * i, nch - 1);
-          raw[q][i] = *reinterpret_cast<const bf16x8*>(sub(c >> 3) + r * 128 + (((c & 7) ^ swz_a(r)) << 4));
-        }
+        for (int h = 0; h < 2; ++h)
 #pragma unroll
-      for (int q = 0; q < NR; ++q) {
-        s1[q] = 0.0f;
-#pragma unroll
-        for (int i = 0; i < CPL; ++i) {
-          const bool ok = lane + 64 * i < nch;
-#pragma unroll
-          for (int j = 0; j < 8; ++j) v[q][i][j] = ok ? (float)raw[q][i][j] : 0.0f;
-#pragma unroll
-          for (int j = 0; j < 8; ++j) s1[q] += (g.norm == NORM_RMS) ? v[q][i][j] * v[q][i][j] : v[q][i][j];
-        }
+          for (int d = 0; d < 4; ++d) {
+            const bf16x2_t xv = pair_of(v[s][h], d);
+            // sum of squares (RMS) or sum (LayerNorm): bf16 products are exact in fp32
+            p[d] = __builtin_amdgcn_fdot2_f32_bf16(xv, NORM == NORM_RMS ? xv : ones, p[d], false);
+          }
       }
+    }
+    float s1 = (p[0] + p[1]) + (p[2] + p[3]);
+    s1 += __shfl_xor(s1, 16, 64);
+    s1 += __shfl_xor(s1, 32, 64);
+    float mu = 0.0f, inv;
+    if constexpr (NORM == NORM_RMS) {
+      inv = 1.0f / sqrtf(s1 / fk + g.eps);
+    } else {
+      mu = s1 / fk;
+      float s2[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-      for (int q = 0; q < NR; ++q) s1[q] = wave_sum_dpp(s1[q]);
-      if (g.norm == NORM_RMS) {
+      for (int s = 0; s < 8; ++s) {
+        if (s < nk) {
 #pragma unroll
-        for (int q = 0; q < NR; ++q) {
-          mu[q] = 0.0f;
-          inv[q] = 1.0f / sqrtf(s1[q] / fk + g.eps);
-        }
-      } else {
-        float s2[NR];
+          for (int h = 0; h < 2; ++h)
 #pragma unroll
-        for (int q = 0; q < NR; ++q) {
-          mu[q] = s1[q] / fk;
-          s2[q] = 0.0f;
-#pragma unroll
-          for (int i = 0; i < CPL; ++i) {
-            const bool ok = lane + 64 * i < nch;
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-              const float d = ok ? v[q][i][j] - mu[q] : 0.0f;
-              s2[q] += d * d;
+            for (int e = 0; e < 8; ++e) {
+              const float d0 = (float)v[s][h][e] - mu;
+              s2[e & 3] = fmaf(d0, d0, s2[e & 3]);
             }
-          }
-        }
-#pragma unroll
-        for (int q = 0; q < NR; ++q) inv[q] = 1.0f / sqrtf(wave_sum_dpp(s2[q]) / fk + g.eps);
-      }
-#pragma unroll
-      for (int q = 0; q < NR; ++q) {
-        const int r = r0 + q;
-#pragma unroll
-        for (int i = 0; i < CPL; ++i) {
-          const int c = lane + 64 * i;
-          if (c < nch) {
-            bf16x8 t;
-#pragma unroll
-            for (int j = 0; j < 8; ++j) t[j] = (bf16)fmaf((v[q][i][j] - mu[q]) * inv[q], gm[i][j], bt[i][j]);
-            *reinterpret_cast<bf16x8*>(sub(c >> 3) + r * 128 + (((c & 7) ^ swz_a(r)) << 4)) = t;
-          }
         }
       }
+      float t2 = (s2[0] + s2[1]) + (s2[2] + s2[3]);
+      t2 += __shfl_xor(t2, 16, 64);
+      t2 += __shfl_xor(t2, 32, 64);
+      inv = 1.0f / sqrtf(t2 / fk + g.eps);
     }
-  }
-
-  // ---- column tiles: the (tile, K step) sequence as one stream of steps
-  const int wm = wid / TL::WN, wn = wid % TL::WN;
-  const int fr = lane & 15, g4 = lane >> 4;
-  const int wrow = wm * (BM / TL::WM), wcol = wn * (BN / TL::WN);
-  int a_off[TM], a_sw[TM], w_off[TN], w_sw[TN];
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    __builtin_amdgcn_s_barrier();  // gamma / beta of every wavefront landed
+    if (g.gamma_dtype == DT_BF16) {
+      for (int e = tid; e < 2 * TL::KMAX; e += TL::THREADS)
+        reinterpret_cast<float*>(gbuf)[e] = (float)reinterpret_cast<const bf16*>(sbuf(1))[e];
+      __builtin_amdgcn_s_waitcnt(0xC07F);
+      __builtin_amdgcn_s_barrier();
+    }
+    // normalise: y = bf16((x - mu) inv gamma + beta); K steps past K are 0; back to LDS
 #pragma unroll
-  for (int t = 0; t < TM; ++t) {
-    const int r = wrow + t * 16 + fr;
-    a_off[t] = r * 128;
-    a_sw[t] = swz_a(r);
-  }
+    for (int s = 0; s < 8; ++s) {
+      if (s < nk) {
+        float gm[16], bt[16];
+        const unsigned char* gp = gbuf + (64 * s + 16 * q) * 4;
 #pragma unroll
-  for (int t = 0; t < TN; ++t) {
-    const int r = wcol + (IL ? wrow_of(t >> 1, t & 1, fr) : t * 16 + fr);
-    w_off[t] = r * ROWB;
-    w_sw[t] = wsw(r);
-  }
-  auto read_frags = [&](int j, int ks, bf16x8 (&af)[TM], bf16x8 (&wf)[TN]) {
-    const unsigned char* as = sub(j % nk);
-    const unsigned char* ws = w_stage(j % S);
+        for (int c = 0; c < 4; ++c) {
+          const float4 g4 = *reinterpret_cast<const float4*>(gp + 16 * c);
+          gm[4 * c] = g4.x; gm[4 * c + 1] = g4.y; gm[4 * c + 2] = g4.z; gm[4 * c + 3] = g4.w;
+          if constexpr (NORM != NORM_RMS) {
+            const float4 b4 = *reinterpret_cast<const float4*>(gp + TL::KMAX * 4 + 16 * c);
+            const bool hb = g.beta != nullptr;
+            bt[4 * c] = hb ? b4.x : 0.0f;
+            bt[4 * c + 1] = hb ? b4.y : 0.0f;
+            bt[4 * c + 2] = hb ? b4.z : 0.0f;
+            bt[4 * c + 3] = hb ? b4.w : 0.0f;
+          }
+        }
 #pragma unroll
-    for (int t = 0; t < TM; ++t) af[t] = *reinterpret_cast<const bf16x8*>(as + a_off[t] + (((ks * 4 + g4) ^ a_sw[t]) << 4));
+        for (int h = 0; h < 2; ++h)
 #pragma unroll
-    for (int t = 0; t < TN; ++t) {
-      if constexpr (WI8) {  // K slice [32 ks + 8 g4, +8): half (g4 & 1) of logical chunk 2 ks + g4 / 2
-        const uint2 raw = *reinterpret_cast<const uint2*>(ws + w_off[t] + (((2 * ks + (g4 >> 1)) ^ w_sw[t]) << 4) +
-                                                          (g4 & 1) * 8);
-        wf[t] = widen_i8x8(raw);
+          for (int e = 0; e < 8; ++e) {
+            const float xv = (float)v[s][h][e];
+            if constexpr (NORM == NORM_RMS)
+              mine[s][h][e] = (bf16)((xv * inv) * gm[8 * h + e]);
+            else
+              mine[s][h][e] = (bf16)fmaf((xv - mu) * inv, gm[8 * h + e], bt[8 * h + e]);
+          }
       } else {
-        wf[t] = *reinterpret_cast<const bf16x8*>(ws + w_off[t] + (((ks * 4 + g4) ^ w_sw[t]) << 4));
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) mine[s][h][e] = (bf16)0.0f;
       }
+#pragma unroll
+      for (int h = 0; h < 2; ++h) *reinterpret_cast<bf16x8*>(const_cast<unsigned char*>(xo) + s * 128 + h * 16) = mine[s][h];
     }
-  };
-  f32x4 acc[TM][TN];
+  }
+  __builtin_amdgcn_s_waitcnt(0xC07F);
+  __builtin_amdgcn_s_barrier();  // every wavefront's normalised rows in LDS
+  {
+    bf16x8 (&theirs)[8][2] = a[1];
+    const unsigned char* xp = smem + (other + j16) * RP + 32 * q;
 #pragma unroll
-  for (int i = 0; i < TM; ++i)
+    for (int s = 0; s < 8; ++s)
 #pragma unroll
-    for (int j = 0; j < TN; ++j) acc[i][j] = (f32x4){0, 0, 0, 0};
-  auto mma = [&](const bf16x8 (&af)[TM], const bf16x8 (&wf)[TN]) {
-#pragma unroll
-    for (int i = 0; i < TM; ++i)
-#pragma unroll
-      for (int j = 0; j < TN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf[j], af[i], acc[i][j], 0, 0, 0);
-  };
-  auto epilogue = [&](int n0) {
-    constexpr int NV = IL ? 8 : 4, NG = IL ? TN / 2 : TN;
-    // every scale and bias load first (columns clamped into range, so no load is skipped
-    // and none is left in flight past the epilogue), then one wait, then the stores
-    float sca[NG][NV], bia[NG][NV];
-#pragma unroll
-    for (int p = 0; p < NG; ++p) {
-      const int n = min(n0 + wcol + (IL ? 32 * p + 8 * g4 : 16 * p + 4 * g4), N - NV);
-#pragma unroll
-      for (int h = 0; h < NV / 4; ++h) {
-        const float4 s4 = g.w_scale ? *reinterpret_cast<const float4*>(g.w_scale + n + 4 * h) : make_float4(1.f, 1.f, 1.f, 1.f);
-        const float4 b4 = g.bias ? *reinterpret_cast<const float4*>(g.bias + n + 4 * h) : make_float4(0.f, 0.f, 0.f, 0.f);
-        sca[p][4 * h] = s4.x; sca[p][4 * h + 1] = s4.y; sca[p][4 * h + 2] = s4.z; sca[p][4 * h + 3] = s4.w;
-        bia[p][4 * h] = b4.x; bia[p][4 * h + 1] = b4.y; bia[p][4 * h + 2] = b4.z; bia[p][4 * h + 3] = b4.w;
-      }
-    }
-    wait_vm<0>();
-#pragma unroll
-    for (int p = 0; p < NG; ++p) {
-      const int n = n0 + wcol + (IL ? 32 * p + 8 * g4 : 16 * p + 4 * g4);
-      if (n >= N) continue;  // N % 8 == 0: a lane's columns are all in or all out
-      const float* sc = sca[p];
-      const float* bi = bia[p];
-#pragma unroll
-      for (int i = 0; i < TM; ++i) {
-        const int m = m0 + wrow + i * 16 + fr;
-        if (m >= M) continue;
-        float v[NV];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          if constexpr (IL) {
-            v[r] = acc[i][2 * p][r] * sc[r] + bi[r];
-            v[4 + r] = acc[i][2 * p + 1][r] * sc[4 + r] + bi[4 + r];
-          } else {
-            v[r] = acc[i][p][r] * sc[r] + bi[r];
-          }
-        }
-        if (ACT == ACT_GELU) {
-#pragma unroll
-          for (int e = 0; e < NV; ++e) v[e] = IL ? gelu_erf_bf16out(v[e]) : gelu_erf(v[e]);
-        }
-        TOUT* op = reinterpret_cast<TOUT*>(g.out) + (int64_t)m * g.ld_out + n;
-        if constexpr (IL) {
-          bf16x8 o;
-#pragma unroll
-          for (int e = 0; e < 8; ++e) o[e] = (bf16)v[e];
-          *reinterpret_cast<bf16x8*>(op) = o;
-        } else {
-          *reinterpret_cast<float4*>(op) = make_float4(v[0], v[1], v[2], v[3]);
-        }
-      }
-    }
-  };
+      for (int h = 0; h < 2; ++h) theirs[s][h] = *reinterpret_cast<const bf16x8*>(xp + s * 128 + h * 16);
+  }
+  __builtin_amdgcn_s_waitcnt(0xC07F);
+  __builtin_amdgcn_s_barrier();  // the staged rows are dead: the tile buffers may overwrite them
+  store_wreg(0);
 
-  // Every stage in flight; a stage is refilled as soon as all wavefronts hold its last
-  // fragments in registers (as gemm_bf16_kernel).  A step's wait counts only weight
-  // transfers after it; epilogue loads and stores issued in between make it wait longer,
-  // never shorter (vector-memory operations complete in order).
-  bf16x8 af0[TM], wf0[TN], af1[TM], wf1[TN];
-  if (nsteps > 0) wait_vm_steps<WB, S - 1>(min(S, nsteps) - 1);  // step 0 landed
-  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the normalised rows are stored
-  __builtin_amdgcn_s_barrier();        // ... and visible with step 0 to every wavefront
-  if (nsteps > 0) read_frags(0, 0, af0, wf0);
-  for (int j = 0; j < nsteps; ++j) {
-    read_frags(j, 1, af1, wf1);
-    mma(af0, wf0);
-    if (j + 1 < nsteps) {
-      __builtin_amdgcn_s_waitcnt(0xC07F);  // this wave's reads of stage j % S are in registers
-      wait_vm_steps<WB, S - 1>(min(j + S - 1, nsteps - 1) - (j + 1));  // step j+1 landed
-      __builtin_amdgcn_s_barrier();        // all waves done with stage j % S; step j+1 visible
-      if (j + S < nsteps) issue(j + S);    // refill stage j % S
-      read_frags(j + 1, 0, af0, wf0);
+  // ---- column tiles
+  for (int i = 0; i < nt; ++i) {
+    const int n0 = (grp + i * G) * BN, b = i & 1;
+    if constexpr (!WI8) {
+      if (i > 0) wait_vm<EPI>();  // tile i's transfers: only the previous tile's stores were issued after them
     }
-    mma(af1, wf1);
-    if (j % nk == nk - 1) {  // last K step of a tile: its epilogue, then a fresh accumulator
-      epilogue((grp + (j / nk) * G) * BN);
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wavefront's LDS reads and writes done
+    __builtin_amdgcn_s_barrier();        // tile i visible; buffer b ^ 1 free (tile i - 1 done)
+    if (i + 1 < nt) {
+      issue_sb(i + 1, b ^ 1);
+      if constexpr (WI8)
+        load_wreg(i + 1);
+      else
+        issue_w16(i + 1, b ^ 1);
+    }
+
+    const unsigned char* wb = wbuf(b) + (32 * c2 + j16) * RP + 32 * q;  // fragments 2 c2, 2 c2 + 1
+    f32x4 acc[2][2];
 #pragma unroll
-      for (int i = 0; i < TM; ++i)
+    for (int r = 0; r < 2; ++r)
 #pragma unroll
-        for (int t = 0; t < TN; ++t) acc[i][t] = (f32x4){0, 0, 0, 0};
+      for (int f = 0; f < 2; ++f) acc[r][f] = (f32x4){0, 0, 0, 0};
+    bf16x8 cur[2][2], nxt[2][2];
+#pragma unroll
+    for (int f = 0; f < 2; ++f)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) cur[f][h] = *reinterpret_cast<const bf16x8*>(wb + f * 16 * RP + h * 16);
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      if (s + 1 < 8) {
+#pragma unroll
+        for (int f = 0; f < 2; ++f)
+#pragma unroll
+          for (int h = 0; h < 2; ++h)
+            nxt[f][h] = *reinterpret_cast<const bf16x8*>(wb + f * 16 * RP + (s + 1) * 128 + h * 16);
+      }
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int f = 0; f < 2; ++f)
+#pragma unroll
+          for (int r = 0; r < 2; ++r)
+            acc[r][f] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(cur[f][h], a[r][s][h], acc[r][f], 0, 0, 0);
+      if (s + 1 < 8) {
+#pragma unroll
+        for (int f = 0; f < 2; ++f)
+#pragma unroll
+          for (int h = 0; h < 2; ++h) cur[f][h] = nxt[f][h];
+      }
+    }
+    if constexpr (WI8) {
+      if (i + 1 < nt) {
+        wait_vm<0>();  // the next tile's int8 rows and scales (issued before this tile's multiplications)
+        store_wreg(b ^ 1);
+      }
+    }
+
+    // ---- epilogue: scale, bias (from the tile's LDS copy), activation, stores
+    const unsigned char* sb = sbuf(b);
+    const int cs = min(n0 + 16 * q + 8 * c2, N - 8), lc = cs - n0;
+    float sc[8], bi[8];
+    {
+      const float4 s0 = *reinterpret_cast<const float4*>(sb + 4 * lc), s1 = *reinterpret_cast<const float4*>(sb + 4 * lc + 16);
+      const float4 b0 = *reinterpret_cast<const float4*>(sb + 256 + 4 * lc), b1 = *reinterpret_cast<const float4*>(sb + 256 + 4 * lc + 16);
+      const bool hs = g.w_scale != nullptr, hb = g.bias != nullptr;
+      sc[0] = hs ? s0.x : 1.f; sc[1] = hs ? s0.y : 1.f; sc[2] = hs ? s0.z : 1.f; sc[3] = hs ? s0.w : 1.f;
+      sc[4] = hs ? s1.x : 1.f; sc[5] = hs ? s1.y : 1.f; sc[6] = hs ? s1.z : 1.f; sc[7] = hs ? s1.w : 1.f;
+      bi[0] = hb ? b0.x : 0.f; bi[1] = hb ? b0.y : 0.f; bi[2] = hb ? b0.z : 0.f; bi[3] = hb ? b0.w : 0.f;
+      bi[4] = hb ? b1.x : 0.f; bi[5] = hb ? b1.y : 0.f; bi[6] = hb ? b1.z : 0.f; bi[7] = hb ? b1.w : 0.f;
+    }
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const int m = min(m0 + (r ? other : own) + j16, M - 1);
+      float v[8];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        v[e] = acc[r][0][e] * sc[e] + bi[e];
+        v[4 + e] = acc[r][1][e] * sc[4 + e] + bi[4 + e];
+      }
+      if (ACT == ACT_GELU) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = OBF ? gelu_erf_bf16out(v[e]) : gelu_erf(v[e]);
+      }
+      TOUT* op = reinterpret_cast<TOUT*>(g.out) + (int64_t)m * g.ld_out + cs;
+      if constexpr (OBF) {
+        bf16x8 o;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[e] = (bf16)v[e];
+        *reinterpret_cast<bf16x8*>(op) = o;
+      } else {
+        *reinterpret_cast<float4*>(op) = make_float4(v[0], v[1], v[2], v[3]);
+        *reinterpret_cast<float4*>(op + 4) = make_float4(v[4], v[5], v[6], v[7]);
+      }
     }
   }
 }
 
-using N128x128 = NTile<128, 128, 2, 4, 4, 2>;
-using N64x128 = NTile<64, 128, 2, 4, 8, 6>;
-using N64x256 = NTile<64, 256, 2, 4, 6, 3>;
-
-template <class TL, class TW, int ACT, class TOUT>
-int launch_norm(const NormGemmArgs& a0, hipStream_t stream) {
+template <int NORM, class TW, int ACT, class TOUT>
+int launch_norm_rk(const NormGemmArgs& a0, hipStream_t stream) {
+  using TL = RTile;
   NormGemmArgs a = a0;
   const int64_t panels = cdiv(a.M, TL::BM), ntiles = cdiv(a.N, TL::BN);
-  // column-tile groups: enough workgroups to fill the CUs once, each walking its tiles
+  // column-tile groups: one workgroup per CU
   int64_t G = cdiv((int64_t)cu_count(), panels);
   G = G < 1 ? 1 : (G > ntiles ? ntiles : G);
   if (panels > 65535 || G * panels > 0x7fffffffLL) return 0;
   a.groups = (int)G;
-  hipLaunchKernelGGL((norm_gemm_kernel<TL, TW, ACT, TOUT>), dim3((unsigned)G, (unsigned)panels), dim3(TL::THREADS), 0,
-                     stream, a);
-  CORTEX_CHECK_LAUNCH("norm_gemm_kernel");
+  hipLaunchKernelGGL((norm_gemm_rk_kernel<NORM, TW, ACT, TOUT>), dim3((unsigned)G, (unsigned)panels), dim3(TL::THREADS),
+                     0, stream, a);
+  CORTEX_CHECK_LAUNCH("norm_gemm_rk_kernel");
   return 1;
 }
 
 template <class TW, int ACT, class TOUT>
 int dispatch_norm(const NormGemmArgs& a, hipStream_t stream) {
-  static const int tile = [] {
-    const char* e = getenv("CORTEX_NORM_TILE");
-    return e ? atoi(e) : -1;
-  }();
-  int t = tile;
-  // narrow outputs (N <= 512): 64-row panels, each workgroup one or two 256-column tiles
-  // (the normalisation is repeated per column-tile group, so fewer, wider groups); wider
-  // outputs: 128-row panels, half the weight re-reads
-  if (t < 0) t = a.N <= 512 ? 1 : 0;
-  switch (t) {
-    case 1:
-      return launch_norm<N64x256, TW, ACT, TOUT>(a, stream);
-    case 2:
-      return launch_norm<N64x128, TW, ACT, TOUT>(a, stream);
-    default:
-      return launch_norm<N128x128, TW, ACT, TOUT>(a, stream);
-  }
+  return a.norm == NORM_RMS ? launch_norm_rk<NORM_RMS, TW, ACT, TOUT>(a, stream)
+                            : launch_norm_rk<NORM_LAYER, TW, ACT, TOUT>(a, stream);
 }
 
 }  // namespace
@@ -1070,6 +1094,7 @@ extern "C" int cortex_norm_linear_fused(int64_t M, int64_t N, int64_t K, const v
                        aligned16(out) && ld_out % 8 == 0 && (!w_scale || aligned16(w_scale)) &&
                        (!bias || aligned16(bias)) && aligned16(gamma) && (!beta || aligned16(beta)),
                    "%s: operands must be 16-byte aligned rows", who);
+  CORTEX_CHECK_ARG(N * ld_w * (w_dtype == DT_I8 ? 1 : 2) < (1LL << 31), "%s: weight larger than 2 GiB", who);
   NormGemmArgs a{M, N, K, reinterpret_cast<const bf16*>(x), ld_x, norm, gamma, norm == NORM_LAYER ? beta : nullptr,
                  gamma_dtype, eps, w, ld_w, w_scale, bias, out, ld_out, 1};
   int st;

@@ -194,7 +194,7 @@ int cortex_norm_linear(int64_t M, int64_t N, int64_t K, int x_dtype, const void*
  * to 512; w (N, K): w_dtype 1 bf16 or 3 int8 (widened exactly in the kernel); gamma/beta
  * fp32 or bf16 (gamma_dtype, beta ignored for RMS, optional for LayerNorm); w_scale, bias
  * optional fp32; act 0 or 1 (erf-GELU); out bf16 (1) or fp32 (0); N % 8 == 0; 16-byte
- * aligned rows (ld_w % 16 for int8). */
+ * aligned rows (ld_w % 16 for int8); the weight (N x ld_w elements) under 2 GiB. */
 int cortex_norm_linear_fused(int64_t M, int64_t N, int64_t K, const void* x, int64_t ld_x, int norm,
                              const void* gamma, const void* beta, int gamma_dtype, float eps, int w_dtype,
                              const void* w, int64_t ld_w, const float* w_scale, const float* bias, int act,
