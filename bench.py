@@ -499,10 +499,24 @@ def norm_linear_api(dev, M: int = 8192, K: int = 512, widths=(1536, 2048, 512)) 
         t_kn = time_launches(lambda: rms_norm_linear(x, gam, wkn))
         t_i8 = time_launches(lambda: norm_linear_int8(x, q, sc, norm="rms", gamma=gam, eps=1e-6,
                                                       out_dtype=torch.bfloat16))
+        prev = ops.INT8_WEIGHTS
+        ops.INT8_WEIGHTS = "widen"  # the int8 weight streamed, rows normalised in the kernel
+        try:
+            t_w = time_launches(lambda: norm_linear_int8(x, q, sc, norm="rms", gamma=gam, eps=1e-6,
+                                                         out_dtype=torch.bfloat16))
+        finally:
+            ops.INT8_WEIGHTS = prev
+        fl = 2 * M * n * K
         out[f"N{n}"] = {"rms_norm_linear_kn_bf16_us": round(t_kn * 1e6, 2),
                         "norm_linear_int8_us": round(t_i8 * 1e6, 2),
-                        "int8_tflops": round(2 * M * n * K / t_i8 / 1e12, 1)}
-    return {"M": M, "K": K, **out}
+                        "int8_tflops": round(fl / t_i8 / 1e12, 1),
+                        "int8_mfma_frac": round(fl / t_i8 / 1e12 / BF16_PEAK_TFLOPS, 4),
+                        "int8_hbm_frac": round((M * K * 2 + n * K + n * 4 + M * n * 2) / t_i8 / 1e9 / HBM_PEAK_GBS, 4),
+                        "norm_linear_int8_streamed_us": round(t_w * 1e6, 2)}
+    return {"M": M, "K": K,
+            "note": "norm_linear_int8: the RMS gain folded once into a cached bf16 copy of the int8 weight "
+                    "(1/rms applied to the accumulator); _streamed: CORTEX_INT8_WEIGHTS=widen, the int8 "
+                    "weight itself read by the kernel, rows normalised in the kernel", **out}
 
 
 def api_configs(dev) -> dict:

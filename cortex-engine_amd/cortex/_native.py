@@ -108,6 +108,7 @@ _SIGNATURES = {
     "cortex_ln_rows_i8": (_int, [_i64, _i64, _ptr, _i64, _ptr, _ptr, _f32, _ptr, _i64, _f32, _ptr]),
     "cortex_norm_rows": (_int, [_i64, _i64, _int, _ptr, _i64, _int, _ptr, _ptr, _int, _f32, _ptr, _i64, _ptr]),
     "cortex_transpose_bf16": (_int, [_i64, _i64, _ptr, _i64, _ptr, _i64, _ptr]),
+    "cortex_fold_gain": (_int, [_i64, _i64, _ptr, _int, _int, _i64, _ptr, _int, _ptr, _i64, _ptr]),
     "cortex_splitk_workspace_bytes": (_i64, [_i64, _i64, _i64]),
     "cortex_linear_residual_splitk": (
         _int, [_i64, _i64, _i64, _ptr, _i64, _ptr, _i64, _ptr, _ptr, _ptr, _i64, _i64, _ptr, _i64, _i64, _ptr, _i64,

@@ -10,6 +10,7 @@ synchronises the host.
 from __future__ import annotations
 
 import math
+import os
 from collections import OrderedDict
 
 import torch
@@ -464,26 +465,63 @@ def convert(t: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
 # --------------------------------------------------------------------------- linear
 
 
+# "image" (default): the RMS gain folded into a cached bf16 copy of an int8 weight, which the
+# fused norm + linear kernel reads; "widen": that kernel streams the int8 weight itself and
+# normalises the rows (bit-for-bit the model's CORTEX_INT8_WEIGHTS switch, same variable)
+INT8_WEIGHTS = os.environ.get("CORTEX_INT8_WEIGHTS", "image")
+
 _KN_CACHE: "OrderedDict[tuple, tuple]" = OrderedDict()
 _KN_CACHE_SIZE = 16
 
 
-def kn_weight_rows(w: torch.Tensor) -> torch.Tensor:
-    """The (N, K) bf16 rows of a (K, N) weight (``rms_norm_linear``'s layout), cached per weight:
-    the cache holds the weight's storage (so its address is not reused while cached) and
-    rebuilds the rows when the weight's version counter moves (an in-place update)."""
-    key = (w.untyped_storage().data_ptr(), w.storage_offset(), tuple(w.shape), tuple(w.stride()), w.dtype,
-           w.device)
+def _cached_rows(key: tuple, holds: tuple, versions: tuple, build):
+    """A derived weight tensor kept in ``_KN_CACHE``: ``holds`` are the source tensors (their
+    storages are kept alive, so their addresses are not reused while cached) and ``versions``
+    their version counters (an in-place update rebuilds the entry)."""
     hit = _KN_CACHE.get(key)
-    if hit is not None and hit[1] == w._version:
+    if hit is not None and hit[1] == versions:
         _KN_CACHE.move_to_end(key)
         return hit[2]
-    rows = transpose_bf16(w if w.dtype == torch.bfloat16 else w.to(torch.bfloat16))
-    _KN_CACHE[key] = (w.untyped_storage(), w._version, rows)
+    rows = build()
+    _KN_CACHE[key] = (tuple(t.untyped_storage() for t in holds), versions, rows)
     _KN_CACHE.move_to_end(key)
     while len(_KN_CACHE) > _KN_CACHE_SIZE:
         _KN_CACHE.popitem(last=False)
     return rows
+
+
+def _tensor_key(t: torch.Tensor) -> tuple:
+    return (t.untyped_storage().data_ptr(), t.storage_offset(), tuple(t.shape), tuple(t.stride()), t.dtype, t.device)
+
+
+def kn_weight_rows(w: torch.Tensor) -> torch.Tensor:
+    """The (N, K) bf16 rows of a (K, N) weight (``rms_norm_linear``'s layout), cached per weight
+    and rebuilt when the weight changes in place."""
+    return _cached_rows(("kn", _tensor_key(w)), (w,), (w._version,),
+                        lambda: transpose_bf16(w if w.dtype == torch.bfloat16 else w.to(torch.bfloat16)))
+
+
+def fold_gain(w: torch.Tensor, gamma: torch.Tensor, kn: bool = False) -> torch.Tensor:
+    """bf16 (N, K) rows ``w[n, k] * gamma[k]`` (``cortex_fold_gain``) of an (N, K) weight, or of a
+    (K, N) weight with ``kn``: int8, bf16 or fp32 weights, fp32 or bf16 gamma."""
+    dev = nat.require_gpu(w, gamma, what="fold_gain")
+    w = _row_major_2d(w)
+    g = gamma.detach().contiguous()
+    N, K = (w.shape[1], w.shape[0]) if kn else (w.shape[0], w.shape[1])
+    if g.numel() != K:
+        raise ValueError(f"gamma has {g.numel()} values, the weight's K is {K}")
+    out = torch.empty((N, K), dtype=torch.bfloat16, device=dev)
+    ld_w = w.stride(0) if w.shape[0] > 1 else w.shape[1]
+    nat.call("cortex_fold_gain", N, K, nat.ptr(w), nat.code(w.dtype), int(kn), ld_w, nat.ptr(g), nat.code(g.dtype),
+             nat.ptr(out), K, nat.stream_of(dev))
+    return out
+
+
+def folded_weight_rows(w: torch.Tensor, gamma: torch.Tensor, kn: bool = False) -> torch.Tensor:
+    """``fold_gain(w, gamma, kn)``, cached per (weight, gamma) pair and rebuilt when either changes
+    in place: RMSNorm's gain carried by the weight, so the fused kernel applies only 1 / rms."""
+    key = ("fold", _tensor_key(w), _tensor_key(gamma), kn)
+    return _cached_rows(key, (w, gamma), (w._version, gamma._version), lambda: fold_gain(w, gamma, kn))
 
 
 def norm_linear_fused(x: torch.Tensor, w: torch.Tensor, w_scale=None, *, norm: str = "rms", gamma, beta=None,
@@ -491,16 +529,18 @@ def norm_linear_fused(x: torch.Tensor, w: torch.Tensor, w_scale=None, *, norm: s
                       out: torch.Tensor | None = None, out_dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
     """``act(norm(x) @ w^T * w_scale + bias)`` in one launch (``cortex_norm_linear_fused``): x (M, K)
     bf16 rows (K a multiple of 64 up to 512), w (N, K) bf16 or int8, the RMS / LayerNorm
-    statistics computed in the kernel from the staged rows."""
+    statistics computed in the kernel from the staged rows.  ``gamma=None`` with RMS: no gain
+    (a weight from ``folded_weight_rows`` carries it); 1 / rms scales the accumulator."""
     dev = nat.require_gpu(x, w, w_scale, gamma, beta, bias, out, what="norm_linear_fused")
     M, K = x.shape
     N = w.shape[0]
     if out is None:
         out = torch.empty((M, N), dtype=out_dtype, device=dev)
-    g = gamma.detach().contiguous()
+    g = gamma.detach().contiguous() if gamma is not None else None
     b = beta.detach().contiguous() if (beta is not None and norm == "layer") else None
+    g_code = nat.code(g.dtype if g is not None else torch.float32)
     nat.call("cortex_norm_linear_fused", M, N, K, nat.ptr(x), x.stride(0) if M > 1 else K, NORM[norm], nat.ptr(g),
-             nat.ptr(b), nat.code(g.dtype), float(eps), nat.code(w.dtype), nat.ptr(w), w.stride(0) if N > 1 else K,
+             nat.ptr(b), g_code, float(eps), nat.code(w.dtype), nat.ptr(w), w.stride(0) if N > 1 else K,
              nat.ptr(w_scale), nat.ptr(bias), ACT[act], nat.code(out.dtype), nat.ptr(out),
              out.stride(0) if M > 1 else N, nat.stream_of(dev))
     return out
@@ -550,15 +590,22 @@ def norm_linear(x: torch.Tensor, *, weight: torch.Tensor | None = None, weight_i
     nrm = NORM[norm]
     if (nrm and stats is None and residual is None and compute_dtype == torch.bfloat16 and x2.dtype == torch.bfloat16
             and K % 64 == 0 and K <= 512 and N % 8 == 0 and out_dtype in (torch.bfloat16, torch.float32)
-            and (weight_int8 is not None or w2.dtype == torch.bfloat16 or layout == 1) and gamma is not None
+            and (weight_int8 is not None or w2.dtype == torch.bfloat16 or layout == 1 or nrm == NORM["rms"])
+            and gamma is not None
             and gamma.dtype in (torch.float32, torch.bfloat16) and (beta is None or beta.dtype == gamma.dtype)
             and (bias is None or bias.dtype == torch.float32)
             and x2.data_ptr() % 16 == 0 and (M == 1 or x2.stride(0) % 8 == 0)
             and (layout == 1 or (w2.data_ptr() % 16 == 0 and (N == 1 or w2.stride(0) % 16 == 0)))
             and all(t is None or t.data_ptr() % 16 == 0 for t in (ws, bias, out2, gamma, beta))
             and gamma.is_contiguous() and (beta is None or beta.is_contiguous())):
-        # one launch: the statistics from the staged x panel, the contraction on (N, K) rows
-        if weight_int8 is None and layout == 1:
+        # one launch: the statistics from the staged rows, the contraction on (N, K) rows.  RMS:
+        # the gain is folded once into a cached bf16 copy of the weight (cortex_fold_gain) and
+        # the kernel scales the accumulator by 1 / rms; with CORTEX_INT8_WEIGHTS=widen an int8
+        # weight is streamed as it is and the kernel normalises the rows instead
+        if nrm == NORM["rms"] and not (weight_int8 is not None and INT8_WEIGHTS == "widen"):
+            w2 = folded_weight_rows(w2, gamma, kn=layout == 1)
+            gamma = None
+        elif weight_int8 is None and layout == 1:
             w2 = kn_weight_rows(w2)
         return norm_linear_fused(x2, w2, ws, norm=norm, gamma=gamma, beta=beta, eps=eps, bias=bias, act=act,
                                  out=out2).reshape(out.shape)

@@ -610,7 +610,7 @@ __device__ __forceinline__ bf16x2_t pair_of(const bf16x8& v, int d) {
   }
 }
 
-template <int NORM, class TW, int ACT, class TOUT>
+template <int NORM, bool NRM, class TW, int ACT, class TOUT>
 __global__ __launch_bounds__(512) void norm_gemm_rk_kernel(NormGemmArgs g) {
   using TL = RTile;
   constexpr int BN = TL::BN, RP = TL::RP;
@@ -656,18 +656,22 @@ __global__ __launch_bounds__(512) void norm_gemm_rk_kernel(NormGemmArgs g) {
   // a weight tile through registers: bf16, one row per load (lane: 16-byte chunk); int8, two
   // rows per load (lane / 32 the row, lane % 32 the chunk of 16 values, widened on the store)
   typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
-  u32x4 wr[NW0];  // a native vector type: a HIP uint4 array here ends up in scratch
+  // two register sets (native vector types: a HIP uint4 array here ends up in scratch); the
+  // int8 tile loop alternates them, widening one while the other is in flight
+  u32x4 wr[NW0], wr2[NW0];
   auto wreg_row = [&](int t) { return WI8 ? 8 * wid + 2 * t + (lane >> 5) : 8 * wid + t; };
-  auto load_wreg = [&](int i) {
+  auto load_wreg = [&](int i, u32x4 (&w)[NW0]) {
     const int n0 = (grp + i * G) * BN;
     const int c = WI8 ? min(lane & 31, K / 16 - 1) : min(lane, K / 8 - 1);
     const unsigned char* wl = reinterpret_cast<const unsigned char*>(g.w) + c * 16;
     static_for<NW0>([&](auto t) {
-      wr[t] = *reinterpret_cast<const u32x4*>(wl + (unsigned)rk_wrow(wreg_row(t), n0, N) * ldb);
+      w[t] = *reinterpret_cast<const u32x4*>(wl + (unsigned)rk_wrow(wreg_row(t), n0, N) * ldb);
     });
   };
-  auto store_wreg = [&](int b) {
-    static_for<NW0>([&](auto t) {
+  // load t of a register set into buffer b (int8: widened exactly)
+  auto store_piece = [&](int b, const u32x4 (&wr)[NW0], auto tc) {
+    constexpr int t = decltype(tc)::value;
+    {
       unsigned char* d = wbuf(b) + wreg_row(t) * RP;
       if constexpr (WI8) {
         d += (lane & 31) * 32;
@@ -676,12 +680,14 @@ __global__ __launch_bounds__(512) void norm_gemm_rk_kernel(NormGemmArgs g) {
       } else {
         *reinterpret_cast<u32x4*>(d + lane * 16) = wr[t];
       }
-    });
+    }
   };
+  auto store_wreg = [&](int b, const u32x4 (&w)[NW0]) { static_for<NW0>([&](auto t) { store_piece(b, w, t); }); };
 
   // ---- prologue: tile 0's weight into registers and its scales into LDS, this wavefront's
-  // 16 rows (rows 32 pr + 16 c2 ..) into LDS, gamma / beta
-  load_wreg(0);
+  // 16 rows (rows 32 pr + 16 c2 ..) into LDS, gamma / beta (int8: tile 1's weight as well)
+  load_wreg(0, wr);
+  if constexpr (WI8) load_wreg(1, wr2);
   issue_sb(0, 0);
   const int own = 32 * pr + 16 * c2;  // first staged row of this wavefront
   {
@@ -692,7 +698,7 @@ __global__ __launch_bounds__(512) void norm_gemm_rk_kernel(NormGemmArgs g) {
     const bool gbf = g.gamma_dtype == DT_BF16;
     const int esz = gbf ? 2 : 4;
     const int nb = esz * TL::KMAX / 1024;  // 1 KiB blocks per vector: 1 or 2
-    if (wid < 2 * nb) {
+    if (NRM && wid < 2 * nb) {
       const int which = wid / nb, blk = wid % nb;
       const void* base = (which && g.beta) ? g.beta : g.gamma;
       const int c = min(blk * 64 + lane, K * esz / 16 - 1);
@@ -701,181 +707,166 @@ __global__ __launch_bounds__(512) void norm_gemm_rk_kernel(NormGemmArgs g) {
     }
   }
   wait_vm<0>();  // this wavefront's rows, tile 0's weight and scales, its gamma / beta block
-  // a[0]: this wavefront's own 16 rows (normalised here), a[1]: its partner's 16 rows
+  // a[0]: this wavefront's own 16 rows (normalised here when NRM), a[1]: its partner's 16 rows
   const int other = 32 * pr + 16 * (1 - c2);
   bf16x8 a[2][8][2];
   const unsigned char* xo = smem + (own + j16) * RP + 32 * q;
   bf16x8 (&mine)[8][2] = a[0];
-  {
-    bf16x8 (&v)[8][2] = mine;  // raw rows, normalised in place
+  float rinv[2] = {1.0f, 1.0f};  // without NRM: 1 / rms of this lane's row in a[0], a[1]
+  if constexpr (NRM) {
+    {
+      bf16x8 (&v)[8][2] = mine;  // raw rows, normalised in place
 #pragma unroll
-    for (int s = 0; s < 8; ++s)
+      for (int s = 0; s < 8; ++s)
 #pragma unroll
-      for (int h = 0; h < 2; ++h) v[s][h] = *reinterpret_cast<const bf16x8*>(xo + s * 128 + h * 16);
-    // statistics: a lane's partial sums over its 8 x 16 values, then the four lanes of the
-    // row (l, l ^ 16, l ^ 32, l ^ 48)
-    const float fk = (float)K;  // means as sum / K, as torch's mean
-    const bf16x2_t ones = {(__bf16)1.0f, (__bf16)1.0f};
-    float p[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-    for (int s = 0; s < 8; ++s) {
-      if (s < nk) {
-#pragma unroll
-        for (int h = 0; h < 2; ++h)
-#pragma unroll
-          for (int d = 0; d < 4; ++d) {
-            const bf16x2_t xv = pair_of(v[s][h], d);
-            // sum of squares (RMS) or sum (LayerNorm): bf16 products are exact in fp32
-            p[d] = __builtin_amdgcn_fdot2_f32_bf16(xv, NORM == NORM_RMS ? xv : ones, p[d], false);
-          }
-      }
-    }
-    float s1 = (p[0] + p[1]) + (p[2] + p[3]);
-    s1 += __shfl_xor(s1, 16, 64);
-    s1 += __shfl_xor(s1, 32, 64);
-    float mu = 0.0f, inv;
-    if constexpr (NORM == NORM_RMS) {
-      inv = 1.0f / sqrtf(s1 / fk + g.eps);
-    } else {
-      mu = s1 / fk;
-      float s2[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        for (int h = 0; h < 2; ++h) v[s][h] = *reinterpret_cast<const bf16x8*>(xo + s * 128 + h * 16);
+      // statistics: a lane's partial sums over its 8 x 16 values, then the four lanes of the
+      // row (l, l ^ 16, l ^ 32, l ^ 48)
+      const float fk = (float)K;  // means as sum / K, as torch's mean
+      const bf16x2_t ones = {(__bf16)1.0f, (__bf16)1.0f};
+      float p[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
       for (int s = 0; s < 8; ++s) {
         if (s < nk) {
 #pragma unroll
           for (int h = 0; h < 2; ++h)
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-              const float d0 = (float)v[s][h][e] - mu;
-              s2[e & 3] = fmaf(d0, d0, s2[e & 3]);
+            for (int d = 0; d < 4; ++d) {
+              const bf16x2_t xv = pair_of(v[s][h], d);
+              // sum of squares (RMS) or sum (LayerNorm): bf16 products are exact in fp32
+              p[d] = __builtin_amdgcn_fdot2_f32_bf16(xv, NORM == NORM_RMS ? xv : ones, p[d], false);
             }
         }
       }
-      float t2 = (s2[0] + s2[1]) + (s2[2] + s2[3]);
-      t2 += __shfl_xor(t2, 16, 64);
-      t2 += __shfl_xor(t2, 32, 64);
-      inv = 1.0f / sqrtf(t2 / fk + g.eps);
-    }
-    __builtin_amdgcn_s_waitcnt(0xC07F);
-    __builtin_amdgcn_s_barrier();  // gamma / beta of every wavefront landed
-    if (g.gamma_dtype == DT_BF16) {
-      for (int e = tid; e < 2 * TL::KMAX; e += TL::THREADS)
-        reinterpret_cast<float*>(gbuf)[e] = (float)reinterpret_cast<const bf16*>(sbuf(1))[e];
-      __builtin_amdgcn_s_waitcnt(0xC07F);
-      __builtin_amdgcn_s_barrier();
-    }
-    // normalise: y = bf16((x - mu) inv gamma + beta); K steps past K are 0; back to LDS
+      float s1 = (p[0] + p[1]) + (p[2] + p[3]);
+      s1 += __shfl_xor(s1, 16, 64);
+      s1 += __shfl_xor(s1, 32, 64);
+      float mu = 0.0f, inv;
+      if constexpr (NORM == NORM_RMS) {
+        inv = 1.0f / sqrtf(s1 / fk + g.eps);
+      } else {
+        mu = s1 / fk;
+        float s2[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (int s = 0; s < 8; ++s) {
-      if (s < nk) {
-        float gm[16], bt[16];
-        const unsigned char* gp = gbuf + (64 * s + 16 * q) * 4;
+        for (int s = 0; s < 8; ++s) {
+          if (s < nk) {
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          const float4 g4 = *reinterpret_cast<const float4*>(gp + 16 * c);
-          gm[4 * c] = g4.x; gm[4 * c + 1] = g4.y; gm[4 * c + 2] = g4.z; gm[4 * c + 3] = g4.w;
-          if constexpr (NORM != NORM_RMS) {
-            const float4 b4 = *reinterpret_cast<const float4*>(gp + TL::KMAX * 4 + 16 * c);
-            const bool hb = g.beta != nullptr;
-            bt[4 * c] = hb ? b4.x : 0.0f;
-            bt[4 * c + 1] = hb ? b4.y : 0.0f;
-            bt[4 * c + 2] = hb ? b4.z : 0.0f;
-            bt[4 * c + 3] = hb ? b4.w : 0.0f;
+            for (int h = 0; h < 2; ++h)
+#pragma unroll
+              for (int e = 0; e < 8; ++e) {
+                const float d0 = (float)v[s][h][e] - mu;
+                s2[e & 3] = fmaf(d0, d0, s2[e & 3]);
+              }
           }
         }
-#pragma unroll
-        for (int h = 0; h < 2; ++h)
-#pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            const float xv = (float)v[s][h][e];
-            if constexpr (NORM == NORM_RMS)
-              mine[s][h][e] = (bf16)((xv * inv) * gm[8 * h + e]);
-            else
-              mine[s][h][e] = (bf16)fmaf((xv - mu) * inv, gm[8 * h + e], bt[8 * h + e]);
-          }
-      } else {
-#pragma unroll
-        for (int h = 0; h < 2; ++h)
-#pragma unroll
-          for (int e = 0; e < 8; ++e) mine[s][h][e] = (bf16)0.0f;
+        float t2 = (s2[0] + s2[1]) + (s2[2] + s2[3]);
+        t2 += __shfl_xor(t2, 16, 64);
+        t2 += __shfl_xor(t2, 32, 64);
+        inv = 1.0f / sqrtf(t2 / fk + g.eps);
       }
+      __builtin_amdgcn_s_waitcnt(0xC07F);
+      __builtin_amdgcn_s_barrier();  // gamma / beta of every wavefront landed
+      if (g.gamma_dtype == DT_BF16) {
+        for (int e = tid; e < 2 * TL::KMAX; e += TL::THREADS)
+          reinterpret_cast<float*>(gbuf)[e] = (float)reinterpret_cast<const bf16*>(sbuf(1))[e];
+        __builtin_amdgcn_s_waitcnt(0xC07F);
+        __builtin_amdgcn_s_barrier();
+      }
+      // normalise: y = bf16((x - mu) inv gamma + beta); K steps past K are 0; back to LDS
 #pragma unroll
-      for (int h = 0; h < 2; ++h) *reinterpret_cast<bf16x8*>(const_cast<unsigned char*>(xo) + s * 128 + h * 16) = mine[s][h];
+      for (int s = 0; s < 8; ++s) {
+        if (s < nk) {
+          float gm[16], bt[16];
+          const unsigned char* gp = gbuf + (64 * s + 16 * q) * 4;
+#pragma unroll
+          for (int c = 0; c < 4; ++c) {
+            const float4 g4 = *reinterpret_cast<const float4*>(gp + 16 * c);
+            gm[4 * c] = g4.x; gm[4 * c + 1] = g4.y; gm[4 * c + 2] = g4.z; gm[4 * c + 3] = g4.w;
+            if constexpr (NORM != NORM_RMS) {
+              const float4 b4 = *reinterpret_cast<const float4*>(gp + TL::KMAX * 4 + 16 * c);
+              const bool hb = g.beta != nullptr;
+              bt[4 * c] = hb ? b4.x : 0.0f;
+              bt[4 * c + 1] = hb ? b4.y : 0.0f;
+              bt[4 * c + 2] = hb ? b4.z : 0.0f;
+              bt[4 * c + 3] = hb ? b4.w : 0.0f;
+            }
+          }
+#pragma unroll
+          for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+              const float xv = (float)v[s][h][e];
+              if constexpr (NORM == NORM_RMS)
+                mine[s][h][e] = (bf16)((xv * inv) * gm[8 * h + e]);
+              else
+                mine[s][h][e] = (bf16)fmaf((xv - mu) * inv, gm[8 * h + e], bt[8 * h + e]);
+            }
+        } else {
+#pragma unroll
+          for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) mine[s][h][e] = (bf16)0.0f;
+        }
+#pragma unroll
+        for (int h = 0; h < 2; ++h) *reinterpret_cast<bf16x8*>(const_cast<unsigned char*>(xo) + s * 128 + h * 16) = mine[s][h];
+      }
     }
-  }
-  __builtin_amdgcn_s_waitcnt(0xC07F);
-  __builtin_amdgcn_s_barrier();  // every wavefront's normalised rows in LDS
-  {
-    bf16x8 (&theirs)[8][2] = a[1];
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    __builtin_amdgcn_s_barrier();  // every wavefront's normalised rows in LDS
+    {
+      bf16x8 (&theirs)[8][2] = a[1];
+      const unsigned char* xp = smem + (other + j16) * RP + 32 * q;
+#pragma unroll
+      for (int s = 0; s < 8; ++s)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) theirs[s][h] = *reinterpret_cast<const bf16x8*>(xp + s * 128 + h * 16);
+    }
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    __builtin_amdgcn_s_barrier();  // the staged rows are dead: the tile buffers may overwrite them
+  } else {
+    // rows as given (the gain is in the weight): both halves straight from LDS, the
+    // statistics of both, and 1 / rms applied to the accumulator in the epilogue
+    __builtin_amdgcn_s_barrier();  // the partner's rows landed
     const unsigned char* xp = smem + (other + j16) * RP + 32 * q;
 #pragma unroll
     for (int s = 0; s < 8; ++s)
 #pragma unroll
-      for (int h = 0; h < 2; ++h) theirs[s][h] = *reinterpret_cast<const bf16x8*>(xp + s * 128 + h * 16);
-  }
-  __builtin_amdgcn_s_waitcnt(0xC07F);
-  __builtin_amdgcn_s_barrier();  // the staged rows are dead: the tile buffers may overwrite them
-  store_wreg(0);
-
-  // ---- column tiles
-  for (int i = 0; i < nt; ++i) {
-    const int n0 = (grp + i * G) * BN, b = i & 1;
-    if constexpr (!WI8) {
-      if (i > 0) wait_vm<EPI>();  // tile i's transfers: only the previous tile's stores were issued after them
-    }
-    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wavefront's LDS reads and writes done
-    __builtin_amdgcn_s_barrier();        // tile i visible; buffer b ^ 1 free (tile i - 1 done)
-    if (i + 1 < nt) {
-      issue_sb(i + 1, b ^ 1);
-      if constexpr (WI8)
-        load_wreg(i + 1);
-      else
-        issue_w16(i + 1, b ^ 1);
-    }
-
-    const unsigned char* wb = wbuf(b) + (32 * c2 + j16) * RP + 32 * q;  // fragments 2 c2, 2 c2 + 1
-    f32x4 acc[2][2];
+      for (int h = 0; h < 2; ++h) {
+        a[0][s][h] = *reinterpret_cast<const bf16x8*>(xo + s * 128 + h * 16);
+        a[1][s][h] = *reinterpret_cast<const bf16x8*>(xp + s * 128 + h * 16);
+      }
+    const float fk = (float)K;
 #pragma unroll
-    for (int r = 0; r < 2; ++r)
+    for (int r = 0; r < 2; ++r) {
+      float p[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-      for (int f = 0; f < 2; ++f) acc[r][f] = (f32x4){0, 0, 0, 0};
-    bf16x8 cur[2][2], nxt[2][2];
-#pragma unroll
-    for (int f = 0; f < 2; ++f)
-#pragma unroll
-      for (int h = 0; h < 2; ++h) cur[f][h] = *reinterpret_cast<const bf16x8*>(wb + f * 16 * RP + h * 16);
-#pragma unroll
-    for (int s = 0; s < 8; ++s) {
-      if (s + 1 < 8) {
-#pragma unroll
-        for (int f = 0; f < 2; ++f)
+      for (int s = 0; s < 8; ++s) {
+        if (s < nk) {
 #pragma unroll
           for (int h = 0; h < 2; ++h)
-            nxt[f][h] = *reinterpret_cast<const bf16x8*>(wb + f * 16 * RP + (s + 1) * 128 + h * 16);
+#pragma unroll
+            for (int d = 0; d < 4; ++d) {
+              const bf16x2_t xv = pair_of(a[r][s][h], d);
+              p[d] = __builtin_amdgcn_fdot2_f32_bf16(xv, xv, p[d], false);
+            }
+        } else {
+#pragma unroll
+          for (int h = 0; h < 2; ++h) a[r][s][h] = (bf16x8){};  // K steps past K are 0
+        }
       }
-#pragma unroll
-      for (int h = 0; h < 2; ++h)
-#pragma unroll
-        for (int f = 0; f < 2; ++f)
-#pragma unroll
-          for (int r = 0; r < 2; ++r)
-            acc[r][f] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(cur[f][h], a[r][s][h], acc[r][f], 0, 0, 0);
-      if (s + 1 < 8) {
-#pragma unroll
-        for (int f = 0; f < 2; ++f)
-#pragma unroll
-          for (int h = 0; h < 2; ++h) cur[f][h] = nxt[f][h];
-      }
+      float s1 = (p[0] + p[1]) + (p[2] + p[3]);
+      s1 += __shfl_xor(s1, 16, 64);
+      s1 += __shfl_xor(s1, 32, 64);
+      rinv[r] = 1.0f / sqrtf(s1 / fk + g.eps);
     }
-    if constexpr (WI8) {
-      if (i + 1 < nt) {
-        wait_vm<0>();  // the next tile's int8 rows and scales (issued before this tile's multiplications)
-        store_wreg(b ^ 1);
-      }
-    }
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    __builtin_amdgcn_s_barrier();  // the staged rows are dead: the tile buffers may overwrite them
+  }
+  store_wreg(0, wr);
 
-    // ---- epilogue: scale, bias (from the tile's LDS copy), activation, stores
-    const unsigned char* sb = sbuf(b);
+  // ---- epilogue of one tile: scale, bias (from the tile's LDS copy), activation, stores
+  auto epilogue = [&](const f32x4 (&ac)[2][2], int n0, int sbi) {
+    const unsigned char* sb = sbuf(sbi);
     const int cs = min(n0 + 16 * q + 8 * c2, N - 8), lc = cs - n0;
     float sc[8], bi[8];
     {
@@ -893,8 +884,13 @@ __global__ __launch_bounds__(512) void norm_gemm_rk_kernel(NormGemmArgs g) {
       float v[8];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        v[e] = acc[r][0][e] * sc[e] + bi[e];
-        v[4 + e] = acc[r][1][e] * sc[4 + e] + bi[4 + e];
+        if constexpr (NRM) {
+          v[e] = ac[r][0][e] * sc[e] + bi[e];
+          v[4 + e] = ac[r][1][e] * sc[4 + e] + bi[4 + e];
+        } else {
+          v[e] = (ac[r][0][e] * rinv[r]) * sc[e] + bi[e];
+          v[4 + e] = (ac[r][1][e] * rinv[r]) * sc[4 + e] + bi[4 + e];
+        }
       }
       if (ACT == ACT_GELU) {
 #pragma unroll
@@ -911,10 +907,74 @@ __global__ __launch_bounds__(512) void norm_gemm_rk_kernel(NormGemmArgs g) {
         *reinterpret_cast<float4*>(op + 4) = make_float4(v[4], v[5], v[6], v[7]);
       }
     }
+  };
+
+  // ---- column tiles.  int8: during tile i the registers `cur` hold tile i + 1's rows (loaded
+  // a tile earlier), widened piece by piece between the K steps into the other buffer, while
+  // `nxt` receives tile i + 2's (the last tiles' successors clamp into range; their buffer is
+  // never read).  bf16: tile i + 1 is transferred direct to LDS at the top of tile i.
+  auto tile = [&](int i, const u32x4 (&cur)[NW0], u32x4 (&nxt)[NW0]) {
+    const int n0 = (grp + i * G) * BN, b = i & 1;
+    if (i > 0) {
+      if constexpr (WI8)
+        wait_vm<NW0 + EPI>();  // tile i's scales: issued before tile i + 1's loads and tile i - 1's stores
+      else
+        wait_vm<EPI>();  // tile i's transfers: only the previous tile's stores were issued after them
+    }
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wavefront's LDS reads and writes done
+    __builtin_amdgcn_s_barrier();        // tile i visible; buffer b ^ 1 free (tile i - 1 done)
+    if constexpr (WI8) {
+      issue_sb(i + 1, b ^ 1);
+      load_wreg(i + 2, nxt);
+    } else if (i + 1 < nt) {
+      issue_sb(i + 1, b ^ 1);
+      issue_w16(i + 1, b ^ 1);
+    }
+
+    const unsigned char* wb = wbuf(b) + (32 * c2 + j16) * RP + 32 * q;  // fragments 2 c2, 2 c2 + 1
+    f32x4 acc[2][2];
+#pragma unroll
+    for (int r = 0; r < 2; ++r)
+#pragma unroll
+      for (int f = 0; f < 2; ++f) acc[r][f] = (f32x4){0, 0, 0, 0};
+    bf16x8 cf[2][2], nf[2][2];
+#pragma unroll
+    for (int f = 0; f < 2; ++f)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) cf[f][h] = *reinterpret_cast<const bf16x8*>(wb + f * 16 * RP + h * 16);
+    static_for<8>([&](auto sc) {
+      constexpr int s = decltype(sc)::value;
+      if constexpr (s + 1 < 8) {
+#pragma unroll
+        for (int f = 0; f < 2; ++f)
+#pragma unroll
+          for (int h = 0; h < 2; ++h)
+            nf[f][h] = *reinterpret_cast<const bf16x8*>(wb + f * 16 * RP + (s + 1) * 128 + h * 16);
+      }
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int f = 0; f < 2; ++f)
+#pragma unroll
+          for (int r = 0; r < 2; ++r)
+            acc[r][f] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(cf[f][h], a[r][s][h], acc[r][f], 0, 0, 0);
+      if constexpr (WI8 && s < NW0) store_piece(b ^ 1, cur, std::integral_constant<int, s>{});
+      if constexpr (s + 1 < 8) {
+#pragma unroll
+        for (int f = 0; f < 2; ++f)
+#pragma unroll
+          for (int h = 0; h < 2; ++h) cf[f][h] = nf[f][h];
+      }
+    });
+    epilogue(acc, n0, b);
+  };
+  for (int i = 0; i < nt; i += 2) {
+    tile(i, wr2, wr);
+    if (i + 1 < nt) tile(i + 1, wr, wr2);
   }
 }
 
-template <int NORM, class TW, int ACT, class TOUT>
+template <int NORM, bool NRM, class TW, int ACT, class TOUT>
 int launch_norm_rk(const NormGemmArgs& a0, hipStream_t stream) {
   using TL = RTile;
   NormGemmArgs a = a0;
@@ -924,7 +984,7 @@ int launch_norm_rk(const NormGemmArgs& a0, hipStream_t stream) {
   G = G < 1 ? 1 : (G > ntiles ? ntiles : G);
   if (panels > 65535 || G * panels > 0x7fffffffLL) return 0;
   a.groups = (int)G;
-  hipLaunchKernelGGL((norm_gemm_rk_kernel<NORM, TW, ACT, TOUT>), dim3((unsigned)G, (unsigned)panels), dim3(TL::THREADS),
+  hipLaunchKernelGGL((norm_gemm_rk_kernel<NORM, NRM, TW, ACT, TOUT>), dim3((unsigned)G, (unsigned)panels), dim3(TL::THREADS),
                      0, stream, a);
   CORTEX_CHECK_LAUNCH("norm_gemm_rk_kernel");
   return 1;
@@ -932,8 +992,11 @@ int launch_norm_rk(const NormGemmArgs& a0, hipStream_t stream) {
 
 template <class TW, int ACT, class TOUT>
 int dispatch_norm(const NormGemmArgs& a, hipStream_t stream) {
-  return a.norm == NORM_RMS ? launch_norm_rk<NORM_RMS, TW, ACT, TOUT>(a, stream)
-                            : launch_norm_rk<NORM_LAYER, TW, ACT, TOUT>(a, stream);
+  // rows normalised in the kernel (LayerNorm, RMS with a gain), or RMS without a gain: raw
+  // rows and 1 / rms on the accumulator (cortex_fold_gain builds a weight that carries it)
+  if (a.norm == NORM_LAYER) return launch_norm_rk<NORM_LAYER, true, TW, ACT, TOUT>(a, stream);
+  return a.gamma ? launch_norm_rk<NORM_RMS, true, TW, ACT, TOUT>(a, stream)
+                 : launch_norm_rk<NORM_RMS, false, TW, ACT, TOUT>(a, stream);
 }
 
 }  // namespace
@@ -1084,7 +1147,8 @@ extern "C" int cortex_norm_linear_fused(int64_t M, int64_t N, int64_t K, const v
   CORTEX_CHECK_ARG(M <= 0x7fffffffLL && N <= 0x7fffffffLL, "%s: size too large", who);
   CORTEX_CHECK_ARG(K % 64 == 0 && K <= 512 && N % 8 == 0, "%s: need K a multiple of 64 up to 512 and N of 8", who);
   CORTEX_CHECK_ARG(norm == NORM_RMS || norm == NORM_LAYER, "%s: norm must be 1 (layer) or 2 (rms)", who);
-  CORTEX_CHECK_ARG(gamma && (gamma_dtype == DT_F32 || gamma_dtype == DT_BF16), "%s: gamma must be fp32 or bf16", who);
+  CORTEX_CHECK_ARG((gamma || norm == NORM_RMS) && (gamma_dtype == DT_F32 || gamma_dtype == DT_BF16),
+                   "%s: gamma must be fp32 or bf16 (NULL only with RMS)", who);
   CORTEX_CHECK_ARG(w_dtype == DT_BF16 || w_dtype == DT_I8, "%s: weight must be bf16 or int8", who);
   CORTEX_CHECK_ARG(act == ACT_NONE || act == ACT_GELU, "%s: act must be 0 (none) or 1 (GELU)", who);
   CORTEX_CHECK_ARG(out_dtype == DT_BF16 || out_dtype == DT_F32, "%s: out must be bf16 or fp32", who);
@@ -1092,7 +1156,7 @@ extern "C" int cortex_norm_linear_fused(int64_t M, int64_t N, int64_t K, const v
   CORTEX_CHECK_ARG(ld_x >= K && ld_w >= K && ld_out >= N, "%s: row strides too small", who);
   CORTEX_CHECK_ARG(aligned16(x) && ld_x % 8 == 0 && aligned16(w) && ld_w % (w_dtype == DT_I8 ? 16 : 8) == 0 &&
                        aligned16(out) && ld_out % 8 == 0 && (!w_scale || aligned16(w_scale)) &&
-                       (!bias || aligned16(bias)) && aligned16(gamma) && (!beta || aligned16(beta)),
+                       (!bias || aligned16(bias)) && (!gamma || aligned16(gamma)) && (!beta || aligned16(beta)),
                    "%s: operands must be 16-byte aligned rows", who);
   CORTEX_CHECK_ARG(N * ld_w * (w_dtype == DT_I8 ? 1 : 2) < (1LL << 31), "%s: weight larger than 2 GiB", who);
   NormGemmArgs a{M, N, K, reinterpret_cast<const bf16*>(x), ld_x, norm, gamma, norm == NORM_LAYER ? beta : nullptr,

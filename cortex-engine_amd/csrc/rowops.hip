@@ -183,6 +183,39 @@ __global__ __launch_bounds__(256) void transpose_bf16_kernel(const bf16* __restr
   }
 }
 
+// A weight with a norm gain folded into its input columns, as bf16 (N, K) rows:
+//   out[n, k] = bf16( float(w[n, k]) * gamma[k] )        (KN = false: (N, K) rows)
+//   out[n, k] = bf16( float(w[k, n]) * gamma[k] )        (KN = true: (K, N) rows, through a
+//                                                          64 x 64 LDS tile)
+// for int8, bf16 or fp32 weights and fp32 or bf16 gamma.  Rows of 64 x 4 threads.
+template <class TW, class TG, bool KN>
+__global__ __launch_bounds__(256) void fold_gain_kernel(const TW* __restrict__ w, int64_t N, int64_t K, int64_t ld_w,
+                                                        const TG* __restrict__ gamma, bf16* __restrict__ out,
+                                                        int64_t ld_out) {
+  __shared__ float tile[64][65];
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  const int64_t n0 = (int64_t)blockIdx.y * 64, k0 = (int64_t)blockIdx.x * 64;
+  if constexpr (KN) {
+#pragma unroll
+    for (int i = 0; i < 64; i += 4) {  // rows k of the (K, N) weight, columns n
+      const int64_t k = k0 + ty + i, n = n0 + tx;
+      if (k < K && n < N) tile[ty + i][tx] = (float)w[k * ld_w + n];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 64; i += 4) {
+      const int64_t n = n0 + ty + i, k = k0 + tx;
+      if (n < N && k < K) out[n * ld_out + k] = (bf16)(tile[tx][ty + i] * (float)gamma[k]);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 64; i += 4) {
+      const int64_t n = n0 + ty + i, k = k0 + tx;
+      if (n < N && k < K) out[n * ld_out + k] = (bf16)((float)w[n * ld_w + k] * (float)gamma[k]);
+    }
+  }
+}
+
 // Spike tokens straight to the LayerNorm'd bf16 operand of the cross-attention kv
 // projection: row r of the CSR token matrix is
 //   x = (neuron_emb[nid[e]] + time_emb[tb[e]]) + value_emb[val[e]]   (fp32, left to right)
@@ -431,6 +464,39 @@ int cortex_transpose_bf16(int64_t R, int64_t C, const void* in, int64_t ld_in, v
   hipLaunchKernelGGL(transpose_bf16_kernel, dim3((unsigned)cdiv(C, 64), (unsigned)cdiv(R, 64)), dim3(256), 0, stream,
                      (const bf16*)in, R, C, ld_in, (bf16*)out, ld_out);
   CORTEX_CHECK_LAUNCH("transpose_bf16_kernel");
+  return OK;
+}
+
+int cortex_fold_gain(int64_t N, int64_t K, const void* w, int w_dtype, int kn, int64_t ld_w, const void* gamma,
+                     int gamma_dtype, void* out, int64_t ld_out, hipStream_t stream) {
+  const char* who = "cortex_fold_gain";
+  CORTEX_CHECK_ARG(N >= 0 && K >= 0, "%s: negative size", who);
+  if (N == 0 || K == 0) return OK;
+  CORTEX_CHECK_ARG(w && gamma && out && ld_out >= K && ld_w >= (kn ? N : K), "%s: null pointer or short rows", who);
+  CORTEX_CHECK_ARG(w_dtype == DT_I8 || w_dtype == DT_BF16 || w_dtype == DT_F32, "%s: weight must be int8, bf16 or fp32",
+                   who);
+  CORTEX_CHECK_ARG(gamma_dtype == DT_F32 || gamma_dtype == DT_BF16, "%s: gamma must be fp32 or bf16", who);
+  CORTEX_CHECK_ARG(cdiv(N, 64) <= 65535 && cdiv(K, 64) <= 0x7fffffffLL, "%s: too large", who);
+  const dim3 grid((unsigned)cdiv(K, 64), (unsigned)cdiv(N, 64));
+#define CORTEX_FOLD(TW, TG, KN)                                                                                    \
+  hipLaunchKernelGGL((fold_gain_kernel<TW, TG, KN>), grid, dim3(256), 0, stream, (const TW*)w, N, K, ld_w, \
+                     (const TG*)gamma, (bf16*)out, ld_out)
+#define CORTEX_FOLD_G(TW)                                                  \
+  if (gamma_dtype == DT_F32) {                                             \
+    if (kn) CORTEX_FOLD(TW, float, true); else CORTEX_FOLD(TW, float, false); \
+  } else {                                                                 \
+    if (kn) CORTEX_FOLD(TW, bf16, true); else CORTEX_FOLD(TW, bf16, false);   \
+  }
+  if (w_dtype == DT_I8) {
+    CORTEX_FOLD_G(int8_t)
+  } else if (w_dtype == DT_BF16) {
+    CORTEX_FOLD_G(bf16)
+  } else {
+    CORTEX_FOLD_G(float)
+  }
+#undef CORTEX_FOLD_G
+#undef CORTEX_FOLD
+  CORTEX_CHECK_LAUNCH("fold_gain_kernel");
   return OK;
 }
 

@@ -143,6 +143,15 @@ int cortex_norm_rows(int64_t M, int64_t K, int x_dtype, const void* x, int64_t l
  * (fused_rmsnorm.py:239-245) as the (N, K) rows the GEMM streams.  Exact copies. */
 int cortex_transpose_bf16(int64_t R, int64_t C, const void* in, int64_t ld_in, void* out, int64_t ld_out,
                           hipStream_t stream);
+/* The RMSNorm gain of rms_norm_linear (fused_rmsnorm.py:223: (x / rms) * gamma) folded into
+ * the weight's input columns, once per (weight, gamma) pair, as bf16 (N, K) rows:
+ *   out[n, k] = bf16( float(w[n, k]) * gamma[k] )   (kn = 0, (N, K) rows: QuantizedLinear's
+ *                                                    int8 weight or an nn.Linear weight)
+ *   out[n, k] = bf16( float(w[k, n]) * gamma[k] )   (kn = 1, rms_norm_linear's (K, N) weight)
+ * w int8, bf16 or fp32 (w_dtype); gamma fp32 or bf16.  cortex_norm_linear_fused with
+ * norm 2 and gamma = NULL then applies the per-row 1 / rms to the fp32 accumulator. */
+int cortex_fold_gain(int64_t N, int64_t K, const void* w, int w_dtype, int kn, int64_t ld_w, const void* gamma,
+                     int gamma_dtype, void* out, int64_t ld_out, hipStream_t stream);
 
 /* ---- a5/a8: LayerNorm rows to bf16 ----------------------------------------
  * Replaces nn.LayerNorm feeding a bf16 linear (cortex/models/perceiver.py:67-68,
@@ -192,7 +201,9 @@ int cortex_norm_linear(int64_t M, int64_t N, int64_t K, int x_dtype, const void*
  * The row statistics are computed in the kernel's prologue from the x panel it stages in
  * LDS (no stats pass, no normalised rows in HBM).  x (M, K) bf16 with K a multiple of 64 up
  * to 512; w (N, K): w_dtype 1 bf16 or 3 int8 (widened exactly in the kernel); gamma/beta
- * fp32 or bf16 (gamma_dtype, beta ignored for RMS, optional for LayerNorm); w_scale, bias
+ * fp32 or bf16 (gamma_dtype, beta ignored for RMS, optional for LayerNorm; gamma NULL with
+ * RMS: no gain, the rows enter the MFMA as given and 1 / rms scales the fp32 accumulator,
+ * for a weight that carries the gain, see cortex_fold_gain); w_scale, bias
  * optional fp32; act 0 or 1 (erf-GELU); out bf16 (1) or fp32 (0); N % 8 == 0; 16-byte
  * aligned rows (ld_w % 16 for int8); the weight (N x ld_w elements) under 2 GiB. */
 int cortex_norm_linear_fused(int64_t M, int64_t N, int64_t K, const void* x, int64_t ld_x, int norm,

@@ -178,11 +178,12 @@ def test_transpose_bf16_exact(R, C):
 
 def _exact_rows(M, K, seed):
     """Rows x = c * s with s in {-1, +1}, c a power of two: with eps = 0 the RMS is |c| and
-    x / rms = s exactly, so the normalised row s * gamma is exact in bf16 (gamma bf16-valued)."""
+    x / rms = s exactly.  Gains are powers of two, so the normalised row s * gamma is exact in
+    bf16, and so is a weight that carries the gain (w * gamma, the int8 path's widening)."""
     g = torch.Generator().manual_seed(seed)
     s = torch.randint(0, 2, (M, K), generator=g).float() * 2 - 1
     c = 2.0 ** torch.randint(-3, 4, (M, 1), generator=g).float()
-    gam = (1 + 0.1 * torch.randn(K, generator=g)).bfloat16().float()
+    gam = 2.0 ** torch.randint(-2, 3, (K,), generator=g).float()
     return (s * c).bfloat16(), s, gam
 
 
@@ -212,11 +213,12 @@ def test_fused_rms_linear_one_launch_exact_rows(M, N, K, wform):
 @pytest.mark.parametrize("norm", ["rms", "layer"])
 @pytest.mark.parametrize("act", [None, "gelu"])
 def test_fused_norm_linear_vs_oracle(norm, act):
-    """The one-launch path with general rows: bf16 output against the normalised rows
-    rounded to bf16 (as the reference does) times the dequantised weight in float64; the
-    row statistics differ from torch's only in summation order, so a rounding of the
-    normalised row may flip by one bf16 step: within 2 bf16 steps of the output plus
-    1e-3 of the largest output everywhere, and within one step for 99 % of outputs."""
+    """The one-launch path with a gain given to the kernel (rows normalised in the kernel, the
+    int8 weight streamed): bf16 output against the normalised rows rounded to bf16 (as the
+    reference does) times the dequantised weight in float64; the row statistics differ from
+    torch's only in summation order, so a rounding of the normalised row may flip by one bf16
+    step: within 2 bf16 steps of the output plus 1e-3 of the largest output everywhere, and
+    within one step for 99 % of outputs."""
     from cortex.kernels import ops
 
     M, N, K = 1000, 768, 512
@@ -245,9 +247,9 @@ def test_fused_norm_linear_vs_oracle(norm, act):
 
 
 def test_config2_is_one_launch_and_kn_weights_are_cached():
-    """Config 2 through the API: norm_linear_int8 and rms_norm_linear launch exactly one kernel
-    (the fused one, no norm rows or weight conversion), and the (K, N) weight's (N, K) rows
-    are rebuilt only when the weight changes in place."""
+    """Config 2 through the API: one kernel per call (the fused one).  The RMS gain is folded into
+    a cached bf16 copy of the weight once per (weight, gamma) pair -- one cortex_fold_gain,
+    rebuilt when either changes in place -- for the int8 and the (K, N) weight alike."""
     from cortex import _native as nat
     from cortex.kernels import ops
     from cortex.kernels.fused_rmsnorm import norm_linear_int8, rms_norm_linear
@@ -263,16 +265,98 @@ def test_config2_is_one_launch_and_kn_weights_are_cached():
     nat.call = spy
     try:
         norm_linear_int8(xd, qd, sd, norm="rms", gamma=gd, eps=1e-6)
+        assert names == ["cortex_fold_gain", "cortex_norm_linear_fused"], names  # the gain folded once
+        names.clear()
+        norm_linear_int8(xd, qd, sd, norm="rms", gamma=gd, eps=1e-6)
         assert names == ["cortex_norm_linear_fused"], names
         w = (torch.randn(512, 1536) * 0.02).bfloat16().to(DEV)
         names.clear()
         a = rms_norm_linear(xd, gd, w)
         b = rms_norm_linear(xd, gd, w)
-        assert names.count("cortex_norm_linear_fused") == 2 and names.count("cortex_transpose_bf16") == 1, names
+        assert names.count("cortex_norm_linear_fused") == 2 and names.count("cortex_fold_gain") == 1, names
         torch.testing.assert_close(a, b, rtol=0, atol=0)
         w.mul_(2)  # in place: the cached rows must follow
         c = rms_norm_linear(xd, gd, w)
-        assert names.count("cortex_transpose_bf16") == 2, names
+        assert names.count("cortex_fold_gain") == 2, names
         torch.testing.assert_close(c.float(), 2 * a.float(), rtol=1e-2, atol=1e-2)
+        gd.mul_(0.5)  # so must a change of gamma
+        d = rms_norm_linear(xd, gd, w)
+        assert names.count("cortex_fold_gain") == 3, names
+        torch.testing.assert_close(d.float(), a.float(), rtol=1e-2, atol=1e-2)
     finally:
         nat.call = real
+
+
+@pytest.mark.parametrize("wdt", [torch.int8, torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("kn", [False, True])
+@pytest.mark.parametrize("gdt", [torch.float32, torch.bfloat16])
+def test_fold_gain_exact(wdt, kn, gdt):
+    """cortex_fold_gain: bf16(float(w) * gamma) per element, bit-exact against torch's fp32
+    product rounded to bf16 (round to nearest even), for both weight layouts."""
+    from cortex.kernels import ops
+
+    g = torch.Generator().manual_seed(5)
+    N, K = 200, 448
+    if wdt == torch.int8:
+        w = torch.randint(-127, 128, (N, K), generator=g, dtype=torch.int8)
+    else:
+        w = (torch.randn(N, K, generator=g) * 0.05).to(wdt)
+    gam = (1 + 0.1 * torch.randn(K, generator=g)).to(gdt)
+    src = w.T.contiguous() if kn else w
+    out = ops.fold_gain(src.to(DEV), gam.to(DEV), kn=kn).cpu()
+    ref = (w.float() * gam.float()).bfloat16()
+    assert out.shape == (N, K) and out.dtype == torch.bfloat16
+    assert torch.equal(out.view(torch.int16), ref.view(torch.int16))
+
+
+@pytest.mark.parametrize("M,N,K,wform", [(8192, 1536, 512, "int8"), (300, 200, 256, "bf16"), (1, 64, 448, "int8")])
+def test_rms_linear_folded_gain_exact_rows(M, N, K, wform):
+    """The API's RMS path: gain folded into the cached weight, 1 / rms on the accumulator.  With
+    power-of-two gains the folded weight is exact and with rows c * sign (eps = 0) 1 / rms is
+    exact, so the fp32 output is within 1e-5 of a float64 contraction."""
+    from cortex.kernels import ops
+
+    x, sgn, gam = _exact_rows(M, K, seed=M + N)
+    g = torch.Generator().manual_seed(N + K)
+    w = torch.randn(N, K, generator=g) * 0.03
+    bias = torch.randn(N, generator=g) * 0.1
+    if wform == "int8":
+        q, s = O.quantize_int8(w.numpy())
+        kw = {"weight_int8": torch.from_numpy(q).to(DEV), "weight_scale": torch.from_numpy(s).to(DEV)}
+        wref = torch.from_numpy(O.dequantize(q, s))
+    else:
+        kw = {"weight": w.bfloat16().to(DEV)}
+        wref = w.bfloat16().float()
+    out = ops.norm_linear(x.to(DEV), **kw, norm="rms", gamma=gam.to(DEV), eps=0.0, bias=bias.to(DEV),
+                          out_dtype=torch.float32, compute_dtype=torch.bfloat16)
+    ref = (sgn.double() * gam.double()) @ wref.double().T + bias.double()
+    assert out.shape == (M, N)
+    assert _rel_err(out.cpu(), ref) <= 1e-5
+
+
+@pytest.mark.parametrize("N", [1536, 512])
+def test_config2_widen_mode_streams_int8(N, monkeypatch):
+    """CORTEX_INT8_WEIGHTS=widen: norm_linear_int8 hands the int8 weight and the gain to the kernel
+    (rows normalised in the kernel, no folded copy) in one launch, and agrees with the default
+    (folded) path and the oracle to the config-2 tolerance."""
+    from cortex import _native as nat
+    from cortex.kernels import ops
+    from cortex.kernels.fused_rmsnorm import norm_linear_int8
+
+    x, g, q, s = _config2(N, seed=3)
+    xd, gd, qd, sd = x.to(DEV), g.to(DEV), q.to(DEV), s.to(DEV)
+    ref = O.rms_norm_linear(x, g, torch.from_numpy(O.dequantize(q.numpy(), s.numpy())).T.contiguous())
+    folded = norm_linear_int8(xd, qd, sd, norm="rms", gamma=gd, eps=1e-6).float().cpu()
+    monkeypatch.setattr(ops, "INT8_WEIGHTS", "widen")
+    names, real = [], nat.call
+
+    def spy(name, *a):
+        names.append(name)
+        return real(name, *a)
+    monkeypatch.setattr(nat, "call", spy)
+    streamed = norm_linear_int8(xd, qd, sd, norm="rms", gamma=gd, eps=1e-6).float().cpu()
+    assert names == ["cortex_norm_linear_fused"], names
+    for out in (folded, streamed):
+        err = (out - ref).abs()
+        assert float((err / ref.abs().clamp_min(1e-3)).median()) < 4e-3
+        assert float(err.max()) <= 2e-2 * float(ref.abs().max())
