@@ -14,7 +14,8 @@ Usage:
       prints exactly one JSON line on stdout
   python bench.py --kernel NAME [--iters N]
       launches one hot kernel N times on synthetic operands of its forward shape (for
-      rocprofv3 --kernel-trace / --pmc runs); NAME in KERNELS
+      rocprofv3 --kernel-trace / --pmc runs); NAME in KERNELS, or one of the API
+      configurations 0-2 (API_WORKLOADS)
   python bench.py --copy-calibration [--iters N]
       a plain 64 MiB device-to-device copy N times (the reference for PMC byte counters)
 """
@@ -174,11 +175,68 @@ def make_kernel(name: str, dev):
         by = E * (D * 2 + 4 * 8) + (137 + 600 + 8) * D * 4 + 2 * D * 4 + (B_MAIN + 1) * 8
         return fn, 1, "hbm", 0.0, by, ("fused tokenizer + norm_kv LayerNorm into bf16 CSR rows, E=16384 D=512 "
                                       "(tokenize_ln_kernel)")
+    if name.startswith("api_"):
+        return make_api_workload(name, dev)
     raise ValueError(f"unknown kernel {name}")
+
+
+def _api_events(dev, seed: int = 0):
+    """B = 32 ragged samples, E_b ~ U{128..512}, and fp32 tables 137/600/8 x 512 ~ N(0, 0.02)."""
+    rng = np.random.default_rng(seed)
+    B, D = 32, 512
+    counts = rng.integers(128, 513, B)
+    E = int(counts.sum())
+    ev = [torch.from_numpy(a).to(dev) for a in (rng.integers(0, 137, E), rng.integers(0, 600, E),
+                                                 np.clip(rng.poisson(1.0, E) + 1, 0, 7), np.repeat(np.arange(B), counts))]
+    tables = [torch.from_numpy(rng.normal(0, 0.02, (n, D)).astype(np.float32)).to(dev) for n in (137, 600, 8)]
+    return rng, B, D, counts, E, ev, tables
+
+
+def make_api_workload(name: str, dev):
+    """The kernel-level configurations through the public API, as make_kernel's tuple (the whole
+    call is the unit: every kernel it launches is in the trace):
+
+    * api_tokenize_pack: config 0, fused_tokenizer + pack to CSR rows, fp32;
+    * api_sparse_xattn: config 1, sparse_cross_attention bf16 with per-sample lengths;
+    * api_norm_linear_int8_n{1536,2048,512}: config 2, RMSNorm (eps 1e-6) + INT8 linear,
+      M = 8192, K = 512, bf16 in / out."""
+    from cortex.kernels.fused_rmsnorm import norm_linear_int8
+    from cortex.kernels import ops
+    from cortex.kernels.sparse_xattn import sparse_cross_attention
+    from cortex.kernels.tokenizer import tokenize_and_pack
+
+    if name == "api_tokenize_pack":
+        rng, B, D, counts, E, ev, tables = _api_events(dev)
+        by = E * (D * 4 + 4 * 8) + (137 + 600 + 8) * D * 4 + (B + 1) * 8
+        return (lambda: tokenize_and_pack(*tables, *ev, batch_size=B)), 1, "hbm", 0.0, by, \
+            f"config 0: fused tokenizer + pack, CSR rows, fp32, B=32 E={E} D=512"
+    if name == "api_sparse_xattn":
+        rng, B, D, counts, E, ev, tables = _api_events(dev)
+        H, L, Dh, Ek = 8, 256, 64, 512
+        g = torch.Generator(device="cpu").manual_seed(1)
+        q, k, v = ((torch.randn(B, H, n, Dh, generator=g) / 8).bfloat16().to(dev) for n in (L, Ek, Ek))
+        lens = torch.from_numpy(rng.integers(128, 513, B)).to(dev)
+        fl = 4.0 * H * L * Dh * float(lens.sum())
+        return (lambda: sparse_cross_attention(q, k, v, kv_lengths=lens)), 1, "mfma", fl, 0.0, \
+            "config 1: sparse cross-attention bf16, q (32,8,256,64), k/v (32,8,512,64), lengths U{128..512}"
+    m = re.fullmatch(r"api_norm_linear_int8_n(\d+)", name)
+    if m:
+        n, M, K = int(m.group(1)), 8192, 512
+        g = torch.Generator(device="cpu").manual_seed(2)
+        x = torch.randn(M, K, generator=g).bfloat16().to(dev)
+        gam = (1 + 0.02 * torch.randn(K, generator=g)).to(dev)
+        q, sc = ops.quantize_int8((0.02 * torch.randn(n, K, generator=g)).to(dev))
+        fl = 2.0 * M * n * K
+        by = M * K * 2 + n * K + n * 4 + M * n * 2
+        return (lambda: norm_linear_int8(x, q, sc, norm="rms", gamma=gam, eps=1e-6, out_dtype=torch.bfloat16)), \
+            1, ("hbm" if n <= 512 else "mfma"), fl, by, f"config 2: RMSNorm + INT8 linear, M=8192 K=512 N={n}, bf16"
+    raise ValueError(f"unknown API workload {name}")
 
 
 KERNELS = ("gemm_mlp2_residual", "gemm_mlp0_gelu", "qkv_attention", "out_residual_ln", "attention_cross", "ln_rows",
            "tokenize")
+API_WORKLOADS = ("api_tokenize_pack", "api_sparse_xattn", "api_norm_linear_int8_n1536", "api_norm_linear_int8_n2048",
+                 "api_norm_linear_int8_n512")
 
 
 def time_launches(fn, iters: int = 20, reps: int = 5) -> float:
@@ -764,7 +822,8 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--latency-requests", type=int, default=1000)
     ap.add_argument("--quick", action="store_true", help="skip latency, sweep, breakdown and CPU baseline")
-    ap.add_argument("--kernel", choices=KERNELS, help="launch one hot kernel only (profiling)")
+    ap.add_argument("--kernel", choices=KERNELS + API_WORKLOADS,
+                    help="launch one hot kernel (or one API workload) only, for profiling")
     ap.add_argument("--copy-calibration", action="store_true", help="64 MiB copies only (PMC calibration)")
     ap.add_argument("--iters", type=int, default=20)
     args = ap.parse_args()
