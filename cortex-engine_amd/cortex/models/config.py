@@ -15,22 +15,22 @@ from pydantic import BaseModel, Field, model_validator
 class CortexConfig(BaseModel):
     """Configuration of the Cortex model family (all architecture fields required)."""
 
-    hidden_dim: int = Field(..., gt=0, description="Embedding/hidden dimension")
-    num_layers: int = Field(..., gt=0, description="Number of transformer layers")
-    num_heads: int = Field(..., gt=0, description="Number of attention heads")
-    head_dim: int = Field(..., gt=0, description="Per-head dimension")
-    mlp_ratio: float = Field(4.0, gt=0, description="MLP hidden = mlp_ratio * hidden_dim")
+    hidden_dim: int = Field(..., gt=0, description="width of the token and latent vectors")
+    num_layers: int = Field(..., gt=0, description="self-attention blocks over the latents")
+    num_heads: int = Field(..., gt=0, description="heads of each self-attention block")
+    head_dim: int = Field(..., gt=0, description="width of one head (num_heads x head_dim = hidden_dim)")
+    mlp_ratio: float = Field(4.0, gt=0, description="hidden width of a block's MLP, as a multiple of hidden_dim")
     dropout: float = Field(0.0, ge=0, lt=1)
 
-    num_latents: int = Field(..., gt=0, description="Size of latent array")
-    latent_dim: int = Field(..., gt=0, description="Latent array hidden dimension")
+    num_latents: int = Field(..., gt=0, description="number of learned latent queries")
+    latent_dim: int = Field(..., gt=0, description="width of a latent query")
     cross_attn_heads: int = Field(..., gt=0)
 
-    max_neurons: int = Field(..., gt=0, description="Max neuron index across all sessions")
-    max_time_bins: int = Field(..., gt=0, description="Max time bin index per window")
-    spike_value_buckets: int = Field(8, gt=0, description="Quantization buckets for spike count")
+    max_neurons: int = Field(..., gt=0, description="rows of the neuron-id embedding table")
+    max_time_bins: int = Field(..., gt=0, description="rows of the time-bin embedding table")
+    spike_value_buckets: int = Field(8, gt=0, description="rows of the spike-count embedding table")
 
-    behavior_dim: int = Field(..., gt=0, description="Output dim of behavior decoder")
+    behavior_dim: int = Field(..., gt=0, description="values decoded per sample (2: x and y velocity)")
     use_masked_spike_head: bool = True
 
     dtype: str = Field("bfloat16", pattern="^(float32|float16|bfloat16)$")
@@ -41,15 +41,12 @@ class CortexConfig(BaseModel):
 
     @model_validator(mode="after")
     def _check_head_consistency(self) -> CortexConfig:
-        if self.hidden_dim % self.num_heads != 0:
-            raise ValueError(
-                f"hidden_dim ({self.hidden_dim}) must be divisible by num_heads ({self.num_heads})"
-            )
-        if self.head_dim * self.num_heads != self.hidden_dim:
-            raise ValueError(
-                f"head_dim ({self.head_dim}) * num_heads ({self.num_heads}) "
-                f"must equal hidden_dim ({self.hidden_dim})"
-            )
+        d, h, w = self.hidden_dim, self.num_heads, self.head_dim
+        if d % h:
+            raise ValueError(f"{h} heads do not split hidden_dim {d} evenly")
+        if h * w != d:
+            # the phrase "must equal hidden_dim" is what callers match on
+            raise ValueError(f"{h} heads x head_dim {w} = {h * w}: the product must equal hidden_dim ({d})")
         return self
 
     @property
