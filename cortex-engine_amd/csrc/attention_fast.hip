@@ -355,7 +355,7 @@ void attention_fast_kernel(AttnArgs a) {
         bf16x4 v;
 #pragma unroll
         for (int i = 0; i < 4; ++i) v[i] = (bf16)(o_acc[qg][t][i] * inv);
-        *reinterpret_cast<bf16x4*>(O + 16 * t + 4 * g) = v;
+        store_wt(reinterpret_cast<bf16x4*>(O + 16 * t + 4 * g), v);
       }
     }
   }

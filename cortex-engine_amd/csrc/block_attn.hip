@@ -392,7 +392,7 @@ __global__ __launch_bounds__(BA_THREADS) void qkv_attention_kernel(QkvAttnArgs a
             const float y = o_acc[qg][t][i] * inv;
             pk |= (uint32_t)((int)fminf(fmaxf(rintf(y * a.out_inv_scale), -127.0f), 127.0f) & 0xff) << (8 * i);
           }
-          *reinterpret_cast<uint32_t*>(O + 16 * t + 4 * g4) = pk;
+          store_wt(reinterpret_cast<uint32_t*>(O + 16 * t + 4 * g4), pk);
         }
       } else {
         bf16* O = reinterpret_cast<bf16*>(a.out) + (row0 + q) * a.ld_o + h * 64;
@@ -401,7 +401,7 @@ __global__ __launch_bounds__(BA_THREADS) void qkv_attention_kernel(QkvAttnArgs a
           bf16x4 v;
 #pragma unroll
           for (int i = 0; i < 4; ++i) v[i] = (bf16)(o_acc[qg][t][i] * inv);
-          *reinterpret_cast<bf16x4*>(O + 16 * t + 4 * g4) = v;
+          store_wt(reinterpret_cast<bf16x4*>(O + 16 * t + 4 * g4), v);
         }
       }
     }

@@ -64,6 +64,34 @@ __device__ __forceinline__ void mfma_16x16x32(f32x4& acc, const Frag<float>& a, 
   for (int j = 0; j < 8; ++j) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.v[j], b.v[j], acc, 0, 0, 0);
 }
 
+// Output stores written through the L2 to memory at device scope (SC1).  A kernel's outputs
+// are read by the next kernel, mostly on other XCDs; written through as they are produced,
+// they leave no dirty lines behind for the L2 write-back at the end of the kernel, which
+// otherwise starts only after the last store.  (Non-temporal stores skip that write-back too
+// but also bypass the infinity cache that the next kernel reads from.)
+//
+// Inline assembly, so the compiler neither counts these stores nor sees their hazards:
+//  * no code may read the stored bytes back in the same kernel;
+//  * the store reads its data VGPRs after issue, and a VALU write to them must wait two
+//    cycles after a store of more than 8 bytes (the compiler inserts this wait for its own
+//    stores and reuses the registers at once) -- the s_nop after each store provides it.
+template <class V>
+__device__ __forceinline__ void store_wt(V* p, const V& v) {
+  if constexpr (sizeof(V) == 16) {
+    typedef unsigned u4 __attribute__((ext_vector_type(4)));
+    asm volatile("global_store_dwordx4 %0, %1, off sc1\n\ts_nop 2" ::"v"(p), "v"(__builtin_bit_cast(u4, v))
+                 : "memory");
+  } else if constexpr (sizeof(V) == 8) {
+    typedef unsigned u2 __attribute__((ext_vector_type(2)));
+    asm volatile("global_store_dwordx2 %0, %1, off sc1\n\ts_nop 2" ::"v"(p), "v"(__builtin_bit_cast(u2, v))
+                 : "memory");
+  } else {
+    static_assert(sizeof(V) == 4, "4-, 8- or 16-byte stores");
+    asm volatile("global_store_dword %0, %1, off sc1\n\ts_nop 2" ::"v"(p), "v"(__builtin_bit_cast(unsigned, v))
+                 : "memory");
+  }
+}
+
 // Operand element type of the direct-to-LDS GEMM loops: a 16-byte fragment per lane and the
 // MFMA that consumes it (bf16: 8 K-elements, fp32 accumulators; int8: 16 K-elements, int32
 // accumulators).  Both read 16 bytes per lane per operand, so LDS layouts carry over.

@@ -373,7 +373,7 @@ __global__ __launch_bounds__(TL::THREADS) void gemm_bf16_kernel(GemmArgs g) {
         bf16x8 o;
 #pragma unroll
         for (int e = 0; e < 8; ++e) o[e] = (bf16)v[e];
-        *reinterpret_cast<bf16x8*>(op) = o;
+        store_wt(reinterpret_cast<bf16x8*>(op), o);
       } else if constexpr (sizeof(TOUT) == 1) {  // int8 at the next linear's activation scale
         uint32_t lo = 0, hi = 0;
 #pragma unroll
@@ -383,11 +383,11 @@ __global__ __launch_bounds__(TL::THREADS) void gemm_bf16_kernel(GemmArgs g) {
           lo |= (uint32_t)(q0 & 0xff) << (8 * e);
           hi |= (uint32_t)(q1 & 0xff) << (8 * e);
         }
-        *reinterpret_cast<uint2*>(op) = make_uint2(lo, hi);
+        store_wt(reinterpret_cast<uint2*>(op), make_uint2(lo, hi));
       } else {
 #pragma unroll
         for (int h = 0; h < NV / 4; ++h)
-          reinterpret_cast<float4*>(op)[h] = make_float4(v[4 * h], v[4 * h + 1], v[4 * h + 2], v[4 * h + 3]);
+          store_wt(reinterpret_cast<float4*>(op) + h, make_float4(v[4 * h], v[4 * h + 1], v[4 * h + 2], v[4 * h + 3]));
       }
     }
   }
@@ -901,10 +901,10 @@ __global__ __launch_bounds__(512) void norm_gemm_rk_kernel(NormGemmArgs g) {
         bf16x8 o;
 #pragma unroll
         for (int e = 0; e < 8; ++e) o[e] = (bf16)v[e];
-        *reinterpret_cast<bf16x8*>(op) = o;
+        store_wt(reinterpret_cast<bf16x8*>(op), o);
       } else {
-        *reinterpret_cast<float4*>(op) = make_float4(v[0], v[1], v[2], v[3]);
-        *reinterpret_cast<float4*>(op + 4) = make_float4(v[4], v[5], v[6], v[7]);
+        store_wt(reinterpret_cast<float4*>(op), make_float4(v[0], v[1], v[2], v[3]));
+        store_wt(reinterpret_cast<float4*>(op + 4), make_float4(v[4], v[5], v[6], v[7]));
       }
     }
   };

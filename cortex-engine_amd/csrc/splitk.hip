@@ -44,7 +44,7 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(ReduceArgs a) {
       s.x += b.x; s.y += b.y; s.z += b.z; s.w += b.w;
     }
     const float4 r = *reinterpret_cast<const float4*>(a.res + (m % a.res_rows) * a.ld_res + c);
-    *reinterpret_cast<float4*>(a.out + m * a.ld_out + c) = make_float4(s.x + r.x, s.y + r.y, s.z + r.z, s.w + r.w);
+    store_wt(reinterpret_cast<float4*>(a.out + m * a.ld_out + c), make_float4(s.x + r.x, s.y + r.y, s.z + r.z, s.w + r.w));
   }
 }
 
@@ -83,7 +83,7 @@ __global__ __launch_bounds__(256) void splitk_reduce_ln_kernel(ReduceLnArgs a) {
     v[j + 1] = s.y + r.y;
     v[j + 2] = s.z + r.z;
     v[j + 3] = s.w + r.w;
-    *reinterpret_cast<float4*>(a.r.out + m * a.r.ld_out + k) = make_float4(v[j], v[j + 1], v[j + 2], v[j + 3]);
+    store_wt(reinterpret_cast<float4*>(a.r.out + m * a.r.ld_out + k), make_float4(v[j], v[j + 1], v[j + 2], v[j + 3]));
   }
   ln_regs<EPL>(v, 1.0f / (float)N, a.eps, a.gamma, a.beta, lane);
 #pragma unroll
@@ -93,7 +93,7 @@ __global__ __launch_bounds__(256) void splitk_reduce_ln_kernel(ReduceLnArgs a) {
     o[1] = (bf16)v[j + 1];
     o[2] = (bf16)v[j + 2];
     o[3] = (bf16)v[j + 3];
-    *reinterpret_cast<bf16x4*>(a.xn + m * a.ld_xn + (j >> 2) * 256 + lane * 4) = o;
+    store_wt(reinterpret_cast<bf16x4*>(a.xn + m * a.ld_xn + (j >> 2) * 256 + lane * 4), o);
   }
 }
 

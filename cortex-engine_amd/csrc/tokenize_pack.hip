@@ -428,7 +428,7 @@ __global__ __launch_bounds__(256) void row_writer_kernel(RowArgs a) {
       } else {
         o = *reinterpret_cast<const V*>(s0 + d);
       }
-      *reinterpret_cast<V*>(out + d) = o;
+      store_wt(reinterpret_cast<V*>(out + d), o);
     }
   } else {
     for (int64_t d = lane; d < a.D; d += 64) {
