@@ -342,6 +342,7 @@ void attention_fast_kernel(AttnArgs a) {
     }
   }
   af_wait_vm(0);  // the last chunk's unused stages: no transfer into LDS outlives the workgroup
+  const bool wt = wt_one_wave();
 
 #pragma unroll
   for (int qg = 0; qg < QG; ++qg) {
@@ -355,7 +356,7 @@ void attention_fast_kernel(AttnArgs a) {
         bf16x4 v;
 #pragma unroll
         for (int i = 0; i < 4; ++i) v[i] = (bf16)(o_acc[qg][t][i] * inv);
-        store_wt(reinterpret_cast<bf16x4*>(O + 16 * t + 4 * g), v);
+        store_out(reinterpret_cast<bf16x4*>(O + 16 * t + 4 * g), v, wt);
       }
     }
   }

@@ -92,6 +92,28 @@ __device__ __forceinline__ void store_wt(V* p, const V& v) {
   }
 }
 
+// When write-through pays (measured on the Cortex-S forward, B = 32 / 64 / 256):
+//  * a GEMM or attention launch whose grid is a single wave of one workgroup per CU (MI355X:
+//    256 CUs) produces all its outputs at the end, so their write-back would run after the
+//    last store: written through, MLP-up, MLP-down and the kv projection are 1.8-2.5 us faster
+//    at B = 32.  With more workgroups than CUs the early ones' lines are written back while
+//    later ones run, and writing through only adds partial-line writes (3-12 % slower);
+//  * the LayerNorm row pass gains at every size (a streaming kernel with bf16 output);
+//  * the tokenizer gains while its output stays small (16 MiB at B = 32; 33 MiB at B = 64 loses).
+constexpr int WT_MAX_WORKGROUPS = 256;
+constexpr int64_t WT_MAX_BYTES = 24ll << 20;
+__device__ __forceinline__ bool wt_one_wave() {
+  return (int64_t)gridDim.x * gridDim.y * gridDim.z <= WT_MAX_WORKGROUPS;
+}
+__device__ __forceinline__ bool wt_fits(int64_t bytes) { return bytes <= WT_MAX_BYTES; }
+template <class V>
+__device__ __forceinline__ void store_out(V* p, const V& v, bool wt) {
+  if (wt)
+    store_wt(p, v);
+  else
+    *p = v;
+}
+
 // Operand element type of the direct-to-LDS GEMM loops: a 16-byte fragment per lane and the
 // MFMA that consumes it (bf16: 8 K-elements, fp32 accumulators; int8: 16 K-elements, int32
 // accumulators).  Both read 16 bytes per lane per operand, so LDS layouts carry over.

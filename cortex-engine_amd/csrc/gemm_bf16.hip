@@ -319,6 +319,7 @@ __global__ __launch_bounds__(TL::THREADS) void gemm_bf16_kernel(GemmArgs g) {
   //   !IL: tile j         -> n0 + wcol + 16 j + 4 g4 .. +3
   const float* bias = reinterpret_cast<const float*>(g.bias);
   TOUT* out = reinterpret_cast<TOUT*>(g.out) + (int64_t)kz * M * g.ld_out;
+  const bool wt = wt_one_wave();
   constexpr int NV = IL ? 8 : 4;           // consecutive columns per lane and group
   constexpr int NG = IL ? TN / 2 : TN;     // column groups per lane
   // Every scale and bias load first, then one wait: a wait left to the compiler would
@@ -373,7 +374,7 @@ __global__ __launch_bounds__(TL::THREADS) void gemm_bf16_kernel(GemmArgs g) {
         bf16x8 o;
 #pragma unroll
         for (int e = 0; e < 8; ++e) o[e] = (bf16)v[e];
-        store_wt(reinterpret_cast<bf16x8*>(op), o);
+        store_out(reinterpret_cast<bf16x8*>(op), o, wt);
       } else if constexpr (sizeof(TOUT) == 1) {  // int8 at the next linear's activation scale
         uint32_t lo = 0, hi = 0;
 #pragma unroll
@@ -383,11 +384,11 @@ __global__ __launch_bounds__(TL::THREADS) void gemm_bf16_kernel(GemmArgs g) {
           lo |= (uint32_t)(q0 & 0xff) << (8 * e);
           hi |= (uint32_t)(q1 & 0xff) << (8 * e);
         }
-        store_wt(reinterpret_cast<uint2*>(op), make_uint2(lo, hi));
+        store_out(reinterpret_cast<uint2*>(op), make_uint2(lo, hi), wt);
       } else {
 #pragma unroll
         for (int h = 0; h < NV / 4; ++h)
-          store_wt(reinterpret_cast<float4*>(op) + h, make_float4(v[4 * h], v[4 * h + 1], v[4 * h + 2], v[4 * h + 3]));
+          store_out(reinterpret_cast<float4*>(op) + h, make_float4(v[4 * h], v[4 * h + 1], v[4 * h + 2], v[4 * h + 3]), wt);
       }
     }
   }
@@ -625,6 +626,7 @@ __global__ __launch_bounds__(512) void norm_gemm_rk_kernel(NormGemmArgs g) {
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int pr = wid & 3, c2 = wid >> 2;  // row pair (rows 32 pr ..) and column half
   const int M = (int)g.M, N = (int)g.N, K = (int)g.K, nk = K / 64;
+  const bool wt = wt_one_wave();
   const int G = gridDim.x, total = gridDim.x * gridDim.y;
   const int id = xcd_affine(blockIdx.x + G * blockIdx.y, total);
   const int m0 = (id / G) * TL::BM, grp = id % G;
@@ -901,10 +903,10 @@ __global__ __launch_bounds__(512) void norm_gemm_rk_kernel(NormGemmArgs g) {
         bf16x8 o;
 #pragma unroll
         for (int e = 0; e < 8; ++e) o[e] = (bf16)v[e];
-        store_wt(reinterpret_cast<bf16x8*>(op), o);
+        store_out(reinterpret_cast<bf16x8*>(op), o, wt);
       } else {
-        store_wt(reinterpret_cast<float4*>(op), make_float4(v[0], v[1], v[2], v[3]));
-        store_wt(reinterpret_cast<float4*>(op + 4), make_float4(v[4], v[5], v[6], v[7]));
+        store_out(reinterpret_cast<float4*>(op), make_float4(v[0], v[1], v[2], v[3]), wt);
+        store_out(reinterpret_cast<float4*>(op + 4), make_float4(v[4], v[5], v[6], v[7]), wt);
       }
     }
   };
