@@ -626,7 +626,10 @@ __global__ __launch_bounds__(512) void norm_gemm_rk_kernel(NormGemmArgs g) {
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int pr = wid & 3, c2 = wid >> 2;  // row pair (rows 32 pr ..) and column half
   const int M = (int)g.M, N = (int)g.N, K = (int)g.K, nk = K / 64;
-  const bool wt = wt_one_wave();
+  // plain stores: wavefronts w and w + 4 write alternate 16-byte pieces of each 128-byte output
+  // line, which the L2 merges; written through, each half crosses to memory on its own (twice
+  // the write bytes, no time saved)
+  constexpr bool wt = false;
   const int G = gridDim.x, total = gridDim.x * gridDim.y;
   const int id = xcd_affine(blockIdx.x + G * blockIdx.y, total);
   const int m0 = (id / G) * TL::BM, grp = id % G;
