@@ -193,13 +193,172 @@ void attention_fast_kernel(AttnArgs a) {
     }
     return __ballot(ok);
   };
-  int wbase = 0, kc = 0;
+  int wbase = 0;
   uint64_t pend = MASK ? wg_window(0) : 0;
 
-  for (bool first = true;; first = false) {
-    int tl[AF_CH];
-    int nc = 0;
-    if (MASK) {
+  // ---- the loads of tile t (keys clamped to the sample) into stage j: the K transfer and
+  // this lane's two V rows (V^T is written from registers once they land)
+  auto issue_tile = [&](int t, int j, uint2& va, uint2& vb) {
+    const int64_t k0 = (int64_t)t * AF_KT;
+    const int64_t kr = min(k0 + k_row, len - 1);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+        k_rsrc, (__attribute__((address_space(3))) void*)(k_stage(j) + wid * 1024), 16,
+        (int)(uint32_t)((kr * a.k_sl + k_col) * 2), 0, 0, 0);
+    const int64_t ka = min(k0 + 2 * kp, len - 1), kb = min(k0 + 2 * kp + 1, len - 1);
+    va = *reinterpret_cast<const uint2*>(v_src + ka * a.v_sl);
+    vb = *reinterpret_cast<const uint2*>(v_src + kb * a.v_sl);
+    __builtin_amdgcn_sched_barrier(0);  // keep the issue order tile by tile (vmcnt below)
+  };
+  // V^T: dword (V[2kp][4dq+e], V[2kp+1][4dq+e]) into row 4dq+e, column kp of stage j
+  auto write_vt = [&](int j, const uint2& va, const uint2& vb) {
+    unsigned char* base = v_stage(j) + (4 * dq) * AF_VP + kp * 4;
+    const uint32_t a0 = va.x, a1 = va.y, b0 = vb.x, b1 = vb.y;
+    *reinterpret_cast<uint32_t*>(base + 0 * AF_VP) = (a0 & 0xffffu) | (b0 << 16);
+    *reinterpret_cast<uint32_t*>(base + 1 * AF_VP) = (a0 >> 16) | (b0 & 0xffff0000u);
+    *reinterpret_cast<uint32_t*>(base + 2 * AF_VP) = (a1 & 0xffffu) | (b1 << 16);
+    *reinterpret_cast<uint32_t*>(base + 3 * AF_VP) = (a1 >> 16) | (b1 & 0xffff0000u);
+  };
+  // ---- scores S^T = K Q^T of the key tile in stage j (16-query groups with okq set)
+  typedef f32x4 Scores[QG][4];
+  auto scores = [&](int j, const bool (&okq)[QG], Scores& s) {
+    const unsigned char* ks_ = k_stage(j);
+#pragma unroll
+    for (int st = 0; st < 4; ++st) {
+      const bf16x8 k0f = *reinterpret_cast<const bf16x8*>(ks_ + k_off[st][0]);
+      const bf16x8 k1f = *reinterpret_cast<const bf16x8*>(ks_ + k_off[st][1]);
+#pragma unroll
+      for (int qg = 0; qg < QG; ++qg) {
+        f32x4 acc = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+        if (!okq[qg]) continue;
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k0f, qf[qg][0], acc, 0, 0, 0);
+        s[qg][st] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k1f, qf[qg][1], acc, 0, 0, 0);
+      }
+    }
+  };
+  // ---- online softmax of the scores of key tile kt, then P V with its V^T in stage j
+  auto softmax_pv = [&](int kt, int j, const bool (&okq)[QG], Scores& s) {
+    const unsigned char* vs_ = v_stage(j);
+    const int64_t rem64 = len - (int64_t)kt * AF_KT;
+    if (rem64 < AF_KT) {  // last, partial tile: mask keys past the sample's length
+      const int rem = (int)rem64;
+#pragma unroll
+      for (int st = 0; st < 4; ++st)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (32 * (st >> 1) + 8 * g + 4 * (st & 1) + i >= rem) {
+#pragma unroll
+            for (int qg = 0; qg < QG; ++qg) s[qg][st][i] = -INFINITY;
+          }
+    }
+    bf16x8 pf[QG][2];
+#pragma unroll
+    for (int qg = 0; qg < QG; ++qg) {
+      if (!okq[qg]) continue;
+      // Lane-local max first: the reference max only has to move (and the lane groups
+      // only have to agree on a new one) when some score exceeds it by AF_RESCALE.
+      float mx = s[qg][0][0];
+#pragma unroll
+      for (int st = 0; st < 4; ++st)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) mx = fmaxf(mx, s[qg][st][i]);
+      // wave-uniform, rare after the group's first tile (m_run = -inf always enters)
+      if (__any(mx * sl > m_run[qg] + AF_RESCALE)) {
+        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        const float m_tile = mx * sl;  // finite: every tile holds at least one valid key
+        if (m_run[qg] == -INFINITY) {
+          m_run[qg] = m_tile;
+        } else {
+          const float m_new = fmaxf(m_run[qg], m_tile);
+          const float alpha = __builtin_amdgcn_exp2f(m_run[qg] - m_new);
+          m_run[qg] = m_new;
+          l_acc[qg] *= alpha;
+#pragma unroll
+          for (int t = 0; t < 4; ++t) o_acc[qg][t] *= alpha;
+        }
+      }
+#pragma unroll
+      for (int c = 0; c < 2; ++c)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          pf[qg][c][i] = (bf16)__builtin_amdgcn_exp2f(fmaf(s[qg][2 * c][i], sl, -m_run[qg]));  // -inf -> 0
+          pf[qg][c][4 + i] = (bf16)__builtin_amdgcn_exp2f(fmaf(s[qg][2 * c + 1][i], sl, -m_run[qg]));
+        }
+    }
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+#pragma unroll
+      for (int qg = 0; qg < QG; ++qg)
+        if (okq[qg]) l_acc[qg] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pf[qg][c], l_acc[qg], 0, 0, 0);
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const bf16x8 vf = *reinterpret_cast<const bf16x8*>(vs_ + v_off[c][t]);
+#pragma unroll
+        for (int qg = 0; qg < QG; ++qg)
+          if (okq[qg]) o_acc[qg][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pf[qg][c], o_acc[qg][t], 0, 0, 0);
+      }
+    }
+  };
+  // the tile-mask path: scores, softmax and P V of tile kt in stage j, one after the other
+  auto do_tile = [&](int kt, int j) {
+    bool okq[QG];  // this 16-query group multiplies tile kt
+    bool any = false;
+#pragma unroll
+    for (int qg = 0; qg < QG; ++qg) {
+      okq[qg] = mk.at(qrow[qg], kt / mk.kpt);
+      any = any || okq[qg];
+    }
+    if (!any) return;
+    Scores s;
+    scores(j, okq, s);
+    softmax_pv(kt, j, okq, s);
+  };
+
+  uint2 va[AF_CH], vb[AF_CH];
+  if constexpr (!MASK) {
+    // Dense keys: the stages form a ring, and the tiles are software-pipelined.  Tiles 0..3
+    // are issued up front.  Iteration kt makes tile kt + 1 visible (V^T written, barrier),
+    // issues its score MFMAs, and only then runs the softmax and P V of tile kt, whose scores
+    // the previous iteration produced: the matrix core works on tile kt + 1 while the VALU
+    // evaluates tile kt's exponentials.  After that barrier every wavefront is done with tile
+    // kt - 1, so its stage is refilled with tile kt + 3 (clamped past the end: issued, never
+    // read).  Each tile is 3 loads; the waits name the tiles issued after the awaited one.
+    bool all[QG];
+#pragma unroll
+    for (int qg = 0; qg < QG; ++qg) all[qg] = true;
+    Scores sc[2];
+    if (nt > 0) {  // (no keys: nothing is loaded, the rows give 0)
+#pragma unroll
+      for (int t = 0; t < AF_CH; ++t) issue_tile(min(t, nt - 1), t, va[t], vb[t]);
+      af_wait_vm(9);
+      write_vt(0, va[0], vb[0]);
+      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's V^T stores are done
+      __builtin_amdgcn_s_barrier();
+      scores(0, all, sc[0]);
+    }
+    for (int kt0 = 0; kt0 < nt; kt0 += AF_CH) {
+#pragma unroll
+      for (int t = 0; t < AF_CH; ++t) {
+        const int kt = kt0 + t;
+        if (kt >= nt) break;
+        const int tn = (t + 1) & 3;  // stage of tile kt + 1
+        if (kt + 1 < nt) {
+          af_wait_vm(kt == 0 ? 6 : 3);
+          write_vt(tn, va[tn], vb[tn]);
+          __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): V^T stores and tile kt-1's reads done
+          __builtin_amdgcn_s_barrier();        // tile kt+1 visible; stage of tile kt-1 free
+          if (kt >= 1) issue_tile(min(kt + 3, nt - 1), (t + 3) & 3, va[(t + 3) & 3], vb[(t + 3) & 3]);
+          scores(tn, all, sc[(t + 1) & 1]);
+        }
+        softmax_pv(kt, t, all, sc[t & 1]);
+      }
+    }
+  } else {
+    // Tile mask: the workgroup's allowed tiles come from ballot windows, taken in chunks of
+    // AF_CH tiles whose loads are all issued at once.
+    for (bool first = true;; first = false) {
+      int tl[AF_CH];
+      int nc = 0;
 #pragma unroll
       for (int j = 0; j < AF_CH; ++j) {
         while (pend == 0 && wbase + 64 < nt) {
@@ -214,130 +373,21 @@ void attention_fast_kernel(AttnArgs a) {
           tl[j] = j > 0 ? tl[j - 1] : 0;  // loaded, never used
         }
       }
-    } else {
-      nc = min(AF_CH, nt - kc);
+      if (nc <= 0) break;
+      if (!first) __syncthreads();  // every wave is done with the previous chunk's stages
+      // Stages past the chunk's last tile are filled too (clamped keys) and never read:
+      // unconditional issue keeps the load counter exact, so each tile below waits for its
+      // own loads only (vmcnt(3 (AF_CH-1-j)): tile j's K transfer and V registers are in).
 #pragma unroll
-      for (int j = 0; j < AF_CH; ++j) tl[j] = kc + j;
-      kc += AF_CH;
-    }
-    if (nc <= 0) break;
-    if (!first) __syncthreads();  // every wave is done with the previous chunk's stages
-    // ---- issue every load of the chunk. Stages past the chunk's last tile are filled
-    // too (clamped keys) and never read: unconditional issue keeps the load counter
-    // exact, so each tile below waits for its own loads only.
-    uint2 va[AF_CH], vb[AF_CH];
+      for (int j = 0; j < AF_CH; ++j) issue_tile(tl[j], j, va[j], vb[j]);
 #pragma unroll
-    for (int j = 0; j < AF_CH; ++j) {
-      const int64_t k0 = (int64_t)tl[j] * AF_KT;
-      const int64_t kr = min(k0 + k_row, len - 1);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          k_rsrc, (__attribute__((address_space(3))) void*)(k_stage(j) + wid * 1024), 16,
-          (int)(uint32_t)((kr * a.k_sl + k_col) * 2), 0, 0, 0);
-      const int64_t ka = min(k0 + 2 * kp, len - 1), kb = min(k0 + 2 * kp + 1, len - 1);
-      va[j] = *reinterpret_cast<const uint2*>(v_src + ka * a.v_sl);
-      vb[j] = *reinterpret_cast<const uint2*>(v_src + kb * a.v_sl);
-      __builtin_amdgcn_sched_barrier(0);  // keep the issue order tile by tile (vmcnt below)
-    }
-    // Tiles are handed to the MFMAs one by one as their loads land: vmcnt counts the 3
-    // loads per tile in issue order, so vmcnt(3 (AF_CH-1-j)) means tile j's K transfer
-    // and V registers are in, and the raw barrier does not drain the later tiles' loads.
-#pragma unroll
-    for (int j = 0; j < AF_CH; ++j) {
-      if (j >= nc) break;
-      af_wait_vm(3 * (AF_CH - 1 - j));
-      {  // V^T: dword (V[2kp][4dq+e], V[2kp+1][4dq+e]) into row 4dq+e, column kp
-        unsigned char* base = v_stage(j) + (4 * dq) * AF_VP + kp * 4;
-        const uint32_t a0 = va[j].x, a1 = va[j].y, b0 = vb[j].x, b1 = vb[j].y;
-        *reinterpret_cast<uint32_t*>(base + 0 * AF_VP) = (a0 & 0xffffu) | (b0 << 16);
-        *reinterpret_cast<uint32_t*>(base + 1 * AF_VP) = (a0 >> 16) | (b0 & 0xffff0000u);
-        *reinterpret_cast<uint32_t*>(base + 2 * AF_VP) = (a1 & 0xffffu) | (b1 << 16);
-        *reinterpret_cast<uint32_t*>(base + 3 * AF_VP) = (a1 >> 16) | (b1 & 0xffff0000u);
-      }
-      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's V^T stores are done
-      __builtin_amdgcn_s_barrier();        // tile j's K transfers and V^T rows visible to all
-      const int kt = tl[j];
-      bool okq[QG];  // this 16-query group multiplies tile kt
-      bool any = !MASK;
-#pragma unroll
-      for (int qg = 0; qg < QG; ++qg) {
-        okq[qg] = !MASK || mk.at(qrow[qg], kt / mk.kpt);
-        any = any || okq[qg];
-      }
-      if (!any) continue;
-      const unsigned char* ks_ = k_stage(j);
-      const unsigned char* vs_ = v_stage(j);
-      f32x4 s[QG][4];
-#pragma unroll
-      for (int st = 0; st < 4; ++st) {
-        const bf16x8 k0f = *reinterpret_cast<const bf16x8*>(ks_ + k_off[st][0]);
-        const bf16x8 k1f = *reinterpret_cast<const bf16x8*>(ks_ + k_off[st][1]);
-#pragma unroll
-        for (int qg = 0; qg < QG; ++qg) {
-          f32x4 acc = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
-          if (!okq[qg]) continue;
-          acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k0f, qf[qg][0], acc, 0, 0, 0);
-          s[qg][st] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k1f, qf[qg][1], acc, 0, 0, 0);
-        }
-      }
-      const int64_t rem64 = len - (int64_t)kt * AF_KT;
-      if (rem64 < AF_KT) {  // last, partial tile: mask keys past the sample's length
-        const int rem = (int)rem64;
-#pragma unroll
-        for (int st = 0; st < 4; ++st)
-#pragma unroll
-          for (int i = 0; i < 4; ++i)
-            if (32 * (st >> 1) + 8 * g + 4 * (st & 1) + i >= rem) {
-#pragma unroll
-              for (int qg = 0; qg < QG; ++qg) s[qg][st][i] = -INFINITY;
-            }
-      }
-      bf16x8 pf[QG][2];
-#pragma unroll
-      for (int qg = 0; qg < QG; ++qg) {
-        if (!okq[qg]) continue;
-        // Lane-local max first: the reference max only has to move (and the lane groups
-        // only have to agree on a new one) when some score exceeds it by AF_RESCALE.
-        float mx = s[qg][0][0];
-#pragma unroll
-        for (int st = 0; st < 4; ++st)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) mx = fmaxf(mx, s[qg][st][i]);
-        // wave-uniform, rare after the group's first tile (m_run = -inf always enters)
-        if (__any(mx * sl > m_run[qg] + AF_RESCALE)) {
-          mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-          mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-          const float m_tile = mx * sl;  // finite: every tile holds at least one valid key
-          if (m_run[qg] == -INFINITY) {
-            m_run[qg] = m_tile;
-          } else {
-            const float m_new = fmaxf(m_run[qg], m_tile);
-            const float alpha = __builtin_amdgcn_exp2f(m_run[qg] - m_new);
-            m_run[qg] = m_new;
-            l_acc[qg] *= alpha;
-#pragma unroll
-            for (int t = 0; t < 4; ++t) o_acc[qg][t] *= alpha;
-          }
-        }
-#pragma unroll
-        for (int c = 0; c < 2; ++c)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            pf[qg][c][i] = (bf16)__builtin_amdgcn_exp2f(fmaf(s[qg][2 * c][i], sl, -m_run[qg]));  // -inf -> 0
-            pf[qg][c][4 + i] = (bf16)__builtin_amdgcn_exp2f(fmaf(s[qg][2 * c + 1][i], sl, -m_run[qg]));
-          }
-      }
-#pragma unroll
-      for (int c = 0; c < 2; ++c) {
-#pragma unroll
-        for (int qg = 0; qg < QG; ++qg)
-          if (okq[qg]) l_acc[qg] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pf[qg][c], l_acc[qg], 0, 0, 0);
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          const bf16x8 vf = *reinterpret_cast<const bf16x8*>(vs_ + v_off[c][t]);
-#pragma unroll
-          for (int qg = 0; qg < QG; ++qg)
-            if (okq[qg]) o_acc[qg][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pf[qg][c], o_acc[qg][t], 0, 0, 0);
-        }
+      for (int j = 0; j < AF_CH; ++j) {
+        if (j >= nc) break;
+        af_wait_vm(3 * (AF_CH - 1 - j));
+        write_vt(j, va[j], vb[j]);
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's V^T stores are done
+        __builtin_amdgcn_s_barrier();        // tile j's K transfers and V^T rows visible to all
+        do_tile(tl[j], j);
       }
     }
   }

@@ -25,7 +25,7 @@ def _close(got: np.ndarray, ref: np.ndarray, frac: float = 1e-2):
     assert err <= tol, f"max |err| {err:.3e} > {tol:.3e}"
 
 
-@pytest.mark.parametrize("lens", [[512, 300, 1, 0, 63, 64, 65, 640], [128] * 4, [7, 700, 129]])
+@pytest.mark.parametrize("lens", [[512, 300, 1, 0, 63, 64, 65, 640], [128] * 4, [7, 700, 129], [2048, 5, 1500, 0]])
 def test_csr_cross_attention_bf16(lens):
     """Batch-invariant latent queries (q batch stride 0) against ragged CSR keys."""
     from cortex.kernels import ops
