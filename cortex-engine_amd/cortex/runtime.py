@@ -1,6 +1,6 @@
 """HIP-graph capture of the Cortex forward for a fixed (batch_size, n_events).
 
-The forward is a fixed sequence of ~60 kernel launches once B and the total event
+The forward is a fixed sequence of ~45 kernel launches once B and the total event
 count are known (the pack plan and every per-sample length live on the device).
 Capturing it once and replaying removes the host launch cost, which dominates at
 small batches (serving latency at B = 1).
@@ -16,15 +16,23 @@ from cortex.models.cortex import CortexModel, _raise_on_flag
 class CapturedForward:
     """Replayable ``model(neuron_ids, time_bins, values, batch_indices)["behavior"]``.
 
-    Inputs are copied into static device buffers before each replay; the returned
-    tensor is the graph's static output (clone it to keep it past the next call).
-    ``err_flag`` is cleared before every replay, so after a call it holds that call's
-    index-range violations only; with ``check_indices=True`` each call reads it back
-    (one synchronisation) and raises ``IndexError`` as ``CortexModel.forward`` does.
+    The graph reads its events from four static int64 device buffers of length
+    ``n_events``.  By default they are allocated here and ``cap(nid, tb, val, bidx)`` copies
+    the caller's tensors into them before each replay.  A caller whose events already live in
+    device buffers it owns can pass them as ``inputs=(nid, tb, val, bidx)``: the graph is then
+    captured on those buffers, and ``cap()`` replays on whatever they hold, with no copies.
+    Writing new events into them (``cap.neuron_ids.copy_(...)``, an H2D straight from pinned
+    memory, ...) before ``cap()`` serves the next request.
+
+    The returned tensor is the graph's static output (clone it to keep it past the next call).
+    ``err_flag`` is cleared at the start of every replay (a fill kernel inside the graph), so
+    after a call it holds that call's index-range violations only; with
+    ``check_indices=True`` each call reads it back (one synchronisation) and raises
+    ``IndexError`` as ``CortexModel.forward`` does.
     """
 
     def __init__(self, model: CortexModel, batch_size: int, n_events: int, warmup: int = 2, *,
-                 check_indices: bool = False) -> None:
+                 check_indices: bool = False, inputs: tuple[torch.Tensor, ...] | None = None) -> None:
         if n_events < 1 or batch_size < 1:
             raise ValueError("need batch_size >= 1 and n_events >= 1")
         dev = next(model.parameters()).device
@@ -34,10 +42,19 @@ class CapturedForward:
         self.check_indices = check_indices
         self.batch_size = batch_size
         self.n_events = n_events
-        self.neuron_ids = torch.zeros(n_events, dtype=torch.int64, device=dev)
-        self.time_bins = torch.zeros(n_events, dtype=torch.int64, device=dev)
-        self.values = torch.zeros(n_events, dtype=torch.int64, device=dev)
-        self.batch_indices = (torch.arange(n_events, device=dev) * batch_size) // n_events
+        if inputs is None:
+            self.neuron_ids = torch.zeros(n_events, dtype=torch.int64, device=dev)
+            self.time_bins = torch.zeros(n_events, dtype=torch.int64, device=dev)
+            self.values = torch.zeros(n_events, dtype=torch.int64, device=dev)
+            self.batch_indices = (torch.arange(n_events, device=dev) * batch_size) // n_events
+        else:
+            if len(inputs) != 4:
+                raise ValueError("inputs must be (neuron_ids, time_bins, values, batch_indices)")
+            for t in inputs:
+                if (t.device != dev or t.dtype != torch.int64 or t.dim() != 1 or t.shape[0] != n_events
+                        or not t.is_contiguous()):
+                    raise ValueError(f"inputs must be contiguous int64 ({n_events},) tensors on {dev}")
+            self.neuron_ids, self.time_bins, self.values, self.batch_indices = inputs
         self.err_flag = torch.zeros(1, dtype=torch.int32, device=dev)
         side = torch.cuda.Stream(device=dev)
         side.wait_stream(torch.cuda.current_stream(dev))
@@ -50,17 +67,20 @@ class CapturedForward:
             self.output = self._run()
 
     def _run(self) -> torch.Tensor:
+        self.err_flag.zero_()  # a fill kernel (captured: no memset node in the graph)
         return self.model(self.neuron_ids, self.time_bins, self.values, self.batch_indices,
                           batch_size=self.batch_size, err_flag=self.err_flag)["behavior"]
 
-    def __call__(self, neuron_ids, time_bins, values, batch_indices) -> torch.Tensor:
-        if neuron_ids.shape[0] != self.n_events:
-            raise ValueError(f"captured for {self.n_events} events, got {neuron_ids.shape[0]}")
-        self.neuron_ids.copy_(neuron_ids, non_blocking=True)
-        self.time_bins.copy_(time_bins, non_blocking=True)
-        self.values.copy_(values, non_blocking=True)
-        self.batch_indices.copy_(batch_indices, non_blocking=True)
-        self.err_flag.zero_()  # a fill kernel, outside the graph
+    def __call__(self, *events: torch.Tensor) -> torch.Tensor:
+        """Replay on the static buffers; with four tensors, copy them in first."""
+        if events:
+            if len(events) != 4:
+                raise ValueError("pass (neuron_ids, time_bins, values, batch_indices) or nothing")
+            if events[0].shape[0] != self.n_events:
+                raise ValueError(f"captured for {self.n_events} events, got {events[0].shape[0]}")
+            for dst, src in zip((self.neuron_ids, self.time_bins, self.values, self.batch_indices), events):
+                if src.data_ptr() != dst.data_ptr():
+                    dst.copy_(src, non_blocking=True)
         self.graph.replay()
         if self.check_indices:
             _raise_on_flag(self.err_flag)

@@ -168,6 +168,36 @@ def test_captured_graph_replays_match_eager():
         torch.testing.assert_close(got, want, rtol=0, atol=0)
 
 
+def test_captured_graph_on_caller_buffers():
+    """A graph captured on the caller's event buffers replays whatever they hold (no copies), and
+    the error flag is cleared inside every replay: an out-of-range call leaves it set, the next
+    valid call clears it."""
+    from cortex.runtime import CapturedForward
+
+    model = _int8(_model("s", "bfloat16"), [torch.from_numpy(a).to(DEV) for a in _config3_inputs(2, 64)])
+    bufs = tuple(torch.from_numpy(a).to(DEV) for a in _config3_inputs(4, 300, seed=30))
+    cap = CapturedForward(model, batch_size=4, n_events=4 * 300, inputs=bufs)
+    assert cap.neuron_ids.data_ptr() == bufs[0].data_ptr()
+    for seed in range(3):
+        new = [torch.from_numpy(a).to(DEV) for a in _config3_inputs(4, 300, seed=40 + seed)]
+        for dst, src in zip(bufs, new):
+            dst.copy_(src)
+        got = cap().clone()
+        with torch.no_grad():
+            want = model(*new, batch_size=4)["behavior"]
+        torch.cuda.synchronize()
+        torch.testing.assert_close(got, want, rtol=0, atol=0)
+    good = bufs[0].clone()
+    bufs[0][5] = 10_000
+    cap()
+    assert int(cap.err_flag.item()) & 1
+    bufs[0].copy_(good)
+    cap()
+    assert int(cap.err_flag.item()) == 0
+    with pytest.raises(ValueError):
+        CapturedForward(model, batch_size=4, n_events=4 * 300, inputs=bufs[:3])
+
+
 def test_invalid_token_index_sets_error_flag():
     model = _model("xs", "bfloat16")
     nid, tb, val, bidx = (torch.from_numpy(a).to(DEV) for a in _config3_inputs(2, 50))
