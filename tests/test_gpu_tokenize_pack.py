@@ -243,7 +243,7 @@ def _sorted_cases():
 
 @pytest.mark.parametrize("name", list(_sorted_cases()))
 def test_pack_plan_sorted_fast_path(name):
-    """Sorted batch indices take the identity plan (pack_sorted_kernel); anything else found
+    """Sorted batch indices take the identity plan (pack_small_kernel's first pass); anything else found
     there -- an inversion, an index out of range -- falls back to the full plan.  Same
     results as the oracle either way, with and without ranks."""
     from cortex.kernels import ops
