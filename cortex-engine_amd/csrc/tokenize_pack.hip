@@ -183,55 +183,95 @@ constexpr int PS_WAVES = 16;
 constexpr int PS_MAX_B = 1024;
 constexpr int64_t PS_MAX_E = 65536;
 constexpr int PS_UNROLL = 16;
-constexpr int PS_SORT_UNROLL = 8;
+
+// Sorted batch indices (the collate order) need no sort: the plan is the identity and
+// offsets[s] is the first event of sample s.  Event e (index b, the event before it bp; -1
+// for the first event) writes its identity row and the offsets of the samples bp+1 .. b
+// (empty ones too), which start at e; the last event closes the samples after it.  Returns
+// false, writing nothing, when e breaks the order or an index is out of range.  (bp is -1
+// only for the first event: a negative index before e is out of range, and taking it as the
+// loop start would write offsets[] below index 0.)
+__device__ __forceinline__ bool sorted_event(int64_t e, int64_t b, int64_t bp, int64_t E, int B,
+                                             int64_t* __restrict__ offsets, int64_t* __restrict__ order,
+                                             int64_t* __restrict__ dst_rows) {
+  if (b < 0 || b >= B || bp > b || (e > 0 && bp < 0)) return false;
+  order[e] = e;
+  if (dst_rows) dst_rows[e] = e;
+  for (int64_t s = bp + 1; s <= b; ++s) offsets[s] = e;
+  if (e == E - 1)
+    for (int64_t s = b + 1; s <= B; ++s) offsets[s] = E;
+  return true;
+}
+
+// Above PS_ONE_E events the sorted check runs wide first: one workgroup per PS_SORTED_EV
+// events applies sorted_event to its range and records in status[blockIdx.x] whether the
+// range (with the event before it) was sorted and in range: 1 yes, 2 no.  pack_small_kernel
+// then returns at once when every status is 1 and otherwise recomputes the whole plan.  Up
+// to PS_ONE_E events pack_small_kernel makes the check itself (one round of loads per
+// thread), so a plan is one launch.
+constexpr int PS_SORTED_EV = 1024;
+constexpr int PS_ONE_UNROLL = 8;
+constexpr int64_t PS_ONE_E = 64 * PS_WAVES * PS_ONE_UNROLL;
+
+__global__ __launch_bounds__(256) void pack_sorted_kernel(const int64_t* __restrict__ bidx, int64_t s_bidx,
+                                                          int64_t E, int B, int64_t* __restrict__ offsets,
+                                                          int64_t* __restrict__ order, int64_t* __restrict__ dst_rows,
+                                                          int* __restrict__ status) {
+  __shared__ int bad;
+  if (threadIdx.x == 0) bad = 0;
+  __syncthreads();
+  const int64_t c0 = (int64_t)blockIdx.x * PS_SORTED_EV;
+  bool my_bad = false;
+  for (int k = threadIdx.x; k < PS_SORTED_EV; k += blockDim.x) {
+    const int64_t e = c0 + k;
+    if (e >= E) break;
+    const int64_t b = bidx[e * s_bidx];
+    const int64_t bp = e > 0 ? bidx[(e - 1) * s_bidx] : -1;
+    if (!sorted_event(e, b, bp, E, B, offsets, order, dst_rows)) my_bad = true;
+  }
+  if (my_bad) bad = 1;
+  __syncthreads();
+  if (threadIdx.x == 0) status[blockIdx.x] = bad ? 2 : 1;
+}
 
 __global__ __launch_bounds__(1024) void pack_small_kernel(const int64_t* __restrict__ bidx, int64_t s_bidx, int64_t E,
                                                           int B, int64_t* __restrict__ offsets,
                                                           int64_t* __restrict__ order, int64_t* __restrict__ dst_rows,
                                                           int64_t* __restrict__ rank, int32_t* __restrict__ err,
+                                                          const int* __restrict__ status, int n_status,
                                                           bool try_sorted) {
   __shared__ int cnt[PS_WAVES * PS_MAX_B];  // per-wave counts, then per-wave next CSR row
   __shared__ int first[PS_MAX_B];           // CSR offset of each sample
   __shared__ int wsum[PS_WAVES];
   __shared__ int unsorted;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  if (try_sorted) {
-    // Sorted batch indices (the collate order) need no sort: the plan is the identity and
-    // offsets[s] is the first event of sample s, written by the one event where the index
-    // steps past s (empty samples included).  Any inversion or index out of range found
-    // here sends the whole workgroup on to the full plan below, which rewrites every
-    // offset and every CSR row of `order`.
+  if (status) {  // after pack_sorted_kernel: nothing left to do when every range was sorted
     if (tid == 0) unsorted = 0;
     __syncthreads();
+    for (int i = tid; i < n_status; i += blockDim.x)
+      if (status[i] != 1) unsorted = 1;
+    __syncthreads();
+    if (!unsorted) return;
+  } else if (try_sorted) {  // E <= PS_ONE_E: the sorted check here, every load issued first
+    if (tid == 0) unsorted = 0;
+    __syncthreads();
+    int64_t bv[PS_ONE_UNROLL], pv[PS_ONE_UNROLL];
+#pragma unroll
+    for (int u = 0; u < PS_ONE_UNROLL; ++u) {
+      const int64_t e = (int64_t)u * blockDim.x + tid;
+      bv[u] = e < E ? bidx[e * s_bidx] : 0;
+      pv[u] = (e < E && e > 0) ? bidx[(e - 1) * s_bidx] : -1;
+    }
     bool my_bad = false;
-    for (int64_t base = 0; base < E; base += (int64_t)blockDim.x * PS_SORT_UNROLL) {
-      int64_t bv[PS_SORT_UNROLL], pv[PS_SORT_UNROLL];  // every load in flight before the checks
 #pragma unroll
-      for (int u = 0; u < PS_SORT_UNROLL; ++u) {
-        const int64_t e = base + (int64_t)u * blockDim.x + tid;
-        bv[u] = e < E ? bidx[e * s_bidx] : 0;
-        pv[u] = (e < E && e > 0) ? bidx[(e - 1) * s_bidx] : -1;
-      }
-#pragma unroll
-      for (int u = 0; u < PS_SORT_UNROLL; ++u) {
-        const int64_t e = base + (int64_t)u * blockDim.x + tid;
-        if (e >= E) break;
-        const int64_t b = bv[u], bp = pv[u];
-        // bp is -1 only for the first event: a negative index before e is out of range, and
-        // taking it as the loop start below would write offsets[] below index 0.
-        if (b < 0 || b >= B || bp > b || (e > 0 && bp < 0)) {
-          my_bad = true;
-          continue;
-        }
-        order[e] = e;
-        if (dst_rows) dst_rows[e] = e;
-        for (int64_t s = bp + 1; s <= b; ++s) offsets[s] = e;  // samples bp+1 .. b start at e
-        if (e == E - 1)
-          for (int64_t s = b + 1; s <= B; ++s) offsets[s] = E;
-      }
+    for (int u = 0; u < PS_ONE_UNROLL; ++u) {
+      const int64_t e = (int64_t)u * blockDim.x + tid;
+      if (e < E && !sorted_event(e, bv[u], pv[u], E, B, offsets, order, dst_rows)) my_bad = true;
     }
     if (my_bad) unsorted = 1;
-    __threadfence_block();  // the identity writes complete before any rewrite below
+    // the identity writes complete before the full plan below rewrites every offset and
+    // every CSR row of `order`
+    __threadfence_block();
     __syncthreads();
     if (!unsorted) return;
   }
@@ -528,9 +568,20 @@ static int pack_plan_impl(const char* who, const int64_t* batch_indices, int64_t
     return E_WORKSPACE;
   }
   if (B <= PS_MAX_B && E <= PS_MAX_E) {
-    // without ranks the kernel first tries the identity plan of sorted indices
+    // without ranks, the identity plan of sorted indices first: inside the one launch up to
+    // PS_ONE_E events, above that in the wide pack_sorted_kernel (one status word per 1024
+    // events, in the workspace: cortex_pack_workspace_bytes covers them)
+    int* status = nullptr;
+    const int n_status = (int)cdiv(E, (int64_t)PS_SORTED_EV);
+    const bool one = rank == nullptr && E <= PS_ONE_E;
+    if (rank == nullptr && !one && workspace != nullptr && workspace_bytes >= n_status * (int64_t)sizeof(int)) {
+      status = reinterpret_cast<int*>(workspace);
+      hipLaunchKernelGGL(pack_sorted_kernel, dim3((unsigned)n_status), dim3(256), 0, stream, batch_indices, s_bidx, E,
+                         (int)B, offsets, order, dst_rows, status);
+      CORTEX_CHECK_LAUNCH("pack_sorted_kernel");
+    }
     hipLaunchKernelGGL(pack_small_kernel, dim3(1), dim3(64 * PS_WAVES), 0, stream, batch_indices, s_bidx, E, (int)B,
-                       offsets, order, dst_rows, rank, err_flag, rank == nullptr);
+                       offsets, order, dst_rows, rank, err_flag, status, n_status, one);
     CORTEX_CHECK_LAUNCH("pack_small_kernel");
     return OK;
   }
@@ -548,8 +599,9 @@ static int pack_plan_impl(const char* who, const int64_t* batch_indices, int64_t
   return OK;
 }
 
-// Scratch of cortex_pack_plan_noalloc: the per-chunk counts of the three-launch plan that
-// cortex_pack_plan keeps in the caller's workspace.  One copy per GPU, held until the process ends.  In host code `scratch`
+// Scratch of cortex_pack_plan_noalloc: the per-chunk counts (three-launch plan) or the
+// per-range status words (wide sorted check) that cortex_pack_plan keeps in the caller's
+// workspace.  One copy per GPU, held until the process ends.  In host code `scratch`
 // only names the symbol: its device address comes from hipGetSymbolAddress, once per
 // device, and only that address is ever handed to a kernel.
 constexpr int64_t PACK_SCRATCH_BYTES = (int64_t)4 << 20;

@@ -238,12 +238,22 @@ def _sorted_cases():
     b = np.sort(rng.integers(0, 6, 2500))
     b[1024] = -7  # first event of the second range
     cases["negative_at_range_start"] = (b, 6)
+    # above 8192 events the check runs wide (a workgroup per 1024 events) before the plan kernel
+    b = np.sort(rng.integers(0, 21, 12000))
+    b[5119], b[5120] = b[5120], b[5119] - 1 if b[5119] > 0 else 1
+    cases["inversion_wide"] = (b, 21)
+    b = np.sort(rng.integers(0, 30, 9000))
+    b[8999] = 30
+    cases["out_of_range_tail_wide"] = (b, 30)
+    cases["sorted_8192"] = (np.sort(rng.integers(0, 33, 8192)), 33)
+    cases["sorted_8193"] = (np.sort(rng.integers(0, 33, 8193)), 40)
     return cases
 
 
 @pytest.mark.parametrize("name", list(_sorted_cases()))
 def test_pack_plan_sorted_fast_path(name):
-    """Sorted batch indices take the identity plan (pack_small_kernel's first pass); anything else found
+    """Sorted batch indices take the identity plan (checked inside the plan kernel up to 8192
+    events, by the wide pack_sorted_kernel above); anything else found
     there -- an inversion, an index out of range -- falls back to the full plan.  Same
     results as the oracle either way, with and without ranks."""
     from cortex.kernels import ops

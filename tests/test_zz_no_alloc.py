@@ -2,8 +2,8 @@
 that cannot allocate) against cortex_pack_plan with a caller workspace, through the C-ABI.
 
 Two calls in a row, the second with a smaller input, then the reverse order of paths:
-the three-launch plan (per-chunk counts in the scratch) and the one-workgroup plan (sorted
-fast path and full plan).  Bit-exact offsets, order, ranks and error flags.  Sizes whose
+the three-launch plan (per-chunk counts in the scratch) and the sorted fast path (status
+words in the scratch above 8192 events).  Bit-exact offsets, order, ranks and error flags.  Sizes whose
 counts do not fit the scratch are refused on the host with an error, before any launch.
 """
 
