@@ -201,20 +201,31 @@ __global__ __launch_bounds__(BA_THREADS) void qkv_attention_kernel(QkvAttnArgs a
   }
   __builtin_amdgcn_s_barrier();
   read_frags(0, 0, af0, wf0);
-  for (int kt = 0; kt < nk; ++kt) {
+  // One K step that hands over to the next (as in gemm_bf16.hip): the loop is peeled so that
+  // no branch joins in front of an MFMA group, where the compiler would wait for the
+  // fragment reads just issued, and each step first waits explicitly for the fragments read
+  // after the previous barrier.
+  auto step = [&](int kt, auto refill) {
     const int st = kt % BA_S;
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): sub-step 0's fragments
     read_frags(st, 1, af1, wf1);
     mma(af0, wf0);
-    if (kt + 1 < nk) {
-      ba_wait_vm<0>();                     // step kt+1 landed (two stages: nothing newer in flight)
-      commit_w((kt + 1) % BA_S);           // (int8 weights: widened into its W stage)
-      __builtin_amdgcn_s_waitcnt(0xC07F);  // this wave's reads of stage st (and W stores) are done
-      __builtin_amdgcn_s_barrier();        // all waves done with stage st; step kt+1 visible
-      if (kt + BA_S < nk) issue(kt + BA_S);
-      read_frags((kt + 1) % BA_S, 0, af0, wf0);
-    }
+    ba_wait_vm<0>();                     // step kt+1 landed (two stages: nothing newer in flight)
+    commit_w((kt + 1) % BA_S);           // (int8 weights: widened into its W stage)
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // this wave's reads of stage st (and W stores) are done
+    __builtin_amdgcn_s_barrier();        // all waves done with stage st; step kt+1 visible
+    read_frags((kt + 1) % BA_S, 0, af0, wf0);
+    if constexpr (decltype(refill)::value) issue(kt + BA_S);
     mma(af1, wf1);
-  }
+  };
+  int kt = 0;
+  for (; kt + BA_S < nk; ++kt) step(kt, std::integral_constant<bool, true>{});
+  for (; kt + 1 < nk; ++kt) step(kt, std::integral_constant<bool, false>{});
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // the last step
+  read_frags((nk - 1) % BA_S, 1, af1, wf1);
+  mma(af0, wf0);
+  __builtin_amdgcn_s_waitcnt(0xC07F);
+  mma(af1, wf1);
 
   // ---- scale / bias per column, round to bf16, write Q, K rows and V^T into LDS
   float4 scv[BA_TN], biv[BA_TN];  // C^T tiles: 4 consecutive columns

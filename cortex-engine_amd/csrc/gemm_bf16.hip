@@ -273,24 +273,39 @@ __global__ __launch_bounds__(TL::THREADS) void gemm_bf16_kernel(GemmArgs g) {
   wait_step(0, S - 1);
   __builtin_amdgcn_s_barrier();
   read_frags(0, 0, af0, wf0);
-  for (int kt = 0; kt < nk; ++kt) {
+  // One K step that hands over to the next: sub-step 1's fragments are read while sub-step 0
+  // multiplies; after the barrier, the next step's sub-step 0 fragments (and the refill of
+  // the freed stage) are issued before sub-step 1 multiplies.  The loop is peeled (steps
+  // that refill, steps that do not, the last step) so that no branch joins in front of an
+  // MFMA group: at a join the compiler waits for every LDS read in flight, including the ones
+  // just issued, and the double-buffered fragments would no longer overlap the MFMAs.  Each
+  // step starts with an explicit wait for the fragments read after the previous barrier, for
+  // the same reason (the compiler cannot track them across the loop's back edge).
+  auto step = [&](int kt, auto refill) {
     const int st = kt % S;
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): sub-step 0's fragments
     read_frags(st, 1, af1, wf1);
     mma(af0, wf0);
-    if (kt + 1 < nk) {
-      if constexpr (WI8) {
-        wait_vm<0>();                      // step kt+1: A transfers and weight registers
-        commit_w((kt + 1) % S);
-      } else {
-        wait_step(kt + 1, kt + S - 1);
-      }
-      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's reads of stage st (and W stores) done
-      __builtin_amdgcn_s_barrier();        // all waves done with stage st; step kt+1 visible
-      if (kt + S < nk) issue(kt + S);      // refill stage st
-      read_frags((kt + 1) % S, 0, af0, wf0);
+    if constexpr (WI8) {
+      wait_vm<0>();                      // step kt+1: A transfers and weight registers
+      commit_w((kt + 1) % S);
+    } else {
+      wait_step(kt + 1, kt + S - 1);
     }
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's reads of stage st (and W stores) done
+    __builtin_amdgcn_s_barrier();        // all waves done with stage st; step kt+1 visible
+    read_frags((kt + 1) % S, 0, af0, wf0);
+    if constexpr (decltype(refill)::value) issue(kt + S);  // refill stage st
     mma(af1, wf1);
-  }
+  };
+  int kt = 0;
+  for (; kt + S < nk; ++kt) step(kt, std::integral_constant<bool, true>{});
+  for (; kt + 1 < nk; ++kt) step(kt, std::integral_constant<bool, false>{});
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // the last step
+  read_frags((nk - 1) % S, 1, af1, wf1);
+  mma(af0, wf0);
+  __builtin_amdgcn_s_waitcnt(0xC07F);
+  mma(af1, wf1);
 
   if constexpr (TL::KS > 1) {
     // group 1 hands its partial tile to group 0 through LDS (lane-contiguous: conflict free)

@@ -225,24 +225,35 @@ __global__ __launch_bounds__(RL_THREADS) void gemm_rowln_kernel(RowLnArgs g) {
   if constexpr (!WI8) wait_step(0, S - 1);  // (int8 weights: step 0 landed before it was widened)
   __builtin_amdgcn_s_barrier();
   read_frags(0, 0, af0, wf0);
-  for (int kt = 0; kt < nk; ++kt) {
+  // One K step that hands over to the next (as in gemm_bf16.hip): the loop is peeled so that
+  // no branch joins in front of an MFMA group, where the compiler would wait for the
+  // fragment reads just issued, and each step first waits explicitly for the fragments read
+  // after the previous barrier.
+  auto step = [&](int kt, auto refill) {
     const int st = kt % S;
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): sub-step 0's fragments
     read_frags(st, 1, af1, wf1);
     mma(af0, wf0);
-    if (kt + 1 < nk) {
-      if constexpr (WI8) {
-        rl_wait_vm<0>();  // step kt+1: A transfer and weight registers
-        commit_w((kt + 1) % S);
-      } else {
-        wait_step(kt + 1, kt + S - 1);
-      }
-      __builtin_amdgcn_s_waitcnt(0xC07F);  // this wave's reads of stage st (and W stores) done
-      __builtin_amdgcn_s_barrier();        // all waves done with stage st; step kt+1 visible
-      if (kt + S < nk) issue(kt + S);
-      read_frags((kt + 1) % S, 0, af0, wf0);
+    if constexpr (WI8) {
+      rl_wait_vm<0>();  // step kt+1: A transfer and weight registers
+      commit_w((kt + 1) % S);
+    } else {
+      wait_step(kt + 1, kt + S - 1);
     }
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // this wave's reads of stage st (and W stores) done
+    __builtin_amdgcn_s_barrier();        // all waves done with stage st; step kt+1 visible
+    read_frags((kt + 1) % S, 0, af0, wf0);
+    if constexpr (decltype(refill)::value) issue(kt + S);
     mma(af1, wf1);
-  }
+  };
+  int kt = 0;
+  for (; kt + S < nk; ++kt) step(kt, std::integral_constant<bool, true>{});
+  for (; kt + 1 < nk; ++kt) step(kt, std::integral_constant<bool, false>{});
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // the last step
+  read_frags((nk - 1) % S, 1, af1, wf1);
+  mma(af0, wf0);
+  __builtin_amdgcn_s_waitcnt(0xC07F);
+  mma(af1, wf1);
 
   // ---- epilogue.  Lane (fr, g4), tile (i, j): row m0 + 16 i + fr, columns
   // wcol + 16 j + 4 g4 .. +3.  Every per-column parameter is loaded before the first
