@@ -285,7 +285,9 @@ __global__ __launch_bounds__(TL::THREADS) void gemm_bf16_kernel(GemmArgs g) {
     const int st = kt % S;
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): sub-step 0's fragments
     read_frags(st, 1, af1, wf1);
+    __builtin_amdgcn_sched_barrier(0);   // the reads go out first: the barrier below waits for them
     mma(af0, wf0);
+    __builtin_amdgcn_sched_barrier(0);   // and every MFMA of sub-step 0 is issued before that wait
     if constexpr (WI8) {
       wait_vm<0>();                      // step kt+1: A transfers and weight registers
       commit_w((kt + 1) % S);
@@ -295,6 +297,7 @@ __global__ __launch_bounds__(TL::THREADS) void gemm_bf16_kernel(GemmArgs g) {
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's reads of stage st (and W stores) done
     __builtin_amdgcn_s_barrier();        // all waves done with stage st; step kt+1 visible
     read_frags((kt + 1) % S, 0, af0, wf0);
+    __builtin_amdgcn_sched_barrier(0);   // the next step's first reads go out before these MFMAs
     if constexpr (decltype(refill)::value) issue(kt + S);  // refill stage st
     mma(af1, wf1);
   };
