@@ -35,6 +35,9 @@ struct GemmArgs {
   // and an int8 output is written as clamp(rint(y * out_inv_scale), -127, 127)
   float a_scale;
   float out_inv_scale;
+  // bf16 row-scaled kernels only (gemm_bf16.hip, RS): the accumulator of row m is scaled by
+  // 1 / sqrt(mean_k(x[m, k]^2) + rms_eps) before the weight scale (RMSNorm without a gain)
+  float rms_eps;
 };
 
 // Fast path for aligned bf16-compute GEMMs (gemm_fast.hip).  Returns 1 when it

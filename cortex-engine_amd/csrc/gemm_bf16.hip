@@ -45,6 +45,32 @@ __device__ __forceinline__ void wait_vm() {
   __builtin_amdgcn_s_waitcnt((n & 15) | 0x70 | 0xF00 | ((n >> 4) << 14));
 }
 
+// pair d (values 2d, 2d + 1) of eight bf16 values, for the two-term dot products
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ bf16x2_t pair_of(const bf16x8& v, int d) {
+  switch (d) {
+    case 0: return __builtin_shufflevector(v, v, 0, 1);
+    case 1: return __builtin_shufflevector(v, v, 2, 3);
+    case 2: return __builtin_shufflevector(v, v, 4, 5);
+    default: return __builtin_shufflevector(v, v, 6, 7);
+  }
+}
+
+// Direct-to-LDS transfer of 16 bytes per lane from a uniform base plus a 32-bit lane offset
+// (global_load_lds_dwordx4 in its scalar-base form: one VGPR per transfer instead of a 64-bit
+// address).  LDS destination lds_dst + 16 * lane; the caller's vmcnt waits order the reads.
+__device__ __forceinline__ void lds_dma16_sbase(const void* base, uint32_t voff, void* lds_dst) {
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds_dst);
+  const uint64_t b = (uint64_t)(uintptr_t)base;
+  // (readfirstlane returns int: each half goes through uint32_t, or the low half would
+  // sign-extend into the high one)
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(b >> 32));
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)b);
+  const uint64_t sb = ((uint64_t)hi << 32) | (uint64_t)lo;
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sb), "s"(m0)
+               : "memory", "m0");
+}
+
 // KS > 1 splits K over KS groups of WM x WN wavefronts, each streaming its own part of
 // K through its own LDS ring; the partial tiles are summed through LDS before the
 // epilogue.  This doubles the wavefronts per CU for narrow outputs (N = 512) without
@@ -88,7 +114,7 @@ __device__ __forceinline__ void widen_store_i8x16(unsigned char* row, int sw, in
   *reinterpret_cast<bf16x8*>(row + (((2 * c + 1) ^ sw) << 4)) = widen_i8x8(make_uint2(raw.z, raw.w));
 }
 
-template <class TL, int ACT, bool RES, class TOUT, class TIN = bf16, class TW = TIN>
+template <class TL, int ACT, bool RES, class TOUT, class TIN = bf16, class TW = TIN, bool RS = false>
 __global__ __launch_bounds__(TL::THREADS) void gemm_bf16_kernel(GemmArgs g) {
   constexpr int BM = TL::BM, BN = TL::BN, TM = TL::TM, TN = TL::TN, S = TL::STAGES;
   constexpr int AB = TL::A_BLOCKS, WB = TL::W_BLOCKS, PER = TL::PER;
@@ -103,6 +129,9 @@ __global__ __launch_bounds__(TL::THREADS) void gemm_bf16_kernel(GemmArgs g) {
   constexpr bool WI8 = sizeof(TW) == 1 && sizeof(TIN) == 2;
   constexpr int WL = WI8 ? BN / (16 * TL::WAVES) : 1;
   static_assert(!WI8 || (BN % (16 * TL::WAVES) == 0 && S == 2), "int8 weight staging shape");
+  // RS: each lane sums the squares of the A values its fragments hold (row wrow + 16 t + fr,
+  // eight of every 32 K per sub-step); the four lanes of a row complete the sum at the end
+  static_assert(!RS || (TL::KS == 1 && sizeof(TIN) == 2 && sizeof(TW) == 2 && !RES), "row scale: bf16, one K group");
   constexpr int WOPS = WI8 ? WL : WB;  // vector-memory operations per step for W
   constexpr int STEP_OPS = AB + WOPS;
   __shared__ __attribute__((aligned(1024))) unsigned char smem[TL::LDS];
@@ -123,13 +152,21 @@ __global__ __launch_bounds__(TL::THREADS) void gemm_bf16_kernel(GemmArgs g) {
   // Global source of each of this lane's transfers (K offset added per step).  Lane i
   // of a transfer writes LDS bytes [16 i, 16 i + 16) of its 1 KiB block: row i / 8,
   // stored chunk i % 8, which holds logical chunk (i % 8) ^ swizzle(row).
-  const TIN* a_src[AB];
+  // RS: 32-bit byte offsets from the uniform operand bases instead of 64-bit pointers (the
+  // transfers take the scalar-base form, and the kernel stays within its registers; the host
+  // keeps both operands below 4 GiB)
+  constexpr bool O32 = RS;
+  const TIN* a_src[O32 ? 1 : AB];
+  uint32_t a_vo[O32 ? AB : 1];
 #pragma unroll
   for (int i = 0; i < AB; ++i) {
     const int r = (wid * AB + i) * 8 + (lane >> 3);
-    a_src[i] = A + (int64_t)min(m0 + r, M - 1) * g.ld_x + ((lane & 7) ^ swz_a(r)) * EPC;
+    const int64_t e = (int64_t)min(m0 + r, M - 1) * g.ld_x + ((lane & 7) ^ swz_a(r)) * EPC;
+    if constexpr (O32) a_vo[i] = (uint32_t)(e * (int64_t)sizeof(TIN));
+    else a_src[i] = A + e;
   }
-  const TW* w_src[WI8 ? WL : WB];
+  const TW* w_src[O32 ? 1 : (WI8 ? WL : WB)];
+  uint32_t w_vo[O32 ? WB : 1];
   int w_row[WI8 ? WL : 1];
   if constexpr (WI8) {
 #pragma unroll
@@ -142,7 +179,9 @@ __global__ __launch_bounds__(TL::THREADS) void gemm_bf16_kernel(GemmArgs g) {
 #pragma unroll
     for (int i = 0; i < WB; ++i) {
       const int r = (wid * WB + i) * 8 + (lane >> 3);
-      w_src[i] = W + (int64_t)min(n0 + r, N - 1) * g.ld_w + ((lane & 7) ^ (IL ? swz_w(r) : swz_a(r))) * EPC;
+      const int64_t e = (int64_t)min(n0 + r, N - 1) * g.ld_w + ((lane & 7) ^ (IL ? swz_w(r) : swz_a(r))) * EPC;
+      if constexpr (O32) w_vo[i] = (uint32_t)(e * (int64_t)sizeof(TW));
+      else w_src[i] = W + e;
     }
   }
   auto a_stage = [&](int s) { return ring + s * TL::A_STAGE; };
@@ -155,6 +194,15 @@ __global__ __launch_bounds__(TL::THREADS) void gemm_bf16_kernel(GemmArgs g) {
     if constexpr (WI8) {
 #pragma unroll
       for (int i = 0; i < WL; ++i) wreg[i] = *reinterpret_cast<const uint4*>(w_src[i] + k0);
+    }
+    if constexpr (O32) {
+      const unsigned char* ab = reinterpret_cast<const unsigned char*>(A + k0);
+      const unsigned char* wb = reinterpret_cast<const unsigned char*>(W + k0);
+#pragma unroll
+      for (int i = 0; i < AB; ++i) lds_dma16_sbase(ab, a_vo[i], a_stage(s) + (wid * AB + i) * 1024);
+#pragma unroll
+      for (int i = 0; i < WB; ++i) lds_dma16_sbase(wb, w_vo[i], w_stage(s) + (wid * WB + i) * 1024);
+      return;
     }
 #pragma unroll
     for (int i = 0; i < AB; ++i)
@@ -210,12 +258,22 @@ __global__ __launch_bounds__(TL::THREADS) void gemm_bf16_kernel(GemmArgs g) {
     for (int t = 0; t < TN; ++t)
       wf[t] = *reinterpret_cast<const frag*>(ws + w_off[t] + (((ks * 4 + g4) ^ w_sw[t]) << 4));
   };
+  float ssq[RS ? TM : 1] = {};  // RS: this lane's sum of squares of each row fragment
   auto mma = [&](const frag (&af)[TM], const frag (&wf)[TN]) {
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
       for (int j = 0; j < TN; ++j)
         acc[i][j] = OP::mma(wf[j], af[i], acc[i][j]);
+    if constexpr (RS) {
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+          const bf16x2_t xv = pair_of(af[i], d);
+          ssq[i] = __builtin_amdgcn_fdot2_f32_bf16(xv, xv, ssq[i], false);
+        }
+    }
   };
 
   // The residual tile is fetched into registers before the main loop, so its latency
@@ -332,6 +390,21 @@ __global__ __launch_bounds__(TL::THREADS) void gemm_bf16_kernel(GemmArgs g) {
         for (int r = 0; r < 4; ++r) acc[i][j][r] += red[(((wid * TM + i) * TN + j) * 4 + r) * 64 + lane];
   }
 
+  float rinv[RS ? TM : 1];
+  if constexpr (RS) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      float s1 = ssq[i];
+      s1 += __shfl_xor(s1, 16, 64);
+      s1 += __shfl_xor(s1, 32, 64);
+      rinv[i] = 1.0f / sqrtf(s1 / (float)K + g.rms_eps);
+    }
+  }
+  auto row_scaled = [&](float a, int i) {
+    if constexpr (RS) return a * rinv[i];
+    else return a;
+  };
+
   // ---- epilogue from registers.  Row m0 + wrow + 16 i + fr; columns
   //   IL:  tiles 2p, 2p+1 -> n0 + wcol + 32 p + 8 g4 .. +7
   //   !IL: tile j         -> n0 + wcol + 16 j + 4 g4 .. +3
@@ -373,10 +446,10 @@ __global__ __launch_bounds__(TL::THREADS) void gemm_bf16_kernel(GemmArgs g) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         if constexpr (IL) {
-          v[r] = acc[i][2 * p][r] * sc[r] + bi[r];
-          v[4 + r] = acc[i][2 * p + 1][r] * sc[4 + r] + bi[4 + r];
+          v[r] = row_scaled(acc[i][2 * p][r], i) * sc[r] + bi[r];
+          v[4 + r] = row_scaled(acc[i][2 * p + 1][r], i) * sc[4 + r] + bi[4 + r];
         } else {
-          v[r] = acc[i][p][r] * sc[r] + bi[r];
+          v[r] = row_scaled(acc[i][p][r], i) * sc[r] + bi[r];
         }
       }
       if (ACT == ACT_GELU) {
@@ -412,11 +485,11 @@ __global__ __launch_bounds__(TL::THREADS) void gemm_bf16_kernel(GemmArgs g) {
   }
 }
 
-template <class TL, int ACT, bool RES, class TOUT, class TIN = bf16, class TW = TIN>
+template <class TL, int ACT, bool RES, class TOUT, class TIN = bf16, class TW = TIN, bool RS = false>
 int launch(const GemmArgs& g, hipStream_t stream) {
   const int64_t gy = cdiv(g.M, TL::BM), gx = cdiv(g.N, TL::BN);
   if (gy > 65535 || gx * gy > 0x7fffffffLL) return 0;
-  hipLaunchKernelGGL((gemm_bf16_kernel<TL, ACT, RES, TOUT, TIN, TW>), dim3((unsigned)gx, (unsigned)gy),
+  hipLaunchKernelGGL((gemm_bf16_kernel<TL, ACT, RES, TOUT, TIN, TW, RS>), dim3((unsigned)gx, (unsigned)gy),
                      dim3(TL::THREADS), 0, stream, g);
   CORTEX_CHECK_LAUNCH("gemm_bf16_kernel");
   return 1;
@@ -498,6 +571,31 @@ int dispatch(const GemmArgs& g, hipStream_t stream) {
       default:
         return launch<B128x128s2, ACT, RES, TOUT>(g, stream);
     }
+  }
+}
+
+// RMSNorm without a gain (the gain folded into bf16 weight rows): the plain GEMM, its A
+// fragments also summed as squares, 1 / rms on the accumulator.  Tiles as dispatch() picks
+// them for bf16 weights, limited to the 128 x 128, 256 x 192 and 256 x 256 shapes.
+template <int ACT, class TOUT>
+int dispatch_rs(const GemmArgs& g, hipStream_t stream) {
+  int t = bf16_tile();
+  if (t != 0 && t != 4 && t != 6) {
+    const int64_t t256 = cdiv(g.M, 256) * cdiv(g.N, 256), t192 = cdiv(g.M, 256) * cdiv(g.N, 192);
+    const int ncu = cu_count();
+    if (g.N % 256 == 0 && t256 >= ncu * 15 / 16)
+      t = 4;
+    else if (g.N % 192 == 0 && t192 >= ncu * 15 / 16 && t192 <= ncu)
+      t = 6;
+    else if (t256 >= ncu * 3 / 4)
+      t = 4;
+    else
+      t = 0;
+  }
+  switch (t) {
+    case 4: return launch<B256x256s2, ACT, false, TOUT, bf16, bf16, true>(g, stream);
+    case 6: return launch<B256x192s2, ACT, false, TOUT, bf16, bf16, true>(g, stream);
+    default: return launch<B128x128s2, ACT, false, TOUT, bf16, bf16, true>(g, stream);
   }
 }
 
@@ -617,16 +715,6 @@ __device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int
 template <int N, class F>
 __device__ __forceinline__ void static_for(F&& f) {
   static_for_impl(f, std::make_integer_sequence<int, N>{});
-}
-
-typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-__device__ __forceinline__ bf16x2_t pair_of(const bf16x8& v, int d) {
-  switch (d) {
-    case 0: return __builtin_shufflevector(v, v, 0, 1);
-    case 1: return __builtin_shufflevector(v, v, 2, 3);
-    case 2: return __builtin_shufflevector(v, v, 4, 5);
-    default: return __builtin_shufflevector(v, v, 6, 7);
-  }
 }
 
 template <int NORM, bool NRM, class TW, int ACT, class TOUT>
@@ -1016,7 +1104,8 @@ int launch_norm_rk(const NormGemmArgs& a0, hipStream_t stream) {
 template <class TW, int ACT, class TOUT>
 int dispatch_norm(const NormGemmArgs& a, hipStream_t stream) {
   // rows normalised in the kernel (LayerNorm, RMS with a gain), or RMS without a gain: raw
-  // rows and 1 / rms on the accumulator (cortex_fold_gain builds a weight that carries it)
+  // rows and 1 / rms on the accumulator (cortex_fold_gain builds a weight that carries it;
+  // a bf16 weight of that form goes to dispatch_rs while the rows stay below 4 GiB)
   if (a.norm == NORM_LAYER) return launch_norm_rk<NORM_LAYER, true, TW, ACT, TOUT>(a, stream);
   return a.gamma ? launch_norm_rk<NORM_RMS, true, TW, ACT, TOUT>(a, stream)
                  : launch_norm_rk<NORM_RMS, false, TW, ACT, TOUT>(a, stream);
@@ -1186,7 +1275,28 @@ extern "C" int cortex_norm_linear_fused(int64_t M, int64_t N, int64_t K, const v
                  gamma_dtype, eps, w, ld_w, w_scale, bias, out, ld_out, 1};
   int st;
   const bool gelu = act == ACT_GELU, obf = out_dtype == DT_BF16;
-  if (w_dtype == DT_I8) {
+  if (norm == NORM_RMS && !gamma && w_dtype == DT_BF16 && M * ld_x * 2 < (1LL << 32)) {
+    // rows as given and 1 / rms on the accumulator: the tiled GEMM sums the squares itself
+    GemmArgs g = {};
+    g.M = M;
+    g.N = N;
+    g.K = K;
+    g.x = x;
+    g.ld_x = ld_x;
+    g.w = w;
+    g.ld_w = ld_w;
+    g.w_scale = w_scale;
+    g.bias = bias;
+    g.bias_dtype = DT_F32;
+    g.act = act;
+    g.out = out;
+    g.out_dtype = out_dtype;
+    g.ld_out = ld_out;
+    g.vec = 1;
+    g.rms_eps = eps;
+    st = obf ? (gelu ? dispatch_rs<ACT_GELU, bf16>(g, stream) : dispatch_rs<ACT_NONE, bf16>(g, stream))
+             : (gelu ? dispatch_rs<ACT_GELU, float>(g, stream) : dispatch_rs<ACT_NONE, float>(g, stream));
+  } else if (w_dtype == DT_I8) {
     st = obf ? (gelu ? dispatch_norm<int8_t, ACT_GELU, bf16>(a, stream) : dispatch_norm<int8_t, ACT_NONE, bf16>(a, stream))
              : (gelu ? dispatch_norm<int8_t, ACT_GELU, float>(a, stream) : dispatch_norm<int8_t, ACT_NONE, float>(a, stream));
   } else {
