@@ -131,7 +131,7 @@ __global__ __launch_bounds__(TL::THREADS) void gemm_bf16_kernel(GemmArgs g) {
   static_assert(!WI8 || (BN % (16 * TL::WAVES) == 0 && S == 2), "int8 weight staging shape");
   // RS: each lane sums the squares of the A values its fragments hold (row wrow + 16 t + fr,
   // eight of every 32 K per sub-step); the four lanes of a row complete the sum at the end
-  static_assert(!RS || (TL::KS == 1 && sizeof(TIN) == 2 && sizeof(TW) == 2 && !RES), "row scale: bf16, one K group");
+  static_assert(!RS || (sizeof(TIN) == 2 && sizeof(TW) == 2 && !RES), "row scale: bf16 operands");
   constexpr int WOPS = WI8 ? WL : WB;  // vector-memory operations per step for W
   constexpr int STEP_OPS = AB + WOPS;
   __shared__ __attribute__((aligned(1024))) unsigned char smem[TL::LDS];
@@ -371,6 +371,8 @@ __global__ __launch_bounds__(TL::THREADS) void gemm_bf16_kernel(GemmArgs g) {
   if constexpr (TL::KS > 1) {
     // group 1 hands its partial tile to group 0 through LDS (lane-contiguous: conflict free)
     typename OP::elem* red = reinterpret_cast<typename OP::elem*>(smem);
+    float* red_ss = reinterpret_cast<float*>(smem + TL::RED);  // RS: the partial sums of squares
+    static_assert(!RS || TL::RED + TL::WAVES * TM * 64 * 4 <= TL::LDS, "exchange area");
     __syncthreads();  // every ring read is done; the exchange area may overwrite the rings
     if (kg == 1) {
 #pragma unroll
@@ -379,6 +381,10 @@ __global__ __launch_bounds__(TL::THREADS) void gemm_bf16_kernel(GemmArgs g) {
         for (int j = 0; j < TN; ++j)
 #pragma unroll
           for (int r = 0; r < 4; ++r) red[(((wid * TM + i) * TN + j) * 4 + r) * 64 + lane] = acc[i][j][r];
+      if constexpr (RS) {
+#pragma unroll
+        for (int i = 0; i < TM; ++i) red_ss[(wid * TM + i) * 64 + lane] = ssq[i];
+      }
     }
     __syncthreads();
     if (kg == 1) return;
@@ -388,6 +394,10 @@ __global__ __launch_bounds__(TL::THREADS) void gemm_bf16_kernel(GemmArgs g) {
       for (int j = 0; j < TN; ++j)
 #pragma unroll
         for (int r = 0; r < 4; ++r) acc[i][j][r] += red[(((wid * TM + i) * TN + j) * 4 + r) * 64 + lane];
+    if constexpr (RS) {
+#pragma unroll
+      for (int i = 0; i < TM; ++i) ssq[i] += red_ss[(wid * TM + i) * 64 + lane];
+    }
   }
 
   float rinv[RS ? TM : 1];
@@ -576,12 +586,14 @@ int dispatch(const GemmArgs& g, hipStream_t stream) {
 
 // RMSNorm without a gain (the gain folded into bf16 weight rows): the plain GEMM, its A
 // fragments also summed as squares, 1 / rms on the accumulator.  Tiles as dispatch() picks
-// them for bf16 weights, limited to the 128 x 128, 256 x 192 and 256 x 256 shapes.
+// them for bf16 weights (256 x 256, 256 x 192, 128 x 128), and for grids of at most one
+// 128 x 128 workgroup per CU the K split of the residual GEMMs.
 template <int ACT, class TOUT>
 int dispatch_rs(const GemmArgs& g, hipStream_t stream) {
   int t = bf16_tile();
-  if (t != 0 && t != 4 && t != 6) {
+  if (t != 0 && t != 4 && t != 6 && !(t == 7 && g.K % 128 == 0)) {
     const int64_t t256 = cdiv(g.M, 256) * cdiv(g.N, 256), t192 = cdiv(g.M, 256) * cdiv(g.N, 192);
+    const int64_t t128 = cdiv(g.M, 128) * cdiv(g.N, 128);
     const int ncu = cu_count();
     if (g.N % 256 == 0 && t256 >= ncu * 15 / 16)
       t = 4;
@@ -589,12 +601,15 @@ int dispatch_rs(const GemmArgs& g, hipStream_t stream) {
       t = 6;
     else if (t256 >= ncu * 3 / 4)
       t = 4;
+    else if (g.K % 128 == 0 && t128 <= ncu)
+      t = 7;  // at most one workgroup per CU: K split over two wave groups (eight wavefronts)
     else
       t = 0;
   }
   switch (t) {
     case 4: return launch<B256x256s2, ACT, false, TOUT, bf16, bf16, true>(g, stream);
     case 6: return launch<B256x192s2, ACT, false, TOUT, bf16, bf16, true>(g, stream);
+    case 7: return launch<B128x128s2k2, ACT, false, TOUT, bf16, bf16, true>(g, stream);
     default: return launch<B128x128s2, ACT, false, TOUT, bf16, bf16, true>(g, stream);
   }
 }
