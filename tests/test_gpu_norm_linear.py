@@ -334,6 +334,41 @@ def test_rms_linear_folded_gain_exact_rows(M, N, K, wform):
     assert _rel_err(out.cpu(), ref) <= 1e-5
 
 
+@pytest.mark.parametrize("M,N,K,act,odt", [(1, 256, 64, None, torch.float32), (300, 200, 64, "gelu", torch.bfloat16),
+                                            (257, 520, 128, None, torch.float32), (257, 520, 128, "gelu", torch.float32),
+                                            (1000, 2048, 512, "gelu", torch.bfloat16), (7937, 2048, 128, None, torch.bfloat16),
+                                            (7937, 1536, 64, "gelu", torch.float32)])
+def test_rms_without_gain_row_scaled_gemm(M, N, K, act, odt):
+    """RMS without a gain on a bf16 weight (the form the API hands over after folding the gain):
+    the tiled GEMM sums the squares of its own A fragments and scales the accumulator by
+    1 / rms.  The shapes reach every tile it picks (128 x 128 with and without the K split over
+    two wave groups, 256 x 192, 256 x 256), a single K step (K = 64), one step per wave group
+    (K = 128), M = 1 and ragged M and N.  Against the float64 value of the same arithmetic,
+    act(x W^T / sqrt(mean(x^2) + eps) * scale + bias): fp32 output within 1e-5 of the largest
+    output, bf16 output within one bf16 rounding (2^-8 relative) plus 1e-5 of the largest."""
+    from cortex.kernels import ops
+
+    g = torch.Generator().manual_seed(M + N + K)
+    x = (torch.randn(M, K, generator=g) * (1 + 3 * torch.rand(M, 1, generator=g))).bfloat16()
+    w = (torch.randn(N, K, generator=g) * 0.05).bfloat16()
+    sc = 0.5 + torch.rand(N, generator=g)
+    bias = 0.1 * torch.randn(N, generator=g)
+    out = ops.norm_linear_fused(x.to(DEV), w.to(DEV), sc.to(DEV), norm="rms", gamma=None, eps=1e-6,
+                                bias=bias.to(DEV), act=act, out_dtype=odt)
+    xd = x.double()
+    rinv = 1.0 / torch.sqrt(xd.pow(2).mean(-1, keepdim=True) + 1e-6)
+    ref = (xd @ w.double().T) * rinv * sc.double() + bias.double()
+    if act == "gelu":
+        ref = F.gelu(ref)
+    assert out.shape == (M, N) and out.dtype == odt
+    got = out.double().cpu()
+    big = float(ref.abs().max())
+    if odt == torch.float32:
+        assert _rel_err(got, ref) <= 1e-5
+    else:
+        assert bool(((got - ref).abs() <= ref.abs() * 2.0 ** -8 + 1e-5 * big).all()), float((got - ref).abs().max())
+
+
 @pytest.mark.parametrize("N", [1536, 512])
 def test_config2_widen_mode_streams_int8(N, monkeypatch):
     """CORTEX_INT8_WEIGHTS=widen: norm_linear_int8 hands the int8 weight and the gain to the kernel
