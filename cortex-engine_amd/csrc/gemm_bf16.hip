@@ -259,12 +259,19 @@ __global__ __launch_bounds__(TL::THREADS) void gemm_bf16_kernel(GemmArgs g) {
       wf[t] = *reinterpret_cast<const frag*>(ws + w_off[t] + (((ks * 4 + g4) ^ w_sw[t]) << 4));
   };
   float ssq[RS ? TM : 1] = {};  // RS: this lane's sum of squares of each row fragment
+  // Raised wave priority over each MFMA group, so a wavefront ready to multiply issues ahead of
+  // its SIMD partner's fragment reads and transfers.  Measured per kernel: it pays for the
+  // row-scaled form with the K split (config 2 at N = 512: 9.75 -> 9.29 us) and costs the
+  // single-group tiles and the residual GEMMs 0.4-1 us, so only that form sets it.
+  constexpr bool PRIO = RS && TL::KS > 1;
   auto mma = [&](const frag (&af)[TM], const frag (&wf)[TN]) {
+    if constexpr (PRIO) __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
       for (int j = 0; j < TN; ++j)
         acc[i][j] = OP::mma(wf[j], af[i], acc[i][j]);
+    if constexpr (PRIO) __builtin_amdgcn_s_setprio(0);
     if constexpr (RS) {
 #pragma unroll
       for (int i = 0; i < TM; ++i)
