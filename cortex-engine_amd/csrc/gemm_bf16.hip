@@ -376,8 +376,9 @@ __global__ __launch_bounds__(TL::THREADS) void gemm_bf16_kernel(GemmArgs g) {
   mma(af1, wf1);
 
   if constexpr (TL::KS > 1) {
-    // group 1 hands its partial tile to group 0 through LDS (lane-contiguous: conflict free)
-    typename OP::elem* red = reinterpret_cast<typename OP::elem*>(smem);
+    // group 1 hands its partial tile to group 0 through LDS: one 16-byte access per accumulator
+    // fragment, lane-contiguous (conflict free)
+    typename OP::accum* red4 = reinterpret_cast<typename OP::accum*>(smem);
     float* red_ss = reinterpret_cast<float*>(smem + TL::RED);  // RS: the partial sums of squares
     static_assert(!RS || TL::RED + TL::WAVES * TM * 64 * 4 <= TL::LDS, "exchange area");
     __syncthreads();  // every ring read is done; the exchange area may overwrite the rings
@@ -385,9 +386,7 @@ __global__ __launch_bounds__(TL::THREADS) void gemm_bf16_kernel(GemmArgs g) {
 #pragma unroll
       for (int i = 0; i < TM; ++i)
 #pragma unroll
-        for (int j = 0; j < TN; ++j)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) red[(((wid * TM + i) * TN + j) * 4 + r) * 64 + lane] = acc[i][j][r];
+        for (int j = 0; j < TN; ++j) red4[((wid * TM + i) * TN + j) * 64 + lane] = acc[i][j];
       if constexpr (RS) {
 #pragma unroll
         for (int i = 0; i < TM; ++i) red_ss[(wid * TM + i) * 64 + lane] = ssq[i];
@@ -398,9 +397,7 @@ __global__ __launch_bounds__(TL::THREADS) void gemm_bf16_kernel(GemmArgs g) {
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
-      for (int j = 0; j < TN; ++j)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) acc[i][j][r] += red[(((wid * TM + i) * TN + j) * 4 + r) * 64 + lane];
+      for (int j = 0; j < TN; ++j) acc[i][j] += red4[((wid * TM + i) * TN + j) * 64 + lane];
     if constexpr (RS) {
 #pragma unroll
       for (int i = 0; i < TM; ++i) ssq[i] += red_ss[(wid * TM + i) * 64 + lane];
