@@ -19,7 +19,9 @@ from cortex.kernels import ops
 
 
 def rms_norm_linear_reference(x, gamma, w, bias=None, eps: float = 1e-6):
-    """PyTorch formulation kept for API compatibility (reference fused_rmsnorm.py:86-108)."""
+    """PyTorch formulation (reference fused_rmsnorm.py:86-108): what ``rms_norm_linear`` returns
+    for rows that are not on a ROCm device, as the reference dispatcher does.  GPU tensors
+    never reach it."""
     x_f32 = x.float()
     rms = torch.sqrt(x_f32.pow(2).mean(dim=-1, keepdim=True) + eps)
     x_norm = (x_f32 / rms) * gamma.float()
@@ -31,7 +33,13 @@ def rms_norm_linear_reference(x, gamma, w, bias=None, eps: float = 1e-6):
 
 def rms_norm_linear(x: torch.Tensor, gamma: torch.Tensor, w: torch.Tensor, bias: torch.Tensor | None = None,
                     eps: float = 1e-6) -> torch.Tensor:
-    """Fused RMSNorm + linear, output ``(..., N)`` in x's dtype (reference :239-301)."""
+    """Fused RMSNorm + linear, output ``(..., N)`` in x's dtype (reference :239-301).
+
+    Rows on a ROCm device run the HIP kernel; on any other device the call returns
+    ``rms_norm_linear_reference`` over the flattened rows (reference :266-269)."""
+    if x.device.type != "cuda":
+        lead, K = x.shape[:-1], x.shape[-1]
+        return rms_norm_linear_reference(x.reshape(-1, K), gamma, w, bias, eps).reshape(*lead, w.shape[1])
     nat.require_gpu(x, gamma, w, bias, what="rms_norm_linear")
     if w.dtype != x.dtype:
         raise RuntimeError(f"rms_norm_linear: w dtype {w.dtype} differs from x dtype {x.dtype}")

@@ -472,22 +472,53 @@ INT8_WEIGHTS = os.environ.get("CORTEX_INT8_WEIGHTS", "image")
 
 _KN_CACHE: "OrderedDict[tuple, tuple]" = OrderedDict()
 _KN_CACHE_SIZE = 16
+# keys whose rows a captured HIP graph reads: never evicted (the graph holds their address)
+_KN_PINNED: set = set()
+_KN_RETIRED: list = []  # rows of pinned entries rebuilt since their capture
+
+
+def capturing_graph() -> bool:
+    """Whether torch's current stream is capturing a HIP graph: kernels launched now are only
+    recorded, so their outputs must not be cached for eager use."""
+    return torch.cuda.is_available() and torch.cuda.is_current_stream_capturing()
 
 
 def _cached_rows(key: tuple, holds: tuple, versions: tuple, build):
     """A derived weight tensor kept in ``_KN_CACHE``: ``holds`` are the source tensors (their
     storages are kept alive, so their addresses are not reused while cached) and ``versions``
-    their version counters (an in-place update rebuilds the entry)."""
+    their version counters (an in-place update rebuilds the entry).
+
+    Under HIP graph capture the build kernel is only recorded, not run, so a miss builds a
+    temporary that the graph recomputes on every replay and is not cached (a later eager call
+    would otherwise read rows that were never written); a hit is pinned, since the graph keeps
+    reading that tensor's address on every replay."""
+    capturing = capturing_graph()
     hit = _KN_CACHE.get(key)
     if hit is not None and hit[1] == versions:
         _KN_CACHE.move_to_end(key)
+        if capturing:
+            _KN_PINNED.add(key)
         return hit[2]
+    if capturing:
+        return build()
     rows = build()
+    if hit is not None and key in _KN_PINNED:  # a graph still reads the old rows: keep them alive
+        _KN_RETIRED.append(hit[2])
+        _KN_PINNED.discard(key)
     _KN_CACHE[key] = (tuple(t.untyped_storage() for t in holds), versions, rows)
     _KN_CACHE.move_to_end(key)
-    while len(_KN_CACHE) > _KN_CACHE_SIZE:
-        _KN_CACHE.popitem(last=False)
+    for k in list(_KN_CACHE):
+        if len(_KN_CACHE) - len(_KN_PINNED & _KN_CACHE.keys()) <= _KN_CACHE_SIZE:
+            break
+        if k not in _KN_PINNED and k != key:
+            del _KN_CACHE[k]
     return rows
+
+
+def derived_weight_bytes() -> int:
+    """Device bytes held by the cached derived weights (folded-gain and transposed rows)."""
+    rows = [e[2] for e in _KN_CACHE.values()] + _KN_RETIRED
+    return sum(t.numel() * t.element_size() for t in rows)
 
 
 def _tensor_key(t: torch.Tensor) -> tuple:

@@ -24,10 +24,11 @@ from cortex.kernels import ops
 
 def sparse_cross_attention_reference(q, k, v, block_mask=None, BLOCK_L: int = 64, BLOCK_E: int = 64,
                                      scale: float | None = None):
-    """PyTorch formulation kept for API compatibility (reference sparse_xattn.py:96-146).
+    """PyTorch formulation (reference sparse_xattn.py:96-146): what ``sparse_cross_attention``
+    returns for queries that are not on a ROCm device, as the reference dispatcher does.
 
     Dense SDPA when ``block_mask`` is None; otherwise the tile mask expanded to
-    elements, -inf outside it, softmax in fp32.  Never called by the HIP path.
+    elements, -inf outside it, softmax in fp32.  GPU tensors never reach it.
     """
     L, Dh = q.shape[-2], q.shape[-1]
     E = k.shape[-2]
@@ -85,8 +86,15 @@ def sparse_cross_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, bl
 
     Signature of reference sparse_xattn.py:340-348.  ``block_mask`` may be
     ``(n_q, n_k)`` (shared by every (b, h), as in the reference) or ``(B, n_q, n_k)``;
-    ``None`` is dense attention (also on the HIP kernel).
+    ``None`` is dense attention (also on the HIP kernel).  Queries on a ROCm device run the
+    HIP kernel; on any other device the call returns ``sparse_cross_attention_reference``
+    (reference :366-368), which has no keyword-only extensions.
     """
+    if q.device.type != "cuda":
+        if kv_lengths is not None or key_padding_mask is not None or (
+                block_mask is not None and block_mask.dim() != 2):
+            raise ValueError("kv_lengths, key_padding_mask and per-sample tile masks need ROCm GPU tensors")
+        return sparse_cross_attention_reference(q, k, v, block_mask, BLOCK_L, BLOCK_E, scale)
     nat.require_gpu(q, k, v, what="sparse_cross_attention")
     B, H, L, Dh = q.shape
     E = k.shape[2]

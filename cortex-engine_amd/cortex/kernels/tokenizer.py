@@ -18,11 +18,9 @@ from cortex.kernels import ops
 
 
 def fused_tokenizer_reference(neuron_emb, time_emb, value_emb, neuron_ids, time_bins, values):
-    """PyTorch formulation kept for API compatibility (reference tokenizer.py:68-81).
-
-    It is never called by the HIP path; it evaluates the closed form with torch ops
-    on whatever device the tensors live on.
-    """
+    """PyTorch formulation (reference tokenizer.py:68-81): what ``fused_tokenizer`` returns for
+    tables that are not on a ROCm device, as the reference dispatcher does for non-CUDA
+    devices.  GPU tensors never reach it."""
     return neuron_emb[neuron_ids] + time_emb[time_bins] + value_emb[values]
 
 
@@ -52,11 +50,16 @@ def fused_tokenizer(neuron_emb: torch.Tensor, time_emb: torch.Tensor, value_emb:
 
     Same contract as reference cortex/kernels/tokenizer.py:177-249 (ValueError on
     non-contiguous tables, mismatched index shapes or hidden dims; ``E == 0``
-    returns an empty ``(0, D)`` tensor; indices may be strided).  Requires ROCm
-    GPU tensors.  Out-of-range indices never touch memory outside the tables: the
-    row is written as zeros; with ``check_indices=True`` an ``IndexError`` is raised
-    (this synchronises the host, like the reference's eager CPU path).
+    returns an empty ``(0, D)`` tensor; indices may be strided).  Tables on a ROCm
+    device run the HIP kernel (a missing library raises ``NativeLibraryError``);
+    tables on any other device take ``fused_tokenizer_reference``, as the reference
+    dispatcher does (tokenizer.py:201-206).  On the GPU, out-of-range indices never
+    touch memory outside the tables: the row is written as zeros; with
+    ``check_indices=True`` an ``IndexError`` is raised (this synchronises the host,
+    like the reference's eager CPU path).
     """
+    if neuron_emb.device.type != "cuda":
+        return fused_tokenizer_reference(neuron_emb, time_emb, value_emb, neuron_ids, time_bins, values)
     D = _check(neuron_emb, time_emb, value_emb, neuron_ids, time_bins, values)
     dev = nat.require_gpu(neuron_emb, time_emb, value_emb, neuron_ids, time_bins, values,
                           what="fused_tokenizer")

@@ -47,6 +47,9 @@ def exec_weights(lin: nn.Module, compute: torch.dtype) -> dict:
     key = (src.data_ptr(), src._version, tuple(src.shape), src.device)
     cached = lin.__dict__.get("_cortex_exec")
     if cached is None or cached[0] != key:
+        if ops.capturing_graph():  # only recorded now: the graph converts on every replay, nothing cached
+            return {"weight": ops.convert(src, torch.bfloat16), "weight_scale": lin.weight_scale if quant else None,
+                    "bias": lin.bias}
         cached = (key, ops.convert(src, torch.bfloat16))
         lin.__dict__["_cortex_exec"] = cached
     return {"weight": cached[1], "weight_scale": lin.weight_scale if quant else None, "bias": lin.bias}
@@ -99,7 +102,8 @@ def batch_invariant(owner: nn.Module, name: str, inputs: list, mods: list, fn):
     For results that depend on weights only (the learned latent queries after their
     norm and projection, the behaviour queries after theirs): a forward then reads
     them instead of recomputing them.  Never cached while a module carries forward
-    pre-hooks, so that calibration still sees every input.
+    pre-hooks, so that calibration still sees every input, nor from inside a HIP graph
+    capture (the graph then recomputes it on every replay).
     """
     if any(m._forward_pre_hooks for m in mods):
         return fn()
@@ -112,7 +116,8 @@ def batch_invariant(owner: nn.Module, name: str, inputs: list, mods: list, fn):
     if hit is not None and hit[0] == key:
         return hit[1]
     val = fn()
-    slot[name] = (key, val)
+    if not ops.capturing_graph():  # under capture fn() was only recorded: recomputed per replay
+        slot[name] = (key, val)
     return val
 
 

@@ -205,41 +205,57 @@ class CortexModel(nn.Module):
                          aux: bool = False) -> dict[str, torch.Tensor]:
         """The forward from a CSR plan: row r of the packed events is event ``order[r]``
         (``r`` itself when ``order`` is None); rows past ``offsets[B]`` are ignored."""
-        cfg = self.config
-        compute = cfg.compute_dtype
-        tok = self.tokenizer
         enc = self.encoder
-        xa = enc.cross_attn
-        D, L, H = cfg.latent_dim, cfg.num_latents, xa.num_heads
-        tables = (tok.neuron_emb.weight, tok.time_emb.weight, tok.value_emb.weight)
-        E = neuron_ids.shape[0]
-        if compute == torch.bfloat16 and not xa.kv_proj._forward_pre_hooks and fused_tokens_ok(tables, xa.norm_kv):
-            # tokens -> norm_kv -> bf16 operand in one pass; the fp32 tokens are never stored
-            xn = ops.tokenize_ln(*tables, neuron_ids, time_bins, values, ln_params(xa.norm_kv), order=order,
-                                 csr_offsets=offsets, err=err_flag)
-            kv = ops.norm_linear(xn, **exec_weights(xa.kv_proj, compute), out_dtype=compute, compute_dtype=compute)
-        else:
-            tokens = ops.tokenize(*tables, neuron_ids, time_bins, values, order=order, csr_offsets=offsets,
-                                  err=err_flag)  # CSR rows
-            kv = apply_linear(xa.kv_proj, tokens, norm=xa.norm_kv, out_dtype=compute, compute=compute)  # (E, 2D)
-        q = xa.project_queries(enc.latents, compute)  # (L, D), shared by every sample
-        o_buf, o = ops.merge_heads_out(B, L, H, D // H, compute, kv.device)
-        ops.attention(ops.heads_view(q, 1, L, H), ops.heads_view(kv, 1, E, H, 0, D),
-                      ops.heads_view(kv, 1, E, H, D, D), kv_offsets=offsets, out=o, batch=B)
-        first = enc.self_attn_blocks[0] if len(enc.self_attn_blocks) else None
-        xn = None
-        if first is not None and residual_ln_ok(xa.out_proj, first.norm_attn, first.qkv_proj, enc.latents, compute):
-            # latents + out_proj(attn) and the first block's norm_attn in one launch
-            x, xn = linear_residual_ln(xa.out_proj, o_buf, enc.latents, first.norm_attn, res_rows=L,
-                                       out=torch.empty(B * L, D, dtype=torch.float32, device=kv.device))
-        else:
-            x = apply_linear(xa.out_proj, o_buf, residual=enc.latents, res_rows=L, out_dtype=torch.float32,
-                             compute=compute)  # (B*L, D) fp32 residual stream
+        tokens = self._token_rows(neuron_ids, time_bins, values, offsets, order, err_flag)
+        x, xn = self._cross_rows(tokens, offsets, B)
         x = self._encode(x, B, xn)
         out = {"behavior": self.behavior_head.forward_rows(x, B, pre_norm=enc.final_norm)}
         if aux and self.masked_spike_head is not None:
             out["masked_spike_logits"] = self.masked_spike_head.forward_rows(x, B, pre_norm=enc.final_norm)
         return out
+
+    def _token_rows(self, neuron_ids, time_bins, values, offsets, order, err_flag) -> tuple[torch.Tensor, bool]:
+        """The event rows in CSR order: ``(norm_kv(tokens) as bf16 rows, True)`` in one pass over the
+        tables when the fused tokenizer + LayerNorm applies (the fp32 tokens are never stored),
+        else ``(tokens, False)``."""
+        cfg = self.config
+        tok, xa = self.tokenizer, self.encoder.cross_attn
+        tables = (tok.neuron_emb.weight, tok.time_emb.weight, tok.value_emb.weight)
+        if (cfg.compute_dtype == torch.bfloat16 and not xa.kv_proj._forward_pre_hooks
+                and fused_tokens_ok(tables, xa.norm_kv)):
+            return ops.tokenize_ln(*tables, neuron_ids, time_bins, values, ln_params(xa.norm_kv), order=order,
+                                   csr_offsets=offsets, err=err_flag), True
+        return ops.tokenize(*tables, neuron_ids, time_bins, values, order=order, csr_offsets=offsets,
+                            err=err_flag), False
+
+    def _cross_rows(self, tokens: tuple[torch.Tensor, bool], offsets: torch.Tensor, B: int):
+        """Cross-attention of the latents into each sample's CSR event rows: ``kv_proj`` on the real
+        events, the batch-invariant latent queries against them, ``out_proj`` with the latents as a
+        broadcast residual.  Returns the fp32 residual rows ``x`` (B*L, D) and, when computed in
+        the same launch, the first block's ``norm_attn(x)`` (else None)."""
+        cfg = self.config
+        compute = cfg.compute_dtype
+        enc = self.encoder
+        xa = enc.cross_attn
+        D, L, H = cfg.latent_dim, cfg.num_latents, xa.num_heads
+        rows, normed = tokens
+        E = rows.shape[0]
+        if normed:
+            kv = ops.norm_linear(rows, **exec_weights(xa.kv_proj, compute), out_dtype=compute, compute_dtype=compute)
+        else:
+            kv = apply_linear(xa.kv_proj, rows, norm=xa.norm_kv, out_dtype=compute, compute=compute)  # (E, 2D)
+        q = xa.project_queries(enc.latents, compute)  # (L, D), shared by every sample
+        o_buf, o = ops.merge_heads_out(B, L, H, D // H, compute, kv.device)
+        ops.attention(ops.heads_view(q, 1, L, H), ops.heads_view(kv, 1, E, H, 0, D),
+                      ops.heads_view(kv, 1, E, H, D, D), kv_offsets=offsets, out=o, batch=B)
+        first = enc.self_attn_blocks[0] if len(enc.self_attn_blocks) else None
+        if first is not None and residual_ln_ok(xa.out_proj, first.norm_attn, first.qkv_proj, enc.latents, compute):
+            # latents + out_proj(attn) and the first block's norm_attn in one launch
+            return linear_residual_ln(xa.out_proj, o_buf, enc.latents, first.norm_attn, res_rows=L,
+                                      out=torch.empty(B * L, D, dtype=torch.float32, device=kv.device))
+        x = apply_linear(xa.out_proj, o_buf, residual=enc.latents, res_rows=L, out_dtype=torch.float32,
+                         compute=compute)  # (B*L, D) fp32 residual stream
+        return x, None
 
     def _encode(self, x: torch.Tensor, B: int, xn: torch.Tensor | None = None) -> torch.Tensor:
         """The self-attention stack on the fresh residual buffer ``x`` (updated in place)."""

@@ -7,6 +7,7 @@ import pytest
 import torch
 
 from oracle import cortex_oracle as O
+from tests._bars import check_forward
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -69,7 +70,7 @@ def test_int8_forward_matches_reference_golden(golden, name, dtype, tol):
         if tol == "rel1e-5":
             assert np.abs(beh - ref).max() <= 1e-5 * np.abs(ref).max(), np.abs(beh - ref).max()
         else:
-            assert np.abs(beh - ref).max() <= tol, np.abs(beh - ref).max()
+            check_forward(beh, ref, 4e-3 if name == "s" else 1.5e-3, f"golden {name} {inputs} int8 bf16")
 
 
 def _config3_inputs(B=32, per=512, seed=0):
@@ -93,7 +94,7 @@ def test_config3_int8_bf16_forward_vs_oracle():
     torch.set_num_threads(max(1, torch.get_num_threads()))
     ref = O.forward(sd, O.CORTEX_S_SHAPE, *arrs).numpy()
     assert beh.shape == (32, 2)
-    assert np.abs(beh - ref).max() <= 2e-2, np.abs(beh - ref).max()
+    check_forward(beh, ref, 5e-3, "config 3 B=32x512")
 
 
 @pytest.mark.parametrize("B,lo,hi,seed", [(1, 1, 1, 11), (1, 2048, 2048, 12), (3, 64, 2048, 13), (17, 1, 700, 14),
@@ -115,7 +116,7 @@ def test_ragged_batches_int8_bf16_vs_oracle(B, lo, hi, seed):
     sd = {k: v.detach().cpu() for k, v in model.state_dict().items()}
     ref = O.forward(sd, O.CORTEX_S_SHAPE, *arrs, batch_size=B).numpy()
     assert beh.shape == (B, 2) and np.isfinite(beh).all()
-    assert np.abs(beh - ref).max() <= 2e-2, np.abs(beh - ref).max()
+    check_forward(beh, ref, 5e-3, f"ragged B={B} U[{lo},{hi}]")
 
 
 def test_cortex_m_int8_bf16_forward_vs_oracle():
@@ -135,7 +136,7 @@ def test_cortex_m_int8_bf16_forward_vs_oracle():
     shape = O.ModelShape(768, 11, 12, 384, 768, 12)
     ref = O.forward(sd, shape, *arrs).numpy()
     assert beh.shape == (2, 2) and np.isfinite(beh).all()
-    assert np.abs(beh - ref).max() <= 2e-2, np.abs(beh - ref).max()
+    check_forward(beh, ref, 1e-3, "CORTEX_M")
 
 
 def test_module_path_equals_fused_csr_path_fp32():
@@ -254,16 +255,16 @@ def test_fused_behavior_head_matches_oracle_and_unfused(name):
     ref = O.behavior_head(sd, shape, x).numpy()
     f, p = fused.cpu().numpy(), plain.cpu().numpy()
     assert f.shape == (B, 2) and np.isfinite(f).all()
-    assert np.abs(f - ref).max() <= 2e-2, (np.abs(f - ref).max(), np.abs(ref).max())
-    assert np.abs(f - p).max() <= 2e-2
+    check_forward(f, ref, 5e-4, f"fused head {name} vs oracle")
+    check_forward(f, p, 5e-4, f"fused head {name} vs the head as written")
     assert torch.equal(fused, again)
 
 
 def test_widen_mode_streams_int8_weights_through_the_fused_path(monkeypatch):
     """CORTEX_INT8_WEIGHTS=widen: no bf16 weight image is built; the GEMMs, the fused QKV +
     attention and the residual linear + LayerNorm read the int8 weights and widen them on chip.
-    Config-3 shape (B=32 x 512 events): equal to the image mode (the same widened operands)
-    and within 2e-2 of the float32 oracle; the resident weight bytes drop to the int8 weights,
+    Config-3 shape (B=32 x 512 events): bit-identical to the image mode (the same int8 values
+    reach the MFMAs, with the same tiles and K order) and within 2e-2 of the float32 oracle; the resident weight bytes drop to the int8 weights,
     their scales and the float parameters."""
     from cortex.kernels import ops
     from cortex.models import _layers
@@ -293,7 +294,8 @@ def test_widen_mode_streams_int8_weights_through_the_fused_path(monkeypatch):
     # (the batch-invariant query projections and the folded head stay cached from the widen run)
     assert 1.5 * wb["int8_weights"] < _layers.resident_weight_bytes(model)["bf16_images"] <= 2 * wb["int8_weights"]
     torch.testing.assert_close(widen, widen2, rtol=0, atol=0)
-    torch.testing.assert_close(widen, image, rtol=0, atol=1e-5 * float(image.abs().max()))
+    # the same int8 values reach the MFMAs in both modes and the tiles and K order agree
+    torch.testing.assert_close(widen, image, rtol=0, atol=0)
     sd = {k: v.detach().cpu() for k, v in model.state_dict().items()}
     ref = O.forward(sd, O.CORTEX_S_SHAPE, *arrs).numpy()
     assert np.abs(widen.cpu().numpy() - ref).max() <= 2e-2

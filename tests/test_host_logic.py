@@ -1,5 +1,6 @@
 """Host-side logic of the package (CPU only): config, calibration bookkeeping,
-save/load, temporal tile mask, and the refusal to run kernels on CPU tensors."""
+save/load, temporal tile mask, and the CPU-device fallback of the three kernel
+dispatchers."""
 
 from __future__ import annotations
 
@@ -104,22 +105,58 @@ def test_reference_formulations_are_exported():
     assert sparse_cross_attention_reference(q, q, q).shape == q.shape
 
 
-def test_kernels_refuse_cpu_tensors():
+def test_dispatchers_fall_back_on_cpu_tensors():
+    """The three kernel dispatchers return the reference's PyTorch formulation for tensors on a
+    non-ROCm device, as the reference's dispatchers do (tokenizer.py:201-206,
+    sparse_xattn.py:366-368, fused_rmsnorm.py:266-269); checked against the oracle."""
     from cortex.kernels.fused_rmsnorm import rms_norm_linear
     from cortex.kernels.sparse_xattn import sparse_cross_attention
     from cortex.kernels.tokenizer import fused_tokenizer
+
+    g = torch.Generator().manual_seed(42)
+    n, t, v = (torch.randn(r, 16, generator=g) * 0.02 for r in (37, 60, 8))
+    nid, tb = torch.randint(0, 37, (50,), generator=g), torch.randint(0, 60, (50,), generator=g)
+    val = torch.randint(0, 8, (50,), generator=g)
+    got = fused_tokenizer(n, t, v, nid, tb, val)
+    np.testing.assert_array_equal(got.numpy(), O.tokenize(n.numpy(), t.numpy(), v.numpy(), nid, tb, val))
+    # the reference's own known answers: the manual sum and a single event
+    assert torch.equal(fused_tokenizer(n, t, v, nid[:1], tb[:1], val[:1]), (n[nid[:1]] + t[tb[:1]]) + v[val[:1]])
+
+    x, gm, w, b = torch.randn(3, 5, 32, generator=g), 1 + 0.02 * torch.randn(32, generator=g), \
+        torch.randn(32, 24, generator=g), torch.randn(24, generator=g)
+    got = rms_norm_linear(x, gm, w, b)
+    assert got.shape == (3, 5, 24)
+    torch.testing.assert_close(got.reshape(15, 24), O.rms_norm_linear(x.reshape(15, 32), gm, w, b),
+                               rtol=1e-5, atol=1e-5)
+
+    q, k, vv = (torch.randn(2, 2, s, 16, generator=g) for s in (40, 70, 70))
+    dense = sparse_cross_attention(q, k, vv)
+    np.testing.assert_allclose(dense.numpy(), O.sparse_cross_attention(q.numpy(), k.numpy(), vv.numpy()),
+                               rtol=1e-5, atol=1e-5)
+    mask = torch.tensor([[True, False, True], [False, True, True]])
+    got = sparse_cross_attention(q, k, vv, mask, BLOCK_L=32, BLOCK_E=32)
+    want = O.sparse_cross_attention(q.numpy(), k.numpy(), vv.numpy(), mask.numpy(), 32, 32, empty_rows="nan")
+    np.testing.assert_allclose(got.numpy(), want, rtol=1e-5, atol=1e-5)
+    with pytest.raises(AssertionError, match="block_mask shape"):
+        sparse_cross_attention(q, k, vv, mask[:, :2], BLOCK_L=32, BLOCK_E=32)
+    with pytest.raises(ValueError, match="ROCm GPU"):
+        sparse_cross_attention(q, k, vv, kv_lengths=torch.tensor([3, 4]))
+
+
+def test_model_and_extensions_refuse_cpu_tensors():
+    """Everything beyond the three reference dispatchers (the fused model forward, the pack and
+    tokenize + pack extensions) runs on ROCm tensors only and says so."""
+    from cortex.kernels import ops
+    from cortex.kernels.tokenizer import tokenize_and_pack
     from cortex.models import CortexModel
     from cortex.models.config import CORTEX_XS
 
     n = torch.randn(4, 8)
     i = torch.zeros(3, dtype=torch.int64)
     with pytest.raises(RuntimeError, match="ROCm GPU"):
-        fused_tokenizer(n, n, n, i, i, i)
+        tokenize_and_pack(n, n, n, i, i, i, i, batch_size=1)
     with pytest.raises(RuntimeError, match="ROCm GPU"):
-        rms_norm_linear(torch.randn(2, 8), torch.ones(8), torch.randn(8, 4))
-    q = torch.randn(1, 1, 4, 8)
-    with pytest.raises(RuntimeError, match="ROCm GPU"):
-        sparse_cross_attention(q, q, q)
+        ops.pack_plan(i, 1)
     model = CortexModel(CORTEX_XS)
     with pytest.raises(RuntimeError, match="ROCm GPU"):
         model(i, i, i, i)
