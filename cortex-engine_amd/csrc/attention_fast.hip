@@ -392,7 +392,9 @@ void attention_fast_kernel(AttnArgs a) {
     }
   }
   af_wait_vm(0);  // the last chunk's unused stages: no transfer into LDS outlives the workgroup
-  const bool wt = wt_one_wave();
+  // the last element of the output view, in bytes from its base
+  const int64_t o_bytes = ((a.B - 1) * a.o_sb + (a.H - 1) * a.o_sh + (a.Lq - 1) * a.o_sl + a.Dh) * 2;
+  const WtOut store(a.out, o_bytes, wt_one_wave());
 
 #pragma unroll
   for (int qg = 0; qg < QG; ++qg) {
@@ -406,7 +408,7 @@ void attention_fast_kernel(AttnArgs a) {
         bf16x4 v;
 #pragma unroll
         for (int i = 0; i < 4; ++i) v[i] = (bf16)(o_acc[qg][t][i] * inv);
-        store_out(reinterpret_cast<bf16x4*>(O + 16 * t + 4 * g), v, wt);
+        store(reinterpret_cast<bf16x4*>(O + 16 * t + 4 * g), v);
       }
     }
   }

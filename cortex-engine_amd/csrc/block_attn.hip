@@ -387,7 +387,7 @@ __global__ __launch_bounds__(BA_THREADS) void qkv_attention_kernel(QkvAttnArgs a
       }
     }
   }
-  const bool wt = wt_one_wave();
+  const WtOut store(a.out, a.B * a.L * a.ld_o * (Q8OUT ? 1 : 2), wt_one_wave());
 #pragma unroll
   for (int qg = 0; qg < QG; ++qg) {
     const float l = l_acc[qg][0];
@@ -404,7 +404,7 @@ __global__ __launch_bounds__(BA_THREADS) void qkv_attention_kernel(QkvAttnArgs a
             const float y = o_acc[qg][t][i] * inv;
             pk |= (uint32_t)((int)fminf(fmaxf(rintf(y * a.out_inv_scale), -127.0f), 127.0f) & 0xff) << (8 * i);
           }
-          store_out(reinterpret_cast<uint32_t*>(O + 16 * t + 4 * g4), pk, wt);
+          store(reinterpret_cast<uint32_t*>(O + 16 * t + 4 * g4), pk);
         }
       } else {
         bf16* O = reinterpret_cast<bf16*>(a.out) + (row0 + q) * a.ld_o + h * 64;
@@ -413,7 +413,7 @@ __global__ __launch_bounds__(BA_THREADS) void qkv_attention_kernel(QkvAttnArgs a
           bf16x4 v;
 #pragma unroll
           for (int i = 0; i < 4; ++i) v[i] = (bf16)(o_acc[qg][t][i] * inv);
-          store_out(reinterpret_cast<bf16x4*>(O + 16 * t + 4 * g4), v, wt);
+          store(reinterpret_cast<bf16x4*>(O + 16 * t + 4 * g4), v);
         }
       }
     }

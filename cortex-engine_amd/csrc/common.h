@@ -70,27 +70,41 @@ __device__ __forceinline__ void mfma_16x16x32(f32x4& acc, const Frag<float>& a, 
 // otherwise starts only after the last store.  (Non-temporal stores skip that write-back too
 // but also bypass the infinity cache that the next kernel reads from.)
 //
-// Inline assembly, so the compiler neither counts these stores nor sees their hazards:
-//  * no code may read the stored bytes back in the same kernel;
-//  * the store reads its data VGPRs after issue, and a VALU write to them must wait two
-//    cycles after a store of more than 8 bytes (the compiler inserts this wait for its own
-//    stores and reuses the registers at once) -- the s_nop after each store provides it.
-template <class V>
-__device__ __forceinline__ void store_wt(V* p, const V& v) {
-  if constexpr (sizeof(V) == 16) {
+// The stores are the compiler's own buffer stores with the SC1 cache-policy bit, so it counts
+// them in its vmcnt waits and inserts the wait states their data registers need.  WtOut holds
+// the buffer descriptor of one output tensor (built once per kernel from its base, which must
+// be uniform: a kernel argument); a store passes its 32-bit byte offset from that base.  A
+// tensor of 4 GiB or more is written with plain stores.  No code may read the stored bytes back
+// in the same kernel.
+constexpr int CPOL_SC1 = 16;  // cache-policy operand: SC1 (device scope)
+struct WtOut {
+  __amdgpu_buffer_rsrc_t rsrc;
+  uint32_t base_lo;
+  bool wt;
+  // raw buffer (stride 0) over 4 GiB; word 3: the 32-bit data format that untyped accesses need
+  __device__ __forceinline__ WtOut(const void* base, int64_t bytes, bool wt_)
+      : rsrc(__builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, -1, 0x00020000)),
+        base_lo((uint32_t)(uintptr_t)base),
+        wt(wt_ && bytes < (1ll << 32)) {}
+  template <class V>
+  __device__ __forceinline__ void operator()(V* p, const V& v) const {
+    if (!wt) {
+      *p = v;
+      return;
+    }
     typedef unsigned u4 __attribute__((ext_vector_type(4)));
-    asm volatile("global_store_dwordx4 %0, %1, off sc1\n\ts_nop 2" ::"v"(p), "v"(__builtin_bit_cast(u4, v))
-                 : "memory");
-  } else if constexpr (sizeof(V) == 8) {
     typedef unsigned u2 __attribute__((ext_vector_type(2)));
-    asm volatile("global_store_dwordx2 %0, %1, off sc1\n\ts_nop 2" ::"v"(p), "v"(__builtin_bit_cast(u2, v))
-                 : "memory");
-  } else {
-    static_assert(sizeof(V) == 4, "4-, 8- or 16-byte stores");
-    asm volatile("global_store_dword %0, %1, off sc1\n\ts_nop 2" ::"v"(p), "v"(__builtin_bit_cast(unsigned, v))
-                 : "memory");
+    const uint32_t off = (uint32_t)(uintptr_t)p - base_lo;  // the byte offset (below 4 GiB)
+    if constexpr (sizeof(V) == 16) {
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4, v), rsrc, off, 0, CPOL_SC1);
+    } else if constexpr (sizeof(V) == 8) {
+      __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u2, v), rsrc, off, 0, CPOL_SC1);
+    } else {
+      static_assert(sizeof(V) == 4, "4-, 8- or 16-byte stores");
+      __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, v), rsrc, off, 0, CPOL_SC1);
+    }
   }
-}
+};
 
 // When write-through pays (measured on the Cortex-S forward, B = 32 / 64 / 256):
 //  * a GEMM or attention launch whose grid is a single wave of one workgroup per CU (MI355X:
@@ -106,13 +120,6 @@ __device__ __forceinline__ bool wt_one_wave() {
   return (int64_t)gridDim.x * gridDim.y * gridDim.z <= WT_MAX_WORKGROUPS;
 }
 __device__ __forceinline__ bool wt_fits(int64_t bytes) { return bytes <= WT_MAX_BYTES; }
-template <class V>
-__device__ __forceinline__ void store_out(V* p, const V& v, bool wt) {
-  if (wt)
-    store_wt(p, v);
-  else
-    *p = v;
-}
 
 // Operand element type of the direct-to-LDS GEMM loops: a 16-byte fragment per lane and the
 // MFMA that consumes it (bf16: 8 K-elements, fp32 accumulators; int8: 16 K-elements, int32

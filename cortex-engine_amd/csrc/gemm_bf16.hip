@@ -424,7 +424,7 @@ __global__ __launch_bounds__(TL::THREADS) void gemm_bf16_kernel(GemmArgs g) {
   //   !IL: tile j         -> n0 + wcol + 16 j + 4 g4 .. +3
   const float* bias = reinterpret_cast<const float*>(g.bias);
   TOUT* out = reinterpret_cast<TOUT*>(g.out) + (int64_t)kz * M * g.ld_out;
-  const bool wt = wt_one_wave();
+  const WtOut store(out, (int64_t)M * g.ld_out * (int64_t)sizeof(TOUT), wt_one_wave());
   constexpr int NV = IL ? 8 : 4;           // consecutive columns per lane and group
   constexpr int NG = IL ? TN / 2 : TN;     // column groups per lane
   // Every scale and bias load first, then one wait: a wait left to the compiler would
@@ -479,7 +479,7 @@ __global__ __launch_bounds__(TL::THREADS) void gemm_bf16_kernel(GemmArgs g) {
         bf16x8 o;
 #pragma unroll
         for (int e = 0; e < 8; ++e) o[e] = (bf16)v[e];
-        store_out(reinterpret_cast<bf16x8*>(op), o, wt);
+        store(reinterpret_cast<bf16x8*>(op), o);
       } else if constexpr (sizeof(TOUT) == 1) {  // int8 at the next linear's activation scale
         uint32_t lo = 0, hi = 0;
 #pragma unroll
@@ -489,11 +489,11 @@ __global__ __launch_bounds__(TL::THREADS) void gemm_bf16_kernel(GemmArgs g) {
           lo |= (uint32_t)(q0 & 0xff) << (8 * e);
           hi |= (uint32_t)(q1 & 0xff) << (8 * e);
         }
-        store_out(reinterpret_cast<uint2*>(op), make_uint2(lo, hi), wt);
+        store(reinterpret_cast<uint2*>(op), make_uint2(lo, hi));
       } else {
 #pragma unroll
         for (int h = 0; h < NV / 4; ++h)
-          store_out(reinterpret_cast<float4*>(op) + h, make_float4(v[4 * h], v[4 * h + 1], v[4 * h + 2], v[4 * h + 3]), wt);
+          store(reinterpret_cast<float4*>(op) + h, make_float4(v[4 * h], v[4 * h + 1], v[4 * h + 2], v[4 * h + 3]));
       }
     }
   }
@@ -754,7 +754,6 @@ __global__ __launch_bounds__(512) void norm_gemm_rk_kernel(NormGemmArgs g) {
   // plain stores: wavefronts w and w + 4 write alternate 16-byte pieces of each 128-byte output
   // line, which the L2 merges; written through, each half crosses to memory on its own (twice
   // the write bytes, no time saved)
-  constexpr bool wt = false;
   const int G = gridDim.x, total = gridDim.x * gridDim.y;
   const int id = xcd_affine(blockIdx.x + G * blockIdx.y, total);
   const int m0 = (id / G) * TL::BM, grp = id % G;
@@ -1031,10 +1030,10 @@ __global__ __launch_bounds__(512) void norm_gemm_rk_kernel(NormGemmArgs g) {
         bf16x8 o;
 #pragma unroll
         for (int e = 0; e < 8; ++e) o[e] = (bf16)v[e];
-        store_out(reinterpret_cast<bf16x8*>(op), o, wt);
+        *reinterpret_cast<bf16x8*>(op) = o;
       } else {
-        store_out(reinterpret_cast<float4*>(op), make_float4(v[0], v[1], v[2], v[3]), wt);
-        store_out(reinterpret_cast<float4*>(op + 4), make_float4(v[4], v[5], v[6], v[7]), wt);
+        *reinterpret_cast<float4*>(op) = make_float4(v[0], v[1], v[2], v[3]);
+        *reinterpret_cast<float4*>(op + 4) = make_float4(v[4], v[5], v[6], v[7]);
       }
     }
   };

@@ -38,12 +38,12 @@ __device__ __forceinline__ void dma16(const void* g, void* lds_block) {
   __builtin_amdgcn_global_load_lds(g, lds_block, 16, 0, 0);
 }
 
-// output row chunk of 8 values (global memory only; written through when wt)
-__device__ __forceinline__ void st_bf16x8(bf16* dst, const float (&f)[8], bool wt) {
+// output row chunk of 8 values (global memory only; written through as `store` says)
+__device__ __forceinline__ void st_bf16x8(bf16* dst, const float (&f)[8], const WtOut& store) {
   bf16x8 v;
 #pragma unroll
   for (int j = 0; j < 8; ++j) v[j] = (bf16)f[j];
-  store_out(reinterpret_cast<bf16x8*>(dst), v, wt);
+  store(reinterpret_cast<bf16x8*>(dst), v);
 }
 
 template <int BM_, int BN_, int WM_, int WN_, int STAGES_, int WBYTES_ = 1>
@@ -76,7 +76,6 @@ __global__ __launch_bounds__(TL::THREADS, 2) void gemm_pipe_kernel(GemmArgs g) {
   const int id = xcd_affine(blockIdx.x + nbx * blockIdx.y, total);
   const int m0 = (id / nbx) * BM, n0 = (id % nbx) * BN;
   const int M = (int)g.M, N = (int)g.N, K = (int)g.K;
-  const bool wt = wt_one_wave();
   const bf16* __restrict__ A = reinterpret_cast<const bf16*>(g.x);
   const unsigned char* __restrict__ W = reinterpret_cast<const unsigned char*>(g.w);
   constexpr int WROW = 64 * TL::WBYTES;  // bytes of one weight row per K step
@@ -190,6 +189,7 @@ __global__ __launch_bounds__(TL::THREADS, 2) void gemm_pipe_kernel(GemmArgs g) {
   const int res_rows = g.res_rows > 0 ? (int)g.res_rows : M;
   const float* res = reinterpret_cast<const float*>(g.res);
   TOUT* out = reinterpret_cast<TOUT*>(g.out);
+  const WtOut store(out, (int64_t)M * g.ld_out * (int64_t)sizeof(TOUT), wt_one_wave());
 #pragma unroll
   for (int p = 0; p < TM; ++p) {
 #pragma unroll
@@ -223,10 +223,10 @@ __global__ __launch_bounds__(TL::THREADS, 2) void gemm_pipe_kernel(GemmArgs g) {
       TOUT* op = out + (int64_t)m * g.ld_out + n;
       if (full) {
         if constexpr (sizeof(TOUT) == 2) {
-          st_bf16x8(reinterpret_cast<bf16*>(op), v, wt);
+          st_bf16x8(reinterpret_cast<bf16*>(op), v, store);
         } else {
-          store_out(reinterpret_cast<float4*>(op), make_float4(v[0], v[1], v[2], v[3]), wt);
-          store_out(reinterpret_cast<float4*>(op) + 1, make_float4(v[4], v[5], v[6], v[7]), wt);
+          store(reinterpret_cast<float4*>(op), make_float4(v[0], v[1], v[2], v[3]));
+          store(reinterpret_cast<float4*>(op) + 1, make_float4(v[4], v[5], v[6], v[7]));
         }
       } else {
         for (int e = 0; e < 8 && n + e < N; ++e) op[e] = from_f32<TOUT>(v[e]);

@@ -100,7 +100,9 @@ __global__ __launch_bounds__(RL_THREADS) void gemm_rowln_kernel(RowLnArgs g) {
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int fr = lane & 15, g4 = lane >> 4;
   const int M = (int)g.M, K = (int)g.K;
-  const bool wt = wt_one_wave();
+  // the fp32 residual rows and the normalised rows (bf16, or int8 with Q8), written through
+  const WtOut store_x(g.out, g.M * g.ld_out * 4, wt_one_wave());
+  const WtOut store_xn(g.xn, g.M * g.ld_xn * (Q8 ? 1 : 2), wt_one_wave());
   const int m0 = blockIdx.x * RL_BM;
   const int wcol = wid * WN;
 
@@ -304,8 +306,8 @@ __global__ __launch_bounds__(RL_THREADS) void gemm_rowln_kernel(RowLnArgs g) {
     if (m < M) {
 #pragma unroll
       for (int j = 0; j < TN; ++j)
-        store_out(reinterpret_cast<float4*>(g.out + (int64_t)m * g.ld_out + wcol + 16 * j + 4 * g4),
-                  make_float4(v[i][j][0], v[i][j][1], v[i][j][2], v[i][j][3]), wt);
+        store_x(reinterpret_cast<float4*>(g.out + (int64_t)m * g.ld_out + wcol + 16 * j + 4 * g4),
+                make_float4(v[i][j][0], v[i][j][1], v[i][j][2], v[i][j][3]));
     }
   }
 
@@ -385,7 +387,7 @@ __global__ __launch_bounds__(RL_THREADS) void gemm_rowln_kernel(RowLnArgs g) {
         o[1] = (bf16)y1;
         o[2] = (bf16)y2;
         o[3] = (bf16)y3;
-        store_out(reinterpret_cast<bf16x4*>(reinterpret_cast<bf16*>(g.xn) + (int64_t)m * g.ld_xn + n), o, wt);
+        store_xn(reinterpret_cast<bf16x4*>(reinterpret_cast<bf16*>(g.xn) + (int64_t)m * g.ld_xn + n), o);
       }
     }
   }

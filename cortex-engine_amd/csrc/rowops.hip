@@ -56,7 +56,8 @@ __global__ __launch_bounds__(256) void ln_rows_kernel(const float* __restrict__ 
   const int lane = threadIdx.x & 63;
   const int64_t m = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
   if (m >= M) return;
-  constexpr bool wt = true;
+  const WtOut store_bf(out_bf, M * ld_bf * 2, true), store_f(out_f, M * ld_f * 4, true),
+      store_q(out_q, M * ld_q, true);
   const float* row = x + m * ld_x;
   float v[EPL];
 #pragma unroll
@@ -79,15 +80,15 @@ __global__ __launch_bounds__(256) void ln_rows_kernel(const float* __restrict__ 
       b[1] = (bf16)v[j + 1];
       b[2] = (bf16)v[j + 2];
       b[3] = (bf16)v[j + 3];
-      store_out(reinterpret_cast<bf16x4*>(out_bf + m * ld_bf + k), b, wt);
+      store_bf(reinterpret_cast<bf16x4*>(out_bf + m * ld_bf + k), b);
     }
-    if (out_f) store_out(reinterpret_cast<float4*>(out_f + m * ld_f + k), make_float4(v[j], v[j + 1], v[j + 2], v[j + 3]), wt);
+    if (out_f) store_f(reinterpret_cast<float4*>(out_f + m * ld_f + k), make_float4(v[j], v[j + 1], v[j + 2], v[j + 3]));
     if (out_q) {  // W8A8: clamp(rint(y * q_inv), -127, 127)
       uint32_t pk = 0;
 #pragma unroll
       for (int i = 0; i < 4; ++i)
         pk |= (uint32_t)((int)fminf(fmaxf(rintf(v[j + i] * q_inv), -127.0f), 127.0f) & 0xff) << (8 * i);
-      store_out(reinterpret_cast<uint32_t*>(out_q + m * ld_q + k), pk, wt);
+      store_q(reinterpret_cast<uint32_t*>(out_q + m * ld_q + k), pk);
     }
   }
 }
@@ -108,7 +109,7 @@ __global__ __launch_bounds__(256) void norm_rows_kernel(const TX* __restrict__ x
   const int lane = threadIdx.x & 63;
   const int64_t m = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
   if (m >= M) return;
-  constexpr bool wt = true;
+  const WtOut store(out, M * ld_out * 2, true);
   const TX* row = x + m * ld_x;
   float v[EPL];
 #pragma unroll
@@ -161,7 +162,7 @@ __global__ __launch_bounds__(256) void norm_rows_kernel(const TX* __restrict__ x
     o[1] = (bf16)v[j + 1];
     o[2] = (bf16)v[j + 2];
     o[3] = (bf16)v[j + 3];
-    store_out(reinterpret_cast<bf16x4*>(out + m * ld_out + (j >> 2) * 256 + lane * 4), o, wt);
+    store(reinterpret_cast<bf16x4*>(out + m * ld_out + (j >> 2) * 256 + lane * 4), o);
   }
 }
 
@@ -236,7 +237,7 @@ __global__ __launch_bounds__(256) void tokenize_ln_kernel(TokLnArgs a) {
   const int lane = threadIdx.x & 63;
   const int64_t r0 = ((int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6)) * R;
   if (r0 >= a.E) return;
-  const bool wt = wt_fits(a.E * K * 2);
+  const WtOut store(a.out, a.E * a.ld_out * 2, wt_fits(a.E * K * 2));
   const int64_t end = a.csr_end ? *a.csr_end : a.E;
   int64_t e[R];
 #pragma unroll
@@ -319,7 +320,7 @@ __global__ __launch_bounds__(256) void tokenize_ln_kernel(TokLnArgs a) {
       o[1] = (bf16)((v[i][j + 1] - mean) * rstd * g.y + b.y);
       o[2] = (bf16)((v[i][j + 2] - mean) * rstd * g.z + b.z);
       o[3] = (bf16)((v[i][j + 3] - mean) * rstd * g.w + b.w);
-      store_out(reinterpret_cast<bf16x4*>(out + (j >> 2) * 256 + lane * 4), o, wt);
+      store(reinterpret_cast<bf16x4*>(out + (j >> 2) * 256 + lane * 4), o);
     }
   }
 }

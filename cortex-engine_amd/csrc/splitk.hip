@@ -31,7 +31,7 @@ struct ReduceArgs {
 
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(ReduceArgs a) {
   const int64_t groups = a.M * (a.N >> 2);
-  constexpr bool wt = true;  // few rows (the K split serves B <= 8)
+  const WtOut store(a.out, a.M * a.ld_out * 4, true);  // few rows (the K split serves B <= 8)
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < groups; i += (int64_t)gridDim.x * blockDim.x) {
     const int64_t m = i / (a.N >> 2), c = (i - m * (a.N >> 2)) * 4;
     const float* p = a.part + m * a.N + c;
@@ -45,7 +45,7 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(ReduceArgs a) {
       s.x += b.x; s.y += b.y; s.z += b.z; s.w += b.w;
     }
     const float4 r = *reinterpret_cast<const float4*>(a.res + (m % a.res_rows) * a.ld_res + c);
-    store_out(reinterpret_cast<float4*>(a.out + m * a.ld_out + c), make_float4(s.x + r.x, s.y + r.y, s.z + r.z, s.w + r.w), wt);
+    store(reinterpret_cast<float4*>(a.out + m * a.ld_out + c), make_float4(s.x + r.x, s.y + r.y, s.z + r.z, s.w + r.w));
   }
 }
 
@@ -65,7 +65,7 @@ __global__ __launch_bounds__(256) void splitk_reduce_ln_kernel(ReduceLnArgs a) {
   const int64_t m = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
   if (m >= a.r.M) return;
   const int64_t N = a.r.N;
-  constexpr bool wt = true;
+  const WtOut store_x(a.r.out, a.r.M * a.r.ld_out * 4, true), store_xn(a.xn, a.r.M * a.ld_xn * 2, true);
   float v[EPL];
 #pragma unroll
   for (int j = 0; j < EPL; j += 4) {
@@ -85,7 +85,7 @@ __global__ __launch_bounds__(256) void splitk_reduce_ln_kernel(ReduceLnArgs a) {
     v[j + 1] = s.y + r.y;
     v[j + 2] = s.z + r.z;
     v[j + 3] = s.w + r.w;
-    store_out(reinterpret_cast<float4*>(a.r.out + m * a.r.ld_out + k), make_float4(v[j], v[j + 1], v[j + 2], v[j + 3]), wt);
+    store_x(reinterpret_cast<float4*>(a.r.out + m * a.r.ld_out + k), make_float4(v[j], v[j + 1], v[j + 2], v[j + 3]));
   }
   ln_regs<EPL>(v, 1.0f / (float)N, a.eps, a.gamma, a.beta, lane);
 #pragma unroll
@@ -95,7 +95,7 @@ __global__ __launch_bounds__(256) void splitk_reduce_ln_kernel(ReduceLnArgs a) {
     o[1] = (bf16)v[j + 1];
     o[2] = (bf16)v[j + 2];
     o[3] = (bf16)v[j + 3];
-    store_out(reinterpret_cast<bf16x4*>(a.xn + m * a.ld_xn + (j >> 2) * 256 + lane * 4), o, wt);
+    store_xn(reinterpret_cast<bf16x4*>(a.xn + m * a.ld_xn + (j >> 2) * 256 + lane * 4), o);
   }
 }
 

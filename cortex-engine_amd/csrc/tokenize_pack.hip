@@ -425,7 +425,7 @@ __global__ __launch_bounds__(256) void row_writer_kernel(RowArgs a) {
   }
   if (e >= a.E) e = -1;  // defensive: never follow a corrupt order entry
   T* out = reinterpret_cast<T*>(a.out) + r * a.out_ld;
-  const bool wt = wt_fits(rows * a.D * (int64_t)sizeof(T));
+  const WtOut store(a.out, rows * a.out_ld * (int64_t)sizeof(T), wt_fits(rows * a.D * (int64_t)sizeof(T)));
   const T* s0 = nullptr;
   const T* s1 = nullptr;
   const T* s2 = nullptr;
@@ -463,7 +463,7 @@ __global__ __launch_bounds__(256) void row_writer_kernel(RowArgs a) {
       } else {
         o = *reinterpret_cast<const V*>(s0 + d);
       }
-      store_out(reinterpret_cast<V*>(out + d), o, wt);
+      store(reinterpret_cast<V*>(out + d), o);
     }
   } else {
     for (int64_t d = lane; d < a.D; d += 64) {
