@@ -432,11 +432,7 @@ int try_attention_fast(const AttnArgs& a, int dtype, hipStream_t stream) {
   const int64_t nbh = a.B * a.H;
   // 32 queries per wavefront (K/V fragments read once per two MFMAs) while that still
   // gives every CU a workgroup; 16 otherwise
-  static const int env_qg = [] {
-    const char* e = getenv("CORTEX_ATTN_QG");
-    return e ? atoi(e) : 0;
-  }();
-  const int qg = env_qg == 1 || env_qg == 2 ? env_qg : (cdiv(a.Lq, 16 * 2 * AF_WAVES) * nbh >= 256 ? 2 : 1);
+  const int qg = cdiv(a.Lq, 16 * 2 * AF_WAVES) * nbh >= 256 ? 2 : 1;
   const int64_t nqb = cdiv(a.Lq, 16 * qg * AF_WAVES);
   if (nbh > 65535 || nqb * nbh > 0x7fffffffLL) return 0;
   // K byte offsets from a (sample, head) start are 32-bit buffer offsets

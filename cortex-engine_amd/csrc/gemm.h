@@ -40,11 +40,6 @@ struct GemmArgs {
   float rms_eps;
 };
 
-// Fast path for aligned bf16-compute GEMMs (gemm_fast.hip).  Returns 1 when it
-// launched the kernel, 0 when the request is outside its specialisations (the
-// caller then uses the general kernel), or a negative status on a launch error.
-int try_gemm_fast(const GemmArgs& g, int x_dtype, int w_dtype, int w_layout, int compute, hipStream_t stream);
-
 // bf16 x bf16 path with a register epilogue (gemm_bf16.hip), same return convention.
 int try_gemm_bf16(const GemmArgs& g, int x_dtype, int w_dtype, int w_layout, int compute, hipStream_t stream);
 

@@ -510,11 +510,8 @@ int launch(const GemmArgs& g, hipStream_t stream) {
 }
 
 using B128x128s2 = BTile<128, 128, 2, 2, 2>;
-using B128x128s3 = BTile<128, 128, 3, 2, 2>;
 using B256x128s2 = BTile<256, 128, 2, 4, 2>;
-using B128x256s2 = BTile<128, 256, 2, 2, 4>;
 using B256x256s2 = BTile<256, 256, 2, 4, 2>;
-using B64x128s2 = BTile<64, 128, 2, 1, 2>;
 using B256x192s2 = BTile<256, 192, 2, 4, 2>;
 using B128x128s2k2 = BTile<128, 128, 2, 2, 2, 2>;
 
@@ -529,61 +526,30 @@ int cu_count() {
   return v;
 }
 
-int bf16_tile() {
-  static int v = [] {
-    const char* s = getenv("CORTEX_BF16_TILE");
-    return s ? atoi(s) : -1;
-  }();
-  return v;
+// Tile by shape: 256-row tiles halve the operand traffic per MFMA, so take the widest tile
+// that still fills (nearly) every CU once, else 128 x 128 (two workgroups per CU).
+enum TileChoice { T128 = 0, T256 = 4, T192 = 6, T128_K2 = 7 };
+TileChoice wide_tile(const GemmArgs& g, bool allow192) {
+  const int64_t t256 = cdiv(g.M, 256) * cdiv(g.N, 256), t192 = cdiv(g.M, 256) * cdiv(g.N, 192);
+  const int ncu = cu_count();
+  if (g.N % 256 == 0 && t256 >= ncu * 15 / 16) return T256;
+  if (allow192 && g.N % 192 == 0 && t192 >= ncu * 15 / 16 && t192 <= ncu) return T192;
+  if (t256 >= ncu * 3 / 4) return T256;
+  return T128;
 }
 
 template <int ACT, bool RES, class TOUT, class TW = bf16>
 int dispatch(const GemmArgs& g, hipStream_t stream) {
-  constexpr bool W8 = sizeof(TW) == 1;  // int8 weights: two-stage rings without the 192-column tile
-  int t = bf16_tile();
-  if (t < 0) {
-    // 256-row tiles halve the operand traffic per MFMA; take the widest tile that still
-    // fills (nearly) every CU once, else 128x128 (two workgroups per CU)
-    const int64_t t256 = cdiv(g.M, 256) * cdiv(g.N, 256), t192 = cdiv(g.M, 256) * cdiv(g.N, 192);
-    const int ncu = cu_count();
-    if (g.N % 256 == 0 && t256 >= ncu * 15 / 16)
-      t = 4;
-    else if (!W8 && g.N % 192 == 0 && t192 >= ncu * 15 / 16 && t192 <= ncu)
-      t = 6;
-    else if (t256 >= ncu * 3 / 4)
-      t = 4;
-    else
-      t = 0;
-  }
-  if constexpr (W8) {
-    // (the 256 x 256 tile has no room for the weight registers: 256 x 128 instead)
-    switch (t) {
-      case 2:
-      case 4:
-        return launch<B256x128s2, ACT, RES, TOUT, bf16, TW>(g, stream);
-      case 3:
-        return launch<B128x256s2, ACT, RES, TOUT, bf16, TW>(g, stream);
-      case 5:
-        return launch<B64x128s2, ACT, RES, TOUT, bf16, TW>(g, stream);
-      default:
-        return launch<B128x128s2, ACT, RES, TOUT, bf16, TW>(g, stream);
-    }
+  if constexpr (sizeof(TW) == 1) {
+    // int8 weights widened through registers: the 256 x 256 tile has no room for the weight
+    // registers (256 x 128 instead), and no 192-column tile
+    return wide_tile(g, false) == T256 ? launch<B256x128s2, ACT, RES, TOUT, bf16, TW>(g, stream)
+                                       : launch<B128x128s2, ACT, RES, TOUT, bf16, TW>(g, stream);
   } else {
-    switch (t) {
-      case 1:
-        return launch<B128x128s3, ACT, RES, TOUT>(g, stream);
-      case 2:
-        return launch<B256x128s2, ACT, RES, TOUT>(g, stream);
-      case 3:
-        return launch<B128x256s2, ACT, RES, TOUT>(g, stream);
-      case 4:
-        return launch<B256x256s2, ACT, RES, TOUT>(g, stream);
-      case 5:
-        return launch<B64x128s2, ACT, RES, TOUT>(g, stream);
-      case 6:
-        return launch<B256x192s2, ACT, RES, TOUT>(g, stream);
-      default:
-        return launch<B128x128s2, ACT, RES, TOUT>(g, stream);
+    switch (wide_tile(g, true)) {
+      case T256: return launch<B256x256s2, ACT, RES, TOUT>(g, stream);
+      case T192: return launch<B256x192s2, ACT, RES, TOUT>(g, stream);
+      default: return launch<B128x128s2, ACT, RES, TOUT>(g, stream);
     }
   }
 }
@@ -594,46 +560,14 @@ int dispatch(const GemmArgs& g, hipStream_t stream) {
 // 128 x 128 workgroup per CU the K split of the residual GEMMs.
 template <int ACT, class TOUT>
 int dispatch_rs(const GemmArgs& g, hipStream_t stream) {
-  int t = bf16_tile();
-  if (t != 0 && t != 4 && t != 6 && !(t == 7 && g.K % 128 == 0)) {
-    const int64_t t256 = cdiv(g.M, 256) * cdiv(g.N, 256), t192 = cdiv(g.M, 256) * cdiv(g.N, 192);
-    const int64_t t128 = cdiv(g.M, 128) * cdiv(g.N, 128);
-    const int ncu = cu_count();
-    if (g.N % 256 == 0 && t256 >= ncu * 15 / 16)
-      t = 4;
-    else if (g.N % 192 == 0 && t192 >= ncu * 15 / 16 && t192 <= ncu)
-      t = 6;
-    else if (t256 >= ncu * 3 / 4)
-      t = 4;
-    else if (g.K % 128 == 0 && t128 <= ncu)
-      t = 7;  // at most one workgroup per CU: K split over two wave groups (eight wavefronts)
-    else
-      t = 0;
-  }
+  TileChoice t = wide_tile(g, true);
+  // at most one 128 x 128 workgroup per CU: K split over two wave groups (eight wavefronts)
+  if (t == T128 && g.K % 128 == 0 && cdiv(g.M, 128) * cdiv(g.N, 128) <= cu_count()) t = T128_K2;
   switch (t) {
-    case 4: return launch<B256x256s2, ACT, false, TOUT, bf16, bf16, true>(g, stream);
-    case 6: return launch<B256x192s2, ACT, false, TOUT, bf16, bf16, true>(g, stream);
-    case 7: return launch<B128x128s2k2, ACT, false, TOUT, bf16, bf16, true>(g, stream);
+    case T256: return launch<B256x256s2, ACT, false, TOUT, bf16, bf16, true>(g, stream);
+    case T192: return launch<B256x192s2, ACT, false, TOUT, bf16, bf16, true>(g, stream);
+    case T128_K2: return launch<B128x128s2k2, ACT, false, TOUT, bf16, bf16, true>(g, stream);
     default: return launch<B128x128s2, ACT, false, TOUT, bf16, bf16, true>(g, stream);
-  }
-}
-
-template <class TW>
-int dispatch_res(const GemmArgs& g, int t, hipStream_t stream) {
-  switch (t) {
-    case 7:
-      return g.K % 128 ? 0 : launch<B128x128s2k2, ACT_NONE, true, float, bf16, TW>(g, stream);
-    case 1:
-      if constexpr (sizeof(TW) == 1) return 0;
-      else return launch<B128x128s3, ACT_NONE, true, float>(g, stream);
-    case 2:
-      return launch<B256x128s2, ACT_NONE, true, float, bf16, TW>(g, stream);
-    case 3:
-      return launch<B128x256s2, ACT_NONE, true, float, bf16, TW>(g, stream);
-    case 5:
-      return launch<B64x128s2, ACT_NONE, true, float, bf16, TW>(g, stream);
-    default:
-      return launch<B128x128s2, ACT_NONE, true, float, bf16, TW>(g, stream);
   }
 }
 
@@ -1154,16 +1088,13 @@ int try_gemm_bf16(const GemmArgs& g, int x_dtype, int w_dtype, int w_layout, int
   const bool out_bf16 = g.out_dtype == DT_BF16;
   if (!out_bf16 && g.out_dtype != DT_F32) return 0;
   if (!aligned16(g.out) || g.ld_out % 8) return 0;
-  // Residual (fp32 in/out) GEMMs are memory bound.
+  // Residual (fp32 in/out) GEMMs are memory bound: 128 x 128 tiles with K split over two wave
+  // groups (eight wavefronts per CU) while the grid is at most one workgroup per CU; larger
+  // grids go to the pipelined kernel (gemm_pipe.hip)
   if (res) {
-    if (g.act) return 0;
-    const char* e = getenv("CORTEX_RES_TILE");
-    int t = e ? atoi(e) : -1;
-    // default: 128x128 tiles with K split over two wave groups (eight wavefronts per CU)
-    // while the grid is at most one workgroup per CU; larger grids go to the pipelined kernel
-    if (t < 0) t = (g.K % 128 == 0 && cdiv(g.M, 128) * cdiv(g.N, 128) <= cu_count()) ? 7 : 10;
-    if (t >= 10) return 0;
-    return w8 ? dispatch_res<int8_t>(g, t, stream) : dispatch_res<bf16>(g, t, stream);
+    if (g.act || g.K % 128 || cdiv(g.M, 128) * cdiv(g.N, 128) > cu_count()) return 0;
+    return w8 ? launch<B128x128s2k2, ACT_NONE, true, float, bf16, int8_t>(g, stream)
+              : launch<B128x128s2k2, ACT_NONE, true, float, bf16, bf16>(g, stream);
   }
   if (w8) {
     if (out_bf16)
@@ -1225,36 +1156,18 @@ extern "C" int cortex_linear_w8a8(int64_t M, int64_t N, int64_t K, const int8_t*
   g.out_inv_scale = out_dtype == DT_I8 ? 1.0f / out_scale : 0.0f;
   const int ncu = cu_count();
   const int64_t t128 = cdiv(M, 128) * cdiv(N, 128), t256 = cdiv(M, 256) * cdiv(N, 256);
-  static const int tile_env = [] {
-    const char* e = getenv("CORTEX_W8A8_TILE");
-    return e ? atoi(e) : -1;
-  }();
   int st;
   if (out_dtype == DT_I8) {
-    int t = tile_env;
-    if (t < 0) t = (N % 256 == 0 && t256 >= ncu * 15 / 16) ? 4 : 0;
-    if (act == ACT_GELU) {
-      switch (t) {
-        case 4: st = launch<B256x256s2, ACT_GELU, false, int8_t, int8_t>(g, stream); break;
-        case 2: st = launch<B256x128s2, ACT_GELU, false, int8_t, int8_t>(g, stream); break;
-        case 3: st = launch<B128x256s2, ACT_GELU, false, int8_t, int8_t>(g, stream); break;
-        case 1: st = launch<B128x128s3, ACT_GELU, false, int8_t, int8_t>(g, stream); break;
-        default: st = launch<B128x128s2, ACT_GELU, false, int8_t, int8_t>(g, stream); break;
-      }
-    } else {
-      st = t == 4 ? launch<B256x256s2, ACT_NONE, false, int8_t, int8_t>(g, stream)
-                  : launch<B128x128s2, ACT_NONE, false, int8_t, int8_t>(g, stream);
-    }
+    const bool wide = N % 256 == 0 && t256 >= ncu * 15 / 16;
+    if (act == ACT_GELU)
+      st = wide ? launch<B256x256s2, ACT_GELU, false, int8_t, int8_t>(g, stream)
+                : launch<B128x128s2, ACT_GELU, false, int8_t, int8_t>(g, stream);
+    else
+      st = wide ? launch<B256x256s2, ACT_NONE, false, int8_t, int8_t>(g, stream)
+                : launch<B128x128s2, ACT_NONE, false, int8_t, int8_t>(g, stream);
   } else if (res) {
-    int t = tile_env;
-    if (t < 0) t = (K % 256 == 0 && t128 <= ncu) ? 7 : 0;
-    switch (t) {
-      case 7: st = K % 256 ? 0 : launch<B128x128s2k2, ACT_NONE, true, float, int8_t>(g, stream); break;
-      case 2: st = launch<B256x128s2, ACT_NONE, true, float, int8_t>(g, stream); break;
-      case 5: st = launch<B64x128s2, ACT_NONE, true, float, int8_t>(g, stream); break;
-      case 1: st = launch<B128x128s3, ACT_NONE, true, float, int8_t>(g, stream); break;
-      default: st = launch<B128x128s2, ACT_NONE, true, float, int8_t>(g, stream); break;
-    }
+    st = (K % 256 == 0 && t128 <= ncu) ? launch<B128x128s2k2, ACT_NONE, true, float, int8_t>(g, stream)
+                                       : launch<B128x128s2, ACT_NONE, true, float, int8_t>(g, stream);
   } else {
     st = act == ACT_GELU ? launch<B128x128s2, ACT_GELU, false, float, int8_t>(g, stream)
                          : launch<B128x128s2, ACT_NONE, false, float, int8_t>(g, stream);

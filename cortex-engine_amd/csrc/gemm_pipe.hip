@@ -246,69 +246,25 @@ int launch(const GemmArgs& g, hipStream_t stream) {
 }
 
 using P128x128s3 = PTile<128, 128, 2, 2, 3>;
-using P128x128s4 = PTile<128, 128, 2, 2, 4>;
 using P64x128s3 = PTile<64, 128, 1, 2, 3>;
-using P128x64s3 = PTile<128, 64, 2, 1, 3>;
 using Q128x128s2 = PTile<128, 128, 2, 2, 2, 2>;
-using Q128x128s3 = PTile<128, 128, 2, 2, 3, 2>;
-using Q128x64s3 = PTile<128, 64, 2, 1, 3, 2>;
 using Q64x128s3 = PTile<64, 128, 1, 2, 3, 2>;
 
-int residual_tile() {
-  static int v = [] {
-    const char* s = getenv("CORTEX_RES_TILE");
-    return s ? atoi(s) : -1;
-  }();
-  return v;
-}
-
-int pipe_tile() {
-  static int v = [] {
-    const char* s = getenv("CORTEX_PIPE_TILE");
-    return s ? atoi(s) : -1;
-  }();
-  return v;
-}
-
+// int8 weights: small grids (N = 512) get the 64-row tile for twice the workgroups
 template <int ACT, bool RES, class TOUT>
 int dispatch_i8(const GemmArgs& g, hipStream_t stream) {
-  int t = pipe_tile();
-  if (t < 0) {
-    const int64_t tiles = cdiv(g.M, 128) * cdiv(g.N, 128);
-    t = tiles < 512 ? 2 : 0;  // small grids (N = 512) get the 64-row tile for twice the workgroups
-  }
-  switch (t) {
-    case 1:
-      return launch<P128x128s4, ACT, RES, TOUT>(g, stream);
-    case 2:
-      return launch<P64x128s3, ACT, RES, TOUT>(g, stream);
-    case 3:
-      return launch<P128x64s3, ACT, RES, TOUT>(g, stream);
-    default:
-      return launch<P128x128s3, ACT, RES, TOUT>(g, stream);
-  }
+  return cdiv(g.M, 128) * cdiv(g.N, 128) < 512 ? launch<P64x128s3, ACT, RES, TOUT>(g, stream)
+                                                : launch<P128x128s3, ACT, RES, TOUT>(g, stream);
 }
 
+// bf16 weights: residual GEMMs (memory bound) take 64-row tiles, twice the workgroups per CU;
+// the others 128 x 128 with two stages (two workgroups per CU)
 template <int ACT, bool RES, class TOUT>
 int dispatch_bf16(const GemmArgs& g, hipStream_t stream) {
-  int t = pipe_tile();
-  if (t < 0) {
-    // residual GEMMs (memory bound): 64-row tiles, twice the workgroups per CU;
-    // otherwise 128x128 with two stages (two workgroups per CU)
-    t = RES ? 12 : 11;
-    const int r = residual_tile();
-    if (RES && r >= 10) t = r;
-  }
-  switch (t) {
-    case 11:
-      return launch<Q128x128s2, ACT, RES, TOUT>(g, stream);
-    case 12:
-      return launch<Q64x128s3, ACT, RES, TOUT>(g, stream);
-    case 13:
-      return launch<Q128x128s3, ACT, RES, TOUT>(g, stream);
-    default:
-      return launch<Q128x64s3, ACT, RES, TOUT>(g, stream);
-  }
+  if constexpr (RES)
+    return launch<Q64x128s3, ACT, RES, TOUT>(g, stream);
+  else
+    return launch<Q128x128s2, ACT, RES, TOUT>(g, stream);
 }
 
 template <int ACT, bool RES, class TOUT>
