@@ -169,12 +169,12 @@ def make_kernel(name: str, dev):
         nid, tb, val, bidx = (torch.from_numpy(a).to(dev) for a in make_events(B_MAIN, PER_MAIN, seed=3))
         ne, te, ve = rnd(512, D, scale=0.02), rnd(1024, D, scale=0.02), rnd(8, D, scale=0.02)
         lw, lb = rnd(D), rnd(D)
-        offsets, order, _ = ops.pack_plan(bidx, B_MAIN)
+        offsets, order, _, ident = ops.pack_plan(bidx, B_MAIN, with_rank=False, identity=True)
         fn = lambda: ops.tokenize_ln(ne, te, ve, nid, tb, val, (lw, lb, 1e-5), order=order,  # noqa: E731
-                                     csr_offsets=offsets)
-        # compulsory: 3 indices + the order entry per event, bf16 row out, the touched table rows
-        # (137 neuron, 600 time, 8 value) and the LayerNorm parameters
-        by = E * (D * 2 + 4 * 8) + (137 + 600 + 8) * D * 4 + 2 * D * 4 + (B_MAIN + 1) * 8
+                                     csr_offsets=offsets, identity=ident)
+        # compulsory: 3 indices per event (the sorted plan is the identity), bf16 row out, the
+        # touched table rows (137 neuron, 600 time, 8 value) and the LayerNorm parameters
+        by = E * (D * 2 + 3 * 8) + (137 + 600 + 8) * D * 4 + 2 * D * 4 + (B_MAIN + 1) * 8
         return fn, 1, "hbm", 0.0, by, ("fused tokenizer + norm_kv LayerNorm into bf16 CSR rows, E=16384 D=512 "
                                       "(tokenize_ln_kernel)")
     if name.startswith("api_"):
@@ -335,8 +335,8 @@ def section_breakdown(model, inputs, dev, step_ms: float):
     err = torch.zeros(1, dtype=torch.int32, device=dev)
     blk = enc.self_attn_blocks[0]
     with torch.no_grad():
-        offsets, order, _ = ops.pack_plan(bidx, B, err=err, with_rank=False)
-        tokens = model._token_rows(nid, tb, val, offsets, order, err)
+        offsets, order, _, ident = ops.pack_plan(bidx, B, err=err, with_rank=False, identity=True)
+        tokens = model._token_rows(nid, tb, val, offsets, order, err, ident)
         x0, xn0 = model._cross_rows(tokens, offsets, B)
         lat = model._encode(x0.clone(), B, xn0)
         x_all, x_one, x_mlp = x0.clone(), x0.clone(), x0.clone()
@@ -347,8 +347,8 @@ def section_breakdown(model, inputs, dev, step_ms: float):
             return apply_linear(blk.mlp[2], h, residual=x_mlp, out_dtype=torch.float32, compute=comp, out=x_mlp)
 
         parts = {
-            "pack_plan": lambda: ops.pack_plan(bidx, B, err=err, with_rank=False),
-            "tokenizer": lambda: model._token_rows(nid, tb, val, offsets, order, err),
+            "pack_plan": lambda: ops.pack_plan(bidx, B, err=err, with_rank=False, identity=True),
+            "tokenizer": lambda: model._token_rows(nid, tb, val, offsets, order, err, ident),
             "cross_attn": lambda: model._cross_rows(tokens, offsets, B),
             "self_attn_all": lambda: model._encode(x_all, B, xn0),
             "self_attn_single": lambda: blk.forward_rows(x_one, B, L, inplace=True, xn=xn0),

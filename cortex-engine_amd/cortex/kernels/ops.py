@@ -51,11 +51,14 @@ def _row_major_2d(x: torch.Tensor) -> torch.Tensor:
 
 
 def pack_plan(batch_indices: torch.Tensor, batch_size: int, err: torch.Tensor | None = None, *,
-              with_rank: bool = True):
+              with_rank: bool = True, identity: bool = False):
     """Stable CSR plan of ragged events: ``(offsets (B+1), order (E), rank (E))``.
 
     offsets/order/rank are int64 device tensors; see ``cortex_pack_plan``.  With
     ``with_rank=False`` the rank is not written and ``None`` is returned in its place.
+    With ``identity=True`` a fourth value is returned, the plan's int32 identity flag: a
+    plan of sorted indices sets it and leaves ``order`` unwritten, so ``order`` may only be
+    handed on together with the flag (``tokenize`` / ``tokenize_ln`` take both).
     """
     dev = nat.require_gpu(batch_indices, what="pack_plan")
     if batch_indices.dtype != torch.int64 or batch_indices.dim() != 1:
@@ -65,21 +68,25 @@ def pack_plan(batch_indices: torch.Tensor, batch_size: int, err: torch.Tensor | 
     offsets = torch.empty(B + 1, dtype=torch.int64, device=dev)
     order = torch.empty(E, dtype=torch.int64, device=dev)
     rank = torch.empty(E, dtype=torch.int64, device=dev) if with_rank else None
+    ident = torch.empty(1, dtype=torch.int32, device=dev) if identity else None
     ws_bytes = nat.load().cortex_pack_workspace_bytes(E, B)
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
     nat.call("cortex_pack_plan", nat.ptr(batch_indices), batch_indices.stride(0) if E else 1, E, B,
              nat.ptr(offsets), nat.ptr(order), None, nat.ptr(rank), nat.ptr(ws), ws_bytes, nat.ptr(err),
-             nat.stream_of(dev))
-    return offsets, order, rank
+             nat.ptr(ident), nat.stream_of(dev))
+    return (offsets, order, rank, ident) if identity else (offsets, order, rank)
 
 
 def tokenize(neuron_emb, time_emb, value_emb, neuron_ids, time_bins, values, *, order=None, offsets=None,
-             csr_offsets=None, batch_size: int = 0, max_events: int = 0, out=None, mask=None, err=None):
+             csr_offsets=None, batch_size: int = 0, max_events: int = 0, out=None, mask=None, err=None,
+             identity=None):
     """Fused gather-add ``(N[nid] + T[tb]) + V[val]`` into CSR rows (``offsets`` None) or
     the padded ``(B, max_events, D)`` layout with its mask (``offsets`` given).
 
     In CSR mode pass the plan's offsets as ``csr_offsets``: rows past
     ``offsets[B]`` (events dropped for an invalid batch index) are then zeroed.
+    ``identity``: the plan's identity flag (``pack_plan(..., identity=True)``), when ``order``
+    came from such a plan.
     """
     dev = nat.require_gpu(neuron_emb, time_emb, value_emb, neuron_ids, time_bins, values, what="tokenize")
     D = neuron_emb.shape[1]
@@ -98,16 +105,16 @@ def tokenize(neuron_emb, time_emb, value_emb, neuron_ids, time_bins, values, *, 
              nat.ptr(value_emb), value_emb.shape[0], value_emb.stride(0),
              nat.ptr(neuron_ids), st[0], nat.ptr(time_bins), st[1], nat.ptr(values), st[2], E,
              nat.ptr(order), _end_ptr(csr_offsets), nat.ptr(offsets), batch_size, max_events, nat.ptr(out),
-             ld_out, nat.ptr(mask) if padded else None, nat.ptr(err), nat.stream_of(dev))
+             ld_out, nat.ptr(mask) if padded else None, nat.ptr(identity), nat.ptr(err), nat.stream_of(dev))
     return (out, mask) if padded else out
 
 
 def tokenize_ln(neuron_emb, time_emb, value_emb, neuron_ids, time_bins, values, ln, *, order=None,
-                csr_offsets=None, err=None, out=None) -> torch.Tensor:
+                csr_offsets=None, err=None, out=None, identity=None) -> torch.Tensor:
     """``LN((N[nid] + T[tb]) + V[val])`` as bf16 CSR rows (one launch, fp32 tokens never stored).
 
-    ``ln`` is ``(weight, bias, eps)``; rows follow ``order`` (the pack plan) and rows past
-    ``csr_offsets[B]`` come out as ``LN(0)``."""
+    ``ln`` is ``(weight, bias, eps)``; rows follow ``order`` (the pack plan, with its identity
+    flag when it has one) and rows past ``csr_offsets[B]`` come out as ``LN(0)``."""
     dev = nat.require_gpu(neuron_emb, time_emb, value_emb, neuron_ids, time_bins, values, order, err,
                           what="tokenize_ln")
     for t in (neuron_emb, time_emb, value_emb):
@@ -121,7 +128,8 @@ def tokenize_ln(neuron_emb, time_emb, value_emb, neuron_ids, time_bins, values, 
              nat.ptr(time_emb), time_emb.shape[0], time_emb.stride(0), nat.ptr(value_emb), value_emb.shape[0],
              value_emb.stride(0), nat.ptr(neuron_ids), neuron_ids.stride(0) if E else 1, nat.ptr(time_bins),
              time_bins.stride(0) if E else 1, nat.ptr(values), values.stride(0) if E else 1, E, nat.ptr(order),
-             _end_ptr(csr_offsets), nat.ptr(g), nat.ptr(b), float(eps), nat.ptr(out), out.stride(0),
+             nat.ptr(identity), _end_ptr(csr_offsets), nat.ptr(g), nat.ptr(b), float(eps), nat.ptr(out),
+             out.stride(0),
              nat.ptr(err), nat.stream_of(dev))
     return out
 

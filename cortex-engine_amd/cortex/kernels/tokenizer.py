@@ -91,14 +91,16 @@ def tokenize_and_pack(neuron_emb, time_emb, value_emb, neuron_ids, time_bins, va
     E = neuron_ids.shape[0]
     if batch_size is None:
         batch_size = int(batch_indices.max().item()) + 1 if E > 0 else 1
-    offsets, order, _ = ops.pack_plan(batch_indices, batch_size, err=err, with_rank=False)
+    # sorted batch indices (the collate order): the plan only flags the identity, no order array
+    offsets, order, _, ident = ops.pack_plan(batch_indices, batch_size, err=err, with_rank=False, identity=True)
     if layout == "csr":
         tok = ops.tokenize(neuron_emb, time_emb, value_emb, neuron_ids, time_bins, values, order=order,
-                           csr_offsets=offsets, err=err)
+                           csr_offsets=offsets, err=err, identity=ident)
         return tok, offsets
     if layout == "padded":
         if max_events is None:
             max_events = int((offsets[1:] - offsets[:-1]).max().item()) if E > 0 else 0
         return ops.tokenize(neuron_emb, time_emb, value_emb, neuron_ids, time_bins, values, order=order,
-                            offsets=offsets, batch_size=batch_size, max_events=max_events, err=err)
+                            offsets=offsets, batch_size=batch_size, max_events=max_events, err=err,
+                            identity=ident)
     raise ValueError(f"layout must be 'csr' or 'padded', got {layout!r}")

@@ -173,9 +173,10 @@ class CortexModel(nn.Module):
         if batch_size is None:
             batch_size = int(batch_indices.max().item()) + 1 if E > 0 else 1
         err_flag = _checked_flag(err_flag, check_indices, neuron_ids.device)
-        offsets, order, _ = ops.pack_plan(batch_indices, int(batch_size), err=err_flag, with_rank=False)
+        offsets, order, _, ident = ops.pack_plan(batch_indices, int(batch_size), err=err_flag, with_rank=False,
+                                                 identity=True)
         out = self._forward_planned(neuron_ids, time_bins, values, offsets, order, int(batch_size), err_flag,
-                                    aux=return_aux)
+                                    aux=return_aux, identity=ident)
         if check_indices:
             _raise_on_flag(err_flag)
         return out
@@ -202,11 +203,12 @@ class CortexModel(nn.Module):
         return out
 
     def _forward_planned(self, neuron_ids, time_bins, values, offsets, order, B: int, err_flag,
-                         aux: bool = False) -> dict[str, torch.Tensor]:
+                         aux: bool = False, identity: torch.Tensor | None = None) -> dict[str, torch.Tensor]:
         """The forward from a CSR plan: row r of the packed events is event ``order[r]``
-        (``r`` itself when ``order`` is None); rows past ``offsets[B]`` are ignored."""
+        (``r`` itself when ``order`` is None or the plan's ``identity`` flag is set); rows past
+        ``offsets[B]`` are ignored."""
         enc = self.encoder
-        tokens = self._token_rows(neuron_ids, time_bins, values, offsets, order, err_flag)
+        tokens = self._token_rows(neuron_ids, time_bins, values, offsets, order, err_flag, identity)
         x, xn = self._cross_rows(tokens, offsets, B)
         x = self._encode(x, B, xn)
         out = {"behavior": self.behavior_head.forward_rows(x, B, pre_norm=enc.final_norm)}
@@ -214,7 +216,8 @@ class CortexModel(nn.Module):
             out["masked_spike_logits"] = self.masked_spike_head.forward_rows(x, B, pre_norm=enc.final_norm)
         return out
 
-    def _token_rows(self, neuron_ids, time_bins, values, offsets, order, err_flag) -> tuple[torch.Tensor, bool]:
+    def _token_rows(self, neuron_ids, time_bins, values, offsets, order, err_flag,
+                    identity: torch.Tensor | None = None) -> tuple[torch.Tensor, bool]:
         """The event rows in CSR order: ``(norm_kv(tokens) as bf16 rows, True)`` in one pass over the
         tables when the fused tokenizer + LayerNorm applies (the fp32 tokens are never stored),
         else ``(tokens, False)``."""
@@ -224,9 +227,9 @@ class CortexModel(nn.Module):
         if (cfg.compute_dtype == torch.bfloat16 and not xa.kv_proj._forward_pre_hooks
                 and fused_tokens_ok(tables, xa.norm_kv)):
             return ops.tokenize_ln(*tables, neuron_ids, time_bins, values, ln_params(xa.norm_kv), order=order,
-                                   csr_offsets=offsets, err=err_flag), True
+                                   csr_offsets=offsets, err=err_flag, identity=identity), True
         return ops.tokenize(*tables, neuron_ids, time_bins, values, order=order, csr_offsets=offsets,
-                            err=err_flag), False
+                            err=err_flag, identity=identity), False
 
     def _cross_rows(self, tokens: tuple[torch.Tensor, bool], offsets: torch.Tensor, B: int):
         """Cross-attention of the latents into each sample's CSR event rows: ``kv_proj`` on the real

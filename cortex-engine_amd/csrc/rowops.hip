@@ -34,6 +34,7 @@ struct TokLnArgs {
   int64_t s_val;
   int64_t E;
   const int64_t* order;
+  const int32_t* ident;  // nullable: *ident != 0 means the plan is the identity (order unused)
   const int64_t* csr_end;
   const float* gamma;
   const float* beta;
@@ -239,11 +240,12 @@ __global__ __launch_bounds__(256) void tokenize_ln_kernel(TokLnArgs a) {
   if (r0 >= a.E) return;
   const WtOut store(a.out, a.E * a.ld_out * 2, wt_fits(a.E * K * 2));
   const int64_t end = a.csr_end ? *a.csr_end : a.E;
+  const bool identity = !a.order || (a.ident && *a.ident);  // sorted events: row r is event r
   int64_t e[R];
 #pragma unroll
   for (int i = 0; i < R; ++i) {
     const int64_t r = r0 + i;
-    e[i] = r < a.E ? (a.order ? a.order[r] : r) : -1;
+    e[i] = r < a.E ? (identity ? r : a.order[r]) : -1;
   }
   float4 gm[EPL / 4], bt[EPL / 4];
 #pragma unroll
@@ -303,14 +305,14 @@ __global__ __launch_bounds__(256) void tokenize_ln_kernel(TokLnArgs a) {
     float sum = 0.0f;
 #pragma unroll
     for (int j = 0; j < EPL; ++j) sum += v[i][j];
-    const float mean = wave_sum(sum) * inv_k;
+    const float mean = wave_sum_dpp(sum) * inv_k;
     float ss = 0.0f;
 #pragma unroll
     for (int j = 0; j < EPL; ++j) {
       const float d = v[i][j] - mean;
       ss += d * d;
     }
-    const float rstd = 1.0f / sqrtf(wave_sum(ss) * inv_k + a.eps);
+    const float rstd = 1.0f / sqrtf(wave_sum_dpp(ss) * inv_k + a.eps);
     bf16* out = reinterpret_cast<bf16*>(a.out) + (r0 + i) * a.ld_out;
 #pragma unroll
     for (int j = 0; j < EPL; j += 4) {
@@ -393,9 +395,9 @@ int cortex_ln_rows(int64_t M, int64_t K, const float* x, int64_t ld_x, const flo
 int cortex_tokenize_ln(int64_t D, const float* neuron_emb, int64_t n_neuron, int64_t ld_neuron, const float* time_emb,
                        int64_t n_time, int64_t ld_time, const float* value_emb, int64_t n_value, int64_t ld_value,
                        const int64_t* neuron_ids, int64_t s_nid, const int64_t* time_bins, int64_t s_tb,
-                       const int64_t* values, int64_t s_val, int64_t E, const int64_t* order, const int64_t* csr_end,
-                       const float* gamma, const float* beta, float eps, void* out_bf16, int64_t ld_out,
-                       int32_t* err_flag, hipStream_t stream) {
+                       const int64_t* values, int64_t s_val, int64_t E, const int64_t* order, const int32_t* identity,
+                       const int64_t* csr_end, const float* gamma, const float* beta, float eps, void* out_bf16,
+                       int64_t ld_out, int32_t* err_flag, hipStream_t stream) {
   CORTEX_CHECK_ARG(E >= 0, "cortex_tokenize_ln: negative E");
   if (E == 0) return OK;
   CORTEX_CHECK_ARG(D == 256 || D == 512 || D == 768 || D == 1024, "cortex_tokenize_ln: D=%lld not in {256, 512, 768, 1024}",
@@ -411,7 +413,7 @@ int cortex_tokenize_ln(int64_t D, const float* neuron_emb, int64_t n_neuron, int
                    "cortex_tokenize_ln: tables, gamma, beta need 16-byte aligned rows and out 8-byte aligned rows");
   CORTEX_CHECK_ARG(cdiv(E, 4 * TL_ROWS) <= 0x7fffffffLL, "cortex_tokenize_ln: E too large");
   TokLnArgs a = {neuron_emb, n_neuron, ld_neuron, time_emb, n_time, ld_time, value_emb, n_value, ld_value,
-                 neuron_ids, s_nid, time_bins, s_tb, values, s_val, E, order, csr_end, gamma, beta, eps,
+                 neuron_ids, s_nid, time_bins, s_tb, values, s_val, E, order, identity, csr_end, gamma, beta, eps,
                  out_bf16, ld_out, err_flag};
   const dim3 grid((unsigned)cdiv(E, 4 * TL_ROWS));
   switch (D) {

@@ -14,6 +14,7 @@
 //     padded (B, E_max) layout with its bool mask (cortex.py:146-147,163-164).
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <mutex>
 
 #include "common.h"
@@ -59,8 +60,12 @@ __host__ __device__ inline int sample_bits(int B) {
   return bits;
 }
 
-// Small fill (kept as a kernel so that callers may capture it in a graph).
+// Small fills (kept as kernels so that callers may capture them in a graph).
 __global__ void fill_i64_kernel(int64_t* p, int64_t n, int64_t v) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = v;
+}
+__global__ void fill_i32_kernel(int32_t* p, int64_t n, int32_t v) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i < n) p[i] = v;
 }
@@ -100,7 +105,7 @@ __global__ __launch_bounds__(256) void pack_count_kernel(const int64_t* __restri
 
 // 2) exclusive scan over chunks per sample (in place), then over samples.
 __global__ __launch_bounds__(1024) void pack_scan_kernel(int* __restrict__ counts, int nchunks, int B,
-                                                          int64_t* __restrict__ offsets) {
+                                                          int64_t* __restrict__ offsets, int32_t* __restrict__ ident) {
   __shared__ int64_t part[1024];
   __shared__ int totals[PACK_MAX_B];
   const int tid = threadIdx.x;
@@ -134,6 +139,7 @@ __global__ __launch_bounds__(1024) void pack_scan_kernel(int* __restrict__ count
     run += totals[b];
   }
   if (tid == blockDim.x - 1) offsets[B] = part[tid];
+  if (ident && tid == 0) *ident = 0;  // this plan always writes `order`
 }
 
 // 3) in-order ranking inside each chunk: one wavefront walks its chunk 64 events
@@ -178,7 +184,9 @@ __global__ __launch_bounds__(64) void pack_rank_kernel(const int64_t* __restrict
 // owning the contiguous event chunk w.  Per-wave histograms in LDS, the two scans
 // (over waves per sample, then over samples), then the same in-order ranking as
 // pack_rank_kernel.  Same results as the three-launch path, a third of its launches.
-// Without ranks, sorted indices are recognised first and take the identity plan.
+// Without ranks, sorted indices are recognised first and take the identity plan.  When the
+// caller asks for an identity flag, a sorted plan sets it and leaves `order` unwritten (a
+// consumer then maps row r to event r); an unsorted one clears it and writes `order`.
 constexpr int PS_WAVES = 16;
 constexpr int PS_MAX_B = 1024;
 constexpr int64_t PS_MAX_E = 65536;
@@ -195,7 +203,7 @@ __device__ __forceinline__ bool sorted_event(int64_t e, int64_t b, int64_t bp, i
                                              int64_t* __restrict__ offsets, int64_t* __restrict__ order,
                                              int64_t* __restrict__ dst_rows) {
   if (b < 0 || b >= B || bp > b || (e > 0 && bp < 0)) return false;
-  order[e] = e;
+  if (order) order[e] = e;
   if (dst_rows) dst_rows[e] = e;
   for (int64_t s = bp + 1; s <= b; ++s) offsets[s] = e;
   if (e == E - 1)
@@ -203,33 +211,40 @@ __device__ __forceinline__ bool sorted_event(int64_t e, int64_t b, int64_t bp, i
   return true;
 }
 
+// The batch index of the event before this lane's: the previous lane's value (lane 0 loads
+// its own).  `b` is this lane's index, `e` its event; only lanes with 0 < e < E use the result,
+// and lane 0 loads only then (every lane takes part in the shuffle).
+__device__ __forceinline__ int64_t prev_index(int64_t b, int64_t e, int64_t E, const int64_t* __restrict__ bidx,
+                                              int64_t s_bidx, int lane) {
+  const int64_t up = __shfl_up(b, 1, 64);
+  if (lane != 0) return up;
+  return (e > 0 && e < E) ? bidx[(e - 1) * s_bidx] : -1;
+}
+
 // Above PS_ONE_E events the sorted check runs wide first: one workgroup per PS_SORTED_EV
-// events applies sorted_event to its range and records in status[blockIdx.x] whether the
-// range (with the event before it) was sorted and in range: 1 yes, 2 no.  pack_small_kernel
-// then returns at once when every status is 1 and otherwise recomputes the whole plan.  Up
-// to PS_ONE_E events pack_small_kernel makes the check itself (one round of loads per
-// thread), so a plan is one launch.
-constexpr int PS_SORTED_EV = 1024;
-constexpr int PS_ONE_UNROLL = 8;
+// events (one per thread) applies sorted_event to its range and records in
+// status[blockIdx.x] whether the range (with the event before it) was sorted and in range: 1
+// yes, 2 no.  pack_small_kernel then returns at once when every status is 1 and otherwise
+// recomputes the whole plan.  Up to PS_ONE_E events pack_small_kernel makes the check itself
+// (one round of loads per thread), so a plan is one launch; above that one workgroup is
+// latency-bound (9.5 us at 16384 events against about 2 + 1.5 us for the wide check and the
+// status read).
+constexpr int PS_SORTED_EV = 256;
+constexpr int PS_ONE_UNROLL = 4;
 constexpr int64_t PS_ONE_E = 64 * PS_WAVES * PS_ONE_UNROLL;
 
-__global__ __launch_bounds__(256) void pack_sorted_kernel(const int64_t* __restrict__ bidx, int64_t s_bidx,
-                                                          int64_t E, int B, int64_t* __restrict__ offsets,
-                                                          int64_t* __restrict__ order, int64_t* __restrict__ dst_rows,
-                                                          int* __restrict__ status) {
+__global__ __launch_bounds__(PS_SORTED_EV) void pack_sorted_kernel(const int64_t* __restrict__ bidx, int64_t s_bidx,
+                                                                   int64_t E, int B, int64_t* __restrict__ offsets,
+                                                                   int64_t* __restrict__ order,
+                                                                   int64_t* __restrict__ dst_rows,
+                                                                   int* __restrict__ status) {
   __shared__ int bad;
   if (threadIdx.x == 0) bad = 0;
   __syncthreads();
-  const int64_t c0 = (int64_t)blockIdx.x * PS_SORTED_EV;
-  bool my_bad = false;
-  for (int k = threadIdx.x; k < PS_SORTED_EV; k += blockDim.x) {
-    const int64_t e = c0 + k;
-    if (e >= E) break;
-    const int64_t b = bidx[e * s_bidx];
-    const int64_t bp = e > 0 ? bidx[(e - 1) * s_bidx] : -1;
-    if (!sorted_event(e, b, bp, E, B, offsets, order, dst_rows)) my_bad = true;
-  }
-  if (my_bad) bad = 1;
+  const int64_t e = (int64_t)blockIdx.x * PS_SORTED_EV + threadIdx.x;
+  const int64_t b = e < E ? bidx[e * s_bidx] : 0;
+  const int64_t bp = prev_index(b, e, E, bidx, s_bidx, threadIdx.x & 63);
+  if (e < E && !sorted_event(e, b, bp, E, B, offsets, order, dst_rows)) bad = 1;
   __syncthreads();
   if (threadIdx.x == 0) status[blockIdx.x] = bad ? 2 : 1;
 }
@@ -239,7 +254,7 @@ __global__ __launch_bounds__(1024) void pack_small_kernel(const int64_t* __restr
                                                           int64_t* __restrict__ order, int64_t* __restrict__ dst_rows,
                                                           int64_t* __restrict__ rank, int32_t* __restrict__ err,
                                                           const int* __restrict__ status, int n_status,
-                                                          bool try_sorted) {
+                                                          bool try_sorted, int32_t* __restrict__ ident) {
   __shared__ int cnt[PS_WAVES * PS_MAX_B];  // per-wave counts, then per-wave next CSR row
   __shared__ int first[PS_MAX_B];           // CSR offset of each sample
   __shared__ int wsum[PS_WAVES];
@@ -251,30 +266,38 @@ __global__ __launch_bounds__(1024) void pack_small_kernel(const int64_t* __restr
     for (int i = tid; i < n_status; i += blockDim.x)
       if (status[i] != 1) unsorted = 1;
     __syncthreads();
-    if (!unsorted) return;
+    if (!unsorted) {
+      if (ident && tid == 0) *ident = 1;
+      return;
+    }
   } else if (try_sorted) {  // E <= PS_ONE_E: the sorted check here, every load issued first
     if (tid == 0) unsorted = 0;
     __syncthreads();
-    int64_t bv[PS_ONE_UNROLL], pv[PS_ONE_UNROLL];
+    int64_t bv[PS_ONE_UNROLL];
 #pragma unroll
     for (int u = 0; u < PS_ONE_UNROLL; ++u) {
       const int64_t e = (int64_t)u * blockDim.x + tid;
       bv[u] = e < E ? bidx[e * s_bidx] : 0;
-      pv[u] = (e < E && e > 0) ? bidx[(e - 1) * s_bidx] : -1;
     }
     bool my_bad = false;
+    int64_t* const ord = ident ? nullptr : order;  // with the flag, a sorted plan writes no order
 #pragma unroll
     for (int u = 0; u < PS_ONE_UNROLL; ++u) {
       const int64_t e = (int64_t)u * blockDim.x + tid;
-      if (e < E && !sorted_event(e, bv[u], pv[u], E, B, offsets, order, dst_rows)) my_bad = true;
+      const int64_t bp = prev_index(bv[u], e, E, bidx, s_bidx, lane);
+      if (e < E && !sorted_event(e, bv[u], bp, E, B, offsets, ord, dst_rows)) my_bad = true;
     }
     if (my_bad) unsorted = 1;
     // the identity writes complete before the full plan below rewrites every offset and
     // every CSR row of `order`
     __threadfence_block();
     __syncthreads();
-    if (!unsorted) return;
+    if (!unsorted) {
+      if (ident && tid == 0) *ident = 1;
+      return;
+    }
   }
+  if (ident && tid == 0) *ident = 0;
   for (int i = tid; i < PS_WAVES * B; i += blockDim.x) cnt[i] = 0;
   __syncthreads();
   const int64_t C = cdiv(E, (int64_t)PS_WAVES);
@@ -394,6 +417,7 @@ struct RowArgs {
   int64_t E;               // number of events
   int64_t D;
   const int64_t* order;    // CSR row -> source event (nullable: identity)
+  const int32_t* ident;    // nullable: when *ident != 0 the plan is the identity and order is unused
   const int64_t* offsets;  // padded mode: (B+1) CSR offsets
   const int64_t* csr_end;  // CSR mode (nullable): number of valid CSR rows (offsets[B])
   int64_t B, E_max;        // padded mode
@@ -417,11 +441,13 @@ __global__ __launch_bounds__(256) void row_writer_kernel(RowArgs a) {
   if (PADDED) {
     const int64_t b = r / a.E_max, j = r - b * a.E_max;
     const int64_t o0 = a.offsets[b], cnt = a.offsets[b + 1] - o0;
-    e = (j < cnt) ? (a.order ? a.order[o0 + j] : o0 + j) : -1;
+    const bool identity = !a.order || (a.ident && *a.ident);
+    e = (j < cnt) ? (identity ? o0 + j : a.order[o0 + j]) : -1;
     if (a.mask && lane == 0) a.mask[r] = (j < cnt) ? 1 : 0;
   } else {
     // rows past offsets[B] exist only when some batch indices were invalid: zero them
-    e = (a.csr_end && r >= *a.csr_end) ? -1 : (a.order ? a.order[r] : r);
+    const bool identity = !a.order || (a.ident && *a.ident);
+    e = (a.csr_end && r >= *a.csr_end) ? -1 : (identity ? r : a.order[r]);
   }
   if (e >= a.E) e = -1;  // defensive: never follow a corrupt order entry
   T* out = reinterpret_cast<T*>(a.out) + r * a.out_ld;
@@ -480,6 +506,67 @@ __global__ __launch_bounds__(256) void row_writer_kernel(RowArgs a) {
   }
 }
 
+// Tokens in CSR order from the tables (the API tokenizer's main case), TOK_ROWS rows per
+// wavefront.  A row is a chain of dependent loads (order -> the three indices -> the three
+// table rows), so every load of one link is issued for all rows before any is waited on; with
+// the plan's identity flag set (sorted batch indices) the first link is r itself.  Rows past
+// *csr_end and rows with an index outside its table are zero (the latter set the error bit).
+// 16-byte aligned rows, D a multiple of the 16-byte vector.
+constexpr int TOK_ROWS = 4;
+
+template <class T>
+__global__ __launch_bounds__(256) void tokenize_csr_kernel(RowArgs a) {
+  constexpr int R = TOK_ROWS;
+  using V = Vec16<T>;
+  constexpr int NV = V::N;
+  const int lane = threadIdx.x & 63;
+  const int64_t r0 = ((int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6)) * R;
+  if (r0 >= a.E) return;
+  const bool identity = !a.order || (a.ident && *a.ident);
+  const int64_t end = a.csr_end ? *a.csr_end : a.E;
+  int64_t e[R];
+#pragma unroll
+  for (int i = 0; i < R; ++i) {
+    const int64_t r = r0 + i;
+    e[i] = (r < a.E && r < end) ? (identity ? r : a.order[r]) : -1;
+    if (e[i] >= a.E) e[i] = -1;  // defensive: never follow a corrupt order entry
+  }
+  int64_t id[R][3];
+#pragma unroll
+  for (int i = 0; i < R; ++i)
+#pragma unroll
+    for (int t = 0; t < 3; ++t) id[i][t] = e[i] >= 0 ? a.ids[t][e[i] * a.ids_stride[t]] : 0;
+  const T* src[R][3];
+#pragma unroll
+  for (int i = 0; i < R; ++i) {
+    if (e[i] >= 0 && (id[i][0] < 0 || id[i][0] >= a.tab_rows[0] || id[i][1] < 0 || id[i][1] >= a.tab_rows[1] ||
+                      id[i][2] < 0 || id[i][2] >= a.tab_rows[2])) {
+      if (lane == 0 && a.err) atomicOr(a.err, ERR_TOKEN_INDEX);
+      e[i] = -1;  // never read out of bounds: the row is written as zeros
+    }
+#pragma unroll
+    for (int t = 0; t < 3; ++t) src[i][t] = reinterpret_cast<const T*>(a.tab[t]) + (e[i] >= 0 ? id[i][t] : 0) * a.tab_ld[t];
+  }
+  const WtOut store(a.out, a.E * a.out_ld * (int64_t)sizeof(T), wt_fits(a.E * a.D * (int64_t)sizeof(T)));
+  for (int64_t d = (int64_t)lane * NV; d < a.D; d += 64 * NV) {
+    V x[R][3];
+#pragma unroll
+    for (int i = 0; i < R; ++i)
+#pragma unroll
+      for (int t = 0; t < 3; ++t)
+        if (e[i] >= 0) x[i][t] = *reinterpret_cast<const V*>(src[i][t] + d);
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+      if (r0 + i >= a.E) break;
+      V o;
+#pragma unroll
+      for (int q = 0; q < NV; ++q)
+        o.v[q] = e[i] >= 0 ? add_rn<T>(add_rn<T>(x[i][0].v[q], x[i][1].v[q]), x[i][2].v[q]) : from_f32<T>(0.0f);
+      store(reinterpret_cast<V*>(reinterpret_cast<T*>(a.out) + (r0 + i) * a.out_ld + d), o);
+    }
+  }
+}
+
 }  // namespace cortex
 
 using namespace cortex;
@@ -502,7 +589,10 @@ static int launch_rows(const RowArgs& a, bool padded, hipStream_t stream) {
   } else {
     vec = vec && ((uintptr_t)a.src % 16 == 0) && ((a.src_ld * (int64_t)sizeof(T)) % 16 == 0);
   }
-  if (padded) {
+  if (MODE == MODE_TABLE && !padded && vec) {
+    const dim3 g((unsigned)cdiv(cdiv(rows, TOK_ROWS), waves_per_block));
+    hipLaunchKernelGGL((tokenize_csr_kernel<T>), g, dim3(256), 0, stream, a);
+  } else if (padded) {
     if (vec)
       hipLaunchKernelGGL((row_writer_kernel<T, MODE, true, true>), grid, dim3(256), 0, stream, a);
     else
@@ -538,7 +628,9 @@ int64_t cortex_pack_workspace_bytes(int64_t E, int64_t B) {
   if (E <= 0 || B <= 0) return 0;
   const int64_t C = pack_chunk_size(E);
   const int64_t nchunks = cdiv(E, C);
-  return nchunks * B * (int64_t)sizeof(int);
+  // per-chunk counts (three-launch plan) or one status word per sorted-check workgroup
+  const int64_t words = std::max(nchunks * B, cdiv(E, (int64_t)PS_SORTED_EV));
+  return words * (int64_t)sizeof(int);
 }
 
 }  // extern "C"
@@ -549,7 +641,7 @@ int64_t cortex_pack_workspace_bytes(int64_t E, int64_t B) {
 // needs clearing between calls.
 static int pack_plan_impl(const char* who, const int64_t* batch_indices, int64_t s_bidx, int64_t E, int64_t B,
                           int64_t* offsets, int64_t* order, int64_t* dst_rows, int64_t* rank, void* workspace,
-                          int64_t workspace_bytes, int32_t* err_flag, hipStream_t stream) {
+                          int64_t workspace_bytes, int32_t* err_flag, int32_t* identity, hipStream_t stream) {
   CORTEX_CHECK_ARG(E >= 0 && B >= 1, "%s: need E >= 0 and B >= 1 (got E=%lld B=%lld)", who, (long long)E,
                    (long long)B);
   CORTEX_CHECK_ARG(B <= PACK_MAX_B, "%s: B=%lld exceeds the supported maximum %d", who, (long long)B, PACK_MAX_B);
@@ -558,6 +650,10 @@ static int pack_plan_impl(const char* who, const int64_t* batch_indices, int64_t
     hipLaunchKernelGGL(fill_i64_kernel, dim3((unsigned)cdiv(B + 1, 256)), dim3(256), 0, stream, offsets, B + 1,
                        (int64_t)0);
     CORTEX_CHECK_LAUNCH("cortex_pack_plan(E=0)");
+    if (identity) {  // the empty plan is the identity
+      hipLaunchKernelGGL(fill_i32_kernel, dim3(1), dim3(64), 0, stream, identity, (int64_t)1, 1);
+      CORTEX_CHECK_LAUNCH("cortex_pack_plan(E=0)");
+    }
     return OK;
   }
   CORTEX_CHECK_ARG(batch_indices && order, "%s: batch_indices and order must not be null", who);
@@ -576,12 +672,12 @@ static int pack_plan_impl(const char* who, const int64_t* batch_indices, int64_t
     const bool one = rank == nullptr && E <= PS_ONE_E;
     if (rank == nullptr && !one && workspace != nullptr && workspace_bytes >= n_status * (int64_t)sizeof(int)) {
       status = reinterpret_cast<int*>(workspace);
-      hipLaunchKernelGGL(pack_sorted_kernel, dim3((unsigned)n_status), dim3(256), 0, stream, batch_indices, s_bidx, E,
-                         (int)B, offsets, order, dst_rows, status);
+      hipLaunchKernelGGL(pack_sorted_kernel, dim3((unsigned)n_status), dim3(PS_SORTED_EV), 0, stream, batch_indices,
+                         s_bidx, E, (int)B, offsets, identity ? nullptr : order, dst_rows, status);
       CORTEX_CHECK_LAUNCH("pack_sorted_kernel");
     }
     hipLaunchKernelGGL(pack_small_kernel, dim3(1), dim3(64 * PS_WAVES), 0, stream, batch_indices, s_bidx, E, (int)B,
-                       offsets, order, dst_rows, rank, err_flag, status, n_status, one);
+                       offsets, order, dst_rows, rank, err_flag, status, n_status, one, identity);
     CORTEX_CHECK_LAUNCH("pack_small_kernel");
     return OK;
   }
@@ -591,7 +687,7 @@ static int pack_plan_impl(const char* who, const int64_t* batch_indices, int64_t
   hipLaunchKernelGGL(pack_count_kernel, dim3(nchunks), dim3(256), 0, stream, batch_indices, s_bidx, E, (int)B, C,
                      counts, err_flag);
   CORTEX_CHECK_LAUNCH("pack_count_kernel");
-  hipLaunchKernelGGL(pack_scan_kernel, dim3(1), dim3(1024), 0, stream, counts, nchunks, (int)B, offsets);
+  hipLaunchKernelGGL(pack_scan_kernel, dim3(1), dim3(1024), 0, stream, counts, nchunks, (int)B, offsets, identity);
   CORTEX_CHECK_LAUNCH("pack_scan_kernel");
   hipLaunchKernelGGL(pack_rank_kernel, dim3(nchunks), dim3(64), 0, stream, batch_indices, s_bidx, E, (int)B, C,
                      counts, offsets, order, dst_rows, rank);
@@ -643,9 +739,9 @@ extern "C" {
 
 int cortex_pack_plan(const int64_t* batch_indices, int64_t s_bidx, int64_t E, int64_t B, int64_t* offsets,
                      int64_t* order, int64_t* dst_rows, int64_t* rank, void* workspace, int64_t workspace_bytes,
-                     int32_t* err_flag, hipStream_t stream) {
+                     int32_t* err_flag, int32_t* identity, hipStream_t stream) {
   return pack_plan_impl("cortex_pack_plan", batch_indices, s_bidx, E, B, offsets, order, dst_rows, rank, workspace,
-                        workspace_bytes, err_flag, stream);
+                        workspace_bytes, err_flag, identity, stream);
 }
 
 int64_t cortex_pack_noalloc_max_workspace_bytes(void) { return PACK_SCRATCH_BYTES; }
@@ -670,7 +766,7 @@ int cortex_pack_plan_noalloc(const int64_t* batch_indices, int64_t s_bidx, int64
   const int rc = pack_scratch_ptr(dev, &ws);
   if (rc != OK) return rc;
   return pack_plan_impl("cortex_pack_plan_noalloc", batch_indices, s_bidx, E, B, offsets, order, dst_rows, rank, ws,
-                        PACK_SCRATCH_BYTES, err_flag, stream);
+                        PACK_SCRATCH_BYTES, err_flag, nullptr, stream);
 }
 
 int cortex_tokenize(int dtype, int64_t D, const void* neuron_emb, int64_t n_neuron, int64_t ld_neuron,
@@ -678,7 +774,7 @@ int cortex_tokenize(int dtype, int64_t D, const void* neuron_emb, int64_t n_neur
                     int64_t ld_value, const int64_t* neuron_ids, int64_t s_nid, const int64_t* time_bins,
                     int64_t s_tb, const int64_t* values, int64_t s_val, int64_t E, const int64_t* order,
                     const int64_t* csr_end, const int64_t* offsets, int64_t B, int64_t E_max, void* out,
-                    int64_t ld_out, uint8_t* mask, int32_t* err_flag, hipStream_t stream) {
+                    int64_t ld_out, uint8_t* mask, const int32_t* identity, int32_t* err_flag, hipStream_t stream) {
   CORTEX_CHECK_ARG(D > 0 && E >= 0, "cortex_tokenize: need D > 0 and E >= 0");
   CORTEX_CHECK_ARG(neuron_emb && time_emb && value_emb, "cortex_tokenize: null embedding table");
   CORTEX_CHECK_ARG(E == 0 || (neuron_ids && time_bins && values), "cortex_tokenize: null index array");
@@ -704,6 +800,7 @@ int cortex_tokenize(int dtype, int64_t D, const void* neuron_emb, int64_t n_neur
   a.E = E;
   a.D = D;
   a.order = order;
+  a.ident = identity;
   a.csr_end = csr_end;
   a.offsets = offsets;
   a.B = B;

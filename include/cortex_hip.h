@@ -41,14 +41,19 @@ const char* cortex_last_error(void);
  *   order    (E)    source event of every CSR row (stable in event order)
  *   dst_rows (E)    CSR row of every event (nullable)
  *   rank     (E)    position of every event inside its sample (nullable)
+ *   identity (1)    int32 (nullable): when given, a plan of sorted batch indices sets it
+ *                   to 1 and leaves `order` unwritten (row r is event r); any other plan
+ *                   sets it to 0 and writes `order`.  Consumers take the flag beside
+ *                   `order` (cortex_tokenize, cortex_tokenize_ln).
  * workspace: at least cortex_pack_workspace_bytes(E, B) bytes of device memory.
  * Sorted batch indices (the collate order) are recognised on the device when rank is
- * null: the identity plan is written by one launch over all events and the general plan
- * runs only where some 1024-event range was not sorted or held an index out of range. */
+ * null: up to 4096 events the check and the plan are one launch; above, the identity
+ * plan is written by one launch over all events and the general plan runs only where
+ * some 256-event range was not sorted or held an index out of range. */
 int64_t cortex_pack_workspace_bytes(int64_t E, int64_t B);
 int cortex_pack_plan(const int64_t* batch_indices, int64_t s_bidx, int64_t E, int64_t B, int64_t* offsets,
                      int64_t* order, int64_t* dst_rows, int64_t* rank, void* workspace, int64_t workspace_bytes,
-                     int32_t* err_flag, hipStream_t stream);
+                     int32_t* err_flag, int32_t* identity, hipStream_t stream);
 
 /* cortex_pack_plan without a workspace argument and without any allocation.  No
  * counterpart in the reference: it is for callers that cannot allocate device memory
@@ -57,7 +62,7 @@ int cortex_pack_plan(const int64_t* batch_indices, int64_t s_bidx, int64_t E, in
  * (4 MiB) per GPU, held until the process ends; sizes with
  * cortex_pack_workspace_bytes(E, B) above it return -4 before any launch.  Every call on
  * one GPU uses that GPU's one array: calls that overlap on a GPU (concurrent streams)
- * race.  Outputs and semantics equal cortex_pack_plan's. */
+ * race.  Outputs and semantics equal cortex_pack_plan's with identity == NULL. */
 int64_t cortex_pack_noalloc_max_workspace_bytes(void);
 int cortex_pack_plan_noalloc(const int64_t* batch_indices, int64_t s_bidx, int64_t E, int64_t B, int64_t* offsets,
                              int64_t* order, int64_t* dst_rows, int64_t* rank, int32_t* err_flag,
@@ -75,29 +80,32 @@ int cortex_pack_plan_noalloc(const int64_t* batch_indices, int64_t s_bidx, int64
  *                              batch index never leave an unwritten order entry), or
  *   - order[offsets[b] + j]    for padded row r = b*E_max + j when offsets != NULL;
  *     rows j >= count_b are zero and mask[r] = (j < count_b), as the padded
- *     output of _pack_events (cortex/models/cortex.py:146-147,163-164). */
+ *     output of _pack_events (cortex/models/cortex.py:146-147,163-164).
+ * identity (nullable): the plan's flag; when *identity != 0, order is not read and
+ * order[x] is taken as x. */
 int cortex_tokenize(int dtype, int64_t D, const void* neuron_emb, int64_t n_neuron, int64_t ld_neuron,
                     const void* time_emb, int64_t n_time, int64_t ld_time, const void* value_emb, int64_t n_value,
                     int64_t ld_value, const int64_t* neuron_ids, int64_t s_nid, const int64_t* time_bins,
                     int64_t s_tb, const int64_t* values, int64_t s_val, int64_t E, const int64_t* order,
                     const int64_t* csr_end, const int64_t* offsets, int64_t B, int64_t E_max, void* out,
-                    int64_t ld_out, uint8_t* mask, int32_t* err_flag, hipStream_t stream);
+                    int64_t ld_out, uint8_t* mask, const int32_t* identity, int32_t* err_flag,
+                    hipStream_t stream);
 
 /* ---- a1 + a3: tokens straight to the kv-projection operand -------------------
  * Replaces SpikeTokenizer.forward (cortex/models/tokenizer.py:90-93) followed by
  * CrossAttentionBlock.norm_kv (cortex/models/perceiver.py:67) in the model forward,
  * without storing the fp32 tokens:
  *   row r = LN((neuron_emb[nid[e]] + time_emb[tb[e]]) + value_emb[val[e]]) in bf16,
- *   e = order[r] (order NULL: e = r), the sum in fp32 left to right, LN with
+ *   e = order[r] (order NULL or *identity != 0: e = r), the sum in fp32 left to right, LN with
  *   gamma/beta/eps.  Rows r >= *csr_end (when csr_end is given) and rows with an index
  *   outside its table take x = 0 (LN gives beta); the latter OR 1 into err_flag.
  * fp32 tables, gamma, beta with 16-byte aligned rows; D in {256, 512, 768, 1024}. */
 int cortex_tokenize_ln(int64_t D, const float* neuron_emb, int64_t n_neuron, int64_t ld_neuron, const float* time_emb,
                        int64_t n_time, int64_t ld_time, const float* value_emb, int64_t n_value, int64_t ld_value,
                        const int64_t* neuron_ids, int64_t s_nid, const int64_t* time_bins, int64_t s_tb,
-                       const int64_t* values, int64_t s_val, int64_t E, const int64_t* order, const int64_t* csr_end,
-                       const float* gamma, const float* beta, float eps, void* out_bf16, int64_t ld_out,
-                       int32_t* err_flag, hipStream_t stream);
+                       const int64_t* values, int64_t s_val, int64_t E, const int64_t* order, const int32_t* identity,
+                       const int64_t* csr_end, const float* gamma, const float* beta, float eps, void* out_bf16,
+                       int64_t ld_out, int32_t* err_flag, hipStream_t stream);
 
 /* ---- a2: pack existing token rows ------------------------------------------
  * Replaces the gather/scatter of _pack_events (cortex/models/cortex.py:150-164)

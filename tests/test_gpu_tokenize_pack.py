@@ -238,24 +238,33 @@ def _sorted_cases():
     b = np.sort(rng.integers(0, 6, 2500))
     b[1024] = -7  # first event of the second range
     cases["negative_at_range_start"] = (b, 6)
-    # above 8192 events the check runs wide (a workgroup per 1024 events) before the plan kernel
-    b = np.sort(rng.integers(0, 21, 12000))
+    b = np.sort(rng.integers(0, 21, 4000))
+    b[2047], b[2048] = b[2048], b[2047] - 1 if b[2047] > 0 else 1
+    cases["inversion_4000"] = (b, 21)
+    # above 4096 events the check runs wide (a workgroup per 256 events) before the plan kernel
+    b = np.sort(rng.integers(0, 21, 20000))
     b[5119], b[5120] = b[5120], b[5119] - 1 if b[5119] > 0 else 1
     cases["inversion_wide"] = (b, 21)
-    b = np.sort(rng.integers(0, 30, 9000))
-    b[8999] = 30
+    b = np.sort(rng.integers(0, 33, 20000))
+    b[256], b[255] = b[255], b[256] + 1  # an inversion across a 256-event range edge
+    cases["inversion_wide_range_edge"] = (b, 34)
+    b = np.sort(rng.integers(0, 30, 17000))
+    b[16999] = 30
     cases["out_of_range_tail_wide"] = (b, 30)
-    cases["sorted_8192"] = (np.sort(rng.integers(0, 33, 8192)), 33)
-    cases["sorted_8193"] = (np.sort(rng.integers(0, 33, 8193)), 40)
+    cases["sorted_4096"] = (np.sort(rng.integers(0, 33, 4096)), 33)
+    cases["sorted_4097"] = (np.sort(rng.integers(0, 33, 4097)), 40)
+    cases["sorted_16447"] = (np.sort(rng.integers(0, 33, 16447)), 33)  # partial last wave of the wide check
     return cases
 
 
 @pytest.mark.parametrize("name", list(_sorted_cases()))
 def test_pack_plan_sorted_fast_path(name):
-    """Sorted batch indices take the identity plan (checked inside the plan kernel up to 8192
+    """Sorted batch indices take the identity plan (checked inside the plan kernel up to 4096
     events, by the wide pack_sorted_kernel above); anything else found
     there -- an inversion, an index out of range -- falls back to the full plan.  Same
-    results as the oracle either way, with and without ranks."""
+    results as the oracle either way, with and without ranks; with the identity flag, a
+    sorted in-range plan sets it (order is then the identity by definition) and any other
+    clears it and writes order."""
     from cortex.kernels import ops
 
     bidx, B = _sorted_cases()[name]
@@ -272,3 +281,12 @@ def test_pack_plan_sorted_fast_path(name):
         np.testing.assert_array_equal(order.cpu().numpy()[:n], np.flatnonzero(valid)[p.order])
         if with_rank:
             np.testing.assert_array_equal(rank.cpu().numpy()[valid], p.rank)
+    err = torch.zeros(1, dtype=torch.int32, device=DEV)
+    off, order, _, ident = ops.pack_plan(t, B, err=err, with_rank=False, identity=True)
+    torch.cuda.synchronize()
+    sorted_ok = bool(valid.all() and (np.diff(bidx) >= 0).all())
+    assert int(ident.item()) == int(sorted_ok)
+    np.testing.assert_array_equal(off.cpu().numpy(), p.offsets)
+    if not sorted_ok:
+        n = int(p.offsets[-1])
+        np.testing.assert_array_equal(order.cpu().numpy()[:n], np.flatnonzero(valid)[p.order])
