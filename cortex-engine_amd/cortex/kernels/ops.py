@@ -51,7 +51,7 @@ def _row_major_2d(x: torch.Tensor) -> torch.Tensor:
 
 
 def pack_plan(batch_indices: torch.Tensor, batch_size: int, err: torch.Tensor | None = None, *,
-              with_rank: bool = True, identity: bool = False):
+              with_rank: bool = True, identity: bool = False, clear_err: bool = False):
     """Stable CSR plan of ragged events: ``(offsets (B+1), order (E), rank (E))``.
 
     offsets/order/rank are int64 device tensors; see ``cortex_pack_plan``.  With
@@ -59,6 +59,7 @@ def pack_plan(batch_indices: torch.Tensor, batch_size: int, err: torch.Tensor | 
     With ``identity=True`` a fourth value is returned, the plan's int32 identity flag: a
     plan of sorted indices sets it and leaves ``order`` unwritten, so ``order`` may only be
     handed on together with the flag (``tokenize`` / ``tokenize_ln`` take both).
+    ``clear_err=True`` zeroes ``err`` inside the plan's first launch before anything ORs into it.
     """
     dev = nat.require_gpu(batch_indices, what="pack_plan")
     if batch_indices.dtype != torch.int64 or batch_indices.dim() != 1:
@@ -73,7 +74,7 @@ def pack_plan(batch_indices: torch.Tensor, batch_size: int, err: torch.Tensor | 
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
     nat.call("cortex_pack_plan", nat.ptr(batch_indices), batch_indices.stride(0) if E else 1, E, B,
              nat.ptr(offsets), nat.ptr(order), None, nat.ptr(rank), nat.ptr(ws), ws_bytes, nat.ptr(err),
-             nat.ptr(ident), nat.stream_of(dev))
+             nat.ptr(ident), 1 if clear_err else 0, nat.stream_of(dev))
     return (offsets, order, rank, ident) if identity else (offsets, order, rank)
 
 

@@ -152,7 +152,8 @@ class CortexModel(nn.Module):
 
     def forward(self, neuron_ids: torch.Tensor, time_bins: torch.Tensor, values: torch.Tensor,
                 batch_indices: torch.Tensor, return_aux: bool = False, *, batch_size: int | None = None,
-                err_flag: torch.Tensor | None = None, check_indices: bool = False) -> dict[str, torch.Tensor]:
+                err_flag: torch.Tensor | None = None, check_indices: bool = False,
+                clear_err: bool = False) -> dict[str, torch.Tensor]:
         """Spike events -> ``{"behavior": (B, behavior_dim)}``, plus ``"masked_spike_logits"``
         (B, spike_value_buckets) when ``return_aux`` is set and the model has that head.
 
@@ -162,7 +163,8 @@ class CortexModel(nn.Module):
         zero token row and a batch index outside [0, B) drops the event, flagged in
         ``err_flag`` only; ``check_indices=True`` reads the flag back after the forward
         (one synchronisation) and raises ``IndexError`` as the eager embedding lookup
-        of the reference does (cortex/models/tokenizer.py:90-93).
+        of the reference does (cortex/models/tokenizer.py:90-93).  ``clear_err=True`` zeroes
+        ``err_flag`` first, inside the pack plan's first launch.
         """
         if not (neuron_ids.shape == time_bins.shape == values.shape == batch_indices.shape):
             raise ValueError(
@@ -172,9 +174,10 @@ class CortexModel(nn.Module):
         E = neuron_ids.shape[0]
         if batch_size is None:
             batch_size = int(batch_indices.max().item()) + 1 if E > 0 else 1
-        err_flag = _checked_flag(err_flag, check_indices, neuron_ids.device)
+        if check_indices and err_flag is None:
+            err_flag = torch.empty(1, dtype=torch.int32, device=neuron_ids.device)
         offsets, order, _, ident = ops.pack_plan(batch_indices, int(batch_size), err=err_flag, with_rank=False,
-                                                 identity=True)
+                                                 identity=True, clear_err=clear_err or check_indices)
         out = self._forward_planned(neuron_ids, time_bins, values, offsets, order, int(batch_size), err_flag,
                                     aux=return_aux, identity=ident)
         if check_indices:

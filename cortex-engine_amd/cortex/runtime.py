@@ -25,7 +25,7 @@ class CapturedForward:
     memory, ...) before ``cap()`` serves the next request.
 
     The returned tensor is the graph's static output (clone it to keep it past the next call).
-    ``err_flag`` is cleared at the start of every replay (a fill kernel inside the graph), so
+    ``err_flag`` is cleared at the start of every replay (by the pack plan's first kernel), so
     after a call it holds that call's index-range violations only; with
     ``check_indices=True`` each call reads it back (one synchronisation) and raises
     ``IndexError`` as ``CortexModel.forward`` does.
@@ -67,9 +67,9 @@ class CapturedForward:
             self.output = self._run()
 
     def _run(self) -> torch.Tensor:
-        self.err_flag.zero_()  # a fill kernel (captured: no memset node in the graph)
+        # the pack plan zeroes the flag in its first launch (no fill kernel, no memset node)
         return self.model(self.neuron_ids, self.time_bins, self.values, self.batch_indices,
-                          batch_size=self.batch_size, err_flag=self.err_flag)["behavior"]
+                          batch_size=self.batch_size, err_flag=self.err_flag, clear_err=True)["behavior"]
 
     def __call__(self, *events: torch.Tensor) -> torch.Tensor:
         """Replay on the static buffers; with four tensors, copy them in first."""

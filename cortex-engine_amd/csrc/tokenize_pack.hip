@@ -24,6 +24,7 @@ namespace cortex {
 // Error-flag bits (device int32, OR-ed).
 constexpr int ERR_TOKEN_INDEX = 1;  // neuron/time/value index outside its table
 constexpr int ERR_BATCH_INDEX = 2;  // batch index outside [0, B)
+constexpr int PACK_FLAG_CLEAR_ERR = 1;  // cortex_pack_plan flags: zero err_flag before the plan
 
 constexpr int PACK_MAX_B = 8192;   // LDS histogram bins per chunk
 constexpr int PACK_MAX_CHUNKS = 1024;
@@ -51,6 +52,13 @@ __device__ __forceinline__ uint64_t same_sample_lanes(int b, bool valid, int bit
     same &= bit ? m : ~m;
   }
   return valid ? same : 0ull;
+}
+
+// Clears the error word before any later atomic of this kernel or of the next ones ORs into
+// it: an atomic exchange whose result is consumed, so that the wave waits for it.
+__device__ __forceinline__ void clear_err_word(int32_t* err, int* sink) {
+  const int old = __hip_atomic_exchange(err, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (old == 0x7fffffff) *sink = 0;  // never true for the flag bits: keeps the exchange's wait
 }
 
 // Bits of a sample index below B.
@@ -237,9 +245,10 @@ __global__ __launch_bounds__(PS_SORTED_EV) void pack_sorted_kernel(const int64_t
                                                                    int64_t E, int B, int64_t* __restrict__ offsets,
                                                                    int64_t* __restrict__ order,
                                                                    int64_t* __restrict__ dst_rows,
-                                                                   int* __restrict__ status) {
+                                                                   int* __restrict__ status, int32_t* clear_err) {
   __shared__ int bad;
   if (threadIdx.x == 0) bad = 0;
+  if (clear_err && blockIdx.x == 0 && threadIdx.x == 0) clear_err_word(clear_err, &bad);
   __syncthreads();
   const int64_t e = (int64_t)blockIdx.x * PS_SORTED_EV + threadIdx.x;
   const int64_t b = e < E ? bidx[e * s_bidx] : 0;
@@ -254,12 +263,15 @@ __global__ __launch_bounds__(1024) void pack_small_kernel(const int64_t* __restr
                                                           int64_t* __restrict__ order, int64_t* __restrict__ dst_rows,
                                                           int64_t* __restrict__ rank, int32_t* __restrict__ err,
                                                           const int* __restrict__ status, int n_status,
-                                                          bool try_sorted, int32_t* __restrict__ ident) {
+                                                          bool try_sorted, int32_t* __restrict__ ident,
+                                                          bool clear_err) {
   __shared__ int cnt[PS_WAVES * PS_MAX_B];  // per-wave counts, then per-wave next CSR row
   __shared__ int first[PS_MAX_B];           // CSR offset of each sample
   __shared__ int wsum[PS_WAVES];
   __shared__ int unsorted;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  // (every OR into err below follows at least one barrier)
+  if (clear_err && err && tid == 0) clear_err_word(err, &wsum[0]);
   if (status) {  // after pack_sorted_kernel: nothing left to do when every range was sorted
     if (tid == 0) unsorted = 0;
     __syncthreads();
@@ -641,7 +653,9 @@ int64_t cortex_pack_workspace_bytes(int64_t E, int64_t B) {
 // needs clearing between calls.
 static int pack_plan_impl(const char* who, const int64_t* batch_indices, int64_t s_bidx, int64_t E, int64_t B,
                           int64_t* offsets, int64_t* order, int64_t* dst_rows, int64_t* rank, void* workspace,
-                          int64_t workspace_bytes, int32_t* err_flag, int32_t* identity, hipStream_t stream) {
+                          int64_t workspace_bytes, int32_t* err_flag, int32_t* identity, int flags,
+                          hipStream_t stream) {
+  const bool clear = (flags & PACK_FLAG_CLEAR_ERR) && err_flag != nullptr;
   CORTEX_CHECK_ARG(E >= 0 && B >= 1, "%s: need E >= 0 and B >= 1 (got E=%lld B=%lld)", who, (long long)E,
                    (long long)B);
   CORTEX_CHECK_ARG(B <= PACK_MAX_B, "%s: B=%lld exceeds the supported maximum %d", who, (long long)B, PACK_MAX_B);
@@ -650,6 +664,10 @@ static int pack_plan_impl(const char* who, const int64_t* batch_indices, int64_t
     hipLaunchKernelGGL(fill_i64_kernel, dim3((unsigned)cdiv(B + 1, 256)), dim3(256), 0, stream, offsets, B + 1,
                        (int64_t)0);
     CORTEX_CHECK_LAUNCH("cortex_pack_plan(E=0)");
+    if (clear) {
+      hipLaunchKernelGGL(fill_i32_kernel, dim3(1), dim3(64), 0, stream, err_flag, (int64_t)1, 0);
+      CORTEX_CHECK_LAUNCH("cortex_pack_plan(E=0)");
+    }
     if (identity) {  // the empty plan is the identity
       hipLaunchKernelGGL(fill_i32_kernel, dim3(1), dim3(64), 0, stream, identity, (int64_t)1, 1);
       CORTEX_CHECK_LAUNCH("cortex_pack_plan(E=0)");
@@ -673,17 +691,23 @@ static int pack_plan_impl(const char* who, const int64_t* batch_indices, int64_t
     if (rank == nullptr && !one && workspace != nullptr && workspace_bytes >= n_status * (int64_t)sizeof(int)) {
       status = reinterpret_cast<int*>(workspace);
       hipLaunchKernelGGL(pack_sorted_kernel, dim3((unsigned)n_status), dim3(PS_SORTED_EV), 0, stream, batch_indices,
-                         s_bidx, E, (int)B, offsets, identity ? nullptr : order, dst_rows, status);
+                         s_bidx, E, (int)B, offsets, identity ? nullptr : order, dst_rows, status,
+                         clear ? err_flag : nullptr);
       CORTEX_CHECK_LAUNCH("pack_sorted_kernel");
     }
     hipLaunchKernelGGL(pack_small_kernel, dim3(1), dim3(64 * PS_WAVES), 0, stream, batch_indices, s_bidx, E, (int)B,
-                       offsets, order, dst_rows, rank, err_flag, status, n_status, one, identity);
+                       offsets, order, dst_rows, rank, err_flag, status, n_status, one, identity,
+                       clear && status == nullptr);
     CORTEX_CHECK_LAUNCH("pack_small_kernel");
     return OK;
   }
   const int64_t C = pack_chunk_size(E);
   const int nchunks = (int)cdiv(E, C);
   int* counts = reinterpret_cast<int*>(workspace);
+  if (clear) {
+    hipLaunchKernelGGL(fill_i32_kernel, dim3(1), dim3(64), 0, stream, err_flag, (int64_t)1, 0);
+    CORTEX_CHECK_LAUNCH("cortex_pack_plan(clear)");
+  }
   hipLaunchKernelGGL(pack_count_kernel, dim3(nchunks), dim3(256), 0, stream, batch_indices, s_bidx, E, (int)B, C,
                      counts, err_flag);
   CORTEX_CHECK_LAUNCH("pack_count_kernel");
@@ -739,9 +763,9 @@ extern "C" {
 
 int cortex_pack_plan(const int64_t* batch_indices, int64_t s_bidx, int64_t E, int64_t B, int64_t* offsets,
                      int64_t* order, int64_t* dst_rows, int64_t* rank, void* workspace, int64_t workspace_bytes,
-                     int32_t* err_flag, int32_t* identity, hipStream_t stream) {
+                     int32_t* err_flag, int32_t* identity, int flags, hipStream_t stream) {
   return pack_plan_impl("cortex_pack_plan", batch_indices, s_bidx, E, B, offsets, order, dst_rows, rank, workspace,
-                        workspace_bytes, err_flag, identity, stream);
+                        workspace_bytes, err_flag, identity, flags, stream);
 }
 
 int64_t cortex_pack_noalloc_max_workspace_bytes(void) { return PACK_SCRATCH_BYTES; }
@@ -766,7 +790,7 @@ int cortex_pack_plan_noalloc(const int64_t* batch_indices, int64_t s_bidx, int64
   const int rc = pack_scratch_ptr(dev, &ws);
   if (rc != OK) return rc;
   return pack_plan_impl("cortex_pack_plan_noalloc", batch_indices, s_bidx, E, B, offsets, order, dst_rows, rank, ws,
-                        PACK_SCRATCH_BYTES, err_flag, nullptr, stream);
+                        PACK_SCRATCH_BYTES, err_flag, nullptr, 0, stream);
 }
 
 int cortex_tokenize(int dtype, int64_t D, const void* neuron_emb, int64_t n_neuron, int64_t ld_neuron,

@@ -45,6 +45,9 @@ const char* cortex_last_error(void);
  *                   to 1 and leaves `order` unwritten (row r is event r); any other plan
  *                   sets it to 0 and writes `order`.  Consumers take the flag beside
  *                   `order` (cortex_tokenize, cortex_tokenize_ln).
+ *   flags           CORTEX_PACK_CLEAR_ERR (1): set *err_flag to 0 before the plan ORs into
+ *                   it, inside the plan's own first launch (a forward's error word starts
+ *                   clean without a separate fill launch).
  * workspace: at least cortex_pack_workspace_bytes(E, B) bytes of device memory.
  * Sorted batch indices (the collate order) are recognised on the device when rank is
  * null: up to 4096 events the check and the plan are one launch; above, the identity
@@ -53,7 +56,8 @@ const char* cortex_last_error(void);
 int64_t cortex_pack_workspace_bytes(int64_t E, int64_t B);
 int cortex_pack_plan(const int64_t* batch_indices, int64_t s_bidx, int64_t E, int64_t B, int64_t* offsets,
                      int64_t* order, int64_t* dst_rows, int64_t* rank, void* workspace, int64_t workspace_bytes,
-                     int32_t* err_flag, int32_t* identity, hipStream_t stream);
+                     int32_t* err_flag, int32_t* identity, int flags, hipStream_t stream);
+#define CORTEX_PACK_CLEAR_ERR 1
 
 /* cortex_pack_plan without a workspace argument and without any allocation.  No
  * counterpart in the reference: it is for callers that cannot allocate device memory

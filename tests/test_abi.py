@@ -70,7 +70,7 @@ def test_invalid_arguments_return_status_and_message():
     assert rc == -1
     assert lib.cortex_pack_workspace_bytes(0, 4) == 0
     assert lib.cortex_pack_workspace_bytes(5000, 32) == 5 * 32 * 4
-    rc = lib.cortex_pack_plan(None, 1, 10, 100000, None, None, None, None, None, 0, None, None, None)
+    rc = lib.cortex_pack_plan(None, 1, 10, 100000, None, None, None, None, None, 0, None, None, 0, None)
     assert rc == -1 and b"exceeds" in lib.cortex_last_error()
 
 

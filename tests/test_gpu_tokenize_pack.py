@@ -281,9 +281,10 @@ def test_pack_plan_sorted_fast_path(name):
         np.testing.assert_array_equal(order.cpu().numpy()[:n], np.flatnonzero(valid)[p.order])
         if with_rank:
             np.testing.assert_array_equal(rank.cpu().numpy()[valid], p.rank)
-    err = torch.zeros(1, dtype=torch.int32, device=DEV)
-    off, order, _, ident = ops.pack_plan(t, B, err=err, with_rank=False, identity=True)
+    err = torch.full((1,), 0x5C, dtype=torch.int32, device=DEV)  # stale bits: cleared by the plan itself
+    off, order, _, ident = ops.pack_plan(t, B, err=err, with_rank=False, identity=True, clear_err=True)
     torch.cuda.synchronize()
+    assert int(err.item()) == (0 if valid.all() else 2)
     sorted_ok = bool(valid.all() and (np.diff(bidx) >= 0).all())
     assert int(ident.item()) == int(sorted_ok)
     np.testing.assert_array_equal(off.cpu().numpy(), p.offsets)

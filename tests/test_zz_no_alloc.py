@@ -38,7 +38,7 @@ def _plan(nat, lib, bidx: torch.Tensor, B: int, with_rank: bool, noalloc: bool):
         ws_bytes = lib.cortex_pack_workspace_bytes(E, B)
         ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=DEV)
         rc = lib.cortex_pack_plan(nat.ptr(bidx), 1, E, B, nat.ptr(offsets), nat.ptr(order), nat.ptr(dst),
-                                  nat.ptr(rank), nat.ptr(ws), ws_bytes, nat.ptr(err), None, stream)
+                                  nat.ptr(rank), nat.ptr(ws), ws_bytes, nat.ptr(err), None, 0, stream)
     assert rc == 0, lib.cortex_last_error()
     torch.cuda.synchronize()
     return [t.cpu() for t in (offsets, order, dst, rank, err) if t is not None]
