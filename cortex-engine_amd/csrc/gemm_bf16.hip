@@ -104,15 +104,14 @@ __device__ __forceinline__ int swz_w(int r) { return ((r >> 1) & 1) | ((r >> 2) 
 // tiles 2p and 2p+1 give lane group g4 the 8 consecutive columns 32 p + 8 g4 .. +7.
 __device__ __forceinline__ int wrow_of(int p, int jj, int rho) { return 32 * p + 8 * (rho >> 2) + 4 * jj + (rho & 3); }
 
-// int8 weight rows streamed into the bf16 LDS ring (TW = int8_t with bf16 activations):
-// lane (row r, chunk c) loads W[r, k0 + 16 c .. +15] (16 bytes) into registers one step
-// ahead, and before the step's barrier widens them exactly to bf16 (every int8 value is a
-// bf16 value) and stores them as the logical 16-byte chunks 2c, 2c+1 of LDS row r.  Each
-// weight element is widened once per workgroup, and half the weight bytes cross L2.
-__device__ __forceinline__ void widen_store_i8x16(unsigned char* row, int sw, int c, uint4 raw) {
-  *reinterpret_cast<bf16x8*>(row + (((2 * c) ^ sw) << 4)) = widen_i8x8(make_uint2(raw.x, raw.y));
-  *reinterpret_cast<bf16x8*>(row + (((2 * c + 1) ^ sw) << 4)) = widen_i8x8(make_uint2(raw.z, raw.w));
-}
+// int8 weight rows with bf16 activations (TW = int8_t, TIN = bf16: the QuantizedLinear int8
+// weight itself): the int8 rows travel global -> LDS by the same direct-to-LDS transfers as
+// bf16 rows, 64 bytes of K per row and step (half the bytes), and each lane widens its 8-byte
+// fragment exactly to bf16 (every int8 value is a bf16 value; one byte convert per value and
+// one pack per pair) right before the MFMAs that use it.  The 16-byte chunk c of LDS row r
+// holds logical chunk c ^ swz8(r): the 16 rows of one fragment read then fall on distinct
+// four-bank groups in both output orders (natural rows 0..15, interleaved rows of wrow_of).
+__device__ __forceinline__ int swz8(int r) { return ((r >> 3) ^ (r >> 2)) & 3; }
 
 template <class TL, int ACT, bool RES, class TOUT, class TIN = bf16, class TW = TIN, bool RS = false>
 __global__ __launch_bounds__(TL::THREADS) void gemm_bf16_kernel(GemmArgs g) {
@@ -124,15 +123,16 @@ __global__ __launch_bounds__(TL::THREADS) void gemm_bf16_kernel(GemmArgs g) {
   using OP = Operand<TIN>;
   typedef typename OP::frag frag;
   constexpr int EPC = OP::EPC, BK = 8 * EPC;  // K elements per 16-byte chunk and per 128-byte row
-  // int8 weight rows widened through registers (see widen_store_i8x16): WL loads of 16 rows
-  // per wavefront and step, each in flight for one step (two-stage rings only)
+  // int8 weight rows through LDS, widened at the fragment read (see swz8): 64-byte rows, so a
+  // stage holds BN * 64 bytes of W and a wavefront transfers W8B 1 KiB blocks per step
   constexpr bool WI8 = sizeof(TW) == 1 && sizeof(TIN) == 2;
-  constexpr int WL = WI8 ? BN / (16 * TL::WAVES) : 1;
-  static_assert(!WI8 || (BN % (16 * TL::WAVES) == 0 && S == 2), "int8 weight staging shape");
+  constexpr int W_STAGE = WI8 ? BN * 64 : TL::W_STAGE;
+  constexpr int W8B = WI8 ? W_STAGE / 1024 / TL::WAVES : 1;
+  static_assert(!WI8 || W_STAGE % (1024 * TL::WAVES) == 0, "int8 weight transfer split");
   // RS: each lane sums the squares of the A values its fragments hold (row wrow + 16 t + fr,
   // eight of every 32 K per sub-step); the four lanes of a row complete the sum at the end
   static_assert(!RS || (sizeof(TIN) == 2 && sizeof(TW) == 2 && !RES), "row scale: bf16 operands");
-  constexpr int WOPS = WI8 ? WL : WB;  // vector-memory operations per step for W
+  constexpr int WOPS = WI8 ? W8B : WB;  // vector-memory operations per step for W
   constexpr int STEP_OPS = AB + WOPS;
   __shared__ __attribute__((aligned(1024))) unsigned char smem[TL::LDS];
 
@@ -165,15 +165,14 @@ __global__ __launch_bounds__(TL::THREADS) void gemm_bf16_kernel(GemmArgs g) {
     if constexpr (O32) a_vo[i] = (uint32_t)(e * (int64_t)sizeof(TIN));
     else a_src[i] = A + e;
   }
-  const TW* w_src[O32 ? 1 : (WI8 ? WL : WB)];
+  const TW* w_src[O32 ? 1 : (WI8 ? W8B : WB)];
   uint32_t w_vo[O32 ? WB : 1];
-  int w_row[WI8 ? WL : 1];
   if constexpr (WI8) {
+    // lane i of block q writes LDS bytes [16 i, 16 i + 16): row 16 q + i / 4, stored chunk i % 4
 #pragma unroll
-    for (int i = 0; i < WL; ++i) {
-      const int r = (wid * WL + i) * 16 + (lane >> 2);
-      w_row[i] = r;
-      w_src[i] = W + (int64_t)min(n0 + r, N - 1) * g.ld_w + (lane & 3) * 16;
+    for (int i = 0; i < W8B; ++i) {
+      const int r = (wid * W8B + i) * 16 + (lane >> 2);
+      w_src[i] = W + (int64_t)min(n0 + r, N - 1) * g.ld_w + (((lane & 3) ^ swz8(r)) * 16);
     }
   } else {
 #pragma unroll
@@ -185,15 +184,16 @@ __global__ __launch_bounds__(TL::THREADS) void gemm_bf16_kernel(GemmArgs g) {
     }
   }
   auto a_stage = [&](int s) { return ring + s * TL::A_STAGE; };
-  auto w_stage = [&](int s) { return ring + S * TL::A_STAGE + s * TL::W_STAGE; };
+  auto w_stage = [&](int s) { return ring + S * TL::A_STAGE + s * W_STAGE; };
   const int nk = K / BK / TL::KS;  // K steps of this group
   const int kbase = kg * nk * BK;
-  uint4 wreg[WI8 ? WL : 1];  // int8 weight rows of the next step, before widening
   auto issue = [&](int kt) {
     const int s = kt % S, k0 = kbase + kt * BK;
     if constexpr (WI8) {
 #pragma unroll
-      for (int i = 0; i < WL; ++i) wreg[i] = *reinterpret_cast<const uint4*>(w_src[i] + k0);
+      for (int i = 0; i < W8B; ++i)
+        __builtin_amdgcn_global_load_lds(static_cast<const void*>(w_src[i] + k0),
+                                         static_cast<void*>(w_stage(s) + (wid * W8B + i) * 1024), 16, 0, 0);
     }
     if constexpr (O32) {
       const unsigned char* ab = reinterpret_cast<const unsigned char*>(A + k0);
@@ -213,16 +213,6 @@ __global__ __launch_bounds__(TL::THREADS) void gemm_bf16_kernel(GemmArgs g) {
       for (int i = 0; i < WB; ++i)
         __builtin_amdgcn_global_load_lds(static_cast<const void*>(w_src[i] + k0),
                                          static_cast<void*>(w_stage(s) + (wid * WB + i) * 1024), 16, 0, 0);
-    }
-  };
-  // widen the registers of the last issued step into its W stage
-  auto commit_w = [&](int s) {
-    if constexpr (WI8) {
-#pragma unroll
-      for (int i = 0; i < WL; ++i) {
-        const int r = w_row[i];
-        widen_store_i8x16(w_stage(s) + r * 128, IL ? swz_w(r) : swz_a(r), lane & 3, wreg[i]);
-      }
     }
   };
 
@@ -245,18 +235,30 @@ __global__ __launch_bounds__(TL::THREADS) void gemm_bf16_kernel(GemmArgs g) {
 #pragma unroll
   for (int t = 0; t < TN; ++t) {
     const int r = wcol + (IL ? wrow_of(t >> 1, t & 1, fr) : t * 16 + fr);
-    w_off[t] = r * 128;
-    w_sw[t] = IL ? swz_w(r) : swz_a(r);
+    w_off[t] = r * (WI8 ? 64 : 128);
+    w_sw[t] = WI8 ? swz8(r) : IL ? swz_w(r) : swz_a(r);
   }
-  auto read_frags = [&](int stage, int ks, frag (&af)[TM], frag (&wf)[TN]) {
+  // W fragments as read from LDS: bf16 fragments, or with int8 weights the raw 8 bytes, widened
+  // in the MFMA loop right before their TM uses (double-buffered raw bytes take half the
+  // registers of widened fragments)
+  typedef typename std::conditional<WI8, uint2, frag>::type wfrag;
+  auto read_frags = [&](int stage, int ks, frag (&af)[TM], wfrag (&wf)[TN]) {
     const unsigned char* as = a_stage(stage);
     const unsigned char* ws = w_stage(stage);
 #pragma unroll
     for (int t = 0; t < TM; ++t)
       af[t] = *reinterpret_cast<const frag*>(as + a_off[t] + (((ks * 4 + g4) ^ a_sw[t]) << 4));
+    if constexpr (WI8) {
+      // K [32 ks + 8 g4, +8) of the row: logical chunk 2 ks + g4 / 2, half g4 % 2
 #pragma unroll
-    for (int t = 0; t < TN; ++t)
-      wf[t] = *reinterpret_cast<const frag*>(ws + w_off[t] + (((ks * 4 + g4) ^ w_sw[t]) << 4));
+      for (int t = 0; t < TN; ++t)
+        wf[t] = *reinterpret_cast<const uint2*>(ws + w_off[t] + (((2 * ks + (g4 >> 1)) ^ w_sw[t]) << 4) +
+                                                ((g4 & 1) << 3));
+    } else {
+#pragma unroll
+      for (int t = 0; t < TN; ++t)
+        wf[t] = *reinterpret_cast<const frag*>(ws + w_off[t] + (((ks * 4 + g4) ^ w_sw[t]) << 4));
+    }
   };
   float ssq[RS ? TM : 1] = {};  // RS: this lane's sum of squares of each row fragment
   // Raised wave priority over each MFMA group, so a wavefront ready to multiply issues ahead of
@@ -264,13 +266,22 @@ __global__ __launch_bounds__(TL::THREADS) void gemm_bf16_kernel(GemmArgs g) {
   // row-scaled form with the K split (config 2 at N = 512: 9.75 -> 9.29 us) and costs the
   // single-group tiles and the residual GEMMs 0.4-1 us, so only that form sets it.
   constexpr bool PRIO = RS && TL::KS > 1;
-  auto mma = [&](const frag (&af)[TM], const frag (&wf)[TN]) {
+  auto mma = [&](const frag (&af)[TM], const wfrag (&wf)[TN]) {
     if constexpr (PRIO) __builtin_amdgcn_s_setprio(1);
+    if constexpr (WI8) {
 #pragma unroll
-    for (int i = 0; i < TM; ++i)
+      for (int j = 0; j < TN; ++j) {
+        const frag w = widen_i8x8(wf[j]);
 #pragma unroll
-      for (int j = 0; j < TN; ++j)
-        acc[i][j] = OP::mma(wf[j], af[i], acc[i][j]);
+        for (int i = 0; i < TM; ++i) acc[i][j] = OP::mma(w, af[i], acc[i][j]);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+          acc[i][j] = OP::mma(wf[j], af[i], acc[i][j]);
+    }
     if constexpr (PRIO) __builtin_amdgcn_s_setprio(0);
     if constexpr (RS) {
 #pragma unroll
@@ -304,19 +315,10 @@ __global__ __launch_bounds__(TL::THREADS) void gemm_bf16_kernel(GemmArgs g) {
 
   // Every stage of the ring is in flight at once; a stage is refilled as soon as all
   // wavefronts hold its last fragments in registers.  Fragments are double-buffered
-  // in registers, so the LDS reads of the next K sub-step overlap the MFMAs.  With
-  // int8 weights, step 0's weight registers are widened before step 1 is issued.
-  if constexpr (WI8) {
-    issue(0);
-    wait_vm<0>();
-    commit_w(0);
-    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the widened rows are in LDS before the barrier
-    if (1 < nk) issue(1);
-  } else {
+  // in registers, so the LDS reads of the next K sub-step overlap the MFMAs.
 #pragma unroll
-    for (int p = 0; p < S; ++p)
-      if (p < nk) issue(p);
-  }
+  for (int p = 0; p < S; ++p)
+    if (p < nk) issue(p);
   // wait until this wave's transfers of step j landed, steps up to `last` being issued
   auto wait_step = [&](int j, int last) {
     const int ahead = min(nk - 1, last) - j;  // steps issued after j
@@ -334,7 +336,8 @@ __global__ __launch_bounds__(TL::THREADS) void gemm_bf16_kernel(GemmArgs g) {
         wait_vm<0>();
     }
   };
-  frag af0[TM], wf0[TN], af1[TM], wf1[TN];
+  frag af0[TM], af1[TM];
+  wfrag wf0[TN], wf1[TN];
   wait_step(0, S - 1);
   __builtin_amdgcn_s_barrier();
   read_frags(0, 0, af0, wf0);
@@ -353,13 +356,8 @@ __global__ __launch_bounds__(TL::THREADS) void gemm_bf16_kernel(GemmArgs g) {
     __builtin_amdgcn_sched_barrier(0);   // the reads go out first: the barrier below waits for them
     mma(af0, wf0);
     __builtin_amdgcn_sched_barrier(0);   // and every MFMA of sub-step 0 is issued before that wait
-    if constexpr (WI8) {
-      wait_vm<0>();                      // step kt+1: A transfers and weight registers
-      commit_w((kt + 1) % S);
-    } else {
-      wait_step(kt + 1, kt + S - 1);
-    }
-    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's reads of stage st (and W stores) done
+    wait_step(kt + 1, kt + S - 1);
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's reads of stage st done
     __builtin_amdgcn_s_barrier();        // all waves done with stage st; step kt+1 visible
     read_frags((kt + 1) % S, 0, af0, wf0);
     __builtin_amdgcn_sched_barrier(0);   // the next step's first reads go out before these MFMAs
@@ -514,6 +512,12 @@ using B256x128s2 = BTile<256, 128, 2, 4, 2>;
 using B256x256s2 = BTile<256, 256, 2, 4, 2>;
 using B256x192s2 = BTile<256, 192, 2, 4, 2>;
 using B128x128s2k2 = BTile<128, 128, 2, 2, 2, 2>;
+// int8 weights widened at the fragment read: wavefronts span more rows, so that each widened
+// W fragment feeds more MFMAs (128 x 64 and 128 x 32 wavefront tiles).  Measured at the
+// forward's shapes: MLP-up 25.7 against 28.6 us with the bf16 tiles' layout, MLP-down 28.3
+// against 30.2 us; the bf16 weights gain nothing from these layouts (22.9 / 25.4 us).
+using B256x256s2w = BTile<256, 256, 2, 2, 4>;
+using B128x128s2k2w = BTile<128, 128, 2, 1, 4, 2>;
 
 int cu_count() {
   static int v = [] {
@@ -541,9 +545,9 @@ TileChoice wide_tile(const GemmArgs& g, bool allow192) {
 template <int ACT, bool RES, class TOUT, class TW = bf16>
 int dispatch(const GemmArgs& g, hipStream_t stream) {
   if constexpr (sizeof(TW) == 1) {
-    // int8 weights widened through registers: the 256 x 256 tile has no room for the weight
-    // registers (256 x 128 instead), and no 192-column tile
-    return wide_tile(g, false) == T256 ? launch<B256x128s2, ACT, RES, TOUT, bf16, TW>(g, stream)
+    // int8 weights (widened at the fragment read): the same tiles as bf16 weights but the
+    // 192-column one
+    return wide_tile(g, false) == T256 ? launch<B256x256s2w, ACT, RES, TOUT, bf16, TW>(g, stream)
                                        : launch<B128x128s2, ACT, RES, TOUT, bf16, TW>(g, stream);
   } else {
     switch (wide_tile(g, true)) {
@@ -1093,7 +1097,7 @@ int try_gemm_bf16(const GemmArgs& g, int x_dtype, int w_dtype, int w_layout, int
   // grids go to the pipelined kernel (gemm_pipe.hip)
   if (res) {
     if (g.act || g.K % 128 || cdiv(g.M, 128) * cdiv(g.N, 128) > cu_count()) return 0;
-    return w8 ? launch<B128x128s2k2, ACT_NONE, true, float, bf16, int8_t>(g, stream)
+    return w8 ? launch<B128x128s2k2w, ACT_NONE, true, float, bf16, int8_t>(g, stream)
               : launch<B128x128s2k2, ACT_NONE, true, float, bf16, bf16>(g, stream);
   }
   if (w8) {
