@@ -8,8 +8,10 @@ A step is one forward of the fixed workload (CORTEX_S, weights quantised to INT8
 channel on the GPU, bf16 MFMA with fp32 accumulation and an fp32 residual stream,
 B = 32 samples x 512 events) replayed from a HIP graph captured on the resident event
 buffers: the inputs are in HBM before the timed region and a step copies nothing.
-``steady_state`` re-times the same replay after every other measurement, once the GPU
-clocks have left the ramp that the first few dozen replays of a fresh process see.
+The first few dozen replays of a fresh process run while the GPU clocks ramp up: they
+are reported as ``cold_start``, and the headline's W warmup + K timed replays follow the
+eager forward and the per-kernel timings.  ``steady_state`` re-times 200 replays after
+every other measurement.
 
 Usage:
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--quick]
@@ -921,17 +923,23 @@ def main() -> int:
     # the graph reads the resident event buffers in place (no staging copies in a step)
     cap = CapturedForward(model, batch_size=B, n_events=B * per, inputs=tuple(inputs))
     log("bench: graph captured; warmup")
-    for _ in range(args.warmup):
-        cap()
-    torch.cuda.synchronize(dev)
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        cap()
-    torch.cuda.synchronize(dev)
-    elapsed = time.perf_counter() - t0
-    ms_step = elapsed / args.steps * 1e3
-    value = B * args.steps / elapsed
-    log(f"bench: {ms_step:.4f} ms/step, {value:.1f} samples/s")
+
+    def timed_steps() -> float:  # W untimed replays, then K timed ones: seconds for the K
+        for _ in range(args.warmup):
+            cap()
+        torch.cuda.synchronize(dev)
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            cap()
+        torch.cuda.synchronize(dev)
+        return time.perf_counter() - t0
+
+    # The first few dozen replays of a fresh process run while the GPU clocks are still
+    # ramping up (a short run is up to 4 % slower there).  They are timed and reported as
+    # `cold_start`; the headline is timed after the eager forward and the kernel timings below
+    # have brought the clocks up, with the same W + K protocol.
+    cold_ms = timed_steps() / args.steps * 1e3
+    log(f"bench: cold start {cold_ms:.4f} ms/step")
 
     with torch.no_grad():  # eager (no graph) forward, for reference
         for _ in range(3):
@@ -947,6 +955,11 @@ def main() -> int:
     dominant = max(kern, key=lambda k: kern[k]["avg_us"] * kern[k]["launches_per_forward"])
     roof = roofline_of(dominant, kern[dominant])
     log(f"bench: dominant kernel {dominant}: {roof['avg_us']} us, {roof['achieved']} {roof['unit']}")
+
+    elapsed = timed_steps()
+    ms_step = elapsed / args.steps * 1e3
+    value = B * args.steps / elapsed
+    log(f"bench: {ms_step:.4f} ms/step, {value:.1f} samples/s")
     extra = {}
     if not args.quick:
         with torch.no_grad():
@@ -998,9 +1011,11 @@ def main() -> int:
         "forward_tflops_algorithmic": round(fwd_flops / (ms_step * 1e-3) / 1e12, 2),
         "forward_mfma_frac_algorithmic": round(fwd_flops / (ms_step * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4),
         "eager_ms_per_forward": round(eager_ms, 4),
+        "cold_start": {"ms_per_step": round(cold_ms, 4), "samples_per_s": round(B / cold_ms * 1e3, 2),
+                       "when": "W warmup + K timed replays right after the graph capture, while the GPU "
+                               "clocks ramp up; value above repeats W + K after the kernel timings"},
         "steady_state": {"ms_per_step": round(steady_ms, 4), "samples_per_s": round(B / steady_ms * 1e3, 2),
-                         "steps": 200, "when": "after every other GPU measurement of this run (clocks settled); "
-                                               "value above is the timed K steps right after W warmup steps"},
+                         "steps": 200, "when": "200 replays after every other GPU measurement of this run"},
         "roofline": roof, "kernels": kern, "cpu_baseline": cpu, **extra,
     }
     print(json.dumps(line), flush=True)

@@ -231,13 +231,19 @@ __global__ __launch_bounds__(RL_THREADS) void gemm_rowln_kernel(RowLnArgs g) {
   // no branch joins in front of an MFMA group, where the compiler would wait for the
   // fragment reads just issued, and each step first waits explicitly for the fragments read
   // after the previous barrier.
-  auto step = [&](int kt, auto refill) {
+  // `first`: step 0, whose successor's transfers were issued before the residual loads,
+  // which stay outstanding.
+  auto step = [&](int kt, auto refill, auto first) {
     const int st = kt % S;
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): sub-step 0's fragments
     read_frags(st, 1, af1, wf1);
     mma(af0, wf0);
     if constexpr (WI8) {
-      rl_wait_vm<0>();  // step kt+1: A transfer and weight registers
+      // step kt+1: A transfer and weight registers
+      if constexpr (decltype(first)::value)
+        rl_wait_vm<RV>();
+      else
+        rl_wait_vm<0>();
       commit_w((kt + 1) % S);
     } else {
       wait_step(kt + 1, kt + S - 1);
@@ -248,9 +254,17 @@ __global__ __launch_bounds__(RL_THREADS) void gemm_rowln_kernel(RowLnArgs g) {
     if constexpr (decltype(refill)::value) issue(kt + S);
     mma(af1, wf1);
   };
+  using yes = std::integral_constant<bool, true>;
+  using no = std::integral_constant<bool, false>;
   int kt = 0;
-  for (; kt + S < nk; ++kt) step(kt, std::integral_constant<bool, true>{});
-  for (; kt + 1 < nk; ++kt) step(kt, std::integral_constant<bool, false>{});
+  if constexpr (WI8) {
+    if (S < nk)
+      step(kt++, yes{}, yes{});
+    else if (1 < nk)
+      step(kt++, no{}, yes{});
+  }
+  for (; kt + S < nk; ++kt) step(kt, yes{}, no{});
+  for (; kt + 1 < nk; ++kt) step(kt, no{}, no{});
   __builtin_amdgcn_s_waitcnt(0xC07F);  // the last step
   read_frags((nk - 1) % S, 1, af1, wf1);
   mma(af0, wf0);

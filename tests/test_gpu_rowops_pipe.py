@@ -209,10 +209,11 @@ def test_pipe_gemm_float_weight_image():
 def test_gemm_outputs_repeatable(M, N, act, out):
     """Every output element is written with the value computed for it, on every launch.
 
-    The kernels write their outputs with device-scope write-through stores issued as inline
-    assembly; a VALU write to a store's data registers too soon after the store (a hazard the
-    compiler does not see through the assembly) changed a few rows from launch to launch at
-    these shapes.  Five launches into fresh buffers must agree bit for bit and with float64."""
+    The kernels write their outputs with device-scope write-through stores (single-wave grids)
+    or write-back ones, some of them while later K steps run; when these stores were inline
+    assembly, a VALU write to a store's data registers too soon after it (a hazard the compiler
+    did not see) changed a few rows from launch to launch at these shapes.  Five launches into
+    fresh buffers must agree bit for bit and with float64."""
     from cortex.kernels import ops
 
     K = 512
@@ -233,6 +234,41 @@ def test_gemm_outputs_repeatable(M, N, act, out):
         assert bool((err <= _bf16_ulp(ref) + 1e-5 * float(ref.abs().max())).all())
     else:
         assert float(err.max()) <= 1e-5 * float(ref.abs().max())
+
+
+@pytest.mark.parametrize("M,N,act,with_bias,with_scale", [(8192, 2048, "gelu", True, True),
+                                                          (16000, 1024, None, True, False),
+                                                          (8000, 2048, "gelu", False, True),
+                                                          (16384, 1024, None, False, False)])
+def test_wide_tile_bf16_epilogue(M, N, act, with_bias, with_scale):
+    """bf16-output GEMMs at K = 512 on 256 x 256 tiles filling the chip (the MLP-up and
+    kv-projection shapes): bias or none, scale or none, GELU or none, a ragged last row tile.
+    Every element within one bf16 rounding of float64, every launch bit-identical."""
+    from cortex.kernels import ops
+
+    K = 512
+    g = torch.Generator().manual_seed(M + N + 3)
+    a = torch.randn(M, K, generator=g).bfloat16()
+    q, s = O.quantize_int8((torch.randn(N, K, generator=g) * 0.05).numpy())
+    q, s = torch.from_numpy(q), torch.from_numpy(s)
+    bias = torch.randn(N, generator=g) if with_bias else None
+    img = ops.convert(q.to(DEV), torch.bfloat16)
+    if not with_scale:  # the scale folded into a float weight rounded to bf16 (exact in float64 below)
+        w = (q.double() * s.double()[:, None]).to(torch.bfloat16)
+        img, s_dev, wref = w.to(DEV), None, w.double()
+    else:
+        s_dev, wref = s.to(DEV), q.double() * s.double()[:, None]
+    ad = a.to(DEV)
+    ys = [ops.norm_linear(ad, weight=img, weight_scale=s_dev, bias=None if bias is None else bias.to(DEV),
+                          act=act, out_dtype=torch.bfloat16) for _ in range(3)]
+    assert all(torch.equal(y, ys[0]) for y in ys[1:])
+    ref = a.double() @ wref.T
+    if bias is not None:
+        ref = ref + bias.double()
+    if act == "gelu":
+        ref = F.gelu(ref)
+    err = (ys[0].cpu().double() - ref).abs()
+    assert bool((err <= _bf16_ulp(ref) + 1e-5 * float(ref.abs().max())).all()), float(err.max())
 
 
 @pytest.mark.parametrize("N", [1, 2, 8])
