@@ -260,6 +260,38 @@ def test_fused_behavior_head_matches_oracle_and_unfused(name):
     assert torch.equal(fused, again)
 
 
+@pytest.mark.parametrize("D,L,B", [(512, 256, 3), (512, 100, 2), (256, 77, 4), (512, 1, 1), (768, 70, 2)])
+def test_behavior_head_kernel_latent_counts(D, L, B):
+    """``cortex_behavior_head`` on latent counts that are not multiples of its 16-latent split
+    (partials per 16 latents, merged per sample by the second launch) against float64: both
+    LayerNorms, rows rounded to bf16 as the kernel's MFMA operand, the exp2-domain softmax over
+    latents of the folded score rows, the weighted value rows summed over heads."""
+    import torch.nn.functional as F
+    from cortex.kernels import ops
+
+    g = torch.Generator().manual_seed(D + L + B)
+    Q, H = 2, 8
+    QH = Q * H
+    x = torch.randn(B * L, D, generator=g) * 1.3 + 0.1
+    g1, g2 = (1 + 0.1 * torch.randn(D, generator=g) for _ in range(2))
+    b1, b2 = (0.1 * torch.randn(D, generator=g) for _ in range(2))
+    ac = torch.zeros(32, D)
+    ac[:QH] = torch.randn(QH, D, generator=g) * (3.0 / D ** 0.5)
+    ac[16:16 + QH] = torch.randn(QH, D, generator=g) * 0.05
+    ac = ac.bfloat16()
+    out = ops.behavior_head(x.to(DEV), B, (g1.to(DEV), b1.to(DEV), 1e-5), (g2.to(DEV), b2.to(DEV), 1e-5),
+                            ac.to(DEV), Q, H).cpu().double()
+    n = F.layer_norm(F.layer_norm(x.double(), (D,), g1.double(), b1.double(), 1e-5), (D,), g2.double(),
+                     b2.double(), 1e-5)
+    n = n.to(torch.bfloat16).double().reshape(B, L, D)
+    a = ac.double()
+    sc, tv = n @ a[:QH].T, n @ a[16:16 + QH].T  # (B, L, QH)
+    wts = torch.softmax(sc * np.log(2.0), dim=1)
+    ref = (wts * tv).sum(1).reshape(B, Q, H).sum(-1)
+    err = float((out - ref).abs().max())
+    assert err <= 2e-3 * float(ref.abs().max()) + 1e-5, (err, float(ref.abs().max()))
+
+
 def test_widen_mode_streams_int8_weights_through_the_fused_path(monkeypatch):
     """CORTEX_INT8_WEIGHTS=widen: no bf16 weight image is built; the GEMMs, the fused QKV +
     attention and the residual linear + LayerNorm read the int8 weights and widen them on chip.
