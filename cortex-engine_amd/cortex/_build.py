@@ -21,7 +21,7 @@ INCLUDE = ROOT.parent / "include"
 BUILD = ROOT / "_build"
 LIB = PKG_DIR / "libcortex_hip.so"
 
-SOURCES = ["abi.cpp", "tokenize_pack.hip", "quant.hip", "norm_gemm.hip", "gemm_pipe.hip", "gemm_bf16.hip", "rowops.hip", "attention.hip", "attention_fast.hip", "block_mask.hip", "pages.hip", "head.hip", "gemm_rowln.hip", "block_attn.hip", "page_table.cpp", "splitk.hip"]
+SOURCES = ["abi.cpp", "tokenize_pack.hip", "quant.hip", "norm_gemm.hip", "gemm_bf16.hip", "rowops.hip", "attention.hip", "attention_fast.hip", "block_mask.hip", "pages.hip", "head.hip", "gemm_rowln.hip", "block_attn.hip", "page_table.cpp", "splitk.hip"]
 ARCH = os.environ.get("CORTEX_OFFLOAD_ARCH", "gfx950")
 
 HIP_FLAGS = [

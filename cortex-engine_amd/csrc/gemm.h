@@ -1,4 +1,4 @@
-// Arguments shared by the general and the fast-path GEMM kernels.
+// Arguments shared by the general and the tiled GEMM kernels.
 #pragma once
 
 #include "common.h"
@@ -48,8 +48,5 @@ int try_gemm_bf16(const GemmArgs& g, int x_dtype, int w_dtype, int w_layout, int
 // K = g.K is the per-slab depth (a multiple of 64) and g.x / g.w are the full rows.  No
 // bias, activation or residual.  Returns 1 when launched, 0 when the grid is too large.
 int split_k_partials(const GemmArgs& g, int splits, hipStream_t stream);
-
-// Pipelined bf16 x int8 path (gemm_pipe.hip), same return convention.
-int try_gemm_pipe(const GemmArgs& g, int x_dtype, int w_dtype, int w_layout, int compute, hipStream_t stream);
 
 }  // namespace cortex

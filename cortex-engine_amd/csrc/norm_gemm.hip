@@ -525,7 +525,6 @@ int cortex_norm_linear(int64_t M, int64_t N, int64_t K, int x_dtype, const void*
   g.vec = vec ? 1 : 0;
   int fast = try_rowdot(g, x_dtype, w_dtype, w_layout, compute, stream);
   if (fast == 0) fast = try_gemm_bf16(g, x_dtype, w_dtype, w_layout, compute, stream);
-  if (fast == 0) fast = try_gemm_pipe(g, x_dtype, w_dtype, w_layout, compute, stream);
   if (fast != 0) return fast > 0 ? OK : fast;
   if (compute == DT_BF16) {
     // fp32 weights are rounded to bf16 (RNE) while staged, i.e. W.to(bfloat16)

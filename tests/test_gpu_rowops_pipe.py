@@ -1,11 +1,12 @@
-"""LayerNorm row kernel, dtype conversion and the pipelined bf16-operand GEMM on the GPU.
+"""LayerNorm row kernel, dtype conversion and the tiled bf16-operand GEMMs on the GPU.
 
 The LayerNorm rows (a5's norm half) are checked against torch's CPU LayerNorm in
 fp32 (fp32 output <= 2e-5 absolute at unit scale; bf16 output within one bf16
-rounding of the fp32 result).  The pipelined GEMM (a6/a7: bf16 rows x int8 or
-bf16 weight rows, per-channel scale, bias, GELU, fp32 residual) is checked
-against a float64 contraction of the same bf16/int8 operands, and the int8-widen
-and bf16-image weight forms are checked to agree with each other.
+rounding of the fp32 result).  The tiled GEMMs (a6/a7: bf16 rows x int8 or bf16
+weight rows, per-channel scale, bias, GELU, fp32 residual, K split over wave groups
+or over workgroups) are checked against a float64 contraction of the same bf16/int8
+operands, and the int8-widen and bf16-image weight forms are checked to agree with
+each other.
 """
 
 from __future__ import annotations
@@ -109,7 +110,7 @@ def _ref(a, q, s, bias=None, act=None, res=None, res_rows=0):
 
 @pytest.mark.parametrize("M,N,K", [(8192, 1536, 512), (8192, 2048, 512), (8192, 512, 2048), (8192, 512, 512),
                                    (16384, 1024, 512), (300, 512, 512), (1, 1024, 512), (130, 200, 64)])
-def test_pipe_gemm_int8_and_image(M, N, K):
+def test_gemm_int8_and_image(M, N, K):
     """int8 weights widened in the kernel and their bf16 image agree, and both match fp64."""
     from cortex.kernels import ops
 
@@ -128,7 +129,7 @@ def test_pipe_gemm_int8_and_image(M, N, K):
 
 
 @pytest.mark.parametrize("wform", ["int8", "image"])
-def test_pipe_gemm_gelu_bf16_out(wform):
+def test_gemm_gelu_bf16_out(wform):
     """MLP-up shape: GELU epilogue, bf16 output within bf16 rounding of the fp64 result."""
     from cortex.kernels import ops
 
@@ -171,7 +172,7 @@ def test_gelu_epilogue_dense_grid(wform):
     assert bool((err <= bound).all()), float((err - bound).max())
 
 
-def test_pipe_gemm_bias_and_broadcast_residual():
+def test_gemm_bias_and_broadcast_residual():
     """Bias epilogue, and the latents residual broadcast every 256 rows into fp32 output."""
     from cortex.kernels import ops
 
@@ -190,7 +191,28 @@ def test_pipe_gemm_bias_and_broadcast_residual():
     assert float((y2.double() - ref2).abs().max()) <= 1e-5 * float(ref2.abs().max())
 
 
-def test_pipe_gemm_float_weight_image():
+@pytest.mark.parametrize("M,K,form", [(16384, 2048, "int8"), (16384, 2048, "image"), (20000, 512, "image"),
+                                      (300, 2048, "image")])
+def test_residual_gemm_every_grid(M, K, form):
+    """Residual GEMMs into the fp32 stream (MLP-down 2048 -> 512 and the 512 -> 512 shape) at
+    one and at several workgroups per CU (B = 64 and larger batches): the K split over two
+    wave groups at every grid size, with a ragged last row tile; within 1e-5 of float64
+    (computed on the device) relative to the largest output, in place over the residual."""
+    from cortex.kernels import ops
+
+    N = 512
+    a, q, s = _operands(M, N, K, seed=M + K)
+    ad, qd, sd = a.to(DEV), q.to(DEV), s.to(DEV)
+    res = torch.randn(M, N, device=DEV)
+    w = {"weight_int8": qd} if form == "int8" else {"weight": ops.convert(qd, torch.bfloat16)}
+    ref = (ad.double() @ (qd.double() * sd.double()[:, None]).T) + res.double()
+    out = res.clone()
+    ops.norm_linear(ad, **w, weight_scale=sd, residual=out, out_dtype=torch.float32, out=out)
+    err = float((out.double() - ref).abs().max())
+    assert err <= 1e-5 * float(ref.abs().max()), err
+
+
+def test_gemm_float_weight_image():
     """A float nn.Linear weight rounded to bf16 (no scale), residual into fp32 output."""
     from cortex.kernels import ops
 
