@@ -78,11 +78,30 @@ __global__ void fill_i32_kernel(int32_t* p, int64_t n, int32_t v) {
   if (i < n) p[i] = v;
 }
 
+// Whether every range of the wide sorted check (pack_sorted_kernel's status words: 1 sorted
+// and in range, 2 not) was sorted; the whole workgroup takes part and gets the same answer.
+// A null status list means no check ran.
+__device__ bool ranges_sorted(const int* __restrict__ status, int n_status, int* s_flag) {
+  if (!status) return false;
+  if (threadIdx.x == 0) *s_flag = 1;
+  __syncthreads();
+  for (int i = threadIdx.x; i < n_status; i += blockDim.x)
+    if (status[i] != 1) *s_flag = 0;
+  __syncthreads();
+  return *s_flag != 0;
+}
+
+// The three launches below return at once when the wide sorted check found every range
+// sorted (the identity plan it wrote is the plan).
+
 // 1) per-chunk histogram of batch indices.
 __global__ __launch_bounds__(256) void pack_count_kernel(const int64_t* __restrict__ bidx, int64_t s_bidx, int64_t E,
                                                           int B, int64_t C, int* __restrict__ counts,
-                                                          int* __restrict__ err) {
+                                                          int* __restrict__ err, const int* __restrict__ status,
+                                                          int n_status) {
   __shared__ int hist[PACK_MAX_B];
+  __shared__ int sorted_flag;
+  if (ranges_sorted(status, n_status, &sorted_flag)) return;
   const int chunk = blockIdx.x;
   for (int b = threadIdx.x; b < B; b += blockDim.x) hist[b] = 0;
   __syncthreads();
@@ -113,10 +132,16 @@ __global__ __launch_bounds__(256) void pack_count_kernel(const int64_t* __restri
 
 // 2) exclusive scan over chunks per sample (in place), then over samples.
 __global__ __launch_bounds__(1024) void pack_scan_kernel(int* __restrict__ counts, int nchunks, int B,
-                                                          int64_t* __restrict__ offsets, int32_t* __restrict__ ident) {
+                                                          int64_t* __restrict__ offsets, int32_t* __restrict__ ident,
+                                                          const int* __restrict__ status, int n_status) {
   __shared__ int64_t part[1024];
   __shared__ int totals[PACK_MAX_B];
+  __shared__ int sorted_flag;
   const int tid = threadIdx.x;
+  if (ranges_sorted(status, n_status, &sorted_flag)) {
+    if (ident && tid == 0) *ident = 1;
+    return;
+  }
   for (int b = tid; b < B; b += blockDim.x) {
     int run = 0;
     for (int c = 0; c < nchunks; ++c) {
@@ -156,8 +181,11 @@ __global__ __launch_bounds__(64) void pack_rank_kernel(const int64_t* __restrict
                                                         int B, int64_t C, const int* __restrict__ chunk_base,
                                                         const int64_t* __restrict__ offsets,
                                                         int64_t* __restrict__ order, int64_t* __restrict__ dst_rows,
-                                                        int64_t* __restrict__ rank) {
+                                                        int64_t* __restrict__ rank, const int* __restrict__ status,
+                                                        int n_status) {
   __shared__ int64_t next[PACK_MAX_B];
+  __shared__ int sorted_flag;
+  if (ranges_sorted(status, n_status, &sorted_flag)) return;
   const int chunk = blockIdx.x;
   const int lane = threadIdx.x;
   for (int b = lane; b < B; b += 64) next[b] = offsets[b] + chunk_base[(int64_t)chunk * B + b];
@@ -640,8 +668,8 @@ int64_t cortex_pack_workspace_bytes(int64_t E, int64_t B) {
   if (E <= 0 || B <= 0) return 0;
   const int64_t C = pack_chunk_size(E);
   const int64_t nchunks = cdiv(E, C);
-  // per-chunk counts (three-launch plan) or one status word per sorted-check workgroup
-  const int64_t words = std::max(nchunks * B, cdiv(E, (int64_t)PS_SORTED_EV));
+  // per-chunk counts (three-launch plan) and one status word per sorted-check workgroup
+  const int64_t words = nchunks * B + cdiv(E, (int64_t)PS_SORTED_EV);
   return words * (int64_t)sizeof(int);
 }
 
@@ -704,17 +732,28 @@ static int pack_plan_impl(const char* who, const int64_t* batch_indices, int64_t
   const int64_t C = pack_chunk_size(E);
   const int nchunks = (int)cdiv(E, C);
   int* counts = reinterpret_cast<int*>(workspace);
-  if (clear) {
+  // Without ranks, sorted indices first (the wide check, its status words after the counts):
+  // the three launches then return at once.  The check also clears the error word.
+  int* status = nullptr;
+  const int n_status = (int)cdiv(E, (int64_t)PS_SORTED_EV);
+  if (rank == nullptr) {
+    status = counts + (int64_t)nchunks * B;
+    hipLaunchKernelGGL(pack_sorted_kernel, dim3((unsigned)n_status), dim3(PS_SORTED_EV), 0, stream, batch_indices,
+                       s_bidx, E, (int)B, offsets, identity ? nullptr : order, dst_rows, status,
+                       clear ? err_flag : nullptr);
+    CORTEX_CHECK_LAUNCH("pack_sorted_kernel");
+  } else if (clear) {
     hipLaunchKernelGGL(fill_i32_kernel, dim3(1), dim3(64), 0, stream, err_flag, (int64_t)1, 0);
     CORTEX_CHECK_LAUNCH("cortex_pack_plan(clear)");
   }
   hipLaunchKernelGGL(pack_count_kernel, dim3(nchunks), dim3(256), 0, stream, batch_indices, s_bidx, E, (int)B, C,
-                     counts, err_flag);
+                     counts, err_flag, status, n_status);
   CORTEX_CHECK_LAUNCH("pack_count_kernel");
-  hipLaunchKernelGGL(pack_scan_kernel, dim3(1), dim3(1024), 0, stream, counts, nchunks, (int)B, offsets, identity);
+  hipLaunchKernelGGL(pack_scan_kernel, dim3(1), dim3(1024), 0, stream, counts, nchunks, (int)B, offsets, identity,
+                     status, n_status);
   CORTEX_CHECK_LAUNCH("pack_scan_kernel");
   hipLaunchKernelGGL(pack_rank_kernel, dim3(nchunks), dim3(64), 0, stream, batch_indices, s_bidx, E, (int)B, C,
-                     counts, offsets, order, dst_rows, rank);
+                     counts, offsets, order, dst_rows, rank, status, n_status);
   CORTEX_CHECK_LAUNCH("pack_rank_kernel");
   return OK;
 }

@@ -50,9 +50,10 @@ const char* cortex_last_error(void);
  *                   clean without a separate fill launch).
  * workspace: at least cortex_pack_workspace_bytes(E, B) bytes of device memory.
  * Sorted batch indices (the collate order) are recognised on the device when rank is
- * null: up to 4096 events the check and the plan are one launch; above, the identity
- * plan is written by one launch over all events and the general plan runs only where
- * some 256-event range was not sorted or held an index out of range. */
+ * null: up to 4096 events the check and the plan are one launch; above (any E and B), the
+ * identity plan is written by one launch over all events, and the launches of the general
+ * plan that follow return at once unless some 256-event range was not sorted or held an
+ * index out of range. */
 int64_t cortex_pack_workspace_bytes(int64_t E, int64_t B);
 int cortex_pack_plan(const int64_t* batch_indices, int64_t s_bidx, int64_t E, int64_t B, int64_t* offsets,
                      int64_t* order, int64_t* dst_rows, int64_t* rank, void* workspace, int64_t workspace_bytes,

@@ -69,7 +69,8 @@ def test_invalid_arguments_return_status_and_message():
                                 None, 0, 0, 0, None, 4, None)
     assert rc == -1
     assert lib.cortex_pack_workspace_bytes(0, 4) == 0
-    assert lib.cortex_pack_workspace_bytes(5000, 32) == 5 * 32 * 4
+    # five 1024-event chunks of 32 counts, then one status word per 256 events
+    assert lib.cortex_pack_workspace_bytes(5000, 32) == (5 * 32 + 20) * 4
     rc = lib.cortex_pack_plan(None, 1, 10, 100000, None, None, None, None, None, 0, None, None, 0, None)
     assert rc == -1 and b"exceeds" in lib.cortex_last_error()
 

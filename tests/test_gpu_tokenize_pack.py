@@ -254,13 +254,27 @@ def _sorted_cases():
     cases["sorted_4096"] = (np.sort(rng.integers(0, 33, 4096)), 33)
     cases["sorted_4097"] = (np.sort(rng.integers(0, 33, 4097)), 40)
     cases["sorted_16447"] = (np.sort(rng.integers(0, 33, 16447)), 33)  # partial last wave of the wide check
+    # above 65536 events (or above 1024 samples) the general three-launch plan follows the wide
+    # check and returns at once when every range was sorted
+    cases["sorted_70000"] = (np.sort(rng.integers(0, 200, 70000)), 200)
+    b = np.sort(rng.integers(0, 200, 70000))
+    b[60000], b[60001] = b[60001], b[60000] - 1 if b[60000] > 0 else 1
+    cases["inversion_70000"] = (b, 200)
+    b = np.sort(rng.integers(0, 90, 66000))
+    b[65999] = 90
+    cases["out_of_range_tail_66000"] = (b, 90)
+    cases["sorted_b2000"] = (np.sort(rng.integers(0, 2000, 9000)), 2000)
+    b = np.sort(rng.integers(0, 2000, 9000))
+    b[0] = -3
+    cases["negative_first_b2000"] = (b, 2000)
     return cases
 
 
 @pytest.mark.parametrize("name", list(_sorted_cases()))
 def test_pack_plan_sorted_fast_path(name):
     """Sorted batch indices take the identity plan (checked inside the plan kernel up to 4096
-    events, by the wide pack_sorted_kernel above); anything else found
+    events, by the wide pack_sorted_kernel above, also ahead of the general three-launch plan
+    past 65536 events or 1024 samples); anything else found
     there -- an inversion, an index out of range -- falls back to the full plan.  Same
     results as the oracle either way, with and without ranks; with the identity flag, a
     sorted in-range plan sets it (order is then the identity by definition) and any other
