@@ -508,7 +508,7 @@ int launch(const GemmArgs& g, hipStream_t stream) {
 }
 
 using B128x128s2 = BTile<128, 128, 2, 2, 2>;
-using B256x128s2 = BTile<256, 128, 2, 4, 2>;
+using B256x128s3 = BTile<256, 128, 3, 4, 2>;
 using B256x256s2 = BTile<256, 256, 2, 4, 2>;
 using B256x192s2 = BTile<256, 192, 2, 4, 2>;
 using B128x128s2k2 = BTile<128, 128, 2, 2, 2, 2>;
@@ -1092,12 +1092,17 @@ int try_gemm_bf16(const GemmArgs& g, int x_dtype, int w_dtype, int w_layout, int
   const bool out_bf16 = g.out_dtype == DT_BF16;
   if (!out_bf16 && g.out_dtype != DT_F32) return 0;
   if (!aligned16(g.out) || g.ld_out % 8) return 0;
-  // Residual (fp32 in/out) GEMMs are memory bound: 128 x 128 tiles with K split over two wave
-  // groups (eight wavefronts per CU), at every grid size (measured against a three-stage
-  // pipelined kernel with an LDS-staged epilogue at B = 64 / 128 / 256: forward 1.524 / 2.99 /
-  // 6.20 ms there, 1.466 / 2.84 / 5.98 ms here)
+  // Residual (fp32 in/out) GEMMs are memory bound.  While 128 x 128 tiles give at most one
+  // workgroup per CU: those tiles with K split over two wave groups (eight wavefronts per CU).
+  // Larger grids (B >= 64 in the forward, the activation rows no longer in the infinity
+  // cache): 256 x 128 tiles with a three-stage ring (144 KiB), whose extra stage of lead covers
+  // the longer load latency and whose taller tile halves the weight refill per row.  Measured
+  // forward at B = 64 / 128 / 256: 1.467 / 2.816 / 5.93 ms with the K-split tiles, 1.393 /
+  // 2.647 / 5.42 ms with these.
   if (res) {
     if (g.act || g.K % 128) return 0;
+    if (!w8 && g.N % 128 == 0 && cdiv(g.M, 128) * cdiv(g.N, 128) > cu_count())
+      return launch<B256x128s3, ACT_NONE, true, float, bf16, bf16>(g, stream);
     return w8 ? launch<B128x128s2k2w, ACT_NONE, true, float, bf16, int8_t>(g, stream)
               : launch<B128x128s2k2, ACT_NONE, true, float, bf16, bf16>(g, stream);
   }
