@@ -22,6 +22,8 @@
 // LDS in one exchange.
 #include <hip/hip_runtime.h>
 
+#include <type_traits>
+
 #include "common.h"
 
 namespace cortex {
@@ -53,6 +55,10 @@ __device__ __forceinline__ void rl_wait_ahead(int ahead) {
 }
 
 __device__ __forceinline__ int rl_swz(int r) { return (r >> 1) & 7; }
+// int8 weight rows (64 bytes of K per row and step): the 16-byte chunk c of LDS row r holds
+// logical chunk c ^ rl_swz8(r), so the 16 rows of one fragment read fall on distinct
+// four-bank groups (the layout gemm_bf16.hip uses for the same rows)
+__device__ __forceinline__ int rl_swz8(int r) { return ((r >> 3) ^ (r >> 2)) & 3; }
 
 struct RowLnArgs {
   int64_t M, N, K;
@@ -75,10 +81,10 @@ struct RowLnArgs {
   float a_scale;       // int8 A rows: A_f = a_scale * A
 };
 
-// TW = int8_t with bf16 A rows: the QuantizedLinear int8 weight itself, loaded 8 bytes per
-// lane into registers one step ahead and widened exactly to bf16 into the LDS ring before
-// the step's barrier (lane (row r, chunk c): W[r, k0 + 8c .. +7] -> logical chunk c of LDS
-// row r), so the fragment reads are those of the bf16 weight.
+// TW = int8_t with bf16 A rows: the QuantizedLinear int8 weight itself, moved into the LDS ring
+// by the same direct-to-LDS transfers as bf16 rows (64 bytes of K per row and step, half the
+// bytes, so the ring may hold more stages), and each lane widens its 8-byte fragment exactly
+// to bf16 (every int8 value is a bf16 value) right before the MFMAs that use it.
 template <int BN, int S, bool Q8 = false, class TIN = bf16, class TW = TIN>
 __global__ __launch_bounds__(RL_THREADS) void gemm_rowln_kernel(RowLnArgs g) {
   using OP = Operand<TIN>;
@@ -86,14 +92,13 @@ __global__ __launch_bounds__(RL_THREADS) void gemm_rowln_kernel(RowLnArgs g) {
   constexpr int EPC = OP::EPC, BK = 8 * EPC;  // K elements per 16-byte chunk and per 128-byte LDS row
   constexpr int WN = BN / RL_WAVES;   // columns per wavefront
   constexpr int TM = RL_BM / 16, TN = WN / 16;
-  constexpr int A_STAGE = RL_BM * 128, W_STAGE = BN * 128;  // bytes
-  constexpr int WB = W_STAGE / 1024 / RL_WAVES;             // W transfers per wavefront and step
   constexpr bool WI8 = sizeof(TW) == 1 && sizeof(TIN) == 2;
-  constexpr int WL = WI8 ? BN / (8 * RL_WAVES) : 1;         // 8-byte int8 weight loads per lane and step
-  static_assert(!WI8 || S == 2, "int8 weights: two-stage ring");
-  constexpr int PER = 1 + (WI8 ? WL : WB);                   // + one A transfer (blocks shared 2:1)
+  constexpr int A_STAGE = RL_BM * 128, W_STAGE = BN * (WI8 ? 64 : 128);  // bytes
+  constexpr int WB = W_STAGE / 1024 / RL_WAVES;             // W transfers per wavefront and step
+  constexpr int PER = 1 + WB;                                // + one A transfer (blocks shared 2:1)
   constexpr int RING = S * (A_STAGE + W_STAGE);
   static_assert(A_STAGE == 4 * 1024 && W_STAGE % (1024 * RL_WAVES) == 0 && TN >= 1, "shape");
+  static_assert(RING <= 160 * 1024, "LDS");
   static_assert(PER * (S - 1) < 64, "vmcnt range");
   __shared__ __attribute__((aligned(1024))) unsigned char smem[RING];
 
@@ -111,12 +116,13 @@ __global__ __launch_bounds__(RL_THREADS) void gemm_rowln_kernel(RowLnArgs g) {
   const int ar = (wid & 3) * 8 + (lane >> 3);
   const TIN* a_src = reinterpret_cast<const TIN*>(g.x) + (int64_t)min(m0 + ar, M - 1) * g.ld_x +
                      ((lane & 7) ^ rl_swz(ar)) * EPC;
-  const TW* w_src[WI8 ? WL : WB];
+  const TW* w_src[WB];
   if constexpr (WI8) {
+    // lane i of block q writes LDS bytes [16 i, 16 i + 16): row 16 q + i / 4, stored chunk i % 4
 #pragma unroll
-    for (int i = 0; i < WL; ++i) {
-      const int r = (wid * WL + i) * 8 + (lane >> 3);
-      w_src[i] = reinterpret_cast<const TW*>(g.w) + (int64_t)r * g.ld_w + (lane & 7) * 8;
+    for (int i = 0; i < WB; ++i) {
+      const int r = (wid * WB + i) * 16 + (lane >> 2);
+      w_src[i] = reinterpret_cast<const TW*>(g.w) + (int64_t)r * g.ld_w + ((lane & 3) ^ rl_swz8(r)) * 16;
     }
   } else {
 #pragma unroll
@@ -128,30 +134,14 @@ __global__ __launch_bounds__(RL_THREADS) void gemm_rowln_kernel(RowLnArgs g) {
   auto a_stage = [&](int s) { return smem + s * A_STAGE; };
   auto w_stage = [&](int s) { return smem + S * A_STAGE + s * W_STAGE; };
   const int nk = K / BK;
-  uint2 wreg[WI8 ? WL : 1];  // int8 weight rows of the last issued step
   auto issue = [&](int kt) {
-    const int s = kt % S, k0 = kt * BK;
-    if constexpr (WI8) {
-#pragma unroll
-      for (int i = 0; i < WL; ++i) wreg[i] = *reinterpret_cast<const uint2*>(w_src[i] + k0);
-    }
+    const int s = kt % S, k0 = kt * BK;  // (K elements: bytes for the int8 rows)
     __builtin_amdgcn_global_load_lds(static_cast<const void*>(a_src + k0),
                                      static_cast<void*>(a_stage(s) + (wid & 3) * 1024), 16, 0, 0);
-    if constexpr (!WI8) {
 #pragma unroll
-      for (int i = 0; i < WB; ++i)
-        __builtin_amdgcn_global_load_lds(static_cast<const void*>(w_src[i] + k0),
-                                         static_cast<void*>(w_stage(s) + (wid * WB + i) * 1024), 16, 0, 0);
-    }
-  };
-  auto commit_w = [&](int s) {  // widen the registers into W stage s
-    if constexpr (WI8) {
-#pragma unroll
-      for (int i = 0; i < WL; ++i) {
-        const int r = (wid * WL + i) * 8 + (lane >> 3), c = lane & 7;
-        *reinterpret_cast<bf16x8*>(w_stage(s) + r * 128 + ((c ^ rl_swz(r)) << 4)) = widen_i8x8(wreg[i]);
-      }
-    }
+    for (int i = 0; i < WB; ++i)
+      __builtin_amdgcn_global_load_lds(static_cast<const void*>(w_src[i] + k0),
+                                       static_cast<void*>(w_stage(s) + (wid * WB + i) * 1024), 16, 0, 0);
   };
 
   typename OP::accum acc[TM][TN];
@@ -169,37 +159,49 @@ __global__ __launch_bounds__(RL_THREADS) void gemm_rowln_kernel(RowLnArgs g) {
 #pragma unroll
   for (int t = 0; t < TN; ++t) {
     const int r = wcol + t * 16 + fr;
-    w_off[t] = r * 128;
-    w_sw[t] = rl_swz(r);
+    w_off[t] = r * (WI8 ? 64 : 128);
+    w_sw[t] = WI8 ? rl_swz8(r) : rl_swz(r);
   }
-  auto read_frags = [&](int stage, int ks, frag (&af)[TM], frag (&wf)[TN]) {
+  // W fragments as read from LDS: bf16 fragments, or the raw 8 int8 bytes, widened right
+  // before their TM uses
+  typedef typename std::conditional<WI8, uint2, frag>::type wfrag;
+  auto read_frags = [&](int stage, int ks, frag (&af)[TM], wfrag (&wf)[TN]) {
     const unsigned char* as = a_stage(stage);
     const unsigned char* ws = w_stage(stage);
 #pragma unroll
     for (int t = 0; t < TM; ++t)
       af[t] = *reinterpret_cast<const frag*>(as + a_off[t] + (((ks * 4 + g4) ^ a_sw[t]) << 4));
+    if constexpr (WI8) {
+      // K [32 ks + 8 g4, +8) of the row: logical chunk 2 ks + g4 / 2, half g4 % 2
 #pragma unroll
-    for (int t = 0; t < TN; ++t)
-      wf[t] = *reinterpret_cast<const frag*>(ws + w_off[t] + (((ks * 4 + g4) ^ w_sw[t]) << 4));
+      for (int t = 0; t < TN; ++t)
+        wf[t] = *reinterpret_cast<const uint2*>(ws + w_off[t] + (((2 * ks + (g4 >> 1)) ^ w_sw[t]) << 4) +
+                                                ((g4 & 1) << 3));
+    } else {
+#pragma unroll
+      for (int t = 0; t < TN; ++t)
+        wf[t] = *reinterpret_cast<const frag*>(ws + w_off[t] + (((ks * 4 + g4) ^ w_sw[t]) << 4));
+    }
   };
-  auto mma = [&](const frag (&af)[TM], const frag (&wf)[TN]) {
+  auto mma = [&](const frag (&af)[TM], const wfrag (&wf)[TN]) {
+    if constexpr (WI8) {
 #pragma unroll
-    for (int i = 0; i < TM; ++i)
+      for (int j = 0; j < TN; ++j) {
+        const frag w = widen_i8x8(wf[j]);
 #pragma unroll
-      for (int j = 0; j < TN; ++j) acc[i][j] = OP::mma(wf[j], af[i], acc[i][j]);
+        for (int i = 0; i < TM; ++i) acc[i][j] = OP::mma(w, af[i], acc[i][j]);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = OP::mma(wf[j], af[i], acc[i][j]);
+    }
   };
 
-  if constexpr (WI8) {
-    issue(0);
-    rl_wait_vm<0>();
-    commit_w(0);
-    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): widened rows in LDS before the barrier
-    if (1 < nk) issue(1);
-  } else {
 #pragma unroll
-    for (int p = 0; p < S; ++p)
-      if (p < nk) issue(p);
-  }
+  for (int p = 0; p < S; ++p)
+    if (p < nk) issue(p);
   // The residual tile goes into registers right after the first ring stages: the first
   // MFMAs do not wait for it and its latency hides behind the main loop.  Its RV loads
   // sit behind the prologue's transfers in the wave's vmcnt (the scheduling barrier keeps
@@ -223,48 +225,30 @@ __global__ __launch_bounds__(RL_THREADS) void gemm_rowln_kernel(RowLnArgs g) {
     else
       rl_wait_ahead<PER, S, 0>(ahead);
   };
-  frag af0[TM], wf0[TN], af1[TM], wf1[TN];
-  if constexpr (!WI8) wait_step(0, S - 1);  // (int8 weights: step 0 landed before it was widened)
+  frag af0[TM], af1[TM];
+  wfrag wf0[TN], wf1[TN];
+  wait_step(0, S - 1);
   __builtin_amdgcn_s_barrier();
   read_frags(0, 0, af0, wf0);
   // One K step that hands over to the next (as in gemm_bf16.hip): the loop is peeled so that
   // no branch joins in front of an MFMA group, where the compiler would wait for the
   // fragment reads just issued, and each step first waits explicitly for the fragments read
   // after the previous barrier.
-  // `first`: step 0, whose successor's transfers were issued before the residual loads,
-  // which stay outstanding.
-  auto step = [&](int kt, auto refill, auto first) {
+  auto step = [&](int kt, auto refill) {
     const int st = kt % S;
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): sub-step 0's fragments
     read_frags(st, 1, af1, wf1);
     mma(af0, wf0);
-    if constexpr (WI8) {
-      // step kt+1: A transfer and weight registers
-      if constexpr (decltype(first)::value)
-        rl_wait_vm<RV>();
-      else
-        rl_wait_vm<0>();
-      commit_w((kt + 1) % S);
-    } else {
-      wait_step(kt + 1, kt + S - 1);
-    }
-    __builtin_amdgcn_s_waitcnt(0xC07F);  // this wave's reads of stage st (and W stores) done
+    wait_step(kt + 1, kt + S - 1);
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // this wave's reads of stage st done
     __builtin_amdgcn_s_barrier();        // all waves done with stage st; step kt+1 visible
     read_frags((kt + 1) % S, 0, af0, wf0);
     if constexpr (decltype(refill)::value) issue(kt + S);
     mma(af1, wf1);
   };
-  using yes = std::integral_constant<bool, true>;
-  using no = std::integral_constant<bool, false>;
   int kt = 0;
-  if constexpr (WI8) {
-    if (S < nk)
-      step(kt++, yes{}, yes{});
-    else if (1 < nk)
-      step(kt++, no{}, yes{});
-  }
-  for (; kt + S < nk; ++kt) step(kt, yes{}, no{});
-  for (; kt + 1 < nk; ++kt) step(kt, no{}, no{});
+  for (; kt + S < nk; ++kt) step(kt, std::integral_constant<bool, true>{});
+  for (; kt + 1 < nk; ++kt) step(kt, std::integral_constant<bool, false>{});
   __builtin_amdgcn_s_waitcnt(0xC07F);  // the last step
   read_frags((nk - 1) % S, 1, af1, wf1);
   mma(af0, wf0);
