@@ -71,6 +71,23 @@ __device__ __forceinline__ void lds_dma16_sbase(const void* base, uint32_t voff,
                : "memory", "m0");
 }
 
+// Direct-to-LDS transfer from a uniform base plus a 32-bit lane offset into the LDS address
+// m0 (wave-uniform: lane i writes m0 + SIZE * i), SIZE 16 (dwordx4) or 4 (dword).
+template <int SIZE>
+__device__ __forceinline__ void lds_dma_m0(const void* base, uint32_t voff, uint32_t m0) {
+  const uint64_t b = (uint64_t)(uintptr_t)base;
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(b >> 32));
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)b);
+  const uint64_t sb = ((uint64_t)hi << 32) | (uint64_t)lo;
+  const uint32_t m = __builtin_amdgcn_readfirstlane(m0);
+  if constexpr (SIZE == 16)
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sb), "s"(m)
+                 : "memory", "m0");
+  else
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1" ::"v"(voff), "s"(sb), "s"(m)
+                 : "memory", "m0");
+}
+
 // KS > 1 splits K over KS groups of WM x WN wavefronts, each streaming its own part of
 // K through its own LDS ring; the partial tiles are summed through LDS before the
 // epilogue.  This doubles the wavefronts per CU for narrow outputs (N = 512) without
@@ -530,6 +547,241 @@ int cu_count() {
   return v;
 }
 
+// ---------------------------------------------------------------------------------------
+// Persistent 256 x 256 tiles for bf16-output GEMMs past one wave of tiles (MLP-up with its
+// GELU and the kv projection at B >= 64; bf16 rows and bf16 weight rows, N % 256 == 0).
+//
+// One workgroup per CU walks its tiles in turn (the tiles of an XCD in contiguous order, so
+// the row panels stay shared in its L2).  When a tile's K loop is done, the workgroup first
+// issues the next tile's first ring stages and only then runs the epilogue: the cold operand
+// fetch of the next tile hides behind the GELU work, and the output stores drain while the
+// next tile's first K steps run.  Launched as separate workgroups, each tile would pay both.
+// The K loop, ring, swizzles and epilogue arithmetic are gemm_bf16_kernel's (B256x256s2,
+// interleaved W rows, 8 consecutive columns per lane; transfers from a uniform base plus a
+// 32-bit lane offset).  A tile's 256 column scales and biases travel into LDS with its first
+// stages (two buffers, by tile parity, since the next tile's arrive during this tile's
+// epilogue).  The epilogue issues exactly one 16-byte store per (row group, column group) and
+// lane -- rows past M store row M - 1's values again, computed from the clamped A rows, so the
+// duplicates are bit-identical -- so the first waits of the next tile count them exactly.
+template <int ACT>
+__global__ __launch_bounds__(512) void gemm_persist_kernel(GemmArgs g) {
+  using TL = BTile<256, 256, 2, 4, 2>;
+  using OP = Operand<bf16>;
+  typedef OP::frag frag;
+  constexpr int BM = TL::BM, BN = TL::BN, TM = TL::TM, TN = TL::TN, S = TL::STAGES;
+  constexpr int AB = TL::A_BLOCKS, WB = TL::W_BLOCKS, PER = TL::PER;
+  constexpr int NG = TN / 2;    // 8-column groups per lane
+  constexpr int NST = TM * NG;  // stores per lane and tile
+  static_assert(S == 2 && TL::KS == 1 && TL::WAVES == 8, "two-stage ring, one K group, 8 wavefronts");
+  static_assert(PER + NST < 64, "vmcnt range");
+  constexpr int PAR = TL::LDS;  // column parameters: [parity][scale 256 | bias 256] floats
+  __shared__ __attribute__((aligned(1024))) unsigned char smem[TL::LDS + 2 * 2 * BN * 4];
+
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int wm = wid / TL::WN, wn = wid % TL::WN;
+  const int M = (int)g.M, K = (int)g.K;
+  const int gx = (int)(g.N / BN), ntiles = (int)cdiv(g.M, (int64_t)BM) * gx;
+  // tile order: XCD x (workgroups x, x + 8, ...) owns the contiguous eighth of the tiles
+  const int G = gridDim.x;
+  int t0, tstep, tend;
+  if ((ntiles & 7) == 0 && (G & 7) == 0) {
+    const int per_xcd = ntiles >> 3;
+    t0 = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
+    tstep = G >> 3;
+    tend = (blockIdx.x & 7) * per_xcd + per_xcd;
+  } else {
+    t0 = blockIdx.x;
+    tstep = G;
+    tend = ntiles;
+  }
+  const bf16* const A = reinterpret_cast<const bf16*>(g.x);
+  const bf16* const W = reinterpret_cast<const bf16*>(g.w);
+  const float* const scale = g.w_scale;
+  const float* const bias = reinterpret_cast<const float*>(g.bias);
+  // the LDS address of smem (wave-uniform) and of each wavefront's transfer blocks
+  const uint32_t lds0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)smem);
+  const int wu = __builtin_amdgcn_readfirstlane(wid);
+  auto a_stage = [&](int s) __attribute__((always_inline)) { return smem + s * TL::A_STAGE; };
+  auto w_stage = [&](int s) __attribute__((always_inline)) { return smem + S * TL::A_STAGE + s * TL::W_STAGE; };
+  auto params = [&](int t) __attribute__((always_inline)) { return reinterpret_cast<float*>(smem + PAR) + (t & 1) * 2 * BN; };
+  const int nk = K / TL::BK;
+
+  // The transfer offsets (bytes from the operand bases; the host keeps both below 4 GiB) are
+  // computed where the transfers are issued, from the tile's row and column origin, so that
+  // no per-tile offsets stay live through the K loop and the epilogue.
+  const int ldx = (int)g.ld_x, ldw = (int)g.ld_w;
+  int m0c = 0, n0c = 0;  // origin of the tile whose transfers issue() sends
+  auto issue = [&](int kt) __attribute__((always_inline)) {
+    const int s = kt % S, k0 = kt * TL::BK;
+    // the lane id through an instruction the compiler may not move: the offsets below are
+    // recomputed at each issue instead of being kept live (or spilled) between issues
+    int lane;
+    asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(lane));
+#pragma unroll
+    for (int i = 0; i < AB; ++i) {
+      const int r = (wid * AB + i) * 8 + (lane >> 3);
+      const uint32_t vo = (uint32_t)(min(m0c + r, M - 1) * ldx + ((lane & 7) ^ swz_a(r)) * 8) * 2u;
+      lds_dma_m0<16>(A + k0, vo, lds0 + s * TL::A_STAGE + (wu * AB + i) * 1024);
+    }
+#pragma unroll
+    for (int i = 0; i < WB; ++i) {
+      const int r = (wid * WB + i) * 8 + (lane >> 3);
+      const uint32_t vo = (uint32_t)((n0c + r) * ldw + ((lane & 7) ^ swz_w(r)) * 8) * 2u;
+      lds_dma_m0<16>(W + k0, vo, lds0 + S * TL::A_STAGE + s * TL::W_STAGE + (wu * WB + i) * 1024);
+    }
+  };
+  // a tile's first stages, its column parameters ahead of them (4 bytes per lane: wavefronts
+  // 0-3 the 256 scales, 4-7 the biases; null ones are never read)
+  auto prologue = [&](int t) __attribute__((always_inline)) {
+    m0c = (t / gx) * BM;
+    n0c = (t % gx) * BN;
+    const int n0 = n0c;
+    const float* src = wu < 4 ? scale : bias;
+    if (src)
+      lds_dma_m0<4>(src + n0 + (wu & 3) * 64, (uint32_t)(threadIdx.x & 63) * 4u,
+                    lds0 + PAR + ((t & 1) * 2 * BN + (wu < 4 ? 0 : BN) + (wu & 3) * 64) * 4);
+#pragma unroll
+    for (int p = 0; p < S; ++p)
+      if (p < nk) issue(p);
+  };
+
+  const int fr = lane & 15, g4 = lane >> 4;
+  const int wrow = wm * (BM / TL::WM), wcol = wn * (BN / TL::WN);
+  // Fragment reads: fragment t of A is row wrow + 16 t + fr and of W row wcol + wrow_of(t / 2,
+  // t % 2, fr); their chunk swizzles depend on fr only (the tile offsets are multiples of 16
+  // rows), so each sub-step's reads are one per-lane address plus compile-time offsets.
+  const int a_x0 = (wrow + fr) * 128, w_x0 = (wcol + wrow_of(0, 0, fr)) * 128;
+  const int a_sw0 = swz_a(fr), w_sw0 = swz_w(wrow_of(0, 0, fr));
+  auto read_frags = [&](int stage, int ks, frag (&af)[TM], frag (&wf)[TN]) __attribute__((always_inline)) {
+    const unsigned char* as = a_stage(stage) + a_x0 + (((ks * 4 + g4) ^ a_sw0) << 4);
+    const unsigned char* ws = w_stage(stage) + w_x0 + (((ks * 4 + g4) ^ w_sw0) << 4);
+#pragma unroll
+    for (int t = 0; t < TM; ++t) af[t] = *reinterpret_cast<const frag*>(as + t * 16 * 128);
+#pragma unroll
+    for (int t = 0; t < TN; ++t)
+      wf[t] = *reinterpret_cast<const frag*>(ws + (wrow_of(t >> 1, t & 1, 0)) * 128);
+  };
+  OP::accum acc[TM][TN];
+  auto mma = [&](const frag (&af)[TM], const frag (&wf)[TN]) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j) acc[i][j] = OP::mma(wf[j], af[i], acc[i][j]);
+  };
+  bf16* const out = reinterpret_cast<bf16*>(g.out);
+
+  frag af0[TM], af1[TM], wf0[TN], wf1[TN];
+  // One K step handing over to the next, gemm_bf16_kernel's; `first_x`: step 0 of a tile whose
+  // predecessor's NST epilogue stores were issued after this tile's first stages
+  auto step = [&](int kt, auto refill, bool first_x) __attribute__((always_inline)) {
+    const int st = kt % S;
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): sub-step 0's fragments
+    read_frags(st, 1, af1, wf1);
+    __builtin_amdgcn_sched_barrier(0);
+    mma(af0, wf0);
+    __builtin_amdgcn_sched_barrier(0);
+    // step kt + 1 landed: issued with the tile's first stages (only the stores are newer) or
+    // in step kt - 1 (nothing newer)
+    if (first_x)
+      wait_vm<NST>();
+    else
+      wait_vm<0>();
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    __builtin_amdgcn_s_barrier();
+    read_frags((kt + 1) % S, 0, af0, wf0);
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (decltype(refill)::value) issue(kt + S);
+    mma(af1, wf1);
+  };
+
+  // tile t's epilogue from registers and its column parameters in LDS: one store per (row
+  // group, column group) and lane
+  auto epilogue = [&](int t) __attribute__((always_inline)) {
+    const int m0 = (t / gx) * BM, n0 = (t % gx) * BN;
+    const float* sp = params(t);
+#pragma unroll
+    for (int p = 0; p < NG; ++p) {
+      const int c = wcol + 32 * p + 8 * g4;  // column inside the tile
+      float sc[8], bi[8];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const float4 s4 = *reinterpret_cast<const float4*>(sp + c + 4 * h);
+        const float4 b4 = *reinterpret_cast<const float4*>(sp + BN + c + 4 * h);
+        sc[4 * h] = scale ? s4.x : 1.f; sc[4 * h + 1] = scale ? s4.y : 1.f;
+        sc[4 * h + 2] = scale ? s4.z : 1.f; sc[4 * h + 3] = scale ? s4.w : 1.f;
+        bi[4 * h] = bias ? b4.x : 0.f; bi[4 * h + 1] = bias ? b4.y : 0.f;
+        bi[4 * h + 2] = bias ? b4.z : 0.f; bi[4 * h + 3] = bias ? b4.w : 0.f;
+      }
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        const int m = min(m0 + wrow + i * 16 + fr, M - 1);
+        bf16x8 o;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          float v0 = acc[i][2 * p][r] * sc[r] + bi[r];
+          float v1 = acc[i][2 * p + 1][r] * sc[4 + r] + bi[4 + r];
+          if constexpr (ACT == ACT_GELU) {
+            v0 = gelu_erf_bf16out(v0);
+            v1 = gelu_erf_bf16out(v1);
+          }
+          o[r] = (bf16)v0;
+          o[4 + r] = (bf16)v1;
+        }
+        *reinterpret_cast<bf16x8*>(out + (int64_t)m * g.ld_out + n0 + c) = o;
+      }
+    }
+  };
+
+  if (t0 >= tend) return;
+  prologue(t0);
+  bool after = false;  // the previous tile's epilogue stores are still counted by vmcnt
+  for (int t = t0;; t += tstep) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j) acc[i][j] = (OP::accum){0, 0, 0, 0};
+    // step 0 landed (and the column parameters, issued before it)
+    if (after) {
+      if (nk > 1)
+        wait_vm<PER + NST>();
+      else
+        wait_vm<NST>();
+    } else {
+      if (nk > 1)
+        wait_vm<PER>();
+      else
+        wait_vm<0>();
+    }
+    __builtin_amdgcn_s_barrier();
+    read_frags(0, 0, af0, wf0);
+    int kt = 0;
+    for (; kt + S < nk; ++kt) step(kt, std::integral_constant<bool, true>{}, after && kt == 0);
+    for (; kt + 1 < nk; ++kt) step(kt, std::integral_constant<bool, false>{}, after && kt == 0);
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // the last step
+    read_frags((nk - 1) % S, 1, af1, wf1);
+    mma(af0, wf0);
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    mma(af1, wf1);
+    const int next = t + tstep;
+    __builtin_amdgcn_s_barrier();  // every wave is done with the ring: the next tile may refill it
+    if (next < tend) prologue(next);
+    epilogue(t);
+    if (next >= tend) break;
+    after = true;
+  }
+}
+
+template <int ACT>
+int launch_persist(const GemmArgs& g, hipStream_t stream) {
+  const int64_t ntiles = cdiv(g.M, 256) * (g.N / 256);
+  // 32-bit transfer offsets (the scalar-base form) address both operands
+  if (g.M * g.ld_x * 2 >= (1LL << 32) || g.N * g.ld_w * 2 >= (1LL << 32) || ntiles > 0x7fffffffLL) return 0;
+  const int G = (int)std::min<int64_t>(ntiles, cu_count() & ~7);
+  hipLaunchKernelGGL((gemm_persist_kernel<ACT>), dim3((unsigned)G), dim3(512), 0, stream, g);
+  CORTEX_CHECK_LAUNCH("gemm_persist_kernel");
+  return 1;
+}
+
 // Tile by shape: 256-row tiles halve the operand traffic per MFMA, so take the widest tile
 // that still fills (nearly) every CU once, else 128 x 128 (two workgroups per CU).
 enum TileChoice { T128 = 0, T256 = 4, T192 = 6, T128_K2 = 7 };
@@ -551,7 +803,13 @@ int dispatch(const GemmArgs& g, hipStream_t stream) {
                                        : launch<B128x128s2, ACT, RES, TOUT, bf16, TW>(g, stream);
   } else {
     switch (wide_tile(g, true)) {
-      case T256: return launch<B256x256s2, ACT, RES, TOUT>(g, stream);
+      case T256:
+        // past one wave of 256 x 256 tiles, bf16 out: persistent tiles (see gemm_persist_kernel)
+        if constexpr (!RES && sizeof(TOUT) == 2) {
+          if (g.N % 256 == 0 && cdiv(g.M, 256) * (g.N / 256) > cu_count() && cu_count() >= 8)
+            return launch_persist<ACT>(g, stream);
+        }
+        return launch<B256x256s2, ACT, RES, TOUT>(g, stream);
       case T192: return launch<B256x192s2, ACT, RES, TOUT>(g, stream);
       default: return launch<B128x128s2, ACT, RES, TOUT>(g, stream);
     }
