@@ -56,23 +56,10 @@ __device__ __forceinline__ bf16x2_t pair_of(const bf16x8& v, int d) {
   }
 }
 
-// Direct-to-LDS transfer of 16 bytes per lane from a uniform base plus a 32-bit lane offset
-// (global_load_lds_dwordx4 in its scalar-base form: one VGPR per transfer instead of a 64-bit
-// address).  LDS destination lds_dst + 16 * lane; the caller's vmcnt waits order the reads.
-__device__ __forceinline__ void lds_dma16_sbase(const void* base, uint32_t voff, void* lds_dst) {
-  const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds_dst);
-  const uint64_t b = (uint64_t)(uintptr_t)base;
-  // (readfirstlane returns int: each half goes through uint32_t, or the low half would
-  // sign-extend into the high one)
-  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(b >> 32));
-  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)b);
-  const uint64_t sb = ((uint64_t)hi << 32) | (uint64_t)lo;
-  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sb), "s"(m0)
-               : "memory", "m0");
-}
-
-// Direct-to-LDS transfer from a uniform base plus a 32-bit lane offset into the LDS address
-// m0 (wave-uniform: lane i writes m0 + SIZE * i), SIZE 16 (dwordx4) or 4 (dword).
+// Direct-to-LDS transfer from a uniform base plus a 32-bit lane offset (global_load_lds in its
+// scalar-base form: one VGPR per transfer instead of a 64-bit address) into the LDS address m0
+// (wave-uniform: lane i writes m0 + SIZE * i), SIZE 16 (dwordx4) or 4 (dword).  The caller's
+// vmcnt waits order the reads.
 template <int SIZE>
 __device__ __forceinline__ void lds_dma_m0(const void* base, uint32_t voff, uint32_t m0) {
   const uint64_t b = (uint64_t)(uintptr_t)base;
@@ -213,12 +200,14 @@ __global__ __launch_bounds__(TL::THREADS) void gemm_bf16_kernel(GemmArgs g) {
                                          static_cast<void*>(w_stage(s) + (wid * W8B + i) * 1024), 16, 0, 0);
     }
     if constexpr (O32) {
-      const unsigned char* ab = reinterpret_cast<const unsigned char*>(A + k0);
-      const unsigned char* wb = reinterpret_cast<const unsigned char*>(W + k0);
+      // LDS destinations as wave-uniform 32-bit addresses (no per-lane generic pointers)
+      const uint32_t ring0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)ring);
+      const int wu = __builtin_amdgcn_readfirstlane(wid);
 #pragma unroll
-      for (int i = 0; i < AB; ++i) lds_dma16_sbase(ab, a_vo[i], a_stage(s) + (wid * AB + i) * 1024);
+      for (int i = 0; i < AB; ++i) lds_dma_m0<16>(A + k0, a_vo[i], ring0 + s * TL::A_STAGE + (wu * AB + i) * 1024);
 #pragma unroll
-      for (int i = 0; i < WB; ++i) lds_dma16_sbase(wb, w_vo[i], w_stage(s) + (wid * WB + i) * 1024);
+      for (int i = 0; i < WB; ++i)
+        lds_dma_m0<16>(W + k0, w_vo[i], ring0 + S * TL::A_STAGE + s * W_STAGE + (wu * WB + i) * 1024);
       return;
     }
 #pragma unroll
