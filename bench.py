@@ -722,20 +722,24 @@ def _time_captured(model, dev, inputs, reps: int = 50) -> tuple[float, torch.Ten
 
 
 def weights_and_modes(model, dev, inputs, reference: torch.Tensor) -> dict:
-    """Resident weight bytes of the default forward (INT8 weights + their bf16 execution images)
-    and of the widen mode (INT8 weights streamed and widened on chip, no images), with the widen
-    mode's time; and the float32-compute forward (the reference's own arithmetic: fp32
+    """Resident weight bytes of the default forward (INT8 weights + their bf16 execution images),
+    of the widen mode (INT8 weights streamed and widened on chip, no images) and of the window
+    mode (INT8 weights + two bf16 windows filled by riders of the row kernels), with each mode's
+    time; and the float32-compute forward (the reference's own arithmetic: fp32
     activations, INT8 weights dequantised) on the same weights and events."""
     from cortex.models import CortexModel, _layers
     from cortex.models.config import CORTEX_S, CortexConfig
 
     wb = _layers.resident_weight_bytes(model)
     prev = _layers.INT8_WEIGHTS
-    _layers.INT8_WEIGHTS = "widen"
     try:
+        _layers.INT8_WEIGHTS = "widen"
         sec_w, out_w = _time_captured(model, dev, inputs)
+        _layers.INT8_WEIGHTS = "window"
+        sec_v, out_v = _time_captured(model, dev, inputs)
     finally:
         _layers.INT8_WEIGHTS = prev
+    win_bytes = _layers.resident_weight_bytes(model)["bf16_windows"]
     res = {"resident_weight_bytes": wb["total"], "int8_weight_bytes": wb["int8_weights"],
            "bf16_image_bytes": wb["bf16_images"],
            "widen": {"resident_weight_bytes": wb["parameters_and_buffers"], "ms_per_forward": round(sec_w * 1e3, 4),
@@ -743,6 +747,12 @@ def weights_and_modes(model, dev, inputs, reference: torch.Tensor) -> dict:
                      "max_abs_diff_vs_default": float((out_w - reference).abs().max()),
                      "note": "CORTEX_INT8_WEIGHTS=widen: every kernel reads the int8 weights and widens them "
                              "on chip; the default keeps bf16 images because they were measured faster"},
+           "window": {"resident_weight_bytes": wb["parameters_and_buffers"] + win_bytes, "bf16_window_bytes": win_bytes,
+                      "ms_per_forward": round(sec_v * 1e3, 4), "samples_per_s": round(B_MAIN / sec_v, 1),
+                      "max_abs_diff_vs_default": float((out_v - reference).abs().max()),
+                      "note": "CORTEX_INT8_WEIGHTS=window: int8 weights resident; each weight group widened into "
+                              "a shared bf16 window by extra workgroups of the row kernel launched just before "
+                              "it (tokenizer + LayerNorm, then each block's LayerNorm rows)"},
            "reference_int8_bytes_note": "the reference's INT8 model holds 27.8 MB (benchmarks/quantization/"
                                         "results.md:15-18)"}
     torch.manual_seed(0)

@@ -9,6 +9,7 @@ synchronises the host.
 
 from __future__ import annotations
 
+import ctypes
 import math
 import os
 from collections import OrderedDict
@@ -110,12 +111,46 @@ def tokenize(neuron_emb, time_emb, value_emb, neuron_ids, time_bins, values, *, 
     return (out, mask) if padded else out
 
 
+WIDEN_MAX = 8  # arrays per widening rider (WR_MAX in the kernels)
+
+
+def _widen_args(pairs, dev) -> tuple:
+    """``(n, src, dst, count)`` C arrays of the (int8 source, bf16 destination) pairs of a widening
+    rider: contiguous tensors of equal element counts (multiples of 16) on ``dev``."""
+    pairs = list(pairs)
+    if len(pairs) > WIDEN_MAX:
+        raise ValueError(f"at most {WIDEN_MAX} arrays widen in one launch (got {len(pairs)})")
+    for src, dst in pairs:
+        if src.dtype != torch.int8 or dst.dtype != torch.bfloat16:
+            raise ValueError("widening takes int8 sources and bf16 destinations")
+        if src.numel() != dst.numel() or src.numel() % 16 or not (src.is_contiguous() and dst.is_contiguous()):
+            raise ValueError("widening needs contiguous arrays of equal size, a multiple of 16 elements")
+        if src.device != dev or dst.device != dev:
+            raise RuntimeError("widening arrays must be on the launching device")
+    n = len(pairs)
+    src = (ctypes.c_void_p * max(n, 1))(*[p[0].data_ptr() for p in pairs])
+    dst = (ctypes.c_void_p * max(n, 1))(*[p[1].data_ptr() for p in pairs])
+    cnt = (ctypes.c_int64 * max(n, 1))(*[p[0].numel() for p in pairs])
+    return n, src, dst, cnt
+
+
+def widen_int8(pairs) -> None:
+    """``dst.copy_(src)`` (int8 -> bf16, exact) for each ``(src, dst)`` pair in one launch
+    (``cortex_widen_int8``)."""
+    pairs = list(pairs)
+    if not pairs:
+        return
+    dev = nat.require_gpu(*[t for p in pairs for t in p], what="widen_int8")
+    nat.call("cortex_widen_int8", *_widen_args(pairs, dev), nat.stream_of(dev))
+
+
 def tokenize_ln(neuron_emb, time_emb, value_emb, neuron_ids, time_bins, values, ln, *, order=None,
-                csr_offsets=None, err=None, out=None, identity=None) -> torch.Tensor:
+                csr_offsets=None, err=None, out=None, identity=None, widen=None) -> torch.Tensor:
     """``LN((N[nid] + T[tb]) + V[val])`` as bf16 CSR rows (one launch, fp32 tokens never stored).
 
     ``ln`` is ``(weight, bias, eps)``; rows follow ``order`` (the pack plan, with its identity
-    flag when it has one) and rows past ``csr_offsets[B]`` come out as ``LN(0)``."""
+    flag when it has one) and rows past ``csr_offsets[B]`` come out as ``LN(0)``.  ``widen``:
+    (int8, bf16) weight pairs widened by extra workgroups of the same launch (``widen_int8``)."""
     dev = nat.require_gpu(neuron_emb, time_emb, value_emb, neuron_ids, time_bins, values, order, err,
                           what="tokenize_ln")
     for t in (neuron_emb, time_emb, value_emb):
@@ -125,13 +160,16 @@ def tokenize_ln(neuron_emb, time_emb, value_emb, neuron_ids, time_bins, values, 
     g, b, eps = ln
     if out is None:
         out = torch.empty((E, D), dtype=torch.bfloat16, device=dev)
-    nat.call("cortex_tokenize_ln", D, nat.ptr(neuron_emb), neuron_emb.shape[0], neuron_emb.stride(0),
-             nat.ptr(time_emb), time_emb.shape[0], time_emb.stride(0), nat.ptr(value_emb), value_emb.shape[0],
-             value_emb.stride(0), nat.ptr(neuron_ids), neuron_ids.stride(0) if E else 1, nat.ptr(time_bins),
-             time_bins.stride(0) if E else 1, nat.ptr(values), values.stride(0) if E else 1, E, nat.ptr(order),
-             nat.ptr(identity), _end_ptr(csr_offsets), nat.ptr(g), nat.ptr(b), float(eps), nat.ptr(out),
-             out.stride(0),
-             nat.ptr(err), nat.stream_of(dev))
+    args = (D, nat.ptr(neuron_emb), neuron_emb.shape[0], neuron_emb.stride(0),
+            nat.ptr(time_emb), time_emb.shape[0], time_emb.stride(0), nat.ptr(value_emb), value_emb.shape[0],
+            value_emb.stride(0), nat.ptr(neuron_ids), neuron_ids.stride(0) if E else 1, nat.ptr(time_bins),
+            time_bins.stride(0) if E else 1, nat.ptr(values), values.stride(0) if E else 1, E, nat.ptr(order),
+            nat.ptr(identity), _end_ptr(csr_offsets), nat.ptr(g), nat.ptr(b), float(eps), nat.ptr(out),
+            out.stride(0), nat.ptr(err))
+    if widen:
+        nat.call("cortex_tokenize_ln_widen", *args, *_widen_args(widen, dev), nat.stream_of(dev))
+    else:
+        nat.call("cortex_tokenize_ln", *args, nat.stream_of(dev))
     return out
 
 
@@ -232,10 +270,11 @@ def transpose_bf16(w: torch.Tensor) -> torch.Tensor:
     return out
 
 
-def ln_rows(x: torch.Tensor, ln1, ln2=None, out_bf16: bool = True, out_f32: bool = False):
+def ln_rows(x: torch.Tensor, ln1, ln2=None, out_bf16: bool = True, out_f32: bool = False, widen=None):
     """LayerNorm over rows of fp32 ``x`` (K in {256, 512, 768, 1024}); ``ln1``/``ln2``
     are ``(weight, bias, eps)`` triples (``ln2`` applied after ``ln1`` when given).
-    Returns the bf16 and/or fp32 result(s)."""
+    Returns the bf16 and/or fp32 result(s).  ``widen``: (int8, bf16) weight pairs widened by
+    extra workgroups of the same launch (``widen_int8``)."""
     dev = nat.require_gpu(x, what="ln_rows")
     x2 = _row_major_2d(x.reshape(-1, x.shape[-1]))
     M, K = x2.shape
@@ -243,8 +282,12 @@ def ln_rows(x: torch.Tensor, ln1, ln2=None, out_bf16: bool = True, out_f32: bool
     of = torch.empty((M, K), dtype=torch.float32, device=dev) if out_f32 else None
     g1, b1, e1 = ln1
     g2, b2, e2 = ln2 if ln2 is not None else (None, None, 0.0)
-    nat.call("cortex_ln_rows", M, K, nat.ptr(x2), x2.stride(0) if M > 1 else K, nat.ptr(g1), nat.ptr(b1),
-             float(e1), nat.ptr(g2), nat.ptr(b2), float(e2), nat.ptr(ob), K, nat.ptr(of), K, nat.stream_of(dev))
+    args = (M, K, nat.ptr(x2), x2.stride(0) if M > 1 else K, nat.ptr(g1), nat.ptr(b1), float(e1), nat.ptr(g2),
+            nat.ptr(b2), float(e2), nat.ptr(ob), K, nat.ptr(of), K)
+    if widen:
+        nat.call("cortex_ln_rows_widen", *args, *_widen_args(widen, dev), nat.stream_of(dev))
+    else:
+        nat.call("cortex_ln_rows", *args, nat.stream_of(dev))
     if out_bf16 and out_f32:
         return ob, of
     return ob if out_bf16 else of

@@ -13,6 +13,12 @@ bf16 compute (the default):
     QKV projection + attention, the residual linear + LayerNorm) streams the int8
     weight and widens it on chip, bit-identical results with a third of the resident
     weight bytes, at some cost in time (the images are the measured-faster default).
+    ``CORTEX_INT8_WEIGHTS=window`` keeps only the int8 weights resident as well, plus one
+    shared bf16 window per weight group (the cross-attention block; every self-attention
+    block in turn): a group is widened into its window by extra workgroups of the row kernel
+    that feeds it (the tokenizer + LayerNorm for the cross-attention and the first block,
+    each block's own LayerNorm rows after that), so the GEMMs run on bf16 weights at the
+    image speed and no launch is added (``WeightWindow``).
     For a float nn.Linear the image is the weight rounded to bf16, as ``F.linear`` on
     bf16 inputs would use it.
 fp32 compute: int8 or fp32 weights, fp32 operands, fused norm prologue.
@@ -38,10 +44,113 @@ def linear_weights(lin: nn.Module) -> dict:
     return {"weight": lin.weight, "bias": lin.bias}
 
 
+class WeightWindow:
+    """bf16 windows for INT8-resident weights (``CORTEX_INT8_WEIGHTS=window``).
+
+    Each region is one bf16 buffer that the QuantizedLinears of several groups (modules whose
+    linears run together) share in turn: the group last widened into it is resident.  The
+    forward hands a group's ``pairs`` (int8 weight, bf16 view) to the row kernel launched just
+    before the group runs, which widens them in extra workgroups; a linear of a group that is
+    not resident when its weights are asked for is widened on a launch of its own first, so
+    every path stays correct.  The resident set is tracked on the host in launch order (graph
+    capture records the same sequence); forwards that share a model must run on one stream,
+    as its activation buffers already require."""
+
+    def __init__(self, regions: dict, device: torch.device) -> None:
+        # regions: name -> [(owner module, [QuantizedLinear, ...]), ...]
+        self._views = {}      # id(linear) -> bf16 (N, K) view of its region
+        self._owner = {}      # id(linear) -> (region, owner)
+        self._pairs = {}      # id(owner) -> [(int8, view), ...]
+        self._linears = {}    # id(owner) -> [linear, ...]
+        self._held = {}       # region -> (id(owner), version key) resident now
+        self.bytes = 0
+        for region, groups in regions.items():
+            size = max(sum(l.weight_int8.numel() for l in lins) for _, lins in groups)
+            buf = torch.empty(size, dtype=torch.bfloat16, device=device)
+            self.bytes += buf.numel() * buf.element_size()
+            for owner, lins in groups:
+                off, pairs = 0, []
+                for lin in lins:
+                    q = lin.weight_int8
+                    view = buf[off:off + q.numel()].view(q.shape)
+                    off += q.numel()
+                    self._views[id(lin)] = view
+                    self._owner[id(lin)] = (region, owner)
+                    pairs.append((q, view))
+                    lin.__dict__["_cortex_window"] = self
+                self._pairs[id(owner)] = pairs
+                self._linears[id(owner)] = lins
+                owner.__dict__["_cortex_window"] = self
+
+    def _key(self, owner) -> tuple:
+        return tuple((l.weight_int8.data_ptr(), l.weight_int8._version) for l in self._linears[id(owner)])
+
+    def reset(self) -> None:
+        """Nothing resident: a new forward widens every group it reads."""
+        self._held.clear()
+
+    def take(self, owner) -> list:
+        """The (int8, bf16 view) pairs of ``owner``'s group for a rider launched now, which makes
+        it resident; empty when it already is."""
+        if owner is None or id(owner) not in self._pairs:
+            return []
+        region = self._owner[id(self._linears[id(owner)][0])][0]
+        key = (id(owner), self._key(owner))
+        if self._held.get(region) == key:
+            return []
+        self._held[region] = key
+        return list(self._pairs[id(owner)])
+
+    def view(self, lin: nn.Module) -> torch.Tensor:
+        """bf16 weight of ``lin``, its group widened first on a launch of its own unless resident."""
+        pairs = self.take(self._owner[id(lin)][1])
+        if pairs:
+            ops.widen_int8(pairs)
+        return self._views[id(lin)]
+
+
+def weight_window(owner: nn.Module) -> WeightWindow | None:
+    """The window that ``owner``'s group belongs to, in window mode."""
+    return owner.__dict__.get("_cortex_window") if INT8_WEIGHTS == "window" else None
+
+
+def rider(*owners) -> list | None:
+    """The weight pairs that the next row kernel should widen so that ``owners``' groups are
+    resident in their window (None outside window mode or when nothing is to widen)."""
+    pairs = []
+    for o in owners:
+        win = weight_window(o) if o is not None else None
+        if win is not None:
+            pairs += win.take(o)
+    return pairs or None
+
+
+def build_weight_window(regions: dict, device: torch.device) -> WeightWindow | None:
+    """A ``WeightWindow`` over the QuantizedLinears of ``regions`` (name -> [(owner, [linear])])
+    in window mode, None otherwise or when a group holds no int8 weight."""
+    if INT8_WEIGHTS != "window":
+        return None
+    groups = {r: [(o, [l for l in lins if hasattr(l, "weight_int8")]) for o, lins in g] for r, g in regions.items()}
+    groups = {r: [(o, lins) for o, lins in g if lins] for r, g in groups.items()}
+    groups = {r: g for r, g in groups.items() if g}
+    if not groups:
+        return None
+    for g in groups.values():
+        for _, lins in g:
+            for lin in lins:
+                q = lin.weight_int8
+                if not q.is_contiguous() or q.numel() % 16 or q.device != device:
+                    return None
+    return WeightWindow(groups, device)
+
+
 def exec_weights(lin: nn.Module, compute: torch.dtype) -> dict:
     """Weight arguments for the GEMM at ``compute`` precision (bf16 image when bf16)."""
     quant = hasattr(lin, "weight_int8")
-    if compute != torch.bfloat16 or (quant and INT8_WEIGHTS == "widen"):
+    if compute != torch.bfloat16 or (quant and INT8_WEIGHTS != "image"):
+        win = lin.__dict__.get("_cortex_window") if compute == torch.bfloat16 and INT8_WEIGHTS == "window" else None
+        if win is not None:
+            return {"weight": win.view(lin), "weight_scale": lin.weight_scale, "bias": lin.bias}
         return linear_weights(lin)
     src = lin.weight_int8 if quant else lin.weight
     key = (src.data_ptr(), src._version, tuple(src.shape), src.device)
@@ -58,8 +167,12 @@ def exec_weights(lin: nn.Module, compute: torch.dtype) -> dict:
 def fused_weight(lin: nn.Module) -> tuple:
     """``(weight, weight_scale, bias)`` for the fused bf16 kernels (QKV + attention, residual
     linear + LayerNorm): the bf16 image, or with ``CORTEX_INT8_WEIGHTS=widen`` the int8 weight
-    itself, which those kernels widen on chip."""
-    if hasattr(lin, "weight_int8") and INT8_WEIGHTS == "widen":
+    itself, which those kernels widen on chip (with ``window``, the bf16 window when the linear
+    has one)."""
+    if hasattr(lin, "weight_int8") and INT8_WEIGHTS != "image":
+        win = lin.__dict__.get("_cortex_window") if INT8_WEIGHTS == "window" else None
+        if win is not None:
+            return win.view(lin), lin.weight_scale, lin.bias
         return lin.weight_int8, lin.weight_scale, lin.bias
     w = exec_weights(lin, torch.bfloat16)
     return w["weight"], w["weight_scale"], w["bias"]
@@ -67,8 +180,8 @@ def fused_weight(lin: nn.Module) -> tuple:
 
 def bf16_weight(lin: nn.Module) -> tuple:
     """``(bf16 weight, weight_scale)`` for one-time preparation kernels that read bf16 rows:
-    the cached image, or in the widen mode a temporary widened copy (not kept)."""
-    if hasattr(lin, "weight_int8") and INT8_WEIGHTS == "widen":
+    the cached image, or in the widen and window modes a temporary widened copy (not kept)."""
+    if hasattr(lin, "weight_int8") and INT8_WEIGHTS != "image":
         return ops.convert(lin.weight_int8, torch.bfloat16), lin.weight_scale
     w = exec_weights(lin, torch.bfloat16)
     return w["weight"], w["weight_scale"]
@@ -83,8 +196,11 @@ def resident_weight_bytes(model: nn.Module) -> dict:
         c = m.__dict__.get("_cortex_exec")
         if c is not None:
             images += c[1].numel() * c[1].element_size()
+    windows = {id(w): w.bytes for m in model.modules() if (w := m.__dict__.get("_cortex_window")) is not None}
+    window = sum(windows.values())
     int8 = sum(b.numel() for n, b in model.named_buffers() if n.endswith("weight_int8"))
-    return {"total": own + images, "parameters_and_buffers": own, "int8_weights": int8, "bf16_images": images}
+    return {"total": own + images + window, "parameters_and_buffers": own, "int8_weights": int8,
+            "bf16_images": images, "bf16_windows": window}
 
 
 def _state_key(tensors) -> tuple:
@@ -146,12 +262,14 @@ def ln_rows_ok(x: torch.Tensor, *norms: nn.LayerNorm) -> bool:
     return True
 
 
-def normalize_bf16(x: torch.Tensor, norm: nn.LayerNorm, norm2: nn.LayerNorm | None = None) -> torch.Tensor:
-    """``norm2(norm(x))`` (or ``norm(x)``) as bf16 rows (one launch)."""
+def normalize_bf16(x: torch.Tensor, norm: nn.LayerNorm, norm2: nn.LayerNorm | None = None,
+                   widen: list | None = None) -> torch.Tensor:
+    """``norm2(norm(x))`` (or ``norm(x)``) as bf16 rows (one launch; ``widen``: weight pairs that
+    ride along, see ``WeightWindow``)."""
     x2 = x.reshape(-1, x.shape[-1])
     if x2.data_ptr() % 16 or (x2.shape[0] > 1 and x2.stride(0) % 4) or x2.stride(-1) != 1:
         x2 = x2.contiguous()
-    return ops.ln_rows(x2, ln_params(norm), ln_params(norm2) if norm2 is not None else None)
+    return ops.ln_rows(x2, ln_params(norm), ln_params(norm2) if norm2 is not None else None, widen=widen)
 
 
 def residual_ln_ok(lin: nn.Module, norm: nn.LayerNorm, consumer: nn.Module, x: torch.Tensor,

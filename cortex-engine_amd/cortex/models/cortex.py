@@ -29,7 +29,7 @@ from cortex.kernels import ops
 from cortex.kernels.pack import pack_events as _device_pack_events
 from cortex.models._layers import (apply_linear, batch_invariant, bf16_weight, exec_weights, fused_tokens_ok,
                                    linear_residual_ln, linear_weights, ln_params, ln_rows_ok, normalize_bf16,
-                                   residual_ln_ok)
+                                   residual_ln_ok, rider)
 from cortex.models.config import CortexConfig
 from cortex.models.perceiver import PerceiverEncoder
 from cortex.models.tokenizer import SpikeTokenizer
@@ -211,6 +211,9 @@ class CortexModel(nn.Module):
         (``r`` itself when ``order`` is None or the plan's ``identity`` flag is set); rows past
         ``offsets[B]`` are ignored."""
         enc = self.encoder
+        win = enc.weight_window()
+        if win is not None:  # every weight group this forward reads is widened again
+            win.reset()
         tokens = self._token_rows(neuron_ids, time_bins, values, offsets, order, err_flag, identity)
         x, xn = self._cross_rows(tokens, offsets, B)
         x = self._encode(x, B, xn)
@@ -229,8 +232,12 @@ class CortexModel(nn.Module):
         tables = (tok.neuron_emb.weight, tok.time_emb.weight, tok.value_emb.weight)
         if (cfg.compute_dtype == torch.bfloat16 and not xa.kv_proj._forward_pre_hooks
                 and fused_tokens_ok(tables, xa.norm_kv)):
+            # the cross-attention's and the first block's weights widen into their windows in the
+            # same launch (INT8-resident window mode)
+            blocks = self.encoder.self_attn_blocks
+            widen = rider(xa, blocks[0] if len(blocks) else None)
             return ops.tokenize_ln(*tables, neuron_ids, time_bins, values, ln_params(xa.norm_kv), order=order,
-                                   csr_offsets=offsets, err=err_flag, identity=identity), True
+                                   csr_offsets=offsets, err=err_flag, identity=identity, widen=widen), True
         return ops.tokenize(*tables, neuron_ids, time_bins, values, order=order, csr_offsets=offsets,
                             err=err_flag, identity=identity), False
 

@@ -15,8 +15,9 @@ import torch
 from torch import nn
 
 from cortex.kernels import ops
-from cortex.models._layers import (apply_linear, batch_invariant, exec_weights, fused_weight, linear_residual_ln,
-                                   ln_rows_ok, normalize_bf16, residual_ln_ok)
+from cortex.models import _layers
+from cortex.models._layers import (apply_linear, batch_invariant, build_weight_window, exec_weights, fused_weight,
+                                   linear_residual_ln, ln_rows_ok, normalize_bf16, residual_ln_ok, rider)
 from cortex.models.config import CortexConfig
 
 
@@ -97,8 +98,8 @@ class SelfAttentionBlock(nn.Module):
             return self._forward_rows_w8a8(x, batch, length, inplace, w8)
         if self._fused_attention_ok(x, length):
             # qkv projection + attention per (head, sample) on chip: qkv never reaches HBM
-            if xn is None:
-                xn = normalize_bf16(x, self.norm_attn)
+            if xn is None:  # this block's weights widen into their window in the same launch
+                xn = normalize_bf16(x, self.norm_attn, widen=rider(self))
             o_buf = ops.qkv_attention(xn, *fused_weight(self.qkv_proj), batch, length, H)
         else:
             if xn is not None:
@@ -201,6 +202,25 @@ class PerceiverEncoder(nn.Module):
         self.self_attn_blocks = nn.ModuleList([SelfAttentionBlock(config) for _ in range(config.num_layers)])
         self.final_norm = nn.LayerNorm(config.latent_dim)
 
+    def weight_window(self):
+        """The ``WeightWindow`` of the INT8-resident mode (``CORTEX_INT8_WEIGHTS=window``) over the
+        cross-attention's kv / out projections and, in a second region shared block by block, the
+        self-attention blocks' four linears; built on first use, rebuilt when a weight is replaced.
+        None in the other modes."""
+        if _layers.INT8_WEIGHTS != "window":
+            return None
+        xa = self.cross_attn
+        regions = {"cross": [(xa, [xa.kv_proj, xa.out_proj])],
+                   "block": [(b, [b.qkv_proj, b.out_proj, b.mlp[0], b.mlp[2]]) for b in self.self_attn_blocks]}
+        lins = [lin for g in regions.values() for _, ls in g for lin in ls if hasattr(lin, "weight_int8")]
+        sig = tuple((lin.weight_int8.data_ptr(), tuple(lin.weight_int8.shape)) for lin in lins)
+        cached = self.__dict__.get("_cortex_window_sig")
+        if cached is not None and cached[0] == sig:
+            return cached[1]
+        win = build_weight_window(regions, lins[0].weight_int8.device) if lins else None
+        self.__dict__["_cortex_window_sig"] = (sig, win)
+        return win
+
     def encode_rows(self, x: torch.Tensor, batch: int, final_norm: bool = True, inplace: bool = False,
                     xn: torch.Tensor | None = None) -> torch.Tensor:
         """Self-attention stack (+ final norm) on the (B*L, D) residual after cross-attention;
@@ -216,6 +236,9 @@ class PerceiverEncoder(nn.Module):
         """tokens (B, E, D), token_mask (B, E) bool -> latents (B, L, D)."""
         B = tokens.shape[0]
         L, D = self.latents.shape
+        win = self.weight_window()
+        if win is not None:
+            win.reset()
         lat = self.latents.unsqueeze(0).expand(B, -1, -1)
         x = self.cross_attn(lat, tokens, token_mask)
         return self.encode_rows(x.reshape(B * L, D), B).reshape(B, L, D)

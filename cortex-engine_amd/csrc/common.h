@@ -157,6 +157,50 @@ __device__ __forceinline__ bf16x8 widen_i8x8(uint2 raw) {
   return v;
 }
 
+// Widening rider of a streaming row kernel: up to WR_MAX int8 arrays widened exactly to bf16
+// (dst[i][e] = src[i][e]) by the first `blocks` workgroups of the kernel's grid, each taking
+// WR_CHUNK consecutive elements of the concatenated arrays; the kernel's own rows follow.  The
+// row kernels are HBM-bound streams with idle issue slots, so a few MB of weights ride along for
+// about their transfer time and no launch of their own.  Element counts are multiples of 16 and
+// both arrays 16-byte aligned; the bf16 rows are written through (read by later kernels).
+constexpr int WR_MAX = 8;
+constexpr int64_t WR_CHUNK = 32768;
+struct WidenRider {
+  const int8_t* src[WR_MAX];
+  bf16* dst[WR_MAX];
+  int64_t end[WR_MAX];  // cumulative element counts
+  int count;
+  int blocks;  // rider workgroups at the front of the grid (0: none)
+};
+__device__ __forceinline__ void widen_rider_run(const WidenRider& r, int blk) {
+  const int64_t lo = (int64_t)blk * WR_CHUNK, hi = lo + WR_CHUNK;
+  int64_t s0 = 0;
+  for (int s = 0; s < r.count; ++s) {
+    const int64_t s1 = r.end[s], a = lo > s0 ? lo : s0, b = hi < s1 ? hi : s1;
+    if (a < b) {
+      const WtOut store(r.dst[s], (s1 - s0) * 2, true);
+      const int8_t* src = r.src[s] + (a - s0);
+      bf16* dst = r.dst[s] + (a - s0);
+      auto put = [&](int64_t i, const i32x4& raw) {
+        store(reinterpret_cast<bf16x8*>(dst + i), widen_i8x8(make_uint2((uint32_t)raw[0], (uint32_t)raw[1])));
+        store(reinterpret_cast<bf16x8*>(dst + i + 8), widen_i8x8(make_uint2((uint32_t)raw[2], (uint32_t)raw[3])));
+      };
+      if (b - a == WR_CHUNK && blockDim.x == 256) {  // a whole chunk: every load in flight first
+        constexpr int U = (int)(WR_CHUNK / (256 * 16));
+        i32x4 raw[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) raw[u] = *reinterpret_cast<const i32x4*>(src + (u * 256 + threadIdx.x) * 16);
+#pragma unroll
+        for (int u = 0; u < U; ++u) put((u * 256 + threadIdx.x) * 16, raw[u]);
+      } else {
+        for (int64_t i = threadIdx.x * 16; i < b - a; i += (int64_t)blockDim.x * 16)
+          put(i, *reinterpret_cast<const i32x4*>(src + i));
+      }
+    }
+    s0 = s1;
+  }
+}
+
 // Cross-lane reductions inside one wavefront.
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll

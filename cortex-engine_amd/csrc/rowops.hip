@@ -46,7 +46,7 @@ struct TokLnArgs {
 
 // Row r: lane l holds elements (j/4)*256 + 4l + (j%4), loaded as float4 (coalesced).
 template <int EPL>
-__global__ __launch_bounds__(256) void ln_rows_kernel(const float* __restrict__ x, int64_t M, int64_t ld_x,
+__global__ __launch_bounds__(256) void ln_rows_kernel(WidenRider wr, const float* __restrict__ x, int64_t M, int64_t ld_x,
                                                        const float* g1, const float* b1, float eps1,
                                                        const float* g2, const float* b2, float eps2, int two,
                                                        bf16* __restrict__ out_bf, int64_t ld_bf,
@@ -54,8 +54,12 @@ __global__ __launch_bounds__(256) void ln_rows_kernel(const float* __restrict__ 
                                                        int8_t* __restrict__ out_q = nullptr, int64_t ld_q = 0,
                                                        float q_inv = 0.0f) {
   constexpr int K = 64 * EPL;
+  if ((int)blockIdx.x < wr.blocks) {
+    widen_rider_run(wr, (int)blockIdx.x);
+    return;
+  }
   const int lane = threadIdx.x & 63;
-  const int64_t m = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  const int64_t m = (int64_t)(blockIdx.x - wr.blocks) * (blockDim.x >> 6) + (threadIdx.x >> 6);
   if (m >= M) return;
   const WtOut store_bf(out_bf, M * ld_bf * 2, true), store_f(out_f, M * ld_f * 4, true),
       store_q(out_q, M * ld_q, true);
@@ -233,10 +237,14 @@ __global__ __launch_bounds__(256) void fold_gain_kernel(const TW* __restrict__ w
 constexpr int TL_ROWS = 4;  // 4: 11.1 us at E = 16384, D = 512; 2: 11.4; 1: 11.5
 
 template <int EPL>
-__global__ __launch_bounds__(256) void tokenize_ln_kernel(TokLnArgs a) {
+__global__ __launch_bounds__(256) void tokenize_ln_kernel(TokLnArgs a, WidenRider wr) {
   constexpr int K = 64 * EPL, R = TL_ROWS;
+  if ((int)blockIdx.x < wr.blocks) {
+    widen_rider_run(wr, (int)blockIdx.x);
+    return;
+  }
   const int lane = threadIdx.x & 63;
-  const int64_t r0 = ((int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6)) * R;
+  const int64_t r0 = ((int64_t)(blockIdx.x - wr.blocks) * (blockDim.x >> 6) + (threadIdx.x >> 6)) * R;
   if (r0 >= a.E) return;
   const WtOut store(a.out, a.E * a.ld_out * 2, wt_fits(a.E * K * 2));
   const int64_t end = a.csr_end ? *a.csr_end : a.E;
@@ -327,6 +335,100 @@ __global__ __launch_bounds__(256) void tokenize_ln_kernel(TokLnArgs a) {
   }
 }
 
+// The whole grid as rider workgroups: the widening on its own launch.
+__global__ __launch_bounds__(256) void widen_kernel(WidenRider wr) { widen_rider_run(wr, (int)blockIdx.x); }
+
+// Rider of up to WR_MAX (src int8, dst bf16, count) arrays; arrays with count 0 are dropped.
+int make_rider(const char* who, int n, const void* const* src, void* const* dst, const int64_t* count,
+               WidenRider* r) {
+  *r = WidenRider{};
+  CORTEX_CHECK_ARG(n >= 0 && n <= WR_MAX, "%s: %d arrays to widen (at most %d)", who, n, WR_MAX);
+  if (n == 0) return OK;
+  CORTEX_CHECK_ARG(src && dst && count, "%s: null widen list", who);
+  int64_t total = 0;
+  for (int i = 0; i < n; ++i) {
+    CORTEX_CHECK_ARG(count[i] >= 0 && count[i] % 16 == 0, "%s: widen count %lld is not a multiple of 16", who,
+                     (long long)count[i]);
+    if (count[i] == 0) continue;
+    CORTEX_CHECK_ARG(src[i] && dst[i] && ((uintptr_t)src[i] & 15) == 0 && ((uintptr_t)dst[i] & 15) == 0,
+                     "%s: widen arrays must be 16-byte aligned", who);
+    total += count[i];
+    r->src[r->count] = static_cast<const int8_t*>(src[i]);
+    r->dst[r->count] = static_cast<bf16*>(dst[i]);
+    r->end[r->count] = total;
+    ++r->count;
+  }
+  CORTEX_CHECK_ARG(cdiv(total, WR_CHUNK) <= (1 << 24), "%s: %lld elements to widen", who, (long long)total);
+  r->blocks = (int)cdiv(total, WR_CHUNK);
+  return OK;
+}
+
+int ln_rows_launch(int64_t M, int64_t K, const float* x, int64_t ld_x, const float* gamma1, const float* beta1,
+                   float eps1, const float* gamma2, const float* beta2, float eps2, void* out_bf16, int64_t ld_bf16,
+                   float* out_f32, int64_t ld_f32, const WidenRider& wr, hipStream_t stream) {
+  CORTEX_CHECK_ARG(M >= 0, "cortex_ln_rows: negative M");
+  if (M == 0 && wr.blocks == 0) return OK;
+  CORTEX_CHECK_ARG(M == 0 || (x && (out_bf16 || out_f32)), "cortex_ln_rows: null input or no output");
+  CORTEX_CHECK_ARG(K == 256 || K == 512 || K == 768 || K == 1024,
+                   "cortex_ln_rows: K=%lld not one of 256, 512, 768, 1024", (long long)K);
+  CORTEX_CHECK_ARG(((uintptr_t)x & 15) == 0 && ld_x % 4 == 0, "cortex_ln_rows: x rows must be 16-byte aligned");
+  CORTEX_CHECK_ARG(!out_bf16 || (((uintptr_t)out_bf16 & 7) == 0 && ld_bf16 % 4 == 0),
+                   "cortex_ln_rows: bf16 output rows must be 8-byte aligned");
+  CORTEX_CHECK_ARG(!out_f32 || (((uintptr_t)out_f32 & 15) == 0 && ld_f32 % 4 == 0),
+                   "cortex_ln_rows: fp32 output rows must be 16-byte aligned");
+  for (const float* p : {gamma1, beta1, gamma2, beta2})
+    CORTEX_CHECK_ARG(((uintptr_t)p & 15) == 0, "cortex_ln_rows: gamma/beta must be 16-byte aligned fp32");
+  CORTEX_CHECK_ARG(cdiv(M, 4) + wr.blocks <= 0x7fffffffLL, "cortex_ln_rows: M too large");
+  const int two = gamma2 != nullptr || beta2 != nullptr;
+  const dim3 grid((unsigned)(cdiv(M, 4) + wr.blocks));
+#define CORTEX_LNR(EPL)                                                                                              \
+  hipLaunchKernelGGL((ln_rows_kernel<EPL>), grid, dim3(256), 0, stream, wr, x, M, ld_x, gamma1, beta1, eps1, gamma2, \
+                     beta2, eps2, two, (bf16*)out_bf16, ld_bf16, out_f32, ld_f32)
+  switch (K) {
+    case 256: CORTEX_LNR(4); break;
+    case 512: CORTEX_LNR(8); break;
+    case 768: CORTEX_LNR(12); break;
+    default: CORTEX_LNR(16); break;
+  }
+#undef CORTEX_LNR
+  CORTEX_CHECK_LAUNCH("ln_rows_kernel");
+  return OK;
+}
+
+int tokenize_ln_launch(int64_t D, const float* neuron_emb, int64_t n_neuron, int64_t ld_neuron, const float* time_emb,
+                       int64_t n_time, int64_t ld_time, const float* value_emb, int64_t n_value, int64_t ld_value,
+                       const int64_t* neuron_ids, int64_t s_nid, const int64_t* time_bins, int64_t s_tb,
+                       const int64_t* values, int64_t s_val, int64_t E, const int64_t* order, const int32_t* identity,
+                       const int64_t* csr_end, const float* gamma, const float* beta, float eps, void* out_bf16,
+                       int64_t ld_out, int32_t* err_flag, const WidenRider& wr, hipStream_t stream) {
+  CORTEX_CHECK_ARG(E >= 0, "cortex_tokenize_ln: negative E");
+  if (E == 0 && wr.blocks == 0) return OK;
+  CORTEX_CHECK_ARG(D == 256 || D == 512 || D == 768 || D == 1024, "cortex_tokenize_ln: D=%lld not in {256, 512, 768, 1024}",
+                   (long long)D);
+  CORTEX_CHECK_ARG(E == 0 || (neuron_emb && time_emb && value_emb && neuron_ids && time_bins && values && out_bf16),
+                   "cortex_tokenize_ln: null pointer");
+  CORTEX_CHECK_ARG(ld_out >= D && ld_neuron >= D && ld_time >= D && ld_value >= D, "cortex_tokenize_ln: ld < D");
+  CORTEX_CHECK_ARG(n_neuron > 0 && n_time > 0 && n_value > 0, "cortex_tokenize_ln: empty embedding table");
+  auto al16 = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
+  CORTEX_CHECK_ARG(al16(neuron_emb) && al16(time_emb) && al16(value_emb) && ld_neuron % 4 == 0 && ld_time % 4 == 0 &&
+                       ld_value % 4 == 0 && ((uintptr_t)out_bf16 & 7) == 0 && ld_out % 4 == 0 &&
+                       (!gamma || al16(gamma)) && (!beta || al16(beta)),
+                   "cortex_tokenize_ln: tables, gamma, beta need 16-byte aligned rows and out 8-byte aligned rows");
+  CORTEX_CHECK_ARG(cdiv(E, 4 * TL_ROWS) + wr.blocks <= 0x7fffffffLL, "cortex_tokenize_ln: E too large");
+  TokLnArgs a = {neuron_emb, n_neuron, ld_neuron, time_emb, n_time, ld_time, value_emb, n_value, ld_value,
+                 neuron_ids, s_nid, time_bins, s_tb, values, s_val, E, order, identity, csr_end, gamma, beta, eps,
+                 out_bf16, ld_out, err_flag};
+  const dim3 grid((unsigned)(cdiv(E, 4 * TL_ROWS) + wr.blocks));
+  switch (D) {
+    case 256: hipLaunchKernelGGL(tokenize_ln_kernel<4>, grid, dim3(256), 0, stream, a, wr); break;
+    case 512: hipLaunchKernelGGL(tokenize_ln_kernel<8>, grid, dim3(256), 0, stream, a, wr); break;
+    case 768: hipLaunchKernelGGL(tokenize_ln_kernel<12>, grid, dim3(256), 0, stream, a, wr); break;
+    default: hipLaunchKernelGGL(tokenize_ln_kernel<16>, grid, dim3(256), 0, stream, a, wr); break;
+  }
+  CORTEX_CHECK_LAUNCH("tokenize_ln_kernel");
+  return OK;
+}
+
 }  // namespace cortex
 
 using namespace cortex;
@@ -364,32 +466,19 @@ int cortex_convert(int in_dtype, const void* in, int out_dtype, void* out, int64
 int cortex_ln_rows(int64_t M, int64_t K, const float* x, int64_t ld_x, const float* gamma1, const float* beta1,
                    float eps1, const float* gamma2, const float* beta2, float eps2, void* out_bf16, int64_t ld_bf16,
                    float* out_f32, int64_t ld_f32, hipStream_t stream) {
-  CORTEX_CHECK_ARG(M >= 0, "cortex_ln_rows: negative M");
-  if (M == 0) return OK;
-  CORTEX_CHECK_ARG(x && (out_bf16 || out_f32), "cortex_ln_rows: null input or no output");
-  CORTEX_CHECK_ARG(K == 256 || K == 512 || K == 768 || K == 1024,
-                   "cortex_ln_rows: K=%lld not one of 256, 512, 768, 1024", (long long)K);
-  CORTEX_CHECK_ARG(((uintptr_t)x & 15) == 0 && ld_x % 4 == 0, "cortex_ln_rows: x rows must be 16-byte aligned");
-  CORTEX_CHECK_ARG(!out_bf16 || (((uintptr_t)out_bf16 & 7) == 0 && ld_bf16 % 4 == 0),
-                   "cortex_ln_rows: bf16 output rows must be 8-byte aligned");
-  CORTEX_CHECK_ARG(!out_f32 || (((uintptr_t)out_f32 & 15) == 0 && ld_f32 % 4 == 0),
-                   "cortex_ln_rows: fp32 output rows must be 16-byte aligned");
-  for (const float* p : {gamma1, beta1, gamma2, beta2})
-    CORTEX_CHECK_ARG(((uintptr_t)p & 15) == 0, "cortex_ln_rows: gamma/beta must be 16-byte aligned fp32");
-  const int two = gamma2 != nullptr || beta2 != nullptr;
-  const dim3 grid((unsigned)cdiv(M, 4));
-#define CORTEX_LNR(EPL)                                                                                          \
-  hipLaunchKernelGGL((ln_rows_kernel<EPL>), grid, dim3(256), 0, stream, x, M, ld_x, gamma1, beta1, eps1, gamma2, \
-                     beta2, eps2, two, (bf16*)out_bf16, ld_bf16, out_f32, ld_f32)
-  switch (K) {
-    case 256: CORTEX_LNR(4); break;
-    case 512: CORTEX_LNR(8); break;
-    case 768: CORTEX_LNR(12); break;
-    default: CORTEX_LNR(16); break;
-  }
-#undef CORTEX_LNR
-  CORTEX_CHECK_LAUNCH("ln_rows_kernel");
-  return OK;
+  return ln_rows_launch(M, K, x, ld_x, gamma1, beta1, eps1, gamma2, beta2, eps2, out_bf16, ld_bf16, out_f32, ld_f32,
+                        WidenRider{}, stream);
+}
+
+int cortex_ln_rows_widen(int64_t M, int64_t K, const float* x, int64_t ld_x, const float* gamma1, const float* beta1,
+                         float eps1, const float* gamma2, const float* beta2, float eps2, void* out_bf16,
+                         int64_t ld_bf16, float* out_f32, int64_t ld_f32, int n_widen, const void* const* widen_src,
+                         void* const* widen_dst, const int64_t* widen_count, hipStream_t stream) {
+  WidenRider wr;
+  const int st = make_rider("cortex_ln_rows_widen", n_widen, widen_src, widen_dst, widen_count, &wr);
+  if (st != OK) return st;
+  return ln_rows_launch(M, K, x, ld_x, gamma1, beta1, eps1, gamma2, beta2, eps2, out_bf16, ld_bf16, out_f32, ld_f32,
+                        wr, stream);
 }
 
 int cortex_tokenize_ln(int64_t D, const float* neuron_emb, int64_t n_neuron, int64_t ld_neuron, const float* time_emb,
@@ -398,31 +487,34 @@ int cortex_tokenize_ln(int64_t D, const float* neuron_emb, int64_t n_neuron, int
                        const int64_t* values, int64_t s_val, int64_t E, const int64_t* order, const int32_t* identity,
                        const int64_t* csr_end, const float* gamma, const float* beta, float eps, void* out_bf16,
                        int64_t ld_out, int32_t* err_flag, hipStream_t stream) {
-  CORTEX_CHECK_ARG(E >= 0, "cortex_tokenize_ln: negative E");
-  if (E == 0) return OK;
-  CORTEX_CHECK_ARG(D == 256 || D == 512 || D == 768 || D == 1024, "cortex_tokenize_ln: D=%lld not in {256, 512, 768, 1024}",
-                   (long long)D);
-  CORTEX_CHECK_ARG(neuron_emb && time_emb && value_emb && neuron_ids && time_bins && values && out_bf16,
-                   "cortex_tokenize_ln: null pointer");
-  CORTEX_CHECK_ARG(ld_out >= D && ld_neuron >= D && ld_time >= D && ld_value >= D, "cortex_tokenize_ln: ld < D");
-  CORTEX_CHECK_ARG(n_neuron > 0 && n_time > 0 && n_value > 0, "cortex_tokenize_ln: empty embedding table");
-  auto al16 = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
-  CORTEX_CHECK_ARG(al16(neuron_emb) && al16(time_emb) && al16(value_emb) && ld_neuron % 4 == 0 && ld_time % 4 == 0 &&
-                       ld_value % 4 == 0 && ((uintptr_t)out_bf16 & 7) == 0 && ld_out % 4 == 0 &&
-                       (!gamma || al16(gamma)) && (!beta || al16(beta)),
-                   "cortex_tokenize_ln: tables, gamma, beta need 16-byte aligned rows and out 8-byte aligned rows");
-  CORTEX_CHECK_ARG(cdiv(E, 4 * TL_ROWS) <= 0x7fffffffLL, "cortex_tokenize_ln: E too large");
-  TokLnArgs a = {neuron_emb, n_neuron, ld_neuron, time_emb, n_time, ld_time, value_emb, n_value, ld_value,
-                 neuron_ids, s_nid, time_bins, s_tb, values, s_val, E, order, identity, csr_end, gamma, beta, eps,
-                 out_bf16, ld_out, err_flag};
-  const dim3 grid((unsigned)cdiv(E, 4 * TL_ROWS));
-  switch (D) {
-    case 256: hipLaunchKernelGGL(tokenize_ln_kernel<4>, grid, dim3(256), 0, stream, a); break;
-    case 512: hipLaunchKernelGGL(tokenize_ln_kernel<8>, grid, dim3(256), 0, stream, a); break;
-    case 768: hipLaunchKernelGGL(tokenize_ln_kernel<12>, grid, dim3(256), 0, stream, a); break;
-    default: hipLaunchKernelGGL(tokenize_ln_kernel<16>, grid, dim3(256), 0, stream, a); break;
-  }
-  CORTEX_CHECK_LAUNCH("tokenize_ln_kernel");
+  return tokenize_ln_launch(D, neuron_emb, n_neuron, ld_neuron, time_emb, n_time, ld_time, value_emb, n_value,
+                            ld_value, neuron_ids, s_nid, time_bins, s_tb, values, s_val, E, order, identity, csr_end,
+                            gamma, beta, eps, out_bf16, ld_out, err_flag, WidenRider{}, stream);
+}
+
+int cortex_tokenize_ln_widen(int64_t D, const float* neuron_emb, int64_t n_neuron, int64_t ld_neuron,
+                             const float* time_emb, int64_t n_time, int64_t ld_time, const float* value_emb,
+                             int64_t n_value, int64_t ld_value, const int64_t* neuron_ids, int64_t s_nid,
+                             const int64_t* time_bins, int64_t s_tb, const int64_t* values, int64_t s_val, int64_t E,
+                             const int64_t* order, const int32_t* identity, const int64_t* csr_end, const float* gamma,
+                             const float* beta, float eps, void* out_bf16, int64_t ld_out, int32_t* err_flag,
+                             int n_widen, const void* const* widen_src, void* const* widen_dst,
+                             const int64_t* widen_count, hipStream_t stream) {
+  WidenRider wr;
+  const int st = make_rider("cortex_tokenize_ln_widen", n_widen, widen_src, widen_dst, widen_count, &wr);
+  if (st != OK) return st;
+  return tokenize_ln_launch(D, neuron_emb, n_neuron, ld_neuron, time_emb, n_time, ld_time, value_emb, n_value,
+                            ld_value, neuron_ids, s_nid, time_bins, s_tb, values, s_val, E, order, identity, csr_end,
+                            gamma, beta, eps, out_bf16, ld_out, err_flag, wr, stream);
+}
+
+int cortex_widen_int8(int n, const void* const* src, void* const* dst, const int64_t* count, hipStream_t stream) {
+  WidenRider wr;
+  const int st = make_rider("cortex_widen_int8", n, src, dst, count, &wr);
+  if (st != OK) return st;
+  if (wr.blocks == 0) return OK;
+  hipLaunchKernelGGL(widen_kernel, dim3((unsigned)wr.blocks), dim3(256), 0, stream, wr);
+  CORTEX_CHECK_LAUNCH("widen_kernel");
   return OK;
 }
 
@@ -520,9 +612,9 @@ int cortex_ln_rows_i8(int64_t M, int64_t K, const float* x, int64_t ld_x, const 
     CORTEX_CHECK_ARG(((uintptr_t)p & 15) == 0, "cortex_ln_rows_i8: gamma/beta must be 16-byte aligned fp32");
   const dim3 grid((unsigned)cdiv(M, 4));
   const float inv = 1.0f / out_scale;
-#define CORTEX_LNQ(EPL)                                                                                           \
-  hipLaunchKernelGGL((ln_rows_kernel<EPL>), grid, dim3(256), 0, stream, x, M, ld_x, gamma, beta, eps, nullptr, \
-                     nullptr, 0.0f, 0, nullptr, 0, nullptr, 0, out, ld_out, inv)
+#define CORTEX_LNQ(EPL)                                                                                              \
+  hipLaunchKernelGGL((ln_rows_kernel<EPL>), grid, dim3(256), 0, stream, WidenRider{}, x, M, ld_x, gamma, beta, eps, \
+                     nullptr, nullptr, 0.0f, 0, nullptr, 0, nullptr, 0, out, ld_out, inv)
   switch (K) {
     case 256: CORTEX_LNQ(4); break;
     case 512: CORTEX_LNQ(8); break;

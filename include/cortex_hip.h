@@ -175,6 +175,30 @@ int cortex_ln_rows(int64_t M, int64_t K, const float* x, int64_t ld_x, const flo
                    float eps1, const float* gamma2, const float* beta2, float eps2, void* out_bf16, int64_t ld_bf16,
                    float* out_f32, int64_t ld_f32, hipStream_t stream);
 
+/* ---- a7: INT8 weights widened to bf16 on the way ----------------------------
+ * dst[i][e] = (bf16) src[i][e] for n <= 8 int8 arrays of count[i] elements (count[i] a
+ * multiple of 16, both arrays 16-byte aligned): the dequantise step of
+ * QuantizedLinear.forward (cortex/quantization/calibrate.py:227-228, q.float() before the
+ * per-channel scale, which stays on the GEMM's accumulator), exact since every int8 value is a
+ * bf16 value.  cortex_widen_int8 launches it on its own; the _widen forms of the LayerNorm row
+ * kernels and of the tokenizer + LayerNorm run it in extra workgroups of their own launch (the
+ * next block's weights ride along with the rows that feed it), otherwise exactly as
+ * cortex_ln_rows / cortex_tokenize_ln.  The widened arrays must not overlap the kernel's
+ * inputs or outputs. */
+int cortex_widen_int8(int n, const void* const* src, void* const* dst, const int64_t* count, hipStream_t stream);
+int cortex_ln_rows_widen(int64_t M, int64_t K, const float* x, int64_t ld_x, const float* gamma1, const float* beta1,
+                         float eps1, const float* gamma2, const float* beta2, float eps2, void* out_bf16,
+                         int64_t ld_bf16, float* out_f32, int64_t ld_f32, int n_widen, const void* const* widen_src,
+                         void* const* widen_dst, const int64_t* widen_count, hipStream_t stream);
+int cortex_tokenize_ln_widen(int64_t D, const float* neuron_emb, int64_t n_neuron, int64_t ld_neuron,
+                             const float* time_emb, int64_t n_time, int64_t ld_time, const float* value_emb,
+                             int64_t n_value, int64_t ld_value, const int64_t* neuron_ids, int64_t s_nid,
+                             const int64_t* time_bins, int64_t s_tb, const int64_t* values, int64_t s_val, int64_t E,
+                             const int64_t* order, const int32_t* identity, const int64_t* csr_end, const float* gamma,
+                             const float* beta, float eps, void* out_bf16, int64_t ld_out, int32_t* err_flag,
+                             int n_widen, const void* const* widen_src, void* const* widen_dst,
+                             const int64_t* widen_count, hipStream_t stream);
+
 /* ---- a7: dtype conversion ---------------------------------------------------
  * out[i] = (out dtype) in[i]; int8 / f32 / bf16 / f16 in, f32 / bf16 out (bf16 by
  * round-to-nearest-even).  Builds the bf16 execution image of INT8 weights, which is

@@ -73,6 +73,19 @@ def test_invalid_arguments_return_status_and_message():
     assert lib.cortex_pack_workspace_bytes(5000, 32) == (5 * 32 + 20) * 4
     rc = lib.cortex_pack_plan(None, 1, 10, 100000, None, None, None, None, None, 0, None, None, 0, None)
     assert rc == -1 and b"exceeds" in lib.cortex_last_error()
+    # widening riders: at most 8 arrays, counts in multiples of 16, 16-byte aligned arrays
+    src = (ctypes.c_void_p * 9)(*([16] * 9))
+    cnt = (ctypes.c_int64 * 9)(*([16] * 9))
+    rc = lib.cortex_widen_int8(9, src, src, cnt, None)
+    assert rc == -1 and b"at most 8" in lib.cortex_last_error()
+    cnt[0] = 24
+    rc = lib.cortex_widen_int8(1, src, src, cnt, None)
+    assert rc == -1 and b"multiple of 16" in lib.cortex_last_error()
+    cnt[0], src[0] = 16, 8
+    rc = lib.cortex_ln_rows_widen(0, 512, None, 512, None, None, 1e-5, None, None, 0.0, None, 512, None, 512, 1, src,
+                                  src, cnt, None)
+    assert rc == -1 and b"16-byte aligned" in lib.cortex_last_error()
+    assert lib.cortex_widen_int8(0, None, None, None, None) == 0
 
 
 def test_missing_library_fails_loudly(monkeypatch, tmp_path):

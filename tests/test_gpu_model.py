@@ -331,3 +331,72 @@ def test_widen_mode_streams_int8_weights_through_the_fused_path(monkeypatch):
     sd = {k: v.detach().cpu() for k, v in model.state_dict().items()}
     ref = O.forward(sd, O.CORTEX_S_SHAPE, *arrs).numpy()
     assert np.abs(widen.cpu().numpy() - ref).max() <= 2e-2
+
+
+def test_window_mode_widens_each_block_in_the_row_kernel_ahead_of_it(monkeypatch):
+    """CORTEX_INT8_WEIGHTS=window: only the int8 weights stay resident, plus two bf16 windows (the
+    cross-attention's kv / out projections; one self-attention block's four linears, which the
+    blocks take in turn).  In a forward the tokenizer + LayerNorm launch widens the
+    cross-attention's and the first block's weights and each later block's LayerNorm row launch
+    its own, with no widening launch of its own.  Config-3 shape: bit-identical to the image mode
+    (the same bf16 weight values reach the same kernels), eager and replayed from a graph."""
+    from cortex.kernels import ops
+    from cortex.models import _layers
+    from cortex.runtime import CapturedForward
+
+    arrs = _config3_inputs(seed=9)
+    inputs = [torch.from_numpy(a).to(DEV) for a in arrs]
+    monkeypatch.setattr(_layers, "INT8_WEIGHTS", "window")
+    model = _int8(_model("s", "bfloat16"), [t[:2048] for t in inputs])
+    seen = {"alone": 0, "tokenize_ln": [], "ln_rows": []}
+    orig_w, orig_t, orig_l = ops.widen_int8, ops.tokenize_ln, ops.ln_rows
+
+    def widen_spy(pairs):
+        seen["alone"] += 1
+        return orig_w(pairs)
+
+    def tok_spy(*a, widen=None, **k):
+        seen["tokenize_ln"].append(len(widen or []))
+        return orig_t(*a, widen=widen, **k)
+
+    def ln_spy(*a, widen=None, **k):
+        seen["ln_rows"].append(len(widen or []))
+        return orig_l(*a, widen=widen, **k)
+    monkeypatch.setattr(ops, "widen_int8", widen_spy)
+    monkeypatch.setattr(ops, "tokenize_ln", tok_spy)
+    monkeypatch.setattr(ops, "ln_rows", ln_spy)
+    with torch.no_grad():
+        model(*inputs, batch_size=32)  # caches the batch-invariant query projections
+        seen.update(alone=0, tokenize_ln=[], ln_rows=[])
+        win = model(*inputs, batch_size=32)["behavior"].clone()
+        win2 = model(*inputs, batch_size=32)["behavior"].clone()
+    assert seen["alone"] == 0, seen
+    assert seen["tokenize_ln"] == [2 + 4] * 2 and seen["ln_rows"] == [4] * 12, seen
+    wb = _layers.resident_weight_bytes(model)
+    D = 512
+    assert wb["bf16_images"] == 0
+    assert wb["bf16_windows"] == 2 * (3 * D * D) + 2 * (12 * D * D), wb
+    cap = CapturedForward(model, batch_size=32, n_events=32 * 512)
+    graph = cap(*inputs).clone()
+    # blocks run outside the model forward: one normalising its own rows carries its weights in
+    # that launch; one handed its normalised rows widens them on a launch of its own first
+    blk, blk2 = model.encoder.self_attn_blocks[3], model.encoder.self_attn_blocks[5]
+    x = torch.randn(32 * 256, D, device=DEV)
+    with torch.no_grad():
+        xn2 = _layers.normalize_bf16(x, blk2.norm_attn)
+        seen.update(alone=0, ln_rows=[])
+        y_win = blk.forward_rows(x.clone(), 32, 256)
+        assert seen["ln_rows"] == [4] and seen["alone"] == 0, seen
+        y2_win = blk2.forward_rows(x.clone(), 32, 256, xn=xn2)
+        assert seen["alone"] == 1, seen
+    monkeypatch.undo()
+    with torch.no_grad():
+        image = model(*inputs, batch_size=32)["behavior"]
+        y_img = blk.forward_rows(x.clone(), 32, 256)
+        y2_img = blk2.forward_rows(x.clone(), 32, 256, xn=xn2)
+    assert _layers.resident_weight_bytes(model)["bf16_images"] > 2 * wb["bf16_windows"]
+    torch.testing.assert_close(win, win2, rtol=0, atol=0)
+    torch.testing.assert_close(win, image, rtol=0, atol=0)
+    torch.testing.assert_close(graph, image, rtol=0, atol=0)
+    torch.testing.assert_close(y_win, y_img, rtol=0, atol=0)
+    torch.testing.assert_close(y2_win, y2_img, rtol=0, atol=0)
