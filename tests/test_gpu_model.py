@@ -389,11 +389,20 @@ def test_window_mode_widens_each_block_in_the_row_kernel_ahead_of_it(monkeypatch
         assert seen["ln_rows"] == [4] and seen["alone"] == 0, seen
         y2_win = blk2.forward_rows(x.clone(), 32, 256, xn=xn2)
         assert seen["alone"] == 1, seen
+        # other batch shapes take other kernels on the same windows: B = 1 (K split across
+        # workgroups), B = 64 (persistent and three-stage tiles), ragged and shuffled events
+        other = [[torch.from_numpy(a).to(DEV) for a in _config3_inputs(B, per, seed=20 + B)]
+                 for B, per in ((1, 700), (64, 160))]
+        other[1][3] = other[1][3][torch.randperm(other[1][3].shape[0], device=DEV)]
+        other_win = [model(*o, batch_size=o[3].max().item() + 1)["behavior"].clone() for o in other]
     monkeypatch.undo()
     with torch.no_grad():
         image = model(*inputs, batch_size=32)["behavior"]
         y_img = blk.forward_rows(x.clone(), 32, 256)
         y2_img = blk2.forward_rows(x.clone(), 32, 256, xn=xn2)
+        other_img = [model(*o, batch_size=o[3].max().item() + 1)["behavior"] for o in other]
+    for w, i in zip(other_win, other_img):
+        torch.testing.assert_close(w, i, rtol=0, atol=0)
     assert _layers.resident_weight_bytes(model)["bf16_images"] > 2 * wb["bf16_windows"]
     torch.testing.assert_close(win, win2, rtol=0, atol=0)
     torch.testing.assert_close(win, image, rtol=0, atol=0)
