@@ -429,6 +429,12 @@ __global__ __launch_bounds__(TL::THREADS) void gemm_bf16_kernel(GemmArgs g) {
   const float* bias = reinterpret_cast<const float*>(g.bias);
   TOUT* out = reinterpret_cast<TOUT*>(g.out) + (int64_t)kz * M * g.ld_out;
   const WtOut store(out, (int64_t)M * g.ld_out * (int64_t)sizeof(TOUT), wt_one_wave());
+  // the lane's first output row once; each further 16-row group adds a uniform step, kept
+  // opaque so that the compiler does not fold it back into a 64-bit multiply per store
+  const int64_t row_base = (int64_t)(m0 + wrow + fr) * g.ld_out;
+  const int64_t step16 =
+      (int64_t)(((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(g.ld_out >> 28)) << 32) |
+                (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(g.ld_out << 4)));
   constexpr int NV = IL ? 8 : 4;           // consecutive columns per lane and group
   constexpr int NG = IL ? TN / 2 : TN;     // column groups per lane
   // Every scale and bias load first, then one wait: a wait left to the compiler would
@@ -478,7 +484,7 @@ __global__ __launch_bounds__(TL::THREADS) void gemm_bf16_kernel(GemmArgs g) {
         const float4 x = rv[i][p];
         v[0] += x.x; v[1] += x.y; v[2] += x.z; v[3] += x.w;
       }
-      TOUT* op = out + (int64_t)m * g.ld_out + n;
+      TOUT* op = out + (row_base + i * step16 + n);
       if constexpr (sizeof(TOUT) == 2) {
         bf16x8 o;
 #pragma unroll
@@ -688,6 +694,10 @@ __global__ __launch_bounds__(512) void gemm_persist_kernel(GemmArgs g) {
   auto epilogue = [&](int t) __attribute__((always_inline)) {
     const int m0 = (t / gx) * BM, n0 = (t % gx) * BN;
     const float* sp = params(t);
+    // row offsets in elements, 32-bit (M * ld_out * 2 < 4 GiB, checked at launch), once per tile
+    uint32_t roff[TM];
+#pragma unroll
+    for (int i = 0; i < TM; ++i) roff[i] = (uint32_t)min(m0 + wrow + i * 16 + fr, M - 1) * (uint32_t)g.ld_out;
 #pragma unroll
     for (int p = 0; p < NG; ++p) {
       const int c = wcol + 32 * p + 8 * g4;  // column inside the tile
@@ -703,7 +713,6 @@ __global__ __launch_bounds__(512) void gemm_persist_kernel(GemmArgs g) {
       }
 #pragma unroll
       for (int i = 0; i < TM; ++i) {
-        const int m = min(m0 + wrow + i * 16 + fr, M - 1);
         bf16x8 o;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
@@ -716,7 +725,7 @@ __global__ __launch_bounds__(512) void gemm_persist_kernel(GemmArgs g) {
           o[r] = (bf16)v0;
           o[4 + r] = (bf16)v1;
         }
-        *reinterpret_cast<bf16x8*>(out + (int64_t)m * g.ld_out + n0 + c) = o;
+        *reinterpret_cast<bf16x8*>(out + (roff[i] + (uint32_t)(n0 + c))) = o;
       }
     }
   };
@@ -763,8 +772,11 @@ __global__ __launch_bounds__(512) void gemm_persist_kernel(GemmArgs g) {
 template <int ACT>
 int launch_persist(const GemmArgs& g, hipStream_t stream) {
   const int64_t ntiles = cdiv(g.M, 256) * (g.N / 256);
-  // 32-bit transfer offsets (the scalar-base form) address both operands
-  if (g.M * g.ld_x * 2 >= (1LL << 32) || g.N * g.ld_w * 2 >= (1LL << 32) || ntiles > 0x7fffffffLL) return 0;
+  // 32-bit transfer offsets (the scalar-base form) address both operands, 32-bit element
+  // offsets the output; larger tensors take the one-tile-per-workgroup kernel
+  if (g.M * g.ld_x * 2 >= (1LL << 32) || g.N * g.ld_w * 2 >= (1LL << 32) || g.M * g.ld_out * 2 >= (1LL << 32) ||
+      ntiles > 0x7fffffffLL)
+    return 0;
   const int G = (int)std::min<int64_t>(ntiles, cu_count() & ~7);
   hipLaunchKernelGGL((gemm_persist_kernel<ACT>), dim3((unsigned)G), dim3(512), 0, stream, g);
   CORTEX_CHECK_LAUNCH("gemm_persist_kernel");
@@ -795,8 +807,10 @@ int dispatch(const GemmArgs& g, hipStream_t stream) {
       case T256:
         // past one wave of 256 x 256 tiles, bf16 out: persistent tiles (see gemm_persist_kernel)
         if constexpr (!RES && sizeof(TOUT) == 2) {
-          if (g.N % 256 == 0 && cdiv(g.M, 256) * (g.N / 256) > cu_count() && cu_count() >= 8)
-            return launch_persist<ACT>(g, stream);
+          if (g.N % 256 == 0 && cdiv(g.M, 256) * (g.N / 256) > cu_count() && cu_count() >= 8) {
+            const int st = launch_persist<ACT>(g, stream);
+            if (st != 0) return st;
+          }
         }
         return launch<B256x256s2, ACT, RES, TOUT>(g, stream);
       case T192: return launch<B256x192s2, ACT, RES, TOUT>(g, stream);
