@@ -201,6 +201,16 @@ __device__ __forceinline__ void widen_rider_run(const WidenRider& r, int blk) {
   }
 }
 
+// A value every lane of the wavefront holds alike (a row index, a loaded table index), moved to
+// scalar registers: the compiler cannot prove such values uniform, and would otherwise keep
+// their 64-bit address arithmetic in vector registers (quarter-rate multiplies per lane).
+__device__ __forceinline__ int64_t wave_uniform(int64_t v) {
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)v);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)((uint64_t)v >> 32));
+  return (int64_t)(((uint64_t)hi << 32) | lo);
+}
+__device__ __forceinline__ int wave_uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
+
 // Cross-lane reductions inside one wavefront.
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll

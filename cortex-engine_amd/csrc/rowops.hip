@@ -59,7 +59,7 @@ __global__ __launch_bounds__(256) void ln_rows_kernel(WidenRider wr, const float
     return;
   }
   const int lane = threadIdx.x & 63;
-  const int64_t m = (int64_t)(blockIdx.x - wr.blocks) * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  const int64_t m = (int64_t)(blockIdx.x - wr.blocks) * (blockDim.x >> 6) + wave_uniform((int)threadIdx.x >> 6);
   if (m >= M) return;
   const WtOut store_bf(out_bf, M * ld_bf * 2, true), store_f(out_f, M * ld_f * 4, true),
       store_q(out_q, M * ld_q, true);
@@ -244,7 +244,9 @@ __global__ __launch_bounds__(256) void tokenize_ln_kernel(TokLnArgs a, WidenRide
     return;
   }
   const int lane = threadIdx.x & 63;
-  const int64_t r0 = ((int64_t)(blockIdx.x - wr.blocks) * (blockDim.x >> 6) + (threadIdx.x >> 6)) * R;
+  // a wavefront's rows, the events they map to and those events' table indices are the same in
+  // every lane: kept in scalar registers, as is their address arithmetic
+  const int64_t r0 = ((int64_t)(blockIdx.x - wr.blocks) * (blockDim.x >> 6) + wave_uniform((int)threadIdx.x >> 6)) * R;
   if (r0 >= a.E) return;
   const WtOut store(a.out, a.E * a.ld_out * 2, wt_fits(a.E * K * 2));
   const int64_t end = a.csr_end ? *a.csr_end : a.E;
@@ -253,7 +255,7 @@ __global__ __launch_bounds__(256) void tokenize_ln_kernel(TokLnArgs a, WidenRide
 #pragma unroll
   for (int i = 0; i < R; ++i) {
     const int64_t r = r0 + i;
-    e[i] = r < a.E ? (identity ? r : a.order[r]) : -1;
+    e[i] = r < a.E ? (identity ? r : wave_uniform(a.order[r])) : -1;
   }
   float4 gm[EPL / 4], bt[EPL / 4];
 #pragma unroll
@@ -268,9 +270,9 @@ __global__ __launch_bounds__(256) void tokenize_ln_kernel(TokLnArgs a, WidenRide
     if (r0 + i >= end || e[i] >= a.E) e[i] = -1;  // past the CSR end, or a corrupt order entry
     i0[i] = i1[i] = i2[i] = 0;
     if (e[i] >= 0) {
-      i0[i] = a.nid[e[i] * a.s_nid];
-      i1[i] = a.tb[e[i] * a.s_tb];
-      i2[i] = a.val[e[i] * a.s_val];
+      i0[i] = wave_uniform(a.nid[e[i] * a.s_nid]);
+      i1[i] = wave_uniform(a.tb[e[i] * a.s_tb]);
+      i2[i] = wave_uniform(a.val[e[i] * a.s_val]);
     }
   }
   const float* s0[R];

@@ -560,7 +560,9 @@ __global__ __launch_bounds__(256) void tokenize_csr_kernel(RowArgs a) {
   using V = Vec16<T>;
   constexpr int NV = V::N;
   const int lane = threadIdx.x & 63;
-  const int64_t r0 = ((int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6)) * R;
+  // the wavefront's rows, their events and table indices are alike in every lane: scalar
+  // registers and scalar address arithmetic
+  const int64_t r0 = ((int64_t)blockIdx.x * (blockDim.x >> 6) + wave_uniform((int)threadIdx.x >> 6)) * R;
   if (r0 >= a.E) return;
   const bool identity = !a.order || (a.ident && *a.ident);
   const int64_t end = a.csr_end ? *a.csr_end : a.E;
@@ -570,12 +572,13 @@ __global__ __launch_bounds__(256) void tokenize_csr_kernel(RowArgs a) {
     const int64_t r = r0 + i;
     e[i] = (r < a.E && r < end) ? (identity ? r : a.order[r]) : -1;
     if (e[i] >= a.E) e[i] = -1;  // defensive: never follow a corrupt order entry
+    e[i] = wave_uniform(e[i]);
   }
   int64_t id[R][3];
 #pragma unroll
   for (int i = 0; i < R; ++i)
 #pragma unroll
-    for (int t = 0; t < 3; ++t) id[i][t] = e[i] >= 0 ? a.ids[t][e[i] * a.ids_stride[t]] : 0;
+    for (int t = 0; t < 3; ++t) id[i][t] = e[i] >= 0 ? wave_uniform(a.ids[t][e[i] * a.ids_stride[t]]) : 0;
   const T* src[R][3];
 #pragma unroll
   for (int i = 0; i < R; ++i) {
