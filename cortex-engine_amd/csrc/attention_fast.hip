@@ -115,6 +115,7 @@ void attention_fast_kernel(AttnArgs a) {
   }
   if (a.kv_len) len = min(len, a.kv_len[b]);
   if (len < 0) len = 0;
+  len = wave_uniform(len);  // one (sample, head) per workgroup: the branches on it stay scalar
   const int nt = (int)cdiv(len, AF_KT);
 
   // Q fragments: query q0 + 16 qg + fr, head-dim slice [32 ks + 8 g, +8)
@@ -197,16 +198,30 @@ void attention_fast_kernel(AttnArgs a) {
   uint64_t pend = MASK ? wg_window(0) : 0;
 
   // ---- the loads of tile t (keys clamped to the sample) into stage j: the K transfer and
-  // this lane's two V rows (V^T is written from registers once they land)
+  // this lane's two V rows (V^T is written from registers once they land).  With 32 queries per
+  // wavefront a whole tile takes a uniform tile offset plus the lane's constant offsets (no
+  // per-lane multiply) and only the sample's last, partial tile clamps its rows; the 16-query
+  // form (128 VGPRs) has no registers to spare for the constants and clamps every tile.
+  const uint32_t k_lane = (uint32_t)(((int64_t)k_row * a.k_sl + k_col) * 2);
+  const int64_t va_lane = (int64_t)(2 * kp) * a.v_sl;
   auto issue_tile = [&](int t, int j, uint2& va, uint2& vb) {
     const int64_t k0 = (int64_t)t * AF_KT;
-    const int64_t kr = min(k0 + k_row, len - 1);
+    uint32_t koff;
+    const bf16 *pa, *pb;
+    if (QG == 2 && k0 + AF_KT <= len) {
+      koff = (uint32_t)(k0 * a.k_sl * 2) + k_lane;
+      pa = v_src + (k0 * a.v_sl + va_lane);
+      pb = pa + a.v_sl;
+    } else {
+      const int64_t kr = min(k0 + k_row, len - 1);
+      koff = (uint32_t)((kr * a.k_sl + k_col) * 2);
+      pa = v_src + min(k0 + 2 * kp, len - 1) * a.v_sl;
+      pb = v_src + min(k0 + 2 * kp + 1, len - 1) * a.v_sl;
+    }
     __builtin_amdgcn_raw_ptr_buffer_load_lds(
-        k_rsrc, (__attribute__((address_space(3))) void*)(k_stage(j) + wid * 1024), 16,
-        (int)(uint32_t)((kr * a.k_sl + k_col) * 2), 0, 0, 0);
-    const int64_t ka = min(k0 + 2 * kp, len - 1), kb = min(k0 + 2 * kp + 1, len - 1);
-    va = *reinterpret_cast<const uint2*>(v_src + ka * a.v_sl);
-    vb = *reinterpret_cast<const uint2*>(v_src + kb * a.v_sl);
+        k_rsrc, (__attribute__((address_space(3))) void*)(k_stage(j) + wid * 1024), 16, (int)koff, 0, 0, 0);
+    va = *reinterpret_cast<const uint2*>(pa);
+    vb = *reinterpret_cast<const uint2*>(pb);
     __builtin_amdgcn_sched_barrier(0);  // keep the issue order tile by tile (vmcnt below)
   };
   // V^T: dword (V[2kp][4dq+e], V[2kp+1][4dq+e]) into row 4dq+e, column kp of stage j
