@@ -45,6 +45,9 @@ _SIGNATURES = {
     "cortex_last_error": (ctypes.c_char_p, []),
     "cortex_pack_workspace_bytes": (_i64, [_i64, _i64]),
     "cortex_pack_plan": (_int, [_ptr, _i64, _i64, _i64, _ptr, _ptr, _ptr, _ptr, _ptr, _i64, _ptr, _ptr, _int, _ptr]),
+    "cortex_pack_plan_widen": (
+        _int, [_ptr, _i64, _i64, _i64, _ptr, _ptr, _ptr, _ptr, _ptr, _i64, _ptr, _ptr, _int, _int, _ptr, _ptr, _ptr,
+               _ptr]),
     "cortex_pack_noalloc_max_workspace_bytes": (_i64, []),
     "cortex_pack_plan_noalloc": (_int, [_ptr, _i64, _i64, _i64, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr]),
     "cortex_tokenize": (

@@ -52,7 +52,7 @@ def _row_major_2d(x: torch.Tensor) -> torch.Tensor:
 
 
 def pack_plan(batch_indices: torch.Tensor, batch_size: int, err: torch.Tensor | None = None, *,
-              with_rank: bool = True, identity: bool = False, clear_err: bool = False):
+              with_rank: bool = True, identity: bool = False, clear_err: bool = False, widen=None):
     """Stable CSR plan of ragged events: ``(offsets (B+1), order (E), rank (E))``.
 
     offsets/order/rank are int64 device tensors; see ``cortex_pack_plan``.  With
@@ -61,6 +61,8 @@ def pack_plan(batch_indices: torch.Tensor, batch_size: int, err: torch.Tensor | 
     plan of sorted indices sets it and leaves ``order`` unwritten, so ``order`` may only be
     handed on together with the flag (``tokenize`` / ``tokenize_ln`` take both).
     ``clear_err=True`` zeroes ``err`` inside the plan's first launch before anything ORs into it.
+    ``widen``: (int8, bf16) weight pairs widened by extra workgroups of the plan's first launch
+    (``widen_int8``).
     """
     dev = nat.require_gpu(batch_indices, what="pack_plan")
     if batch_indices.dtype != torch.int64 or batch_indices.dim() != 1:
@@ -73,9 +75,12 @@ def pack_plan(batch_indices: torch.Tensor, batch_size: int, err: torch.Tensor | 
     ident = torch.empty(1, dtype=torch.int32, device=dev) if identity else None
     ws_bytes = nat.load().cortex_pack_workspace_bytes(E, B)
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
-    nat.call("cortex_pack_plan", nat.ptr(batch_indices), batch_indices.stride(0) if E else 1, E, B,
-             nat.ptr(offsets), nat.ptr(order), None, nat.ptr(rank), nat.ptr(ws), ws_bytes, nat.ptr(err),
-             nat.ptr(ident), 1 if clear_err else 0, nat.stream_of(dev))
+    args = (nat.ptr(batch_indices), batch_indices.stride(0) if E else 1, E, B, nat.ptr(offsets), nat.ptr(order), None,
+            nat.ptr(rank), nat.ptr(ws), ws_bytes, nat.ptr(err), nat.ptr(ident), 1 if clear_err else 0)
+    if widen:
+        nat.call("cortex_pack_plan_widen", *args, *_widen_args(widen, dev), nat.stream_of(dev))
+    else:
+        nat.call("cortex_pack_plan", *args, nat.stream_of(dev))
     return (offsets, order, rank, ident) if identity else (offsets, order, rank)
 
 

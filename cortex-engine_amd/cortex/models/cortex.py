@@ -176,8 +176,11 @@ class CortexModel(nn.Module):
             batch_size = int(batch_indices.max().item()) + 1 if E > 0 else 1
         if check_indices and err_flag is None:
             err_flag = torch.empty(1, dtype=torch.int32, device=neuron_ids.device)
+        # INT8-resident window mode: the cross-attention's and the first block's weights widen into
+        # their windows in the plan's first launch, on the CUs its few workgroups leave idle
+        widen = self._window_rider()
         offsets, order, _, ident = ops.pack_plan(batch_indices, int(batch_size), err=err_flag, with_rank=False,
-                                                 identity=True, clear_err=clear_err or check_indices)
+                                                 identity=True, clear_err=clear_err or check_indices, widen=widen)
         out = self._forward_planned(neuron_ids, time_bins, values, offsets, order, int(batch_size), err_flag,
                                     aux=return_aux, identity=ident)
         if check_indices:
@@ -199,6 +202,7 @@ class CortexModel(nn.Module):
             raise ValueError(
                 f"shape mismatch: neuron_ids={neuron_ids.shape}, time_bins={time_bins.shape}, values={values.shape}")
         err_flag = _checked_flag(err_flag, check_indices, neuron_ids.device)
+        self._window_rider(take=False)
         out = self._forward_planned(neuron_ids, time_bins, values, offsets, None, offsets.shape[0] - 1,
                                     err_flag)["behavior"]
         if check_indices:
@@ -211,9 +215,6 @@ class CortexModel(nn.Module):
         (``r`` itself when ``order`` is None or the plan's ``identity`` flag is set); rows past
         ``offsets[B]`` are ignored."""
         enc = self.encoder
-        win = enc.weight_window()
-        if win is not None:  # every weight group this forward reads is widened again
-            win.reset()
         tokens = self._token_rows(neuron_ids, time_bins, values, offsets, order, err_flag, identity)
         x, xn = self._cross_rows(tokens, offsets, B)
         x = self._encode(x, B, xn)
@@ -221,6 +222,19 @@ class CortexModel(nn.Module):
         if aux and self.masked_spike_head is not None:
             out["masked_spike_logits"] = self.masked_spike_head.forward_rows(x, B, pre_norm=enc.final_norm)
         return out
+
+    def _window_rider(self, take: bool = True) -> list | None:
+        """Start of a forward in the INT8-resident window mode: nothing is resident yet (every
+        weight group this forward reads is widened again), and with ``take`` the weight pairs of
+        the cross-attention and the first block, for the forward's first launch to widen."""
+        win = self.encoder.weight_window()
+        if win is None:
+            return None
+        win.reset()
+        if not take:
+            return None
+        blocks = self.encoder.self_attn_blocks
+        return rider(self.encoder.cross_attn, blocks[0] if len(blocks) else None)
 
     def _token_rows(self, neuron_ids, time_bins, values, offsets, order, err_flag,
                     identity: torch.Tensor | None = None) -> tuple[torch.Tensor, bool]:
@@ -233,7 +247,7 @@ class CortexModel(nn.Module):
         if (cfg.compute_dtype == torch.bfloat16 and not xa.kv_proj._forward_pre_hooks
                 and fused_tokens_ok(tables, xa.norm_kv)):
             # the cross-attention's and the first block's weights widen into their windows in the
-            # same launch (INT8-resident window mode)
+            # same launch (INT8-resident window mode), unless the pack plan carried them
             blocks = self.encoder.self_attn_blocks
             widen = rider(xa, blocks[0] if len(blocks) else None)
             return ops.tokenize_ln(*tables, neuron_ids, time_bins, values, ln_params(xa.norm_kv), order=order,

@@ -157,23 +157,34 @@ __device__ __forceinline__ bf16x8 widen_i8x8(uint2 raw) {
   return v;
 }
 
-// Widening rider of a streaming row kernel: up to WR_MAX int8 arrays widened exactly to bf16
-// (dst[i][e] = src[i][e]) by the first `blocks` workgroups of the kernel's grid, each taking
-// WR_CHUNK consecutive elements of the concatenated arrays; the kernel's own rows follow.  The
-// row kernels are HBM-bound streams with idle issue slots, so a few MB of weights ride along for
-// about their transfer time and no launch of their own.  Element counts are multiples of 16 and
-// both arrays 16-byte aligned; the bf16 rows are written through (read by later kernels).
+// Widening rider of a launch: up to WR_MAX int8 arrays widened exactly to bf16
+// (dst[i][e] = src[i][e]) by `blocks` extra workgroups of the launch's grid, each taking
+// `chunk` consecutive elements of the concatenated arrays (WR_CHUNK, or WR_CHUNK_SMALL for a
+// launch whose own workgroups leave most CUs idle, so that the rider spreads over all of them).
+// The row kernels are HBM-bound streams with idle issue slots, so a few MB of weights ride along
+// for about their transfer time and no launch of their own.  Element counts are multiples of 16
+// and both arrays 16-byte aligned; the bf16 rows are written through (read by later kernels).
 constexpr int WR_MAX = 8;
-constexpr int64_t WR_CHUNK = 32768;
+constexpr int64_t WR_CHUNK = 32768, WR_CHUNK_SMALL = 8192;
 struct WidenRider {
   const int8_t* src[WR_MAX];
   bf16* dst[WR_MAX];
   int64_t end[WR_MAX];  // cumulative element counts
   int count;
-  int blocks;  // rider workgroups at the front of the grid (0: none)
+  int blocks;           // rider workgroups (0: none)
+  int64_t chunk;        // elements per rider workgroup
 };
+// One whole chunk with every load in flight before the stores (256 threads, U loads each).
+template <int U, class Put>
+__device__ __forceinline__ void widen_chunk(const int8_t* src, const Put& put) {
+  i32x4 raw[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) raw[u] = *reinterpret_cast<const i32x4*>(src + (u * 256 + threadIdx.x) * 16);
+#pragma unroll
+  for (int u = 0; u < U; ++u) put((u * 256 + threadIdx.x) * 16, raw[u]);
+}
 __device__ __forceinline__ void widen_rider_run(const WidenRider& r, int blk) {
-  const int64_t lo = (int64_t)blk * WR_CHUNK, hi = lo + WR_CHUNK;
+  const int64_t lo = (int64_t)blk * r.chunk, hi = lo + r.chunk;
   int64_t s0 = 0;
   for (int s = 0; s < r.count; ++s) {
     const int64_t s1 = r.end[s], a = lo > s0 ? lo : s0, b = hi < s1 ? hi : s1;
@@ -185,13 +196,10 @@ __device__ __forceinline__ void widen_rider_run(const WidenRider& r, int blk) {
         store(reinterpret_cast<bf16x8*>(dst + i), widen_i8x8(make_uint2((uint32_t)raw[0], (uint32_t)raw[1])));
         store(reinterpret_cast<bf16x8*>(dst + i + 8), widen_i8x8(make_uint2((uint32_t)raw[2], (uint32_t)raw[3])));
       };
-      if (b - a == WR_CHUNK && blockDim.x == 256) {  // a whole chunk: every load in flight first
-        constexpr int U = (int)(WR_CHUNK / (256 * 16));
-        i32x4 raw[U];
-#pragma unroll
-        for (int u = 0; u < U; ++u) raw[u] = *reinterpret_cast<const i32x4*>(src + (u * 256 + threadIdx.x) * 16);
-#pragma unroll
-        for (int u = 0; u < U; ++u) put((u * 256 + threadIdx.x) * 16, raw[u]);
+      if (b - a == WR_CHUNK && blockDim.x == 256) {
+        widen_chunk<(int)(WR_CHUNK / (256 * 16))>(src, put);
+      } else if (b - a == WR_CHUNK_SMALL && blockDim.x == 256) {
+        widen_chunk<(int)(WR_CHUNK_SMALL / (256 * 16))>(src, put);
       } else {
         for (int64_t i = threadIdx.x * 16; i < b - a; i += (int64_t)blockDim.x * 16)
           put(i, *reinterpret_cast<const i32x4*>(src + i));
@@ -199,6 +207,12 @@ __device__ __forceinline__ void widen_rider_run(const WidenRider& r, int blk) {
     }
     s0 = s1;
   }
+}
+// The rider re-cut into workgroups of `chunk` elements.
+inline void rider_chunk(WidenRider& r, int64_t chunk) {
+  const int64_t total = r.count ? r.end[r.count - 1] : 0;
+  r.chunk = chunk;
+  r.blocks = (int)((total + chunk - 1) / chunk);
 }
 
 // A value every lane of the wavefront holds alike (a row index, a loaded table index), moved to
@@ -322,6 +336,12 @@ enum Status : int {
   E_WORKSPACE = -4,    // workspace too small
 };
 void set_error(const char* fmt, ...);
+// Widening riders (rowops.hip): build one from the C-ABI arrays (0 or a negative status), and
+// launch one on a grid of its own.
+struct WidenRider;
+int make_rider(const char* who, int n, const void* const* src, void* const* dst, const int64_t* count,
+               WidenRider* r);
+int widen_launch(const WidenRider& wr, hipStream_t stream);
 }  // namespace cortex
 
 #define CORTEX_CHECK_ARG(cond, ...)          \

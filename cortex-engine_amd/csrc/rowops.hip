@@ -360,8 +360,15 @@ int make_rider(const char* who, int n, const void* const* src, void* const* dst,
     r->end[r->count] = total;
     ++r->count;
   }
-  CORTEX_CHECK_ARG(cdiv(total, WR_CHUNK) <= (1 << 24), "%s: %lld elements to widen", who, (long long)total);
-  r->blocks = (int)cdiv(total, WR_CHUNK);
+  CORTEX_CHECK_ARG(cdiv(total, WR_CHUNK_SMALL) <= (1 << 24), "%s: %lld elements to widen", who, (long long)total);
+  rider_chunk(*r, WR_CHUNK);
+  return OK;
+}
+
+int widen_launch(const WidenRider& wr, hipStream_t stream) {
+  if (wr.blocks == 0) return OK;
+  hipLaunchKernelGGL(widen_kernel, dim3((unsigned)wr.blocks), dim3(256), 0, stream, wr);
+  CORTEX_CHECK_LAUNCH("widen_kernel");
   return OK;
 }
 
@@ -514,10 +521,7 @@ int cortex_widen_int8(int n, const void* const* src, void* const* dst, const int
   WidenRider wr;
   const int st = make_rider("cortex_widen_int8", n, src, dst, count, &wr);
   if (st != OK) return st;
-  if (wr.blocks == 0) return OK;
-  hipLaunchKernelGGL(widen_kernel, dim3((unsigned)wr.blocks), dim3(256), 0, stream, wr);
-  CORTEX_CHECK_LAUNCH("widen_kernel");
-  return OK;
+  return widen_launch(wr, stream);
 }
 
 int cortex_norm_rows(int64_t M, int64_t K, int x_dtype, const void* x, int64_t ld_x, int norm, const void* gamma,

@@ -273,7 +273,14 @@ __global__ __launch_bounds__(PS_SORTED_EV) void pack_sorted_kernel(const int64_t
                                                                    int64_t E, int B, int64_t* __restrict__ offsets,
                                                                    int64_t* __restrict__ order,
                                                                    int64_t* __restrict__ dst_rows,
-                                                                   int* __restrict__ status, int32_t* clear_err) {
+                                                                   int* __restrict__ status, int32_t* clear_err,
+                                                                   WidenRider wr) {
+  // the plan's workgroups first; a widening rider's after them, on the CUs the plan leaves idle
+  const int nplan = (int)gridDim.x - wr.blocks;
+  if ((int)blockIdx.x >= nplan) {
+    widen_rider_run(wr, (int)blockIdx.x - nplan);
+    return;
+  }
   __shared__ int bad;
   if (threadIdx.x == 0) bad = 0;
   if (clear_err && blockIdx.x == 0 && threadIdx.x == 0) clear_err_word(clear_err, &bad);
@@ -292,7 +299,11 @@ __global__ __launch_bounds__(1024) void pack_small_kernel(const int64_t* __restr
                                                           int64_t* __restrict__ rank, int32_t* __restrict__ err,
                                                           const int* __restrict__ status, int n_status,
                                                           bool try_sorted, int32_t* __restrict__ ident,
-                                                          bool clear_err) {
+                                                          bool clear_err, WidenRider wr) {
+  if (blockIdx.x > 0) {  // workgroup 0 is the plan; any others carry a widening rider
+    widen_rider_run(wr, (int)blockIdx.x - 1);
+    return;
+  }
   __shared__ int cnt[PS_WAVES * PS_MAX_B];  // per-wave counts, then per-wave next CSR row
   __shared__ int first[PS_MAX_B];           // CSR offset of each sample
   __shared__ int wsum[PS_WAVES];
@@ -685,7 +696,7 @@ int64_t cortex_pack_workspace_bytes(int64_t E, int64_t B) {
 static int pack_plan_impl(const char* who, const int64_t* batch_indices, int64_t s_bidx, int64_t E, int64_t B,
                           int64_t* offsets, int64_t* order, int64_t* dst_rows, int64_t* rank, void* workspace,
                           int64_t workspace_bytes, int32_t* err_flag, int32_t* identity, int flags,
-                          hipStream_t stream) {
+                          hipStream_t stream, const WidenRider& wr = WidenRider{}) {
   const bool clear = (flags & PACK_FLAG_CLEAR_ERR) && err_flag != nullptr;
   CORTEX_CHECK_ARG(E >= 0 && B >= 1, "%s: need E >= 0 and B >= 1 (got E=%lld B=%lld)", who, (long long)E,
                    (long long)B);
@@ -703,7 +714,7 @@ static int pack_plan_impl(const char* who, const int64_t* batch_indices, int64_t
       hipLaunchKernelGGL(fill_i32_kernel, dim3(1), dim3(64), 0, stream, identity, (int64_t)1, 1);
       CORTEX_CHECK_LAUNCH("cortex_pack_plan(E=0)");
     }
-    return OK;
+    return widen_launch(wr, stream);
   }
   CORTEX_CHECK_ARG(batch_indices && order, "%s: batch_indices and order must not be null", who);
   const int64_t need = cortex_pack_workspace_bytes(E, B);
@@ -719,16 +730,18 @@ static int pack_plan_impl(const char* who, const int64_t* batch_indices, int64_t
     int* status = nullptr;
     const int n_status = (int)cdiv(E, (int64_t)PS_SORTED_EV);
     const bool one = rank == nullptr && E <= PS_ONE_E;
+    // a widening rider joins the plan's first launch
     if (rank == nullptr && !one && workspace != nullptr && workspace_bytes >= n_status * (int64_t)sizeof(int)) {
       status = reinterpret_cast<int*>(workspace);
-      hipLaunchKernelGGL(pack_sorted_kernel, dim3((unsigned)n_status), dim3(PS_SORTED_EV), 0, stream, batch_indices,
-                         s_bidx, E, (int)B, offsets, identity ? nullptr : order, dst_rows, status,
-                         clear ? err_flag : nullptr);
+      hipLaunchKernelGGL(pack_sorted_kernel, dim3((unsigned)(n_status + wr.blocks)), dim3(PS_SORTED_EV), 0, stream,
+                         batch_indices, s_bidx, E, (int)B, offsets, identity ? nullptr : order, dst_rows, status,
+                         clear ? err_flag : nullptr, wr);
       CORTEX_CHECK_LAUNCH("pack_sorted_kernel");
     }
-    hipLaunchKernelGGL(pack_small_kernel, dim3(1), dim3(64 * PS_WAVES), 0, stream, batch_indices, s_bidx, E, (int)B,
-                       offsets, order, dst_rows, rank, err_flag, status, n_status, one, identity,
-                       clear && status == nullptr);
+    const WidenRider& wr_small = status ? WidenRider{} : wr;
+    hipLaunchKernelGGL(pack_small_kernel, dim3((unsigned)(1 + wr_small.blocks)), dim3(64 * PS_WAVES), 0, stream,
+                       batch_indices, s_bidx, E, (int)B, offsets, order, dst_rows, rank, err_flag, status, n_status,
+                       one, identity, clear && status == nullptr, wr_small);
     CORTEX_CHECK_LAUNCH("pack_small_kernel");
     return OK;
   }
@@ -741,13 +754,17 @@ static int pack_plan_impl(const char* who, const int64_t* batch_indices, int64_t
   const int n_status = (int)cdiv(E, (int64_t)PS_SORTED_EV);
   if (rank == nullptr) {
     status = counts + (int64_t)nchunks * B;
-    hipLaunchKernelGGL(pack_sorted_kernel, dim3((unsigned)n_status), dim3(PS_SORTED_EV), 0, stream, batch_indices,
-                       s_bidx, E, (int)B, offsets, identity ? nullptr : order, dst_rows, status,
-                       clear ? err_flag : nullptr);
+    hipLaunchKernelGGL(pack_sorted_kernel, dim3((unsigned)(n_status + wr.blocks)), dim3(PS_SORTED_EV), 0, stream,
+                       batch_indices, s_bidx, E, (int)B, offsets, identity ? nullptr : order, dst_rows, status,
+                       clear ? err_flag : nullptr, wr);
     CORTEX_CHECK_LAUNCH("pack_sorted_kernel");
-  } else if (clear) {
-    hipLaunchKernelGGL(fill_i32_kernel, dim3(1), dim3(64), 0, stream, err_flag, (int64_t)1, 0);
-    CORTEX_CHECK_LAUNCH("cortex_pack_plan(clear)");
+  } else {
+    if (clear) {
+      hipLaunchKernelGGL(fill_i32_kernel, dim3(1), dim3(64), 0, stream, err_flag, (int64_t)1, 0);
+      CORTEX_CHECK_LAUNCH("cortex_pack_plan(clear)");
+    }
+    const int st = widen_launch(wr, stream);
+    if (st != OK) return st;
   }
   hipLaunchKernelGGL(pack_count_kernel, dim3(nchunks), dim3(256), 0, stream, batch_indices, s_bidx, E, (int)B, C,
                      counts, err_flag, status, n_status);
@@ -808,6 +825,19 @@ int cortex_pack_plan(const int64_t* batch_indices, int64_t s_bidx, int64_t E, in
                      int32_t* err_flag, int32_t* identity, int flags, hipStream_t stream) {
   return pack_plan_impl("cortex_pack_plan", batch_indices, s_bidx, E, B, offsets, order, dst_rows, rank, workspace,
                         workspace_bytes, err_flag, identity, flags, stream);
+}
+
+int cortex_pack_plan_widen(const int64_t* batch_indices, int64_t s_bidx, int64_t E, int64_t B, int64_t* offsets,
+                           int64_t* order, int64_t* dst_rows, int64_t* rank, void* workspace,
+                           int64_t workspace_bytes, int32_t* err_flag, int32_t* identity, int flags, int n_widen,
+                           const void* const* widen_src, void* const* widen_dst, const int64_t* widen_count,
+                           hipStream_t stream) {
+  WidenRider wr;
+  const int st = make_rider("cortex_pack_plan_widen", n_widen, widen_src, widen_dst, widen_count, &wr);
+  if (st != OK) return st;
+  rider_chunk(wr, WR_CHUNK_SMALL);  // the plan holds a few CUs: the rider takes all the others
+  return pack_plan_impl("cortex_pack_plan_widen", batch_indices, s_bidx, E, B, offsets, order, dst_rows, rank,
+                        workspace, workspace_bytes, err_flag, identity, flags, stream, wr);
 }
 
 int64_t cortex_pack_noalloc_max_workspace_bytes(void) { return PACK_SCRATCH_BYTES; }

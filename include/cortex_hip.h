@@ -59,6 +59,14 @@ int cortex_pack_plan(const int64_t* batch_indices, int64_t s_bidx, int64_t E, in
                      int64_t* order, int64_t* dst_rows, int64_t* rank, void* workspace, int64_t workspace_bytes,
                      int32_t* err_flag, int32_t* identity, int flags, hipStream_t stream);
 #define CORTEX_PACK_CLEAR_ERR 1
+/* cortex_pack_plan with a widening rider (see cortex_widen_int8): up to 8 int8 arrays widened
+ * to bf16 by extra workgroups of the plan's first launch, on the CUs that the plan (a few
+ * workgroups) leaves idle.  The plan itself is exactly cortex_pack_plan's. */
+int cortex_pack_plan_widen(const int64_t* batch_indices, int64_t s_bidx, int64_t E, int64_t B, int64_t* offsets,
+                           int64_t* order, int64_t* dst_rows, int64_t* rank, void* workspace,
+                           int64_t workspace_bytes, int32_t* err_flag, int32_t* identity, int flags, int n_widen,
+                           const void* const* widen_src, void* const* widen_dst, const int64_t* widen_count,
+                           hipStream_t stream);
 
 /* cortex_pack_plan without a workspace argument and without any allocation.  No
  * counterpart in the reference: it is for callers that cannot allocate device memory

@@ -336,9 +336,10 @@ def test_widen_mode_streams_int8_weights_through_the_fused_path(monkeypatch):
 def test_window_mode_widens_each_block_in_the_row_kernel_ahead_of_it(monkeypatch):
     """CORTEX_INT8_WEIGHTS=window: only the int8 weights stay resident, plus two bf16 windows (the
     cross-attention's kv / out projections; one self-attention block's four linears, which the
-    blocks take in turn).  In a forward the tokenizer + LayerNorm launch widens the
-    cross-attention's and the first block's weights and each later block's LayerNorm row launch
-    its own, with no widening launch of its own.  Config-3 shape: bit-identical to the image mode
+    blocks take in turn).  In a forward the pack plan's first launch widens the cross-attention's
+    and the first block's weights (the tokenizer + LayerNorm launch does when the caller hands
+    over a CSR plan) and each later block's LayerNorm row launch its own, with no widening launch
+    of its own.  Config-3 shape: bit-identical to the image mode
     (the same bf16 weight values reach the same kernels), eager and replayed from a graph."""
     from cortex.kernels import ops
     from cortex.models import _layers
@@ -348,8 +349,8 @@ def test_window_mode_widens_each_block_in_the_row_kernel_ahead_of_it(monkeypatch
     inputs = [torch.from_numpy(a).to(DEV) for a in arrs]
     monkeypatch.setattr(_layers, "INT8_WEIGHTS", "window")
     model = _int8(_model("s", "bfloat16"), [t[:2048] for t in inputs])
-    seen = {"alone": 0, "tokenize_ln": [], "ln_rows": []}
-    orig_w, orig_t, orig_l = ops.widen_int8, ops.tokenize_ln, ops.ln_rows
+    seen = {"alone": 0, "pack_plan": [], "tokenize_ln": [], "ln_rows": []}
+    orig_w, orig_t, orig_l, orig_p = ops.widen_int8, ops.tokenize_ln, ops.ln_rows, ops.pack_plan
 
     def widen_spy(pairs):
         seen["alone"] += 1
@@ -362,16 +363,27 @@ def test_window_mode_widens_each_block_in_the_row_kernel_ahead_of_it(monkeypatch
     def ln_spy(*a, widen=None, **k):
         seen["ln_rows"].append(len(widen or []))
         return orig_l(*a, widen=widen, **k)
+
+    def plan_spy(*a, widen=None, **k):
+        seen["pack_plan"].append(len(widen or []))
+        return orig_p(*a, widen=widen, **k)
     monkeypatch.setattr(ops, "widen_int8", widen_spy)
+    monkeypatch.setattr(ops, "pack_plan", plan_spy)
     monkeypatch.setattr(ops, "tokenize_ln", tok_spy)
     monkeypatch.setattr(ops, "ln_rows", ln_spy)
     with torch.no_grad():
         model(*inputs, batch_size=32)  # caches the batch-invariant query projections
-        seen.update(alone=0, tokenize_ln=[], ln_rows=[])
+        seen.update(alone=0, pack_plan=[], tokenize_ln=[], ln_rows=[])
         win = model(*inputs, batch_size=32)["behavior"].clone()
         win2 = model(*inputs, batch_size=32)["behavior"].clone()
-    assert seen["alone"] == 0, seen
-    assert seen["tokenize_ln"] == [2 + 4] * 2 and seen["ln_rows"] == [4] * 12, seen
+        assert seen["alone"] == 0, seen
+        assert seen["pack_plan"] == [2 + 4] * 2 and seen["tokenize_ln"] == [0] * 2, seen
+        assert seen["ln_rows"] == [4] * 12, seen
+        # a caller-built CSR plan (the serving path): the tokenizer launch carries them instead
+        offs = torch.arange(0, 32 * 512 + 1, 512, device=DEV)
+        seen.update(alone=0, pack_plan=[], tokenize_ln=[], ln_rows=[])
+        csr = model.forward_csr(*inputs[:3], offs).clone()
+        assert seen["alone"] == 0 and seen["pack_plan"] == [] and seen["tokenize_ln"] == [2 + 4], seen
     wb = _layers.resident_weight_bytes(model)
     D = 512
     assert wb["bf16_images"] == 0
@@ -406,6 +418,7 @@ def test_window_mode_widens_each_block_in_the_row_kernel_ahead_of_it(monkeypatch
     assert _layers.resident_weight_bytes(model)["bf16_images"] > 2 * wb["bf16_windows"]
     torch.testing.assert_close(win, win2, rtol=0, atol=0)
     torch.testing.assert_close(win, image, rtol=0, atol=0)
+    torch.testing.assert_close(csr, image, rtol=0, atol=0)
     torch.testing.assert_close(graph, image, rtol=0, atol=0)
     torch.testing.assert_close(y_win, y_img, rtol=0, atol=0)
     torch.testing.assert_close(y2_win, y2_img, rtol=0, atol=0)
