@@ -305,3 +305,34 @@ def test_pack_plan_sorted_fast_path(name):
     if not sorted_ok:
         n = int(p.offsets[-1])
         np.testing.assert_array_equal(order.cpu().numpy()[:n], np.flatnonzero(valid)[p.order])
+
+
+@pytest.mark.parametrize("E,B,shuffle,rank", [(0, 4, False, False), (3000, 8, False, False), (3000, 8, True, False),
+                                              (16384, 32, False, False), (16384, 32, True, False),
+                                              (70000, 2000, False, False), (70000, 2000, True, True)])
+def test_pack_plan_widen_rider(E, B, shuffle, rank):
+    """cortex_pack_plan_widen on every plan path (one launch up to 4096 events, the wide sorted
+    check, the three-launch plan with and without ranks, no events): the plan is exactly the
+    one without a rider, and the rider's int8 arrays (ragged sizes, one not a whole workgroup
+    chunk) come out widened exactly."""
+    from cortex.kernels import ops
+
+    g = torch.Generator().manual_seed(E + B)
+    bidx = torch.sort(torch.randint(0, B, (E,), generator=g)).values
+    if shuffle:
+        bidx = bidx[torch.randperm(E, generator=g)]
+    bidx = bidx.to(DEV)
+    src = [torch.randint(-127, 128, (n,), generator=g, dtype=torch.int8).to(DEV) for n in (262144, 8192 + 48, 16)]
+    dst = [torch.zeros(s.shape, dtype=torch.bfloat16, device=DEV) for s in src]
+    want = ops.pack_plan(bidx, B, with_rank=rank, identity=not rank)
+    got = ops.pack_plan(bidx, B, with_rank=rank, identity=not rank, widen=list(zip(src, dst)))
+    torch.cuda.synchronize()
+    if not rank:
+        assert int(got[3].item()) == int(want[3].item())
+    assert torch.equal(got[0], want[0])
+    if rank or not int(want[3].item()):  # order is written unless the identity flag is set
+        assert torch.equal(got[1], want[1])
+    if rank:
+        assert torch.equal(got[2], want[2])
+    for s, d in zip(src, dst):
+        assert torch.equal(d, s.to(torch.bfloat16))
