@@ -400,3 +400,43 @@ def test_split_k_residual_linears(M, N, K, splits, res_rows, ln):
         err = (xn.cpu().float() - lnr).abs()
         assert (err <= _bf16_ulp(lnr) + 1e-5 * float(lnr.abs().max())).all(), float(err.max())
 
+
+
+def _rider(sizes, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    src = [torch.randint(-127, 128, (n,), generator=g, dtype=torch.int8).to(DEV) for n in sizes]
+    return src, [torch.full(s.shape, 7.0, dtype=torch.bfloat16, device=DEV) for s in src]
+
+
+@pytest.mark.parametrize("sizes", [(16,), (32768,), (32768 * 3 + 16, 48, 65536), tuple([4096 + 16 * i for i in range(8)])])
+def test_widen_riders_exact_and_rows_unchanged(sizes):
+    """int8 -> bf16 widening (exact: every int8 value is a bf16 value) on a launch of its own and
+    riding on the LayerNorm row kernel and on the tokenizer + LayerNorm kernel: whole and partial
+    workgroup chunks, up to 8 arrays; the host kernels' own rows are bit-identical with and
+    without the rider."""
+    from cortex.kernels import ops
+
+    src, dst = _rider(sizes)
+    ops.widen_int8(list(zip(src, dst)))
+    torch.cuda.synchronize()
+    for s, d in zip(src, dst):
+        assert torch.equal(d, s.to(torch.bfloat16))
+    g = torch.Generator().manual_seed(1)
+    x = torch.randn(1000, 512, generator=g).to(DEV)
+    ln = (torch.randn(512, generator=g).to(DEV), torch.randn(512, generator=g).to(DEV), 1e-5)
+    src, dst = _rider(sizes, 2)
+    ref = ops.ln_rows(x, ln)
+    out = ops.ln_rows(x, ln, widen=list(zip(src, dst)))
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref)
+    for s, d in zip(src, dst):
+        assert torch.equal(d, s.to(torch.bfloat16))
+    tabs = [torch.randn(n, 512, generator=g).mul(0.02).to(DEV) for n in (137, 600, 8)]
+    ids = [torch.randint(0, n, (777,), generator=g).to(DEV) for n in (137, 600, 8)]
+    src, dst = _rider(sizes, 3)
+    ref = ops.tokenize_ln(*tabs, *ids, ln)
+    out = ops.tokenize_ln(*tabs, *ids, ln, widen=list(zip(src, dst)))
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref)
+    for s, d in zip(src, dst):
+        assert torch.equal(d, s.to(torch.bfloat16))
