@@ -138,13 +138,16 @@ def make_kernel(name: str, dev):
     if name == "out_residual_ln":
         a = rnd(M_ROWS, D, dtype=bf)
         w, sc = _int8_image(D, D, dev, 3)
+        wf = ops.frag_weight(w)  # the forward's layout for this kernel (bf16 images)
         res = rnd(M_ROWS, D)
         g_, b_ = rnd(D), rnd(D)
-        fn = lambda: ops.linear_residual_ln(a, w, sc, None, residual=res, ln=(g_, b_, 1e-5), out=res)  # noqa: E731
+        fn = lambda: ops.linear_residual_ln(a, wf, sc, None, residual=res, ln=(g_, b_, 1e-5), out=res,  # noqa: E731
+                                            frag=True)
         fl = 2.0 * M_ROWS * D * D
         by = M_ROWS * D * 2 + D * D + 4 * D + M_ROWS * D * 4 * 2 + M_ROWS * D * 2 + 2 * D * 4
         return fn, 8, "hbm", fl, by, ("attention out 512->512 + fp32 residual + the next LayerNorm, M=8192 "
-                                      "(gemm_rowln_kernel, 32-row full-width tiles)")
+                                      "(gemm_rowln_dw_kernel: 32-row full-width tiles, each wavefront's weight "
+                                      "rows straight into registers)")
     if name == "attention_cross":
         E = B_MAIN * PER_MAIN
         kv = rnd(E, 2 * D, dtype=bf)

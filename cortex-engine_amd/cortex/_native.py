@@ -21,8 +21,9 @@ class NativeLibraryError(RuntimeError):
     """The Cortex HIP library is missing, failed to load, or a kernel call failed."""
 
 
-# dtype codes of include/cortex_hip.h
-F32, BF16, F16, I8, I32, I64, U8 = 0, 1, 2, 3, 4, 5, 6
+# dtype codes of include/cortex_hip.h; BF16_FRAG is a weight layout code (bf16 weights in MFMA
+# fragment order, written by cortex_frag_weight), not a tensor dtype
+F32, BF16, F16, I8, I32, I64, U8, BF16_FRAG = 0, 1, 2, 3, 4, 5, 6, 7
 DTYPE_CODE = {
     torch.float32: F32,
     torch.bfloat16: BF16,
@@ -120,6 +121,7 @@ _SIGNATURES = {
     "cortex_norm_rows": (_int, [_i64, _i64, _int, _ptr, _i64, _int, _ptr, _ptr, _int, _f32, _ptr, _i64, _ptr]),
     "cortex_transpose_bf16": (_int, [_i64, _i64, _ptr, _i64, _ptr, _i64, _ptr]),
     "cortex_fold_gain": (_int, [_i64, _i64, _ptr, _int, _int, _i64, _ptr, _int, _ptr, _i64, _ptr]),
+    "cortex_frag_weight": (_int, [_i64, _i64, _ptr, _int, _i64, _ptr, _ptr]),
     "cortex_splitk_workspace_bytes": (_i64, [_i64, _i64, _i64]),
     "cortex_linear_residual_splitk": (
         _int, [_i64, _i64, _i64, _ptr, _i64, _ptr, _i64, _ptr, _ptr, _ptr, _i64, _i64, _ptr, _i64, _i64, _ptr, _i64,

@@ -314,30 +314,53 @@ def qkv_attention(xn: torch.Tensor, weight: torch.Tensor, weight_scale, bias, ba
     return out
 
 
+def frag_weight(weight: torch.Tensor) -> torch.Tensor:
+    """The (N, K) weight (int8, bf16 or fp32) as bf16 in MFMA fragment order
+    (``cortex_frag_weight``), shape (N, K) but not row-major: only ``linear_residual_ln(...,
+    frag=True)`` reads it.  Values exactly those of ``convert(weight, torch.bfloat16)``."""
+    dev = nat.require_gpu(weight, what="frag_weight")
+    w2 = _row_major_2d(weight)
+    N, K = w2.shape
+    out = torch.empty((N, K), dtype=torch.bfloat16, device=dev)
+    nat.call("cortex_frag_weight", N, K, nat.ptr(w2), nat.code(w2.dtype), w2.stride(0), nat.ptr(out),
+             nat.stream_of(dev))
+    return out
+
+
+def frag_ok(M: int, N: int, K: int, device: torch.device) -> bool:
+    """Whether ``linear_residual_ln`` takes a fragment-order weight at this shape (the
+    direct-weight kernel: K 256 or 512, and rows enough that no K split applies)."""
+    return N in (256, 512) and K in (256, 512) and not splitk_splits(M, N, K, device)
+
+
 def linear_residual_ln(x: torch.Tensor, weight: torch.Tensor, weight_scale=None, bias=None, *,
                        residual: torch.Tensor, ln, res_rows: int = 0, out: torch.Tensor | None = None,
-                       xq_scale: float | None = None):
+                       xq_scale: float | None = None, frag: bool = False):
     """``out = residual + x @ (weight * scale)^T + bias`` (fp32) and ``LN(out)`` (bf16) in one
-    kernel; ``x`` (M, K) bf16, ``weight`` (N, K) the bf16 image or the int8 weight itself
-    (widened in the kernel), N in {256, 512}.  ``out`` may be ``residual`` itself.  Returns
-    ``(out, xn)``.  With ``xq_scale`` (the W8A8 mode) ``xn`` is int8:
+    kernel; ``x`` (M, K) bf16, ``weight`` (N, K) the bf16 image, the int8 weight itself
+    (widened in the kernel) or, with ``frag``, ``frag_weight``'s fragment-order bf16 copy (see
+    ``frag_ok``), N in {256, 512}.  ``out`` may be ``residual`` itself.  Returns ``(out, xn)``.
+    With ``xq_scale`` (the W8A8 mode) ``xn`` is int8:
     ``clamp(rint(LN(out) * (1 / xq_scale)), -127, 127)``."""
     dev = nat.require_gpu(x, weight, weight_scale, bias, residual, out, what="linear_residual_ln")
     M, K = x.shape
     N = weight.shape[0]
+    if frag and not frag_ok(M, N, K, dev):
+        raise ValueError(f"a fragment-order weight does not apply at M={M}, N={N}, K={K}")
+    w_code = nat.BF16_FRAG if frag else nat.code(weight.dtype)
     if out is None:
         out = torch.empty((M, N), dtype=torch.float32, device=dev)
     g, b, eps = ln
     if xq_scale is not None:
         xq = torch.empty((M, N), dtype=torch.int8, device=dev)
-        nat.call("cortex_linear_residual_ln_i8", M, N, K, nat.ptr(x), x.stride(0), nat.code(weight.dtype),
+        nat.call("cortex_linear_residual_ln_i8", M, N, K, nat.ptr(x), x.stride(0), w_code,
                  nat.ptr(weight), weight.stride(0),
                  nat.ptr(weight_scale), nat.ptr(bias), nat.ptr(residual), residual.stride(0), int(res_rows),
                  nat.ptr(out), out.stride(0), nat.ptr(g), nat.ptr(b), float(eps), nat.ptr(xq), xq.stride(0),
                  float(xq_scale), nat.stream_of(dev))
         return out, xq
     xn = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
-    splits = splitk_splits(M, N, K, dev) if weight.dtype == torch.bfloat16 else 0
+    splits = splitk_splits(M, N, K, dev) if weight.dtype == torch.bfloat16 and not frag else 0
     if splits:  # few rows: K split across workgroups, slabs summed in order, then the LayerNorm
         ws_t = torch.empty(nat.load().cortex_splitk_workspace_bytes(M, N, splits), dtype=torch.uint8, device=dev)
         nat.call("cortex_linear_residual_ln_splitk", M, N, K, nat.ptr(x), x.stride(0), nat.ptr(weight),
@@ -345,7 +368,7 @@ def linear_residual_ln(x: torch.Tensor, weight: torch.Tensor, weight_scale=None,
                  int(res_rows), nat.ptr(out), out.stride(0), nat.ptr(g), nat.ptr(b), float(eps), nat.ptr(xn),
                  xn.stride(0), splits, nat.ptr(ws_t), ws_t.numel(), nat.stream_of(dev))
         return out, xn
-    nat.call("cortex_linear_residual_ln", M, N, K, nat.ptr(x), x.stride(0), nat.code(weight.dtype), nat.ptr(weight),
+    nat.call("cortex_linear_residual_ln", M, N, K, nat.ptr(x), x.stride(0), w_code, nat.ptr(weight),
              weight.stride(0),
              nat.ptr(weight_scale), nat.ptr(bias), nat.ptr(residual), residual.stride(0), int(res_rows),
              nat.ptr(out), out.stride(0), nat.ptr(g), nat.ptr(b), float(eps), nat.ptr(xn), xn.stride(0),

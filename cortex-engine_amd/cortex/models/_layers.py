@@ -178,6 +178,21 @@ def fused_weight(lin: nn.Module) -> tuple:
     return w["weight"], w["weight_scale"], w["bias"]
 
 
+def frag_image(lin: nn.Module) -> torch.Tensor:
+    """The linear's weight as bf16 in MFMA fragment order (``ops.frag_weight``), built once per
+    weight state and cached on the module like the bf16 image (the direct-weight residual
+    LayerNorm kernel streams it; same values as the image)."""
+    src = lin.weight_int8 if hasattr(lin, "weight_int8") else lin.weight
+    key = (src.data_ptr(), src._version, tuple(src.shape), src.device)
+    cached = lin.__dict__.get("_cortex_frag")
+    if cached is None or cached[0] != key:
+        if ops.capturing_graph():  # only recorded now: the graph rebuilds it on every replay, nothing cached
+            return ops.frag_weight(src)
+        cached = (key, ops.frag_weight(src))
+        lin.__dict__["_cortex_frag"] = cached
+    return cached[1]
+
+
 def bf16_weight(lin: nn.Module) -> tuple:
     """``(bf16 weight, weight_scale)`` for one-time preparation kernels that read bf16 rows:
     the cached image, or in the widen and window modes a temporary widened copy (not kept)."""
@@ -193,9 +208,10 @@ def resident_weight_bytes(model: nn.Module) -> dict:
     own = sum(t.numel() * t.element_size() for t in list(model.parameters()) + list(model.buffers()))
     images = 0
     for m in model.modules():
-        c = m.__dict__.get("_cortex_exec")
-        if c is not None:
-            images += c[1].numel() * c[1].element_size()
+        for name in ("_cortex_exec", "_cortex_frag"):
+            c = m.__dict__.get(name)
+            if c is not None:
+                images += c[1].numel() * c[1].element_size()
     windows = {id(w): w.bytes for m in model.modules() if (w := m.__dict__.get("_cortex_window")) is not None}
     window = sum(windows.values())
     int8 = sum(b.numel() for n, b in model.named_buffers() if n.endswith("weight_int8"))
@@ -293,7 +309,15 @@ def residual_ln_ok(lin: nn.Module, norm: nn.LayerNorm, consumer: nn.Module, x: t
 def linear_residual_ln(lin: nn.Module, a: torch.Tensor, residual: torch.Tensor, norm: nn.LayerNorm, *,
                        res_rows: int = 0, out: torch.Tensor | None = None, xq_scale: float | None = None):
     """``x = residual + lin(a)`` (fp32) and ``norm(x)`` (bf16; int8 at ``xq_scale`` when given)
-    in one launch (see ``residual_ln_ok``).  Returns ``(x, norm(x))``."""
+    in one launch (see ``residual_ln_ok``).  Returns ``(x, norm(x))``.  With bf16 images (the
+    default INT8 mode) the weight goes in MFMA fragment order where the direct-weight kernel
+    takes it (``ops.frag_ok``)."""
+    src = lin.weight_int8 if hasattr(lin, "weight_int8") else lin.weight
+    if (not (hasattr(lin, "weight_int8") and INT8_WEIGHTS != "image")
+            and ops.frag_ok(a.shape[0], src.shape[0], src.shape[1], a.device)):
+        return ops.linear_residual_ln(a, frag_image(lin), lin.weight_scale if hasattr(lin, "weight_int8") else None,
+                                      lin.bias, residual=residual, ln=ln_params(norm), res_rows=res_rows, out=out,
+                                      xq_scale=xq_scale, frag=True)
     w, scale, bias = fused_weight(lin)
     return ops.linear_residual_ln(a, w, scale, bias, residual=residual, ln=ln_params(norm), res_rows=res_rows,
                                   out=out, xq_scale=xq_scale)

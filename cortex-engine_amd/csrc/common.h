@@ -26,8 +26,9 @@ typedef float f32x8 __attribute__((ext_vector_type(8)));
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef int i32x2 __attribute__((ext_vector_type(2)));
 
-// dtype codes shared with include/cortex_hip.h
-enum DType : int { DT_F32 = 0, DT_BF16 = 1, DT_F16 = 2, DT_I8 = 3, DT_I32 = 4, DT_I64 = 5, DT_U8 = 6 };
+// dtype codes shared with include/cortex_hip.h; DT_BF16_FRAG is a weight layout code, not a
+// tensor dtype: bf16 weights in MFMA fragment order (cortex_frag_weight)
+enum DType : int { DT_F32 = 0, DT_BF16 = 1, DT_F16 = 2, DT_I8 = 3, DT_I32 = 4, DT_I64 = 5, DT_U8 = 6, DT_BF16_FRAG = 7 };
 
 __device__ __forceinline__ float to_f32(float x) { return x; }
 __device__ __forceinline__ float to_f32(bf16 x) { return (float)x; }

@@ -81,6 +81,155 @@ struct RowLnArgs {
   float a_scale;       // int8 A rows: A_f = a_scale * A
 };
 
+// Epilogue of both forms: scale, bias and residual in fp32, the fp32 rows written, then the
+// row statistics and the LayerNorm'd rows.  Lane (fr, g4), tile (i, j): row m0 + 16 i + fr,
+// columns wcol + 16 j + 4 g4 .. +3.  Every per-column parameter is loaded before the first
+// store, so no wait for them drains stores.  `smem` is reused for the statistics exchange
+// (2 KiB) after a barrier.
+template <int BN, bool Q8, class TIN, class ACC, int TM, int TN>
+__device__ __forceinline__ void rowln_epilogue(const RowLnArgs& g, const ACC (&acc)[TM][TN],
+                                               const float4 (&rv)[TM][TN], int m0, unsigned char* smem) {
+  constexpr int WN = BN / RL_WAVES;
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int fr = lane & 15, g4 = lane >> 4;
+  const int M = (int)g.M;
+  const int wcol = wid * WN;
+  // the fp32 residual rows and the normalised rows (bf16, or int8 with Q8), written through
+  const WtOut store_x(g.out, g.M * g.ld_out * 4, wt_one_wave());
+  const WtOut store_xn(g.xn, g.M * g.ld_xn * (Q8 ? 1 : 2), wt_one_wave());
+  float4 scv[TN], biv[TN], gmv[TN], bev[TN];
+  // absent scale / bias: load any valid row (gamma) and select the neutral value, so
+  // the loads stay unconditional (no branch, no extra wait at its merge)
+  const float* sp = g.w_scale ? g.w_scale : g.gamma;
+  const float* bp = g.bias ? g.bias : g.gamma;
+#pragma unroll
+  for (int j = 0; j < TN; ++j) {
+    const int n = wcol + 16 * j + 4 * g4;
+    scv[j] = *reinterpret_cast<const float4*>(sp + n);
+    biv[j] = *reinterpret_cast<const float4*>(bp + n);
+    gmv[j] = *reinterpret_cast<const float4*>(g.gamma + n);
+    bev[j] = *reinterpret_cast<const float4*>(g.beta + n);
+  }
+  rl_wait_vm<0>();
+  if (!g.w_scale) {
+#pragma unroll
+    for (int j = 0; j < TN; ++j) scv[j] = make_float4(1.f, 1.f, 1.f, 1.f);
+  }
+  if constexpr (sizeof(TIN) == 1) {  // int8 A rows: A_f = a_scale * A
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      scv[j].x *= g.a_scale; scv[j].y *= g.a_scale; scv[j].z *= g.a_scale; scv[j].w *= g.a_scale;
+    }
+  }
+  if (!g.bias) {
+#pragma unroll
+    for (int j = 0; j < TN; ++j) biv[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+  float v[TM][TN][4];
+#pragma unroll
+  for (int j = 0; j < TN; ++j) {
+    const float4 sc = scv[j], bi = biv[j];
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      v[i][j][0] = acc[i][j][0] * sc.x + bi.x + rv[i][j].x;
+      v[i][j][1] = acc[i][j][1] * sc.y + bi.y + rv[i][j].y;
+      v[i][j][2] = acc[i][j][2] * sc.z + bi.z + rv[i][j].z;
+      v[i][j][3] = acc[i][j][3] * sc.w + bi.w + rv[i][j].w;
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+    const int m = m0 + i * 16 + fr;
+    if (m < M) {
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+        store_x(reinterpret_cast<float4*>(g.out + (int64_t)m * g.ld_out + wcol + 16 * j + 4 * g4),
+                make_float4(v[i][j][0], v[i][j][1], v[i][j][2], v[i][j][3]));
+    }
+  }
+
+  // Row statistics with one exchange between the 8 wavefronts: each wavefront takes
+  // the mean and the sum of squared deviations (M2) of its WN columns of every row
+  // (lane sums, then xor-shuffles over the 4 lane groups), and the 8 equal-sized
+  // parts combine as mean = avg(mean_w), M2 = sum(M2_w) + WN * sum((mean_w - mean)^2)
+  // (Chan, Golub and LeVeque's pairwise update), as stable as two full passes.
+  float2* red = reinterpret_cast<float2*>(smem);  // [RL_WAVES][RL_BM]
+  constexpr float inv_wn = 1.0f / (float)WN;
+  float mean[TM], rstd[TM];
+  __syncthreads();  // every operand read of the LDS is done: it may be reused
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+    float sum = 0.0f;
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) sum += v[i][j][r];
+    sum += __shfl_xor(sum, 16, 64);
+    sum += __shfl_xor(sum, 32, 64);
+    const float mw = sum * inv_wn;
+    float m2 = 0.0f;
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float d = v[i][j][r] - mw;
+        m2 += d * d;
+      }
+    m2 += __shfl_xor(m2, 16, 64);
+    m2 += __shfl_xor(m2, 32, 64);
+    if (g4 == 0) red[wid * RL_BM + i * 16 + fr] = make_float2(mw, m2);
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+    float2 part[RL_WAVES];
+    float msum = 0.0f;
+#pragma unroll
+    for (int w = 0; w < RL_WAVES; ++w) {
+      part[w] = red[w * RL_BM + i * 16 + fr];
+      msum += part[w].x;
+    }
+    const float mu = msum * (1.0f / (float)RL_WAVES);
+    float m2 = 0.0f, dev = 0.0f;
+#pragma unroll
+    for (int w = 0; w < RL_WAVES; ++w) {
+      const float d = part[w].x - mu;
+      m2 += part[w].y;
+      dev += d * d;
+    }
+    mean[i] = mu;
+    rstd[i] = 1.0f / sqrtf(fmaf(dev, (float)WN, m2) * (1.0f / (float)BN) + g.eps);
+  }
+#pragma unroll
+  for (int j = 0; j < TN; ++j) {
+    const int n = wcol + 16 * j + 4 * g4;
+    const float4 gm = gmv[j], be = bev[j];
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      const int m = m0 + i * 16 + fr;
+      if (m >= M) continue;
+      const float y0 = (v[i][j][0] - mean[i]) * rstd[i] * gm.x + be.x;
+      const float y1 = (v[i][j][1] - mean[i]) * rstd[i] * gm.y + be.y;
+      const float y2 = (v[i][j][2] - mean[i]) * rstd[i] * gm.z + be.z;
+      const float y3 = (v[i][j][3] - mean[i]) * rstd[i] * gm.w + be.w;
+      if constexpr (Q8) {
+        auto q = [&](float y) {
+          return (uint32_t)((int)fminf(fmaxf(rintf(y * g.xq_inv_scale), -127.0f), 127.0f) & 0xff);
+        };
+        *reinterpret_cast<uint32_t*>(reinterpret_cast<int8_t*>(g.xn) + (int64_t)m * g.ld_xn + n) =
+            q(y0) | (q(y1) << 8) | (q(y2) << 16) | (q(y3) << 24);
+      } else {
+        bf16x4 o;
+        o[0] = (bf16)y0;
+        o[1] = (bf16)y1;
+        o[2] = (bf16)y2;
+        o[3] = (bf16)y3;
+        store_xn(reinterpret_cast<bf16x4*>(reinterpret_cast<bf16*>(g.xn) + (int64_t)m * g.ld_xn + n), o);
+      }
+    }
+  }
+}
+
 // TW = int8_t with bf16 A rows: the QuantizedLinear int8 weight itself, moved into the LDS ring
 // by the same direct-to-LDS transfers as bf16 rows (64 bytes of K per row and step, half the
 // bytes, so the ring may hold more stages), and each lane widens its 8-byte fragment exactly
@@ -105,9 +254,6 @@ __global__ __launch_bounds__(RL_THREADS) void gemm_rowln_kernel(RowLnArgs g) {
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int fr = lane & 15, g4 = lane >> 4;
   const int M = (int)g.M, K = (int)g.K;
-  // the fp32 residual rows and the normalised rows (bf16, or int8 with Q8), written through
-  const WtOut store_x(g.out, g.M * g.ld_out * 4, wt_one_wave());
-  const WtOut store_xn(g.xn, g.M * g.ld_xn * (Q8 ? 1 : 2), wt_one_wave());
   const int m0 = blockIdx.x * RL_BM;
   const int wcol = wid * WN;
 
@@ -255,140 +401,110 @@ __global__ __launch_bounds__(RL_THREADS) void gemm_rowln_kernel(RowLnArgs g) {
   __builtin_amdgcn_s_waitcnt(0xC07F);
   mma(af1, wf1);
 
-  // ---- epilogue.  Lane (fr, g4), tile (i, j): row m0 + 16 i + fr, columns
-  // wcol + 16 j + 4 g4 .. +3.  Every per-column parameter is loaded before the first
-  // store, so no wait for them drains stores.
-  float4 scv[TN], biv[TN], gmv[TN], bev[TN];
-  // absent scale / bias: load any valid row (gamma) and select the neutral value, so
-  // the loads stay unconditional (no branch, no extra wait at its merge)
-  const float* sp = g.w_scale ? g.w_scale : g.gamma;
-  const float* bp = g.bias ? g.bias : g.gamma;
+  rowln_epilogue<BN, Q8, TIN>(g, acc, rv, m0, smem);
+}
+
+// Direct-weight form, bf16 A rows and K = 64 * NK (the out-projection shapes), for the weight
+// in MFMA fragment order (cortex_frag_weight: 1 KiB blocks of 16 rows x 32 K in lane order).
+// The W rows of a wavefront's WN output columns are read by that wavefront alone, so staging
+// them in LDS only adds a copy and a barrier per K step.  Here each fragment (t, ks) of K step
+// kt is one contiguous 1 KiB read straight into the lane's operand registers (lane (fr, g4):
+// row wcol + 16 t + fr, K [64 kt + 32 ks + 8 g4, +8)), RL_DW_AHEAD K steps ahead of its MFMAs,
+// with no barrier in the K loop.  (From plain (N, K) rows the same fragment is 64 bytes of 16
+// rows, half lines, which measured slower than the LDS ring.)  The 32 A rows, which every
+// wavefront reads, move into LDS once before the loop (all of K: 32 * K * 2 bytes, the ring's
+// swizzled layout, one 64-deep K step per 4 KiB).  Same fragments and the same accumulation
+// order as the ring form, so the results are bit-identical to it.
+constexpr int RL_DW_AHEAD = 3;
+
+template <int BN, int NK, bool Q8>
+__global__ __launch_bounds__(RL_THREADS) void gemm_rowln_dw_kernel(RowLnArgs g) {
+  using OP = Operand<bf16>;
+  typedef typename OP::frag frag;
+  constexpr int WN = BN / RL_WAVES, TM = RL_BM / 16, TN = WN / 16, WD = RL_DW_AHEAD;
+  constexpr int A_STAGE = RL_BM * 128;                   // 32 rows x 64 K of bf16
+  constexpr int AB = NK * (A_STAGE / 1024) / RL_WAVES;   // 1 KiB A transfers per wavefront
+  constexpr int RED = RL_WAVES * RL_BM * 8;              // the epilogue's statistics exchange
+  constexpr int LDS = NK * A_STAGE > RED ? NK * A_STAGE : RED;
+  constexpr int RV = TM * TN, WOPS = TN * 2;             // residual loads; W loads per K step
+  static_assert(NK * (A_STAGE / 1024) % RL_WAVES == 0 && NK >= WD && TN >= 1, "shape");
+  static_assert(RV + WD * WOPS < 64, "vmcnt range");
+  __shared__ __attribute__((aligned(1024))) unsigned char smem[LDS];
+
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int fr = lane & 15, g4 = lane >> 4;
+  const int M = (int)g.M;
+  const int m0 = blockIdx.x * RL_BM;
+  const int wcol = wid * WN;
+
+  // A: the 1 KiB block q = wid * AB + i holds rows 8 (q % 4) .. +7 of K step q / 4 (lane i of a
+  // transfer: row i / 8, stored chunk i % 8 = logical chunk (i % 8) ^ rl_swz(row))
+  const bf16* A = reinterpret_cast<const bf16*>(g.x);
 #pragma unroll
-  for (int j = 0; j < TN; ++j) {
-    const int n = wcol + 16 * j + 4 * g4;
-    scv[j] = *reinterpret_cast<const float4*>(sp + n);
-    biv[j] = *reinterpret_cast<const float4*>(bp + n);
-    gmv[j] = *reinterpret_cast<const float4*>(g.gamma + n);
-    bev[j] = *reinterpret_cast<const float4*>(g.beta + n);
+  for (int i = 0; i < AB; ++i) {
+    const int q = wid * AB + i, r = (q & 3) * 8 + (lane >> 3);
+    const bf16* src = A + (int64_t)min(m0 + r, M - 1) * g.ld_x + (q >> 2) * 64 + ((lane & 7) ^ rl_swz(r)) * 8;
+    __builtin_amdgcn_global_load_lds(static_cast<const void*>(src), static_cast<void*>(smem + q * 1024), 16, 0, 0);
   }
-  rl_wait_vm<0>();
-  if (!g.w_scale) {
+  __builtin_amdgcn_sched_barrier(0);
+  // fragment (t, ks) of K step kt: block (wcol / 16 + t, 2 kt + ks), this lane's 16 bytes
+  const bf16* wp = reinterpret_cast<const bf16*>(g.w) + (int64_t)(wcol / 16) * (2 * NK) * 512 + lane * 8;
+  frag wb[NK][TN][2];  // (fully unrolled: each K step's fragments are registers of their own)
+  auto load_w = [&](int kt) {
 #pragma unroll
-    for (int j = 0; j < TN; ++j) scv[j] = make_float4(1.f, 1.f, 1.f, 1.f);
-  }
-  if constexpr (sizeof(TIN) == 1) {  // int8 A rows: A_f = a_scale * A
+    for (int t = 0; t < TN; ++t)
 #pragma unroll
-    for (int j = 0; j < TN; ++j) {
-      scv[j].x *= g.a_scale; scv[j].y *= g.a_scale; scv[j].z *= g.a_scale; scv[j].w *= g.a_scale;
-    }
-  }
-  if (!g.bias) {
+      for (int ks = 0; ks < 2; ++ks)
+        wb[kt][t][ks] = *reinterpret_cast<const frag*>(wp + (t * (2 * NK) + 2 * kt + ks) * 512);
+  };
 #pragma unroll
-    for (int j = 0; j < TN; ++j) biv[j] = make_float4(0.f, 0.f, 0.f, 0.f);
-  }
-  float v[TM][TN][4];
-#pragma unroll
-  for (int j = 0; j < TN; ++j) {
-    const float4 sc = scv[j], bi = biv[j];
-#pragma unroll
-    for (int i = 0; i < TM; ++i) {
-      v[i][j][0] = acc[i][j][0] * sc.x + bi.x + rv[i][j].x;
-      v[i][j][1] = acc[i][j][1] * sc.y + bi.y + rv[i][j].y;
-      v[i][j][2] = acc[i][j][2] * sc.z + bi.z + rv[i][j].z;
-      v[i][j][3] = acc[i][j][3] * sc.w + bi.w + rv[i][j].w;
-    }
-  }
+  for (int p = 0; p < WD; ++p) load_w(p);
+  // the residual tile after the first W steps, so the first MFMAs do not wait for it
+  __builtin_amdgcn_sched_barrier(0);
+  const int res_rows = g.res_rows > 0 ? (int)g.res_rows : M;
+  float4 rv[TM][TN];
 #pragma unroll
   for (int i = 0; i < TM; ++i) {
-    const int m = m0 + i * 16 + fr;
-    if (m < M) {
+    const int m = min(m0 + i * 16 + fr, M - 1);
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+      rv[i][j] = *reinterpret_cast<const float4*>(g.res + (int64_t)(m % res_rows) * g.ld_res + wcol + 16 * j + 4 * g4);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  typename OP::accum acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) acc[i][j] = (typename OP::accum){0, 0, 0, 0};
+  int a_off[TM], a_sw[TM];
+#pragma unroll
+  for (int t = 0; t < TM; ++t) {
+    const int r = t * 16 + fr;
+    a_off[t] = r * 128;
+    a_sw[t] = rl_swz(r);
+  }
+  rl_wait_vm<RV + WD * WOPS>();  // this wave's A transfers landed (the W and residual loads came after)
+  __builtin_amdgcn_s_barrier();  // every wave's: all 32 A rows in LDS
+#pragma unroll
+  for (int kt = 0; kt < NK; ++kt) {
+    const unsigned char* as = smem + kt * A_STAGE;
+    frag af[2][TM];
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+      for (int t = 0; t < TM; ++t)
+        af[ks][t] = *reinterpret_cast<const frag*>(as + a_off[t] + (((ks * 4 + g4) ^ a_sw[t]) << 4));
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
       for (int j = 0; j < TN; ++j)
-        store_x(reinterpret_cast<float4*>(g.out + (int64_t)m * g.ld_out + wcol + 16 * j + 4 * g4),
-                make_float4(v[i][j][0], v[i][j][1], v[i][j][2], v[i][j][3]));
-    }
+#pragma unroll
+        for (int i = 0; i < TM; ++i) acc[i][j] = OP::mma(wb[kt][j][ks], af[ks][i], acc[i][j]);
+    if (kt + WD < NK) load_w(kt + WD);
+    __builtin_amdgcn_sched_barrier(0);  // a K step's loads stay behind its MFMAs (registers)
   }
-
-  // Row statistics with one exchange between the 8 wavefronts: each wavefront takes
-  // the mean and the sum of squared deviations (M2) of its WN columns of every row
-  // (lane sums, then xor-shuffles over the 4 lane groups), and the 8 equal-sized
-  // parts combine as mean = avg(mean_w), M2 = sum(M2_w) + WN * sum((mean_w - mean)^2)
-  // (Chan, Golub and LeVeque's pairwise update), as stable as two full passes.
-  float2* red = reinterpret_cast<float2*>(smem);  // [RL_WAVES][RL_BM]
-  constexpr float inv_wn = 1.0f / (float)WN;
-  float mean[TM], rstd[TM];
-  __syncthreads();  // every ring read is done: the LDS may be reused
-#pragma unroll
-  for (int i = 0; i < TM; ++i) {
-    float sum = 0.0f;
-#pragma unroll
-    for (int j = 0; j < TN; ++j)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) sum += v[i][j][r];
-    sum += __shfl_xor(sum, 16, 64);
-    sum += __shfl_xor(sum, 32, 64);
-    const float mw = sum * inv_wn;
-    float m2 = 0.0f;
-#pragma unroll
-    for (int j = 0; j < TN; ++j)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float d = v[i][j][r] - mw;
-        m2 += d * d;
-      }
-    m2 += __shfl_xor(m2, 16, 64);
-    m2 += __shfl_xor(m2, 32, 64);
-    if (g4 == 0) red[wid * RL_BM + i * 16 + fr] = make_float2(mw, m2);
-  }
-  __syncthreads();
-#pragma unroll
-  for (int i = 0; i < TM; ++i) {
-    float2 part[RL_WAVES];
-    float msum = 0.0f;
-#pragma unroll
-    for (int w = 0; w < RL_WAVES; ++w) {
-      part[w] = red[w * RL_BM + i * 16 + fr];
-      msum += part[w].x;
-    }
-    const float mu = msum * (1.0f / (float)RL_WAVES);
-    float m2 = 0.0f, dev = 0.0f;
-#pragma unroll
-    for (int w = 0; w < RL_WAVES; ++w) {
-      const float d = part[w].x - mu;
-      m2 += part[w].y;
-      dev += d * d;
-    }
-    mean[i] = mu;
-    rstd[i] = 1.0f / sqrtf(fmaf(dev, (float)WN, m2) * (1.0f / (float)BN) + g.eps);
-  }
-#pragma unroll
-  for (int j = 0; j < TN; ++j) {
-    const int n = wcol + 16 * j + 4 * g4;
-    const float4 gm = gmv[j], be = bev[j];
-#pragma unroll
-    for (int i = 0; i < TM; ++i) {
-      const int m = m0 + i * 16 + fr;
-      if (m >= M) continue;
-      const float y0 = (v[i][j][0] - mean[i]) * rstd[i] * gm.x + be.x;
-      const float y1 = (v[i][j][1] - mean[i]) * rstd[i] * gm.y + be.y;
-      const float y2 = (v[i][j][2] - mean[i]) * rstd[i] * gm.z + be.z;
-      const float y3 = (v[i][j][3] - mean[i]) * rstd[i] * gm.w + be.w;
-      if constexpr (Q8) {
-        auto q = [&](float y) {
-          return (uint32_t)((int)fminf(fmaxf(rintf(y * g.xq_inv_scale), -127.0f), 127.0f) & 0xff);
-        };
-        *reinterpret_cast<uint32_t*>(reinterpret_cast<int8_t*>(g.xn) + (int64_t)m * g.ld_xn + n) =
-            q(y0) | (q(y1) << 8) | (q(y2) << 16) | (q(y3) << 24);
-      } else {
-        bf16x4 o;
-        o[0] = (bf16)y0;
-        o[1] = (bf16)y1;
-        o[2] = (bf16)y2;
-        o[3] = (bf16)y3;
-        store_xn(reinterpret_cast<bf16x4*>(reinterpret_cast<bf16*>(g.xn) + (int64_t)m * g.ld_xn + n), o);
-      }
-    }
-  }
+  rowln_epilogue<BN, Q8, bf16>(g, acc, rv, m0, smem);
 }
 
 bool a16(const void* p) { return ((uintptr_t)p & 15) == 0; }
@@ -408,7 +524,11 @@ int residual_ln(const char* who, int64_t M, int64_t N, int64_t K, const void* x,
                 int w_dtype = DT_BF16) {
   const bool i8in = a_scale > 0.0f;  // int8 A rows and weight (W8A8)
   const bool wi8 = !i8in && w_dtype == DT_I8;  // bf16 rows x the int8 weight (widened in the kernel)
-  CORTEX_CHECK_ARG(w_dtype == DT_BF16 || w_dtype == DT_I8, "%s: weight must be bf16 or int8 (got %d)", who, w_dtype);
+  const bool frag = !i8in && w_dtype == DT_BF16_FRAG;  // bf16 rows x the weight in fragment order
+  CORTEX_CHECK_ARG(w_dtype == DT_BF16 || w_dtype == DT_I8 || (!i8in && w_dtype == DT_BF16_FRAG),
+                   "%s: weight must be bf16, int8 or bf16 in fragment order (got %d)", who, w_dtype);
+  CORTEX_CHECK_ARG(!frag || K == 256 || K == 512, "%s: the fragment-order weight needs K = 256 or 512", who);
+  if (frag) ld_w = K;  // (the blocks are dense; only the bounds check below reads it)
   CORTEX_CHECK_ARG(M >= 0 && K > 0, "%s: need M >= 0 and K > 0", who);
   CORTEX_CHECK_ARG(N == 256 || N == 512, "%s: N must be 256 or 512 (got %lld)", who, (long long)N);
   CORTEX_CHECK_ARG(K % (i8in ? 2 * RL_BK : RL_BK) == 0 && K <= 0x7fffffffLL, "%s: K must be a multiple of %d", who,
@@ -428,6 +548,20 @@ int residual_ln(const char* who, int64_t M, int64_t N, int64_t K, const void* x,
   RowLnArgs a{M,     N,     K,     x,   ld_x, w,     ld_w, w_scale, bias, res, ld_res, res_rows, out, ld_out,
               gamma, beta,  eps,   xn,  ld_xn, q8 ? 1.0f / xq_scale : 0.0f, a_scale};
   const dim3 grid((unsigned)cdiv(M, (int64_t)RL_BM));
+  if (frag) {  // bf16 rows x the fragment-order weight: the direct-weight form
+#define RL_DW(BN_, NK_)                                                                                           \
+  do {                                                                                                            \
+    if (q8) hipLaunchKernelGGL((gemm_rowln_dw_kernel<BN_, NK_, true>), grid, dim3(RL_THREADS), 0, stream, a);   \
+    else hipLaunchKernelGGL((gemm_rowln_dw_kernel<BN_, NK_, false>), grid, dim3(RL_THREADS), 0, stream, a);     \
+  } while (0)
+    if (N == 512 && K == 512) RL_DW(512, 8);
+    else if (N == 512) RL_DW(512, 4);
+    else if (K == 512) RL_DW(256, 8);
+    else RL_DW(256, 4);
+#undef RL_DW
+    CORTEX_CHECK_LAUNCH("gemm_rowln_dw_kernel");
+    return OK;
+  }
   if (i8in) {
     CORTEX_CHECK_ARG(N == 512, "%s: the int8 form needs N = 512", who);
     if (q8)

@@ -191,6 +191,28 @@ __global__ __launch_bounds__(256) void transpose_bf16_kernel(const bf16* __restr
   }
 }
 
+// An (N, K) weight as bf16 in MFMA fragment order, for kernels whose wavefronts each stream
+// their own weight rows straight into registers (the direct-weight residual LayerNorm GEMM):
+// the 1 KiB block (n16, k32) = n16 * (K / 32) + k32 holds rows 16 n16 .. +15 and K 32 k32 ..
+// +31 as 64 lanes x 16 bytes, lane l = row 16 n16 + l % 16, K 32 k32 + 8 (l / 16) .. +7 (the
+// operand layout of v_mfma_f32_16x16x32_bf16), so one fragment is one contiguous 1 KiB read.
+// Values as cortex_convert writes them (int8 exact, fp32 rounded to nearest even).  One
+// thread per 16-byte output chunk.
+template <class TW>
+__global__ __launch_bounds__(256) void frag_weight_kernel(const TW* __restrict__ w, int64_t ld_w, int64_t K,
+                                                          int64_t chunks, bf16* __restrict__ out) {
+  const int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (c >= chunks) return;
+  const int64_t b = c >> 6, nkb = K / 32;
+  const int l = (int)(c & 63);
+  const int64_t n = (b / nkb) * 16 + (l & 15), k = (b % nkb) * 32 + (l >> 4) * 8;
+  const TW* src = w + n * ld_w + k;
+  bf16x8 v;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) v[j] = from_f32<bf16>(to_f32(src[j]));
+  *reinterpret_cast<bf16x8*>(out + c * 8) = v;
+}
+
 // A weight with a norm gain folded into its input columns, as bf16 (N, K) rows:
 //   out[n, k] = bf16( float(w[n, k]) * gamma[k] )        (KN = false: (N, K) rows)
 //   out[n, k] = bf16( float(w[k, n]) * gamma[k] )        (KN = true: (K, N) rows, through a
@@ -601,6 +623,32 @@ int cortex_fold_gain(int64_t N, int64_t K, const void* w, int w_dtype, int kn, i
 #undef CORTEX_FOLD_G
 #undef CORTEX_FOLD
   CORTEX_CHECK_LAUNCH("fold_gain_kernel");
+  return OK;
+}
+
+int cortex_frag_weight(int64_t N, int64_t K, const void* w, int w_dtype, int64_t ld_w, void* out,
+                       hipStream_t stream) {
+  const char* who = "cortex_frag_weight";
+  CORTEX_CHECK_ARG(N >= 0 && K >= 0, "%s: negative size", who);
+  if (N == 0 || K == 0) return OK;
+  CORTEX_CHECK_ARG(N % 16 == 0 && K % 32 == 0, "%s: N must be a multiple of 16 and K of 32", who);
+  CORTEX_CHECK_ARG(w && out && ld_w >= K, "%s: null pointer or short rows", who);
+  CORTEX_CHECK_ARG(w_dtype == DT_I8 || w_dtype == DT_BF16 || w_dtype == DT_F32, "%s: weight must be int8, bf16 or fp32",
+                   who);
+  CORTEX_CHECK_ARG(((uintptr_t)out & 15) == 0, "%s: output must be 16-byte aligned", who);
+  const int64_t chunks = N * K / 8;
+  CORTEX_CHECK_ARG(cdiv(chunks, (int64_t)256) <= 0x7fffffffLL, "%s: too large", who);
+  const dim3 grid((unsigned)cdiv(chunks, (int64_t)256));
+  if (w_dtype == DT_I8)
+    hipLaunchKernelGGL(frag_weight_kernel<int8_t>, grid, dim3(256), 0, stream, (const int8_t*)w, ld_w, K, chunks,
+                       (bf16*)out);
+  else if (w_dtype == DT_BF16)
+    hipLaunchKernelGGL(frag_weight_kernel<bf16>, grid, dim3(256), 0, stream, (const bf16*)w, ld_w, K, chunks,
+                       (bf16*)out);
+  else
+    hipLaunchKernelGGL(frag_weight_kernel<float>, grid, dim3(256), 0, stream, (const float*)w, ld_w, K, chunks,
+                       (bf16*)out);
+  CORTEX_CHECK_LAUNCH("frag_weight_kernel");
   return OK;
 }
 

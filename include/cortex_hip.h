@@ -11,7 +11,8 @@
  *     pointer after returning.  Work is enqueued on `stream` (the caller's current
  *     stream) and the library never synchronises the host.
  *   - Shapes and strides are int64 element counts.  dtype codes:
- *     0 f32, 1 bf16, 2 f16, 3 int8, 4 int32, 5 int64, 6 uint8.
+ *     0 f32, 1 bf16, 2 f16, 3 int8, 4 int32, 5 int64, 6 uint8; weight code 7: a bf16
+ *     weight in MFMA fragment order (cortex_frag_weight), where an entry point says so.
  *   - Index-range violations never read or write out of bounds: the offending row
  *     is written as zeros and a bit is OR-ed into the caller's device `err_flag`
  *     (1: token index outside its table, 2: batch index outside [0, B)).
@@ -173,6 +174,15 @@ int cortex_transpose_bf16(int64_t R, int64_t C, const void* in, int64_t ld_in, v
  * norm 2 and gamma = NULL then applies the per-row 1 / rms to the fp32 accumulator. */
 int cortex_fold_gain(int64_t N, int64_t K, const void* w, int w_dtype, int kn, int64_t ld_w, const void* gamma,
                      int gamma_dtype, void* out, int64_t ld_out, hipStream_t stream);
+/* An (N, K) weight (int8, bf16 or fp32 rows: w_dtype 3 / 1 / 0) as bf16 in MFMA fragment
+ * order, the layout of weight code 7: 1 KiB block (n16, k32) = n16 * (K / 32) + k32 holds rows
+ * 16 n16 .. +15 and K 32 k32 .. +31 as 64 lanes x 8 values, lane l = row 16 n16 + l % 16,
+ * K 32 k32 + 8 (l / 16) .. +7.  Values as cortex_convert writes them (int8 exact).  Built once
+ * per weight, like the bf16 image of QuantizedLinear's dequantised weight (calibrate.py:
+ * 225-228), for cortex_linear_residual_ln.  N % 16 == 0, K % 32 == 0, out (N * K bf16)
+ * 16-byte aligned. */
+int cortex_frag_weight(int64_t N, int64_t K, const void* w, int w_dtype, int64_t ld_w, void* out,
+                       hipStream_t stream);
 
 /* ---- a5/a8: LayerNorm rows to bf16 ----------------------------------------
  * Replaces nn.LayerNorm feeding a bf16 linear (cortex/models/perceiver.py:67-68,
@@ -308,8 +318,10 @@ int cortex_qkv_attention(int64_t B, int64_t L, int64_t D, int64_t H, const void*
  * by the first block's norm_attn):
  *   out[m, n] = res[(m % res_rows) * ld_res + n] + (sum_k x[m, k] w[n, k]) * w_scale[n] + bias[n]
  *   xn[m, :]  = LN(out[m, :]; gamma, beta, eps)   (bf16)
- * x (M, K) bf16; w (N, K): w_dtype 1 the weight's bf16 image, or 3 the int8 weight of
- * the QuantizedLinear, widened exactly to bf16 inside the kernel (ld_w % 16 == 0);
+ * x (M, K) bf16; w (N, K): w_dtype 1 the weight's bf16 image, 3 the int8 weight of the
+ * QuantizedLinear, widened exactly to bf16 inside the kernel (ld_w % 16 == 0), or 7 the
+ * bf16 weight in fragment order (cortex_frag_weight; K 256 or 512, ld_w ignored), which
+ * each wavefront streams straight into registers, bit-identical to w_dtype 1;
  * w_scale/bias optional, fp32; res/out fp32 (out may alias res: in-place residual
  * update); res_rows 0 means M.  N in {256, 512}, K % 64 == 0, 16-byte aligned rows. */
 int cortex_linear_residual_ln(int64_t M, int64_t N, int64_t K, const void* x, int64_t ld_x, int w_dtype,

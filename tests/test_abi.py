@@ -86,6 +86,12 @@ def test_invalid_arguments_return_status_and_message():
                                   src, cnt, None)
     assert rc == -1 and b"16-byte aligned" in lib.cortex_last_error()
     assert lib.cortex_widen_int8(0, None, None, None, None) == 0
+    # the fragment-order weight: 16-row, 32-K blocks; the direct-weight kernel takes K 256 / 512
+    rc = lib.cortex_frag_weight(24, 64, 16, 1, 64, 16, None)
+    assert rc == -1 and b"multiple of 16" in lib.cortex_last_error()
+    rc = lib.cortex_linear_residual_ln(64, 512, 128, 16, 128, 7, 16, 128, None, None, 16, 512, 0, 16, 512, 16, 16,
+                                       ctypes.c_float(1e-5), 16, 512, None)
+    assert rc == -1 and b"K = 256 or 512" in lib.cortex_last_error()
 
 
 def test_missing_library_fails_loudly(monkeypatch, tmp_path):

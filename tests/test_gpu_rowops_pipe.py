@@ -326,12 +326,14 @@ def test_narrow_output_rows(N, form):
 
 
 @pytest.mark.parametrize("M,N,K,res_rows", [(8192, 512, 512, 0), (300, 512, 512, 0), (8192, 512, 512, 256),
-                                            (77, 256, 256, 0), (1024, 256, 2048, 0), (40, 512, 128, 8)])
+                                            (77, 256, 256, 0), (200, 256, 512, 0), (96, 512, 256, 32),
+                                            (1024, 256, 2048, 0), (40, 512, 128, 8)])
 @pytest.mark.parametrize("inplace", [False, True])
 def test_linear_residual_ln(M, N, K, res_rows, inplace):
     """Residual linear + LayerNorm in one kernel (out_proj + norm_mlp): the fp32 residual
     output within 1e-5 of a float64 contraction of the same operands; the bf16 LayerNorm
-    of it within one bf16 rounding of the fp32 LayerNorm of the kernel's own output."""
+    of it within one bf16 rounding of the fp32 LayerNorm of the kernel's own output.
+    K = 256 / 512 run the direct-weight form (each N), other K the LDS-ring form."""
     from cortex.kernels import ops
 
     a, q, s = _operands(M, N, K, seed=M + N + K)
@@ -360,6 +362,43 @@ def test_linear_residual_ln(M, N, K, res_rows, inplace):
     if not ops.splitk_splits(M, N, K, torch.device(DEV)):  # no K split: the same operands in the same order
         torch.testing.assert_close(x8, x, rtol=0, atol=0)
         torch.testing.assert_close(xn8, xn, rtol=0, atol=0)
+    if ops.frag_ok(M, N, K, torch.device(DEV)):
+        # the weight in fragment order (direct-weight kernel): the same fragments in the same
+        # order as the LDS-ring kernel on the bf16 image, so bit-identical to it, bf16 and int8 xn
+        wf = ops.frag_weight(q.to(DEV))
+        # (the residual from the host copy: the in-place case above overwrote res_d)
+        xf, xnf = ops.linear_residual_ln(a.to(DEV), wf, s.to(DEV), bias.to(DEV), residual=res.to(DEV),
+                                         ln=(gam.to(DEV), bet.to(DEV), 1e-5), res_rows=res_rows, frag=True)
+        torch.testing.assert_close(xf, x8, rtol=0, atol=0)
+        torch.testing.assert_close(xnf, xn8, rtol=0, atol=0)
+        kw = dict(residual=res.to(DEV), ln=(gam.to(DEV), bet.to(DEV), 1e-5), res_rows=res_rows, xq_scale=0.03)
+        xq_n = ops.linear_residual_ln(a.to(DEV), w_img, s.to(DEV), bias.to(DEV), **kw)
+        kw["residual"] = res.to(DEV)
+        xq_f = ops.linear_residual_ln(a.to(DEV), wf, s.to(DEV), bias.to(DEV), frag=True, **kw)
+        torch.testing.assert_close(xq_f[0], xq_n[0], rtol=0, atol=0)
+        torch.testing.assert_close(xq_f[1], xq_n[1], rtol=0, atol=0)
+
+
+@pytest.mark.parametrize("N,K", [(512, 512), (256, 256), (48, 96), (16, 32)])
+@pytest.mark.parametrize("src", [torch.int8, torch.bfloat16, torch.float32])
+def test_frag_weight_layout(N, K, src):
+    """cortex_frag_weight: 1 KiB block (n16, k32) = 64 lanes x 8 values, lane l = row 16 n16 +
+    l % 16, K 32 k32 + 8 (l / 16) .. +7, the values of cortex_convert's bf16 image, checked
+    against the same permutation of the image taken on the CPU (and a strided source)."""
+    from cortex.kernels import ops
+
+    g = torch.Generator().manual_seed(N + K)
+    if src == torch.int8:
+        full = torch.randint(-127, 128, (N, K + 16), generator=g, dtype=torch.int8)
+    else:
+        full = (torch.randn(N, K + 16, generator=g) * 3).to(src)
+    w_d = full.to(DEV)[:, :K]  # device rows with a stride of K + 16
+    assert w_d.stride(0) == K + 16
+    w = full[:, :K]
+    img = w.to(torch.bfloat16) if src != torch.float32 else ops.convert(w.contiguous().to(DEV), torch.bfloat16).cpu()
+    want = img.reshape(N // 16, 16, K // 32, 4, 8).permute(0, 2, 3, 1, 4).reshape(-1)
+    got = ops.frag_weight(w_d).cpu().reshape(-1)
+    assert torch.equal(got.view(torch.int16), want.contiguous().view(torch.int16))
 
 
 @pytest.mark.parametrize("M,N,K,splits,res_rows", [(256, 512, 2048, 8, 0), (256, 512, 512, 8, 0), (1, 512, 2048, 4, 0),
