@@ -415,7 +415,7 @@ __global__ __launch_bounds__(RL_THREADS) void gemm_rowln_kernel(RowLnArgs g) {
 // wavefront reads, move into LDS once before the loop (all of K: 32 * K * 2 bytes, the ring's
 // swizzled layout, one 64-deep K step per 4 KiB).  Same fragments and the same accumulation
 // order as the ring form, so the results are bit-identical to it.
-constexpr int RL_DW_AHEAD = 3;
+constexpr int RL_DW_AHEAD = 2;  // 2: forward 0.6945-0.6968 ms; 3: 0.6970-0.6990; 4: 0.6961-0.6986
 
 template <int BN, int NK, bool Q8>
 __global__ __launch_bounds__(RL_THREADS) void gemm_rowln_dw_kernel(RowLnArgs g) {
