@@ -112,8 +112,12 @@ def make_kernel(name: str, dev):
         w, s = _int8_image(n, k, dev, seed)
         res = rnd(M_ROWS, n) if residual else None
         out = torch.empty(M_ROWS, n, dtype=torch.float32 if residual else bf, device=dev)
-        fn = lambda: ops.norm_linear(x, weight=w, weight_scale=s, act=act, residual=res,  # noqa: E731
-                                     out_dtype=out.dtype, compute_dtype=bf, out=out)
+        if residual and ops.frag_res_ok(M_ROWS, n, k, dev):  # the forward's form: the fragment-order weight
+            wf = ops.frag_weight(w)
+            fn = lambda: ops.linear_residual_frag(x, wf, s, None, residual=res, out=out)  # noqa: E731
+        else:
+            fn = lambda: ops.norm_linear(x, weight=w, weight_scale=s, act=act, residual=res,  # noqa: E731
+                                         out_dtype=out.dtype, compute_dtype=bf, out=out)
         flops = 2.0 * M_ROWS * n * k
         # compulsory bytes: activations, the INT8 weight and its scales, residual, output
         byts = M_ROWS * k * 2 + n * k + 4 * n + (M_ROWS * n * 4 if residual else 0) + M_ROWS * n * out.element_size()
@@ -121,8 +125,9 @@ def make_kernel(name: str, dev):
 
     if name == "gemm_mlp2_residual":
         fn, fl, by = gemm(512, 2048, residual=True)
-        return fn, 7, "hbm", fl, by, ("MLP down 2048->512 + fp32 residual, M=8192 (gemm_bf16_kernel, "
-                                      "128x128 tiles, K split over two wave groups)")
+        return fn, 7, "hbm", fl, by, ("MLP down 2048->512 + fp32 residual, M=8192 (gemm_res_dw_kernel, "
+                                      "128x128 tiles, K split over two wave groups, each wavefront's weight "
+                                      "fragments straight into registers)")
     if name == "gemm_mlp0_gelu":
         fn, fl, by = gemm(2048, 512, act="gelu")
         return fn, 7, "mfma", fl, by, "MLP up 512->2048 + GELU, bf16 out, M=8192 (gemm_bf16_kernel)"

@@ -333,6 +333,41 @@ def frag_ok(M: int, N: int, K: int, device: torch.device) -> bool:
     return N in (256, 512) and K in (256, 512) and not splitk_splits(M, N, K, device)
 
 
+def frag_res_ok(M: int, N: int, K: int, device: torch.device) -> bool:
+    """Whether ``linear_residual_frag`` applies: the direct-weight residual GEMM (N a multiple
+    of 128, K 1024 / 2048 / 3072) while its 128 x 128 tiles fit one per CU and no K split
+    across workgroups applies (larger grids keep the (N, K) image and the taller tiles)."""
+    if M < 1 or N % 128 or K not in (1024, 2048, 3072) or splitk_splits(M, N, K, device):
+        return False
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    cus = _CU_COUNT.get(idx)
+    if cus is None:
+        cus = _CU_COUNT[idx] = torch.cuda.get_device_properties(idx).multi_processor_count
+    return math.ceil(M / 128) * (N // 128) <= cus
+
+
+def linear_residual_frag(x: torch.Tensor, weight_frag: torch.Tensor, weight_scale=None, bias=None, *,
+                         residual: torch.Tensor, res_rows: int = 0, out: torch.Tensor | None = None) -> torch.Tensor:
+    """``out = residual + x @ (W * scale)^T + bias`` (fp32; ``out`` may be ``residual``) with the
+    weight in MFMA fragment order (``frag_weight``), on the direct-weight residual GEMM (see
+    ``frag_res_ok``).  Bit-identical to the same call with the bf16 image."""
+    dev = nat.require_gpu(x, weight_frag, weight_scale, bias, residual, out, what="linear_residual_frag")
+    x2 = _row_major_2d(x.reshape(-1, x.shape[-1]))
+    M, K = x2.shape
+    N = weight_frag.shape[0]
+    if not frag_res_ok(M, N, K, dev):
+        raise ValueError(f"the direct-weight residual GEMM does not apply at M={M}, N={N}, K={K}")
+    res2 = _row_major_2d(residual.reshape(-1, N))
+    if out is None:
+        out = torch.empty((*x.shape[:-1], N), dtype=torch.float32, device=dev)
+    out2 = out.reshape(-1, N)
+    nat.call("cortex_norm_linear", M, N, K, nat.BF16, nat.ptr(x2), x2.stride(0), 0, None, None, None, nat.F32,
+             nat.BF16, nat.BF16_FRAG, 0, nat.ptr(weight_frag), K, nat.ptr(weight_scale), nat.F32, nat.ptr(bias), 0,
+             nat.F32, nat.ptr(res2), res2.stride(0), int(res_rows), nat.F32, nat.ptr(out2), out2.stride(0),
+             nat.stream_of(dev))
+    return out
+
+
 def linear_residual_ln(x: torch.Tensor, weight: torch.Tensor, weight_scale=None, bias=None, *,
                        residual: torch.Tensor, ln, res_rows: int = 0, out: torch.Tensor | None = None,
                        xq_scale: float | None = None, frag: bool = False):

@@ -338,6 +338,17 @@ def apply_linear(lin: nn.Module, x: torch.Tensor, *, norm: nn.LayerNorm | None =
             hook(lin, (xin,))
         return ops.norm_linear(xin, **linear_weights(lin), act=act, residual=residual, res_rows=res_rows,
                                out_dtype=out_dtype, compute_dtype=compute, out=out)
+    if (residual is not None and norm is None and act is None and compute == torch.bfloat16
+            and x.dtype == torch.bfloat16 and residual.dtype == torch.float32 and out_dtype == torch.float32
+            and not (hasattr(lin, "weight_int8") and INT8_WEIGHTS != "image")
+            and (lin.bias is None or lin.bias.dtype == torch.float32)):
+        src = lin.weight_int8 if hasattr(lin, "weight_int8") else lin.weight
+        M = x.numel() // x.shape[-1]
+        if (src.dim() == 2 and src.shape[1] == x.shape[-1] and residual.shape[-1] == src.shape[0]
+                and ops.frag_res_ok(M, src.shape[0], src.shape[1], x.device)):
+            # the direct-weight residual GEMM on the fragment-order weight (MLP-down)
+            return ops.linear_residual_frag(x, frag_image(lin), lin.weight_scale if hasattr(lin, "weight_int8")
+                                            else None, lin.bias, residual=residual, res_rows=res_rows, out=out)
     w = exec_weights(lin, compute)
     if norm is not None and compute == torch.bfloat16 and stats is None and ln_rows_ok(x, norm):
         lead = x.shape[:-1]

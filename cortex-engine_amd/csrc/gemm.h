@@ -43,6 +43,11 @@ struct GemmArgs {
 // bf16 x bf16 path with a register epilogue (gemm_bf16.hip), same return convention.
 int try_gemm_bf16(const GemmArgs& g, int x_dtype, int w_dtype, int w_layout, int compute, hipStream_t stream);
 
+// The direct-weight residual GEMM (gemm_bf16.hip): bf16 x, w in MFMA fragment order
+// (DT_BF16_FRAG), fp32 residual and output, N % 128 == 0, K 1024 / 2048 / 3072, 16-byte
+// aligned rows.  Returns OK or an error status.
+int launch_res_dw(const GemmArgs& g, hipStream_t stream);
+
 // K split over gridDim.z = splits workgroup slabs (gemm_bf16.hip): slab z computes
 // (x[:, zK:(z+1)K] . w[:, zK:(z+1)K]^T) * w_scale into g.out + z * M * ld_out (fp32), where
 // K = g.K is the per-slab depth (a multiple of 64) and g.x / g.w are the full rows.  No

@@ -783,6 +783,202 @@ int launch_persist(const GemmArgs& g, hipStream_t stream) {
   return 1;
 }
 
+// ---------------------------------------------------------------------------------------
+// Direct-weight residual GEMM: out = res + (A . W^T) * w_scale + bias (fp32; out may be res),
+// A bf16 rows, W bf16 in MFMA fragment order (cortex_frag_weight), 128 x 128 tiles (MLP-down
+// while the grid is at most one tile per CU).  Eight wavefronts in two K groups, each group
+// taking half of K; wavefront (kg, wn) owns output columns 32 wn .. +31 of the tile for all 128
+// rows, so no other wavefront reads its weight fragments: each is one contiguous 1 KiB read
+// straight into the lane's operand registers, issued a K step ahead of its MFMAs, never staged
+// in LDS.  The activation rows, which the four wavefronts of a group share, stream through a
+// two-stage ring of direct-to-LDS transfers per group (one barrier per K step).  After the loop
+// the groups swap halves of their partial tiles through LDS and each finishes 64 rows (their
+// residual prefetched before the loop): per element the two K halves' sums are added once, as
+// in the K-split tiles of gemm_bf16_kernel, with the same MFMA sequence per half, so the
+// results equal that kernel's.
+constexpr int RD_BM = 128, RD_BN = 128;
+
+// NK = K / 128 (64-deep K steps per group), fully unrolled so that every wait is exact: across a
+// loop's back edge the compiler cannot track the weight loads in flight and waits for all of
+// them.  The activation rows go global -> VGPRs -> LDS (plain loads and ds_write) rather than by
+// direct-to-LDS transfers: with those in flight the compiler's vmcnt count for the weight
+// registers is no longer exact and it waits for every load (measured in its assembly).
+template <int NK>
+__global__ __launch_bounds__(512) void gemm_res_dw_kernel(GemmArgs g) {
+  using OP = Operand<bf16>;
+  typedef typename OP::frag frag;
+  constexpr int TM = RD_BM / 16, TN = 2, HM = TM / 2;       // row tiles, column tiles, rows finished
+  constexpr int A_STAGE = RD_BM * 128, AB = A_STAGE / 1024 / 4;  // 16 KiB; 4 chunks per lane and step
+  constexpr int RING = 2 * A_STAGE;                              // two stages per K group
+  constexpr int XCH = 8 * HM * TN * 64 * 16;                     // swapped half tiles
+  constexpr int LDS = 2 * RING > XCH ? 2 * RING : XCH;
+  static_assert(NK >= 2, "two K steps per group at least");
+  __shared__ __attribute__((aligned(1024))) unsigned char smem[LDS];
+
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int kg = wid >> 2, wn = wid & 3;
+  const int fr = lane & 15, g4 = lane >> 4;
+  const int nbx = gridDim.x, total = gridDim.x * gridDim.y;
+  const int id = xcd_affine(blockIdx.x + nbx * blockIdx.y, total);  // contiguous row tiles per XCD
+  const int m0 = (id / nbx) * RD_BM, n0 = (id % nbx) * RD_BN;
+  const int M = (int)g.M;
+  constexpr int K = NK * 128;
+  const int kb = kg * (K / 2);  // the group's first K
+  unsigned char* const ring = smem + kg * RING;
+
+  // activation chunks: block q = 4 wn + i of a stage holds rows 8 q .. +7; lane l's 16 bytes
+  // are row 8 q + l / 8, logical chunk (l % 8) ^ swz_a(row), stored at byte 16 l of the block
+  const bf16* a_src[AB];
+#pragma unroll
+  for (int i = 0; i < AB; ++i) {
+    const int r = (wn * AB + i) * 8 + (lane >> 3);
+    a_src[i] = reinterpret_cast<const bf16*>(g.x) + (int64_t)min(m0 + r, M - 1) * g.ld_x + kb +
+               ((lane & 7) ^ swz_a(r)) * 8;
+  }
+  unsigned char* const a_dst = ring + wn * AB * 1024 + lane * 16;
+  frag ar[NK][AB];  // (fully unrolled: registers of their own per step)
+  auto load_a = [&](int kt) {
+#pragma unroll
+    for (int i = 0; i < AB; ++i) ar[kt][i] = *reinterpret_cast<const frag*>(a_src[i] + kt * 64);
+  };
+  auto store_a = [&](int kt) {
+#pragma unroll
+    for (int i = 0; i < AB; ++i) *reinterpret_cast<frag*>(a_dst + (kt & 1) * A_STAGE + i * 1024) = ar[kt][i];
+  };
+  // weight fragment (t, ks) of step kt: block ((n0 + 32 wn) / 16 + t, kb / 32 + 2 kt + ks), this lane's 16 bytes
+  const bf16* wp = reinterpret_cast<const bf16*>(g.w) + ((int64_t)((n0 + 32 * wn) / 16) * (K / 32) + kb / 32) * 512 +
+                   lane * 8;
+  frag wb[NK][TN][2];
+  auto load_w = [&](int kt) {
+#pragma unroll
+    for (int t = 0; t < TN; ++t)
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks)
+        wb[kt][t][ks] = *reinterpret_cast<const frag*>(wp + (t * (K / 32) + 2 * kt + ks) * 512);
+  };
+
+  typename OP::accum acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) acc[i][j] = (typename OP::accum){0, 0, 0, 0};
+  const int a_row = fr * 128, a_sw = swz_a(fr);  // rows 16 t + fr: the same swizzle for every t
+  auto read_a = [&](int st, int ks, frag (&af)[TM]) {
+    const unsigned char* as = ring + st * A_STAGE + a_row + (((ks * 4 + g4) ^ a_sw) << 4);
+#pragma unroll
+    for (int t = 0; t < TM; ++t) af[t] = *reinterpret_cast<const frag*>(as + t * 2048);
+  };
+  auto mma = [&](const frag (&af)[TM], int kt, int ks) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j) acc[i][j] = OP::mma(wb[kt][j][ks], af[i], acc[i][j]);
+  };
+
+  // issue order: A(0), A(1), W(0), W(1), the residual of the rows this group finishes; then in
+  // step kt, after its barrier, A(kt + 2) into registers, and after its MFMAs W(kt + 2); A(kt + 1)
+  // goes from registers into its stage in step kt, before the barrier that publishes it
+  load_a(0);
+  load_a(1);
+  load_w(0);
+  load_w(1);
+  const float* res = reinterpret_cast<const float*>(g.res);
+  const int res_rows = g.res_rows > 0 ? (int)g.res_rows : M;
+  float4 rv[HM][TN];
+#pragma unroll
+  for (int ii = 0; ii < HM; ++ii) {
+    const int m = min(m0 + (kg * HM + ii) * 16 + fr, M - 1);
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+      rv[ii][j] = *reinterpret_cast<const float4*>(res + (int64_t)(m % res_rows) * g.ld_res + n0 + 32 * wn + 16 * j +
+                                                   4 * g4);
+  }
+  store_a(0);
+  __syncthreads();  // stage 0 of both groups written
+  frag af0[TM], af1[TM];
+  read_a(0, 0, af0);
+#pragma unroll
+  for (int kt = 0; kt < NK; ++kt) {
+    const int st = kt & 1;
+    __builtin_amdgcn_sched_barrier(0);
+    read_a(st, 1, af1);
+    mma(af0, kt, 0);
+    if (kt + 1 < NK) {
+      store_a(kt + 1);                     // stage st ^ 1: its last reads were before step kt - 1's barrier
+      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): these writes and this wave's reads of stage st
+      __builtin_amdgcn_s_barrier();        // every wave's: step kt + 1 visible, stage st free after its reads
+      __builtin_amdgcn_sched_barrier(0);
+      read_a(st ^ 1, 0, af0);
+      if (kt + 2 < NK) load_a(kt + 2);
+    }
+    mma(af1, kt, 1);
+    if (kt + 2 < NK) load_w(kt + 2);
+  }
+
+  // swap halves through LDS: group kg finishes rows 16 (kg HM + ii) + fr and sends the others
+  float4* xch = reinterpret_cast<float4*>(smem);
+  const float* bias = reinterpret_cast<const float*>(g.bias);
+  float* out = reinterpret_cast<float*>(g.out);
+  auto finish = [&](auto half) {
+    constexpr int own = decltype(half)::value, other = 1 - own;
+    float4 sc[TN], bi[TN];
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int n = n0 + 32 * wn + 16 * j + 4 * g4;
+      sc[j] = g.w_scale ? *reinterpret_cast<const float4*>(g.w_scale + n) : make_float4(1.f, 1.f, 1.f, 1.f);
+      bi[j] = bias ? *reinterpret_cast<const float4*>(bias + n) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    __syncthreads();  // every ring read is done: the exchange area may overwrite the rings
+#pragma unroll
+    for (int ii = 0; ii < HM; ++ii)
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const typename OP::accum v = acc[other * HM + ii][j];
+        xch[((wid * HM + ii) * TN + j) * 64 + lane] = make_float4(v[0], v[1], v[2], v[3]);
+      }
+    __syncthreads();
+    const int partner = other * 4 + wn;
+    wait_vm<0>();
+    const WtOut store(out, (int64_t)M * g.ld_out * 4, wt_one_wave());
+#pragma unroll
+    for (int ii = 0; ii < HM; ++ii) {
+      const int m = m0 + (own * HM + ii) * 16 + fr;
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        // the two K halves' sums added once (commutative: which group adds is of no concern)
+        const float4 o = xch[((partner * HM + ii) * TN + j) * 64 + lane];
+        const typename OP::accum a = acc[own * HM + ii][j];
+        const float4 x = rv[ii][j];
+        const float y0 = (a[0] + o.x) * sc[j].x + bi[j].x + x.x;
+        const float y1 = (a[1] + o.y) * sc[j].y + bi[j].y + x.y;
+        const float y2 = (a[2] + o.z) * sc[j].z + bi[j].z + x.z;
+        const float y3 = (a[3] + o.w) * sc[j].w + bi[j].w + x.w;
+        if (m < M) store(reinterpret_cast<float4*>(out + (int64_t)m * g.ld_out + n0 + 32 * wn + 16 * j + 4 * g4),
+                         make_float4(y0, y1, y2, y3));
+      }
+    }
+  };
+  if (kg == 0) finish(std::integral_constant<int, 0>{});
+  else finish(std::integral_constant<int, 1>{});
+}
+
+int launch_res_dw_impl(const GemmArgs& g, hipStream_t stream) {
+  const int64_t gy = cdiv(g.M, (int64_t)RD_BM), gx = g.N / RD_BN;
+  CORTEX_CHECK_ARG(gy <= 65535 && gx * gy <= 0x7fffffffLL, "gemm_res_dw_kernel: M=%lld exceeds the grid limit",
+                   (long long)g.M);
+  const dim3 grid((unsigned)gx, (unsigned)gy);
+  switch (g.K) {
+    case 1024: hipLaunchKernelGGL(gemm_res_dw_kernel<8>, grid, dim3(512), 0, stream, g); break;
+    case 2048: hipLaunchKernelGGL(gemm_res_dw_kernel<16>, grid, dim3(512), 0, stream, g); break;
+    case 3072: hipLaunchKernelGGL(gemm_res_dw_kernel<24>, grid, dim3(512), 0, stream, g); break;
+    default:
+      set_error("gemm_res_dw_kernel: K=%lld is not 1024, 2048 or 3072", (long long)g.K);
+      return E_INVALID;
+  }
+  CORTEX_CHECK_LAUNCH("gemm_res_dw_kernel");
+  return OK;
+}
+
 // Tile by shape: 256-row tiles halve the operand traffic per MFMA, so take the widest tile
 // that still fills (nearly) every CU once, else 128 x 128 (two workgroups per CU).
 enum TileChoice { T128 = 0, T256 = 4, T192 = 6, T128_K2 = 7 };
@@ -1339,6 +1535,8 @@ int split_k_partials(const GemmArgs& g, int splits, hipStream_t stream) {
   CORTEX_CHECK_LAUNCH("gemm_bf16_kernel (K split)");
   return 1;
 }
+
+int launch_res_dw(const GemmArgs& g, hipStream_t stream) { return launch_res_dw_impl(g, stream); }
 
 int try_gemm_bf16(const GemmArgs& g, int x_dtype, int w_dtype, int w_layout, int compute, hipStream_t stream) {
   if (compute != DT_BF16 || w_layout != 0 || x_dtype != DT_BF16 || (w_dtype != DT_BF16 && w_dtype != DT_I8)) return 0;

@@ -519,6 +519,20 @@ int cortex_norm_linear(int64_t M, int64_t N, int64_t K, int x_dtype, const void*
   g.ld_out = ld_out;
   CORTEX_CHECK_ARG(cdiv(M, GEMM_BM) <= 65535 && cdiv(N, GEMM_BN) <= 0x7fffffffLL,
                    "cortex_norm_linear: M=%lld exceeds the grid limit", (long long)M);
+  if (w_dtype == DT_BF16_FRAG) {  // the weight in MFMA fragment order: the direct-weight residual GEMM alone reads it
+    CORTEX_CHECK_ARG(x_dtype == DT_BF16 && compute == DT_BF16 && w_layout == 0 && norm == NORM_NONE &&
+                         act == ACT_NONE && residual && res_dtype == DT_F32 && out_dtype == DT_F32 &&
+                         (!bias || bias_dtype == DT_F32),
+                     "cortex_norm_linear: a fragment-order weight (w_dtype 7) takes bf16 x, an fp32 residual and "
+                     "output, no norm and no activation");
+    CORTEX_CHECK_ARG(N % 128 == 0 && (K == 1024 || K == 2048 || K == 3072) && M <= 0x7fffffffLL - 128,
+                     "cortex_norm_linear: a fragment-order weight needs N a multiple of 128 and K 1024, 2048 or 3072");
+    auto a16 = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
+    CORTEX_CHECK_ARG(a16(x) && ld_x % 8 == 0 && a16(w) && a16(residual) && ld_res % 4 == 0 && a16(out) &&
+                         ld_out % 4 == 0 && (!w_scale || a16(w_scale)) && (!bias || a16(bias)),
+                     "cortex_norm_linear: operands must be 16-byte aligned rows");
+    return launch_res_dw(g, stream);
+  }
   const int xs = elem_size(x_dtype), ws = elem_size(w_dtype);
   const bool vec = ((uintptr_t)x % 16 == 0) && ((ld_x * xs) % 16 == 0) && ((uintptr_t)w % 16 == 0) &&
                    ((ld_w * ws) % 16 == 0) && (ws != 1 || ((uintptr_t)w % 8 == 0 && (ld_w % 8) == 0));

@@ -212,6 +212,37 @@ def test_residual_gemm_every_grid(M, K, form):
     assert err <= 1e-5 * float(ref.abs().max()), err
 
 
+@pytest.mark.parametrize("M,N,K,res_rows", [(8192, 512, 2048, 0), (8000, 512, 2048, 0), (2900, 512, 2048, 0),
+                                            (8192, 256, 1024, 256), (4096, 768, 3072, 0), (2048, 1024, 2048, 0)])
+def test_direct_weight_residual_gemm(M, N, K, res_rows):
+    """The direct-weight residual GEMM (MLP-down on the fragment-order weight, grids of at most
+    one 128 x 128 tile per CU): within 1e-5 of float64, and bit-identical to the K-split
+    128 x 128 kernel on the bf16 image, whose per-group MFMA sequence it repeats.  Ragged last
+    row tile, broadcast residual rows, in place over the residual."""
+    from cortex.kernels import ops
+
+    a, q, s = _operands(M, N, K, seed=M + N + K)
+    ad, qd, sd = a.to(DEV), q.to(DEV), s.to(DEV)
+    g = torch.Generator().manual_seed(9)
+    bias = (0.1 * torch.randn(N, generator=g)).to(DEV)
+    res = torch.randn(res_rows or M, N, generator=g).to(DEV)
+    dev = torch.device(DEV)
+    assert ops.frag_res_ok(M, N, K, dev)
+    img = ops.convert(qd, torch.bfloat16)
+    out_f = res.clone() if not res_rows else None
+    y_f = ops.linear_residual_frag(ad, ops.frag_weight(qd), sd, bias, residual=res if res_rows else out_f,
+                                   res_rows=res_rows, out=out_f)
+    if out_f is not None:
+        assert y_f.data_ptr() == out_f.data_ptr()
+    y_i = ops.norm_linear(ad, weight=img, weight_scale=sd, bias=bias, residual=res, res_rows=res_rows,
+                          out_dtype=torch.float32)
+    r = res.double().repeat(M // res_rows, 1) if res_rows else res.double()
+    ref = (ad.double() @ (qd.double() * sd.double()[:, None]).T) + bias.double() + r
+    assert float((y_f.double() - ref).abs().max()) <= 1e-5 * float(ref.abs().max())
+    if not ops.splitk_splits(M, N, K, dev) and -(-M // 128) * (N // 128) <= 256:
+        torch.testing.assert_close(y_f, y_i, rtol=0, atol=0)
+
+
 def test_gemm_float_weight_image():
     """A float nn.Linear weight rounded to bf16 (no scale), residual into fp32 output."""
     from cortex.kernels import ops
