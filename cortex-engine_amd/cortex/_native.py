@@ -48,7 +48,7 @@ _SIGNATURES = {
     "cortex_pack_plan": (_int, [_ptr, _i64, _i64, _i64, _ptr, _ptr, _ptr, _ptr, _ptr, _i64, _ptr, _ptr, _int, _ptr]),
     "cortex_pack_plan_widen": (
         _int, [_ptr, _i64, _i64, _i64, _ptr, _ptr, _ptr, _ptr, _ptr, _i64, _ptr, _ptr, _int, _int, _ptr, _ptr, _ptr,
-               _ptr]),
+               _ptr, _ptr]),
     "cortex_pack_noalloc_max_workspace_bytes": (_i64, []),
     "cortex_pack_plan_noalloc": (_int, [_ptr, _i64, _i64, _i64, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr]),
     "cortex_tokenize": (
@@ -69,14 +69,14 @@ _SIGNATURES = {
     "cortex_ln_rows": (
         _int, [_i64, _i64, _ptr, _i64, _ptr, _ptr, _f32, _ptr, _ptr, _f32, _ptr, _i64, _ptr, _i64, _ptr]),
     "cortex_convert": (_int, [_int, _ptr, _int, _ptr, _i64, _ptr]),
-    "cortex_widen_int8": (_int, [_int, _ptr, _ptr, _ptr, _ptr]),
+    "cortex_widen_int8": (_int, [_int, _ptr, _ptr, _ptr, _ptr, _ptr]),
     "cortex_ln_rows_widen": (
         _int, [_i64, _i64, _ptr, _i64, _ptr, _ptr, _f32, _ptr, _ptr, _f32, _ptr, _i64, _ptr, _i64, _int, _ptr, _ptr,
-               _ptr, _ptr]),
+               _ptr, _ptr, _ptr]),
     "cortex_tokenize_ln_widen": (
         _int,
         [_i64, _ptr, _i64, _i64, _ptr, _i64, _i64, _ptr, _i64, _i64, _ptr, _i64, _ptr, _i64, _ptr, _i64, _i64,
-         _ptr, _ptr, _ptr, _ptr, _ptr, _f32, _ptr, _i64, _ptr, _int, _ptr, _ptr, _ptr, _ptr]),
+         _ptr, _ptr, _ptr, _ptr, _ptr, _f32, _ptr, _i64, _ptr, _int, _ptr, _ptr, _ptr, _ptr, _ptr]),
     "cortex_norm_linear": (
         _int,
         [_i64, _i64, _i64, _int, _ptr, _i64, _int, _ptr, _ptr, _ptr, _int, _int, _int, _int, _ptr, _i64, _ptr,

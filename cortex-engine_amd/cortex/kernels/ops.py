@@ -120,12 +120,14 @@ WIDEN_MAX = 8  # arrays per widening rider (WR_MAX in the kernels)
 
 
 def _widen_args(pairs, dev) -> tuple:
-    """``(n, src, dst, count)`` C arrays of the (int8 source, bf16 destination) pairs of a widening
-    rider: contiguous tensors of equal element counts (multiples of 16) on ``dev``."""
-    pairs = list(pairs)
+    """``(n, src, dst, count, frag_k)`` C arrays of the (int8 source, bf16 destination[, K]) items
+    of a widening rider: contiguous tensors of equal element counts (multiples of 16) on ``dev``;
+    a third item K > 0 writes the (N, K) destination in MFMA fragment order (``frag_weight``'s
+    layout; K a power of two from 64)."""
+    pairs = [tuple(p) if len(p) == 3 else (p[0], p[1], 0) for p in pairs]
     if len(pairs) > WIDEN_MAX:
         raise ValueError(f"at most {WIDEN_MAX} arrays widen in one launch (got {len(pairs)})")
-    for src, dst in pairs:
+    for src, dst, _ in pairs:
         if src.dtype != torch.int8 or dst.dtype != torch.bfloat16:
             raise ValueError("widening takes int8 sources and bf16 destinations")
         if src.numel() != dst.numel() or src.numel() % 16 or not (src.is_contiguous() and dst.is_contiguous()):
@@ -136,16 +138,17 @@ def _widen_args(pairs, dev) -> tuple:
     src = (ctypes.c_void_p * max(n, 1))(*[p[0].data_ptr() for p in pairs])
     dst = (ctypes.c_void_p * max(n, 1))(*[p[1].data_ptr() for p in pairs])
     cnt = (ctypes.c_int64 * max(n, 1))(*[p[0].numel() for p in pairs])
-    return n, src, dst, cnt
+    fk = (ctypes.c_int64 * max(n, 1))(*[int(p[2]) for p in pairs])
+    return n, src, dst, cnt, fk
 
 
 def widen_int8(pairs) -> None:
     """``dst.copy_(src)`` (int8 -> bf16, exact) for each ``(src, dst)`` pair in one launch
-    (``cortex_widen_int8``)."""
+    (``cortex_widen_int8``); a ``(src, dst, K)`` item writes dst in MFMA fragment order."""
     pairs = list(pairs)
     if not pairs:
         return
-    dev = nat.require_gpu(*[t for p in pairs for t in p], what="widen_int8")
+    dev = nat.require_gpu(*[t for p in pairs for t in p[:2]], what="widen_int8")
     nat.call("cortex_widen_int8", *_widen_args(pairs, dev), nat.stream_of(dev))
 
 

@@ -54,15 +54,21 @@ class WeightWindow:
     not resident when its weights are asked for is widened on a launch of its own first, so
     every path stays correct.  The resident set is tracked on the host in launch order (graph
     capture records the same sequence); forwards that share a model must run on one stream,
-    as its activation buffers already require."""
+    as its activation buffers already require.
 
-    def __init__(self, regions: dict, device: torch.device) -> None:
-        # regions: name -> [(owner module, [QuantizedLinear, ...]), ...]
+    A linear with a ``role`` ("ln": the residual linear + LayerNorm kernel; "res": the residual
+    GEMM) is widened in MFMA fragment order (``ops.frag_weight``'s layout) when the direct-weight
+    kernel of that role takes the forward's row count, as the bf16 images are in the default
+    mode; the layout is part of what is resident."""
+
+    def __init__(self, regions: dict, device: torch.device, roles: dict | None = None) -> None:
+        # regions: name -> [(owner module, [QuantizedLinear, ...]), ...]; roles: id(linear) -> role
         self._views = {}      # id(linear) -> bf16 (N, K) view of its region
         self._owner = {}      # id(linear) -> (region, owner)
         self._pairs = {}      # id(owner) -> [(int8, view), ...]
         self._linears = {}    # id(owner) -> [linear, ...]
-        self._held = {}       # region -> (id(owner), version key) resident now
+        self._held = {}       # region -> (id(owner), version key, layout per linear) resident now
+        self._roles = dict(roles or {})
         self.bytes = 0
         for region, groups in regions.items():
             size = max(sum(l.weight_int8.numel() for l in lins) for _, lins in groups)
@@ -89,24 +95,53 @@ class WeightWindow:
         """Nothing resident: a new forward widens every group it reads."""
         self._held.clear()
 
-    def take(self, owner) -> list:
-        """The (int8, bf16 view) pairs of ``owner``'s group for a rider launched now, which makes
-        it resident; empty when it already is."""
+    def layout(self, lin: nn.Module, rows: int | None) -> int:
+        """K when ``lin`` is to be widened in fragment order for a forward of ``rows`` rows (its
+        role's direct-weight kernel takes that shape), else 0."""
+        role = self._roles.get(id(lin))
+        if role is None or rows is None:
+            return 0
+        N, K = lin.weight_int8.shape
+        if K < 64 or K & (K - 1):
+            return 0
+        dev = lin.weight_int8.device
+        ok = ops.frag_ok(rows, N, K, dev) if role == "ln" else ops.frag_res_ok(rows, N, K, dev)
+        return K if ok else 0
+
+    def take(self, owner, rows: int | None = None, plain=None) -> list:
+        """The (int8, bf16 view, K) items of ``owner``'s group for a rider launched now, which
+        makes it resident (in the layouts for ``rows``; the linear ``plain`` in plain rows);
+        empty when it already is."""
         if owner is None or id(owner) not in self._pairs:
             return []
-        region = self._owner[id(self._linears[id(owner)][0])][0]
-        key = (id(owner), self._key(owner))
+        lins = self._linears[id(owner)]
+        region = self._owner[id(lins[0])][0]
+        ks = tuple(0 if lin is plain else self.layout(lin, rows) for lin in lins)
+        key = (id(owner), self._key(owner), ks)
         if self._held.get(region) == key:
             return []
         self._held[region] = key
-        return list(self._pairs[id(owner)])
+        return [(q, v, k) for (q, v), k in zip(self._pairs[id(owner)], ks)]
 
-    def view(self, lin: nn.Module) -> torch.Tensor:
-        """bf16 weight of ``lin``, its group widened first on a launch of its own unless resident."""
-        pairs = self.take(self._owner[id(lin)][1])
-        if pairs:
-            ops.widen_int8(pairs)
+    def view(self, lin: nn.Module, rows: int | None = None, plain: bool = False) -> torch.Tensor:
+        """bf16 weight of ``lin``, its group widened first on a launch of its own unless resident:
+        ``lin`` in plain (N, K) rows with ``plain``, else in the layout for ``rows`` rows when
+        given (``is_frag`` tells which); the rest of a group widened here is laid out for ``rows``."""
+        region, owner = self._owner[id(lin)]
+        held = self._held.get(region)
+        want = 0 if plain else (self.layout(lin, rows) if rows is not None else None)
+        if (held is None or held[:2] != (id(owner), self._key(owner))
+                or (want is not None and held[2][self._linears[id(owner)].index(lin)] != want)):
+            pairs = self.take(owner, rows, plain=lin if plain else None)
+            if pairs:
+                ops.widen_int8(pairs)
         return self._views[id(lin)]
+
+    def is_frag(self, lin: nn.Module) -> bool:
+        """Whether ``lin``'s resident window holds it in fragment order."""
+        region, owner = self._owner[id(lin)]
+        held = self._held.get(region)
+        return held is not None and held[0] == id(owner) and held[2][self._linears[id(owner)].index(lin)] != 0
 
 
 def weight_window(owner: nn.Module) -> WeightWindow | None:
@@ -114,20 +149,22 @@ def weight_window(owner: nn.Module) -> WeightWindow | None:
     return owner.__dict__.get("_cortex_window") if INT8_WEIGHTS == "window" else None
 
 
-def rider(*owners) -> list | None:
-    """The weight pairs that the next row kernel should widen so that ``owners``' groups are
-    resident in their window (None outside window mode or when nothing is to widen)."""
+def rider(*owners, rows: int | None = None) -> list | None:
+    """The weight items that the next row kernel should widen so that ``owners``' groups are
+    resident in their window, laid out for a forward of ``rows`` rows (None outside window mode
+    or when nothing is to widen)."""
     pairs = []
     for o in owners:
         win = weight_window(o) if o is not None else None
         if win is not None:
-            pairs += win.take(o)
+            pairs += win.take(o, rows)
     return pairs or None
 
 
-def build_weight_window(regions: dict, device: torch.device) -> WeightWindow | None:
+def build_weight_window(regions: dict, device: torch.device, roles: dict | None = None) -> WeightWindow | None:
     """A ``WeightWindow`` over the QuantizedLinears of ``regions`` (name -> [(owner, [linear])])
-    in window mode, None otherwise or when a group holds no int8 weight."""
+    in window mode, None otherwise or when a group holds no int8 weight; ``roles``: id(linear)
+    -> "ln" / "res" for the linears whose kernels take a fragment-order weight."""
     if INT8_WEIGHTS != "window":
         return None
     groups = {r: [(o, [l for l in lins if hasattr(l, "weight_int8")]) for o, lins in g] for r, g in regions.items()}
@@ -141,16 +178,17 @@ def build_weight_window(regions: dict, device: torch.device) -> WeightWindow | N
                 q = lin.weight_int8
                 if not q.is_contiguous() or q.numel() % 16 or q.device != device:
                     return None
-    return WeightWindow(groups, device)
+    return WeightWindow(groups, device, roles)
 
 
-def exec_weights(lin: nn.Module, compute: torch.dtype) -> dict:
-    """Weight arguments for the GEMM at ``compute`` precision (bf16 image when bf16)."""
+def exec_weights(lin: nn.Module, compute: torch.dtype, rows: int | None = None) -> dict:
+    """Weight arguments for the GEMM at ``compute`` precision (bf16 image when bf16; in window
+    mode the window in plain rows, ``rows`` laying out the rest of a group widened here)."""
     quant = hasattr(lin, "weight_int8")
     if compute != torch.bfloat16 or (quant and INT8_WEIGHTS != "image"):
         win = lin.__dict__.get("_cortex_window") if compute == torch.bfloat16 and INT8_WEIGHTS == "window" else None
         if win is not None:
-            return {"weight": win.view(lin), "weight_scale": lin.weight_scale, "bias": lin.bias}
+            return {"weight": win.view(lin, rows, plain=True), "weight_scale": lin.weight_scale, "bias": lin.bias}
         return linear_weights(lin)
     src = lin.weight_int8 if quant else lin.weight
     key = (src.data_ptr(), src._version, tuple(src.shape), src.device)
@@ -164,15 +202,15 @@ def exec_weights(lin: nn.Module, compute: torch.dtype) -> dict:
     return {"weight": cached[1], "weight_scale": lin.weight_scale if quant else None, "bias": lin.bias}
 
 
-def fused_weight(lin: nn.Module) -> tuple:
+def fused_weight(lin: nn.Module, rows: int | None = None) -> tuple:
     """``(weight, weight_scale, bias)`` for the fused bf16 kernels (QKV + attention, residual
     linear + LayerNorm): the bf16 image, or with ``CORTEX_INT8_WEIGHTS=widen`` the int8 weight
-    itself, which those kernels widen on chip (with ``window``, the bf16 window when the linear
-    has one)."""
+    itself, which those kernels widen on chip (with ``window``, the bf16 window in plain rows
+    when the linear has one; ``rows`` lays out the rest of a group widened here)."""
     if hasattr(lin, "weight_int8") and INT8_WEIGHTS != "image":
         win = lin.__dict__.get("_cortex_window") if INT8_WEIGHTS == "window" else None
         if win is not None:
-            return win.view(lin), lin.weight_scale, lin.bias
+            return win.view(lin, rows, plain=True), lin.weight_scale, lin.bias
         return lin.weight_int8, lin.weight_scale, lin.bias
     w = exec_weights(lin, torch.bfloat16)
     return w["weight"], w["weight_scale"], w["bias"]
@@ -313,6 +351,11 @@ def linear_residual_ln(lin: nn.Module, a: torch.Tensor, residual: torch.Tensor, 
     default INT8 mode) the weight goes in MFMA fragment order where the direct-weight kernel
     takes it (``ops.frag_ok``)."""
     src = lin.weight_int8 if hasattr(lin, "weight_int8") else lin.weight
+    win = lin.__dict__.get("_cortex_window") if hasattr(lin, "weight_int8") and INT8_WEIGHTS == "window" else None
+    if win is not None:  # the window, in fragment order when this shape takes it
+        w = win.view(lin, rows=a.shape[0])
+        return ops.linear_residual_ln(a, w, lin.weight_scale, lin.bias, residual=residual, ln=ln_params(norm),
+                                      res_rows=res_rows, out=out, xq_scale=xq_scale, frag=win.is_frag(lin))
     if (not (hasattr(lin, "weight_int8") and INT8_WEIGHTS != "image")
             and ops.frag_ok(a.shape[0], src.shape[0], src.shape[1], a.device)):
         return ops.linear_residual_ln(a, frag_image(lin), lin.weight_scale if hasattr(lin, "weight_int8") else None,
@@ -349,6 +392,14 @@ def apply_linear(lin: nn.Module, x: torch.Tensor, *, norm: nn.LayerNorm | None =
             # the direct-weight residual GEMM on the fragment-order weight (MLP-down)
             return ops.linear_residual_frag(x, frag_image(lin), lin.weight_scale if hasattr(lin, "weight_int8")
                                             else None, lin.bias, residual=residual, res_rows=res_rows, out=out)
+    win = lin.__dict__.get("_cortex_window") if hasattr(lin, "weight_int8") and INT8_WEIGHTS == "window" else None
+    if (win is not None and residual is not None and norm is None and act is None and compute == torch.bfloat16
+            and x.dtype == torch.bfloat16 and residual.dtype == torch.float32 and out_dtype == torch.float32
+            and (lin.bias is None or lin.bias.dtype == torch.float32)):
+        w = win.view(lin, rows=x.numel() // x.shape[-1])
+        if win.is_frag(lin):  # the window in fragment order: the direct-weight residual GEMM
+            return ops.linear_residual_frag(x, w, lin.weight_scale, lin.bias, residual=residual, res_rows=res_rows,
+                                            out=out)
     w = exec_weights(lin, compute)
     if norm is not None and compute == torch.bfloat16 and stats is None and ln_rows_ok(x, norm):
         lead = x.shape[:-1]

@@ -178,7 +178,7 @@ class CortexModel(nn.Module):
             err_flag = torch.empty(1, dtype=torch.int32, device=neuron_ids.device)
         # INT8-resident window mode: the cross-attention's and the first block's weights widen into
         # their windows in the plan's first launch, on the CUs its few workgroups leave idle
-        widen = self._window_rider()
+        widen = self._window_rider(rows=int(batch_size) * self.config.num_latents)
         offsets, order, _, ident = ops.pack_plan(batch_indices, int(batch_size), err=err_flag, with_rank=False,
                                                  identity=True, clear_err=clear_err or check_indices, widen=widen)
         out = self._forward_planned(neuron_ids, time_bins, values, offsets, order, int(batch_size), err_flag,
@@ -215,7 +215,8 @@ class CortexModel(nn.Module):
         (``r`` itself when ``order`` is None or the plan's ``identity`` flag is set); rows past
         ``offsets[B]`` are ignored."""
         enc = self.encoder
-        tokens = self._token_rows(neuron_ids, time_bins, values, offsets, order, err_flag, identity)
+        tokens = self._token_rows(neuron_ids, time_bins, values, offsets, order, err_flag, identity,
+                                  rows=B * self.config.num_latents)
         x, xn = self._cross_rows(tokens, offsets, B)
         x = self._encode(x, B, xn)
         out = {"behavior": self.behavior_head.forward_rows(x, B, pre_norm=enc.final_norm)}
@@ -223,10 +224,11 @@ class CortexModel(nn.Module):
             out["masked_spike_logits"] = self.masked_spike_head.forward_rows(x, B, pre_norm=enc.final_norm)
         return out
 
-    def _window_rider(self, take: bool = True) -> list | None:
+    def _window_rider(self, take: bool = True, rows: int | None = None) -> list | None:
         """Start of a forward in the INT8-resident window mode: nothing is resident yet (every
-        weight group this forward reads is widened again), and with ``take`` the weight pairs of
-        the cross-attention and the first block, for the forward's first launch to widen."""
+        weight group this forward reads is widened again), and with ``take`` the weight items of
+        the cross-attention and the first block (laid out for ``rows`` latent rows), for the
+        forward's first launch to widen."""
         win = self.encoder.weight_window()
         if win is None:
             return None
@@ -234,13 +236,14 @@ class CortexModel(nn.Module):
         if not take:
             return None
         blocks = self.encoder.self_attn_blocks
-        return rider(self.encoder.cross_attn, blocks[0] if len(blocks) else None)
+        return rider(self.encoder.cross_attn, blocks[0] if len(blocks) else None, rows=rows)
 
     def _token_rows(self, neuron_ids, time_bins, values, offsets, order, err_flag,
-                    identity: torch.Tensor | None = None) -> tuple[torch.Tensor, bool]:
+                    identity: torch.Tensor | None = None, rows: int | None = None) -> tuple[torch.Tensor, bool]:
         """The event rows in CSR order: ``(norm_kv(tokens) as bf16 rows, True)`` in one pass over the
         tables when the fused tokenizer + LayerNorm applies (the fp32 tokens are never stored),
-        else ``(tokens, False)``."""
+        else ``(tokens, False)``.  ``rows``: the latent rows of the forward (B L), for the window
+        layouts of the weights widened in the same launch."""
         cfg = self.config
         tok, xa = self.tokenizer, self.encoder.cross_attn
         tables = (tok.neuron_emb.weight, tok.time_emb.weight, tok.value_emb.weight)
@@ -249,7 +252,7 @@ class CortexModel(nn.Module):
             # the cross-attention's and the first block's weights widen into their windows in the
             # same launch (INT8-resident window mode), unless the pack plan carried them
             blocks = self.encoder.self_attn_blocks
-            widen = rider(xa, blocks[0] if len(blocks) else None)
+            widen = rider(xa, blocks[0] if len(blocks) else None, rows=rows)
             return ops.tokenize_ln(*tables, neuron_ids, time_bins, values, ln_params(xa.norm_kv), order=order,
                                    csr_offsets=offsets, err=err_flag, identity=identity, widen=widen), True
         return ops.tokenize(*tables, neuron_ids, time_bins, values, order=order, csr_offsets=offsets,

@@ -99,8 +99,8 @@ class SelfAttentionBlock(nn.Module):
         if self._fused_attention_ok(x, length):
             # qkv projection + attention per (head, sample) on chip: qkv never reaches HBM
             if xn is None:  # this block's weights widen into their window in the same launch
-                xn = normalize_bf16(x, self.norm_attn, widen=rider(self))
-            o_buf = ops.qkv_attention(xn, *fused_weight(self.qkv_proj), batch, length, H)
+                xn = normalize_bf16(x, self.norm_attn, widen=rider(self, rows=x.numel() // x.shape[-1]))
+            o_buf = ops.qkv_attention(xn, *fused_weight(self.qkv_proj, rows=batch * length), batch, length, H)
         else:
             if xn is not None:
                 qkv = ops.norm_linear(xn, **exec_weights(self.qkv_proj, compute), out_dtype=compute,
@@ -212,12 +212,17 @@ class PerceiverEncoder(nn.Module):
         xa = self.cross_attn
         regions = {"cross": [(xa, [xa.kv_proj, xa.out_proj])],
                    "block": [(b, [b.qkv_proj, b.out_proj, b.mlp[0], b.mlp[2]]) for b in self.self_attn_blocks]}
+        # the residual linear + LayerNorm and the residual GEMM read fragment-order weights
+        roles = {id(xa.out_proj): "ln"}
+        for b in self.self_attn_blocks:
+            roles[id(b.out_proj)] = "ln"
+            roles[id(b.mlp[2])] = "res"
         lins = [lin for g in regions.values() for _, ls in g for lin in ls if hasattr(lin, "weight_int8")]
         sig = tuple((lin.weight_int8.data_ptr(), tuple(lin.weight_int8.shape)) for lin in lins)
         cached = self.__dict__.get("_cortex_window_sig")
         if cached is not None and cached[0] == sig:
             return cached[1]
-        win = build_weight_window(regions, lins[0].weight_int8.device) if lins else None
+        win = build_weight_window(regions, lins[0].weight_int8.device, roles) if lins else None
         self.__dict__["_cortex_window_sig"] = (sig, win)
         return win
 

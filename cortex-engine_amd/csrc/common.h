@@ -171,6 +171,7 @@ struct WidenRider {
   const int8_t* src[WR_MAX];
   bf16* dst[WR_MAX];
   int64_t end[WR_MAX];  // cumulative element counts
+  int fk[WR_MAX];       // log2 of the row length K: dst in MFMA fragment order (cortex_frag_weight); 0: as src
   int count;
   int blocks;           // rider workgroups (0: none)
   int64_t chunk;        // elements per rider workgroup
@@ -193,6 +194,26 @@ __device__ __forceinline__ void widen_rider_run(const WidenRider& r, int blk) {
       const WtOut store(r.dst[s], (s1 - s0) * 2, true);
       const int8_t* src = r.src[s] + (a - s0);
       bf16* dst = r.dst[s] + (a - s0);
+      const int fk = r.fk[s];
+      if (fk != 0) {
+        // fragment-order destination (cortex_frag_weight's layout): the 16-element units are
+        // taken tile by tile, 64 consecutive units = one 16-row x 64-K tile (unit l of a tile: row
+        // l % 16, K 16 (l / 16) .. +15), so a wavefront reads 16 rows x 64 bytes and writes two
+        // whole 1 KiB blocks (block (n / 16) * (K / 32) + k / 32, lane n % 16 + 16 ((k / 8) % 4))
+        const int tk = fk - 6;  // log2 of the 64-K tiles per 16-row band
+        for (int64_t i = threadIdx.x * 16; i < b - a; i += (int64_t)blockDim.x * 16) {
+          const int64_t u = (a - s0 + i) >> 4, w = u >> 6;
+          const int l = (int)(u & 63);
+          const int64_t n = ((w >> tk) << 4) + (l & 15), k = ((w & ((1ll << tk) - 1)) << 6) + ((l >> 4) << 4);
+          const i32x4 raw = *reinterpret_cast<const i32x4*>(r.src[s] + (n << fk) + k);
+          const int64_t off = ((((n >> 4) << (fk - 5)) + (k >> 5)) << 9) + ((((k >> 3) & 3) << 4) + (n & 15)) * 8;
+          store(reinterpret_cast<bf16x8*>(r.dst[s] + off), widen_i8x8(make_uint2((uint32_t)raw[0], (uint32_t)raw[1])));
+          store(reinterpret_cast<bf16x8*>(r.dst[s] + off + 128),
+                widen_i8x8(make_uint2((uint32_t)raw[2], (uint32_t)raw[3])));
+        }
+        s0 = s1;
+        continue;
+      }
       auto put = [&](int64_t i, const i32x4& raw) {
         store(reinterpret_cast<bf16x8*>(dst + i), widen_i8x8(make_uint2((uint32_t)raw[0], (uint32_t)raw[1])));
         store(reinterpret_cast<bf16x8*>(dst + i + 8), widen_i8x8(make_uint2((uint32_t)raw[2], (uint32_t)raw[3])));
@@ -341,7 +362,7 @@ void set_error(const char* fmt, ...);
 // launch one on a grid of its own.
 struct WidenRider;
 int make_rider(const char* who, int n, const void* const* src, void* const* dst, const int64_t* count,
-               WidenRider* r);
+               const int64_t* frag_k, WidenRider* r);
 int widen_launch(const WidenRider& wr, hipStream_t stream);
 }  // namespace cortex
 

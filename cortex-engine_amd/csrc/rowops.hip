@@ -363,8 +363,10 @@ __global__ __launch_bounds__(256) void tokenize_ln_kernel(TokLnArgs a, WidenRide
 __global__ __launch_bounds__(256) void widen_kernel(WidenRider wr) { widen_rider_run(wr, (int)blockIdx.x); }
 
 // Rider of up to WR_MAX (src int8, dst bf16, count) arrays; arrays with count 0 are dropped.
+// frag_k (nullable): per array 0 (dst laid out as src) or the row length K of an (N, K) weight
+// whose dst is in MFMA fragment order (a power of two from 64, count a multiple of 16 K).
 int make_rider(const char* who, int n, const void* const* src, void* const* dst, const int64_t* count,
-               WidenRider* r) {
+               const int64_t* frag_k, WidenRider* r) {
   *r = WidenRider{};
   CORTEX_CHECK_ARG(n >= 0 && n <= WR_MAX, "%s: %d arrays to widen (at most %d)", who, n, WR_MAX);
   if (n == 0) return OK;
@@ -376,7 +378,12 @@ int make_rider(const char* who, int n, const void* const* src, void* const* dst,
     if (count[i] == 0) continue;
     CORTEX_CHECK_ARG(src[i] && dst[i] && ((uintptr_t)src[i] & 15) == 0 && ((uintptr_t)dst[i] & 15) == 0,
                      "%s: widen arrays must be 16-byte aligned", who);
+    const int64_t fk = frag_k ? frag_k[i] : 0;
+    CORTEX_CHECK_ARG(fk == 0 || (fk >= 64 && fk <= (1 << 20) && (fk & (fk - 1)) == 0 && count[i] % (16 * fk) == 0),
+                     "%s: fragment-order widen needs K a power of two from 64 and count a multiple of 16 K (K %lld)",
+                     who, (long long)fk);
     total += count[i];
+    r->fk[r->count] = fk ? __builtin_ctzll((unsigned long long)fk) : 0;
     r->src[r->count] = static_cast<const int8_t*>(src[i]);
     r->dst[r->count] = static_cast<bf16*>(dst[i]);
     r->end[r->count] = total;
@@ -504,9 +511,10 @@ int cortex_ln_rows(int64_t M, int64_t K, const float* x, int64_t ld_x, const flo
 int cortex_ln_rows_widen(int64_t M, int64_t K, const float* x, int64_t ld_x, const float* gamma1, const float* beta1,
                          float eps1, const float* gamma2, const float* beta2, float eps2, void* out_bf16,
                          int64_t ld_bf16, float* out_f32, int64_t ld_f32, int n_widen, const void* const* widen_src,
-                         void* const* widen_dst, const int64_t* widen_count, hipStream_t stream) {
+                         void* const* widen_dst, const int64_t* widen_count, const int64_t* widen_frag_k,
+                         hipStream_t stream) {
   WidenRider wr;
-  const int st = make_rider("cortex_ln_rows_widen", n_widen, widen_src, widen_dst, widen_count, &wr);
+  const int st = make_rider("cortex_ln_rows_widen", n_widen, widen_src, widen_dst, widen_count, widen_frag_k, &wr);
   if (st != OK) return st;
   return ln_rows_launch(M, K, x, ld_x, gamma1, beta1, eps1, gamma2, beta2, eps2, out_bf16, ld_bf16, out_f32, ld_f32,
                         wr, stream);
@@ -530,18 +538,20 @@ int cortex_tokenize_ln_widen(int64_t D, const float* neuron_emb, int64_t n_neuro
                              const int64_t* order, const int32_t* identity, const int64_t* csr_end, const float* gamma,
                              const float* beta, float eps, void* out_bf16, int64_t ld_out, int32_t* err_flag,
                              int n_widen, const void* const* widen_src, void* const* widen_dst,
-                             const int64_t* widen_count, hipStream_t stream) {
+                             const int64_t* widen_count, const int64_t* widen_frag_k, hipStream_t stream) {
   WidenRider wr;
-  const int st = make_rider("cortex_tokenize_ln_widen", n_widen, widen_src, widen_dst, widen_count, &wr);
+  const int st =
+      make_rider("cortex_tokenize_ln_widen", n_widen, widen_src, widen_dst, widen_count, widen_frag_k, &wr);
   if (st != OK) return st;
   return tokenize_ln_launch(D, neuron_emb, n_neuron, ld_neuron, time_emb, n_time, ld_time, value_emb, n_value,
                             ld_value, neuron_ids, s_nid, time_bins, s_tb, values, s_val, E, order, identity, csr_end,
                             gamma, beta, eps, out_bf16, ld_out, err_flag, wr, stream);
 }
 
-int cortex_widen_int8(int n, const void* const* src, void* const* dst, const int64_t* count, hipStream_t stream) {
+int cortex_widen_int8(int n, const void* const* src, void* const* dst, const int64_t* count, const int64_t* frag_k,
+                      hipStream_t stream) {
   WidenRider wr;
-  const int st = make_rider("cortex_widen_int8", n, src, dst, count, &wr);
+  const int st = make_rider("cortex_widen_int8", n, src, dst, count, frag_k, &wr);
   if (st != OK) return st;
   return widen_launch(wr, stream);
 }

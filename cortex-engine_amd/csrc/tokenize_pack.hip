@@ -831,9 +831,9 @@ int cortex_pack_plan_widen(const int64_t* batch_indices, int64_t s_bidx, int64_t
                            int64_t* order, int64_t* dst_rows, int64_t* rank, void* workspace,
                            int64_t workspace_bytes, int32_t* err_flag, int32_t* identity, int flags, int n_widen,
                            const void* const* widen_src, void* const* widen_dst, const int64_t* widen_count,
-                           hipStream_t stream) {
+                           const int64_t* widen_frag_k, hipStream_t stream) {
   WidenRider wr;
-  const int st = make_rider("cortex_pack_plan_widen", n_widen, widen_src, widen_dst, widen_count, &wr);
+  const int st = make_rider("cortex_pack_plan_widen", n_widen, widen_src, widen_dst, widen_count, widen_frag_k, &wr);
   if (st != OK) return st;
   rider_chunk(wr, WR_CHUNK_SMALL);  // the plan holds a few CUs: the rider takes all the others
   return pack_plan_impl("cortex_pack_plan_widen", batch_indices, s_bidx, E, B, offsets, order, dst_rows, rank,

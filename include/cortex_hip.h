@@ -67,7 +67,7 @@ int cortex_pack_plan_widen(const int64_t* batch_indices, int64_t s_bidx, int64_t
                            int64_t* order, int64_t* dst_rows, int64_t* rank, void* workspace,
                            int64_t workspace_bytes, int32_t* err_flag, int32_t* identity, int flags, int n_widen,
                            const void* const* widen_src, void* const* widen_dst, const int64_t* widen_count,
-                           hipStream_t stream);
+                           const int64_t* widen_frag_k, hipStream_t stream);
 
 /* cortex_pack_plan without a workspace argument and without any allocation.  No
  * counterpart in the reference: it is for callers that cannot allocate device memory
@@ -202,12 +202,16 @@ int cortex_ln_rows(int64_t M, int64_t K, const float* x, int64_t ld_x, const flo
  * kernels and of the tokenizer + LayerNorm run it in extra workgroups of their own launch (the
  * next block's weights ride along with the rows that feed it), otherwise exactly as
  * cortex_ln_rows / cortex_tokenize_ln.  The widened arrays must not overlap the kernel's
- * inputs or outputs. */
-int cortex_widen_int8(int n, const void* const* src, void* const* dst, const int64_t* count, hipStream_t stream);
+ * inputs or outputs.  frag_k (nullable): per array 0, or the row length K (a power of two from
+ * 64) of an (N, K) weight to write in MFMA fragment order, the layout of weight code 7
+ * (cortex_frag_weight), count a multiple of 16 K. */
+int cortex_widen_int8(int n, const void* const* src, void* const* dst, const int64_t* count, const int64_t* frag_k,
+                      hipStream_t stream);
 int cortex_ln_rows_widen(int64_t M, int64_t K, const float* x, int64_t ld_x, const float* gamma1, const float* beta1,
                          float eps1, const float* gamma2, const float* beta2, float eps2, void* out_bf16,
                          int64_t ld_bf16, float* out_f32, int64_t ld_f32, int n_widen, const void* const* widen_src,
-                         void* const* widen_dst, const int64_t* widen_count, hipStream_t stream);
+                         void* const* widen_dst, const int64_t* widen_count, const int64_t* widen_frag_k,
+                         hipStream_t stream);
 int cortex_tokenize_ln_widen(int64_t D, const float* neuron_emb, int64_t n_neuron, int64_t ld_neuron,
                              const float* time_emb, int64_t n_time, int64_t ld_time, const float* value_emb,
                              int64_t n_value, int64_t ld_value, const int64_t* neuron_ids, int64_t s_nid,
@@ -215,7 +219,8 @@ int cortex_tokenize_ln_widen(int64_t D, const float* neuron_emb, int64_t n_neuro
                              const int64_t* order, const int32_t* identity, const int64_t* csr_end, const float* gamma,
                              const float* beta, float eps, void* out_bf16, int64_t ld_out, int32_t* err_flag,
                              int n_widen, const void* const* widen_src, void* const* widen_dst,
-                             const int64_t* widen_count, hipStream_t stream);
+                             const int64_t* widen_count, const int64_t* widen_frag_k,
+                             hipStream_t stream);
 
 /* ---- a7: dtype conversion ---------------------------------------------------
  * out[i] = (out dtype) in[i]; int8 / f32 / bf16 / f16 in, f32 / bf16 out (bf16 by

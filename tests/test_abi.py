@@ -76,16 +76,20 @@ def test_invalid_arguments_return_status_and_message():
     # widening riders: at most 8 arrays, counts in multiples of 16, 16-byte aligned arrays
     src = (ctypes.c_void_p * 9)(*([16] * 9))
     cnt = (ctypes.c_int64 * 9)(*([16] * 9))
-    rc = lib.cortex_widen_int8(9, src, src, cnt, None)
+    rc = lib.cortex_widen_int8(9, src, src, cnt, None, None)
     assert rc == -1 and b"at most 8" in lib.cortex_last_error()
     cnt[0] = 24
-    rc = lib.cortex_widen_int8(1, src, src, cnt, None)
+    rc = lib.cortex_widen_int8(1, src, src, cnt, None, None)
     assert rc == -1 and b"multiple of 16" in lib.cortex_last_error()
     cnt[0], src[0] = 16, 8
     rc = lib.cortex_ln_rows_widen(0, 512, None, 512, None, None, 1e-5, None, None, 0.0, None, 512, None, 512, 1, src,
-                                  src, cnt, None)
+                                  src, cnt, None, None)
     assert rc == -1 and b"16-byte aligned" in lib.cortex_last_error()
-    assert lib.cortex_widen_int8(0, None, None, None, None) == 0
+    assert lib.cortex_widen_int8(0, None, None, None, None, None) == 0
+    cnt[0], src[0] = 16 * 96, 16
+    fk = (ctypes.c_int64 * 1)(96)  # a fragment-order K must be a power of two
+    rc = lib.cortex_widen_int8(1, src, src, cnt, fk, None)
+    assert rc == -1 and b"power of two" in lib.cortex_last_error()
     # the fragment-order weight: 16-row, 32-K blocks; the direct-weight kernel takes K 256 / 512
     rc = lib.cortex_frag_weight(24, 64, 16, 1, 64, 16, None)
     assert rc == -1 and b"multiple of 16" in lib.cortex_last_error()

@@ -510,3 +510,31 @@ def test_widen_riders_exact_and_rows_unchanged(sizes):
     assert torch.equal(out, ref)
     for s, d in zip(src, dst):
         assert torch.equal(d, s.to(torch.bfloat16))
+
+
+@pytest.mark.parametrize("shapes", [((512, 512),), ((512, 2048), (1536, 512), (512, 512), (2048, 512)),
+                                    ((16, 64), (64, 64), (48, 1024))])
+def test_widen_rider_fragment_order(shapes):
+    """Widening riders that write MFMA fragment order (K given per array): each destination
+    equals cortex_frag_weight's layout of the same int8 weight, next to plain arrays in the same
+    launch, on a launch of its own and riding on the LayerNorm row kernel."""
+    from cortex.kernels import ops
+
+    g = torch.Generator().manual_seed(len(shapes))
+    for host in ("alone", "ln_rows"):
+        items, want = [], []
+        for i, (n, k) in enumerate(shapes):
+            q = torch.randint(-127, 128, (n, k), generator=g, dtype=torch.int8).to(DEV)
+            d = torch.full((n, k), 7.0, dtype=torch.bfloat16, device=DEV)
+            frag = i % 2 == 0
+            items.append((q, d, k if frag else 0))
+            want.append(ops.frag_weight(q) if frag else q.to(torch.bfloat16))
+        if host == "alone":
+            ops.widen_int8(items)
+        else:
+            x = torch.randn(300, 512, generator=g).to(DEV)
+            ln = (torch.ones(512, device=DEV), torch.zeros(512, device=DEV), 1e-5)
+            assert torch.equal(ops.ln_rows(x, ln, widen=items), ops.ln_rows(x, ln))
+        torch.cuda.synchronize()
+        for (q, d, k), w in zip(items, want):
+            assert torch.equal(d.view(torch.int16), w.view(torch.int16)), (host, tuple(q.shape), k)
