@@ -8,26 +8,28 @@
 // chunks of up to 4 tiles of 64: every load of a chunk is issued at once (one
 // memory round trip per chunk, not per tile), and each tile is multiplied as soon
 // as its own loads have landed, while the later tiles' loads are still in flight.
-// Two workgroups share a CU (68 KiB LDS each).
+// Two workgroups share a CU (64 KiB LDS each).
 //
 //   scores  S^T = K Q^T    (A = K rows from LDS, B = Q held in registers): a lane
 //           holds 4 keys x 1 query per 16x16 sub-tile, so the softmax statistics of
 //           a query are lane-local apart from two xor-shuffles (lane groups);
-//   output  O^T += V^T P^T (A = V^T rows from LDS, B = P^T straight from the score
+//   output  O^T += V^T P^T (A = V^T read transposed from LDS, B = P^T straight from the score
 //           accumulators, rounded to bf16);
 //   sums    l += 1 P^T     (an all-ones A operand: the key-sum of exactly the bf16
 //           probabilities used in O, on the matrix core instead of the VALU).
 //
 // Key order.  Score sub-tile st, row r holds key 32(st/2) + 8(r/4) + 4(st%2) + r%4,
 // so a lane of group g ends up with the 8 CONSECUTIVE keys 32c + 8g .. +7 for
-// key step c; V^T is then read as one 16-byte LDS word per fragment.
+// key step c: its V^T fragment is the 8 key rows 32c + 8g .. +7 at 4 head dims each.
 //
-// Staging.  K: global -> LDS by direct transfers (buffer_load_dwordx4 ... lds), rows of
-// 128 B with the 16-byte chunk c of row r stored at c ^ f(r), f chosen so that the
-// 16 rows of one fragment read cover all 16 bank groups.  V: each lane loads 4 head
-// dims of a pair of keys, packs (key, key+1) dwords and writes them transposed as
-// V^T rows of 64 keys with a 144-byte pitch; the 16 rows read by one fragment, and
-// the two rows (8 apart) written by the two half-waves, fall into distinct banks.
+// Staging.  K and V both go global -> LDS by direct transfers (buffer_load_dwordx4
+// ... lds), row-major, 128 B a key row, the 16-byte chunk c of row r stored at c ^ f(r)
+// (f = kswz for K, vswz for V) so that the rows one fragment read touches fall into
+// distinct banks.  The V^T fragment comes out of the row-major V tile by two LDS
+// transpose reads (ds_read_b64_tr_b16), each 4 key rows x 4 head dims of a 16-lane
+// group.  No load of the tile loop has a register destination, so every wait on the
+// transfers is an explicit vmcnt that counts tiles, and each tile is multiplied as
+// soon as its own K and V have landed.
 //
 // Online softmax in the exp2 domain (FlashAttention-2, Dao 2023) with a lazily
 // moved reference max; keys past the sample's length are masked in the last tile;
@@ -46,8 +48,7 @@ constexpr int AF_CH = 4;                         // tiles per chunk
 constexpr int AF_WAVES = 8;
 constexpr int AF_THREADS = 64 * AF_WAVES;
 constexpr int AF_KTILE = AF_KT * 128;            // bytes of one K tile (64 keys x 64 bf16)
-constexpr int AF_VP = 144;                       // bytes per V^T row (64 keys + 16 B pad)
-constexpr int AF_VTILE = 64 * AF_VP;             // bytes of one V^T tile (64 head dims)
+constexpr int AF_VTILE = AF_KT * 128;            // bytes of one V tile (64 keys x 64 bf16, row-major)
 constexpr int AF_LDS = AF_CH * (AF_KTILE + AF_VTILE);
 // A query's running max is moved only when a tile raises it by more than this
 // (log2 units): the probabilities stay <= 2^8, exact in the fp32 sums, and the
@@ -65,10 +66,23 @@ __device__ __forceinline__ int key_of(int st, int r) {
 __device__ __forceinline__ void af_wait_vm(int n) {
   switch (n) {
     case 0: __builtin_amdgcn_s_waitcnt(0 | 0x70 | 0xF00); break;
-    case 3: __builtin_amdgcn_s_waitcnt(3 | 0x70 | 0xF00); break;
-    case 6: __builtin_amdgcn_s_waitcnt(6 | 0x70 | 0xF00); break;
-    default: __builtin_amdgcn_s_waitcnt(9 | 0x70 | 0xF00); break;
+    case 2: __builtin_amdgcn_s_waitcnt(2 | 0x70 | 0xF00); break;
+    case 4: __builtin_amdgcn_s_waitcnt(4 | 0x70 | 0xF00); break;
+    default: __builtin_amdgcn_s_waitcnt(6 | 0x70 | 0xF00); break;
   }
+}
+
+// V-tile chunk swizzle (16-byte chunks of a 128-byte key row): XOR with 2 h(r), h taking bits
+// 1 and 3 of the row, so the 8 rows that a half-wavefront's transpose reads touch (rows
+// 8 g + 0..3 of two lane groups, 32 bytes each) land on 8 distinct 32-byte bank ranges.
+__device__ __forceinline__ int vswz(int r) { return (((r >> 1) & 1) | (((r >> 3) & 1) << 1)) << 1; }
+
+// LDS transpose read (gfx950 ds_read_b64_tr_b16): in each group of 16 lanes, lane i gets
+// element (i % 4) of the 4 elements at the address of lane 4 p + i / 4, for p = 0..3.
+__device__ __forceinline__ uint2 lds_read_tr16(const unsigned char* p) {
+  typedef short v4i16 __attribute__((ext_vector_type(4)));
+  const v4i16 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4i16*)(p));
+  return __builtin_bit_cast(uint2, r);
 }
 
 // Block-mask view of one sample: tile (qi, kj) is allowed iff m[qi * n_kt + kj] != 0;
@@ -88,7 +102,7 @@ template <int QG, bool MASK>
 __global__ __launch_bounds__(AF_THREADS) __attribute__((amdgpu_waves_per_eu(QG == 1 ? 4 : 2)))
 void attention_fast_kernel(AttnArgs a) {
   constexpr int AF_QB = 16 * QG * AF_WAVES;  // queries per workgroup
-  __shared__ __attribute__((aligned(1024))) unsigned char smem[AF_LDS];  // K tiles, then V^T tiles
+  __shared__ __attribute__((aligned(1024))) unsigned char smem[AF_LDS];  // K tiles, then V tiles
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int fr = lane & 15, g = lane >> 4;
 
@@ -136,11 +150,11 @@ void attention_fast_kernel(AttnArgs a) {
   const int64_t k_col = ((lane & 7) ^ kswz(k_row)) * 8;
   const __amdgpu_buffer_rsrc_t k_rsrc =
       __builtin_amdgcn_make_buffer_rsrc(const_cast<bf16*>(Kb), (short)0, (int)0xffffffffu, 0x00020000);
-  // V of this lane: keys 2 kp, 2 kp + 1, head dims 4 dq .. 4 dq + 3; the two half-waves
-  // take head-dim quads two apart (V^T rows 8 apart).
-  const int half = lane >> 5, kp = lane & 31;
-  const int dq = (wid & 1) + 4 * (wid >> 1) + 2 * half;
-  const bf16* v_src = Vb + dq * 4;
+  // V transfer of this lane: the same rows as K, row-major into the V stage with the vswz
+  // chunk swizzle (lane i: row 8 wid + i / 8, stored chunk i % 8 = logical (i % 8) ^ vswz(row))
+  const int64_t v_col = ((lane & 7) ^ vswz(k_row)) * 8;
+  const __amdgpu_buffer_rsrc_t v_rsrc =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<bf16*>(Vb), (short)0, (int)0xffffffffu, 0x00020000);
 
   auto k_stage = [&](int j) { return smem + j * AF_KTILE; };
   auto v_stage = [&](int j) { return smem + AF_CH * AF_KTILE + j * AF_VTILE; };
@@ -153,10 +167,16 @@ void attention_fast_kernel(AttnArgs a) {
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) k_off[st][ks] = r * 128 + (((ks * 4 + g) ^ kswz(r)) << 4);
   }
+  // V^T fragment (K block c, head dims 16 t ..): lane (fr, g) holds keys 32 c + 8 g + 0..7 of head
+  // dim 16 t + fr, from two transpose reads 4 rows apart: each lane addresses row
+  // 32 c + 8 g + fr / 4, head dims 16 t + 4 (fr % 4) .. +3 (vswz does not change over +4 rows)
 #pragma unroll
   for (int c = 0; c < 2; ++c)
 #pragma unroll
-    for (int t = 0; t < 4; ++t) v_off[c][t] = (16 * t + fr) * AF_VP + (4 * c + g) * 16;
+    for (int t = 0; t < 4; ++t) {
+      const int r = 32 * c + 8 * g + (fr >> 2), d = 16 * t + 4 * (fr & 3);
+      v_off[c][t] = r * 128 + (((d >> 3) ^ vswz(r)) << 4) + ((d >> 2) & 1) * 8;
+    }
 
   float m_run[QG];
   f32x4 o_acc[QG][4], l_acc[QG];
@@ -197,41 +217,30 @@ void attention_fast_kernel(AttnArgs a) {
   int wbase = 0;
   uint64_t pend = MASK ? wg_window(0) : 0;
 
-  // ---- the loads of tile t (keys clamped to the sample) into stage j: the K transfer and
-  // this lane's two V rows (V^T is written from registers once they land).  With 32 queries per
-  // wavefront a whole tile takes a uniform tile offset plus the lane's constant offsets (no
-  // per-lane multiply) and only the sample's last, partial tile clamps its rows; the 16-query
-  // form (128 VGPRs) has no registers to spare for the constants and clamps every tile.
   const uint32_t k_lane = (uint32_t)(((int64_t)k_row * a.k_sl + k_col) * 2);
-  const int64_t va_lane = (int64_t)(2 * kp) * a.v_sl;
-  auto issue_tile = [&](int t, int j, uint2& va, uint2& vb) {
+  const uint32_t v_lane = (uint32_t)(((int64_t)k_row * a.v_sl + v_col) * 2);
+  // ---- the loads of tile t (keys clamped to the sample) into stage j: the K and V transfers,
+  // both direct to LDS, so no load in flight has a register destination and the waits below
+  // count exactly (with the V rows in registers, the compiler waited for every load in flight
+  // before their use, emptying the ring).  With 32 queries per wavefront a whole tile takes a
+  // uniform tile offset plus the lane's constant offsets; the sample's last, partial tile
+  // clamps its rows.
+  auto issue_tile = [&](int t, int j) {
     const int64_t k0 = (int64_t)t * AF_KT;
-    uint32_t koff;
-    const bf16 *pa, *pb;
+    uint32_t koff, voff;
     if (QG == 2 && k0 + AF_KT <= len) {
       koff = (uint32_t)(k0 * a.k_sl * 2) + k_lane;
-      pa = v_src + (k0 * a.v_sl + va_lane);
-      pb = pa + a.v_sl;
+      voff = (uint32_t)(k0 * a.v_sl * 2) + v_lane;
     } else {
       const int64_t kr = min(k0 + k_row, len - 1);
       koff = (uint32_t)((kr * a.k_sl + k_col) * 2);
-      pa = v_src + min(k0 + 2 * kp, len - 1) * a.v_sl;
-      pb = v_src + min(k0 + 2 * kp + 1, len - 1) * a.v_sl;
+      voff = (uint32_t)((kr * a.v_sl + v_col) * 2);
     }
     __builtin_amdgcn_raw_ptr_buffer_load_lds(
         k_rsrc, (__attribute__((address_space(3))) void*)(k_stage(j) + wid * 1024), 16, (int)koff, 0, 0, 0);
-    va = *reinterpret_cast<const uint2*>(pa);
-    vb = *reinterpret_cast<const uint2*>(pb);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+        v_rsrc, (__attribute__((address_space(3))) void*)(v_stage(j) + wid * 1024), 16, (int)voff, 0, 0, 0);
     __builtin_amdgcn_sched_barrier(0);  // keep the issue order tile by tile (vmcnt below)
-  };
-  // V^T: dword (V[2kp][4dq+e], V[2kp+1][4dq+e]) into row 4dq+e, column kp of stage j
-  auto write_vt = [&](int j, const uint2& va, const uint2& vb) {
-    unsigned char* base = v_stage(j) + (4 * dq) * AF_VP + kp * 4;
-    const uint32_t a0 = va.x, a1 = va.y, b0 = vb.x, b1 = vb.y;
-    *reinterpret_cast<uint32_t*>(base + 0 * AF_VP) = (a0 & 0xffffu) | (b0 << 16);
-    *reinterpret_cast<uint32_t*>(base + 1 * AF_VP) = (a0 >> 16) | (b0 & 0xffff0000u);
-    *reinterpret_cast<uint32_t*>(base + 2 * AF_VP) = (a1 & 0xffffu) | (b1 << 16);
-    *reinterpret_cast<uint32_t*>(base + 3 * AF_VP) = (a1 >> 16) | (b1 & 0xffff0000u);
   };
   // ---- scores S^T = K Q^T of the key tile in stage j (16-query groups with okq set)
   typedef f32x4 Scores[QG][4];
@@ -307,7 +316,8 @@ void attention_fast_kernel(AttnArgs a) {
         if (okq[qg]) l_acc[qg] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pf[qg][c], l_acc[qg], 0, 0, 0);
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
-        const bf16x8 vf = *reinterpret_cast<const bf16x8*>(vs_ + v_off[c][t]);
+        const uint2 v0 = lds_read_tr16(vs_ + v_off[c][t]), v1 = lds_read_tr16(vs_ + v_off[c][t] + 4 * 128);
+        const bf16x8 vf = __builtin_bit_cast(bf16x8, make_uint4(v0.x, v0.y, v1.x, v1.y));
 #pragma unroll
         for (int qg = 0; qg < QG; ++qg)
           if (okq[qg]) o_acc[qg][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pf[qg][c], o_acc[qg][t], 0, 0, 0);
@@ -329,25 +339,22 @@ void attention_fast_kernel(AttnArgs a) {
     softmax_pv(kt, j, okq, s);
   };
 
-  uint2 va[AF_CH], vb[AF_CH];
   if constexpr (!MASK) {
     // Dense keys: the stages form a ring, and the tiles are software-pipelined.  Tiles 0..3
-    // are issued up front.  Iteration kt makes tile kt + 1 visible (V^T written, barrier),
+    // are issued up front.  Iteration kt makes tile kt + 1 visible (its transfers awaited, barrier),
     // issues its score MFMAs, and only then runs the softmax and P V of tile kt, whose scores
     // the previous iteration produced: the matrix core works on tile kt + 1 while the VALU
     // evaluates tile kt's exponentials.  After that barrier every wavefront is done with tile
     // kt - 1, so its stage is refilled with tile kt + 3 (clamped past the end: issued, never
-    // read).  Each tile is 3 loads; the waits name the tiles issued after the awaited one.
+    // read).  Each tile is 2 transfers; the waits name the tiles issued after the awaited one.
     bool all[QG];
 #pragma unroll
     for (int qg = 0; qg < QG; ++qg) all[qg] = true;
     Scores sc[2];
     if (nt > 0) {  // (no keys: nothing is loaded, the rows give 0)
 #pragma unroll
-      for (int t = 0; t < AF_CH; ++t) issue_tile(min(t, nt - 1), t, va[t], vb[t]);
-      af_wait_vm(9);
-      write_vt(0, va[0], vb[0]);
-      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's V^T stores are done
+      for (int t = 0; t < AF_CH; ++t) issue_tile(min(t, nt - 1), t);
+      af_wait_vm(6);
       __builtin_amdgcn_s_barrier();
       scores(0, all, sc[0]);
     }
@@ -358,11 +365,10 @@ void attention_fast_kernel(AttnArgs a) {
         if (kt >= nt) break;
         const int tn = (t + 1) & 3;  // stage of tile kt + 1
         if (kt + 1 < nt) {
-          af_wait_vm(kt == 0 ? 6 : 3);
-          write_vt(tn, va[tn], vb[tn]);
-          __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): V^T stores and tile kt-1's reads done
+          af_wait_vm(kt == 0 ? 4 : 2);
+          __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): tile kt-1's reads done
           __builtin_amdgcn_s_barrier();        // tile kt+1 visible; stage of tile kt-1 free
-          if (kt >= 1) issue_tile(min(kt + 3, nt - 1), (t + 3) & 3, va[(t + 3) & 3], vb[(t + 3) & 3]);
+          if (kt >= 1) issue_tile(min(kt + 3, nt - 1), (t + 3) & 3);
           scores(tn, all, sc[(t + 1) & 1]);
         }
         softmax_pv(kt, t, all, sc[t & 1]);
@@ -394,14 +400,12 @@ void attention_fast_kernel(AttnArgs a) {
       // unconditional issue keeps the load counter exact, so each tile below waits for its
       // own loads only (vmcnt(3 (AF_CH-1-j)): tile j's K transfer and V registers are in).
 #pragma unroll
-      for (int j = 0; j < AF_CH; ++j) issue_tile(tl[j], j, va[j], vb[j]);
+      for (int j = 0; j < AF_CH; ++j) issue_tile(tl[j], j);
 #pragma unroll
       for (int j = 0; j < AF_CH; ++j) {
         if (j >= nc) break;
-        af_wait_vm(3 * (AF_CH - 1 - j));
-        write_vt(j, va[j], vb[j]);
-        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's V^T stores are done
-        __builtin_amdgcn_s_barrier();        // tile j's K transfers and V^T rows visible to all
+        af_wait_vm(2 * (AF_CH - 1 - j));
+        __builtin_amdgcn_s_barrier();        // tile j's K and V transfers visible to all
         do_tile(tl[j], j);
       }
     }
@@ -450,8 +454,9 @@ int try_attention_fast(const AttnArgs& a, int dtype, hipStream_t stream) {
   const int qg = cdiv(a.Lq, 16 * 2 * AF_WAVES) * nbh >= 256 ? 2 : 1;
   const int64_t nqb = cdiv(a.Lq, 16 * qg * AF_WAVES);
   if (nbh > 65535 || nqb * nbh > 0x7fffffffLL) return 0;
-  // K byte offsets from a (sample, head) start are 32-bit buffer offsets
-  if (a.Lk > 0 && (a.Lk - 1) * a.k_sl * 2 + 128 > 0xffffffffLL) return 0;
+  // K and V byte offsets from a (sample, head) start are 32-bit buffer offsets
+  if (a.Lk > 0 && ((a.Lk - 1) * a.k_sl * 2 + 128 > 0xffffffffLL || (a.Lk - 1) * a.v_sl * 2 + 128 > 0xffffffffLL))
+    return 0;
   const dim3 grid((unsigned)nqb, (unsigned)nbh);
   if (qg == 2 && mask)
     hipLaunchKernelGGL((attention_fast_kernel<2, true>), grid, dim3(AF_THREADS), 0, stream, a);
