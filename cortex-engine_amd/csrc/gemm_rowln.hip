@@ -82,18 +82,19 @@ struct RowLnArgs {
 };
 
 // Epilogue of both forms: scale, bias and residual in fp32, the fp32 rows written, then the
-// row statistics and the LayerNorm'd rows.  Lane (fr, g4), tile (i, j): row m0 + 16 i + fr,
-// columns wcol + 16 j + 4 g4 .. +3.  Every per-column parameter is loaded before the first
-// store, so no wait for them drains stores.  `smem` is reused for the statistics exchange
-// (2 KiB) after a barrier.
+// row statistics and the LayerNorm'd rows.  The wavefront holds column block cb: lane (fr, g4),
+// tile (i, j): row m0 + 16 i + fr, columns cb WN + 16 j + 4 g4 .. +3.  Every per-column
+// parameter is loaded before the first store, so no wait for them drains stores.  `smem` is
+// reused for the statistics exchange (2 KiB) after a barrier; the parts are indexed and
+// combined by column block, so which wavefront holds a block does not change any result.
 template <int BN, bool Q8, class TIN, class ACC, int TM, int TN>
 __device__ __forceinline__ void rowln_epilogue(const RowLnArgs& g, const ACC (&acc)[TM][TN],
-                                               const float4 (&rv)[TM][TN], int m0, unsigned char* smem) {
+                                               const float4 (&rv)[TM][TN], int m0, int cb, unsigned char* smem) {
   constexpr int WN = BN / RL_WAVES;
-  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
   const int fr = lane & 15, g4 = lane >> 4;
   const int M = (int)g.M;
-  const int wcol = wid * WN;
+  const int wcol = cb * WN;
   // the fp32 residual rows and the normalised rows (bf16, or int8 with Q8), written through
   const WtOut store_x(g.out, g.M * g.ld_out * 4, wt_one_wave());
   const WtOut store_xn(g.xn, g.M * g.ld_xn * (Q8 ? 1 : 2), wt_one_wave());
@@ -177,7 +178,7 @@ __device__ __forceinline__ void rowln_epilogue(const RowLnArgs& g, const ACC (&a
       }
     m2 += __shfl_xor(m2, 16, 64);
     m2 += __shfl_xor(m2, 32, 64);
-    if (g4 == 0) red[wid * RL_BM + i * 16 + fr] = make_float2(mw, m2);
+    if (g4 == 0) red[cb * RL_BM + i * 16 + fr] = make_float2(mw, m2);
   }
   __syncthreads();
 #pragma unroll
@@ -401,7 +402,7 @@ __global__ __launch_bounds__(RL_THREADS) void gemm_rowln_kernel(RowLnArgs g) {
   __builtin_amdgcn_s_waitcnt(0xC07F);
   mma(af1, wf1);
 
-  rowln_epilogue<BN, Q8, TIN>(g, acc, rv, m0, smem);
+  rowln_epilogue<BN, Q8, TIN>(g, acc, rv, m0, wid, smem);
 }
 
 // Direct-weight form, bf16 A rows and K = 64 * NK (the out-projection shapes), for the weight
@@ -435,7 +436,11 @@ __global__ __launch_bounds__(RL_THREADS) void gemm_rowln_dw_kernel(RowLnArgs g) 
   const int fr = lane & 15, g4 = lane >> 4;
   const int M = (int)g.M;
   const int m0 = blockIdx.x * RL_BM;
-  const int wcol = wid * WN;
+  // column block of this wavefront, rotated by workgroup: at any moment the workgroups of an
+  // XCD stream 8 different weight blocks rather than all the same 4 KiB per wavefront index
+  // (out-projection at B = 32: 16.34-16.41 -> 16.13-16.20 us, same box)
+  const int cb = (wid + (int)blockIdx.x) & (RL_WAVES - 1);
+  const int wcol = cb * WN;
 
   // A: the 1 KiB block q = wid * AB + i holds rows 8 (q % 4) .. +7 of K step q / 4 (lane i of a
   // transfer: row i / 8, stored chunk i % 8 = logical chunk (i % 8) ^ rl_swz(row))
@@ -504,7 +509,7 @@ __global__ __launch_bounds__(RL_THREADS) void gemm_rowln_dw_kernel(RowLnArgs g) 
     if (kt + WD < NK) load_w(kt + WD);
     __builtin_amdgcn_sched_barrier(0);  // a K step's loads stay behind its MFMAs (registers)
   }
-  rowln_epilogue<BN, Q8, bf16>(g, acc, rv, m0, smem);
+  rowln_epilogue<BN, Q8, bf16>(g, acc, rv, m0, cb, smem);
 }
 
 bool a16(const void* p) { return ((uintptr_t)p & 15) == 0; }
