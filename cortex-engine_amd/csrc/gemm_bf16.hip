@@ -791,7 +791,8 @@ int launch_persist(const GemmArgs& g, hipStream_t stream) {
 // rows, so no other wavefront reads its weight fragments: each is one contiguous 1 KiB read
 // straight into the lane's operand registers, issued a K step ahead of its MFMAs, never staged
 // in LDS.  The activation rows, which the four wavefronts of a group share, stream through a
-// two-stage ring of direct-to-LDS transfers per group (one barrier per K step).  After the loop
+// four-stage LDS ring per group with one barrier per two K steps (forward at B = 32 0.663-0.666
+// -> 0.655-0.659 ms against two stages and a barrier per step, same box).  After the loop
 // the groups swap halves of their partial tiles through LDS and each finishes 64 rows (their
 // residual prefetched before the loop): per element the two K halves' sums are added once, as
 // in the K-split tiles of gemm_bf16_kernel, with the same MFMA sequence per half, so the
@@ -809,7 +810,8 @@ __global__ __launch_bounds__(512) void gemm_res_dw_kernel(GemmArgs g) {
   typedef typename OP::frag frag;
   constexpr int TM = RD_BM / 16, TN = 2, HM = TM / 2;       // row tiles, column tiles, rows finished
   constexpr int A_STAGE = RD_BM * 128, AB = A_STAGE / 1024 / 4;  // 16 KiB; 4 chunks per lane and step
-  constexpr int RING = 2 * A_STAGE;                              // two stages per K group
+  constexpr int RS = 4;                                          // ring stages per K group
+  constexpr int RING = RS * A_STAGE;
   constexpr int XCH = 8 * HM * TN * 64 * 16;                     // swapped half tiles
   constexpr int LDS = 2 * RING > XCH ? 2 * RING : XCH;
   static_assert(NK >= 2, "two K steps per group at least");
@@ -843,7 +845,7 @@ __global__ __launch_bounds__(512) void gemm_res_dw_kernel(GemmArgs g) {
   };
   auto store_a = [&](int kt) {
 #pragma unroll
-    for (int i = 0; i < AB; ++i) *reinterpret_cast<frag*>(a_dst + (kt & 1) * A_STAGE + i * 1024) = ar[kt][i];
+    for (int i = 0; i < AB; ++i) *reinterpret_cast<frag*>(a_dst + (kt % RS) * A_STAGE + i * 1024) = ar[kt][i];
   };
   // weight fragment (t, ks) of step kt: block ((n0 + 32 wn) / 16 + t, kb / 32 + 2 kt + ks), this lane's 16 bytes
   const bf16* wp = reinterpret_cast<const bf16*>(g.w) + ((int64_t)((n0 + 32 * wn) / 16) * (K / 32) + kb / 32) * 512 +
@@ -875,11 +877,14 @@ __global__ __launch_bounds__(512) void gemm_res_dw_kernel(GemmArgs g) {
       for (int j = 0; j < TN; ++j) acc[i][j] = OP::mma(wb[kt][j][ks], af[i], acc[i][j]);
   };
 
-  // issue order: A(0), A(1), W(0), W(1), the residual of the rows this group finishes; then in
-  // step kt, after its barrier, A(kt + 2) into registers, and after its MFMAs W(kt + 2); A(kt + 1)
-  // goes from registers into its stage in step kt, before the barrier that publishes it
+  // issue order: A(0..2), W(0), W(1), the residual of the rows this group finishes.  The ring has
+  // four stages and a barrier after every second step: in step kt, A(kt + 2) goes from registers
+  // into its stage (read last in step kt - 2, before the previous barrier), A(kt + 3) into
+  // registers, and after the MFMAs W(kt + 2); the barrier closing steps kt and kt + 1 publishes
+  // the stages of kt + 2 and kt + 3, so the wavefronts of a workgroup may drift apart by a step
   load_a(0);
   load_a(1);
+  if (NK > 2) load_a(2);
   load_w(0);
   load_w(1);
   const float* res = reinterpret_cast<const float*>(g.res);
@@ -894,23 +899,24 @@ __global__ __launch_bounds__(512) void gemm_res_dw_kernel(GemmArgs g) {
                                                    4 * g4);
   }
   store_a(0);
-  __syncthreads();  // stage 0 of both groups written
+  store_a(1);
+  __syncthreads();  // stages 0 and 1 of both groups written
   frag af0[TM], af1[TM];
   read_a(0, 0, af0);
 #pragma unroll
   for (int kt = 0; kt < NK; ++kt) {
-    const int st = kt & 1;
+    const int st = kt % RS;
     __builtin_amdgcn_sched_barrier(0);
     read_a(st, 1, af1);
     mma(af0, kt, 0);
-    if (kt + 1 < NK) {
-      store_a(kt + 1);                     // stage st ^ 1: its last reads were before step kt - 1's barrier
-      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): these writes and this wave's reads of stage st
-      __builtin_amdgcn_s_barrier();        // every wave's: step kt + 1 visible, stage st free after its reads
-      __builtin_amdgcn_sched_barrier(0);
-      read_a(st ^ 1, 0, af0);
-      if (kt + 2 < NK) load_a(kt + 2);
+    if (kt + 2 < NK) store_a(kt + 2);
+    if ((kt & 1) && kt + 1 < NK) {
+      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): these writes and this wave's reads of the pair's stages
+      __builtin_amdgcn_s_barrier();        // every wave's: steps kt + 1, kt + 2 visible, the pair's stages free
     }
+    __builtin_amdgcn_sched_barrier(0);
+    if (kt + 1 < NK) read_a((kt + 1) % RS, 0, af0);
+    if (kt + 3 < NK) load_a(kt + 3);
     mma(af1, kt, 1);
     if (kt + 2 < NK) load_w(kt + 2);
   }
